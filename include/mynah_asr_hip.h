@@ -1,0 +1,144 @@
+/* mynah_asr_hip.h — C ABI of the MI355X (gfx950) backend unit for mynah-asr's
+ * linear-layer hot path.
+ *
+ * The unit plays the role src/cuda_gemm.cu plays for CUDA: backend.c and qmat.c
+ * call these functions first and fall back to their CPU code when one returns
+ * -1 (src/backend.c:74-77). Every entry point takes plain host pointers and
+ * sizes; nothing here exposes a HIP or torch type (streams travel as void*).
+ *
+ * Numerics. Two modes, chosen process-wide with mynah_asr_hip_set_numerics():
+ *   EXACT (default): every output row matches an f32 GEMM over the
+ *     dequantized weights to |y - ref| <= 1e-4*|ref| + 1e-6 (ref accumulated in
+ *     double), and a row's bits never depend on how many rows share the call.
+ *   INT8ACT: activations quantized per row to int8 exactly as qmat.c:186-202;
+ *     integer block sums are exact (the reference's small-T path, qmat.c:508-552).
+ *     Supported for INT8, INT4, Q8_0 and Q4_0 weights.
+ *
+ * Return values: 0 = done, -1 = not done (the caller runs its CPU path);
+ * mynah_asr_hip_last_error() names the reason for the calling thread.
+ * Thread safety: every entry point may be called from many threads at once;
+ * each thread gets its own HIP stream and device buffers, and the weight cache
+ * is shared under a lock. */
+#ifndef MYNAH_ASR_HIP_H
+#define MYNAH_ASR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Weight formats. 0..2 are qmat.h's own (src/qmat.h:23); the ggml block formats
+ * are 16 + their GGML type id (third_party/ingot/tests/fixtures/geometry.txt). */
+enum {
+    MYNAH_ASR_HIP_F32 = 0,   /* float [n, k] */
+    MYNAH_ASR_HIP_INT8 = 1,  /* qmat per-row: int8 [n, k] + float scales [n] */
+    MYNAH_ASR_HIP_INT4 = 2,  /* qmat group-32: uint8 [n, k/2] (elements 2j | 2j+1<<4) + float [n, k/32] */
+    MYNAH_ASR_HIP_Q4_0 = 18, /* ggml blocks, GGUF byte layout, row-major [n, k/block] */
+    MYNAH_ASR_HIP_Q8_0 = 24,
+    MYNAH_ASR_HIP_Q2_K = 26,
+    MYNAH_ASR_HIP_Q3_K = 27,
+    MYNAH_ASR_HIP_Q4_K = 28,
+    MYNAH_ASR_HIP_Q5_K = 29,
+    MYNAH_ASR_HIP_Q6_K = 30
+};
+
+enum { MYNAH_ASR_HIP_EXACT = 0, MYNAH_ASR_HIP_INT8ACT = 1 };
+
+/* A weight matrix as the caller holds it in host memory: the fields of
+ * mynah_asr_qmat (src/qmat.h:39-47) plus the raw ggml block pointer. `data` is
+ * also the cache key: it must stay valid and unchanged until evicted
+ * (src/backend.h:16-18). */
+typedef struct {
+    int qtype;
+    int n, k;
+    const void *data;     /* F32 floats, INT8/INT4 quants, or ggml block bytes */
+    const float *scales;  /* INT8 [n], INT4 [n, k/32]; NULL for the other formats */
+} mynah_asr_hip_wdesc;
+
+/* 1 when a gfx950 device is present and usable. Replaces
+ * mynah_asr_cuda_available (src/cuda_gemm.cu:62, declared src/backend.c:24). */
+int mynah_asr_hip_available(void);
+
+/* Process-wide numerics mode (MYNAH_ASR_HIP_EXACT / _INT8ACT). Returns the
+ * mode now in force. The environment variable MYNAH_ASR_HIP_NUMERICS=int8
+ * selects INT8ACT at first use. No reference counterpart: it exposes the
+ * choice qmat.c makes by row count (src/qmat.c:180, 508, 644) as a fixed
+ * setting, so a row's result never depends on the batch size. */
+int mynah_asr_hip_set_numerics(int mode);
+int mynah_asr_hip_numerics(void);
+
+/* ---- host-pointer entry points (the drop-in boundary) ---------------------- */
+
+/* out[T,n] = x[T,k] . w[n,k]^T with f32 weights. Replaces
+ * mynah_asr_cuda_gemm_wt (src/cuda_gemm.cu:144-190); caller mynah_asr_gemm_wt
+ * (src/backend.c:68-81). */
+int mynah_asr_hip_gemm_wt(const float *x, const float *w, float *out, int T, int n, int k);
+
+/* out[T,n2] = SiLU(x . w1^T) . w2^T, the intermediate kept on the device.
+ * Same contract as mynah_asr_metal_ffn_wt (src/backend.c:17-18); caller
+ * mynah_asr_ffn_wt (src/backend.c:110-120). x may alias out. */
+int mynah_asr_hip_ffn_wt(const float *x, const float *w1, int n1, const float *w2, int n2,
+                         float *out, int T, int k);
+
+/* Three GEMMs over one input. Same contract as mynah_asr_metal_gemm3_wt
+ * (src/backend.c:19-21); caller mynah_asr_gemm3_wt (src/backend.c:122-132). */
+int mynah_asr_hip_gemm3_wt(const float *x, const float *wa, const float *wb, const float *wc,
+                           float *oa, float *ob, float *oc, int T, int n, int k);
+
+/* out[T,n] = x[T,k] . W^T for any supported format. The HIP branch of
+ * mynah_asr_qmat_mul (src/qmat.c:503-651). */
+int mynah_asr_hip_qgemm(const mynah_asr_hip_wdesc *w, const float *x, float *out, int T);
+
+/* out = SiLU(x . W1^T) . W2^T. The HIP branch of mynah_asr_qmat_ffn
+ * (src/qmat.c:654-663). x may alias out (src/encoder.c:474 passes the same
+ * buffer). */
+int mynah_asr_hip_qffn(const mynah_asr_hip_wdesc *w1, const mynah_asr_hip_wdesc *w2,
+                       const float *x, float *out, int T);
+
+/* q/k/v over one input (the input is prepared once). The HIP branch of
+ * mynah_asr_qmat_qkv (src/qmat.c:665-674). */
+int mynah_asr_hip_qqkv(const mynah_asr_hip_wdesc *wq, const mynah_asr_hip_wdesc *wk,
+                       const mynah_asr_hip_wdesc *wv, const float *x, float *oq, float *ok,
+                       float *ov, int T);
+
+/* wd[n,k] = the dequantized weight, decoded on the device from the resident
+ * copy (bit-identical to ingot's dequant.c and qmat.c:152-169). The HIP branch
+ * of mynah_asr_qmat_dequant (src/qmat.c:171-177). */
+int mynah_asr_hip_dequant(const mynah_asr_hip_wdesc *w, float *wd);
+
+/* Drop resident copies. The reference's CUDA unit never evicts
+ * (src/cuda_gemm.cu:92-130); the Metal one evicts on model free
+ * (mynah_asr_metal_weights_evict, src/backend.h:55-57). Call from
+ * mynah_asr_qmat_free / mynah_asr_free. */
+void mynah_asr_hip_evict(const void *data);
+void mynah_asr_hip_evict_all(void);
+
+/* Reason for the last -1 returned on this thread ("" when none). */
+const char *mynah_asr_hip_last_error(void);
+
+/* ---- device-resident entry points ----------------------------------------
+ * For callers that keep activations on the device (the fused encoder layer,
+ * the AED decoder loop, benchmarks). `dx`/`dy` are device pointers, `stream`
+ * a hipStream_t (NULL = the calling thread's stream). No reference
+ * counterpart: the reference copies activations per call
+ * (src/cuda_gemm.cu:167-188). */
+typedef struct mynah_asr_hip_weight mynah_asr_hip_weight;
+
+/* Upload + repack into the device layout; NULL on failure. */
+mynah_asr_hip_weight *mynah_asr_hip_weight_create(const mynah_asr_hip_wdesc *w);
+void mynah_asr_hip_weight_destroy(mynah_asr_hip_weight *w);
+/* Device bytes the resident copy occupies. */
+size_t mynah_asr_hip_weight_bytes(const mynah_asr_hip_weight *w);
+
+/* dy[T,n] = dx[T,k] . W^T; act = 0 none, 1 SiLU applied to the output. */
+int mynah_asr_hip_qgemm_dev(const mynah_asr_hip_weight *w, const float *dx, float *dy, int T,
+                            int act, void *stream);
+/* dwd[n,k] = dequantized weight. */
+int mynah_asr_hip_dequant_dev(const mynah_asr_hip_weight *w, float *dwd, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,76 @@
+"""Build the gfx950 backend unit and the C11 host mirror, in-tree.
+
+    python mynah-asr_amd/build.py          # both libraries
+Outputs (git-ignored, shipped with the tree):
+    mynah-asr_amd/lib/libmynah_asr_hip.so  C ABI of include/mynah_asr_hip.h
+    mynah-asr_amd/lib/libmynah_asr.so      C11 mirror of qmat.h / backend.h
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+HOST = os.path.join(PKG, "host")
+LIB = os.path.join(PKG, "lib")
+INC = os.path.join(ROOT, "include")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+HIP_LIB = os.path.join(LIB, "libmynah_asr_hip.so")
+HOST_LIB = os.path.join(LIB, "libmynah_asr.so")
+
+# -packed-fp32-ops: no v_pk_*_f32 in generated code; -ffp-contract=off: every
+# fused multiply-add in the kernels is an explicit fmaf, so all kernels that
+# share a device function perform the same float operations.
+HIP_FLAGS = ["-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC", "-ffp-contract=off",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-Wall", "-Wno-unused-function", "-I", INC, "-I", CSRC]
+
+
+def _run(cmd: list[str]) -> None:
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature: harmless
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in r.stderr.splitlines() if noise not in l)
+    if r.returncode != 0:
+        sys.stderr.write(err + "\n")
+        raise RuntimeError(f"build failed: {' '.join(cmd[:3])} ...")
+    if err.strip():
+        sys.stderr.write(err + "\n")
+
+
+def build_hip() -> str:
+    os.makedirs(LIB, exist_ok=True)
+    srcs = [os.path.join(CSRC, f) for f in ("kernels.hip", "backend.cpp", "repack.cpp")]
+    objs = []
+    for s in srcs:
+        o = os.path.join(LIB, os.path.basename(s) + ".o")
+        _run([HIPCC, *HIP_FLAGS, "-x", "hip", "-c", s, "-o", o])
+        objs.append(o)
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", HIP_LIB, *objs])
+    for o in objs:
+        os.remove(o)
+    return HIP_LIB
+
+
+def build_host() -> str:
+    srcs = [os.path.join(HOST, f) for f in ("qmat.c", "backend.c", "synth.c")]
+    if not all(os.path.exists(s) for s in srcs):
+        return ""
+    _run(["gcc", "-std=c11", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", "-ffp-contract=off",
+          "-I", INC, "-I", HOST, "-o", HOST_LIB, *srcs,
+          "-L", LIB, "-lmynah_asr_hip", "-Wl,-rpath,$ORIGIN", "-lm", "-lpthread"])
+    return HOST_LIB
+
+
+def build() -> None:
+    build_hip()
+    build_host()
+
+
+if __name__ == "__main__":
+    build()
+    print("built", HIP_LIB, HOST_LIB if os.path.exists(HOST_LIB) else "")

@@ -1,0 +1,397 @@
+// backend.cpp — the C ABI of include/mynah_asr_hip.h.
+//
+// Structure (the roles of src/cuda_gemm.cu, built the MI355X way):
+//   * a process-wide resident weight cache keyed by the caller's host pointer,
+//     holding each weight in the repacked device layout (repack.cpp), guarded
+//     by one mutex held only around the cache (src/cuda_gemm.cu:92-130);
+//   * a per-thread context: one HIP stream (default priority) and grow-only
+//     device buffers for activations, outputs and the prepared-activation
+//     workspace (src/cuda_gemm.cu:50-90);
+//   * every host-pointer entry point = H2D copy of x, prep + GEMM kernels on the
+//     thread's stream, D2H copy of out, stream sync. 0 = done, -1 = the caller
+//     runs its CPU path (src/backend.c:74-77).
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "fmt.h"
+#include "launch.h"
+#include "mynah_asr_hip.h"
+#include "repack.h"
+
+struct mynah_asr_hip_weight {
+    DevW dw;
+    int qtype;
+    void *mem;
+    size_t bytes;
+};
+
+namespace {
+
+std::mutex g_mu;
+int g_ready = -1;
+int g_numerics = -1;
+
+struct CacheEnt {
+    const void *key;
+    int qtype, n, k;
+    mynah_asr_hip_weight *w;
+};
+std::vector<CacheEnt> g_cache;
+
+thread_local char t_err[256];
+
+int fail(const char *msg, const char *detail = nullptr) {
+    snprintf(t_err, sizeof t_err, "%s%s%s", msg, detail ? ": " : "", detail ? detail : "");
+    return -1;
+}
+
+// grow-only device buffer
+struct DBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+    void *get(size_t bytes) {
+        if (bytes == 0) bytes = 256;
+        if (p && cap >= bytes) return p;
+        size_t want = cap ? cap : ((size_t)1 << 20);
+        while (want < bytes) want *= 2;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+        if (hipMalloc(&p, want) != hipSuccess) { p = nullptr; return nullptr; }
+        cap = want;
+        return p;
+    }
+};
+
+struct Ctx {
+    int state = 0;  // 0 uninitialised, 1 ok, -1 failed
+    hipStream_t st = nullptr;
+    DBuf x, y, h, xp, xs16, xsh;
+};
+thread_local Ctx t_ctx;
+
+Ctx *ctx() {
+    if (t_ctx.state == 0)
+        t_ctx.state = hipStreamCreateWithFlags(&t_ctx.st, hipStreamNonBlocking) == hipSuccess ? 1 : -1;
+    return t_ctx.state == 1 ? &t_ctx : nullptr;
+}
+
+hipStream_t pick_stream(void *s) {
+    if (s) return (hipStream_t)s;
+    Ctx *c = ctx();
+    return c ? c->st : nullptr;
+}
+
+bool wants_xsum(int qtype) {
+    return qtype == MYNAH_ASR_HIP_Q4_K || qtype == MYNAH_ASR_HIP_Q5_K || qtype == MYNAH_ASR_HIP_Q2_K;
+}
+
+mynah_asr_hip_weight *upload(const mynah_asr_hip_wdesc *w) {
+    HostLayout L;
+    if (mh_repack(w, &L) != 0) {
+        fail("unsupported weight format or shape");
+        return nullptr;
+    }
+    size_t off[4];
+    const size_t bytes = mh_layout_bytes(L, off);
+    void *mem = nullptr;
+    if (hipMalloc(&mem, bytes) != hipSuccess) {
+        fail("hipMalloc for a weight failed");
+        return nullptr;
+    }
+    uint8_t *b = (uint8_t *)mem;
+    hipError_t e = hipSuccess;
+    if (!L.p0.empty()) e = hipMemcpy(b + off[0], L.p0.data(), L.p0.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess && !L.p1.empty()) e = hipMemcpy(b + off[1], L.p1.data(), L.p1.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess && !L.h.empty()) e = hipMemcpy(b + off[2], L.h.data(), L.h.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess && !L.h2.empty())
+        e = hipMemcpy(b + off[3], L.h2.data(), L.h2.size() * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(mem);
+        fail("weight upload failed", hipGetErrorString(e));
+        return nullptr;
+    }
+    auto *W = new mynah_asr_hip_weight;
+    W->qtype = w->qtype;
+    W->mem = mem;
+    W->bytes = bytes;
+    W->dw.p0 = b + off[0];
+    W->dw.p1 = b + off[1];
+    W->dw.h = b + off[2];
+    W->dw.h2 = (const float *)(b + off[3]);
+    W->dw.n = w->n;
+    W->dw.k = w->k;
+    W->dw.Np = L.Np;
+    W->dw.Kp = L.Kp;
+    return W;
+}
+
+// resident copy for a host weight (uploaded on first use)
+const mynah_asr_hip_weight *resident(const mynah_asr_hip_wdesc *w) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (auto &e : g_cache)
+        if (e.key == w->data && e.qtype == w->qtype && e.n == w->n && e.k == w->k) return e.w;
+    mynah_asr_hip_weight *W = upload(w);
+    if (!W) return nullptr;
+    g_cache.push_back({w->data, w->qtype, w->n, w->k, W});
+    return W;
+}
+
+int check_numerics_supported(int qtype) {
+    if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT) return 0;
+    (void)qtype;
+    return fail("INT8ACT numerics are not implemented in this build");
+}
+
+// prep x (device) for a product with inner size k; returns prepared buffers
+int prep(Ctx *c, const float *dx, int T, int k, int Kp, bool xsum, hipStream_t st, uint8_t **xp,
+         float **xs16, int **xsh) {
+    const int Mpad = mh_mpad(T);
+    *xp = (uint8_t *)c->xp.get((size_t)Mpad * Kp * 4);
+    *xs16 = (float *)c->xs16.get((size_t)Mpad * (Kp / 16) * sizeof(float));
+    *xsh = (int *)c->xsh.get((size_t)Mpad * sizeof(int));
+    if (!*xp || !*xs16 || !*xsh) return fail("workspace allocation failed");
+    const int vec = (k % 4 == 0) && (((uintptr_t)dx & 15) == 0);
+    hipError_t e = mh_launch_prep(dx, T, k, Kp, Mpad, *xp, *xs16, *xsh, xsum ? 1 : 0, vec, st);
+    if (e != hipSuccess) return fail("prep launch failed", hipGetErrorString(e));
+    return 0;
+}
+
+int gemm_dev(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, float *dy, int T, int act,
+             hipStream_t st) {
+    uint8_t *xp;
+    float *xs16;
+    int *xsh;
+    if (prep(c, dx, T, W->dw.k, W->dw.Kp, wants_xsum(W->qtype), st, &xp, &xs16, &xsh)) return -1;
+    hipError_t e = mh_launch_gemm(W->qtype, W->dw, xp, xs16, xsh, dy, T, act, st);
+    if (e != hipSuccess) return fail("gemm launch failed", hipGetErrorString(e));
+    return 0;
+}
+
+int h2d(Ctx *c, DBuf &b, const float *x, size_t n, float **d) {
+    *d = (float *)b.get(n * sizeof(float));
+    if (!*d) return fail("device buffer allocation failed");
+    if (hipMemcpyAsync(*d, x, n * sizeof(float), hipMemcpyHostToDevice, c->st) != hipSuccess)
+        return fail("H2D copy failed");
+    return 0;
+}
+
+int d2h_sync(Ctx *c, float *out, const float *d, size_t n) {
+    if (hipMemcpyAsync(out, d, n * sizeof(float), hipMemcpyDeviceToHost, c->st) != hipSuccess)
+        return fail("D2H copy failed");
+    hipError_t e = hipStreamSynchronize(c->st);
+    if (e != hipSuccess) return fail("stream sync failed", hipGetErrorString(e));
+    return 0;
+}
+
+int begin(Ctx **c) {
+    t_err[0] = 0;
+    if (!mynah_asr_hip_available()) return fail("no gfx950 device");
+    *c = ctx();
+    if (!*c) return fail("stream creation failed");
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mynah_asr_hip_available(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_ready < 0) {
+        int n = 0;
+        g_ready = 0;
+        if (hipGetDeviceCount(&n) == hipSuccess && n > 0) {
+            hipDeviceProp_t p;
+            if (hipGetDeviceProperties(&p, 0) == hipSuccess && strncmp(p.gcnArchName, "gfx950", 6) == 0)
+                g_ready = 1;
+        }
+    }
+    return g_ready == 1;
+}
+
+int mynah_asr_hip_set_numerics(int mode) {
+    if (mode == MYNAH_ASR_HIP_EXACT || mode == MYNAH_ASR_HIP_INT8ACT) g_numerics = mode;
+    return mynah_asr_hip_numerics();
+}
+
+int mynah_asr_hip_numerics(void) {
+    if (g_numerics < 0) {
+        const char *e = getenv("MYNAH_ASR_HIP_NUMERICS");
+        g_numerics = (e && strcmp(e, "int8") == 0) ? MYNAH_ASR_HIP_INT8ACT : MYNAH_ASR_HIP_EXACT;
+    }
+    return g_numerics;
+}
+
+const char *mynah_asr_hip_last_error(void) { return t_err; }
+
+mynah_asr_hip_weight *mynah_asr_hip_weight_create(const mynah_asr_hip_wdesc *w) {
+    t_err[0] = 0;
+    if (!mynah_asr_hip_available()) { fail("no gfx950 device"); return nullptr; }
+    return upload(w);
+}
+
+void mynah_asr_hip_weight_destroy(mynah_asr_hip_weight *w) {
+    if (!w) return;
+    (void)hipFree(w->mem);
+    delete w;
+}
+
+size_t mynah_asr_hip_weight_bytes(const mynah_asr_hip_weight *w) { return w ? w->bytes : 0; }
+
+int mynah_asr_hip_qgemm_dev(const mynah_asr_hip_weight *w, const float *dx, float *dy, int T, int act,
+                            void *stream) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    if (!w || !dx || !dy || T < 0) return fail("bad argument");
+    if (T == 0) return 0;
+    if (check_numerics_supported(w->qtype)) return -1;
+    return gemm_dev(c, w, dx, dy, T, act, pick_stream(stream));
+}
+
+int mynah_asr_hip_dequant_dev(const mynah_asr_hip_weight *w, float *dwd, void *stream) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    if (!w || !dwd) return fail("bad argument");
+    if (w->qtype == MYNAH_ASR_HIP_F32) return fail("F32 weights are not decoded (plain copy)");
+    hipError_t e = mh_launch_dequant(w->qtype, w->dw, dwd, pick_stream(stream));
+    if (e != hipSuccess) return fail("dequant launch failed", hipGetErrorString(e));
+    return 0;
+}
+
+int mynah_asr_hip_qgemm(const mynah_asr_hip_wdesc *w, const float *x, float *out, int T) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    if (!w || !x || !out || T < 0) return fail("bad argument");
+    if (T == 0) return 0;
+    if (check_numerics_supported(w->qtype)) return -1;
+    const mynah_asr_hip_weight *W = resident(w);
+    if (!W) return -1;
+    float *dx, *dy = (float *)c->y.get((size_t)T * w->n * sizeof(float));
+    if (!dy) return fail("device buffer allocation failed");
+    if (h2d(c, c->x, x, (size_t)T * w->k, &dx)) return -1;
+    if (gemm_dev(c, W, dx, dy, T, 0, c->st)) return -1;
+    return d2h_sync(c, out, dy, (size_t)T * w->n);
+}
+
+int mynah_asr_hip_qffn(const mynah_asr_hip_wdesc *w1, const mynah_asr_hip_wdesc *w2, const float *x,
+                       float *out, int T) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    if (!w1 || !w2 || !x || !out || T < 0 || w2->k != w1->n) return fail("bad argument");
+    if (T == 0) return 0;
+    if (check_numerics_supported(w1->qtype) || check_numerics_supported(w2->qtype)) return -1;
+    const mynah_asr_hip_weight *W1 = resident(w1), *W2 = resident(w2);
+    if (!W1 || !W2) return -1;
+    float *dx, *dh = (float *)c->h.get((size_t)T * w1->n * sizeof(float));
+    float *dy = (float *)c->y.get((size_t)T * w2->n * sizeof(float));
+    if (!dh || !dy) return fail("device buffer allocation failed");
+    if (h2d(c, c->x, x, (size_t)T * w1->k, &dx)) return -1;  // x is consumed before out is written
+    if (gemm_dev(c, W1, dx, dh, T, 1, c->st)) return -1;
+    if (gemm_dev(c, W2, dh, dy, T, 0, c->st)) return -1;
+    return d2h_sync(c, out, dy, (size_t)T * w2->n);
+}
+
+int mynah_asr_hip_qqkv(const mynah_asr_hip_wdesc *wq, const mynah_asr_hip_wdesc *wk,
+                       const mynah_asr_hip_wdesc *wv, const float *x, float *oq, float *ok, float *ov,
+                       int T) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    if (!wq || !wk || !wv || !x || !oq || !ok || !ov || T < 0 || wk->k != wq->k || wv->k != wq->k)
+        return fail("bad argument");
+    if (T == 0) return 0;
+    const mynah_asr_hip_wdesc *ws[3] = {wq, wk, wv};
+    float *outs[3] = {oq, ok, ov};
+    const mynah_asr_hip_weight *W[3];
+    for (int i = 0; i < 3; i++) {
+        if (check_numerics_supported(ws[i]->qtype)) return -1;
+        if (!(W[i] = resident(ws[i]))) return -1;
+    }
+    float *dx;
+    if (h2d(c, c->x, x, (size_t)T * wq->k, &dx)) return -1;
+    // one prepared input serves the three products when their formats agree
+    // on the activation sums; otherwise it is prepared per product
+    const bool same = W[0]->dw.Kp == W[1]->dw.Kp && W[0]->dw.Kp == W[2]->dw.Kp &&
+                      wants_xsum(W[0]->qtype) == wants_xsum(W[1]->qtype) &&
+                      wants_xsum(W[0]->qtype) == wants_xsum(W[2]->qtype);
+    uint8_t *xp = nullptr;
+    float *xs16 = nullptr;
+    int *xsh = nullptr;
+    for (int i = 0; i < 3; i++) {
+        if (i == 0 || !same)
+            if (prep(c, dx, T, wq->k, W[i]->dw.Kp, wants_xsum(W[i]->qtype), c->st, &xp, &xs16, &xsh))
+                return -1;
+        float *dy = (float *)c->y.get((size_t)T * ws[i]->n * sizeof(float));
+        if (!dy) return fail("device buffer allocation failed");
+        hipError_t e = mh_launch_gemm(W[i]->qtype, W[i]->dw, xp, xs16, xsh, dy, T, 0, c->st);
+        if (e != hipSuccess) return fail("gemm launch failed", hipGetErrorString(e));
+        if (d2h_sync(c, outs[i], dy, (size_t)T * ws[i]->n)) return -1;
+    }
+    return 0;
+}
+
+int mynah_asr_hip_dequant(const mynah_asr_hip_wdesc *w, float *wd) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    if (!w || !wd) return fail("bad argument");
+    if (w->qtype == MYNAH_ASR_HIP_F32) return fail("F32 weights are not decoded (plain copy)");
+    const mynah_asr_hip_weight *W = resident(w);
+    if (!W) return -1;
+    float *dw = (float *)c->y.get((size_t)w->n * w->k * sizeof(float));
+    if (!dw) return fail("device buffer allocation failed");
+    hipError_t e = mh_launch_dequant(W->qtype, W->dw, dw, c->st);
+    if (e != hipSuccess) return fail("dequant launch failed", hipGetErrorString(e));
+    return d2h_sync(c, wd, dw, (size_t)w->n * w->k);
+}
+
+static mynah_asr_hip_wdesc f32_desc(const float *w, int n, int k) {
+    mynah_asr_hip_wdesc d;
+    d.qtype = MYNAH_ASR_HIP_F32;
+    d.n = n;
+    d.k = k;
+    d.data = w;
+    d.scales = nullptr;
+    return d;
+}
+
+int mynah_asr_hip_gemm_wt(const float *x, const float *w, float *out, int T, int n, int k) {
+    const mynah_asr_hip_wdesc d = f32_desc(w, n, k);
+    return mynah_asr_hip_qgemm(&d, x, out, T);
+}
+
+int mynah_asr_hip_ffn_wt(const float *x, const float *w1, int n1, const float *w2, int n2, float *out,
+                         int T, int k) {
+    const mynah_asr_hip_wdesc d1 = f32_desc(w1, n1, k), d2 = f32_desc(w2, n2, n1);
+    return mynah_asr_hip_qffn(&d1, &d2, x, out, T);
+}
+
+int mynah_asr_hip_gemm3_wt(const float *x, const float *wa, const float *wb, const float *wc, float *oa,
+                           float *ob, float *oc, int T, int n, int k) {
+    const mynah_asr_hip_wdesc a = f32_desc(wa, n, k), b = f32_desc(wb, n, k), c = f32_desc(wc, n, k);
+    return mynah_asr_hip_qqkv(&a, &b, &c, x, oa, ob, oc, T);
+}
+
+void mynah_asr_hip_evict(const void *data) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (size_t i = 0; i < g_cache.size();) {
+        if (g_cache[i].key == data) {
+            mynah_asr_hip_weight_destroy(g_cache[i].w);
+            g_cache.erase(g_cache.begin() + i);
+        } else {
+            i++;
+        }
+    }
+}
+
+void mynah_asr_hip_evict_all(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (auto &e : g_cache) mynah_asr_hip_weight_destroy(e.w);
+    g_cache.clear();
+}
+
+}  // extern "C"

@@ -1,0 +1,22 @@
+// launch.h — host-side launchers of kernels.hip (C++ linkage, library-internal).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+struct DevW;
+
+// Rows the prepared-activation buffer must hold for an M-row product: the
+// kernels read whole row groups up to this count.
+static inline int mh_mpad(int M) {
+    if (M <= 512) return (M + 31) / 32 * 32;
+    if (M <= 2048) return (M + 63) / 64 * 64;
+    return (M + 127) / 128 * 128;
+}
+
+hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,
+                          int *xsh, int want_xsum, int vec, hipStream_t st);
+hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
+                          const int *xsh, float *y, int M, int act, hipStream_t st);
+hipError_t mh_launch_dequant(int qtype, const DevW &W, float *out, hipStream_t st);
+hipError_t mh_launch_silu(float *x, size_t n, hipStream_t st);

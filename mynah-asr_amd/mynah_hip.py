@@ -1,0 +1,231 @@
+"""ctypes view of the MI355X backend unit and its C11 host mirror.
+
+Loads the in-tree libraries built by ``build.py``:
+  lib/libmynah_asr_hip.so  include/mynah_asr_hip.h (kernels + C ABI)
+  lib/libmynah_asr.so      the qmat.h / backend.h mirror and synth.h
+Loading fails loudly when they are missing: there is no Python or CPU
+fallback for any product.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+HIP_LIB = os.path.join(PKG, "lib", "libmynah_asr_hip.so")
+HOST_LIB = os.path.join(PKG, "lib", "libmynah_asr.so")
+
+F32, INT8, INT4 = 0, 1, 2
+Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 18, 24, 26, 27, 28, 29, 30
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q2_K: (256, 84), Q3_K: (256, 110),
+         Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
+NAMES = {F32: "F32", INT8: "INT8", INT4: "INT4", Q4_0: "Q4_0", Q8_0: "Q8_0", Q2_K: "Q2_K",
+         Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
+# bits per weight as stored (algorithmic HBM bytes of a weight = n*k*bits/8)
+BITS = {F32: 32.0, INT8: 8.0, INT4: 5.0, Q4_0: 4.5, Q8_0: 8.5, Q2_K: 2.625, Q3_K: 3.4375,
+        Q4_K: 4.5, Q5_K: 5.5, Q6_K: 6.5625}
+EXACT, INT8ACT = 0, 1
+
+# every symbol include/mynah_asr_hip.h declares
+HIP_SYMBOLS = [
+    "mynah_asr_hip_available", "mynah_asr_hip_set_numerics", "mynah_asr_hip_numerics",
+    "mynah_asr_hip_gemm_wt", "mynah_asr_hip_ffn_wt", "mynah_asr_hip_gemm3_wt",
+    "mynah_asr_hip_qgemm", "mynah_asr_hip_qffn", "mynah_asr_hip_qqkv", "mynah_asr_hip_dequant",
+    "mynah_asr_hip_evict", "mynah_asr_hip_evict_all", "mynah_asr_hip_last_error",
+    "mynah_asr_hip_weight_create", "mynah_asr_hip_weight_destroy", "mynah_asr_hip_weight_bytes",
+    "mynah_asr_hip_qgemm_dev", "mynah_asr_hip_dequant_dev",
+]
+HOST_SYMBOLS = [
+    "mynah_asr_set_backend", "mynah_asr_backend", "mynah_asr_gemm_wt", "mynah_asr_silu",
+    "mynah_asr_ffn_wt", "mynah_asr_gemm3_wt", "mynah_asr_set_cpu_fallback",
+    "mynah_asr_qmat_init", "mynah_asr_qmat_init_blocks", "mynah_asr_qmat_free",
+    "mynah_asr_qmat_mul", "mynah_asr_qmat_ffn", "mynah_asr_qmat_qkv", "mynah_asr_qmat_dequant",
+    "mynah_asr_quantize_int8", "mynah_asr_quantize_int4",
+    "mynah_synth_randn", "mynah_synth_quantize", "mynah_synth_nbytes",
+]
+
+_P = C.c_void_p
+
+
+class WDesc(C.Structure):
+    _fields_ = [("qtype", C.c_int), ("n", C.c_int), ("k", C.c_int),
+                ("data", C.c_void_p), ("scales", C.c_void_p)]
+
+
+class QMat(C.Structure):
+    """mynah_asr_qmat (host/qmat.h)."""
+    _fields_ = [("f32", C.c_void_p), ("q8", C.c_void_p), ("q4", C.c_void_p),
+                ("scales", C.c_void_p), ("owned_q", C.c_void_p), ("owned_s", C.c_void_p),
+                ("qtype", C.c_int), ("n", C.c_int), ("k", C.c_int), ("blocks", C.c_void_p)]
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(_P)
+
+
+def weight_bytes(qtype: int, n: int, k: int) -> int:
+    """Algorithmic bytes of a weight as the caller stores it."""
+    if qtype in BLOCK:
+        be, bb = BLOCK[qtype]
+        return n * (k // be) * bb
+    if qtype == F32:
+        return 4 * n * k
+    if qtype == INT8:
+        return n * k + 4 * n
+    return n * k // 2 + 4 * n * (k // 32)
+
+
+class HipLib:
+    def __init__(self, path: str = HIP_LIB, host_path: str = HOST_LIB):
+        if not os.path.exists(path) or not os.path.exists(host_path):
+            raise RuntimeError(f"backend libraries not built ({path}); run mynah-asr_amd/build.py")
+        L = C.CDLL(path, mode=C.RTLD_GLOBAL)
+        H = C.CDLL(host_path)
+        self.L, self.H, self.path, self.host_path = L, H, path, host_path
+        L.mynah_asr_hip_last_error.restype = C.c_char_p
+        L.mynah_asr_hip_weight_create.restype = _P
+        L.mynah_asr_hip_weight_create.argtypes = [C.POINTER(WDesc)]
+        L.mynah_asr_hip_weight_destroy.argtypes = [_P]
+        L.mynah_asr_hip_weight_bytes.restype = C.c_size_t
+        L.mynah_asr_hip_weight_bytes.argtypes = [_P]
+        L.mynah_asr_hip_qgemm_dev.argtypes = [_P, _P, _P, C.c_int, C.c_int, _P]
+        L.mynah_asr_hip_dequant_dev.argtypes = [_P, _P, _P]
+        L.mynah_asr_hip_qgemm.argtypes = [C.POINTER(WDesc), _P, _P, C.c_int]
+        L.mynah_asr_hip_qffn.argtypes = [C.POINTER(WDesc), C.POINTER(WDesc), _P, _P, C.c_int]
+        L.mynah_asr_hip_qqkv.argtypes = [C.POINTER(WDesc)] * 3 + [_P] * 4 + [C.c_int]
+        L.mynah_asr_hip_dequant.argtypes = [C.POINTER(WDesc), _P]
+        L.mynah_asr_hip_gemm_wt.argtypes = [_P, _P, _P, C.c_int, C.c_int, C.c_int]
+        L.mynah_asr_hip_evict.argtypes = [_P]
+        H.mynah_synth_randn.argtypes = [C.c_uint64, C.c_double, _P, C.c_size_t]
+        H.mynah_synth_quantize.restype = C.c_size_t
+        H.mynah_synth_quantize.argtypes = [C.c_int, _P, C.c_size_t, _P]
+        H.mynah_synth_nbytes.restype = C.c_size_t
+        H.mynah_synth_nbytes.argtypes = [C.c_int, C.c_size_t]
+        H.mynah_asr_set_backend.argtypes = [C.c_char_p]
+        H.mynah_asr_qmat_init.argtypes = [C.POINTER(QMat), _P, C.c_int, C.c_int, C.c_int]
+        H.mynah_asr_qmat_init_blocks.argtypes = [C.POINTER(QMat), _P, C.c_int, C.c_int, C.c_int]
+        H.mynah_asr_qmat_free.argtypes = [C.POINTER(QMat)]
+        H.mynah_asr_qmat_mul.argtypes = [C.POINTER(QMat), _P, _P, C.c_int]
+        H.mynah_asr_qmat_ffn.argtypes = [C.POINTER(QMat), C.POINTER(QMat), _P, _P, C.c_int, _P]
+        H.mynah_asr_qmat_qkv.argtypes = [C.POINTER(QMat)] * 3 + [_P] * 4 + [C.c_int]
+        H.mynah_asr_qmat_dequant.argtypes = [C.POINTER(QMat), _P]
+        H.mynah_asr_gemm_wt.argtypes = [_P, _P, _P, C.c_int, C.c_int, C.c_int]
+        H.mynah_asr_quantize_int8.argtypes = [_P, C.c_int, C.c_int, _P, _P]
+        H.mynah_asr_quantize_int4.argtypes = [_P, C.c_int, C.c_int, _P, _P]
+
+    # ------------------------------------------------------------- basics
+    def available(self) -> bool:
+        return bool(self.L.mynah_asr_hip_available())
+
+    def last_error(self) -> str:
+        return self.L.mynah_asr_hip_last_error().decode()
+
+    def set_numerics(self, mode: int) -> int:
+        return self.L.mynah_asr_hip_set_numerics(mode)
+
+    def _check(self, rc: int, what: str) -> None:
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: {self.last_error()}")
+
+    # ------------------------------------------------------ synthetic data
+    def randn(self, seed: int, sigma: float, shape) -> np.ndarray:
+        out = np.empty(int(np.prod(shape)), dtype=np.float32)
+        self.H.mynah_synth_randn(seed, sigma, _ptr(out), out.size)
+        return out.reshape(shape)
+
+    def quantize(self, qtype: int, w: np.ndarray) -> np.ndarray:
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        nb = self.H.mynah_synth_nbytes(qtype, w.size)
+        if nb == 0:
+            raise ValueError(f"cannot quantize {w.size} values to {NAMES.get(qtype, qtype)}")
+        out = np.empty(nb, dtype=np.uint8)
+        assert self.H.mynah_synth_quantize(qtype, _ptr(w), w.size, _ptr(out)) == nb
+        return out
+
+    def quantize_int8(self, w: np.ndarray):
+        n, k = w.shape
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        q = np.empty((n, k), dtype=np.int8)
+        s = np.empty(n, dtype=np.float32)
+        self.H.mynah_asr_quantize_int8(_ptr(w), n, k, _ptr(q), _ptr(s))
+        return q, s
+
+    def quantize_int4(self, w: np.ndarray):
+        n, k = w.shape
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        q = np.empty((n, k // 2), dtype=np.uint8)
+        s = np.empty((n, k // 32), dtype=np.float32)
+        self.H.mynah_asr_quantize_int4(_ptr(w), n, k, _ptr(q), _ptr(s))
+        return q, s
+
+
+class Weight:
+    """A host weight (numpy arrays kept alive) + its descriptor."""
+
+    def __init__(self, qtype: int, n: int, k: int, data: np.ndarray, scales: np.ndarray | None = None):
+        self.qtype, self.n, self.k = qtype, n, k
+        self.data = np.ascontiguousarray(data)
+        self.scales = None if scales is None else np.ascontiguousarray(scales, dtype=np.float32)
+        self.desc = WDesc(qtype, n, k, self.data.ctypes.data,
+                          self.scales.ctypes.data if self.scales is not None else None)
+
+    @staticmethod
+    def make(lib: HipLib, qtype: int, w: np.ndarray) -> "Weight":
+        """Quantize an f32 [n, k] matrix into `qtype` with the library's quantizers."""
+        n, k = w.shape
+        if qtype == F32:
+            return Weight(F32, n, k, np.ascontiguousarray(w, dtype=np.float32))
+        if qtype == INT8:
+            q, s = lib.quantize_int8(w)
+            return Weight(INT8, n, k, q, s)
+        if qtype == INT4:
+            q, s = lib.quantize_int4(w)
+            return Weight(INT4, n, k, q, s)
+        return Weight(qtype, n, k, lib.quantize(qtype, w))
+
+    def nbytes(self) -> int:
+        return weight_bytes(self.qtype, self.n, self.k)
+
+
+class DeviceWeight:
+    """Resident copy created through mynah_asr_hip_weight_create."""
+
+    def __init__(self, lib: HipLib, w: Weight):
+        self.lib, self.w = lib, w
+        self.h = lib.L.mynah_asr_hip_weight_create(C.byref(w.desc))
+        if not self.h:
+            raise RuntimeError(f"weight_create failed: {lib.last_error()}")
+
+    def close(self) -> None:
+        if self.h:
+            self.lib.L.mynah_asr_hip_weight_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def gemm(self, dx_ptr: int, dy_ptr: int, T: int, act: int = 0, stream: int = 0) -> None:
+        rc = self.lib.L.mynah_asr_hip_qgemm_dev(self.h, dx_ptr, dy_ptr, T, act, stream or None)
+        self.lib._check(rc, "qgemm_dev")
+
+    def dequant(self, dwd_ptr: int, stream: int = 0) -> None:
+        rc = self.lib.L.mynah_asr_hip_dequant_dev(self.h, dwd_ptr, stream or None)
+        self.lib._check(rc, "dequant_dev")
+
+
+def host_qgemm(lib: HipLib, w: Weight, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty((x.shape[0], w.n), dtype=np.float32)
+    lib._check(lib.L.mynah_asr_hip_qgemm(C.byref(w.desc), _ptr(x), _ptr(out), x.shape[0]), "qgemm")
+    return out
+
+
+def host_dequant(lib: HipLib, w: Weight) -> np.ndarray:
+    out = np.empty((w.n, w.k), dtype=np.float32)
+    lib._check(lib.L.mynah_asr_hip_dequant(C.byref(w.desc), _ptr(out)), "dequant")
+    return out

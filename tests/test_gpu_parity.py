@@ -1,0 +1,220 @@
+"""GPU parity of the HIP backend against the CPU oracle (EXACT numerics).
+
+Bar (stated where it is checked):
+  * dequantized weights: bit-exact (the reference's llama.cpp fixtures and the
+    oracle's decoders);
+  * f32 outputs: |y - ref| <= 1e-4*|ref| + 1e-6 per element, ref = the product
+    of the dequantized weights and the f32 inputs accumulated in double
+    (the reference's own self-test pattern, tests/test_qmat.c:39-45);
+  * rows: bit-identical across batch sizes M.
+Inputs: weights N(0, 0.02) seed 0 (quantized by the library's quantizers,
+pinned bit-exact to the reference's by test_host_lib), activations N(0, 1)
+seed 1.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import mynah_hip as M
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+FIX = os.path.join(os.path.dirname(__file__), "golden", "ingot_fixtures")
+TO_ORC = {M.Q4_0: O.Q4_0, M.Q8_0: O.Q8_0, M.Q2_K: O.Q2_K, M.Q3_K: O.Q3_K, M.Q4_K: O.Q4_K,
+          M.Q5_K: O.Q5_K, M.Q6_K: O.Q6_K}
+ALL = [M.F32, M.INT8, M.INT4, M.Q4_0, M.Q8_0, M.Q2_K, M.Q3_K, M.Q4_K, M.Q5_K, M.Q6_K]
+RTOL, ATOL = 1e-4, 1e-6
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def oracle_dequant(orc, w: M.Weight) -> np.ndarray:
+    if w.qtype == M.F32:
+        return w.data.reshape(w.n, w.k)
+    if w.qtype in (M.INT8, M.INT4):
+        return orc.qmat_dequant(w.qtype, w.data, w.scales, w.n, w.k)
+    return orc.dequant(TO_ORC[w.qtype], w.data, w.n * w.k).reshape(w.n, w.k)
+
+
+def check_close(y, ref, what):
+    err = np.abs(y.astype(np.float64) - ref)
+    bound = RTOL * np.abs(ref) + ATOL
+    bad = err > bound
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - bound), err.shape)
+        raise AssertionError(f"{what}: {bad.sum()} of {bad.size} outside 1e-4*|ref|+1e-6; "
+                             f"worst at {i}: y={y[i]!r} ref={ref[i]!r}")
+
+
+def kdim(qt):
+    return 1024 if qt in (M.Q2_K, M.Q3_K, M.Q4_K, M.Q5_K, M.Q6_K) else 1056
+
+
+# ---------------------------------------------------------------- dequant
+def _fixture_list():
+    out = []
+    for line in open(os.path.join(FIX, "manifest.txt")):
+        name, t, be, bb, nb = line.split()
+        out.append((name, int(t) + 16, int(be), int(nb)))
+    return out
+
+
+@pytest.mark.parametrize("name,qt,be,nb", _fixture_list())
+def test_dequant_reference_fixtures(gpu, name, qt, be, nb):
+    say("dequant fixture", name)
+    raw = np.fromfile(os.path.join(FIX, name + ".bin"), dtype=np.uint8)
+    ref = np.fromfile(os.path.join(FIX, name + ".ref"), dtype=np.float32)
+    k = 1024 if be == 256 else 512
+    n = nb * be // k
+    w = M.Weight(qt, n, k, raw)
+    got = M.host_dequant(gpu, w)
+    assert np.array_equal(got.ravel().view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("qt", [q for q in ALL if q != M.F32], ids=lambda q: M.NAMES[q])
+def test_dequant_random_weights(gpu, orc, qt):
+    say("dequant random", M.NAMES[qt])
+    k = kdim(qt)
+    w = M.Weight.make(gpu, qt, gpu.randn(0, 0.02, (200, k)))
+    got = M.host_dequant(gpu, w)
+    want = oracle_dequant(orc, w)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ------------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("T", [1, 3, 16, 17, 40, 300])
+@pytest.mark.parametrize("qt", ALL, ids=lambda q: M.NAMES[q])
+def test_gemm_matches_oracle(gpu, orc, qt, T):
+    say("gemm", M.NAMES[qt], "T", T)
+    k = kdim(qt)
+    w = M.Weight.make(gpu, qt, gpu.randn(0, 0.02, (200, k)))
+    x = gpu.randn(1, 1.0, (T, k))
+    y = M.host_qgemm(gpu, w, x)
+    ref = orc.gemm_f64(x, oracle_dequant(orc, w))
+    check_close(y, ref, f"{M.NAMES[qt]} T={T}")
+
+
+def test_gemm_zero_and_tiny_rows(gpu, orc):
+    say("gemm special rows")
+    w = M.Weight.make(gpu, M.Q8_0, gpu.randn(0, 0.02, (64, 256)))
+    x = gpu.randn(1, 1.0, (5, 256))
+    x[1] = 0.0
+    x[2] *= 1e-30
+    x[3] *= 1e20
+    y = M.host_qgemm(gpu, w, x)
+    ref = orc.gemm_f64(x, oracle_dequant(orc, w))
+    assert not y[1].any()
+    check_close(y, ref, "special rows")
+
+
+@pytest.mark.parametrize("n,k", [(1024, 4096), (4096, 1024), (16384, 1024)])
+@pytest.mark.parametrize("qt", [M.Q8_0, M.Q4_0], ids=lambda q: M.NAMES[q])
+def test_decoder_gemv_shapes(gpu, orc, qt, n, k):
+    """BASELINE config 3 shapes at M in {1, 4, 16}."""
+    say("gemv", M.NAMES[qt], n, k)
+    w = M.Weight.make(gpu, qt, gpu.randn(0, 0.02, (n, k)))
+    wd = oracle_dequant(orc, w)
+    for T in (1, 4, 16):
+        x = gpu.randn(1, 1.0, (T, k))
+        check_close(M.host_qgemm(gpu, w, x), orc.gemm_f64(x, wd), f"{n}x{k} T={T}")
+
+
+# --------------------------------------------------------- row stability
+@pytest.mark.parametrize("qt,n,k", [(M.Q8_0, 4096, 1024), (M.Q4_K, 1024, 4096), (M.F32, 1024, 1024)],
+                         ids=["Q8_0-1024to4096", "Q4_K-4096to1024", "F32-1024to1024"])
+def test_rows_bit_identical_across_M(gpu, orc, qt, n, k):
+    """A row's output bits do not depend on the batch size (M = 1, 7, 750, 6000)."""
+    import torch
+    say("row stability", M.NAMES[qt], n, k)
+    w = M.Weight.make(gpu, qt, gpu.randn(0, 0.02, (n, k)))
+    dw = M.DeviceWeight(gpu, w)
+    x = gpu.randn(1, 1.0, (6000, k))
+    xd = torch.from_numpy(x).cuda()
+    outs = {}
+    for T in (6000, 750, 7, 1):
+        yd = torch.empty((T, n), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        dw.gemm(xd.data_ptr(), yd.data_ptr(), T)
+        torch.cuda.synchronize()
+        outs[T] = yd.cpu().numpy()
+    # the single-row case also for a row that sits mid-tile in the big runs
+    for r in (5, 4321):
+        yd = torch.empty((1, n), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        dw.gemm(xd[r:r + 1].data_ptr(), yd.data_ptr(), 1)
+        torch.cuda.synchronize()
+        assert np.array_equal(yd.cpu().numpy()[0].view(np.uint32), outs[6000][r].view(np.uint32)), r
+    for T in (750, 7, 1):
+        assert np.array_equal(outs[T].view(np.uint32), outs[6000][:T].view(np.uint32)), T
+    # and the big run is right
+    check_close(outs[6000][:64], orc.gemm_f64(x[:64], oracle_dequant(orc, w)), "rows 0..63")
+    dw.close()
+
+
+# ------------------------------------------------------ fused entry points
+def test_ffn_and_qkv(gpu, orc):
+    import ctypes as C
+    say("ffn / qkv")
+    k, n1 = 256, 512
+    w1 = M.Weight.make(gpu, M.Q8_0, gpu.randn(0, 0.02, (n1, k)))
+    w2 = M.Weight.make(gpu, M.Q4_K, gpu.randn(2, 0.02, (k, n1)))
+    x = gpu.randn(1, 1.0, (37, k))
+    out = x.copy()  # aliasing as encoder.c:474 does
+    rc = gpu.L.mynah_asr_hip_qffn(C.byref(w1.desc), C.byref(w2.desc), out.ctypes.data, out.ctypes.data, 37)
+    assert rc == 0, gpu.last_error()
+    h = orc.gemm_f64(x, oracle_dequant(orc, w1))
+    h = (h / (1.0 + np.exp(-h))).astype(np.float32)
+    ref = orc.gemm_f64(h, oracle_dequant(orc, w2))
+    err = np.abs(out - ref)
+    assert (err <= 1e-4 * np.abs(ref) + 1e-5).all(), err.max()
+
+    ws = [M.Weight.make(gpu, qt, gpu.randn(10 + i, 0.02, (96, k))) for i, qt in
+          enumerate((M.Q8_0, M.Q6_K, M.F32))]
+    outs = [np.empty((37, 96), np.float32) for _ in range(3)]
+    rc = gpu.L.mynah_asr_hip_qqkv(*[C.byref(w.desc) for w in ws], x.ctypes.data,
+                                  *[o.ctypes.data for o in outs], 37)
+    assert rc == 0, gpu.last_error()
+    for w, o in zip(ws, outs):
+        check_close(o, orc.gemm_f64(x, oracle_dequant(orc, w)), "qkv " + M.NAMES[w.qtype])
+        assert np.array_equal(o, M.host_qgemm(gpu, w, x))
+
+
+def test_qmat_api_mirror(gpu, orc):
+    """The qmat.h entry points (the reference's own API) on the HIP backend."""
+    import ctypes as C
+    say("qmat mirror")
+    H = gpu.H
+    assert H.mynah_asr_set_backend(b"hip") == 3
+    rng_w = gpu.randn(0, 0.5, (96, 1024))
+    x = gpu.randn(1, 1.0, (48, 1024))
+    for qt in (0, 1, 2):
+        m = M.QMat()
+        assert H.mynah_asr_qmat_init(C.byref(m), rng_w.ctypes.data, 96, 1024, qt) == 0
+        out = np.empty((48, 96), np.float32)
+        H.mynah_asr_qmat_mul(C.byref(m), x.ctypes.data, out.ctypes.data, 48)
+        wd = np.empty((96, 1024), np.float32)
+        H.mynah_asr_qmat_dequant(C.byref(m), wd.ctypes.data)
+        if qt == 0:
+            assert np.array_equal(wd, rng_w)
+        else:
+            q = np.ctypeslib.as_array(C.cast(m.q8 if qt == 1 else m.q4, C.POINTER(C.c_uint8)),
+                                      shape=(96 * (1024 if qt == 1 else 512),))
+            s = np.ctypeslib.as_array(C.cast(m.scales, C.POINTER(C.c_float)),
+                                      shape=(96 if qt == 1 else 96 * 32,))
+            assert np.array_equal(wd, orc.qmat_dequant(qt, q.copy(), s.copy(), 96, 1024))
+        check_close(out, orc.gemm_f64(x, wd), f"qmat_mul qtype {qt}")
+        H.mynah_asr_qmat_free(C.byref(m))
+    # ggml blocks straight through qmat_init_blocks
+    raw = gpu.quantize(M.Q4_K, rng_w)
+    m = M.QMat()
+    assert H.mynah_asr_qmat_init_blocks(C.byref(m), raw.ctypes.data, 96, 1024, M.Q4_K) == 0
+    out = np.empty((48, 96), np.float32)
+    H.mynah_asr_qmat_mul(C.byref(m), x.ctypes.data, out.ctypes.data, 48)
+    check_close(out, orc.gemm_f64(x, orc.dequant(O.Q4_K, raw, 96 * 1024).reshape(96, 1024)), "blocks")
+    H.mynah_asr_qmat_free(C.byref(m))
