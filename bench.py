@@ -1,0 +1,278 @@
+#!/usr/bin/env python3
+"""bench.py — throughput of the MI355X linear-layer backend on BASELINE's shapes.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+A step is one pass over the FastConformer-0.6B encoder linear set at
+M = 8 segments x 750 frames = 6000 rows (BASELINE config 2's shapes:
+1024->4096, 4096->1024 and five 1024->1024 for Q, K, V, out, pos), every
+weight Q8_0 (BASELINE's metric), EXACT numerics (the default). Inputs are
+resident in HBM before the timed region; each product is the library's full
+device call (activation prep + GEMM kernel). `value` = dense-equivalent
+2*M*N*K operations per second, summed over the step, in TOPS.
+
+Also reported (not `value`): per-kernel roofline fractions, Q4_K at BASELINE
+config 4's M = 12000 shapes, decoder GEMVs (config 3) in HBM GB/s with >= 512
+MB of rotating weight copies (defeats the 256 MB MALL), the f32-weight GEMM,
+and the reference CPU path timed on this host (ingot dequant, compiled from
+the reference's sources, + OpenBLAS sgemm, as src/weights.c:103-114 +
+src/backend.c:79 do).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mynah-asr_amd"))
+
+PEAK_FP16 = 2500.0  # TFLOP/s dense (MI355X)
+PEAK_HBM = 8000.0   # GB/s
+METRIC = "Q8_0/Q4_K GEMM TOPS & % roofline at FastConformer-0.6B shapes; GEMV HBM GB/s"
+
+ENC_SHAPES = [("ffn1", 1024, 4096), ("ffn2", 4096, 1024), ("q", 1024, 1024), ("k", 1024, 1024),
+              ("v", 1024, 1024), ("out", 1024, 1024), ("pos", 1024, 1024)]
+KQ_SHAPES = [("ffn1", 1024, 4096), ("ffn2", 4096, 1024), ("q", 1024, 1024), ("k", 1024, 1024),
+             ("v", 1024, 1024), ("out", 1024, 1024)]
+GEMV_SHAPES = [(1024, 1024), (1024, 4096), (4096, 1024), (1024, 16384)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def roof_time_s(flops: float, nbytes: float) -> float:
+    return max(flops / (PEAK_FP16 * 1e12), nbytes / (PEAK_HBM * 1e9))
+
+
+class Bench:
+    def __init__(self, lib, torch):
+        self.lib, self.torch = lib, torch
+        self.stream = torch.cuda.Stream()  # default priority
+        self.sp = self.stream.cuda_stream
+
+    def sync(self):
+        self.torch.cuda.synchronize()
+
+    def dev(self, a: np.ndarray):
+        return self.torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+    def empty(self, *shape):
+        return self.torch.empty(shape, dtype=self.torch.float32, device="cuda")
+
+    def kernel_ms(self, dw, M: int, x, y, reps: int) -> float:
+        """Average duration of the GEMM kernel alone (input prepared once),
+        HIP events on the stream the kernel runs on."""
+        torch = self.torch
+        dw.prep(x.data_ptr(), M, self.sp)
+        dw.gemm_prepped(y.data_ptr(), M, 0, self.sp)  # warm
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(self.stream)
+        for _ in range(reps):
+            dw.gemm_prepped(y.data_ptr(), M, 0, self.sp)
+        e1.record(self.stream)
+        self.sync()
+        return e0.elapsed_time(e1) / reps
+
+
+def gemm_row(name, qt, M, k, n, ms, M_):
+    flops = 2.0 * M * n * k
+    nbytes = 4.0 * M * k + M_.weight_bytes(qt, n, k) + 4.0 * M * n
+    t = ms * 1e-3
+    return {"gemm": name, "M": M, "k": k, "n": n, "format": M_.NAMES[qt], "kernel_us": round(ms * 1e3, 2),
+            "tflops": round(flops / t / 1e12, 2), "gbps": round(nbytes / t / 1e9, 1),
+            "roofline_frac": round(roof_time_s(flops, nbytes) / t, 4),
+            "mfma_frac": round(flops / t / 1e12 / PEAK_FP16, 4)}
+
+
+def run_encoder_set(B, M_, qt, M, shapes, steps, warmup, seed0):
+    lib = B.lib
+    ws, dws, xs, ys = [], [], {}, []
+    for i, (name, k, n) in enumerate(shapes):
+        w = M_.Weight.make(lib, qt, lib.randn(seed0 + i, 0.02, (n, k)))
+        ws.append(w)
+        dws.append(M_.DeviceWeight(lib, w))
+        if k not in xs:
+            xs[k] = B.dev(lib.randn(1, 1.0, (M, k)))
+        ys.append(B.empty(M, n))
+    B.sync()
+
+    def step():
+        for dw, (name, k, n), y in zip(dws, shapes, ys):
+            dw.gemm(xs[k].data_ptr(), y.data_ptr(), M, 0, B.sp)
+
+    for _ in range(warmup):
+        step()
+    B.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    B.sync()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / steps
+    flops = sum(2.0 * M * n * k for _, k, n in shapes)
+    rows = []
+    for dw, (name, k, n), y in zip(dws, shapes, ys):
+        ms = B.kernel_ms(dw, M, xs[k], y, reps=10)
+        rows.append(gemm_row(name, qt, M, k, n, ms, M_))
+    for dw in dws:
+        dw.close()
+    return ms_step, flops, rows
+
+
+def run_gemv(B, M_, qt, n, k, Ms, min_bytes=512 << 20, max_copies=512):
+    lib = B.lib
+    w = M_.Weight.make(lib, qt, lib.randn(0, 0.02, (n, k)))
+    wb = M_.weight_bytes(qt, n, k)
+    copies = int(min(max_copies, max(4, -(-min_bytes // wb))))
+    dws = [M_.DeviceWeight(lib, w) for _ in range(copies)]
+    out = []
+    torch = B.torch
+    for M in Ms:
+        x = B.dev(lib.randn(1, 1.0, (M, k)))
+        y = B.empty(M, n)
+        # the full call, as a decoder step issues it: for M <= 16 it is one
+        # kernel (the GEMV splits x in registers), every copy in turn
+        for dw in dws[:4]:
+            dw.gemm(x.data_ptr(), y.data_ptr(), M, 0, B.sp)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(B.stream)
+        for dw in dws:
+            dw.gemm(x.data_ptr(), y.data_ptr(), M, 0, B.sp)
+        e1.record(B.stream)
+        B.sync()
+        kms = e0.elapsed_time(e1) / copies
+        nbytes = wb + 4.0 * M * k + 4.0 * M * n
+        out.append({"format": M_.NAMES[qt], "M": M, "k": k, "n": n, "copies": copies,
+                    "rotated_mb": round(copies * wb / 2**20), "kernel_us": round(kms * 1e3, 2),
+                    "kernel_gbps": round(nbytes / (kms * 1e-3) / 1e9, 1),
+                    "kernel_hbm_frac": round(nbytes / (kms * 1e-3) / 1e9 / PEAK_HBM, 4)})
+    for dw in dws:
+        dw.close()
+    return out
+
+
+def cpu_baseline(M_, lib, seconds_budget=20.0):
+    """The reference CPU path for Q8_0 weights: ingot decodes the blocks to f32
+    once (src/weights.c:103-114; here oracle/_ref, the reference's ingot
+    sources compiled unmodified, or the oracle's restatement when _ref is
+    absent), then every product is cblas_sgemm (src/backend.c:79; here the
+    OpenBLAS numpy links). Timed on a bounded sample of the same step."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    kind = "reference"
+    if O.IngotRef.available():
+        dec = O.IngotRef()
+        decoder = "oracle/_ref ingot_dequant (reference sources)"
+    else:
+        dec = O.Oracle()
+        kind = "port"
+        decoder = "oracle restatement of ingot dequant"
+    try:
+        from threadpoolctl import threadpool_info, threadpool_limits
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()
+                       if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        threadpool_limits = None
+        threads = os.cpu_count()
+    M = 6000
+    wd = {}
+    for i, (name, k, n) in enumerate(ENC_SHAPES):
+        raw = lib.quantize(M_.Q8_0, lib.randn(i, 0.02, (n, k)))
+        wd[name] = dec.dequant(O.Q8_0, raw, n * k).reshape(n, k)
+    xs = {k: lib.randn(1, 1.0, (M, k)) for k in (1024, 4096)}
+
+    def step(rows):
+        for name, k, n in ENC_SHAPES:
+            np.matmul(xs[k][:rows], wd[name].T)
+
+    # bounded sample: whole steps at M = 6000 while within the budget
+    step(750)  # warm the BLAS pool
+    t_all, reps = [], 0
+    start = time.perf_counter()
+    while reps < 5 and time.perf_counter() - start < seconds_budget:
+        t0 = time.perf_counter()
+        step(M)
+        t_all.append(time.perf_counter() - t0)
+        reps += 1
+    med = float(np.median(t_all))
+    flops = sum(2.0 * M * n * k for _, k, n in ENC_SHAPES)
+    return {"value": round(flops / med / 1e12, 4), "unit": "TOPS", "cores": int(threads),
+            "kind": kind,
+            "sample": f"{reps} whole steps (7 GEMMs at M=6000, median {med*1e3:.0f} ms): "
+                      f"{decoder} once + OpenBLAS sgemm per product, {threads} BLAS threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extras", action="store_true", help="primary workload only")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are out of scope "
+                                   "(the path shards by rows with no communication)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+    import mynah_hip as M_
+    lib = M_.HipLib()
+    if not lib.available():
+        raise SystemExit("bench: no usable gfx950 device: " + lib.last_error())
+    B = Bench(lib, torch)
+    M = 6000
+
+    log("[bench] encoder set Q8_0 M=6000")
+    ms_step, flops, rows = run_encoder_set(B, M_, M_.Q8_0, M, ENC_SHAPES, args.steps, args.warmup, 0)
+    value = flops / (ms_step * 1e-3) / 1e12
+    dom = max(rows, key=lambda r: r["kernel_us"])
+    dom_flops = 2.0 * M * dom["n"] * dom["k"]
+    achieved = dom_flops / (dom["kernel_us"] * 1e-6) / 1e12
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_FP16, 4), "traffic": None,
+                "kernel": f"k_gemm<Q8_0,4,4> {dom['gemm']} {dom['k']}->{dom['n']} M={M}"}
+    details = {"encoder_q8_0_m6000": rows}
+
+    if not args.no_extras:
+        log("[bench] K-quant Q4_K M=12000")
+        ms4, fl4, rows4 = run_encoder_set(B, M_, M_.Q4_K, 12000, KQ_SHAPES, 3, 1, 100)
+        details["kquant_q4_k_m12000"] = {"tops_per_layer_set": round(fl4 / (ms4 * 1e-3) / 1e12, 2),
+                                         "ms_per_layer_set": round(ms4, 3), "rows": rows4}
+        log("[bench] f32 weights M=6000")
+        msf, flf, rowsf = run_encoder_set(B, M_, M_.F32, M, ENC_SHAPES[:2], 3, 1, 200)
+        details["f32_m6000"] = {"tflops": round(flf / (msf * 1e-3) / 1e12, 2), "rows": rowsf}
+        log("[bench] decoder GEMVs")
+        gv = []
+        for qt in (M_.Q8_0, M_.Q4_0):
+            for n, k in [(s[1], s[0]) for s in GEMV_SHAPES]:
+                gv += run_gemv(B, M_, qt, n, k, (1, 4, 16))
+        details["gemv"] = gv
+        big = [g for g in gv if g["n"] * g["k"] >= 4 << 20]
+        details["gemv_hbm_frac_mean_large"] = round(float(np.mean([g["kernel_hbm_frac"] for g in big])), 4)
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] CPU baseline")
+        cpu = cpu_baseline(M_, lib)
+
+    line = {"metric": METRIC, "value": round(value, 3), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f16x2-mfma/f32",
+            "data": "synthetic (weights N(0,0.02) seed 0.., activations N(0,1) seed 1)",
+            "config": {"workload": "FastConformer-0.6B encoder linear set, Q8_0 weights, M=6000 "
+                                   "(1024->4096, 4096->1024, 5x 1024->1024), EXACT numerics",
+                       "M": M, "weights": "Q8_0"},
+            "roofline": roofline, "cpu_baseline": cpu, "details": details}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -135,6 +135,14 @@ size_t mynah_asr_hip_weight_bytes(const mynah_asr_hip_weight *w);
 /* dy[T,n] = dx[T,k] . W^T; act = 0 none, 1 SiLU applied to the output. */
 int mynah_asr_hip_qgemm_dev(const mynah_asr_hip_weight *w, const float *dx, float *dy, int T,
                             int act, void *stream);
+/* The two halves of qgemm_dev, for callers that feed one input to several
+ * weights (q/k/v) or time the product kernel alone: prep_dev prepares dx for
+ * weights of w's inner size into the calling thread's workspace;
+ * qgemm_prepped_dev runs the product on the last input this thread prepared
+ * (-1 when it does not fit w). Both on `stream`, in order. */
+int mynah_asr_hip_prep_dev(const mynah_asr_hip_weight *w, const float *dx, int T, void *stream);
+int mynah_asr_hip_qgemm_prepped_dev(const mynah_asr_hip_weight *w, float *dy, int T, int act,
+                                    void *stream);
 /* dwd[n,k] = dequantized weight. */
 int mynah_asr_hip_dequant_dev(const mynah_asr_hip_weight *w, float *dwd, void *stream);
 

@@ -72,6 +72,8 @@ struct Ctx {
     int state = 0;  // 0 uninitialised, 1 ok, -1 failed
     hipStream_t st = nullptr;
     DBuf x, y, h, xp, xs16, xsh;
+    // what the workspace holds now (set by prep)
+    int prep_T = -1, prep_Kp = 0, prep_xsum = 0;
 };
 thread_local Ctx t_ctx;
 
@@ -154,16 +156,25 @@ int prep(Ctx *c, const float *dx, int T, int k, int Kp, bool xsum, hipStream_t s
     const int Mpad = mh_mpad(T);
     *xp = (uint8_t *)c->xp.get((size_t)Mpad * Kp * 4);
     *xs16 = (float *)c->xs16.get((size_t)Mpad * (Kp / 16) * sizeof(float));
-    *xsh = (int *)c->xsh.get((size_t)Mpad * sizeof(int));
+    *xsh = (int *)c->xsh.get((size_t)Mpad * (Kp / 128) * sizeof(int));
     if (!*xp || !*xs16 || !*xsh) return fail("workspace allocation failed");
     const int vec = (k % 4 == 0) && (((uintptr_t)dx & 15) == 0);
     hipError_t e = mh_launch_prep(dx, T, k, Kp, Mpad, *xp, *xs16, *xsh, xsum ? 1 : 0, vec, st);
     if (e != hipSuccess) return fail("prep launch failed", hipGetErrorString(e));
+    c->prep_T = T;
+    c->prep_Kp = Kp;
+    c->prep_xsum = xsum ? 1 : 0;
     return 0;
 }
 
 int gemm_dev(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, float *dy, int T, int act,
              hipStream_t st) {
+    if (mh_use_gemv(W->dw, T)) {
+        const int vec = (W->dw.k % 4 == 0) && (((uintptr_t)dx & 15) == 0);
+        hipError_t e = mh_launch_gemv(W->qtype, W->dw, dx, T, vec, dy, act, st);
+        if (e != hipSuccess) return fail("gemv launch failed", hipGetErrorString(e));
+        return 0;
+    }
     uint8_t *xp;
     float *xs16;
     int *xsh;
@@ -254,6 +265,30 @@ int mynah_asr_hip_qgemm_dev(const mynah_asr_hip_weight *w, const float *dx, floa
     return gemm_dev(c, w, dx, dy, T, act, pick_stream(stream));
 }
 
+int mynah_asr_hip_prep_dev(const mynah_asr_hip_weight *w, const float *dx, int T, void *stream) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    if (!w || !dx || T <= 0) return fail("bad argument");
+    uint8_t *xp;
+    float *xs16;
+    int *xsh;
+    return prep(c, dx, T, w->dw.k, w->dw.Kp, wants_xsum(w->qtype), pick_stream(stream), &xp, &xs16, &xsh);
+}
+
+int mynah_asr_hip_qgemm_prepped_dev(const mynah_asr_hip_weight *w, float *dy, int T, int act,
+                                    void *stream) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    if (!w || !dy || T <= 0) return fail("bad argument");
+    if (check_numerics_supported(w->qtype)) return -1;
+    if (c->prep_T != T || c->prep_Kp != w->dw.Kp || (wants_xsum(w->qtype) && !c->prep_xsum))
+        return fail("the prepared input does not fit this weight");
+    hipError_t e = mh_launch_gemm(w->qtype, w->dw, (const uint8_t *)c->xp.p, (const float *)c->xs16.p,
+                                  (const int *)c->xsh.p, dy, T, act, pick_stream(stream));
+    if (e != hipSuccess) return fail("gemm launch failed", hipGetErrorString(e));
+    return 0;
+}
+
 int mynah_asr_hip_dequant_dev(const mynah_asr_hip_weight *w, float *dwd, void *stream) {
     Ctx *c;
     if (begin(&c)) return -1;
@@ -323,7 +358,15 @@ int mynah_asr_hip_qqkv(const mynah_asr_hip_wdesc *wq, const mynah_asr_hip_wdesc 
     float *xs16 = nullptr;
     int *xsh = nullptr;
     for (int i = 0; i < 3; i++) {
-        if (i == 0 || !same)
+        if (mh_use_gemv(W[i]->dw, T)) {
+            float *dy = (float *)c->y.get((size_t)T * ws[i]->n * sizeof(float));
+            if (!dy) return fail("device buffer allocation failed");
+            if (gemm_dev(c, W[i], dx, dy, T, 0, c->st)) return -1;
+            if (d2h_sync(c, outs[i], dy, (size_t)T * ws[i]->n)) return -1;
+            xp = nullptr;  // the next product prepares again
+            continue;
+        }
+        if (!xp || !same)
             if (prep(c, dx, T, wq->k, W[i]->dw.Kp, wants_xsum(W[i]->qtype), c->st, &xp, &xs16, &xsh))
                 return -1;
         float *dy = (float *)c->y.get((size_t)T * ws[i]->n * sizeof(float));

@@ -1,16 +1,17 @@
 // kernels.hip — gfx950 kernels of the mynah-asr linear-layer backend.
 //
-// EXACT numerics (the default). For output (m, n):
-//   x row m is scaled by 2^sh_m (sh_m puts max|x_m| in [2^14, 2^15)) and split
-//   into two f16 terms xh + xl (22 significant bits). Weight quants are small
-//   integers, exact in f16. Per kstep (32 of K) one MFMA pair gives
-//   t = sum(xh*q) + sum(xl*q) in f32; the sub-block factor is applied in f32:
-//   a = fma(sc, t, a) [; a = fma(-mn, sum_x, a) for affine formats]. a restarts
-//   at zero every chunk (128 of K) and total = total + a, chunk by chunk in
-//   order. y = total * 2^-sh_m.
-// That sequence depends on K only — never on M, on the tile a row lands in, or
-// on the kernel (GEMM or GEMV) that runs it — which makes every row of the
-// output bit-identical whatever the batch size.
+// EXACT numerics (the default). K is cut into chunks of 128. For output (m, n)
+// and chunk c:
+//   * x_m's chunk is scaled by 2^sh (sh puts its largest magnitude in
+//     [2^14, 2^15)) and split into two f16 terms xh + xl (22 significant bits);
+//   * weight quants are small integers, exact in f16; per kstep (32 of K) one
+//     MFMA pair gives t = sum(xh*q) + sum(xl*q) in f32 and the sub-block
+//     factor is applied in f32: a = fma(sc, t, a) [; a = fma(-mn, sum_x, a)
+//     for the affine formats], a starting at zero in every chunk;
+//   * total = total + a * 2^-sh, chunks in order from zero. y = total.
+// Every step depends only on row m's own data and on K — never on M, on the
+// tile the row lands in, or on the kernel (GEMM or GEMV) that runs it — so
+// each row's bits are the same whatever the batch size.
 #include "fmt.h"
 
 #define KSTEPS 4  // ksteps per chunk
@@ -26,20 +27,95 @@ __device__ __forceinline__ float silu_f(float v) {
     return v * (e / (1.0f + e));
 }
 
-// A-fragment address of the prepared activations: [G][chunk][kstep][term][64][16 B]
-__device__ __forceinline__ half8 load_a(const uint8_t *xp, int Kc, int G, int c, int s, int term,
-                                        int lane) {
-    const size_t off = (((((size_t)G * Kc + c) * KSTEPS + s) * 2 + term) * 64 + lane) * 16;
-    return *(const half8 *)(xp + off);
+// ---------------------------------------------------------------------------
+// Activation split of one chunk, in the A-operand layout: lane (r = l&15,
+// g = l>>4) holds elements 8g..8g+7 of each kstep for row m. The chunk's
+// largest magnitude is shared by the four lanes of a row through two xor
+// shuffles (every lane of the wave must call this).
+struct XChunk {
+    half8 h[KSTEPS], l[KSTEPS];
+    float s8[KSTEPS];  // sum of the 8 scaled values, in order
+    int sh;
+};
+
+__device__ __forceinline__ void split_chunk(const float *__restrict__ x, int M, int K, int m, int c,
+                                            int g, int vec, XChunk &o) {
+    float v[KSTEPS][8];
+    const bool live = m < M;
+    const float *row = x + (size_t)(live ? m : 0) * K;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; s++) {
+        const int k0 = 128 * c + 32 * s + 8 * g;
+        if (live && vec && k0 + 8 <= K) {
+            const float4 a = *(const float4 *)(row + k0), b = *(const float4 *)(row + k0 + 4);
+            v[s][0] = a.x; v[s][1] = a.y; v[s][2] = a.z; v[s][3] = a.w;
+            v[s][4] = b.x; v[s][5] = b.y; v[s][6] = b.z; v[s][7] = b.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[s][j] = (live && k0 + j < K) ? row[k0 + j] : 0.0f;
+        }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; s++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[s][j]));
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    int e = 0;
+    if (amax > 0.0f) (void)frexpf(amax, &e);
+    o.sh = amax > 0.0f ? 15 - e : 0;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; s++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float xs = ldexpf(v[s][j], o.sh);
+            const _Float16 h = (_Float16)xs;
+            o.h[s][j] = h;
+            o.l[s][j] = (_Float16)(xs - (float)h);
+            acc += xs;
+        }
+        o.s8[s] = acc;
+    }
 }
 
+// ---------------------------------------------------------------------------
+// Sources of the A operand for a chunk.
+// Prepared buffers (large M): xp [G][chunk][kstep][term][64][16 B],
+// xs16 [G][K/16][16 rows] (sub-block sums), xsh [row][chunk].
+template <int WM>
+struct AFromPrep {
+    const uint8_t *xp;
+    const float *xs16;
+    int Kc, Kp16;
+    const int *gm;
+    __device__ __forceinline__ half8 h(int i, int c, int s, int lane) const {
+        return *(const half8 *)(xp + (((((size_t)gm[i] * Kc + c) * KSTEPS + s) * 2 + 0) * 64 + lane) * 16);
+    }
+    __device__ __forceinline__ half8 l(int i, int c, int s, int lane) const {
+        return *(const half8 *)(xp + (((((size_t)gm[i] * Kc + c) * KSTEPS + s) * 2 + 1) * 64 + lane) * 16);
+    }
+    // sums of the kstep's 16-element half hh for rows 4g..4g+3
+    __device__ __forceinline__ f4 xsum(int i, int c, int s, int hh, int lane) const {
+        return *(const f4 *)(xs16 + (((size_t)gm[i] * Kp16 + 8 * c + 2 * s + hh) * 16 + 4 * (lane >> 4)));
+    }
+};
+
+// Registers (small M): one row group, split in the calling wave.
+struct AFromRegs {
+    const XChunk *xc;
+    const f4 *xs;  // [KSTEPS][2], C-layout rows
+    __device__ __forceinline__ half8 h(int, int, int s, int) const { return xc->h[s]; }
+    __device__ __forceinline__ half8 l(int, int, int s, int) const { return xc->l[s]; }
+    __device__ __forceinline__ f4 xsum(int, int, int s, int hh, int) const { return xs[2 * s + hh]; }
+};
+
 // One chunk of the exact product for a WM x WN block of 16x16 tiles.
-// gm[i] / gn[j]: row groups of activations / weights. acc must be zero on entry.
-template <int QT, int WM, int WN>
-__device__ __forceinline__ void chunk_exact(const DevW &W, int Kc, const uint8_t *xp,
-                                            const float *xs16, int Kp16, const int (&gm)[WM],
-                                            const int (&gn)[WN], int c, int lane,
-                                            f4 (&acc)[WM][WN]) {
+// acc must be zero on entry; gn[j]: weight row groups.
+template <int QT, int WM, int WN, class A>
+__device__ __forceinline__ void chunk_exact(const DevW &W, int Kc, const A &src, const int (&gn)[WN],
+                                            int c, int lane, f4 (&acc)[WM][WN]) {
     using F = Fmt<QT>;
     typename F::Raw raw[WN];
 #pragma unroll
@@ -50,17 +126,15 @@ __device__ __forceinline__ void chunk_exact(const DevW &W, int Kc, const uint8_t
         half8 ah[WM], al[WM];
 #pragma unroll
         for (int i = 0; i < WM; i++) {
-            ah[i] = load_a(xp, Kc, gm[i], c, s, 0, lane);
-            al[i] = load_a(xp, Kc, gm[i], c, s, 1, lane);
+            ah[i] = src.h(i, c, s, lane);
+            al[i] = src.l(i, c, s, lane);
         }
         f4 xsum[WM][2];
         if constexpr (F::MINS) {
 #pragma unroll
             for (int i = 0; i < WM; i++) {
-                // sums over the kstep's 16-element halves for rows 4g..4g+3
-                const int sb = 8 * c + 2 * s;
-                xsum[i][0] = *(const f4 *)(xs16 + (((size_t)gm[i] * Kp16 + sb) * 16 + 4 * g));
-                xsum[i][1] = *(const f4 *)(xs16 + (((size_t)gm[i] * Kp16 + sb + 1) * 16 + 4 * g));
+                xsum[i][0] = src.xsum(i, c, s, 0, lane);
+                xsum[i][1] = src.xsum(i, c, s, 1, lane);
             }
         }
 #pragma unroll
@@ -112,18 +186,17 @@ __device__ __forceinline__ void chunk_exact(const DevW &W, int Kc, const uint8_t
 }
 
 // f32 weights: resident as (wh, wl) f16 pairs scaled per row by 2^shw_n;
-// per kstep t += xh*wh + xh*wl + xl*wh, all of the chunk in one accumulator.
-template <int WM, int WN>
-__device__ __forceinline__ void chunk_f32(const DevW &W, int Kc, const uint8_t *xp,
-                                          const int (&gm)[WM], const int (&gn)[WN], int c,
-                                          int lane, f4 (&acc)[WM][WN]) {
+// per kstep t += xh*wh + xh*wl + xl*wh, the whole chunk in one accumulator.
+template <int WM, int WN, class A>
+__device__ __forceinline__ void chunk_f32(const DevW &W, int Kc, const A &src, const int (&gn)[WN],
+                                          int c, int lane, f4 (&acc)[WM][WN]) {
 #pragma unroll
     for (int s = 0; s < KSTEPS; s++) {
         half8 ah[WM], al[WM], bh[WN], bl[WN];
 #pragma unroll
         for (int i = 0; i < WM; i++) {
-            ah[i] = load_a(xp, Kc, gm[i], c, s, 0, lane);
-            al[i] = load_a(xp, Kc, gm[i], c, s, 1, lane);
+            ah[i] = src.h(i, c, s, lane);
+            al[i] = src.l(i, c, s, lane);
         }
 #pragma unroll
         for (int j = 0; j < WN; j++) {
@@ -142,23 +215,20 @@ __device__ __forceinline__ void chunk_f32(const DevW &W, int Kc, const uint8_t *
     }
 }
 
-template <int QT, int WM, int WN>
-__device__ __forceinline__ void chunk_any(const DevW &W, int Kc, const uint8_t *xp, const float *xs16,
-                                          int Kp16, const int (&gm)[WM], const int (&gn)[WN], int c,
+template <int QT, int WM, int WN, class A>
+__device__ __forceinline__ void chunk_any(const DevW &W, int Kc, const A &src, const int (&gn)[WN], int c,
                                           int lane, f4 (&acc)[WM][WN]) {
     if constexpr (QT == QT_F32)
-        chunk_f32<WM, WN>(W, Kc, xp, gm, gn, c, lane, acc);
+        chunk_f32<WM, WN>(W, Kc, src, gn, c, lane, acc);
     else
-        chunk_exact<QT, WM, WN>(W, Kc, xp, xs16, Kp16, gm, gn, c, lane, acc);
+        chunk_exact<QT, WM, WN>(W, Kc, src, gn, c, lane, acc);
 }
 
+// the per-row weight shift of the f32 format (0 for the quantized ones)
 template <int QT>
-__device__ __forceinline__ float finish(const DevW &W, float total, int sh_m, int n, int act) {
-    int sh = sh_m;
-    if constexpr (QT == QT_F32) sh += (int)W.h2[n];
-    float v = ldexpf(total, -sh);
-    if (act) v = silu_f(v);
-    return v;
+__device__ __forceinline__ int wshift(const DevW &W, int n) {
+    if constexpr (QT == QT_F32) return (int)W.h2[n];
+    return 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -170,12 +240,17 @@ __global__ __launch_bounds__(256) void k_gemm(DevW W, const uint8_t *__restrict_
                                               const int *__restrict__ xsh, float *__restrict__ y,
                                               int M, int act) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, col = lane & 15;
     const int Kc = W.Kp / 128, Kp16 = W.Kp / 16;
-    int gm[WM], gn[WN];
+    int gm[WM], gn[WN], shw[WN];
 #pragma unroll
     for (int i = 0; i < WM; i++) gm[i] = (blockIdx.y * 2 + (wave >> 1)) * WM + i;
 #pragma unroll
-    for (int j = 0; j < WN; j++) gn[j] = (blockIdx.x * 2 + (wave & 1)) * WN + j;
+    for (int j = 0; j < WN; j++) {
+        gn[j] = (blockIdx.x * 2 + (wave & 1)) * WN + j;
+        shw[j] = wshift<QT>(W, 16 * gn[j] + col);
+    }
+    const AFromPrep<WM> src{xp, xs16, Kc, Kp16, gm};
     f4 total[WM][WN];
 #pragma unroll
     for (int i = 0; i < WM; i++)
@@ -187,125 +262,121 @@ __global__ __launch_bounds__(256) void k_gemm(DevW W, const uint8_t *__restrict_
         for (int i = 0; i < WM; i++)
 #pragma unroll
             for (int j = 0; j < WN; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-        chunk_any<QT, WM, WN>(W, Kc, xp, xs16, Kp16, gm, gn, c, lane, acc);
+        chunk_any<QT, WM, WN>(W, Kc, src, gn, c, lane, acc);
 #pragma unroll
         for (int i = 0; i < WM; i++)
 #pragma unroll
-            for (int j = 0; j < WN; j++) total[i][j] = total[i][j] + acc[i][j];
+            for (int r = 0; r < 4; r++) {
+                const int sh = xsh[(size_t)(16 * gm[i] + 4 * g + r) * Kc + c];
+#pragma unroll
+                for (int j = 0; j < WN; j++)
+                    total[i][j][r] = total[i][j][r] + ldexpf(acc[i][j][r], -(sh + shw[j]));
+            }
     }
-    const int g = lane >> 4, col = lane & 15;
 #pragma unroll
     for (int i = 0; i < WM; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int m = 16 * gm[i] + 4 * g + r;
             if (m >= M) continue;
-            const int sh = xsh[m];
 #pragma unroll
             for (int j = 0; j < WN; j++) {
                 const int n = 16 * gn[j] + col;
-                if (n < W.n) y[(size_t)m * W.n + n] = finish<QT>(W, total[i][j][r], sh, n, act);
+                if (n < W.n) y[(size_t)m * W.n + n] = act ? silu_f(total[i][j][r]) : total[i][j][r];
             }
         }
 }
 
 // ---------------------------------------------------------------------------
-// Small-M GEMV (M <= 16): one 16-column group per workgroup; the NW waves
-// take chunks c = w, w+NW, ...; chunk partials meet in LDS and are summed in
-// chunk order — the same sequence k_gemm runs in registers.
-template <int QT, int NW>
-__global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const uint8_t *__restrict__ xp,
-                                                  const float *__restrict__ xs16,
-                                                  const int *__restrict__ xsh, float *__restrict__ y,
-                                                  int M, int act) {
-    extern __shared__ f4 part[];  // [Kc][64]
+// Small-M GEMV (M <= 16), no preparation pass: each wave splits its chunks of
+// x in registers (split_chunk, the same function k_prep runs) and applies
+// them to WNG 16-column groups; the NW waves of a workgroup take chunks
+// c = w, w+NW, ...; the scaled chunk partials meet in LDS and are summed in
+// chunk order from zero — the sequence k_gemm runs in registers.
+template <int QT, int NW, int WNG>
+__global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const float *__restrict__ x, int M, int vec,
+                                                  float *__restrict__ y, int act) {
+    extern __shared__ f4 part[];  // [Kc][WNG][64]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int Kc = W.Kp / 128, Kp16 = W.Kp / 16;
-    const int gm[1] = {0};
-    const int gn[1] = {(int)blockIdx.x};
+    const int g = lane >> 4, col = lane & 15;
+    const int Kc = W.Kp / 128;
+    int gn[WNG], shw[WNG];
+#pragma unroll
+    for (int j = 0; j < WNG; j++) {
+        gn[j] = blockIdx.x * WNG + j;
+        shw[j] = wshift<QT>(W, 16 * gn[j] + col);
+    }
     for (int c = wave; c < Kc; c += NW) {
-        f4 acc[1][1] = {{f4{0.f, 0.f, 0.f, 0.f}}};
-        chunk_any<QT, 1, 1>(W, Kc, xp, xs16, Kp16, gm, gn, c, lane, acc);
-        part[c * 64 + lane] = acc[0][0];
+        XChunk xc;
+        split_chunk(x, M, W.k, col, c, g, vec, xc);
+        // C layout: lane holds rows 4g+i; fetch their shifts and sub-block sums
+        int shc[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) shc[i] = __shfl(xc.sh, 4 * g + i);
+        f4 xs[2 * KSTEPS];
+        if constexpr (Fmt<QT == QT_F32 ? QT_Q8_0 : QT>::MINS) {
+#pragma unroll
+            for (int s = 0; s < KSTEPS; s++) {
+                const float s16 = xc.s8[s] + __shfl_xor(xc.s8[s], 16);
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) xs[2 * s + hh][i] = __shfl(s16, 4 * g + i + 32 * hh);
+            }
+        }
+        const AFromRegs src{&xc, xs};
+        f4 acc[1][WNG];
+#pragma unroll
+        for (int j = 0; j < WNG; j++) acc[0][j] = f4{0.f, 0.f, 0.f, 0.f};
+        chunk_any<QT, 1, WNG>(W, Kc, src, gn, c, lane, acc);
+#pragma unroll
+        for (int j = 0; j < WNG; j++) {
+            f4 v;
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = ldexpf(acc[0][j][i], -(shc[i] + shw[j]));
+            part[(c * WNG + j) * 64 + lane] = v;
+        }
     }
     __syncthreads();
-    if (wave != 0) return;
-    f4 total = f4{0.f, 0.f, 0.f, 0.f};
-    for (int c = 0; c < Kc; c++) total = total + part[c * 64 + lane];
-    const int g = lane >> 4, n = 16 * gn[0] + (lane & 15);
-    if (n >= W.n) return;
+    for (int j = wave; j < WNG; j += NW) {
+        f4 total = f4{0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < Kc; c++) total = total + part[(c * WNG + j) * 64 + lane];
+        const int n = 16 * gn[j] + col;
+        if (n >= W.n) continue;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int m = 4 * g + r;
-        if (m < M) y[(size_t)m * W.n + n] = finish<QT>(W, total[r], xsh[m], n, act);
+        for (int i = 0; i < 4; i++) {
+            const int m = 4 * g + i;
+            if (m < M) y[(size_t)m * W.n + n] = act ? silu_f(total[i]) : total[i];
+        }
     }
 }
 
 // ---------------------------------------------------------------------------
-// Activation preparation: one workgroup per 16-row group.
-//   xsh[m]  = 15 - e where max|x_m| = f * 2^e, f in [0.5, 1)  (0 for a zero row)
-//   xp      = A fragments of (xh, xl), zero beyond M and K
-//   xs16    = per row and 16-element sub-block: sum of the scaled x (for the
-//             affine formats), (first 8 in order) + (next 8 in order)
+// Activation preparation for k_gemm: one workgroup (4 waves) per 16-row
+// group; wave w splits chunks c = w, w+4, ... with split_chunk and stores
+//   xp   A fragments of (xh, xl), zero beyond M and K
+//   xs16 per row and 16-element sub-block: (first 8 in order) + (next 8)
+//   xsh  per row and chunk: the shift
 __global__ __launch_bounds__(256) void k_prep(const float *__restrict__ x, int M, int K, int Kp,
                                               uint8_t *__restrict__ xp, float *__restrict__ xs16,
                                               int *__restrict__ xsh, int want_xsum, int vec) {
-    __shared__ int shs[16];
     const int G = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    // phase 1: row maxima (wave w: rows 4w .. 4w+3)
-    for (int rr = 0; rr < 4; rr++) {
-        const int m = 16 * G + 4 * wave + rr;
-        float amax = 0.0f;
-        if (m < M) {
-            const float *row = x + (size_t)m * K;
-            for (int j = lane; j < K; j += 64) amax = fmaxf(amax, fabsf(row[j]));
-        }
-        for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
-        if (lane == 0) {
-            int e = 0;
-            if (amax > 0.0f) (void)frexpf(amax, &e);
-            const int sh = amax > 0.0f ? 15 - e : 0;
-            shs[4 * wave + rr] = sh;
-            if (m < M) xsh[m] = sh;
-        }
-    }
-    __syncthreads();
-    // phase 2: wave w writes kstep w of every chunk
     const int r = lane & 15, g = lane >> 4, m = 16 * G + r;
-    const int sh = shs[r];
     const int Kc = Kp / 128;
-    const float *row = x + (size_t)m * K;
-    for (int c = 0; c < Kc; c++) {
-        const int k0 = 128 * c + 32 * wave + 8 * g;
-        float v[8];
-        if (vec && m < M && k0 + 8 <= K) {
-            const float4 a = *(const float4 *)(row + k0), b = *(const float4 *)(row + k0 + 4);
-            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-        } else {
+    for (int c = wave; c < Kc; c += 4) {
+        XChunk xc;
+        split_chunk(x, M, K, m, c, g, vec, xc);
 #pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = (m < M && k0 + j < K) ? row[k0 + j] : 0.0f;
-        }
-        half8 hi, lo;
-        float s8 = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float xs = ldexpf(v[j], sh);
-            const _Float16 h = (_Float16)xs;
-            hi[j] = h;
-            lo[j] = (_Float16)(xs - (float)h);
-            s8 += xs;
-        }
-        const size_t off = ((((size_t)G * Kc + c) * KSTEPS + wave) * 2) * 64 * 16;
-        *(half8 *)(xp + off + lane * 16) = hi;
-        *(half8 *)(xp + off + (64 + lane) * 16) = lo;
-        if (want_xsum) {
-            const float other = __shfl_xor(s8, 16);  // lanes g and g^1 hold the two halves
-            if ((g & 1) == 0) {
-                const int sb = 8 * c + 2 * wave + (g >> 1);
-                xs16[((size_t)G * (Kp / 16) + sb) * 16 + r] = s8 + other;
+        for (int s = 0; s < KSTEPS; s++) {
+            const size_t off = ((((size_t)G * Kc + c) * KSTEPS + s) * 2) * 64 * 16;
+            *(half8 *)(xp + off + lane * 16) = xc.h[s];
+            *(half8 *)(xp + off + (64 + lane) * 16) = xc.l[s];
+            if (want_xsum) {
+                const float s16 = xc.s8[s] + __shfl_xor(xc.s8[s], 16);
+                if ((g & 1) == 0) xs16[((size_t)G * (Kp / 16) + 8 * c + 2 * s + (g >> 1)) * 16 + r] = s16;
             }
         }
+        if (g == 0) xsh[(size_t)m * Kc + c] = xc.sh;
     }
 }
 
@@ -348,53 +419,84 @@ __global__ void k_silu(float *__restrict__ x, size_t n) {
 // Host-side launchers (C++ linkage inside the library).
 #include "launch.h"
 
-template <int QT>
-static hipError_t launch_gemm_t(const DevW &W, const uint8_t *xp, const float *xs16, const int *xsh,
-                                float *y, int M, int act, hipStream_t st) {
+template <int QT, int NW, int WNG>
+static hipError_t launch_gemv(const DevW &W, const float *x, int M, int vec, float *y, int act,
+                              hipStream_t st) {
     const int Kc = W.Kp / 128;
-    if (M <= 16 && Kc <= 64) {
-        // GEMV: NW waves per column group
-        if (Kc >= 16) {
-            hipLaunchKernelGGL((k_gemv<QT, 16>), dim3(W.Np / 16), dim3(1024), Kc * 64 * 16, st,
-                               W, xp, xs16, xsh, y, M, act);
-        } else if (Kc >= 8) {
-            hipLaunchKernelGGL((k_gemv<QT, 8>), dim3(W.Np / 16), dim3(512), Kc * 64 * 16, st,
-                               W, xp, xs16, xsh, y, M, act);
-        } else {
-            hipLaunchKernelGGL((k_gemv<QT, 4>), dim3(W.Np / 16), dim3(256), Kc * 64 * 16, st,
-                               W, xp, xs16, xsh, y, M, act);
-        }
-    } else if (M <= 512) {
-        const int Mpad = (M + 31) / 32 * 32;
+    hipLaunchKernelGGL((k_gemv<QT, NW, WNG>), dim3(W.Np / 16 / WNG), dim3(NW * 64),
+                       (size_t)Kc * WNG * 64 * 16, st, W, x, M, vec, y, act);
+    return hipGetLastError();
+}
+
+// column groups per GEMV workgroup: more for wide outputs, so that each chunk
+// of x is split once for several groups
+static int gemv_wng(const DevW &W) {
+    const int Kc = W.Kp / 128, groups = W.Np / 16;
+    if (groups >= 1024 && Kc <= 16) return 4;
+    if (groups >= 256 && Kc <= 32) return 2;
+    return 1;
+}
+
+template <int QT>
+static hipError_t gemv_t(const DevW &W, const float *x, int M, int vec, float *y, int act,
+                         hipStream_t st) {
+    const int Kc = W.Kp / 128, wng = gemv_wng(W);
+    if (wng == 4) {
+        if (Kc >= 8) return launch_gemv<QT, 8, 4>(W, x, M, vec, y, act, st);
+        return launch_gemv<QT, 4, 4>(W, x, M, vec, y, act, st);
+    }
+    if (wng == 2) {
+        if (Kc >= 16) return launch_gemv<QT, 16, 2>(W, x, M, vec, y, act, st);
+        if (Kc >= 8) return launch_gemv<QT, 8, 2>(W, x, M, vec, y, act, st);
+        return launch_gemv<QT, 4, 2>(W, x, M, vec, y, act, st);
+    }
+    if (Kc >= 16) return launch_gemv<QT, 16, 1>(W, x, M, vec, y, act, st);
+    if (Kc >= 8) return launch_gemv<QT, 8, 1>(W, x, M, vec, y, act, st);
+    return launch_gemv<QT, 4, 1>(W, x, M, vec, y, act, st);
+}
+
+template <int QT>
+static hipError_t gemm_t(const DevW &W, const uint8_t *xp, const float *xs16, const int *xsh, float *y,
+                         int M, int act, hipStream_t st) {
+    const int Mpad = mh_mpad(M);
+    if (M <= 512) {
         hipLaunchKernelGGL((k_gemm<QT, 1, 4>), dim3(W.Np / 128, Mpad / 32), dim3(256), 0, st,
                            W, xp, xs16, xsh, y, M, act);
     } else if (M <= 2048) {
-        const int Mpad = (M + 63) / 64 * 64;
         hipLaunchKernelGGL((k_gemm<QT, 2, 4>), dim3(W.Np / 128, Mpad / 64), dim3(256), 0, st,
                            W, xp, xs16, xsh, y, M, act);
     } else {
-        const int Mpad = (M + 127) / 128 * 128;
         hipLaunchKernelGGL((k_gemm<QT, 4, 4>), dim3(W.Np / 128, Mpad / 128), dim3(256), 0, st,
                            W, xp, xs16, xsh, y, M, act);
     }
     return hipGetLastError();
 }
 
+#define MH_DISPATCH(fn, qtype, ...)                                  \
+    switch (qtype) {                                                 \
+    case QT_F32: return fn<QT_F32>(__VA_ARGS__);                     \
+    case QT_INT8: return fn<QT_INT8>(__VA_ARGS__);                   \
+    case QT_INT4: return fn<QT_INT4>(__VA_ARGS__);                   \
+    case QT_Q4_0: return fn<QT_Q4_0>(__VA_ARGS__);                   \
+    case QT_Q8_0: return fn<QT_Q8_0>(__VA_ARGS__);                   \
+    case QT_Q2_K: return fn<QT_Q2_K>(__VA_ARGS__);                   \
+    case QT_Q3_K: return fn<QT_Q3_K>(__VA_ARGS__);                   \
+    case QT_Q4_K: return fn<QT_Q4_K>(__VA_ARGS__);                   \
+    case QT_Q5_K: return fn<QT_Q5_K>(__VA_ARGS__);                   \
+    case QT_Q6_K: return fn<QT_Q6_K>(__VA_ARGS__);                   \
+    }                                                                \
+    return hipErrorInvalidValue;
+
+bool mh_use_gemv(const DevW &W, int M) { return M <= 16 && (W.Kp / 128) * gemv_wng(W) <= 64; }
+
+hipError_t mh_launch_gemv(int qtype, const DevW &W, const float *x, int M, int vec, float *y, int act,
+                          hipStream_t st) {
+    MH_DISPATCH(gemv_t, qtype, W, x, M, vec, y, act, st)
+}
+
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
                           const int *xsh, float *y, int M, int act, hipStream_t st) {
-    switch (qtype) {
-    case QT_F32: return launch_gemm_t<QT_F32>(W, xp, xs16, xsh, y, M, act, st);
-    case QT_INT8: return launch_gemm_t<QT_INT8>(W, xp, xs16, xsh, y, M, act, st);
-    case QT_INT4: return launch_gemm_t<QT_INT4>(W, xp, xs16, xsh, y, M, act, st);
-    case QT_Q4_0: return launch_gemm_t<QT_Q4_0>(W, xp, xs16, xsh, y, M, act, st);
-    case QT_Q8_0: return launch_gemm_t<QT_Q8_0>(W, xp, xs16, xsh, y, M, act, st);
-    case QT_Q2_K: return launch_gemm_t<QT_Q2_K>(W, xp, xs16, xsh, y, M, act, st);
-    case QT_Q3_K: return launch_gemm_t<QT_Q3_K>(W, xp, xs16, xsh, y, M, act, st);
-    case QT_Q4_K: return launch_gemm_t<QT_Q4_K>(W, xp, xs16, xsh, y, M, act, st);
-    case QT_Q5_K: return launch_gemm_t<QT_Q5_K>(W, xp, xs16, xsh, y, M, act, st);
-    case QT_Q6_K: return launch_gemm_t<QT_Q6_K>(W, xp, xs16, xsh, y, M, act, st);
-    }
-    return hipErrorInvalidValue;
+    MH_DISPATCH(gemm_t, qtype, W, xp, xs16, xsh, y, M, act, st)
 }
 
 hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,
@@ -406,23 +508,16 @@ hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_
 
 template <int QT>
 static hipError_t launch_dq(const DevW &W, float *out, hipStream_t st) {
-    hipLaunchKernelGGL((k_dequant<QT>), dim3(W.Kp / 128, W.Np / 16), dim3(64), 0, st, W, out);
-    return hipGetLastError();
+    if constexpr (QT == QT_F32) {
+        return hipErrorInvalidValue;
+    } else {
+        hipLaunchKernelGGL((k_dequant<QT>), dim3(W.Kp / 128, W.Np / 16), dim3(64), 0, st, W, out);
+        return hipGetLastError();
+    }
 }
 
 hipError_t mh_launch_dequant(int qtype, const DevW &W, float *out, hipStream_t st) {
-    switch (qtype) {
-    case QT_INT8: return launch_dq<QT_INT8>(W, out, st);
-    case QT_INT4: return launch_dq<QT_INT4>(W, out, st);
-    case QT_Q4_0: return launch_dq<QT_Q4_0>(W, out, st);
-    case QT_Q8_0: return launch_dq<QT_Q8_0>(W, out, st);
-    case QT_Q2_K: return launch_dq<QT_Q2_K>(W, out, st);
-    case QT_Q3_K: return launch_dq<QT_Q3_K>(W, out, st);
-    case QT_Q4_K: return launch_dq<QT_Q4_K>(W, out, st);
-    case QT_Q5_K: return launch_dq<QT_Q5_K>(W, out, st);
-    case QT_Q6_K: return launch_dq<QT_Q6_K>(W, out, st);
-    }
-    return hipErrorInvalidValue;
+    MH_DISPATCH(launch_dq, qtype, W, out, st)
 }
 
 hipError_t mh_launch_silu(float *x, size_t n, hipStream_t st) {

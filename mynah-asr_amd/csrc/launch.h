@@ -16,6 +16,10 @@ static inline int mh_mpad(int M) {
 
 hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,
                           int *xsh, int want_xsum, int vec, hipStream_t st);
+// M <= 16 (and K small enough for the LDS partials): the preparation-free GEMV
+bool mh_use_gemv(const DevW &W, int M);
+hipError_t mh_launch_gemv(int qtype, const DevW &W, const float *x, int M, int vec, float *y, int act,
+                          hipStream_t st);
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
                           const int *xsh, float *y, int M, int act, hipStream_t st);
 hipError_t mh_launch_dequant(int qtype, const DevW &W, float *out, hipStream_t st);

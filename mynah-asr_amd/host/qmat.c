@@ -105,8 +105,10 @@ static const void *key_of(const mynah_asr_qmat *m) {
 }
 
 void mynah_asr_qmat_free(mynah_asr_qmat *m) {
-    /* the device copy is keyed by this pointer, which may be reused after free */
-    if (m->qtype != MYNAH_ASR_Q_F32 && key_of(m)) mynah_asr_hip_evict(key_of(m));
+    /* the device copy is keyed by this pointer, which may be reused after free
+     * (also for borrowed f32 weights: a later allocation at the same address
+     * must not find this copy) */
+    if (key_of(m)) mynah_asr_hip_evict(key_of(m));
     free(m->owned_q);
     free(m->owned_s);
     memset(m, 0, sizeof(*m));

@@ -35,7 +35,8 @@ HIP_SYMBOLS = [
     "mynah_asr_hip_qgemm", "mynah_asr_hip_qffn", "mynah_asr_hip_qqkv", "mynah_asr_hip_dequant",
     "mynah_asr_hip_evict", "mynah_asr_hip_evict_all", "mynah_asr_hip_last_error",
     "mynah_asr_hip_weight_create", "mynah_asr_hip_weight_destroy", "mynah_asr_hip_weight_bytes",
-    "mynah_asr_hip_qgemm_dev", "mynah_asr_hip_dequant_dev",
+    "mynah_asr_hip_qgemm_dev", "mynah_asr_hip_dequant_dev", "mynah_asr_hip_prep_dev",
+    "mynah_asr_hip_qgemm_prepped_dev",
 ]
 HOST_SYMBOLS = [
     "mynah_asr_set_backend", "mynah_asr_backend", "mynah_asr_gemm_wt", "mynah_asr_silu",
@@ -92,6 +93,8 @@ class HipLib:
         L.mynah_asr_hip_weight_bytes.argtypes = [_P]
         L.mynah_asr_hip_qgemm_dev.argtypes = [_P, _P, _P, C.c_int, C.c_int, _P]
         L.mynah_asr_hip_dequant_dev.argtypes = [_P, _P, _P]
+        L.mynah_asr_hip_prep_dev.argtypes = [_P, _P, C.c_int, _P]
+        L.mynah_asr_hip_qgemm_prepped_dev.argtypes = [_P, _P, C.c_int, C.c_int, _P]
         L.mynah_asr_hip_qgemm.argtypes = [C.POINTER(WDesc), _P, _P, C.c_int]
         L.mynah_asr_hip_qffn.argtypes = [C.POINTER(WDesc), C.POINTER(WDesc), _P, _P, C.c_int]
         L.mynah_asr_hip_qqkv.argtypes = [C.POINTER(WDesc)] * 3 + [_P] * 4 + [C.c_int]
@@ -213,19 +216,38 @@ class DeviceWeight:
         rc = self.lib.L.mynah_asr_hip_qgemm_dev(self.h, dx_ptr, dy_ptr, T, act, stream or None)
         self.lib._check(rc, "qgemm_dev")
 
+    def prep(self, dx_ptr: int, T: int, stream: int = 0) -> None:
+        self.lib._check(self.lib.L.mynah_asr_hip_prep_dev(self.h, dx_ptr, T, stream or None), "prep_dev")
+
+    def gemm_prepped(self, dy_ptr: int, T: int, act: int = 0, stream: int = 0) -> None:
+        rc = self.lib.L.mynah_asr_hip_qgemm_prepped_dev(self.h, dy_ptr, T, act, stream or None)
+        self.lib._check(rc, "qgemm_prepped_dev")
+
     def dequant(self, dwd_ptr: int, stream: int = 0) -> None:
         rc = self.lib.L.mynah_asr_hip_dequant_dev(self.h, dwd_ptr, stream or None)
         self.lib._check(rc, "dequant_dev")
 
 
-def host_qgemm(lib: HipLib, w: Weight, x: np.ndarray) -> np.ndarray:
+def evict(lib: HipLib, w: Weight) -> None:
+    """Drop the resident copy keyed by w's host buffer (call before the buffer
+    is freed: the cache is keyed by address, which numpy reuses)."""
+    lib.L.mynah_asr_hip_evict(w.data.ctypes.data)
+
+
+def host_qgemm(lib: HipLib, w: Weight, x: np.ndarray, keep: bool = False) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.empty((x.shape[0], w.n), dtype=np.float32)
-    lib._check(lib.L.mynah_asr_hip_qgemm(C.byref(w.desc), _ptr(x), _ptr(out), x.shape[0]), "qgemm")
+    rc = lib.L.mynah_asr_hip_qgemm(C.byref(w.desc), _ptr(x), _ptr(out), x.shape[0])
+    if not keep:
+        evict(lib, w)
+    lib._check(rc, "qgemm")
     return out
 
 
-def host_dequant(lib: HipLib, w: Weight) -> np.ndarray:
+def host_dequant(lib: HipLib, w: Weight, keep: bool = False) -> np.ndarray:
     out = np.empty((w.n, w.k), dtype=np.float32)
-    lib._check(lib.L.mynah_asr_hip_dequant(C.byref(w.desc), _ptr(out)), "dequant")
+    rc = lib.L.mynah_asr_hip_dequant(C.byref(w.desc), _ptr(out))
+    if not keep:
+        evict(lib, w)
+    lib._check(rc, "dequant")
     return out
