@@ -238,7 +238,7 @@ def main():
     achieved = dom_flops / (dom["kernel_us"] * 1e-6) / 1e12
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP16, 4), "traffic": None,
-                "kernel": f"k_gemm<Q8_0,4,4> {dom['gemm']} {dom['k']}->{dom['n']} M={M}"}
+                "kernel": f"k_gemm_direct<Q8_0> {dom['gemm']} {dom['k']}->{dom['n']} M={M}"}
     details = {"encoder_q8_0_m6000": rows}
 
     if not args.no_extras:

@@ -25,8 +25,11 @@ HOST_LIB = os.path.join(LIB, "libmynah_asr.so")
 # -packed-fp32-ops: no v_pk_*_f32 in generated code; -ffp-contract=off: every
 # fused multiply-add in the kernels is an explicit fmaf, so all kernels that
 # share a device function perform the same float operations.
+# -amdgpu-mfma-vgpr-form (device pass only): MFMA results land in VGPRs, so the
+# f32 epilogue that scales them reads them without v_accvgpr_read copies.
 HIP_FLAGS = ["-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC", "-ffp-contract=off",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-Xarch_device", "-mllvm=-amdgpu-mfma-vgpr-form",
              "-Wall", "-Wno-unused-function", "-I", INC, "-I", CSRC]
 
 

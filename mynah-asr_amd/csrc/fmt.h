@@ -129,33 +129,37 @@ template <int QT> struct Fmt;
 template <> struct Fmt<QT_Q8_0> {
     static constexpr int B0 = 32, B1 = 0;
     static constexpr bool SUB16 = false, MINS = false;
-    struct Raw { uint32_t w[8]; float d[4]; };
+    struct Raw { uint32_t w[8]; uint32_t d[2]; };  // d: the chunk's four f16 block factors
     static __device__ __forceinline__ void load(const DevW &W, int Kc, int G, int c, int lane, Raw &R) {
         load_plane<32>(W.p0, Kc, G, c, lane, R.w);
         const uint2 hd = *(const uint2 *)(W.h + (((size_t)G * Kc + c) * 16 + (lane & 15)) * 8);
-        R.d[0] = h2f(hd.x & 0xffff); R.d[1] = h2f(hd.x >> 16);
-        R.d[2] = h2f(hd.y & 0xffff); R.d[3] = h2f(hd.y >> 16);
+        R.d[0] = hd.x; R.d[1] = hd.y;
     }
     static __device__ __forceinline__ half8 decode(const Raw &R, int s) { return dec_bytes(R.w[2 * s], R.w[2 * s + 1]); }
-    static __device__ __forceinline__ void scale(const Raw &R, int s, int, float &sc, float &mn) { sc = R.d[s]; mn = 0.0f; }
+    static __device__ __forceinline__ void scale(const Raw &R, int s, int, float &sc, float &mn) {
+        sc = h2f((R.d[s >> 1] >> (16 * (s & 1))) & 0xffff);
+        mn = 0.0f;
+    }
 };
 
 template <> struct Fmt<QT_Q4_0> {
     static constexpr int B0 = 16, B1 = 0;
     static constexpr bool SUB16 = false, MINS = false;
-    struct Raw { uint32_t w[4]; float d[4]; };
+    struct Raw { uint32_t w[4]; uint32_t d[2]; };
     static __device__ __forceinline__ void load(const DevW &W, int Kc, int G, int c, int lane, Raw &R) {
         load_plane<16>(W.p0, Kc, G, c, lane, R.w);
         const uint2 hd = *(const uint2 *)(W.h + (((size_t)G * Kc + c) * 16 + (lane & 15)) * 8);
-        R.d[0] = h2f(hd.x & 0xffff); R.d[1] = h2f(hd.x >> 16);
-        R.d[2] = h2f(hd.y & 0xffff); R.d[3] = h2f(hd.y >> 16);
+        R.d[0] = hd.x; R.d[1] = hd.y;
     }
     static __device__ __forceinline__ half8 decode(const Raw &R, int s) {
         const uint32_t w = R.w[s];
         return pairs_to_half8(nib_pair(w, 0) | MAGIC, nib_pair(w, 1) | MAGIC, nib_pair(w, 2) | MAGIC,
                               nib_pair(w, 3) | MAGIC, (_Float16)1032.0f);
     }
-    static __device__ __forceinline__ void scale(const Raw &R, int s, int, float &sc, float &mn) { sc = R.d[s]; mn = 0.0f; }
+    static __device__ __forceinline__ void scale(const Raw &R, int s, int, float &sc, float &mn) {
+        sc = h2f((R.d[s >> 1] >> (16 * (s & 1))) & 0xffff);
+        mn = 0.0f;
+    }
 };
 
 template <> struct Fmt<QT_INT8> {

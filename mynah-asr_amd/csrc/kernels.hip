@@ -81,9 +81,11 @@ __device__ __forceinline__ void split_chunk(const float *__restrict__ x, int M, 
 }
 
 // ---------------------------------------------------------------------------
-// Sources of the A operand for a chunk.
-// Prepared buffers (large M): xp [G][chunk][kstep][term][64][16 B],
-// xs16 [G][K/16][16 rows] (sub-block sums), xsh [row][chunk].
+// Sources of the A operand: an object with h(i, c, s, lane), l(...) (the two
+// f16 terms of kstep s for row group i) and xsum(i, c, s, half, lane) (the
+// sub-block sums of rows 4g..4g+3, for the affine formats).
+// Prepared buffers read straight from global memory (no LDS staging):
+// xp [G][chunk][kstep][term][64][16 B], xs16 [G][K/16][16 rows].
 template <int WM>
 struct AFromPrep {
     const uint8_t *xp;
@@ -96,7 +98,6 @@ struct AFromPrep {
     __device__ __forceinline__ half8 l(int i, int c, int s, int lane) const {
         return *(const half8 *)(xp + (((((size_t)gm[i] * Kc + c) * KSTEPS + s) * 2 + 1) * 64 + lane) * 16);
     }
-    // sums of the kstep's 16-element half hh for rows 4g..4g+3
     __device__ __forceinline__ f4 xsum(int i, int c, int s, int hh, int lane) const {
         return *(const f4 *)(xs16 + (((size_t)gm[i] * Kp16 + 8 * c + 2 * s + hh) * 16 + 4 * (lane >> 4)));
     }
@@ -111,93 +112,51 @@ struct AFromRegs {
     __device__ __forceinline__ f4 xsum(int, int, int s, int hh, int) const { return xs[2 * s + hh]; }
 };
 
-// One chunk of the exact product for a WM x WN block of 16x16 tiles.
-// acc must be zero on entry; gn[j]: weight row groups.
-template <int QT, int WM, int WN, class A>
-__device__ __forceinline__ void chunk_exact(const DevW &W, int Kc, const A &src, const int (&gn)[WN],
-                                            int c, int lane, f4 (&acc)[WM][WN]) {
-    using F = Fmt<QT>;
-    typename F::Raw raw[WN];
+// Raw weight registers of one chunk for WN column groups (none for F32,
+// whose fragments are read per kstep).
+template <int QT, int WN> struct BRaw { typename Fmt<QT>::Raw r[WN]; };
+template <int WN> struct BRaw<QT_F32, WN> {};
+
+template <int QT, int WN>
+__device__ __forceinline__ void load_b(const DevW &W, int Kc, const int (&gn)[WN], int c, int lane,
+                                       BRaw<QT, WN> &b) {
+    if constexpr (QT != QT_F32) {
 #pragma unroll
-    for (int j = 0; j < WN; j++) F::load(W, Kc, gn[j], c, lane, raw[j]);
-    const int g = lane >> 4;
-#pragma unroll
-    for (int s = 0; s < KSTEPS; s++) {
-        half8 ah[WM], al[WM];
-#pragma unroll
-        for (int i = 0; i < WM; i++) {
-            ah[i] = src.h(i, c, s, lane);
-            al[i] = src.l(i, c, s, lane);
-        }
-        f4 xsum[WM][2];
-        if constexpr (F::MINS) {
-#pragma unroll
-            for (int i = 0; i < WM; i++) {
-                xsum[i][0] = src.xsum(i, c, s, 0, lane);
-                xsum[i][1] = src.xsum(i, c, s, 1, lane);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < WN; j++) {
-            const half8 b = F::decode(raw[j], s);
-            if constexpr (!F::SUB16) {
-                float sc, mn;
-                F::scale(raw[j], s, 0, sc, mn);
-#pragma unroll
-                for (int i = 0; i < WM; i++) {
-                    f4 t = mfma16(ah[i], b, f4{0.f, 0.f, 0.f, 0.f});
-                    t = mfma16(al[i], b, t);
-#pragma unroll
-                    for (int r = 0; r < 4; r++) acc[i][j][r] = __builtin_fmaf(sc, t[r], acc[i][j][r]);
-                    if constexpr (F::MINS) {
-                        const f4 xs = xsum[i][0] + xsum[i][1];
-#pragma unroll
-                        for (int r = 0; r < 4; r++) acc[i][j][r] = __builtin_fmaf(-mn, xs[r], acc[i][j][r]);
-                    }
-                }
-            } else {
-                const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-                const half8 b0 = g < 2 ? b : z, b1 = g < 2 ? z : b;
-                float sc0, mn0, sc1, mn1;
-                F::scale(raw[j], s, 0, sc0, mn0);
-                F::scale(raw[j], s, 1, sc1, mn1);
-#pragma unroll
-                for (int i = 0; i < WM; i++) {
-                    f4 t0 = mfma16(ah[i], b0, f4{0.f, 0.f, 0.f, 0.f});
-                    t0 = mfma16(al[i], b0, t0);
-                    f4 t1 = mfma16(ah[i], b1, f4{0.f, 0.f, 0.f, 0.f});
-                    t1 = mfma16(al[i], b1, t1);
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        acc[i][j][r] = __builtin_fmaf(sc0, t0[r], acc[i][j][r]);
-                        acc[i][j][r] = __builtin_fmaf(sc1, t1[r], acc[i][j][r]);
-                    }
-                    if constexpr (F::MINS) {
-#pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            acc[i][j][r] = __builtin_fmaf(-mn0, xsum[i][0][r], acc[i][j][r]);
-                            acc[i][j][r] = __builtin_fmaf(-mn1, xsum[i][1][r], acc[i][j][r]);
-                        }
-                    }
-                }
-            }
-        }
+        for (int j = 0; j < WN; j++) Fmt<QT>::load(W, Kc, gn[j], c, lane, b.r[j]);
     }
 }
 
-// f32 weights: resident as (wh, wl) f16 pairs scaled per row by 2^shw_n;
-// per kstep t += xh*wh + xh*wl + xl*wh, the whole chunk in one accumulator.
-template <int WM, int WN, class A>
-__device__ __forceinline__ void chunk_f32(const DevW &W, int Kc, const A &src, const int (&gn)[WN],
-                                          int c, int lane, f4 (&acc)[WM][WN]) {
+// The exact product kstep by kstep. kstep_issue loads the A fragments,
+// decodes the weights and issues the MFMAs of one kstep into a pending
+// record; kstep_apply folds a pending record into the chunk accumulator
+// (acc = fma(sc, t, acc) [- mn * sum_x]). Callers issue kstep s+1 before
+// applying kstep s, so the VALU epilogue of one kstep runs while the matrix
+// core works on the next; the float operations each output sees, and their
+// order, are the same in every caller.
+template <int QT, int WM, int WN> struct KPend {
+    static constexpr bool SUB = QT != QT_F32 && Fmt<QT == QT_F32 ? QT_Q8_0 : QT>::SUB16;
+    static constexpr bool MIN = QT != QT_F32 && Fmt<QT == QT_F32 ? QT_Q8_0 : QT>::MINS;
+    static constexpr int NH = SUB ? 2 : 1;
+    f4 t[WM][WN][NH];
+    float sc[WN][NH], mn[WN][NH];
+    f4 xs[WM][2];
+};
+
+template <int QT, int WM, int WN, class A>
+__device__ __forceinline__ void kstep_issue(const DevW &W, int Kc, const A &src, const BRaw<QT, WN> &braw,
+                                            const int (&gn)[WN], int c, int s, int lane,
+                                            KPend<QT, WM, WN> &p, f4 (&acc)[WM][WN]) {
+    half8 ah[WM], al[WM];
 #pragma unroll
-    for (int s = 0; s < KSTEPS; s++) {
-        half8 ah[WM], al[WM], bh[WN], bl[WN];
-#pragma unroll
-        for (int i = 0; i < WM; i++) {
-            ah[i] = src.h(i, c, s, lane);
-            al[i] = src.l(i, c, s, lane);
-        }
+    for (int i = 0; i < WM; i++) {
+        ah[i] = src.h(i, c, s, lane);
+        al[i] = src.l(i, c, s, lane);
+    }
+    if constexpr (QT == QT_F32) {
+        // f32 weights: resident as (wh, wl) f16 pairs scaled per row by
+        // 2^shw_n; t += xh*wh + xh*wl + xl*wh straight into the chunk
+        // accumulator (no per-kstep factor)
+        half8 bh[WN], bl[WN];
 #pragma unroll
         for (int j = 0; j < WN; j++) {
             const size_t base = ((size_t)gn[j] * Kc + c) * 8;
@@ -212,16 +171,105 @@ __device__ __forceinline__ void chunk_f32(const DevW &W, int Kc, const A &src, c
                 acc[i][j] = mfma16(ah[i], bl[j], acc[i][j]);
                 acc[i][j] = mfma16(al[i], bh[j], acc[i][j]);
             }
+    } else {
+        using F = Fmt<QT>;
+        const int g = lane >> 4;
+        if constexpr (F::MINS) {
+#pragma unroll
+            for (int i = 0; i < WM; i++) {
+                p.xs[i][0] = src.xsum(i, c, s, 0, lane);
+                p.xs[i][1] = src.xsum(i, c, s, 1, lane);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < WN; j++) {
+            const half8 b = F::decode(braw.r[j], s);
+            if constexpr (!F::SUB16) {
+                F::scale(braw.r[j], s, 0, p.sc[j][0], p.mn[j][0]);
+#pragma unroll
+                for (int i = 0; i < WM; i++) {
+                    f4 t = mfma16(ah[i], b, f4{0.f, 0.f, 0.f, 0.f});
+                    p.t[i][j][0] = mfma16(al[i], b, t);
+                }
+            } else {
+                const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+                const half8 b0 = g < 2 ? b : z, b1 = g < 2 ? z : b;
+                F::scale(braw.r[j], s, 0, p.sc[j][0], p.mn[j][0]);
+                F::scale(braw.r[j], s, 1, p.sc[j][1], p.mn[j][1]);
+#pragma unroll
+                for (int i = 0; i < WM; i++) {
+                    f4 t0 = mfma16(ah[i], b0, f4{0.f, 0.f, 0.f, 0.f});
+                    p.t[i][j][0] = mfma16(al[i], b0, t0);
+                    f4 t1 = mfma16(ah[i], b1, f4{0.f, 0.f, 0.f, 0.f});
+                    p.t[i][j][1] = mfma16(al[i], b1, t1);
+                }
+            }
+        }
     }
 }
 
-template <int QT, int WM, int WN, class A>
-__device__ __forceinline__ void chunk_any(const DevW &W, int Kc, const A &src, const int (&gn)[WN], int c,
-                                          int lane, f4 (&acc)[WM][WN]) {
-    if constexpr (QT == QT_F32)
-        chunk_f32<WM, WN>(W, Kc, src, gn, c, lane, acc);
-    else
-        chunk_exact<QT, WM, WN>(W, Kc, src, gn, c, lane, acc);
+template <int QT, int WM, int WN>
+__device__ __forceinline__ void kstep_apply(const KPend<QT, WM, WN> &p, f4 (&acc)[WM][WN]) {
+    if constexpr (QT != QT_F32) {
+        using KP = KPend<QT, WM, WN>;
+#pragma unroll
+        for (int i = 0; i < WM; i++)
+#pragma unroll
+            for (int j = 0; j < WN; j++) {
+                if constexpr (!KP::SUB) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[i][j][r] = __builtin_fmaf(p.sc[j][0], p.t[i][j][0][r], acc[i][j][r]);
+                    if constexpr (KP::MIN) {
+                        const f4 xs = p.xs[i][0] + p.xs[i][1];
+#pragma unroll
+                        for (int r = 0; r < 4; r++) acc[i][j][r] = __builtin_fmaf(-p.mn[j][0], xs[r], acc[i][j][r]);
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        acc[i][j][r] = __builtin_fmaf(p.sc[j][0], p.t[i][j][0][r], acc[i][j][r]);
+                        acc[i][j][r] = __builtin_fmaf(p.sc[j][1], p.t[i][j][1][r], acc[i][j][r]);
+                    }
+                    if constexpr (KP::MIN) {
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            acc[i][j][r] = __builtin_fmaf(-p.mn[j][0], p.xs[i][0][r], acc[i][j][r]);
+                            acc[i][j][r] = __builtin_fmaf(-p.mn[j][1], p.xs[i][1][r], acc[i][j][r]);
+                        }
+                    }
+                }
+            }
+    }
+}
+
+template <int QT, int WM, int WN>
+constexpr int kstep_mfmas() {
+    return QT == QT_F32 ? 3 * WM * WN : (KPend<QT, WM, WN>::SUB ? 4 : 2) * WM * WN;
+}
+
+// A whole chunk from one A source. PIPE: issue(s+1) before apply(s) (more
+// registers, more overlap); otherwise each kstep is applied right away.
+template <int QT, int WM, int WN, class A, bool PIPE = true>
+__device__ __forceinline__ void chunk_all(const DevW &W, int Kc, const A &src, const BRaw<QT, WN> &braw,
+                                          const int (&gn)[WN], int c, int lane, f4 (&acc)[WM][WN]) {
+    if constexpr (!PIPE) {
+#pragma unroll
+        for (int s = 0; s < KSTEPS; s++) {
+            KPend<QT, WM, WN> p;
+            kstep_issue<QT, WM, WN>(W, Kc, src, braw, gn, c, s, lane, p, acc);
+            kstep_apply<QT, WM, WN>(p, acc);
+        }
+        return;
+    }
+    KPend<QT, WM, WN> p0, p1;
+    kstep_issue<QT, WM, WN>(W, Kc, src, braw, gn, c, 0, lane, p0, acc);
+    kstep_issue<QT, WM, WN>(W, Kc, src, braw, gn, c, 1, lane, p1, acc);
+    kstep_apply<QT, WM, WN>(p0, acc);
+    kstep_issue<QT, WM, WN>(W, Kc, src, braw, gn, c, 2, lane, p0, acc);
+    kstep_apply<QT, WM, WN>(p1, acc);
+    kstep_issue<QT, WM, WN>(W, Kc, src, braw, gn, c, 3, lane, p1, acc);
+    kstep_apply<QT, WM, WN>(p0, acc);
+    kstep_apply<QT, WM, WN>(p1, acc);
 }
 
 // the per-row weight shift of the f32 format (0 for the quantized ones)
@@ -232,13 +280,19 @@ __device__ __forceinline__ int wshift(const DevW &W, int n) {
 }
 
 // ---------------------------------------------------------------------------
-// Large-M GEMM: 4 waves in 2x2, each a WM x WN block of 16x16 tiles.
+// Large-M GEMM: 4 waves in 2x2, each a WM x WN block of 16x16 tiles; every
+// wave reads its A and B fragments straight from global memory in the
+// MFMA-native layouts (one contiguous 1 KiB block per wave-wide 16-byte load),
+// and L1/L2 serve the sharing between the waves of a workgroup. Staging A
+// through LDS was measured slower on gfx950 for these tiles: the kernel is
+// bound by the VALU work of the per-kstep f32 epilogue, and the extra LDS
+// traffic, barriers and prefetch registers only add to it.
 // grid.x = Np / (32*WN), grid.y = Mpad / (32*WM).
-template <int QT, int WM, int WN>
-__global__ __launch_bounds__(256) void k_gemm(DevW W, const uint8_t *__restrict__ xp,
-                                              const float *__restrict__ xs16,
-                                              const int *__restrict__ xsh, float *__restrict__ y,
-                                              int M, int act) {
+template <int QT, int WM, int WN, bool PIPE>
+__global__ __launch_bounds__(256) void k_gemm_direct(DevW W, const uint8_t *__restrict__ xp,
+                                                     const float *__restrict__ xs16,
+                                                     const int *__restrict__ xsh, float *__restrict__ y,
+                                                     int M, int act) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, col = lane & 15;
     const int Kc = W.Kp / 128, Kp16 = W.Kp / 16;
@@ -257,21 +311,26 @@ __global__ __launch_bounds__(256) void k_gemm(DevW W, const uint8_t *__restrict_
 #pragma unroll
         for (int j = 0; j < WN; j++) total[i][j] = f4{0.f, 0.f, 0.f, 0.f};
     for (int c = 0; c < Kc; c++) {
+        BRaw<QT, WN> braw;
+        load_b<QT, WN>(W, Kc, gn, c, lane, braw);
+        int4 sh4[WM];  // issued now, used after the chunk
+#pragma unroll
+        for (int i = 0; i < WM; i++) sh4[i] = *(const int4 *)(xsh + ((size_t)gm[i] * Kc + c) * 16 + 4 * g);
         f4 acc[WM][WN];
 #pragma unroll
         for (int i = 0; i < WM; i++)
 #pragma unroll
             for (int j = 0; j < WN; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-        chunk_any<QT, WM, WN>(W, Kc, src, gn, c, lane, acc);
+        chunk_all<QT, WM, WN, AFromPrep<WM>, PIPE>(W, Kc, src, braw, gn, c, lane, acc);
 #pragma unroll
-        for (int i = 0; i < WM; i++)
+        for (int i = 0; i < WM; i++) {
+            const int sh[4] = {sh4[i].x, sh4[i].y, sh4[i].z, sh4[i].w};
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int sh = xsh[(size_t)(16 * gm[i] + 4 * g + r) * Kc + c];
+            for (int r = 0; r < 4; r++)
 #pragma unroll
                 for (int j = 0; j < WN; j++)
-                    total[i][j][r] = total[i][j][r] + ldexpf(acc[i][j][r], -(sh + shw[j]));
-            }
+                    total[i][j][r] = total[i][j][r] + ldexpf(acc[i][j][r], -(sh[r] + shw[j]));
+        }
     }
 #pragma unroll
     for (int i = 0; i < WM; i++)
@@ -308,7 +367,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const float *__restric
     }
     for (int c = wave; c < Kc; c += NW) {
         XChunk xc;
-        split_chunk(x, M, W.k, col, c, g, vec, xc);
+        split_chunk(x, M, W.k, col, c, g, vec, xc);  // (weight loads issue below; the
+                                                     // compiler hoists them past the split)
         // C layout: lane holds rows 4g+i; fetch their shifts and sub-block sums
         int shc[4];
 #pragma unroll
@@ -328,7 +388,9 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const float *__restric
         f4 acc[1][WNG];
 #pragma unroll
         for (int j = 0; j < WNG; j++) acc[0][j] = f4{0.f, 0.f, 0.f, 0.f};
-        chunk_any<QT, 1, WNG>(W, Kc, src, gn, c, lane, acc);
+        BRaw<QT, WNG> braw;
+        load_b<QT, WNG>(W, Kc, gn, c, lane, braw);
+        chunk_all<QT, 1, WNG>(W, Kc, src, braw, gn, c, lane, acc);
 #pragma unroll
         for (int j = 0; j < WNG; j++) {
             f4 v;
@@ -356,7 +418,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const float *__restric
 // group; wave w splits chunks c = w, w+4, ... with split_chunk and stores
 //   xp   A fragments of (xh, xl), zero beyond M and K
 //   xs16 per row and 16-element sub-block: (first 8 in order) + (next 8)
-//   xsh  per row and chunk: the shift
+//   xsh  per row group, chunk and row: the shift  [G][chunk][16]
 __global__ __launch_bounds__(256) void k_prep(const float *__restrict__ x, int M, int K, int Kp,
                                               uint8_t *__restrict__ xp, float *__restrict__ xs16,
                                               int *__restrict__ xsh, int want_xsum, int vec) {
@@ -376,7 +438,7 @@ __global__ __launch_bounds__(256) void k_prep(const float *__restrict__ x, int M
                 if ((g & 1) == 0) xs16[((size_t)G * (Kp / 16) + 8 * c + 2 * s + (g >> 1)) * 16 + r] = s16;
             }
         }
-        if (g == 0) xsh[(size_t)m * Kc + c] = xc.sh;
+        if (g == 0) xsh[((size_t)G * Kc + c) * 16 + r] = xc.sh;
     }
 }
 
@@ -417,6 +479,8 @@ __global__ void k_silu(float *__restrict__ x, size_t n) {
 
 // ---------------------------------------------------------------------------
 // Host-side launchers (C++ linkage inside the library).
+#include <stdlib.h>
+
 #include "launch.h"
 
 template <int QT, int NW, int WNG>
@@ -455,21 +519,33 @@ static hipError_t gemv_t(const DevW &W, const float *x, int M, int vec, float *y
     return launch_gemv<QT, 4, 1>(W, x, M, vec, y, act, st);
 }
 
+template <int QT, int WM>
+static hipError_t launch_direct(const DevW &W, const uint8_t *xp, const float *xs16, const int *xsh, float *y,
+                                int M, int act, hipStream_t st) {
+    hipLaunchKernelGGL((k_gemm_direct<QT, WM, 4, false>), dim3(W.Np / 128, mh_mpad(M) / (32 * WM)), dim3(256),
+                       0, st, W, xp, xs16, xsh, y, M, act);
+    return hipGetLastError();
+}
+
+// Rows per wave (WM): 2 for the block-scaled formats at large M, 1 for small
+// M and for the K-quants, whose decoders need the registers (measured best on
+// the BASELINE shapes). MYNAH_ASR_HIP_GEMM_WM=1|2 overrides, for tuning.
+int mh_gemm_wm(int M, bool kquant) {
+    static int forced = -2;
+    if (forced == -2) {
+        const char *e = getenv("MYNAH_ASR_HIP_GEMM_WM");
+        forced = e ? atoi(e) : -1;
+    }
+    if (forced == 1 || forced == 2) return forced;
+    return (kquant || M <= 1024) ? 1 : 2;
+}
+
 template <int QT>
 static hipError_t gemm_t(const DevW &W, const uint8_t *xp, const float *xs16, const int *xsh, float *y,
                          int M, int act, hipStream_t st) {
-    const int Mpad = mh_mpad(M);
-    if (M <= 512) {
-        hipLaunchKernelGGL((k_gemm<QT, 1, 4>), dim3(W.Np / 128, Mpad / 32), dim3(256), 0, st,
-                           W, xp, xs16, xsh, y, M, act);
-    } else if (M <= 2048) {
-        hipLaunchKernelGGL((k_gemm<QT, 2, 4>), dim3(W.Np / 128, Mpad / 64), dim3(256), 0, st,
-                           W, xp, xs16, xsh, y, M, act);
-    } else {
-        hipLaunchKernelGGL((k_gemm<QT, 4, 4>), dim3(W.Np / 128, Mpad / 128), dim3(256), 0, st,
-                           W, xp, xs16, xsh, y, M, act);
-    }
-    return hipGetLastError();
+    constexpr bool kq = QT == QT_Q2_K || QT == QT_Q3_K || QT == QT_Q4_K || QT == QT_Q5_K || QT == QT_Q6_K;
+    if (mh_gemm_wm(M, kq) == 2) return launch_direct<QT, 2>(W, xp, xs16, xsh, y, M, act, st);
+    return launch_direct<QT, 1>(W, xp, xs16, xsh, y, M, act, st);
 }
 
 #define MH_DISPATCH(fn, qtype, ...)                                  \

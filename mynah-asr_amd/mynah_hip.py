@@ -93,8 +93,9 @@ class HipLib:
         L.mynah_asr_hip_weight_bytes.argtypes = [_P]
         L.mynah_asr_hip_qgemm_dev.argtypes = [_P, _P, _P, C.c_int, C.c_int, _P]
         L.mynah_asr_hip_dequant_dev.argtypes = [_P, _P, _P]
-        L.mynah_asr_hip_prep_dev.argtypes = [_P, _P, C.c_int, _P]
-        L.mynah_asr_hip_qgemm_prepped_dev.argtypes = [_P, _P, C.c_int, C.c_int, _P]
+        if hasattr(L, "mynah_asr_hip_prep_dev"):  # absent from older builds
+            L.mynah_asr_hip_prep_dev.argtypes = [_P, _P, C.c_int, _P]
+            L.mynah_asr_hip_qgemm_prepped_dev.argtypes = [_P, _P, C.c_int, C.c_int, _P]
         L.mynah_asr_hip_qgemm.argtypes = [C.POINTER(WDesc), _P, _P, C.c_int]
         L.mynah_asr_hip_qffn.argtypes = [C.POINTER(WDesc), C.POINTER(WDesc), _P, _P, C.c_int]
         L.mynah_asr_hip_qqkv.argtypes = [C.POINTER(WDesc)] * 3 + [_P] * 4 + [C.c_int]
