@@ -287,21 +287,30 @@ __device__ __forceinline__ int wshift(const DevW &W, int n) {
 // through LDS was measured slower on gfx950 for these tiles: the kernel is
 // bound by the VALU work of the per-kstep f32 epilogue, and the extra LDS
 // traffic, barriers and prefetch registers only add to it.
-// grid.x = Np / (32*WN), grid.y = Mpad / (32*WM).
+// grid = tilesM * tilesN workgroups, tiles of (32*WM) x (32*WN).
 template <int QT, int WM, int WN, bool PIPE>
 __global__ __launch_bounds__(256) void k_gemm_direct(DevW W, const uint8_t *__restrict__ xp,
                                                      const float *__restrict__ xs16,
                                                      const int *__restrict__ xsh, float *__restrict__ y,
-                                                     int M, int act) {
+                                                     int M, int act, int tilesM, int tilesN) {
+    // XCD-aware tile order: workgroups are dealt to the 8 XCDs round-robin
+    // (bid % 8), each XCD with its own L2. Give every XCD a contiguous run of
+    // tiles in row-band-major order, so that the N tiles of a row band — which
+    // all read the same activations, the largest operand — share one L2
+    // instead of fetching the band from HBM once per XCD.
+    const int ntiles = tilesM * tilesN, bid = blockIdx.x;
+    const int q = ntiles / 8, rem = ntiles % 8, xcd = bid % 8, loc = bid / 8;
+    const int t = xcd < rem ? xcd * (q + 1) + loc : rem * (q + 1) + (xcd - rem) * q + loc;
+    const int tm = t / tilesN, tn = t % tilesN;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, col = lane & 15;
     const int Kc = W.Kp / 128, Kp16 = W.Kp / 16;
     int gm[WM], gn[WN], shw[WN];
 #pragma unroll
-    for (int i = 0; i < WM; i++) gm[i] = (blockIdx.y * 2 + (wave >> 1)) * WM + i;
+    for (int i = 0; i < WM; i++) gm[i] = (tm * 2 + (wave >> 1)) * WM + i;
 #pragma unroll
     for (int j = 0; j < WN; j++) {
-        gn[j] = (blockIdx.x * 2 + (wave & 1)) * WN + j;
+        gn[j] = (tn * 2 + (wave & 1)) * WN + j;
         shw[j] = wshift<QT>(W, 16 * gn[j] + col);
     }
     const AFromPrep<WM> src{xp, xs16, Kc, Kp16, gm};
@@ -522,8 +531,9 @@ static hipError_t gemv_t(const DevW &W, const float *x, int M, int vec, float *y
 template <int QT, int WM>
 static hipError_t launch_direct(const DevW &W, const uint8_t *xp, const float *xs16, const int *xsh, float *y,
                                 int M, int act, hipStream_t st) {
-    hipLaunchKernelGGL((k_gemm_direct<QT, WM, 4, false>), dim3(W.Np / 128, mh_mpad(M) / (32 * WM)), dim3(256),
-                       0, st, W, xp, xs16, xsh, y, M, act);
+    const int tilesM = mh_mpad(M) / (32 * WM), tilesN = W.Np / 128;
+    hipLaunchKernelGGL((k_gemm_direct<QT, WM, 4, false>), dim3(tilesM * tilesN), dim3(256), 0, st,
+                       W, xp, xs16, xsh, y, M, act, tilesM, tilesN);
     return hipGetLastError();
 }
 
