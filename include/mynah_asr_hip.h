@@ -11,8 +11,9 @@
  *     dequantized weights to |y - ref| <= 1e-4*|ref| + 1e-6 (ref accumulated in
  *     double), and a row's bits never depend on how many rows share the call.
  *   INT8ACT: activations quantized per row to int8 exactly as qmat.c:186-202;
- *     integer block sums are exact (the reference's small-T path, qmat.c:508-552).
- *     Supported for INT8, INT4, Q8_0 and Q4_0 weights.
+ *     integer block sums are exact and the f32 combine follows qmat.c's order
+ *     (the reference's small-T path, qmat.c:508-552), for every M. Supported
+ *     for INT8, INT4, Q8_0 and Q4_0 weights (other formats return -1).
  *
  * Return values: 0 = done, -1 = not done (the caller runs its CPU path);
  * mynah_asr_hip_last_error() names the reason for the calling thread.

@@ -73,7 +73,7 @@ struct Ctx {
     hipStream_t st = nullptr;
     DBuf x, y, h, xp, xs16, xsh;
     // what the workspace holds now (set by prep)
-    int prep_T = -1, prep_Kp = 0, prep_xsum = 0;
+    int prep_T = -1, prep_Kp = 0, prep_xsum = 0, prep_i8 = 0;
 };
 thread_local Ctx t_ctx;
 
@@ -146,42 +146,66 @@ const mynah_asr_hip_weight *resident(const mynah_asr_hip_wdesc *w) {
 
 int check_numerics_supported(int qtype) {
     if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT) return 0;
-    (void)qtype;
-    return fail("INT8ACT numerics are not implemented in this build");
+    if (mh_i8_supported(qtype)) return 0;
+    return fail("INT8ACT numerics: supported for INT8, INT4, Q8_0 and Q4_0 weights only");
 }
 
-// prep x (device) for a product with inner size k; returns prepared buffers
-int prep(Ctx *c, const float *dx, int T, int k, int Kp, bool xsum, hipStream_t st, uint8_t **xp,
-         float **xs16, int **xsh) {
-    const int Mpad = mh_mpad(T);
-    *xp = (uint8_t *)c->xp.get((size_t)Mpad * Kp * 4);
-    *xs16 = (float *)c->xs16.get((size_t)Mpad * (Kp / 16) * sizeof(float));
-    *xsh = (int *)c->xsh.get((size_t)Mpad * (Kp / 128) * sizeof(int));
-    if (!*xp || !*xs16 || !*xsh) return fail("workspace allocation failed");
-    const int vec = (k % 4 == 0) && (((uintptr_t)dx & 15) == 0);
-    hipError_t e = mh_launch_prep(dx, T, k, Kp, Mpad, *xp, *xs16, *xsh, xsum ? 1 : 0, vec, st);
+// Prepare x (device) for products with weight W in the current numerics mode,
+// into the calling thread's workspace.
+//   EXACT:   xp = f16 A fragments, xs16 = sub-block sums, xsh = shifts
+//   INT8ACT: xp = int8 A fragments, xs16 = row scales sx, xsh = group sums
+int prep_for(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, int T, hipStream_t st) {
+    const int Mpad = mh_mpad(T), Kp = W->dw.Kp, k = W->dw.k;
+    const bool i8 = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT;
+    const bool xsum = !i8 && wants_xsum(W->qtype);
+    uint8_t *xp = (uint8_t *)c->xp.get((size_t)Mpad * Kp * (i8 ? 1 : 4));
+    float *xs16 = (float *)c->xs16.get((size_t)Mpad * (i8 ? 1 : Kp / 16) * sizeof(float));
+    int *xsh = (int *)c->xsh.get((size_t)Mpad * (Kp / (i8 ? 32 : 128)) * sizeof(int));
+    if (!xp || !xs16 || !xsh) return fail("workspace allocation failed");
+    hipError_t e;
+    if (i8) {
+        e = mh_launch_prep_i8(dx, T, k, Kp, Mpad, xp, xs16, xsh, st);
+    } else {
+        const int vec = (k % 4 == 0) && (((uintptr_t)dx & 15) == 0);
+        e = mh_launch_prep(dx, T, k, Kp, Mpad, xp, xs16, xsh, xsum ? 1 : 0, vec, st);
+    }
     if (e != hipSuccess) return fail("prep launch failed", hipGetErrorString(e));
     c->prep_T = T;
     c->prep_Kp = Kp;
     c->prep_xsum = xsum ? 1 : 0;
+    c->prep_i8 = i8 ? 1 : 0;
+    return 0;
+}
+
+bool prep_fits(const Ctx *c, const mynah_asr_hip_weight *W, int T) {
+    const bool i8 = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT;
+    return c->prep_T == T && c->prep_Kp == W->dw.Kp && c->prep_i8 == (i8 ? 1 : 0) &&
+           (i8 || !wants_xsum(W->qtype) || c->prep_xsum);
+}
+
+// the product on the prepared input
+int run_prepped(Ctx *c, const mynah_asr_hip_weight *W, float *dy, int T, int act, hipStream_t st) {
+    hipError_t e;
+    if (c->prep_i8)
+        e = mh_launch_gemm_i8(W->qtype, W->dw, (const uint8_t *)c->xp.p, (const float *)c->xs16.p,
+                              (const int *)c->xsh.p, dy, T, act, st);
+    else
+        e = mh_launch_gemm(W->qtype, W->dw, (const uint8_t *)c->xp.p, (const float *)c->xs16.p,
+                           (const int *)c->xsh.p, dy, T, act, st);
+    if (e != hipSuccess) return fail("gemm launch failed", hipGetErrorString(e));
     return 0;
 }
 
 int gemm_dev(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, float *dy, int T, int act,
              hipStream_t st) {
-    if (mh_use_gemv(W->dw, T)) {
+    if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT && mh_use_gemv(W->dw, T)) {
         const int vec = (W->dw.k % 4 == 0) && (((uintptr_t)dx & 15) == 0);
         hipError_t e = mh_launch_gemv(W->qtype, W->dw, dx, T, vec, dy, act, st);
         if (e != hipSuccess) return fail("gemv launch failed", hipGetErrorString(e));
         return 0;
     }
-    uint8_t *xp;
-    float *xs16;
-    int *xsh;
-    if (prep(c, dx, T, W->dw.k, W->dw.Kp, wants_xsum(W->qtype), st, &xp, &xs16, &xsh)) return -1;
-    hipError_t e = mh_launch_gemm(W->qtype, W->dw, xp, xs16, xsh, dy, T, act, st);
-    if (e != hipSuccess) return fail("gemm launch failed", hipGetErrorString(e));
-    return 0;
+    if (prep_for(c, W, dx, T, st)) return -1;
+    return run_prepped(c, W, dy, T, act, st);
 }
 
 int h2d(Ctx *c, DBuf &b, const float *x, size_t n, float **d) {
@@ -269,10 +293,8 @@ int mynah_asr_hip_prep_dev(const mynah_asr_hip_weight *w, const float *dx, int T
     Ctx *c;
     if (begin(&c)) return -1;
     if (!w || !dx || T <= 0) return fail("bad argument");
-    uint8_t *xp;
-    float *xs16;
-    int *xsh;
-    return prep(c, dx, T, w->dw.k, w->dw.Kp, wants_xsum(w->qtype), pick_stream(stream), &xp, &xs16, &xsh);
+    if (check_numerics_supported(w->qtype)) return -1;
+    return prep_for(c, w, dx, T, pick_stream(stream));
 }
 
 int mynah_asr_hip_qgemm_prepped_dev(const mynah_asr_hip_weight *w, float *dy, int T, int act,
@@ -281,12 +303,8 @@ int mynah_asr_hip_qgemm_prepped_dev(const mynah_asr_hip_weight *w, float *dy, in
     if (begin(&c)) return -1;
     if (!w || !dy || T <= 0) return fail("bad argument");
     if (check_numerics_supported(w->qtype)) return -1;
-    if (c->prep_T != T || c->prep_Kp != w->dw.Kp || (wants_xsum(w->qtype) && !c->prep_xsum))
-        return fail("the prepared input does not fit this weight");
-    hipError_t e = mh_launch_gemm(w->qtype, w->dw, (const uint8_t *)c->xp.p, (const float *)c->xs16.p,
-                                  (const int *)c->xsh.p, dy, T, act, pick_stream(stream));
-    if (e != hipSuccess) return fail("gemm launch failed", hipGetErrorString(e));
-    return 0;
+    if (!prep_fits(c, w, T)) return fail("the prepared input does not fit this weight");
+    return run_prepped(c, w, dy, T, act, pick_stream(stream));
 }
 
 int mynah_asr_hip_dequant_dev(const mynah_asr_hip_weight *w, float *dwd, void *stream) {
@@ -349,30 +367,19 @@ int mynah_asr_hip_qqkv(const mynah_asr_hip_wdesc *wq, const mynah_asr_hip_wdesc 
     }
     float *dx;
     if (h2d(c, c->x, x, (size_t)T * wq->k, &dx)) return -1;
-    // one prepared input serves the three products when their formats agree
-    // on the activation sums; otherwise it is prepared per product
-    const bool same = W[0]->dw.Kp == W[1]->dw.Kp && W[0]->dw.Kp == W[2]->dw.Kp &&
-                      wants_xsum(W[0]->qtype) == wants_xsum(W[1]->qtype) &&
-                      wants_xsum(W[0]->qtype) == wants_xsum(W[2]->qtype);
-    uint8_t *xp = nullptr;
-    float *xs16 = nullptr;
-    int *xsh = nullptr;
+    // one prepared input serves the three products whenever it fits them
+    bool prepared = false;
     for (int i = 0; i < 3; i++) {
-        if (mh_use_gemv(W[i]->dw, T)) {
-            float *dy = (float *)c->y.get((size_t)T * ws[i]->n * sizeof(float));
-            if (!dy) return fail("device buffer allocation failed");
-            if (gemm_dev(c, W[i], dx, dy, T, 0, c->st)) return -1;
-            if (d2h_sync(c, outs[i], dy, (size_t)T * ws[i]->n)) return -1;
-            xp = nullptr;  // the next product prepares again
-            continue;
-        }
-        if (!xp || !same)
-            if (prep(c, dx, T, wq->k, W[i]->dw.Kp, wants_xsum(W[i]->qtype), c->st, &xp, &xs16, &xsh))
-                return -1;
         float *dy = (float *)c->y.get((size_t)T * ws[i]->n * sizeof(float));
         if (!dy) return fail("device buffer allocation failed");
-        hipError_t e = mh_launch_gemm(W[i]->qtype, W[i]->dw, xp, xs16, xsh, dy, T, 0, c->st);
-        if (e != hipSuccess) return fail("gemm launch failed", hipGetErrorString(e));
+        if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT && mh_use_gemv(W[i]->dw, T)) {
+            if (gemm_dev(c, W[i], dx, dy, T, 0, c->st)) return -1;
+        } else {
+            if (!prepared || !prep_fits(c, W[i], T))
+                if (prep_for(c, W[i], dx, T, c->st)) return -1;
+            prepared = true;
+            if (run_prepped(c, W[i], dy, T, 0, c->st)) return -1;
+        }
         if (d2h_sync(c, outs[i], dy, (size_t)T * ws[i]->n)) return -1;
     }
     return 0;

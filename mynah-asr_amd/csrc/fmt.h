@@ -19,8 +19,11 @@
 //                                         b  > 16: [G][chunk][b/16][64][16]
 // Lane bit layouts inside a plane, chosen so that a pair of elements (2t, 2t+1)
 // lands in the two 16-bit halves of a dword with one shift and one mask:
-//   bytes  (8 b/elt) : kstep s = dwords 2s, 2s+1; dword 2s+h holds elements
-//                      4h+{0,2,1,3} in bytes 0..3
+//   bytes  (8 b/elt) : kstep s = dwords 2s, 2s+1; dword 2s holds elements
+//                      {0,4,1,5}, dword 2s+1 elements {2,6,3,7} in bytes 0..3
+//                      (the order in which a nibble dword expands to bytes,
+//                      w & 0x0F0F0F0F and (w >> 4) & 0x0F0F0F0F, so that one
+//                      int8 activation layout serves byte and nibble weights)
 //   nibble (4 b/elt) : kstep s = dword s; element 2t+u at bit 16u + 4t
 //   crumb  (2 b/elt) : ksteps 2v, 2v+1 = dword v; element 2t+u of kstep 2v+w
 //                      at bit 16u + 8w + 2t
@@ -100,10 +103,10 @@ __device__ __forceinline__ uint32_t bit_pair(uint32_t w, int s, int t) {
     return (w >> (4 * s + t)) & 0x00010001u;
 }
 
-// int8 bytes -> half8 of their signed values
+// int8 bytes -> half8 of their signed values (pairs (0,1) (2,3) (4,5) (6,7))
 __device__ __forceinline__ half8 dec_bytes(uint32_t w0, uint32_t w1) {
-    const uint32_t a = (w0 & 0x00FF00FFu) ^ 0x64806480u, b = ((w0 >> 8) & 0x00FF00FFu) ^ 0x64806480u;
-    const uint32_t c = (w1 & 0x00FF00FFu) ^ 0x64806480u, d = ((w1 >> 8) & 0x00FF00FFu) ^ 0x64806480u;
+    const uint32_t a = (w0 & 0x00FF00FFu) ^ 0x64806480u, b = (w1 & 0x00FF00FFu) ^ 0x64806480u;
+    const uint32_t c = ((w0 >> 8) & 0x00FF00FFu) ^ 0x64806480u, d = ((w1 >> 8) & 0x00FF00FFu) ^ 0x64806480u;
     return pairs_to_half8(a, b, c, d, (_Float16)1152.0f);
 }
 

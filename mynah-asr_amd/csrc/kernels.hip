@@ -452,6 +452,160 @@ __global__ __launch_bounds__(256) void k_prep(const float *__restrict__ x, int M
 }
 
 // ---------------------------------------------------------------------------
+// INT8ACT numerics: the reference's small-T int8 path (src/qmat.c:508-552),
+// for every M. Activations are quantized per row exactly as
+// quantize_act_int8 (qmat.c:186-202); v_mfma_i32_16x16x64_i8 forms the exact
+// integer sums; the f32 combine follows the reference's order:
+//   INT8   y = ((float)s * ws) * sx           (s over the whole row)
+//   INT4   acc = acc + (float)ig * sg per group of 32, in order; y = acc * sx
+//   Q8_0/Q4_0  the same with the block factor d (the oracle's block semantics)
+// Int8 activation layout: [row group][kstep pair][64][16 B]; each lane's 16
+// bytes are kstep 2p then 2p+1, each as dwords {e0,e4,e1,e5} {e2,e6,e3,e7} of
+// elements 8g..8g+7 — the byte order of the weight planes, so weight bytes
+// (or nibbles expanded with two masks) feed the MFMA unchanged.
+typedef int i4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ i4v mfma_i8(i4v a, i4v b, i4v c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int act_q8(float v, float inv) {
+    const float t = __fmul_rn(v, inv);
+    int q = (int)(t >= 0.0f ? __fadd_rn(t, 0.5f) : __fsub_rn(t, 0.5f));
+    return q > 127 ? 127 : (q < -127 ? -127 : q);
+}
+
+// one workgroup (4 waves) per 16-row group
+__global__ __launch_bounds__(256) void k_prep_i8(const float *__restrict__ x, int M, int K, int Kp,
+                                                 uint8_t *__restrict__ qx, float *__restrict__ sx,
+                                                 int *__restrict__ gsum) {
+    __shared__ float invs[16];
+    const int G = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int rr = 0; rr < 4; rr++) {
+        const int m = 16 * G + 4 * wave + rr;
+        float amax = 0.0f;
+        if (m < M) {
+            const float *row = x + (size_t)m * K;
+            for (int j = lane; j < K; j += 64) amax = fmaxf(amax, fabsf(row[j]));
+        }
+        for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+        if (lane == 0) {
+            invs[4 * wave + rr] = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+            sx[m] = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 0.0f;
+        }
+    }
+    __syncthreads();
+    const int r = lane & 15, g = lane >> 4, m = 16 * G + r;
+    const float inv = invs[r];
+    const bool live = m < M && inv > 0.0f;
+    const float *row = x + (size_t)(m < M ? m : 0) * K;
+    const int P = Kp / 64;
+    static const int kWord[8] = {0, 0, 1, 1, 0, 0, 1, 1};
+    static const int kByte[8] = {0, 2, 0, 2, 1, 3, 1, 3};
+    for (int p = wave; p < P; p += 4) {
+        uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int k0 = 64 * p + 32 * h + 8 * g;
+            int gs = 0;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int q = (live && k0 + j < K) ? act_q8(row[k0 + j], inv) : 0;
+                gs += q;
+                w[2 * h + kWord[j]] |= ((uint32_t)q & 0xffu) << (8 * kByte[j]);
+            }
+            gs += __shfl_xor(gs, 16);
+            gs += __shfl_xor(gs, 32);
+            if (g == 0) gsum[((size_t)G * (Kp / 32) + 2 * p + h) * 16 + r] = gs;
+        }
+        *(uint4 *)(qx + (((size_t)G * P + p) * 64 + lane) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+// 4 waves per workgroup, one 16-column group each, WM row groups per wave.
+template <int QT, int WM>
+__global__ __launch_bounds__(256) void k_gemm_i8(DevW W, const uint8_t *__restrict__ qx,
+                                                 const float *__restrict__ sx, const int *__restrict__ gsum,
+                                                 float *__restrict__ y, int M, int act) {
+    constexpr bool NIB = QT == QT_INT4 || QT == QT_Q4_0;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, col = lane & 15;
+    const int G = blockIdx.x * 4 + wave;       // weight row group
+    const int Kc = W.Kp / 128, P = W.Kp / 64;
+    int gm[WM];
+#pragma unroll
+    for (int i = 0; i < WM; i++) gm[i] = blockIdx.y * WM + i;
+    i4v si[WM];
+    f4 acc[WM];
+#pragma unroll
+    for (int i = 0; i < WM; i++) {
+        si[i] = i4v{0, 0, 0, 0};
+        acc[i] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int p = 0; p < P; p++) {
+        const int c = p >> 1, q = p & 1;
+        uint32_t b[4];
+        if constexpr (NIB) {
+            const uint2 v = *(const uint2 *)(W.p0 + (((size_t)G * Kc + c) * 64 + lane) * 16 + 8 * q);
+            b[0] = v.x & 0x0F0F0F0Fu;
+            b[1] = (v.x >> 4) & 0x0F0F0F0Fu;
+            b[2] = v.y & 0x0F0F0F0Fu;
+            b[3] = (v.y >> 4) & 0x0F0F0F0Fu;
+        } else {
+            const uint4 v = *(const uint4 *)(W.p0 + ((((size_t)G * Kc + c) * 2 + q) * 64 + lane) * 16);
+            b[0] = v.x; b[1] = v.y; b[2] = v.z; b[3] = v.w;
+        }
+        float d0 = 0.f, d1 = 0.f;
+        if constexpr (QT == QT_Q8_0 || QT == QT_Q4_0) {
+            const uint32_t hd = *(const uint32_t *)(W.h + (((size_t)G * Kc + c) * 16 + col) * 8 + 4 * q);
+            d0 = h2f(hd & 0xffff);
+            d1 = h2f(hd >> 16);
+        } else if constexpr (QT == QT_INT4) {
+            const float2 v = *(const float2 *)(W.h2 + (((size_t)G * Kc + c) * 16 + col) * 4 + 2 * q);
+            d0 = v.x;
+            d1 = v.y;
+        }
+        const i4v bb = {(int)b[0], (int)b[1], (int)b[2], (int)b[3]};
+        const i4v blo = {(int)b[0], (int)b[1], 0, 0}, bhi = {0, 0, (int)b[2], (int)b[3]};
+#pragma unroll
+        for (int i = 0; i < WM; i++) {
+            const i4v a = *(const i4v *)(qx + (((size_t)gm[i] * P + p) * 64 + lane) * 16);
+            if constexpr (QT == QT_INT8) {
+                si[i] = mfma_i8(a, bb, si[i]);
+            } else {
+                i4v t0 = mfma_i8(a, blo, i4v{0, 0, 0, 0});
+                i4v t1 = mfma_i8(a, bhi, i4v{0, 0, 0, 0});
+                if constexpr (NIB) {  // sum (n - 8) * q = sum n * q - 8 * sum q
+                    const int4 g0 = *(const int4 *)(gsum + ((size_t)gm[i] * (W.Kp / 32) + 2 * p) * 16 + 4 * g);
+                    const int4 g1 = *(const int4 *)(gsum + ((size_t)gm[i] * (W.Kp / 32) + 2 * p + 1) * 16 + 4 * g);
+                    t0 -= 8 * i4v{g0.x, g0.y, g0.z, g0.w};
+                    t1 -= 8 * i4v{g1.x, g1.y, g1.z, g1.w};
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    acc[i][r] = __fadd_rn(acc[i][r], __fmul_rn((float)t0[r], d0));
+                    acc[i][r] = __fadd_rn(acc[i][r], __fmul_rn((float)t1[r], d1));
+                }
+            }
+        }
+    }
+    const int n = 16 * G + col;
+    if (n >= W.n) return;
+    const float ws = QT == QT_INT8 ? W.h2[n] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = 16 * gm[i] + 4 * g + r;
+            if (m >= M) continue;
+            float v;
+            if constexpr (QT == QT_INT8) v = __fmul_rn(__fmul_rn((float)si[i][r], ws), sx[m]);
+            else v = __fmul_rn(acc[i][r], sx[m]);
+            y[(size_t)m * W.n + n] = act ? silu_f(v) : v;
+        }
+}
+
+// ---------------------------------------------------------------------------
 // Dequantization from the resident layout: one wave per (row group, chunk).
 // Values are formed exactly as the reference decoders form them.
 template <int QT>
@@ -604,6 +758,42 @@ static hipError_t launch_dq(const DevW &W, float *out, hipStream_t st) {
 
 hipError_t mh_launch_dequant(int qtype, const DevW &W, float *out, hipStream_t st) {
     MH_DISPATCH(launch_dq, qtype, W, out, st)
+}
+
+bool mh_i8_supported(int qtype) {
+    return qtype == QT_INT8 || qtype == QT_INT4 || qtype == QT_Q8_0 || qtype == QT_Q4_0;
+}
+
+hipError_t mh_launch_prep_i8(const float *x, int M, int K, int Kp, int Mpad, uint8_t *qx, float *sx,
+                             int *gsum, hipStream_t st) {
+    hipLaunchKernelGGL(k_prep_i8, dim3(Mpad / 16), dim3(256), 0, st, x, M, K, Kp, qx, sx, gsum);
+    return hipGetLastError();
+}
+
+template <int QT, int WM>
+static hipError_t launch_i8(const DevW &W, const uint8_t *qx, const float *sx, const int *gsum, float *y,
+                            int M, int act, hipStream_t st) {
+    hipLaunchKernelGGL((k_gemm_i8<QT, WM>), dim3(W.Np / 64, mh_mpad(M) / (16 * WM)), dim3(256), 0, st,
+                       W, qx, sx, gsum, y, M, act);
+    return hipGetLastError();
+}
+
+template <int QT>
+static hipError_t gemm_i8_t(const DevW &W, const uint8_t *qx, const float *sx, const int *gsum, float *y,
+                            int M, int act, hipStream_t st) {
+    if (M <= 64) return launch_i8<QT, 1>(W, qx, sx, gsum, y, M, act, st);
+    return launch_i8<QT, 2>(W, qx, sx, gsum, y, M, act, st);
+}
+
+hipError_t mh_launch_gemm_i8(int qtype, const DevW &W, const uint8_t *qx, const float *sx, const int *gsum,
+                             float *y, int M, int act, hipStream_t st) {
+    switch (qtype) {
+    case QT_INT8: return gemm_i8_t<QT_INT8>(W, qx, sx, gsum, y, M, act, st);
+    case QT_INT4: return gemm_i8_t<QT_INT4>(W, qx, sx, gsum, y, M, act, st);
+    case QT_Q8_0: return gemm_i8_t<QT_Q8_0>(W, qx, sx, gsum, y, M, act, st);
+    case QT_Q4_0: return gemm_i8_t<QT_Q4_0>(W, qx, sx, gsum, y, M, act, st);
+    }
+    return hipErrorInvalidValue;
 }
 
 hipError_t mh_launch_silu(float *x, size_t n, hipStream_t st) {

@@ -24,3 +24,10 @@ hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const flo
                           const int *xsh, float *y, int M, int act, hipStream_t st);
 hipError_t mh_launch_dequant(int qtype, const DevW &W, float *out, hipStream_t st);
 hipError_t mh_launch_silu(float *x, size_t n, hipStream_t st);
+
+// INT8ACT numerics (formats INT8, INT4, Q8_0, Q4_0)
+bool mh_i8_supported(int qtype);
+hipError_t mh_launch_prep_i8(const float *x, int M, int K, int Kp, int Mpad, uint8_t *qx, float *sx,
+                             int *gsum, hipStream_t st);
+hipError_t mh_launch_gemm_i8(int qtype, const DevW &W, const uint8_t *qx, const float *sx, const int *gsum,
+                             float *y, int M, int act, hipStream_t st);

@@ -176,10 +176,10 @@ int mh_repack(const mynah_asr_hip_wdesc *w, HostLayout *L) {
                         const uint32_t code = code_of(S, row, 128 * c + 32 * s + 8 * g + j);
                         const int t = j >> 1, u = j & 1;
                         if (bytes8) {
-                            // dword 2s + j/4 holds elements {0,2,1,3} of its quad
-                            const int q = j & 3;
-                            const int pos = (q == 0) ? 0 : (q == 2) ? 1 : (q == 1) ? 2 : 3;
-                            w0[2 * s + (j >> 2)] |= (code & 0xffu) << (8 * pos);
+                            // dword 2s: elements {0,4,1,5}; dword 2s+1: {2,6,3,7}
+                            static const int kWord[8] = {0, 0, 1, 1, 0, 0, 1, 1};
+                            static const int kByte[8] = {0, 2, 0, 2, 1, 3, 1, 3};
+                            w0[2 * s + kWord[j]] |= (code & 0xffu) << (8 * kByte[j]);
                         } else if (nib) {
                             w0[s] |= (code & 15u) << (16 * u + 4 * t);
                             if (qt == MYNAH_ASR_HIP_Q5_K)
