@@ -71,7 +71,7 @@ struct DBuf {
 struct Ctx {
     int state = 0;  // 0 uninitialised, 1 ok, -1 failed
     hipStream_t st = nullptr;
-    DBuf x, y, h, xp, xs16, xsh;
+    DBuf x, y, h, xp, xs16, xpf;
     // what the workspace holds now (set by prep)
     int prep_T = -1, prep_Kp = 0, prep_xsum = 0, prep_i8 = 0;
 };
@@ -152,22 +152,22 @@ int check_numerics_supported(int qtype) {
 
 // Prepare x (device) for products with weight W in the current numerics mode,
 // into the calling thread's workspace.
-//   EXACT:   xp = f16 A fragments, xs16 = sub-block sums, xsh = shifts
-//   INT8ACT: xp = int8 A fragments, xs16 = row scales sx, xsh = group sums
+//   EXACT:   xp = f16 A fragments, xs16 = sub-block sums, xpf = chunk fold factors
+//   INT8ACT: xp = int8 A fragments, xs16 = row scales sx
 int prep_for(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, int T, hipStream_t st) {
     const int Mpad = mh_mpad(T), Kp = W->dw.Kp, k = W->dw.k;
     const bool i8 = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT;
     const bool xsum = !i8 && wants_xsum(W->qtype);
     uint8_t *xp = (uint8_t *)c->xp.get((size_t)Mpad * Kp * (i8 ? 1 : 4));
     float *xs16 = (float *)c->xs16.get((size_t)Mpad * (i8 ? 1 : Kp / 16) * sizeof(float));
-    int *xsh = (int *)c->xsh.get((size_t)Mpad * (Kp / (i8 ? 32 : 128)) * sizeof(int));
-    if (!xp || !xs16 || !xsh) return fail("workspace allocation failed");
+    float *xpf = (float *)c->xpf.get((size_t)Mpad * (Kp / 128) * sizeof(float));
+    if (!xp || !xs16 || !xpf) return fail("workspace allocation failed");
     hipError_t e;
     if (i8) {
-        e = mh_launch_prep_i8(dx, T, k, Kp, Mpad, xp, xs16, xsh, st);
+        e = mh_launch_prep_i8(dx, T, k, Kp, Mpad, xp, xs16, st);
     } else {
         const int vec = (k % 4 == 0) && (((uintptr_t)dx & 15) == 0);
-        e = mh_launch_prep(dx, T, k, Kp, Mpad, xp, xs16, xsh, xsum ? 1 : 0, vec, st);
+        e = mh_launch_prep(dx, T, k, Kp, Mpad, xp, xs16, xpf, xsum ? 1 : 0, vec, st);
     }
     if (e != hipSuccess) return fail("prep launch failed", hipGetErrorString(e));
     c->prep_T = T;
@@ -187,11 +187,11 @@ bool prep_fits(const Ctx *c, const mynah_asr_hip_weight *W, int T) {
 int run_prepped(Ctx *c, const mynah_asr_hip_weight *W, float *dy, int T, int act, hipStream_t st) {
     hipError_t e;
     if (c->prep_i8)
-        e = mh_launch_gemm_i8(W->qtype, W->dw, (const uint8_t *)c->xp.p, (const float *)c->xs16.p,
-                              (const int *)c->xsh.p, dy, T, act, st);
+        e = mh_launch_gemm_i8(W->qtype, W->dw, (const uint8_t *)c->xp.p, (const float *)c->xs16.p, dy, T,
+                              act, st);
     else
         e = mh_launch_gemm(W->qtype, W->dw, (const uint8_t *)c->xp.p, (const float *)c->xs16.p,
-                           (const int *)c->xsh.p, dy, T, act, st);
+                           (const float *)c->xpf.p, dy, T, act, st);
     if (e != hipSuccess) return fail("gemm launch failed", hipGetErrorString(e));
     return 0;
 }

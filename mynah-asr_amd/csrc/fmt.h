@@ -1,34 +1,38 @@
 // fmt.h — device-side view of the resident weight layouts (gfx950).
 //
 // Every weight format is repacked at upload into an "MFMA-native" layout: the
-// quant bits each lane of a wave feeds into v_mfma_f32_16x16x32_f16 sit at
+// quant bits each lane of a wave feeds into v_mfma_f32_32x32x16_f16 sit at
 // consecutive addresses, so one wave-wide load of 4/8/16 bytes per lane moves a
 // contiguous 256 B/512 B/1 KiB block. Nothing is widened: the planes hold the
 // same bits as the ggml blocks (or the qmat INT8/INT4 arrays), only reordered.
 //
 // Geometry shared by every kernel:
-//   row group  G  = 16 weight rows (the B/N side of one MFMA)
-//   kstep         = 32 elements of K (one MFMA); chunk = 4 ksteps = 128 of K
-//   lane l (0..63): column r = l & 15, k-group g = l >> 4; in kstep s it carries
-//                   elements 8g .. 8g+7 of that kstep for weight row 16G + r.
-// MFMA operand convention (16x16x32 f16): A = activations (row = l&15, k =
-// 8g+j), B = weights (column = l&15, k = 8g+j); D lane l holds rows 4g+i,
-// column l&15.
+//   column group G = 32 weight rows (the B/N side of one MFMA)
+//   kstep          = 32 elements of K (one block of the 32-block formats)
+//   half-step u    = 16 elements of K (the K of one MFMA); kstep s = u 2s, 2s+1
+//   chunk          = 4 ksteps = 8 half-steps = 128 elements of K
+//   lane l (0..63): column r = l & 31, half h = l >> 5; in half-step u it
+//                   carries chunk elements 16u + 8h + j (j = 0..7) of weight
+//                   row 32G + r.
+// MFMA operand convention (32x32x16 f16): A = activations (row = l&31, k =
+// 8h+j), B = weights (column = l&31, k = 8h+j); D lane l holds column l&31 and
+// rows 8i + 4h + jj in element 4i + jj (i, jj = 0..3).
 //
 // Planes (bytes per lane per chunk = b):  b <= 16: [G][chunk][64][b]
 //                                         b  > 16: [G][chunk][b/16][64][16]
 // Lane bit layouts inside a plane, chosen so that a pair of elements (2t, 2t+1)
 // lands in the two 16-bit halves of a dword with one shift and one mask:
-//   bytes  (8 b/elt) : kstep s = dwords 2s, 2s+1; dword 2s holds elements
-//                      {0,4,1,5}, dword 2s+1 elements {2,6,3,7} in bytes 0..3
+//   bytes  (8 b/elt) : half-step u = dwords 2u, 2u+1; dword 2u holds elements
+//                      {0,4,1,5}, dword 2u+1 elements {2,6,3,7} in bytes 0..3
 //                      (the order in which a nibble dword expands to bytes,
 //                      w & 0x0F0F0F0F and (w >> 4) & 0x0F0F0F0F, so that one
-//                      int8 activation layout serves byte and nibble weights)
-//   nibble (4 b/elt) : kstep s = dword s; element 2t+u at bit 16u + 4t
-//   crumb  (2 b/elt) : ksteps 2v, 2v+1 = dword v; element 2t+u of kstep 2v+w
-//                      at bit 16u + 8w + 2t
-//   bit    (1 b/elt) : one dword per chunk; element 2t+u of kstep s at bit
-//                      16u + 4s + t
+//                      int8 activation layout serves byte and nibble weights);
+//                      kstep s is the 16-byte part s
+//   nibble (4 b/elt) : half-step u = dword u; element 2t+v at bit 16v + 4t
+//   crumb  (2 b/elt) : half-steps 2w, 2w+1 = dword w; element 2t+v of half-step
+//                      2w+x at bit 16v + 8x + 2t
+//   bit    (1 b/elt) : half-steps 4w..4w+3 = dword w; element 2t+v of half-step
+//                      4w+x at bit 16v + 4x + t
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -36,6 +40,7 @@
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
 
 enum {
     QT_F32 = 0, QT_INT8 = 1, QT_INT4 = 2, QT_Q4_0 = 18, QT_Q8_0 = 24, QT_Q2_K = 26,
@@ -51,34 +56,6 @@ struct DevW {
     int n, k;            // logical shape
     int Np, Kp;          // padded: Np multiple of 128, Kp multiple of 256
 };
-
-__device__ __forceinline__ uint32_t ldg32(const uint8_t *p) { return *(const uint32_t *)p; }
-
-// Load b bytes per lane of plane p for (row group G, chunk c) into w[b/4].
-template <int B>
-__device__ __forceinline__ void load_plane(const uint8_t *p, int Kc, int G, int c, int lane,
-                                           uint32_t (&w)[(B + 3) / 4]) {
-    const size_t tile = (size_t)G * Kc + c;
-    if constexpr (B <= 16) {
-        const uint8_t *q = p + (tile * 64 + lane) * B;
-        if constexpr (B == 16) {
-            const uint4 v = *(const uint4 *)q;
-            w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-        } else if constexpr (B == 8) {
-            const uint2 v = *(const uint2 *)q;
-            w[0] = v.x; w[1] = v.y;
-        } else {
-            w[0] = ldg32(q);
-        }
-    } else {
-#pragma unroll
-        for (int part = 0; part < B / 16; part++) {
-            const uint4 v = *(const uint4 *)(p + ((tile * (B / 16) + part) * 64 + lane) * 16);
-            w[4 * part + 0] = v.x; w[4 * part + 1] = v.y;
-            w[4 * part + 2] = v.z; w[4 * part + 3] = v.w;
-        }
-    }
-}
 
 __device__ __forceinline__ half8 pairs_to_half8(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
                                                 _Float16 bias) {
@@ -96,11 +73,12 @@ __device__ __forceinline__ half8 pairs_to_half8(uint32_t a, uint32_t b, uint32_t
 
 #define MAGIC 0x64006400u
 __device__ __forceinline__ uint32_t nib_pair(uint32_t w, int t) { return (w >> (4 * t)) & 0x000F000Fu; }
-__device__ __forceinline__ uint32_t crumb_pair(uint32_t w, int s, int t) {
-    return (w >> (8 * (s & 1) + 2 * t)) & 0x00030003u;
+// pair t of half-step u in a crumb dword / a bit dword
+__device__ __forceinline__ uint32_t crumb_pair(uint32_t w, int u, int t) {
+    return (w >> (8 * (u & 1) + 2 * t)) & 0x00030003u;
 }
-__device__ __forceinline__ uint32_t bit_pair(uint32_t w, int s, int t) {
-    return (w >> (4 * s + t)) & 0x00010001u;
+__device__ __forceinline__ uint32_t bit_pair(uint32_t w, int u, int t) {
+    return (w >> (4 * (u & 3) + t)) & 0x00010001u;
 }
 
 // int8 bytes -> half8 of their signed values (pairs (0,1) (2,3) (4,5) (6,7))
@@ -114,91 +92,215 @@ __device__ __forceinline__ float h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
 
+// a[i] for a runtime i in 0..3 as register selects (a dynamic index into a
+// register array would go through scratch memory)
+__device__ __forceinline__ uint32_t sel4(const uint32_t (&a)[4], int i) {
+    const uint32_t lo = (i & 1) ? a[1] : a[0], hi = (i & 1) ? a[3] : a[2];
+    return (i & 2) ? hi : lo;
+}
+
+// header slot of (column group G, unit c of `units`, the lane's column)
+__device__ __forceinline__ size_t hdr(int G, int units, int c, int lane) {
+    return ((size_t)G * units + c) * 32 + (lane & 31);
+}
+
+// Per-kstep plane words: B bytes per lane per chunk; kstep s uses
+//   B = 64: the 16-byte part s            B = 32: 8 bytes (dwords 2s, 2s+1)
+//   B = 16: dword s                       B =  8: dword s >> 1
+template <int B> struct KWords { static constexpr int N = B == 64 ? 4 : (B == 32 ? 2 : 1); };
+
+template <int B>
+__device__ __forceinline__ void load_kpart(const uint8_t *p, int Kc, int G, int c, int s, int lane,
+                                           uint32_t (&w)[KWords<B>::N]) {
+    const size_t tile = (size_t)G * Kc + c;
+    if constexpr (B == 64) {
+        const uint4 v = *(const uint4 *)(p + ((tile * 4 + s) * 64 + lane) * 16);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else if constexpr (B == 32) {
+        const uint2 v = *(const uint2 *)(p + ((tile * 2 + (s >> 1)) * 64 + lane) * 16 + 8 * (s & 1));
+        w[0] = v.x; w[1] = v.y;
+    } else if constexpr (B == 16) {
+        w[0] = *(const uint32_t *)(p + (tile * 64 + lane) * 16 + 4 * s);
+    } else {
+        static_assert(B == 8, "plane width");
+        w[0] = *(const uint32_t *)(p + (tile * 64 + lane) * 8 + 4 * (s >> 1));
+    }
+}
+
+// Staging of a plane for half a chunk (the LDS-staged GEMM): B >= 32 stages
+// the half's own 32*B bytes of the (G, chunk) block, narrower planes the whole
+// 64*B-byte block. off(h) = byte offset of half h inside the block.
+template <int B> struct Stage {
+    static constexpr int BYTES = B == 0 ? 0 : (B >= 32 ? 32 * B : 64 * B);
+    static __device__ __forceinline__ int off(int h) { return B >= 32 ? h * 32 * B : 0; }
+};
+
+// the same words from a staged region r (the half containing kstep s)
+template <int B>
+__device__ __forceinline__ void lds_kpart(const uint8_t *r, int s, int lane, uint32_t (&w)[KWords<B>::N]) {
+    if constexpr (B == 64) {
+        const uint4 v = *(const uint4 *)(r + ((s & 1) * 64 + lane) * 16);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else if constexpr (B == 32) {
+        const uint2 v = *(const uint2 *)(r + lane * 16 + 8 * (s & 1));
+        w[0] = v.x; w[1] = v.y;
+    } else if constexpr (B == 16) {
+        w[0] = *(const uint32_t *)(r + lane * 16 + 4 * s);
+    } else {
+        static_assert(B == 8, "plane width");
+        w[0] = *(const uint32_t *)(r + lane * 8 + 4 * (s >> 1));
+    }
+}
+
+__device__ __forceinline__ half8 dec_nib(uint32_t w, _Float16 bias) {
+    return pairs_to_half8(nib_pair(w, 0) | MAGIC, nib_pair(w, 1) | MAGIC, nib_pair(w, 2) | MAGIC,
+                          nib_pair(w, 3) | MAGIC, bias);
+}
+
 // ---------------------------------------------------------------------------
 // Format traits. For every format:
-//   B0, B1       bytes per lane per chunk in plane 0 / plane 1
-//   SUB16        sub-blocks of 16 (two scales per kstep) instead of 32
+//   SUB16        sub-blocks of 16 (one per half-step) instead of 32 (per kstep)
 //   MINS         affine format: value = scale*q - min
-//   Raw          per-lane registers for one chunk
-//   load(...)    fetch the chunk's planes and headers for column r
-//   decode(raw,s)            half8 of the integer quant values of kstep s
-//   scale(raw,s,h, &sc,&mn)  factor (and min) of kstep s's sub-block h (h = 0
-//                            for SUB16 == false; 0/1 for the two 16-halves)
+//   B0, B1       plane widths (bytes per lane per chunk) of p0 / p1
+//   HB, H2       header bytes / h2 bytes per column group and header unit
+//   hb_src, h2_src   the (column group, chunk)'s header unit in global memory
+//   Hdr          per-lane header registers of one chunk (block factors)
+//   RawK         per-lane plane words of one kstep
+//   load_hdr(W, Kc, G, c, lane, hdr)      the chunk's headers for column r
+//   load_k(W, Kc, G, c, s, lane, raw)     kstep s's plane words
+//   hdr_lds(hb, h2b, c, lane, hdr), k_lds(r0, r1, s, lane, raw)
+//                                         the same from staged LDS regions
+//   decode(raw, s, kh)                    half8 of the integer quants of
+//                                         half-step 2s+kh
+//   scale(hdr, s, hh, &sc, &mn)           factor (and min) of kstep s's
+//                                         sub-block hh (0 unless SUB16)
 // The factors are computed exactly as the reference decoders do, so that
 // sc*q - mn (or sc*q) reproduces their f32 values bit for bit.
 // ---------------------------------------------------------------------------
 template <int QT> struct Fmt;
 
-template <> struct Fmt<QT_Q8_0> {
-    static constexpr int B0 = 32, B1 = 0;
-    static constexpr bool SUB16 = false, MINS = false;
-    struct Raw { uint32_t w[8]; uint32_t d[2]; };  // d: the chunk's four f16 block factors
-    static __device__ __forceinline__ void load(const DevW &W, int Kc, int G, int c, int lane, Raw &R) {
-        load_plane<32>(W.p0, Kc, G, c, lane, R.w);
-        const uint2 hd = *(const uint2 *)(W.h + (((size_t)G * Kc + c) * 16 + (lane & 15)) * 8);
-        R.d[0] = hd.x; R.d[1] = hd.y;
-    }
-    static __device__ __forceinline__ half8 decode(const Raw &R, int s) { return dec_bytes(R.w[2 * s], R.w[2 * s + 1]); }
-    static __device__ __forceinline__ void scale(const Raw &R, int s, int, float &sc, float &mn) {
-        sc = h2f((R.d[s >> 1] >> (16 * (s & 1))) & 0xffff);
-        mn = 0.0f;
-    }
-};
-
-template <> struct Fmt<QT_Q4_0> {
-    static constexpr int B0 = 16, B1 = 0;
-    static constexpr bool SUB16 = false, MINS = false;
-    struct Raw { uint32_t w[4]; uint32_t d[2]; };
-    static __device__ __forceinline__ void load(const DevW &W, int Kc, int G, int c, int lane, Raw &R) {
-        load_plane<16>(W.p0, Kc, G, c, lane, R.w);
-        const uint2 hd = *(const uint2 *)(W.h + (((size_t)G * Kc + c) * 16 + (lane & 15)) * 8);
-        R.d[0] = hd.x; R.d[1] = hd.y;
-    }
-    static __device__ __forceinline__ half8 decode(const Raw &R, int s) {
-        const uint32_t w = R.w[s];
-        return pairs_to_half8(nib_pair(w, 0) | MAGIC, nib_pair(w, 1) | MAGIC, nib_pair(w, 2) | MAGIC,
-                              nib_pair(w, 3) | MAGIC, (_Float16)1032.0f);
-    }
-    static __device__ __forceinline__ void scale(const Raw &R, int s, int, float &sc, float &mn) {
-        sc = h2f((R.d[s >> 1] >> (16 * (s & 1))) & 0xffff);
-        mn = 0.0f;
-    }
-};
+// headers per chunk: [G][Kc][32 columns][b]; per super-block: [G][Kc/2][32][b]
+__device__ __forceinline__ const uint8_t *chunk_hdr(const uint8_t *h, int Kc, int G, int c, int b) {
+    return h + hdr(G, Kc, c, 0) * b;
+}
+__device__ __forceinline__ const uint8_t *sb_hdr(const uint8_t *h, int Kc, int G, int c, int b) {
+    return h + hdr(G, Kc / 2, c / 2, 0) * b;
+}
 
 template <> struct Fmt<QT_INT8> {
-    static constexpr int B0 = 32, B1 = 0;
     static constexpr bool SUB16 = false, MINS = false;
-    struct Raw { uint32_t w[8]; float s; };
-    static __device__ __forceinline__ void load(const DevW &W, int Kc, int G, int c, int lane, Raw &R) {
-        load_plane<32>(W.p0, Kc, G, c, lane, R.w);
-        R.s = W.h2[16 * G + (lane & 15)];
+    static constexpr int B0 = 64, B1 = 0, HB = 0, H2 = 128;
+    struct Hdr { float s; };
+    struct RawK { uint32_t w[4]; };
+    static __device__ __forceinline__ const uint8_t *hb_src(const DevW &, int, int, int) { return nullptr; }
+    static __device__ __forceinline__ const uint8_t *h2_src(const DevW &W, int, int G, int) {
+        return (const uint8_t *)(W.h2 + 32 * G);
     }
-    static __device__ __forceinline__ half8 decode(const Raw &R, int s) { return dec_bytes(R.w[2 * s], R.w[2 * s + 1]); }
-    static __device__ __forceinline__ void scale(const Raw &R, int, int, float &sc, float &mn) { sc = R.s; mn = 0.0f; }
+    static __device__ __forceinline__ void load_hdr(const DevW &W, int, int G, int, int lane, Hdr &H) {
+        H.s = W.h2[32 * G + (lane & 31)];
+    }
+    static __device__ __forceinline__ void hdr_lds(const uint8_t *, const uint8_t *h2b, int, int lane, Hdr &H) {
+        H.s = ((const float *)h2b)[lane & 31];
+    }
+    static __device__ __forceinline__ void load_k(const DevW &W, int Kc, int G, int c, int s, int lane, RawK &R) {
+        load_kpart<64>(W.p0, Kc, G, c, s, lane, R.w);
+    }
+    static __device__ __forceinline__ void k_lds(const uint8_t *r0, const uint8_t *, int s, int lane, RawK &R) {
+        lds_kpart<64>(r0, s, lane, R.w);
+    }
+    static __device__ __forceinline__ half8 decode(const RawK &R, int, int kh) { return dec_bytes(R.w[2 * kh], R.w[2 * kh + 1]); }
+    static __device__ __forceinline__ void scale(const Hdr &H, int, int, float &sc, float &mn) { sc = H.s; mn = 0.0f; }
 };
 
 template <> struct Fmt<QT_INT4> {
-    static constexpr int B0 = 16, B1 = 0;
     static constexpr bool SUB16 = false, MINS = false;
-    struct Raw { uint32_t w[4]; float d[4]; };
-    static __device__ __forceinline__ void load(const DevW &W, int Kc, int G, int c, int lane, Raw &R) {
-        load_plane<16>(W.p0, Kc, G, c, lane, R.w);
-        const float4 v = *(const float4 *)(W.h2 + (((size_t)G * Kc + c) * 16 + (lane & 15)) * 4);
-        R.d[0] = v.x; R.d[1] = v.y; R.d[2] = v.z; R.d[3] = v.w;
+    static constexpr int B0 = 32, B1 = 0, HB = 0, H2 = 512;
+    struct Hdr { float d[4]; };
+    struct RawK { uint32_t w[2]; };
+    static __device__ __forceinline__ const uint8_t *hb_src(const DevW &, int, int, int) { return nullptr; }
+    static __device__ __forceinline__ const uint8_t *h2_src(const DevW &W, int Kc, int G, int c) {
+        return (const uint8_t *)(W.h2 + hdr(G, Kc, c, 0) * 4);
     }
-    static __device__ __forceinline__ half8 decode(const Raw &R, int s) {
-        const uint32_t w = R.w[s];
-        return pairs_to_half8(nib_pair(w, 0) | MAGIC, nib_pair(w, 1) | MAGIC, nib_pair(w, 2) | MAGIC,
-                              nib_pair(w, 3) | MAGIC, (_Float16)1032.0f);
+    static __device__ __forceinline__ void load_hdr(const DevW &W, int Kc, int G, int c, int lane, Hdr &H) {
+        const float4 v = *(const float4 *)(W.h2 + hdr(G, Kc, c, lane) * 4);
+        H.d[0] = v.x; H.d[1] = v.y; H.d[2] = v.z; H.d[3] = v.w;
     }
-    static __device__ __forceinline__ void scale(const Raw &R, int s, int, float &sc, float &mn) { sc = R.d[s]; mn = 0.0f; }
+    static __device__ __forceinline__ void hdr_lds(const uint8_t *, const uint8_t *h2b, int, int lane, Hdr &H) {
+        const float4 v = *(const float4 *)(h2b + (lane & 31) * 16);
+        H.d[0] = v.x; H.d[1] = v.y; H.d[2] = v.z; H.d[3] = v.w;
+    }
+    static __device__ __forceinline__ void load_k(const DevW &W, int Kc, int G, int c, int s, int lane, RawK &R) {
+        load_kpart<32>(W.p0, Kc, G, c, s, lane, R.w);
+    }
+    static __device__ __forceinline__ void k_lds(const uint8_t *r0, const uint8_t *, int s, int lane, RawK &R) {
+        lds_kpart<32>(r0, s, lane, R.w);
+    }
+    static __device__ __forceinline__ half8 decode(const RawK &R, int, int kh) { return dec_nib(R.w[kh], (_Float16)1032.0f); }
+    static __device__ __forceinline__ void scale(const Hdr &H, int s, int, float &sc, float &mn) { sc = H.d[s]; mn = 0.0f; }
+};
+
+// Q8_0 / Q4_0: header unit = the chunk's four f16 block factors per column
+struct BlkHdr { uint32_t d[2]; };
+__device__ __forceinline__ void blk_scale(const BlkHdr &H, int s, float &sc, float &mn) {
+    sc = h2f((H.d[s >> 1] >> (16 * (s & 1))) & 0xffff);
+    mn = 0.0f;
+}
+
+template <> struct Fmt<QT_Q8_0> {
+    static constexpr bool SUB16 = false, MINS = false;
+    static constexpr int B0 = 64, B1 = 0, HB = 256, H2 = 0;
+    using Hdr = BlkHdr;
+    struct RawK { uint32_t w[4]; };
+    static __device__ __forceinline__ const uint8_t *hb_src(const DevW &W, int Kc, int G, int c) { return chunk_hdr(W.h, Kc, G, c, 8); }
+    static __device__ __forceinline__ const uint8_t *h2_src(const DevW &, int, int, int) { return nullptr; }
+    static __device__ __forceinline__ void load_hdr(const DevW &W, int Kc, int G, int c, int lane, Hdr &H) {
+        const uint2 hd = *(const uint2 *)(W.h + hdr(G, Kc, c, lane) * 8);
+        H.d[0] = hd.x; H.d[1] = hd.y;
+    }
+    static __device__ __forceinline__ void hdr_lds(const uint8_t *hb, const uint8_t *, int, int lane, Hdr &H) {
+        const uint2 hd = *(const uint2 *)(hb + (lane & 31) * 8);
+        H.d[0] = hd.x; H.d[1] = hd.y;
+    }
+    static __device__ __forceinline__ void load_k(const DevW &W, int Kc, int G, int c, int s, int lane, RawK &R) {
+        load_kpart<64>(W.p0, Kc, G, c, s, lane, R.w);
+    }
+    static __device__ __forceinline__ void k_lds(const uint8_t *r0, const uint8_t *, int s, int lane, RawK &R) {
+        lds_kpart<64>(r0, s, lane, R.w);
+    }
+    static __device__ __forceinline__ half8 decode(const RawK &R, int, int kh) { return dec_bytes(R.w[2 * kh], R.w[2 * kh + 1]); }
+    static __device__ __forceinline__ void scale(const Hdr &H, int s, int, float &sc, float &mn) { blk_scale(H, s, sc, mn); }
+};
+
+template <> struct Fmt<QT_Q4_0> {
+    static constexpr bool SUB16 = false, MINS = false;
+    static constexpr int B0 = 32, B1 = 0, HB = 256, H2 = 0;
+    using Hdr = BlkHdr;
+    struct RawK { uint32_t w[2]; };
+    static __device__ __forceinline__ const uint8_t *hb_src(const DevW &W, int Kc, int G, int c) { return chunk_hdr(W.h, Kc, G, c, 8); }
+    static __device__ __forceinline__ const uint8_t *h2_src(const DevW &, int, int, int) { return nullptr; }
+    static __device__ __forceinline__ void load_hdr(const DevW &W, int Kc, int G, int c, int lane, Hdr &H) {
+        const uint2 hd = *(const uint2 *)(W.h + hdr(G, Kc, c, lane) * 8);
+        H.d[0] = hd.x; H.d[1] = hd.y;
+    }
+    static __device__ __forceinline__ void hdr_lds(const uint8_t *hb, const uint8_t *, int, int lane, Hdr &H) {
+        const uint2 hd = *(const uint2 *)(hb + (lane & 31) * 8);
+        H.d[0] = hd.x; H.d[1] = hd.y;
+    }
+    static __device__ __forceinline__ void load_k(const DevW &W, int Kc, int G, int c, int s, int lane, RawK &R) {
+        load_kpart<32>(W.p0, Kc, G, c, s, lane, R.w);
+    }
+    static __device__ __forceinline__ void k_lds(const uint8_t *r0, const uint8_t *, int s, int lane, RawK &R) {
+        lds_kpart<32>(r0, s, lane, R.w);
+    }
+    static __device__ __forceinline__ half8 decode(const RawK &R, int, int kh) { return dec_nib(R.w[kh], (_Float16)1032.0f); }
+    static __device__ __forceinline__ void scale(const Hdr &H, int s, int, float &sc, float &mn) { blk_scale(H, s, sc, mn); }
 };
 
 // Q4_K / Q5_K super-block header: f16 d, f16 dmin, 12 bytes of packed 6-bit
 // scales and mins (ingot dequant.c:59-68 unpacking).
 __device__ __forceinline__ void k4_scale_min(const uint32_t (&hd)[4], int j, float &sc, float &mn) {
     const float d = h2f(hd[0] & 0xffff), dmin = h2f(hd[0] >> 16);
-    auto byte = [&](int i) -> uint32_t { return (hd[1 + i / 4] >> (8 * (i % 4))) & 0xffu; };
+    auto byte = [&](int i) -> uint32_t { return (sel4(hd, 1 + (i >> 2)) >> (8 * (i & 3))) & 0xffu; };
     uint32_t s, m;
     if (j < 4) {
         s = byte(j) & 63u;
@@ -211,133 +313,251 @@ __device__ __forceinline__ void k4_scale_min(const uint32_t (&hd)[4], int j, flo
     mn = dmin * (float)m;
 }
 
+// the chunk's four sub-block factors and mins, decoded once per chunk
+struct K4Hdr { float sc[4], mn[4]; };
+__device__ __forceinline__ void k4hdr_from(const uint8_t *p, int c, K4Hdr &H) {
+    const uint4 v = *(const uint4 *)p;
+    const uint32_t hd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int s = 0; s < 4; s++) k4_scale_min(hd, 4 * (c & 1) + s, H.sc[s], H.mn[s]);
+}
+
 template <> struct Fmt<QT_Q4_K> {
-    static constexpr int B0 = 16, B1 = 0;
     static constexpr bool SUB16 = false, MINS = true;
-    struct Raw { uint32_t w[4]; uint32_t hd[4]; int half_sb; };
-    static __device__ __forceinline__ void load(const DevW &W, int Kc, int G, int c, int lane, Raw &R) {
-        load_plane<16>(W.p0, Kc, G, c, lane, R.w);
-        const uint4 v = *(const uint4 *)(W.h + (((size_t)G * (Kc / 2) + c / 2) * 16 + (lane & 15)) * 16);
-        R.hd[0] = v.x; R.hd[1] = v.y; R.hd[2] = v.z; R.hd[3] = v.w;
-        R.half_sb = 4 * (c & 1);
+    static constexpr int B0 = 32, B1 = 0, HB = 512, H2 = 0;
+    using Hdr = K4Hdr;
+    struct RawK { uint32_t w[2]; };
+    static __device__ __forceinline__ const uint8_t *hb_src(const DevW &W, int Kc, int G, int c) { return sb_hdr(W.h, Kc, G, c, 16); }
+    static __device__ __forceinline__ const uint8_t *h2_src(const DevW &, int, int, int) { return nullptr; }
+    static __device__ __forceinline__ void load_hdr(const DevW &W, int Kc, int G, int c, int lane, Hdr &H) {
+        k4hdr_from(W.h + hdr(G, Kc / 2, c / 2, lane) * 16, c, H);
     }
-    static __device__ __forceinline__ half8 decode(const Raw &R, int s) {
-        const uint32_t w = R.w[s];
-        return pairs_to_half8(nib_pair(w, 0) | MAGIC, nib_pair(w, 1) | MAGIC, nib_pair(w, 2) | MAGIC,
-                              nib_pair(w, 3) | MAGIC, (_Float16)1024.0f);
+    static __device__ __forceinline__ void hdr_lds(const uint8_t *hb, const uint8_t *, int c, int lane, Hdr &H) {
+        k4hdr_from(hb + (lane & 31) * 16, c, H);
     }
-    static __device__ __forceinline__ void scale(const Raw &R, int s, int, float &sc, float &mn) {
-        k4_scale_min(R.hd, R.half_sb + s, sc, mn);
+    static __device__ __forceinline__ void load_k(const DevW &W, int Kc, int G, int c, int s, int lane, RawK &R) {
+        load_kpart<32>(W.p0, Kc, G, c, s, lane, R.w);
+    }
+    static __device__ __forceinline__ void k_lds(const uint8_t *r0, const uint8_t *, int s, int lane, RawK &R) {
+        lds_kpart<32>(r0, s, lane, R.w);
+    }
+    static __device__ __forceinline__ half8 decode(const RawK &R, int, int kh) { return dec_nib(R.w[kh], (_Float16)1024.0f); }
+    static __device__ __forceinline__ void scale(const Hdr &H, int s, int, float &sc, float &mn) {
+        sc = H.sc[s];
+        mn = H.mn[s];
     }
 };
 
 template <> struct Fmt<QT_Q5_K> {
-    static constexpr int B0 = 16, B1 = 4;
     static constexpr bool SUB16 = false, MINS = true;
-    struct Raw { uint32_t w[4]; uint32_t hb[1]; uint32_t hd[4]; int half_sb; };
-    static __device__ __forceinline__ void load(const DevW &W, int Kc, int G, int c, int lane, Raw &R) {
-        load_plane<16>(W.p0, Kc, G, c, lane, R.w);
-        load_plane<4>(W.p1, Kc, G, c, lane, R.hb);
-        const uint4 v = *(const uint4 *)(W.h + (((size_t)G * (Kc / 2) + c / 2) * 16 + (lane & 15)) * 16);
-        R.hd[0] = v.x; R.hd[1] = v.y; R.hd[2] = v.z; R.hd[3] = v.w;
-        R.half_sb = 4 * (c & 1);
+    static constexpr int B0 = 32, B1 = 8, HB = 512, H2 = 0;
+    using Hdr = K4Hdr;
+    struct RawK { uint32_t w[2]; uint32_t hb[1]; };
+    static __device__ __forceinline__ const uint8_t *hb_src(const DevW &W, int Kc, int G, int c) { return sb_hdr(W.h, Kc, G, c, 16); }
+    static __device__ __forceinline__ const uint8_t *h2_src(const DevW &, int, int, int) { return nullptr; }
+    static __device__ __forceinline__ void load_hdr(const DevW &W, int Kc, int G, int c, int lane, Hdr &H) {
+        k4hdr_from(W.h + hdr(G, Kc / 2, c / 2, lane) * 16, c, H);
     }
-    static __device__ __forceinline__ half8 decode(const Raw &R, int s) {
-        const uint32_t w = R.w[s], h = R.hb[0];
+    static __device__ __forceinline__ void hdr_lds(const uint8_t *hb, const uint8_t *, int c, int lane, Hdr &H) {
+        k4hdr_from(hb + (lane & 31) * 16, c, H);
+    }
+    static __device__ __forceinline__ void load_k(const DevW &W, int Kc, int G, int c, int s, int lane, RawK &R) {
+        load_kpart<32>(W.p0, Kc, G, c, s, lane, R.w);
+        load_kpart<8>(W.p1, Kc, G, c, s, lane, R.hb);
+    }
+    static __device__ __forceinline__ void k_lds(const uint8_t *r0, const uint8_t *r1, int s, int lane, RawK &R) {
+        lds_kpart<32>(r0, s, lane, R.w);
+        lds_kpart<8>(r1, s, lane, R.hb);
+    }
+    static __device__ __forceinline__ half8 decode(const RawK &R, int s, int kh) {
+        const int u = 2 * s + kh;
+        const uint32_t w = R.w[kh], h = R.hb[0];
         uint32_t p[4];
 #pragma unroll
-        for (int t = 0; t < 4; t++) p[t] = nib_pair(w, t) | (bit_pair(h, s, t) << 4) | MAGIC;
+        for (int t = 0; t < 4; t++) p[t] = nib_pair(w, t) | (bit_pair(h, u, t) << 4) | MAGIC;
         return pairs_to_half8(p[0], p[1], p[2], p[3], (_Float16)1024.0f);
     }
-    static __device__ __forceinline__ void scale(const Raw &R, int s, int, float &sc, float &mn) {
-        k4_scale_min(R.hd, R.half_sb + s, sc, mn);
+    static __device__ __forceinline__ void scale(const Hdr &H, int s, int, float &sc, float &mn) {
+        sc = H.sc[s];
+        mn = H.mn[s];
     }
 };
 
-// Q6_K: header plane = 16 int8 sub-block scales per super-block, h2 = d (f32).
+// Q6_K / Q3_K: header unit = 16 sub-block scale bytes (Q3_K: 12 packed + 4
+// pad) per column and super-block; h2 = d (f32).
+struct ScHdr { float sc[8]; };  // the chunk's eight 16-element sub-block factors
+
 template <> struct Fmt<QT_Q6_K> {
-    static constexpr int B0 = 16, B1 = 8;
     static constexpr bool SUB16 = true, MINS = false;
-    struct Raw { uint32_t w[4]; uint32_t hi[2]; uint32_t sc[4]; float d; int half_sb; };
-    static __device__ __forceinline__ void load(const DevW &W, int Kc, int G, int c, int lane, Raw &R) {
-        load_plane<16>(W.p0, Kc, G, c, lane, R.w);
-        load_plane<8>(W.p1, Kc, G, c, lane, R.hi);
-        const size_t u = ((size_t)G * (Kc / 2) + c / 2) * 16 + (lane & 15);
-        const uint4 v = *(const uint4 *)(W.h + u * 16);
-        R.sc[0] = v.x; R.sc[1] = v.y; R.sc[2] = v.z; R.sc[3] = v.w;
-        R.d = W.h2[u];
-        R.half_sb = 8 * (c & 1);
+    static constexpr int B0 = 32, B1 = 16, HB = 512, H2 = 128;
+    using Hdr = ScHdr;
+    struct RawK { uint32_t w[2]; uint32_t hi[1]; };
+    static __device__ __forceinline__ const uint8_t *hb_src(const DevW &W, int Kc, int G, int c) { return sb_hdr(W.h, Kc, G, c, 16); }
+    static __device__ __forceinline__ const uint8_t *h2_src(const DevW &W, int Kc, int G, int c) {
+        return (const uint8_t *)(W.h2 + hdr(G, Kc / 2, c / 2, 0));
     }
-    static __device__ __forceinline__ half8 decode(const Raw &R, int s) {
-        const uint32_t w = R.w[s], h = R.hi[s >> 1];
+    static __device__ __forceinline__ void from(const uint8_t *p, float d, int c, Hdr &H) {
+        const uint4 v = *(const uint4 *)p;
+        const uint32_t sc[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int j = 8 * (c & 1) + q;
+            H.sc[q] = d * (float)(int8_t)((sel4(sc, j >> 2) >> (8 * (j & 3))) & 0xffu);
+        }
+    }
+    static __device__ __forceinline__ void load_hdr(const DevW &W, int Kc, int G, int c, int lane, Hdr &H) {
+        const size_t u = hdr(G, Kc / 2, c / 2, lane);
+        from(W.h + u * 16, W.h2[u], c, H);
+    }
+    static __device__ __forceinline__ void hdr_lds(const uint8_t *hb, const uint8_t *h2b, int c, int lane, Hdr &H) {
+        from(hb + (lane & 31) * 16, ((const float *)h2b)[lane & 31], c, H);
+    }
+    static __device__ __forceinline__ void load_k(const DevW &W, int Kc, int G, int c, int s, int lane, RawK &R) {
+        load_kpart<32>(W.p0, Kc, G, c, s, lane, R.w);
+        load_kpart<16>(W.p1, Kc, G, c, s, lane, R.hi);
+    }
+    static __device__ __forceinline__ void k_lds(const uint8_t *r0, const uint8_t *r1, int s, int lane, RawK &R) {
+        lds_kpart<32>(r0, s, lane, R.w);
+        lds_kpart<16>(r1, s, lane, R.hi);
+    }
+    static __device__ __forceinline__ half8 decode(const RawK &R, int s, int kh) {
+        const int u = 2 * s + kh;
+        const uint32_t w = R.w[kh], h = R.hi[0];
         uint32_t p[4];
 #pragma unroll
-        for (int t = 0; t < 4; t++) p[t] = nib_pair(w, t) | (crumb_pair(h, s, t) << 4) | MAGIC;
+        for (int t = 0; t < 4; t++) p[t] = nib_pair(w, t) | (crumb_pair(h, u, t) << 4) | MAGIC;
         return pairs_to_half8(p[0], p[1], p[2], p[3], (_Float16)1056.0f);
     }
-    static __device__ __forceinline__ void scale(const Raw &R, int s, int hh, float &sc, float &mn) {
-        const int j = R.half_sb + 2 * s + hh;
-        const int8_t v = (int8_t)((R.sc[j >> 2] >> (8 * (j & 3))) & 0xffu);
-        sc = R.d * (float)v;
+    static __device__ __forceinline__ void scale(const Hdr &H, int s, int hh, float &sc, float &mn) {
+        sc = H.sc[2 * s + hh];
         mn = 0.0f;
     }
 };
 
-// Q3_K: header plane = the 12 packed scale bytes (+4 pad), h2 = d (f32).
 template <> struct Fmt<QT_Q3_K> {
-    static constexpr int B0 = 8, B1 = 4;
     static constexpr bool SUB16 = true, MINS = false;
-    struct Raw { uint32_t w[2]; uint32_t hb[1]; uint32_t sc[4]; float d; int half_sb; };
-    static __device__ __forceinline__ void load(const DevW &W, int Kc, int G, int c, int lane, Raw &R) {
-        load_plane<8>(W.p0, Kc, G, c, lane, R.w);
-        load_plane<4>(W.p1, Kc, G, c, lane, R.hb);
-        const size_t u = ((size_t)G * (Kc / 2) + c / 2) * 16 + (lane & 15);
-        const uint4 v = *(const uint4 *)(W.h + u * 16);
-        R.sc[0] = v.x; R.sc[1] = v.y; R.sc[2] = v.z; R.sc[3] = v.w;
-        R.d = W.h2[u];
-        R.half_sb = 8 * (c & 1);
+    static constexpr int B0 = 16, B1 = 8, HB = 512, H2 = 128;
+    using Hdr = ScHdr;
+    struct RawK { uint32_t w[1]; uint32_t hb[1]; };
+    static __device__ __forceinline__ const uint8_t *hb_src(const DevW &W, int Kc, int G, int c) { return sb_hdr(W.h, Kc, G, c, 16); }
+    static __device__ __forceinline__ const uint8_t *h2_src(const DevW &W, int Kc, int G, int c) {
+        return (const uint8_t *)(W.h2 + hdr(G, Kc / 2, c / 2, 0));
     }
-    static __device__ __forceinline__ half8 decode(const Raw &R, int s) {
-        const uint32_t w = R.w[s >> 1], h = R.hb[0];
+    static __device__ __forceinline__ void from(const uint8_t *p, float d, int c, Hdr &H) {
+        const uint4 v = *(const uint4 *)p;
+        const uint32_t sc[4] = {v.x, v.y, v.z, v.w};
+        auto byte = [&](int i) -> int { return (int)((sel4(sc, i >> 2) >> (8 * (i & 3))) & 0xffu); };
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int j = 8 * (c & 1) + q;
+            const int lo = j < 8 ? (byte(j) & 15) : (byte(j - 8) >> 4);
+            const int hi = (byte(8 + (j & 3)) >> (2 * (j >> 2))) & 3;
+            H.sc[q] = d * (float)((lo | (hi << 4)) - 32);
+        }
+    }
+    static __device__ __forceinline__ void load_hdr(const DevW &W, int Kc, int G, int c, int lane, Hdr &H) {
+        const size_t u = hdr(G, Kc / 2, c / 2, lane);
+        from(W.h + u * 16, W.h2[u], c, H);
+    }
+    static __device__ __forceinline__ void hdr_lds(const uint8_t *hb, const uint8_t *h2b, int c, int lane, Hdr &H) {
+        from(hb + (lane & 31) * 16, ((const float *)h2b)[lane & 31], c, H);
+    }
+    static __device__ __forceinline__ void load_k(const DevW &W, int Kc, int G, int c, int s, int lane, RawK &R) {
+        load_kpart<16>(W.p0, Kc, G, c, s, lane, R.w);
+        load_kpart<8>(W.p1, Kc, G, c, s, lane, R.hb);
+    }
+    static __device__ __forceinline__ void k_lds(const uint8_t *r0, const uint8_t *r1, int s, int lane, RawK &R) {
+        lds_kpart<16>(r0, s, lane, R.w);
+        lds_kpart<8>(r1, s, lane, R.hb);
+    }
+    static __device__ __forceinline__ half8 decode(const RawK &R, int s, int kh) {
+        const int u = 2 * s + kh;
+        const uint32_t w = R.w[0], h = R.hb[0];
         uint32_t p[4];
 #pragma unroll
-        for (int t = 0; t < 4; t++) p[t] = crumb_pair(w, s, t) | (bit_pair(h, s, t) << 2) | MAGIC;
+        for (int t = 0; t < 4; t++) p[t] = crumb_pair(w, u, t) | (bit_pair(h, u, t) << 2) | MAGIC;
         return pairs_to_half8(p[0], p[1], p[2], p[3], (_Float16)1028.0f);
     }
-    static __device__ __forceinline__ void scale(const Raw &R, int s, int hh, float &sc, float &mn) {
-        const int j = R.half_sb + 2 * s + hh;
-        auto byte = [&](int i) -> int { return (int)((R.sc[i >> 2] >> (8 * (i & 3))) & 0xffu); };
-        const int lo = j < 8 ? (byte(j) & 15) : (byte(j - 8) >> 4);
-        const int hi = (byte(8 + (j & 3)) >> (2 * (j >> 2))) & 3;
-        sc = R.d * (float)((lo | (hi << 4)) - 32);
+    static __device__ __forceinline__ void scale(const Hdr &H, int s, int hh, float &sc, float &mn) {
+        sc = H.sc[2 * s + hh];
         mn = 0.0f;
     }
 };
 
-// Q2_K: header plane = 16 scale|min bytes, h2 = (d, dmin) (f32 pair).
+// Q2_K: header unit = 16 scale|min bytes per column, h2 = (d, dmin) (f32 pair).
+struct Q2Hdr { float sc[8], mn[8]; };  // the chunk's eight sub-block factors and mins
+
 template <> struct Fmt<QT_Q2_K> {
-    static constexpr int B0 = 8, B1 = 0;
     static constexpr bool SUB16 = true, MINS = true;
-    struct Raw { uint32_t w[2]; uint32_t sc[4]; float d, dmin; int half_sb; };
-    static __device__ __forceinline__ void load(const DevW &W, int Kc, int G, int c, int lane, Raw &R) {
-        load_plane<8>(W.p0, Kc, G, c, lane, R.w);
-        const size_t u = ((size_t)G * (Kc / 2) + c / 2) * 16 + (lane & 15);
-        const uint4 v = *(const uint4 *)(W.h + u * 16);
-        R.sc[0] = v.x; R.sc[1] = v.y; R.sc[2] = v.z; R.sc[3] = v.w;
-        const float2 dd = *(const float2 *)(W.h2 + 2 * u);
-        R.d = dd.x; R.dmin = dd.y;
-        R.half_sb = 8 * (c & 1);
+    static constexpr int B0 = 16, B1 = 0, HB = 512, H2 = 256;
+    using Hdr = Q2Hdr;
+    struct RawK { uint32_t w[1]; };
+    static __device__ __forceinline__ const uint8_t *hb_src(const DevW &W, int Kc, int G, int c) { return sb_hdr(W.h, Kc, G, c, 16); }
+    static __device__ __forceinline__ const uint8_t *h2_src(const DevW &W, int Kc, int G, int c) {
+        return (const uint8_t *)(W.h2 + 2 * hdr(G, Kc / 2, c / 2, 0));
     }
-    static __device__ __forceinline__ half8 decode(const Raw &R, int s) {
-        const uint32_t w = R.w[s >> 1];
-        return pairs_to_half8(crumb_pair(w, s, 0) | MAGIC, crumb_pair(w, s, 1) | MAGIC,
-                              crumb_pair(w, s, 2) | MAGIC, crumb_pair(w, s, 3) | MAGIC,
+    static __device__ __forceinline__ void from(const uint8_t *p, float2 dd, int c, Hdr &H) {
+        const uint4 v = *(const uint4 *)p;
+        const uint32_t sc[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int j = 8 * (c & 1) + q;
+            const uint32_t b = (sel4(sc, j >> 2) >> (8 * (j & 3))) & 0xffu;
+            H.sc[q] = dd.x * (float)(b & 15u);
+            H.mn[q] = dd.y * (float)(b >> 4);
+        }
+    }
+    static __device__ __forceinline__ void load_hdr(const DevW &W, int Kc, int G, int c, int lane, Hdr &H) {
+        const size_t u = hdr(G, Kc / 2, c / 2, lane);
+        from(W.h + u * 16, *(const float2 *)(W.h2 + 2 * u), c, H);
+    }
+    static __device__ __forceinline__ void hdr_lds(const uint8_t *hb, const uint8_t *h2b, int c, int lane, Hdr &H) {
+        from(hb + (lane & 31) * 16, *(const float2 *)(h2b + (lane & 31) * 8), c, H);
+    }
+    static __device__ __forceinline__ void load_k(const DevW &W, int Kc, int G, int c, int s, int lane, RawK &R) {
+        load_kpart<16>(W.p0, Kc, G, c, s, lane, R.w);
+    }
+    static __device__ __forceinline__ void k_lds(const uint8_t *r0, const uint8_t *, int s, int lane, RawK &R) {
+        lds_kpart<16>(r0, s, lane, R.w);
+    }
+    static __device__ __forceinline__ half8 decode(const RawK &R, int s, int kh) {
+        const int u = 2 * s + kh;
+        const uint32_t w = R.w[0];
+        return pairs_to_half8(crumb_pair(w, u, 0) | MAGIC, crumb_pair(w, u, 1) | MAGIC,
+                              crumb_pair(w, u, 2) | MAGIC, crumb_pair(w, u, 3) | MAGIC,
                               (_Float16)1024.0f);
     }
-    static __device__ __forceinline__ void scale(const Raw &R, int s, int hh, float &sc, float &mn) {
-        const int j = R.half_sb + 2 * s + hh;
-        const uint32_t b = (R.sc[j >> 2] >> (8 * (j & 3))) & 0xffu;
-        sc = R.d * (float)(b & 15u);
-        mn = R.dmin * (float)(b >> 4);
+    static __device__ __forceinline__ void scale(const Hdr &H, int s, int hh, float &sc, float &mn) {
+        sc = H.sc[2 * s + hh];
+        mn = H.mn[2 * s + hh];
+    }
+};
+
+// F32: (wh, wl) f16 fragments of w * 2^shw_n; the plane's 16-byte part 2u is
+// wh of half-step u and part 2u+1 its wl; h2 = shw_n per row.
+template <> struct Fmt<QT_F32> {
+    static constexpr bool SUB16 = false, MINS = false;
+    static constexpr int B0 = 256, B1 = 0, HB = 0, H2 = 0;
+    struct Hdr {};
+    struct RawK { half8 h[2], l[2]; };
+    static __device__ __forceinline__ const uint8_t *hb_src(const DevW &, int, int, int) { return nullptr; }
+    static __device__ __forceinline__ const uint8_t *h2_src(const DevW &, int, int, int) { return nullptr; }
+    static __device__ __forceinline__ void load_hdr(const DevW &, int, int, int, int, Hdr &) {}
+    static __device__ __forceinline__ void hdr_lds(const uint8_t *, const uint8_t *, int, int, Hdr &) {}
+    static __device__ __forceinline__ void load_k(const DevW &W, int Kc, int G, int c, int s, int lane, RawK &R) {
+        const size_t base = ((size_t)G * Kc + c) * 16 + 4 * s;
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++) {
+            R.h[kh] = *(const half8 *)(W.p0 + ((base + 2 * kh) * 64 + lane) * 16);
+            R.l[kh] = *(const half8 *)(W.p0 + ((base + 2 * kh + 1) * 64 + lane) * 16);
+        }
+    }
+    static __device__ __forceinline__ void k_lds(const uint8_t *r0, const uint8_t *, int s, int lane, RawK &R) {
+        // staged half = parts 8h .. 8h+7; kstep s is local kstep s & 1
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++) {
+            R.h[kh] = *(const half8 *)(r0 + ((4 * (s & 1) + 2 * kh) * 64 + lane) * 16);
+            R.l[kh] = *(const half8 *)(r0 + ((4 * (s & 1) + 2 * kh + 1) * 64 + lane) * 16);
+        }
     }
 };

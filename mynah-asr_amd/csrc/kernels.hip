@@ -4,21 +4,35 @@
 // and chunk c:
 //   * x_m's chunk is scaled by 2^sh (sh puts its largest magnitude in
 //     [2^14, 2^15)) and split into two f16 terms xh + xl (22 significant bits);
-//   * weight quants are small integers, exact in f16; per kstep (32 of K) one
-//     MFMA pair gives t = sum(xh*q) + sum(xl*q) in f32 and the sub-block
-//     factor is applied in f32: a = fma(sc, t, a) [; a = fma(-mn, sum_x, a)
-//     for the affine formats], a starting at zero in every chunk;
-//   * total = total + a * 2^-sh, chunks in order from zero. y = total.
+//   * weight quants are small integers, exact in f16; per kstep (32 of K) four
+//     v_mfma_f32_32x32x16_f16 give t = sum(xh*q) + sum(xl*q) in f32 and the
+//     sub-block factor is applied in f32: a = fma(sc, t, a) [; a = fma(-mn,
+//     sum_x, a) for the affine formats], a starting at zero in every chunk;
+//   * total = fma(2^-sh, a, total), chunks in order from zero. y = total.
 // Every step depends only on row m's own data and on K — never on M, on the
 // tile the row lands in, or on the kernel (GEMM or GEMV) that runs it — so
 // each row's bits are the same whatever the batch size.
+//
+// The 32x32x16 MFMA is used throughout: on gfx950 it issues twice the work of
+// the 16x16x32 shape per cycle (measured 2.04 vs 1.19 PFLOP/s f16).
 #include "fmt.h"
 
 #define KSTEPS 4  // ksteps per chunk
+#define HSTEPS 8  // half-steps per chunk
 
-__device__ __forceinline__ f4 mfma16(half8 a, half8 b, f4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f16v mfma32(half8 a, half8 b, f16v c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
+
+__device__ __forceinline__ f16v zero16() {
+    f16v z;
+#pragma unroll
+    for (int e = 0; e < 16; e++) z[e] = 0.0f;
+    return z;
+}
+
+// D-layout row of accumulator element e for lane half hh
+__device__ __forceinline__ int drow(int e, int hh) { return 8 * (e >> 2) + 4 * hh + (e & 3); }
 
 __device__ __forceinline__ float silu_f(float v) {
     // the reference's stable sigmoid (src/qmat.h:31-35)
@@ -28,248 +42,153 @@ __device__ __forceinline__ float silu_f(float v) {
 }
 
 // ---------------------------------------------------------------------------
-// Activation split of one chunk, in the A-operand layout: lane (r = l&15,
-// g = l>>4) holds elements 8g..8g+7 of each kstep for row m. The chunk's
-// largest magnitude is shared by the four lanes of a row through two xor
-// shuffles (every lane of the wave must call this).
+// Activation split of one chunk, in the A-operand layout: lane (r = l&31,
+// hh = l>>5) holds elements 16u + 8hh .. +7 of half-step u for row m. The
+// chunk's largest magnitude is shared by the two lanes of a row through one
+// xor shuffle (every lane of the wave must call this).
 struct XChunk {
-    half8 h[KSTEPS], l[KSTEPS];
-    float s8[KSTEPS];  // sum of the 8 scaled values, in order
-    int sh;
+    half8 h[HSTEPS], l[HSTEPS];
+    float s8[HSTEPS];  // sum of the lane's 8 scaled values of half-step u, in order
+    float p;           // 2^-sh: the chunk's fold factor for this row
 };
 
 __device__ __forceinline__ void split_chunk(const float *__restrict__ x, int M, int K, int m, int c,
-                                            int g, int vec, XChunk &o) {
-    float v[KSTEPS][8];
+                                            int hh, int vec, XChunk &o) {
+    float v[HSTEPS][8];
     const bool live = m < M;
     const float *row = x + (size_t)(live ? m : 0) * K;
 #pragma unroll
-    for (int s = 0; s < KSTEPS; s++) {
-        const int k0 = 128 * c + 32 * s + 8 * g;
+    for (int u = 0; u < HSTEPS; u++) {
+        const int k0 = 128 * c + 16 * u + 8 * hh;
         if (live && vec && k0 + 8 <= K) {
             const float4 a = *(const float4 *)(row + k0), b = *(const float4 *)(row + k0 + 4);
-            v[s][0] = a.x; v[s][1] = a.y; v[s][2] = a.z; v[s][3] = a.w;
-            v[s][4] = b.x; v[s][5] = b.y; v[s][6] = b.z; v[s][7] = b.w;
+            v[u][0] = a.x; v[u][1] = a.y; v[u][2] = a.z; v[u][3] = a.w;
+            v[u][4] = b.x; v[u][5] = b.y; v[u][6] = b.z; v[u][7] = b.w;
         } else {
 #pragma unroll
-            for (int j = 0; j < 8; j++) v[s][j] = (live && k0 + j < K) ? row[k0 + j] : 0.0f;
+            for (int j = 0; j < 8; j++) v[u][j] = (live && k0 + j < K) ? row[k0 + j] : 0.0f;
         }
     }
     float amax = 0.0f;
 #pragma unroll
-    for (int s = 0; s < KSTEPS; s++)
+    for (int u = 0; u < HSTEPS; u++)
 #pragma unroll
-        for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[s][j]));
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
+        for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[u][j]));
     amax = fmaxf(amax, __shfl_xor(amax, 32));
     int e = 0;
     if (amax > 0.0f) (void)frexpf(amax, &e);
-    o.sh = amax > 0.0f ? 15 - e : 0;
+    const int sh = amax > 0.0f ? 15 - e : 0;
+    o.p = ldexpf(1.0f, -sh);
 #pragma unroll
-    for (int s = 0; s < KSTEPS; s++) {
+    for (int u = 0; u < HSTEPS; u++) {
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const float xs = ldexpf(v[s][j], o.sh);
+            const float xs = ldexpf(v[u][j], sh);
             const _Float16 h = (_Float16)xs;
-            o.h[s][j] = h;
-            o.l[s][j] = (_Float16)(xs - (float)h);
+            o.h[u][j] = h;
+            o.l[u][j] = (_Float16)(xs - (float)h);
             acc += xs;
         }
-        o.s8[s] = acc;
+        o.s8[u] = acc;
     }
 }
 
 // ---------------------------------------------------------------------------
-// Sources of the A operand: an object with h(i, c, s, lane), l(...) (the two
-// f16 terms of kstep s for row group i) and xsum(i, c, s, half, lane) (the
-// sub-block sums of rows 4g..4g+3, for the affine formats).
-// Prepared buffers read straight from global memory (no LDS staging):
-// xp [G][chunk][kstep][term][64][16 B], xs16 [G][K/16][16 rows].
-template <int WM>
-struct AFromPrep {
-    const uint8_t *xp;
-    const float *xs16;
-    int Kc, Kp16;
-    const int *gm;
-    __device__ __forceinline__ half8 h(int i, int c, int s, int lane) const {
-        return *(const half8 *)(xp + (((((size_t)gm[i] * Kc + c) * KSTEPS + s) * 2 + 0) * 64 + lane) * 16);
-    }
-    __device__ __forceinline__ half8 l(int i, int c, int s, int lane) const {
-        return *(const half8 *)(xp + (((((size_t)gm[i] * Kc + c) * KSTEPS + s) * 2 + 1) * 64 + lane) * 16);
-    }
-    __device__ __forceinline__ f4 xsum(int i, int c, int s, int hh, int lane) const {
-        return *(const f4 *)(xs16 + (((size_t)gm[i] * Kp16 + 8 * c + 2 * s + hh) * 16 + 4 * (lane >> 4)));
-    }
-};
-
-// Registers (small M): one row group, split in the calling wave.
-struct AFromRegs {
-    const XChunk *xc;
-    const f4 *xs;  // [KSTEPS][2], C-layout rows
-    __device__ __forceinline__ half8 h(int, int, int s, int) const { return xc->h[s]; }
-    __device__ __forceinline__ half8 l(int, int, int s, int) const { return xc->l[s]; }
-    __device__ __forceinline__ f4 xsum(int, int, int s, int hh, int) const { return xs[2 * s + hh]; }
-};
-
-// Raw weight registers of one chunk for WN column groups (none for F32,
-// whose fragments are read per kstep).
-template <int QT, int WN> struct BRaw { typename Fmt<QT>::Raw r[WN]; };
-template <int WN> struct BRaw<QT_F32, WN> {};
+// Weight fragments of WN column groups: per-chunk headers and per-kstep words.
+template <int QT, int WN> struct BH { typename Fmt<QT>::Hdr h[WN]; };
+template <int QT, int WN> struct BK { typename Fmt<QT>::RawK r[WN]; };
 
 template <int QT, int WN>
-__device__ __forceinline__ void load_b(const DevW &W, int Kc, const int (&gn)[WN], int c, int lane,
-                                       BRaw<QT, WN> &b) {
-    if constexpr (QT != QT_F32) {
+__device__ __forceinline__ void load_bh(const DevW &W, int Kc, const int (&gn)[WN], int c, int lane, BH<QT, WN> &b) {
 #pragma unroll
-        for (int j = 0; j < WN; j++) Fmt<QT>::load(W, Kc, gn[j], c, lane, b.r[j]);
-    }
+    for (int j = 0; j < WN; j++) Fmt<QT>::load_hdr(W, Kc, gn[j], c, lane, b.h[j]);
+}
+template <int QT, int WN>
+__device__ __forceinline__ void load_bk(const DevW &W, int Kc, const int (&gn)[WN], int c, int s, int lane,
+                                        BK<QT, WN> &b) {
+#pragma unroll
+    for (int j = 0; j < WN; j++) Fmt<QT>::load_k(W, Kc, gn[j], c, s, lane, b.r[j]);
 }
 
-// The exact product kstep by kstep. kstep_issue loads the A fragments,
-// decodes the weights and issues the MFMAs of one kstep into a pending
-// record; kstep_apply folds a pending record into the chunk accumulator
-// (acc = fma(sc, t, acc) [- mn * sum_x]). Callers issue kstep s+1 before
-// applying kstep s, so the VALU epilogue of one kstep runs while the matrix
-// core works on the next; the float operations each output sees, and their
-// order, are the same in every caller.
-template <int QT, int WM, int WN> struct KPend {
-    static constexpr bool SUB = QT != QT_F32 && Fmt<QT == QT_F32 ? QT_Q8_0 : QT>::SUB16;
-    static constexpr bool MIN = QT != QT_F32 && Fmt<QT == QT_F32 ? QT_Q8_0 : QT>::MINS;
-    static constexpr int NH = SUB ? 2 : 1;
-    f4 t[WM][WN][NH];
-    float sc[WN][NH], mn[WN][NH];
-    f4 xs[WM][2];
+// A fragments of one kstep for WM row groups: the two f16 terms of its two
+// half-steps, and (affine formats) the 16-element sub-block sums of the
+// lane's 16 D-layout rows.
+template <int WM> struct AK {
+    half8 h[WM][2], l[WM][2];
+    f16v xs[WM][2];
 };
 
-template <int QT, int WM, int WN, class A>
-__device__ __forceinline__ void kstep_issue(const DevW &W, int Kc, const A &src, const BRaw<QT, WN> &braw,
-                                            const int (&gn)[WN], int c, int s, int lane,
-                                            KPend<QT, WM, WN> &p, f4 (&acc)[WM][WN]) {
-    half8 ah[WM], al[WM];
-#pragma unroll
-    for (int i = 0; i < WM; i++) {
-        ah[i] = src.h(i, c, s, lane);
-        al[i] = src.l(i, c, s, lane);
-    }
+// The exact product of one kstep, folded into the chunk accumulator
+// (acc = fma(sc, t, acc) [- mn * sum_x]). The float operations each output
+// sees, and their order, are the same in every caller.
+template <int QT, int WM, int WN>
+__device__ __forceinline__ void kstep(const AK<WM> &a, const BK<QT, WN> &b, const BH<QT, WN> &hd, int s,
+                                      f16v (&acc)[WM][WN]) {
+    using F = Fmt<QT>;
     if constexpr (QT == QT_F32) {
         // f32 weights: resident as (wh, wl) f16 pairs scaled per row by
-        // 2^shw_n; t += xh*wh + xh*wl + xl*wh straight into the chunk
+        // 2^shw_n; acc += xh*wh + xh*wl + xl*wh straight into the chunk
         // accumulator (no per-kstep factor)
-        half8 bh[WN], bl[WN];
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+            for (int j = 0; j < WN; j++)
+#pragma unroll
+                for (int i = 0; i < WM; i++) {
+                    acc[i][j] = mfma32(a.h[i][kh], b.r[j].h[kh], acc[i][j]);
+                    acc[i][j] = mfma32(a.h[i][kh], b.r[j].l[kh], acc[i][j]);
+                    acc[i][j] = mfma32(a.l[i][kh], b.r[j].h[kh], acc[i][j]);
+                }
+    } else if constexpr (!F::SUB16) {
 #pragma unroll
         for (int j = 0; j < WN; j++) {
-            const size_t base = ((size_t)gn[j] * Kc + c) * 8;
-            bh[j] = *(const half8 *)(W.p0 + ((base + 2 * s) * 64 + lane) * 16);
-            bl[j] = *(const half8 *)(W.p0 + ((base + 2 * s + 1) * 64 + lane) * 16);
-        }
-#pragma unroll
-        for (int i = 0; i < WM; i++)
-#pragma unroll
-            for (int j = 0; j < WN; j++) {
-                acc[i][j] = mfma16(ah[i], bh[j], acc[i][j]);
-                acc[i][j] = mfma16(ah[i], bl[j], acc[i][j]);
-                acc[i][j] = mfma16(al[i], bh[j], acc[i][j]);
-            }
-    } else {
-        using F = Fmt<QT>;
-        const int g = lane >> 4;
-        if constexpr (F::MINS) {
+            const half8 b0 = F::decode(b.r[j], s, 0), b1 = F::decode(b.r[j], s, 1);
+            float sc, mn;
+            F::scale(hd.h[j], s, 0, sc, mn);
 #pragma unroll
             for (int i = 0; i < WM; i++) {
-                p.xs[i][0] = src.xsum(i, c, s, 0, lane);
-                p.xs[i][1] = src.xsum(i, c, s, 1, lane);
+                f16v t = mfma32(a.h[i][0], b0, zero16());
+                t = mfma32(a.h[i][1], b1, t);
+                t = mfma32(a.l[i][0], b0, t);
+                t = mfma32(a.l[i][1], b1, t);
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[i][j][e] = __builtin_fmaf(sc, t[e], acc[i][j][e]);
+                if constexpr (F::MINS) {
+#pragma unroll
+                    for (int e = 0; e < 16; e++)
+                        acc[i][j][e] = __builtin_fmaf(-mn, a.xs[i][0][e] + a.xs[i][1][e], acc[i][j][e]);
+                }
             }
         }
+    } else {
 #pragma unroll
         for (int j = 0; j < WN; j++) {
-            const half8 b = F::decode(braw.r[j], s);
-            if constexpr (!F::SUB16) {
-                F::scale(braw.r[j], s, 0, p.sc[j][0], p.mn[j][0]);
+            const half8 b0 = F::decode(b.r[j], s, 0), b1 = F::decode(b.r[j], s, 1);
+            float sc0, mn0, sc1, mn1;
+            F::scale(hd.h[j], s, 0, sc0, mn0);
+            F::scale(hd.h[j], s, 1, sc1, mn1);
 #pragma unroll
-                for (int i = 0; i < WM; i++) {
-                    f4 t = mfma16(ah[i], b, f4{0.f, 0.f, 0.f, 0.f});
-                    p.t[i][j][0] = mfma16(al[i], b, t);
+            for (int i = 0; i < WM; i++) {
+                f16v t0 = mfma32(a.h[i][0], b0, zero16());
+                t0 = mfma32(a.l[i][0], b0, t0);
+                f16v t1 = mfma32(a.h[i][1], b1, zero16());
+                t1 = mfma32(a.l[i][1], b1, t1);
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    acc[i][j][e] = __builtin_fmaf(sc0, t0[e], acc[i][j][e]);
+                    acc[i][j][e] = __builtin_fmaf(sc1, t1[e], acc[i][j][e]);
                 }
-            } else {
-                const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-                const half8 b0 = g < 2 ? b : z, b1 = g < 2 ? z : b;
-                F::scale(braw.r[j], s, 0, p.sc[j][0], p.mn[j][0]);
-                F::scale(braw.r[j], s, 1, p.sc[j][1], p.mn[j][1]);
+                if constexpr (F::MINS) {
 #pragma unroll
-                for (int i = 0; i < WM; i++) {
-                    f4 t0 = mfma16(ah[i], b0, f4{0.f, 0.f, 0.f, 0.f});
-                    p.t[i][j][0] = mfma16(al[i], b0, t0);
-                    f4 t1 = mfma16(ah[i], b1, f4{0.f, 0.f, 0.f, 0.f});
-                    p.t[i][j][1] = mfma16(al[i], b1, t1);
+                    for (int e = 0; e < 16; e++) {
+                        acc[i][j][e] = __builtin_fmaf(-mn0, a.xs[i][0][e], acc[i][j][e]);
+                        acc[i][j][e] = __builtin_fmaf(-mn1, a.xs[i][1][e], acc[i][j][e]);
+                    }
                 }
             }
         }
     }
-}
-
-template <int QT, int WM, int WN>
-__device__ __forceinline__ void kstep_apply(const KPend<QT, WM, WN> &p, f4 (&acc)[WM][WN]) {
-    if constexpr (QT != QT_F32) {
-        using KP = KPend<QT, WM, WN>;
-#pragma unroll
-        for (int i = 0; i < WM; i++)
-#pragma unroll
-            for (int j = 0; j < WN; j++) {
-                if constexpr (!KP::SUB) {
-#pragma unroll
-                    for (int r = 0; r < 4; r++) acc[i][j][r] = __builtin_fmaf(p.sc[j][0], p.t[i][j][0][r], acc[i][j][r]);
-                    if constexpr (KP::MIN) {
-                        const f4 xs = p.xs[i][0] + p.xs[i][1];
-#pragma unroll
-                        for (int r = 0; r < 4; r++) acc[i][j][r] = __builtin_fmaf(-p.mn[j][0], xs[r], acc[i][j][r]);
-                    }
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        acc[i][j][r] = __builtin_fmaf(p.sc[j][0], p.t[i][j][0][r], acc[i][j][r]);
-                        acc[i][j][r] = __builtin_fmaf(p.sc[j][1], p.t[i][j][1][r], acc[i][j][r]);
-                    }
-                    if constexpr (KP::MIN) {
-#pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            acc[i][j][r] = __builtin_fmaf(-p.mn[j][0], p.xs[i][0][r], acc[i][j][r]);
-                            acc[i][j][r] = __builtin_fmaf(-p.mn[j][1], p.xs[i][1][r], acc[i][j][r]);
-                        }
-                    }
-                }
-            }
-    }
-}
-
-template <int QT, int WM, int WN>
-constexpr int kstep_mfmas() {
-    return QT == QT_F32 ? 3 * WM * WN : (KPend<QT, WM, WN>::SUB ? 4 : 2) * WM * WN;
-}
-
-// A whole chunk from one A source. PIPE: issue(s+1) before apply(s) (more
-// registers, more overlap); otherwise each kstep is applied right away.
-template <int QT, int WM, int WN, class A, bool PIPE = true>
-__device__ __forceinline__ void chunk_all(const DevW &W, int Kc, const A &src, const BRaw<QT, WN> &braw,
-                                          const int (&gn)[WN], int c, int lane, f4 (&acc)[WM][WN]) {
-    if constexpr (!PIPE) {
-#pragma unroll
-        for (int s = 0; s < KSTEPS; s++) {
-            KPend<QT, WM, WN> p;
-            kstep_issue<QT, WM, WN>(W, Kc, src, braw, gn, c, s, lane, p, acc);
-            kstep_apply<QT, WM, WN>(p, acc);
-        }
-        return;
-    }
-    KPend<QT, WM, WN> p0, p1;
-    kstep_issue<QT, WM, WN>(W, Kc, src, braw, gn, c, 0, lane, p0, acc);
-    kstep_issue<QT, WM, WN>(W, Kc, src, braw, gn, c, 1, lane, p1, acc);
-    kstep_apply<QT, WM, WN>(p0, acc);
-    kstep_issue<QT, WM, WN>(W, Kc, src, braw, gn, c, 2, lane, p0, acc);
-    kstep_apply<QT, WM, WN>(p1, acc);
-    kstep_issue<QT, WM, WN>(W, Kc, src, braw, gn, c, 3, lane, p1, acc);
-    kstep_apply<QT, WM, WN>(p0, acc);
-    kstep_apply<QT, WM, WN>(p1, acc);
 }
 
 // the per-row weight shift of the f32 format (0 for the quantized ones)
@@ -279,20 +198,104 @@ __device__ __forceinline__ int wshift(const DevW &W, int n) {
     return 0;
 }
 
+__device__ __forceinline__ f16v load_rows16(const float *b) {
+    // the lane's 16 D-layout rows from a [32]-row float vector (b at row 4*hh)
+    f16v r;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float4 v = *(const float4 *)(b + 8 * q);
+        r[4 * q + 0] = v.x; r[4 * q + 1] = v.y; r[4 * q + 2] = v.z; r[4 * q + 3] = v.w;
+    }
+    return r;
+}
+
 // ---------------------------------------------------------------------------
-// Large-M GEMM: 4 waves in 2x2, each a WM x WN block of 16x16 tiles; every
-// wave reads its A and B fragments straight from global memory in the
-// MFMA-native layouts (one contiguous 1 KiB block per wave-wide 16-byte load),
-// and L1/L2 serve the sharing between the waves of a workgroup. Staging A
-// through LDS was measured slower on gfx950 for these tiles: the kernel is
-// bound by the VALU work of the per-kstep f32 epilogue, and the extra LDS
-// traffic, barriers and prefetch registers only add to it.
-// grid = tilesM * tilesN workgroups, tiles of (32*WM) x (32*WN).
-template <int QT, int WM, int WN, bool PIPE>
-__global__ __launch_bounds__(256) void k_gemm_direct(DevW W, const uint8_t *__restrict__ xp,
-                                                     const float *__restrict__ xs16,
-                                                     const int *__restrict__ xsh, float *__restrict__ y,
-                                                     int M, int act, int tilesM, int tilesN) {
+// Global -> LDS copies (global_load_lds: no VGPRs; the LDS destination is
+// wave-uniform, lane l writes bytes [l*size, (l+1)*size) of each piece).
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int BYTES>
+__device__ __forceinline__ void dma(const uint8_t *src, uint8_t *dst, int lane) {
+    if constexpr (BYTES == 0) {
+        return;
+    } else if constexpr (BYTES % 1024 == 0) {
+#pragma unroll
+        for (int k = 0; k < BYTES / 1024; k++)
+            __builtin_amdgcn_global_load_lds((const void *)(src + k * 1024 + lane * 16), (lds_void *)(dst + k * 1024),
+                                             16, 0, 0);
+    } else if constexpr (BYTES % 256 == 0) {
+#pragma unroll
+        for (int k = 0; k < BYTES / 256; k++)
+            __builtin_amdgcn_global_load_lds((const void *)(src + k * 256 + lane * 4), (lds_void *)(dst + k * 256), 4,
+                                             0, 0);
+    } else {
+        static_assert(BYTES == 128, "staged region size");
+        if (lane < 32) __builtin_amdgcn_global_load_lds((const void *)(src + lane * 4), (lds_void *)dst, 4, 0, 0);
+    }
+}
+// number of copy instructions dma<BYTES> issues (each counts once in vmcnt)
+template <int BYTES> constexpr int dma_n() {
+    return BYTES == 0 ? 0 : (BYTES % 1024 == 0 ? BYTES / 1024 : (BYTES % 256 == 0 ? BYTES / 256 : 1));
+}
+
+// the lane's 16 D-layout rows from a staged [32]-row float vector
+__device__ __forceinline__ f16v lds_rows16(const uint8_t *v, int hh) {
+    f16v r;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float4 x = *(const float4 *)(v + (8 * q + 4 * hh) * 4);
+        r[4 * q + 0] = x.x; r[4 * q + 1] = x.y; r[4 * q + 2] = x.z; r[4 * q + 3] = x.w;
+    }
+    return r;
+}
+
+template <int N> __device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// LDS stage of k_gemm: half a chunk (2 ksteps) of everything the workgroup
+// reads, for its 2 row groups and 4 column groups.
+template <int QT> struct StageLayout {
+    using F = Fmt<QT>;
+    static constexpr int A = 0;                                   // [2 rg][4 u][2 term][1 KiB]
+    static constexpr int B0S = Stage<F::B0>::BYTES, B1S = Stage<F::B1>::BYTES;
+    static constexpr int P0 = A + 2 * 8192;                       // [4 cg][B0S]
+    static constexpr int P1 = P0 + 4 * B0S;                       // [4 cg][B1S]
+    static constexpr int HB = P1 + 4 * B1S;                       // [4 cg][F::HB]
+    static constexpr int H2 = HB + 4 * F::HB;                     // [4 cg][F::H2]
+    static constexpr int PF = H2 + 4 * F::H2;                     // [2 rg][32 floats]
+    static constexpr int XS = PF + 2 * 128;                       // [2 rg][4 sub-blocks][32 floats]
+    static constexpr int BYTES = XS + (F::MINS ? 2 * 512 : 0);
+};
+
+// ---------------------------------------------------------------------------
+// Large-M GEMM. Workgroup = 4 waves side by side over N, tile 64 x 128: row
+// groups G0, G0+1 and column groups GC0..GC0+3; wave w computes both row
+// groups against column group GC0+w (2 x 1 tiles of 32x32).
+// Everything the MFMAs read goes through LDS in half-chunk stages,
+// double-buffered: the stage for ksteps k+2, k+3 lands while ksteps k, k+1
+// compute. The copies are global_load_lds (no VGPRs hold prefetched data),
+// shared out so that wave w brings its own column group's plane bytes and
+// headers and a quarter of the activation pieces. ~50 KiB of LDS and <= 168
+// VGPRs per wave let three workgroups share a CU: their waves fill each
+// other's stalls and overlap one's VALU epilogue with another's MFMAs.
+// grid = tilesM * tilesN workgroups.
+// workgroups per CU the register budget is sized for: the K-quants (affine
+// sums, sub-block factors) and the f32 pairs need more registers per wave
+template <int QT> constexpr int gemm_occ() {
+    return (QT == QT_F32 || Fmt<QT>::MINS || Fmt<QT>::SUB16) ? 2 : 3;
+}
+
+template <int QT>
+__global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint8_t *__restrict__ xp,
+                                                 const float *__restrict__ xs16,
+                                                 const float *__restrict__ xpf, float *__restrict__ y,
+                                                 int M, int act, int tilesM, int tilesN) {
+    using F = Fmt<QT>;
+    using L = StageLayout<QT>;
+    constexpr int WM = 2, WN = 1;
+    __shared__ __attribute__((aligned(16))) uint8_t sbuf[2][L::BYTES];
     // XCD-aware tile order: workgroups are dealt to the 8 XCDs round-robin
     // (bid % 8), each XCD with its own L2. Give every XCD a contiguous run of
     // tiles in row-band-major order, so that the N tiles of a row band — which
@@ -302,171 +305,218 @@ __global__ __launch_bounds__(256) void k_gemm_direct(DevW W, const uint8_t *__re
     const int q = ntiles / 8, rem = ntiles % 8, xcd = bid % 8, loc = bid / 8;
     const int t = xcd < rem ? xcd * (q + 1) + loc : rem * (q + 1) + (xcd - rem) * q + loc;
     const int tm = t / tilesN, tn = t % tilesN;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int g = lane >> 4, col = lane & 15;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int hh = lane >> 5, col = lane & 31;
     const int Kc = W.Kp / 128, Kp16 = W.Kp / 16;
-    int gm[WM], gn[WN], shw[WN];
+    const int G0 = tm * 2, GC0 = tn * 4;
+    const int gj[WN] = {wave};
+
+    auto stage = [&](int c, int h, uint8_t *B) {
+        const int rg = wave >> 1, gc = GC0 + wave;
+        dma<4096>(xp + (((size_t)(G0 + rg) * Kc + c) * 16 + 8 * h + 4 * (wave & 1)) * 1024,
+                  B + L::A + rg * 8192 + (wave & 1) * 4096, lane);
+        dma<L::B0S>(W.p0 + ((size_t)gc * Kc + c) * 64 * F::B0 + Stage<F::B0>::off(h), B + L::P0 + wave * L::B0S, lane);
+        if constexpr (F::B1 > 0)
+            dma<L::B1S>(W.p1 + ((size_t)gc * Kc + c) * 64 * F::B1 + Stage<F::B1>::off(h), B + L::P1 + wave * L::B1S,
+                        lane);
+        if constexpr (F::HB > 0) dma<F::HB>(F::hb_src(W, Kc, gc, c), B + L::HB + wave * F::HB, lane);
+        if constexpr (F::H2 > 0) dma<F::H2>(F::h2_src(W, Kc, gc, c), B + L::H2 + wave * F::H2, lane);
+        if (wave < 2) {
+            dma<128>((const uint8_t *)(xpf + ((size_t)(G0 + wave) * Kc + c) * 32), B + L::PF + wave * 128, lane);
+            if constexpr (F::MINS)
+                dma<512>((const uint8_t *)(xs16 + ((size_t)(G0 + wave) * Kp16 + 8 * c + 4 * h) * 32),
+                         B + L::XS + wave * 512, lane);
+        }
+    };
+
+    auto compute = [&](const uint8_t *B, int c, int h, f16v (&acc)[WM][WN]) {
+        BH<QT, WN> hd;
+        F::hdr_lds(B + L::HB + wave * F::HB, B + L::H2 + wave * F::H2, c, lane, hd.h[0]);
 #pragma unroll
-    for (int i = 0; i < WM; i++) gm[i] = (tm * 2 + (wave >> 1)) * WM + i;
+        for (int sl = 0; sl < 2; sl++) {
+            const int s = 2 * h + sl;
+            AK<WM> a;
 #pragma unroll
-    for (int j = 0; j < WN; j++) {
-        gn[j] = (tn * 2 + (wave & 1)) * WN + j;
-        shw[j] = wshift<QT>(W, 16 * gn[j] + col);
-    }
-    const AFromPrep<WM> src{xp, xs16, Kc, Kp16, gm};
-    f4 total[WM][WN];
+            for (int i = 0; i < WM; i++)
 #pragma unroll
-    for (int i = 0; i < WM; i++)
+                for (int kh = 0; kh < 2; kh++) {
+                    const uint8_t *pp = B + L::A + i * 8192 + ((2 * sl + kh) * 2) * 1024 + lane * 16;
+                    a.h[i][kh] = *(const half8 *)pp;
+                    a.l[i][kh] = *(const half8 *)(pp + 1024);
+                    if constexpr (F::MINS) a.xs[i][kh] = lds_rows16(B + L::XS + i * 512 + (2 * sl + kh) * 128, hh);
+                }
+            BK<QT, WN> b;
+            F::k_lds(B + L::P0 + wave * L::B0S, B + L::P1 + wave * L::B1S, s, lane, b.r[0]);
+            kstep<QT, WM, WN>(a, b, hd, s, acc);
+            // the affine formats' sub-block sums would otherwise be hoisted a
+            // kstep ahead, past the register budget
+            if constexpr (F::MINS) __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    f16v total[WM][WN];
 #pragma unroll
-        for (int j = 0; j < WN; j++) total[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < WM; i++) total[i][0] = zero16();
+    stage(0, 0, sbuf[0]);
     for (int c = 0; c < Kc; c++) {
-        BRaw<QT, WN> braw;
-        load_b<QT, WN>(W, Kc, gn, c, lane, braw);
-        int4 sh4[WM];  // issued now, used after the chunk
+        // the stage (issued one half ago) has landed for every wave, and every
+        // wave is done reading the buffer the next stage overwrites
+        wait_vm<0>();
+        __syncthreads();
+        stage(c, 1, sbuf[1]);
+        f16v acc[WM][WN];
 #pragma unroll
-        for (int i = 0; i < WM; i++) sh4[i] = *(const int4 *)(xsh + ((size_t)gm[i] * Kc + c) * 16 + 4 * g);
-        f4 acc[WM][WN];
-#pragma unroll
-        for (int i = 0; i < WM; i++)
-#pragma unroll
-            for (int j = 0; j < WN; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-        chunk_all<QT, WM, WN, AFromPrep<WM>, PIPE>(W, Kc, src, braw, gn, c, lane, acc);
+        for (int i = 0; i < WM; i++) acc[i][0] = zero16();
+        compute(sbuf[0], c, 0, acc);
+        wait_vm<0>();
+        __syncthreads();
+        if (c + 1 < Kc) stage(c + 1, 0, sbuf[0]);
+        compute(sbuf[1], c, 1, acc);
 #pragma unroll
         for (int i = 0; i < WM; i++) {
-            const int sh[4] = {sh4[i].x, sh4[i].y, sh4[i].z, sh4[i].w};
+            const f16v pv = lds_rows16(sbuf[1] + L::PF + i * 128, hh);
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-#pragma unroll
-                for (int j = 0; j < WN; j++)
-                    total[i][j][r] = total[i][j][r] + ldexpf(acc[i][j][r], -(sh[r] + shw[j]));
+            for (int e = 0; e < 16; e++) total[i][0][e] = __builtin_fmaf(pv[e], acc[i][0][e], total[i][0][e]);
         }
     }
+    wait_vm<0>();
+    const int n = 32 * (GC0 + wave) + col;
+    if (n >= W.n) return;
+    const int shw = wshift<QT>(W, n);
 #pragma unroll
     for (int i = 0; i < WM; i++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int m = 16 * gm[i] + 4 * g + r;
+        for (int e = 0; e < 16; e++) {
+            const int m = 32 * (G0 + i) + drow(e, hh);
             if (m >= M) continue;
-#pragma unroll
-            for (int j = 0; j < WN; j++) {
-                const int n = 16 * gn[j] + col;
-                if (n < W.n) y[(size_t)m * W.n + n] = act ? silu_f(total[i][j][r]) : total[i][j][r];
-            }
+            float v = total[i][0][e];
+            if constexpr (QT == QT_F32) v = ldexpf(v, -shw);
+            y[(size_t)m * W.n + n] = act ? silu_f(v) : v;
         }
 }
 
 // ---------------------------------------------------------------------------
 // Small-M GEMV (M <= 16), no preparation pass: each wave splits its chunks of
 // x in registers (split_chunk, the same function k_prep runs) and applies
-// them to WNG 16-column groups; the NW waves of a workgroup take chunks
-// c = w, w+NW, ...; the scaled chunk partials meet in LDS and are summed in
-// chunk order from zero — the sequence k_gemm runs in registers.
+// them to WNG 32-column groups; the NW waves of a workgroup take chunks
+// c = w, w+NW, ...; the chunk results of rows 0..15 and their fold factors
+// meet in LDS and are folded in chunk order from zero — the sequence k_gemm
+// runs in registers.
 template <int QT, int NW, int WNG>
 __global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const float *__restrict__ x, int M, int vec,
                                                   float *__restrict__ y, int act) {
-    extern __shared__ f4 part[];  // [Kc][WNG][64]
+    extern __shared__ float part[];  // [Kc][WNG][8][64] chunk results, then pf [Kc][16]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int g = lane >> 4, col = lane & 15;
+    const int hh = lane >> 5, col = lane & 31;
     const int Kc = W.Kp / 128;
-    int gn[WNG], shw[WNG];
+    float *pf = part + (size_t)Kc * WNG * 8 * 64;
+    int gn[WNG];
 #pragma unroll
-    for (int j = 0; j < WNG; j++) {
-        gn[j] = blockIdx.x * WNG + j;
-        shw[j] = wshift<QT>(W, 16 * gn[j] + col);
-    }
+    for (int j = 0; j < WNG; j++) gn[j] = blockIdx.x * WNG + j;
     for (int c = wave; c < Kc; c += NW) {
+        BH<QT, WNG> hd;
+        load_bh<QT, WNG>(W, Kc, gn, c, lane, hd);
+        BK<QT, WNG> bk[KSTEPS];
+#pragma unroll
+        for (int s = 0; s < KSTEPS; s++) load_bk<QT, WNG>(W, Kc, gn, c, s, lane, bk[s]);
         XChunk xc;
-        split_chunk(x, M, W.k, col, c, g, vec, xc);  // (weight loads issue below; the
-                                                     // compiler hoists them past the split)
-        // C layout: lane holds rows 4g+i; fetch their shifts and sub-block sums
-        int shc[4];
+        split_chunk(x, M, W.k, col, c, hh, vec, xc);
+        if (hh == 0 && col < 16) pf[c * 16 + col] = xc.p;
+        f16v acc[1][WNG];
 #pragma unroll
-        for (int i = 0; i < 4; i++) shc[i] = __shfl(xc.sh, 4 * g + i);
-        f4 xs[2 * KSTEPS];
-        if constexpr (Fmt<QT == QT_F32 ? QT_Q8_0 : QT>::MINS) {
+        for (int j = 0; j < WNG; j++) acc[0][j] = zero16();
 #pragma unroll
-            for (int s = 0; s < KSTEPS; s++) {
-                const float s16 = xc.s8[s] + __shfl_xor(xc.s8[s], 16);
+        for (int s = 0; s < KSTEPS; s++) {
+            AK<1> a;
 #pragma unroll
-                for (int hh = 0; hh < 2; hh++)
+            for (int kh = 0; kh < 2; kh++) {
+                a.h[0][kh] = xc.h[2 * s + kh];
+                a.l[0][kh] = xc.l[2 * s + kh];
+                if constexpr (Fmt<QT>::MINS) {
+                    // sub-block sums of the D-layout rows (rows >= 16 are not live)
+                    const float s16 = xc.s8[2 * s + kh] + __shfl_xor(xc.s8[2 * s + kh], 32);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) xs[2 * s + hh][i] = __shfl(s16, 4 * g + i + 32 * hh);
+                    for (int e = 0; e < 16; e++) a.xs[0][kh][e] = e < 8 ? __shfl(s16, drow(e, hh)) : 0.0f;
+                }
             }
+            kstep<QT, 1, WNG>(a, bk[s], hd, s, acc);
         }
-        const AFromRegs src{&xc, xs};
-        f4 acc[1][WNG];
 #pragma unroll
-        for (int j = 0; j < WNG; j++) acc[0][j] = f4{0.f, 0.f, 0.f, 0.f};
-        BRaw<QT, WNG> braw;
-        load_b<QT, WNG>(W, Kc, gn, c, lane, braw);
-        chunk_all<QT, 1, WNG>(W, Kc, src, braw, gn, c, lane, acc);
+        for (int j = 0; j < WNG; j++)
 #pragma unroll
-        for (int j = 0; j < WNG; j++) {
-            f4 v;
-#pragma unroll
-            for (int i = 0; i < 4; i++) v[i] = ldexpf(acc[0][j][i], -(shc[i] + shw[j]));
-            part[(c * WNG + j) * 64 + lane] = v;
-        }
+            for (int e = 0; e < 8; e++) part[((c * WNG + j) * 8 + e) * 64 + lane] = acc[0][j][e];
     }
     __syncthreads();
     for (int j = wave; j < WNG; j += NW) {
-        f4 total = f4{0.f, 0.f, 0.f, 0.f};
-        for (int c = 0; c < Kc; c++) total = total + part[(c * WNG + j) * 64 + lane];
-        const int n = 16 * gn[j] + col;
-        if (n >= W.n) continue;
+        float total[8];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = 4 * g + i;
-            if (m < M) y[(size_t)m * W.n + n] = act ? silu_f(total[i]) : total[i];
+        for (int e = 0; e < 8; e++) total[e] = 0.0f;
+        for (int c = 0; c < Kc; c++)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                total[e] = __builtin_fmaf(pf[c * 16 + drow(e, hh)], part[((c * WNG + j) * 8 + e) * 64 + lane], total[e]);
+        const int n = 32 * gn[j] + col;
+        if (n >= W.n) continue;
+        const int shw = wshift<QT>(W, n);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int m = drow(e, hh);
+            if (m >= M) continue;
+            float v = total[e];
+            if constexpr (QT == QT_F32) v = ldexpf(v, -shw);
+            y[(size_t)m * W.n + n] = act ? silu_f(v) : v;
         }
     }
 }
 
 // ---------------------------------------------------------------------------
-// Activation preparation for k_gemm: one workgroup (4 waves) per 16-row
+// Activation preparation for k_gemm: one workgroup (4 waves) per 32-row
 // group; wave w splits chunks c = w, w+4, ... with split_chunk and stores
-//   xp   A fragments of (xh, xl), zero beyond M and K
+//   xp   A fragments of (xh, xl), zero beyond M and K   [G][chunk][u][term][64][16 B]
 //   xs16 per row and 16-element sub-block: (first 8 in order) + (next 8)
-//   xsh  per row group, chunk and row: the shift  [G][chunk][16]
+//   xpf  per row group, chunk and row: the fold factor 2^-sh  [G][chunk][32]
 __global__ __launch_bounds__(256) void k_prep(const float *__restrict__ x, int M, int K, int Kp,
                                               uint8_t *__restrict__ xp, float *__restrict__ xs16,
-                                              int *__restrict__ xsh, int want_xsum, int vec) {
+                                              float *__restrict__ xpf, int want_xsum, int vec) {
     const int G = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r = lane & 15, g = lane >> 4, m = 16 * G + r;
+    const int r = lane & 31, hh = lane >> 5, m = 32 * G + r;
     const int Kc = Kp / 128;
     for (int c = wave; c < Kc; c += 4) {
         XChunk xc;
-        split_chunk(x, M, K, m, c, g, vec, xc);
+        split_chunk(x, M, K, m, c, hh, vec, xc);
 #pragma unroll
-        for (int s = 0; s < KSTEPS; s++) {
-            const size_t off = ((((size_t)G * Kc + c) * KSTEPS + s) * 2) * 64 * 16;
-            *(half8 *)(xp + off + lane * 16) = xc.h[s];
-            *(half8 *)(xp + off + (64 + lane) * 16) = xc.l[s];
+        for (int u = 0; u < HSTEPS; u++) {
+            const size_t off = ((((size_t)G * Kc + c) * HSTEPS + u) * 2) * 64 * 16;
+            *(half8 *)(xp + off + lane * 16) = xc.h[u];
+            *(half8 *)(xp + off + (64 + lane) * 16) = xc.l[u];
             if (want_xsum) {
-                const float s16 = xc.s8[s] + __shfl_xor(xc.s8[s], 16);
-                if ((g & 1) == 0) xs16[((size_t)G * (Kp / 16) + 8 * c + 2 * s + (g >> 1)) * 16 + r] = s16;
+                const float s16 = xc.s8[u] + __shfl_xor(xc.s8[u], 32);
+                if (hh == 0) xs16[((size_t)G * (Kp / 16) + 8 * c + u) * 32 + r] = s16;
             }
         }
-        if (g == 0) xsh[((size_t)G * Kc + c) * 16 + r] = xc.sh;
+        if (hh == 0) xpf[((size_t)G * Kc + c) * 32 + r] = xc.p;
     }
 }
 
 // ---------------------------------------------------------------------------
 // INT8ACT numerics: the reference's small-T int8 path (src/qmat.c:508-552),
 // for every M. Activations are quantized per row exactly as
-// quantize_act_int8 (qmat.c:186-202); v_mfma_i32_16x16x64_i8 forms the exact
-// integer sums; the f32 combine follows the reference's order:
+// quantize_act_int8 (qmat.c:186-202); v_mfma_i32_32x32x32_i8 forms the exact
+// integer sum of one 32-block per instruction; the f32 combine follows the
+// reference's order:
 //   INT8   y = ((float)s * ws) * sx           (s over the whole row)
 //   INT4   acc = acc + (float)ig * sg per group of 32, in order; y = acc * sx
 //   Q8_0/Q4_0  the same with the block factor d (the oracle's block semantics)
-// Int8 activation layout: [row group][kstep pair][64][16 B]; each lane's 16
-// bytes are kstep 2p then 2p+1, each as dwords {e0,e4,e1,e5} {e2,e6,e3,e7} of
-// elements 8g..8g+7 — the byte order of the weight planes, so weight bytes
+// Int8 activation layout: [row group][kstep][64][16 B]; each lane's 16 bytes
+// are half-steps 2s then 2s+1, each as dwords {e0,e4,e1,e5} {e2,e6,e3,e7} of
+// elements 8hh..8hh+7 — the byte order of the weight planes, so weight bytes
 // (or nibbles expanded with two masks) feed the MFMA unchanged.
 typedef int i4v __attribute__((ext_vector_type(4)));
+typedef int i16v __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ i4v mfma_i8(i4v a, i4v b, i4v c) {
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+__device__ __forceinline__ i16v mfma_i8(i4v a, i4v b, i16v c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ int act_q8(float v, float inv) {
@@ -475,14 +525,13 @@ __device__ __forceinline__ int act_q8(float v, float inv) {
     return q > 127 ? 127 : (q < -127 ? -127 : q);
 }
 
-// one workgroup (4 waves) per 16-row group
+// one workgroup (4 waves) per 32-row group
 __global__ __launch_bounds__(256) void k_prep_i8(const float *__restrict__ x, int M, int K, int Kp,
-                                                 uint8_t *__restrict__ qx, float *__restrict__ sx,
-                                                 int *__restrict__ gsum) {
-    __shared__ float invs[16];
+                                                 uint8_t *__restrict__ qx, float *__restrict__ sx) {
+    __shared__ float invs[32];
     const int G = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int rr = 0; rr < 4; rr++) {
-        const int m = 16 * G + 4 * wave + rr;
+    for (int rr = 0; rr < 8; rr++) {
+        const int m = 32 * G + 8 * wave + rr;
         float amax = 0.0f;
         if (m < M) {
             const float *row = x + (size_t)m * K;
@@ -490,147 +539,141 @@ __global__ __launch_bounds__(256) void k_prep_i8(const float *__restrict__ x, in
         }
         for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
         if (lane == 0) {
-            invs[4 * wave + rr] = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+            invs[8 * wave + rr] = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
             sx[m] = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 0.0f;
         }
     }
     __syncthreads();
-    const int r = lane & 15, g = lane >> 4, m = 16 * G + r;
+    const int r = lane & 31, hh = lane >> 5, m = 32 * G + r;
     const float inv = invs[r];
     const bool live = m < M && inv > 0.0f;
     const float *row = x + (size_t)(m < M ? m : 0) * K;
-    const int P = Kp / 64;
+    const int S = Kp / 32;
     static const int kWord[8] = {0, 0, 1, 1, 0, 0, 1, 1};
     static const int kByte[8] = {0, 2, 0, 2, 1, 3, 1, 3};
-    for (int p = wave; p < P; p += 4) {
+    for (int s = wave; s < S; s += 4) {
         uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int k0 = 64 * p + 32 * h + 8 * g;
-            int gs = 0;
+        for (int kh = 0; kh < 2; kh++) {
+            const int k0 = 32 * s + 16 * kh + 8 * hh;
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const int q = (live && k0 + j < K) ? act_q8(row[k0 + j], inv) : 0;
-                gs += q;
-                w[2 * h + kWord[j]] |= ((uint32_t)q & 0xffu) << (8 * kByte[j]);
+                w[2 * kh + kWord[j]] |= ((uint32_t)q & 0xffu) << (8 * kByte[j]);
             }
-            gs += __shfl_xor(gs, 16);
-            gs += __shfl_xor(gs, 32);
-            if (g == 0) gsum[((size_t)G * (Kp / 32) + 2 * p + h) * 16 + r] = gs;
         }
-        *(uint4 *)(qx + (((size_t)G * P + p) * 64 + lane) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+        *(uint4 *)(qx + (((size_t)G * S + s) * 64 + lane) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
     }
 }
 
-// 4 waves per workgroup, one 16-column group each, WM row groups per wave.
+// 4 waves per workgroup, one 32-column group each, WM row groups per wave.
 template <int QT, int WM>
 __global__ __launch_bounds__(256) void k_gemm_i8(DevW W, const uint8_t *__restrict__ qx,
-                                                 const float *__restrict__ sx, const int *__restrict__ gsum,
-                                                 float *__restrict__ y, int M, int act) {
+                                                 const float *__restrict__ sx, float *__restrict__ y,
+                                                 int M, int act) {
     constexpr bool NIB = QT == QT_INT4 || QT == QT_Q4_0;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int g = lane >> 4, col = lane & 15;
-    const int G = blockIdx.x * 4 + wave;       // weight row group
-    const int Kc = W.Kp / 128, P = W.Kp / 64;
+    const int hh = lane >> 5, col = lane & 31;
+    const int G = blockIdx.x * 4 + wave;  // weight column group
+    const int Kc = W.Kp / 128, S = W.Kp / 32;
     int gm[WM];
 #pragma unroll
     for (int i = 0; i < WM; i++) gm[i] = blockIdx.y * WM + i;
-    i4v si[WM];
-    f4 acc[WM];
+    i16v si[WM];
+    f16v acc[WM];
 #pragma unroll
-    for (int i = 0; i < WM; i++) {
-        si[i] = i4v{0, 0, 0, 0};
-        acc[i] = f4{0.f, 0.f, 0.f, 0.f};
-    }
-    for (int p = 0; p < P; p++) {
-        const int c = p >> 1, q = p & 1;
+    for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            si[i][e] = 0;
+            acc[i][e] = 0.0f;
+        }
+    i16v zi;
+#pragma unroll
+    for (int e = 0; e < 16; e++) zi[e] = 0;
+    const i4v minus8 = {(int)0xF8F8F8F8u, (int)0xF8F8F8F8u, (int)0xF8F8F8F8u, (int)0xF8F8F8F8u};
+    for (int ks = 0; ks < S; ks++) {
+        const int c = ks >> 2, s = ks & 3;
+        const size_t tile = (size_t)G * Kc + c;
         uint32_t b[4];
         if constexpr (NIB) {
-            const uint2 v = *(const uint2 *)(W.p0 + (((size_t)G * Kc + c) * 64 + lane) * 16 + 8 * q);
+            const uint2 v = *(const uint2 *)(W.p0 + ((tile * 2 + (s >> 1)) * 64 + lane) * 16 + 8 * (s & 1));
             b[0] = v.x & 0x0F0F0F0Fu;
             b[1] = (v.x >> 4) & 0x0F0F0F0Fu;
             b[2] = v.y & 0x0F0F0F0Fu;
             b[3] = (v.y >> 4) & 0x0F0F0F0Fu;
         } else {
-            const uint4 v = *(const uint4 *)(W.p0 + ((((size_t)G * Kc + c) * 2 + q) * 64 + lane) * 16);
+            const uint4 v = *(const uint4 *)(W.p0 + ((tile * 4 + s) * 64 + lane) * 16);
             b[0] = v.x; b[1] = v.y; b[2] = v.z; b[3] = v.w;
         }
-        float d0 = 0.f, d1 = 0.f;
+        float d = 0.f;
         if constexpr (QT == QT_Q8_0 || QT == QT_Q4_0) {
-            const uint32_t hd = *(const uint32_t *)(W.h + (((size_t)G * Kc + c) * 16 + col) * 8 + 4 * q);
-            d0 = h2f(hd & 0xffff);
-            d1 = h2f(hd >> 16);
+            const uint32_t hd = *(const uint32_t *)(W.h + (tile * 32 + col) * 8 + 4 * (s >> 1));
+            d = h2f((hd >> (16 * (s & 1))) & 0xffff);
         } else if constexpr (QT == QT_INT4) {
-            const float2 v = *(const float2 *)(W.h2 + (((size_t)G * Kc + c) * 16 + col) * 4 + 2 * q);
-            d0 = v.x;
-            d1 = v.y;
+            d = W.h2[(tile * 32 + col) * 4 + s];
         }
         const i4v bb = {(int)b[0], (int)b[1], (int)b[2], (int)b[3]};
-        const i4v blo = {(int)b[0], (int)b[1], 0, 0}, bhi = {0, 0, (int)b[2], (int)b[3]};
 #pragma unroll
         for (int i = 0; i < WM; i++) {
-            const i4v a = *(const i4v *)(qx + (((size_t)gm[i] * P + p) * 64 + lane) * 16);
+            const i4v a = *(const i4v *)(qx + (((size_t)gm[i] * S + ks) * 64 + lane) * 16);
             if constexpr (QT == QT_INT8) {
                 si[i] = mfma_i8(a, bb, si[i]);
             } else {
-                i4v t0 = mfma_i8(a, blo, i4v{0, 0, 0, 0});
-                i4v t1 = mfma_i8(a, bhi, i4v{0, 0, 0, 0});
-                if constexpr (NIB) {  // sum (n - 8) * q = sum n * q - 8 * sum q
-                    const int4 g0 = *(const int4 *)(gsum + ((size_t)gm[i] * (W.Kp / 32) + 2 * p) * 16 + 4 * g);
-                    const int4 g1 = *(const int4 *)(gsum + ((size_t)gm[i] * (W.Kp / 32) + 2 * p + 1) * 16 + 4 * g);
-                    t0 -= 8 * i4v{g0.x, g0.y, g0.z, g0.w};
-                    t1 -= 8 * i4v{g1.x, g1.y, g1.z, g1.w};
-                }
+                // nibble formats: sum (n - 8) * q = sum q * (-8) + sum n * q
+                const i16v t = mfma_i8(a, bb, NIB ? mfma_i8(a, minus8, zi) : zi);
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    acc[i][r] = __fadd_rn(acc[i][r], __fmul_rn((float)t0[r], d0));
-                    acc[i][r] = __fadd_rn(acc[i][r], __fmul_rn((float)t1[r], d1));
-                }
+                for (int e = 0; e < 16; e++) acc[i][e] = __fadd_rn(acc[i][e], __fmul_rn((float)t[e], d));
             }
         }
     }
-    const int n = 16 * G + col;
+    const int n = 32 * G + col;
     if (n >= W.n) return;
     const float ws = QT == QT_INT8 ? W.h2[n] : 0.0f;
 #pragma unroll
     for (int i = 0; i < WM; i++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int m = 16 * gm[i] + 4 * g + r;
+        for (int e = 0; e < 16; e++) {
+            const int m = 32 * gm[i] + drow(e, hh);
             if (m >= M) continue;
             float v;
-            if constexpr (QT == QT_INT8) v = __fmul_rn(__fmul_rn((float)si[i][r], ws), sx[m]);
-            else v = __fmul_rn(acc[i][r], sx[m]);
+            if constexpr (QT == QT_INT8) v = __fmul_rn(__fmul_rn((float)si[i][e], ws), sx[m]);
+            else v = __fmul_rn(acc[i][e], sx[m]);
             y[(size_t)m * W.n + n] = act ? silu_f(v) : v;
         }
 }
 
 // ---------------------------------------------------------------------------
-// Dequantization from the resident layout: one wave per (row group, chunk).
+// Dequantization from the resident layout: one wave per (column group, chunk).
 // Values are formed exactly as the reference decoders form them.
 template <int QT>
 __global__ __launch_bounds__(64) void k_dequant(DevW W, float *__restrict__ out) {
     using F = Fmt<QT>;
     const int lane = threadIdx.x, c = blockIdx.x, G = blockIdx.y;
     const int Kc = W.Kp / 128;
-    typename F::Raw raw;
-    F::load(W, Kc, G, c, lane, raw);
-    const int n = 16 * G + (lane & 15), g = lane >> 4;
+    typename F::Hdr hd;
+    F::load_hdr(W, Kc, G, c, lane, hd);
+    const int n = 32 * G + (lane & 31), hh = lane >> 5;
     if (n >= W.n) return;
 #pragma unroll
     for (int s = 0; s < KSTEPS; s++) {
-        const half8 q = F::decode(raw, s);
-        float sc, mn;
-        F::scale(raw, s, F::SUB16 ? (g >> 1) : 0, sc, mn);
+        typename F::RawK raw;
+        F::load_k(W, Kc, G, c, s, lane, raw);
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int k = 128 * c + 32 * s + 8 * g + j;
-            if (k >= W.k) continue;
-            const float qv = (float)q[j];
-            float v;
-            if constexpr (F::MINS) v = __fsub_rn(__fmul_rn(sc, qv), mn);
-            else v = __fmul_rn(sc, qv);
-            out[(size_t)n * W.k + k] = v;
+        for (int kh = 0; kh < 2; kh++) {
+            const half8 q = F::decode(raw, s, kh);
+            float sc, mn;
+            F::scale(hd, s, F::SUB16 ? kh : 0, sc, mn);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int k = 128 * c + 32 * s + 16 * kh + 8 * hh + j;
+                if (k >= W.k) continue;
+                const float qv = (float)q[j];
+                float v;
+                if constexpr (F::MINS) v = __fsub_rn(__fmul_rn(sc, qv), mn);
+                else v = __fmul_rn(sc, qv);
+                out[(size_t)n * W.k + k] = v;
+            }
         }
     }
 }
@@ -650,16 +693,22 @@ template <int QT, int NW, int WNG>
 static hipError_t launch_gemv(const DevW &W, const float *x, int M, int vec, float *y, int act,
                               hipStream_t st) {
     const int Kc = W.Kp / 128;
-    hipLaunchKernelGGL((k_gemv<QT, NW, WNG>), dim3(W.Np / 16 / WNG), dim3(NW * 64),
-                       (size_t)Kc * WNG * 64 * 16, st, W, x, M, vec, y, act);
+    const size_t lds = ((size_t)Kc * WNG * 8 * 64 + (size_t)Kc * 16) * sizeof(float);
+    static bool attr = false;  // allow dynamic LDS beyond 64 KiB (gfx950 has 160 KiB)
+    if (!attr) {
+        (void)hipFuncSetAttribute((const void *)k_gemv<QT, NW, WNG>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024);
+        attr = true;
+    }
+    hipLaunchKernelGGL((k_gemv<QT, NW, WNG>), dim3(W.Np / 32 / WNG), dim3(NW * 64), lds, st, W, x, M, vec,
+                       y, act);
     return hipGetLastError();
 }
 
-// column groups per GEMV workgroup: more for wide outputs, so that each chunk
-// of x is split once for several groups
+// column groups per GEMV workgroup: two for wide outputs, so that each chunk
+// of x is split once for both
 static int gemv_wng(const DevW &W) {
-    const int Kc = W.Kp / 128, groups = W.Np / 16;
-    if (groups >= 1024 && Kc <= 16) return 4;
+    const int Kc = W.Kp / 128, groups = W.Np / 32;
     if (groups >= 256 && Kc <= 32) return 2;
     return 1;
 }
@@ -668,48 +717,23 @@ template <int QT>
 static hipError_t gemv_t(const DevW &W, const float *x, int M, int vec, float *y, int act,
                          hipStream_t st) {
     const int Kc = W.Kp / 128, wng = gemv_wng(W);
-    if (wng == 4) {
-        if (Kc >= 8) return launch_gemv<QT, 8, 4>(W, x, M, vec, y, act, st);
-        return launch_gemv<QT, 4, 4>(W, x, M, vec, y, act, st);
-    }
     if (wng == 2) {
-        if (Kc >= 16) return launch_gemv<QT, 16, 2>(W, x, M, vec, y, act, st);
         if (Kc >= 8) return launch_gemv<QT, 8, 2>(W, x, M, vec, y, act, st);
         return launch_gemv<QT, 4, 2>(W, x, M, vec, y, act, st);
     }
-    if (Kc >= 16) return launch_gemv<QT, 16, 1>(W, x, M, vec, y, act, st);
     if (Kc >= 8) return launch_gemv<QT, 8, 1>(W, x, M, vec, y, act, st);
     return launch_gemv<QT, 4, 1>(W, x, M, vec, y, act, st);
 }
 
-template <int QT, int WM>
-static hipError_t launch_direct(const DevW &W, const uint8_t *xp, const float *xs16, const int *xsh, float *y,
-                                int M, int act, hipStream_t st) {
-    const int tilesM = mh_mpad(M) / (32 * WM), tilesN = W.Np / 128;
-    hipLaunchKernelGGL((k_gemm_direct<QT, WM, 4, false>), dim3(tilesM * tilesN), dim3(256), 0, st,
-                       W, xp, xs16, xsh, y, M, act, tilesM, tilesN);
-    return hipGetLastError();
-}
-
-// Rows per wave (WM): 2 for the block-scaled formats at large M, 1 for small
-// M and for the K-quants, whose decoders need the registers (measured best on
-// the BASELINE shapes). MYNAH_ASR_HIP_GEMM_WM=1|2 overrides, for tuning.
-int mh_gemm_wm(int M, bool kquant) {
-    static int forced = -2;
-    if (forced == -2) {
-        const char *e = getenv("MYNAH_ASR_HIP_GEMM_WM");
-        forced = e ? atoi(e) : -1;
-    }
-    if (forced == 1 || forced == 2) return forced;
-    return (kquant || M <= 1024) ? 1 : 2;
-}
-
 template <int QT>
-static hipError_t gemm_t(const DevW &W, const uint8_t *xp, const float *xs16, const int *xsh, float *y,
+static hipError_t gemm_t(const DevW &W, const uint8_t *xp, const float *xs16, const float *xpf, float *y,
                          int M, int act, hipStream_t st) {
-    constexpr bool kq = QT == QT_Q2_K || QT == QT_Q3_K || QT == QT_Q4_K || QT == QT_Q5_K || QT == QT_Q6_K;
-    if (mh_gemm_wm(M, kq) == 2) return launch_direct<QT, 2>(W, xp, xs16, xsh, y, M, act, st);
-    return launch_direct<QT, 1>(W, xp, xs16, xsh, y, M, act, st);
+    const int mpad = mh_mpad(M);
+    if (mpad % 64 != 0 || W.Np % 128 != 0) return hipErrorInvalidValue;
+    const int tilesM = mpad / 64, tilesN = W.Np / 128;
+    hipLaunchKernelGGL((k_gemm<QT>), dim3(tilesM * tilesN), dim3(256), 0, st, W, xp, xs16, xpf, y, M, act, tilesM,
+                       tilesN);
+    return hipGetLastError();
 }
 
 #define MH_DISPATCH(fn, qtype, ...)                                  \
@@ -735,13 +759,13 @@ hipError_t mh_launch_gemv(int qtype, const DevW &W, const float *x, int M, int v
 }
 
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
-                          const int *xsh, float *y, int M, int act, hipStream_t st) {
-    MH_DISPATCH(gemm_t, qtype, W, xp, xs16, xsh, y, M, act, st)
+                          const float *xpf, float *y, int M, int act, hipStream_t st) {
+    MH_DISPATCH(gemm_t, qtype, W, xp, xs16, xpf, y, M, act, st)
 }
 
 hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,
-                          int *xsh, int want_xsum, int vec, hipStream_t st) {
-    hipLaunchKernelGGL(k_prep, dim3(Mpad / 16), dim3(256), 0, st, x, M, K, Kp, xp, xs16, xsh,
+                          float *xpf, int want_xsum, int vec, hipStream_t st) {
+    hipLaunchKernelGGL(k_prep, dim3(Mpad / 32), dim3(256), 0, st, x, M, K, Kp, xp, xs16, xpf,
                        want_xsum, vec);
     return hipGetLastError();
 }
@@ -751,7 +775,7 @@ static hipError_t launch_dq(const DevW &W, float *out, hipStream_t st) {
     if constexpr (QT == QT_F32) {
         return hipErrorInvalidValue;
     } else {
-        hipLaunchKernelGGL((k_dequant<QT>), dim3(W.Kp / 128, W.Np / 16), dim3(64), 0, st, W, out);
+        hipLaunchKernelGGL((k_dequant<QT>), dim3(W.Kp / 128, W.Np / 32), dim3(64), 0, st, W, out);
         return hipGetLastError();
     }
 }
@@ -765,33 +789,35 @@ bool mh_i8_supported(int qtype) {
 }
 
 hipError_t mh_launch_prep_i8(const float *x, int M, int K, int Kp, int Mpad, uint8_t *qx, float *sx,
-                             int *gsum, hipStream_t st) {
-    hipLaunchKernelGGL(k_prep_i8, dim3(Mpad / 16), dim3(256), 0, st, x, M, K, Kp, qx, sx, gsum);
+                             hipStream_t st) {
+    hipLaunchKernelGGL(k_prep_i8, dim3(Mpad / 32), dim3(256), 0, st, x, M, K, Kp, qx, sx);
     return hipGetLastError();
 }
 
 template <int QT, int WM>
-static hipError_t launch_i8(const DevW &W, const uint8_t *qx, const float *sx, const int *gsum, float *y,
-                            int M, int act, hipStream_t st) {
-    hipLaunchKernelGGL((k_gemm_i8<QT, WM>), dim3(W.Np / 64, mh_mpad(M) / (16 * WM)), dim3(256), 0, st,
-                       W, qx, sx, gsum, y, M, act);
+static hipError_t launch_i8(const DevW &W, const uint8_t *qx, const float *sx, float *y, int M, int act,
+                            hipStream_t st) {
+    const int mpad = mh_mpad(M);
+    if (mpad % (32 * WM) != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((k_gemm_i8<QT, WM>), dim3(W.Np / 128, mpad / (32 * WM)), dim3(256), 0, st, W, qx, sx, y,
+                       M, act);
     return hipGetLastError();
 }
 
 template <int QT>
-static hipError_t gemm_i8_t(const DevW &W, const uint8_t *qx, const float *sx, const int *gsum, float *y,
-                            int M, int act, hipStream_t st) {
-    if (M <= 64) return launch_i8<QT, 1>(W, qx, sx, gsum, y, M, act, st);
-    return launch_i8<QT, 2>(W, qx, sx, gsum, y, M, act, st);
+static hipError_t gemm_i8_t(const DevW &W, const uint8_t *qx, const float *sx, float *y, int M, int act,
+                            hipStream_t st) {
+    if (M <= 64 || mh_mpad(M) % 64 != 0) return launch_i8<QT, 1>(W, qx, sx, y, M, act, st);
+    return launch_i8<QT, 2>(W, qx, sx, y, M, act, st);
 }
 
-hipError_t mh_launch_gemm_i8(int qtype, const DevW &W, const uint8_t *qx, const float *sx, const int *gsum,
-                             float *y, int M, int act, hipStream_t st) {
+hipError_t mh_launch_gemm_i8(int qtype, const DevW &W, const uint8_t *qx, const float *sx, float *y, int M,
+                             int act, hipStream_t st) {
     switch (qtype) {
-    case QT_INT8: return gemm_i8_t<QT_INT8>(W, qx, sx, gsum, y, M, act, st);
-    case QT_INT4: return gemm_i8_t<QT_INT4>(W, qx, sx, gsum, y, M, act, st);
-    case QT_Q8_0: return gemm_i8_t<QT_Q8_0>(W, qx, sx, gsum, y, M, act, st);
-    case QT_Q4_0: return gemm_i8_t<QT_Q4_0>(W, qx, sx, gsum, y, M, act, st);
+    case QT_INT8: return gemm_i8_t<QT_INT8>(W, qx, sx, y, M, act, st);
+    case QT_INT4: return gemm_i8_t<QT_INT4>(W, qx, sx, y, M, act, st);
+    case QT_Q8_0: return gemm_i8_t<QT_Q8_0>(W, qx, sx, y, M, act, st);
+    case QT_Q4_0: return gemm_i8_t<QT_Q4_0>(W, qx, sx, y, M, act, st);
     }
     return hipErrorInvalidValue;
 }

@@ -8,26 +8,22 @@ struct DevW;
 
 // Rows the prepared-activation buffer must hold for an M-row product: the
 // kernels read whole row groups up to this count.
-static inline int mh_mpad(int M) {
-    if (M <= 512) return (M + 31) / 32 * 32;
-    if (M <= 2048) return (M + 63) / 64 * 64;
-    return (M + 127) / 128 * 128;
-}
+static inline int mh_mpad(int M) { return (M + 63) / 64 * 64; }
 
 hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,
-                          int *xsh, int want_xsum, int vec, hipStream_t st);
+                          float *xpf, int want_xsum, int vec, hipStream_t st);
 // M <= 16 (and K small enough for the LDS partials): the preparation-free GEMV
 bool mh_use_gemv(const DevW &W, int M);
 hipError_t mh_launch_gemv(int qtype, const DevW &W, const float *x, int M, int vec, float *y, int act,
                           hipStream_t st);
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
-                          const int *xsh, float *y, int M, int act, hipStream_t st);
+                          const float *xpf, float *y, int M, int act, hipStream_t st);
 hipError_t mh_launch_dequant(int qtype, const DevW &W, float *out, hipStream_t st);
 hipError_t mh_launch_silu(float *x, size_t n, hipStream_t st);
 
 // INT8ACT numerics (formats INT8, INT4, Q8_0, Q4_0)
 bool mh_i8_supported(int qtype);
 hipError_t mh_launch_prep_i8(const float *x, int M, int K, int Kp, int Mpad, uint8_t *qx, float *sx,
-                             int *gsum, hipStream_t st);
-hipError_t mh_launch_gemm_i8(int qtype, const DevW &W, const uint8_t *qx, const float *sx, const int *gsum,
-                             float *y, int M, int act, hipStream_t st);
+                             hipStream_t st);
+hipError_t mh_launch_gemm_i8(int qtype, const DevW &W, const uint8_t *qx, const float *sx, float *y, int M,
+                             int act, hipStream_t st);

@@ -104,25 +104,23 @@ int mh_repack(const mynah_asr_hip_wdesc *w, HostLayout *L) {
     const int n = w->n, k = w->k;
     const int Np = (n + 127) / 128 * 128;
     const int Kp = (k + 255) / 256 * 256;
-    const int Kc = Kp / 128, NG = Np / 16;
+    const int Kc = Kp / 128, NG = Np / 32;
     L->Np = Np;
     L->Kp = Kp;
     int b0 = 0, b1 = 0;
     size_t hbytes = 0, h2floats = 0;
+    const size_t slots = (size_t)NG * Kc * 32, sb_slots = (size_t)NG * (Kc / 2) * 32;
     switch (qt) {
-    case MYNAH_ASR_HIP_F32: b0 = 128; h2floats = Np; break;
-    case MYNAH_ASR_HIP_INT8: b0 = 32; h2floats = Np; break;
-    case MYNAH_ASR_HIP_INT4: b0 = 16; h2floats = (size_t)NG * Kc * 16 * 4; break;
-    case MYNAH_ASR_HIP_Q8_0: b0 = 32; hbytes = (size_t)NG * Kc * 16 * 8; break;
-    case MYNAH_ASR_HIP_Q4_0: b0 = 16; hbytes = (size_t)NG * Kc * 16 * 8; break;
-    case MYNAH_ASR_HIP_Q4_K: b0 = 16; hbytes = (size_t)NG * (Kc / 2) * 16 * 16; break;
-    case MYNAH_ASR_HIP_Q5_K: b0 = 16; b1 = 4; hbytes = (size_t)NG * (Kc / 2) * 16 * 16; break;
-    case MYNAH_ASR_HIP_Q6_K: b0 = 16; b1 = 8; hbytes = (size_t)NG * (Kc / 2) * 16 * 16;
-        h2floats = (size_t)NG * (Kc / 2) * 16; break;
-    case MYNAH_ASR_HIP_Q3_K: b0 = 8; b1 = 4; hbytes = (size_t)NG * (Kc / 2) * 16 * 16;
-        h2floats = (size_t)NG * (Kc / 2) * 16; break;
-    case MYNAH_ASR_HIP_Q2_K: b0 = 8; hbytes = (size_t)NG * (Kc / 2) * 16 * 16;
-        h2floats = (size_t)NG * (Kc / 2) * 16 * 2; break;
+    case MYNAH_ASR_HIP_F32: b0 = 256; h2floats = Np; break;
+    case MYNAH_ASR_HIP_INT8: b0 = 64; h2floats = Np; break;
+    case MYNAH_ASR_HIP_INT4: b0 = 32; h2floats = slots * 4; break;
+    case MYNAH_ASR_HIP_Q8_0: b0 = 64; hbytes = slots * 8; break;
+    case MYNAH_ASR_HIP_Q4_0: b0 = 32; hbytes = slots * 8; break;
+    case MYNAH_ASR_HIP_Q4_K: b0 = 32; hbytes = sb_slots * 16; break;
+    case MYNAH_ASR_HIP_Q5_K: b0 = 32; b1 = 8; hbytes = sb_slots * 16; break;
+    case MYNAH_ASR_HIP_Q6_K: b0 = 32; b1 = 16; hbytes = sb_slots * 16; h2floats = sb_slots; break;
+    case MYNAH_ASR_HIP_Q3_K: b0 = 16; b1 = 8; hbytes = sb_slots * 16; h2floats = sb_slots; break;
+    case MYNAH_ASR_HIP_Q2_K: b0 = 16; hbytes = sb_slots * 16; h2floats = sb_slots * 2; break;
     }
     L->p0.assign((size_t)NG * Kc * 64 * b0, 0);
     L->p1.assign((size_t)NG * Kc * 64 * b1, 0);
@@ -141,23 +139,24 @@ int mh_repack(const mynah_asr_hip_wdesc *w, HostLayout *L) {
             sh[r] = amax > 0.0f ? 15 - e : 0;
             L->h2[r] = (float)sh[r];
         }
+        // 16-byte part 2u = wh of half-step u, part 2u+1 = wl
         for (int G = 0; G < NG; G++)
             for (int c = 0; c < Kc; c++)
                 for (int lane = 0; lane < 64; lane++) {
-                    const int row = 16 * G + (lane & 15), g = lane >> 4;
-                    uint32_t dw[32];
-                    for (int s = 0; s < 4; s++) {
+                    const int row = 32 * G + (lane & 31), h = lane >> 5;
+                    uint32_t dw[64];
+                    for (int u = 0; u < 8; u++) {
                         _Float16 hi[8], lo[8];
                         for (int j = 0; j < 8; j++) {
-                            const int kk = 128 * c + 32 * s + 8 * g + j;
+                            const int kk = 128 * c + 16 * u + 8 * h + j;
                             const float v = (row < n && kk < k) ? ldexpf(W[(size_t)row * k + kk], sh[row]) : 0.0f;
                             hi[j] = (_Float16)v;
                             lo[j] = (_Float16)(v - (float)hi[j]);
                         }
-                        memcpy(dw + 8 * s, hi, 16);
-                        memcpy(dw + 8 * s + 4, lo, 16);
+                        memcpy(dw + 8 * u, hi, 16);
+                        memcpy(dw + 8 * u + 4, lo, 16);
                     }
-                    put_lane(L->p0.data(), 128, Kc, G, c, lane, dw);
+                    put_lane(L->p0.data(), 256, Kc, G, c, lane, dw);
                 }
         return 0;
     }
@@ -169,39 +168,39 @@ int mh_repack(const mynah_asr_hip_wdesc *w, HostLayout *L) {
     for (int G = 0; G < NG; G++)
         for (int c = 0; c < Kc; c++)
             for (int lane = 0; lane < 64; lane++) {
-                const int row = 16 * G + (lane & 15), g = lane >> 4;
-                uint32_t w0[8] = {0}, w1[2] = {0};
-                for (int s = 0; s < 4; s++)
+                const int row = 32 * G + (lane & 31), h = lane >> 5;
+                uint32_t w0[16] = {0}, w1[4] = {0};
+                for (int u = 0; u < 8; u++)
                     for (int j = 0; j < 8; j++) {
-                        const uint32_t code = code_of(S, row, 128 * c + 32 * s + 8 * g + j);
-                        const int t = j >> 1, u = j & 1;
+                        const uint32_t code = code_of(S, row, 128 * c + 16 * u + 8 * h + j);
+                        const int t = j >> 1, v = j & 1;
                         if (bytes8) {
-                            // dword 2s: elements {0,4,1,5}; dword 2s+1: {2,6,3,7}
+                            // dword 2u: elements {0,4,1,5}; dword 2u+1: {2,6,3,7}
                             static const int kWord[8] = {0, 0, 1, 1, 0, 0, 1, 1};
                             static const int kByte[8] = {0, 2, 0, 2, 1, 3, 1, 3};
-                            w0[2 * s + kWord[j]] |= (code & 0xffu) << (8 * kByte[j]);
+                            w0[2 * u + kWord[j]] |= (code & 0xffu) << (8 * kByte[j]);
                         } else if (nib) {
-                            w0[s] |= (code & 15u) << (16 * u + 4 * t);
+                            w0[u] |= (code & 15u) << (16 * v + 4 * t);
                             if (qt == MYNAH_ASR_HIP_Q5_K)
-                                w1[0] |= ((code >> 4) & 1u) << (16 * u + 4 * s + t);
+                                w1[u >> 2] |= ((code >> 4) & 1u) << (16 * v + 4 * (u & 3) + t);
                             else if (qt == MYNAH_ASR_HIP_Q6_K)
-                                w1[s >> 1] |= ((code >> 4) & 3u) << (16 * u + 8 * (s & 1) + 2 * t);
+                                w1[u >> 1] |= ((code >> 4) & 3u) << (16 * v + 8 * (u & 1) + 2 * t);
                         } else {  // Q3_K, Q2_K: low two bits as crumbs
-                            w0[s >> 1] |= (code & 3u) << (16 * u + 8 * (s & 1) + 2 * t);
+                            w0[u >> 1] |= (code & 3u) << (16 * v + 8 * (u & 1) + 2 * t);
                             if (qt == MYNAH_ASR_HIP_Q3_K)
-                                w1[0] |= ((code >> 2) & 1u) << (16 * u + 4 * s + t);
+                                w1[u >> 2] |= ((code >> 2) & 1u) << (16 * v + 4 * (u & 3) + t);
                         }
                     }
                 put_lane(L->p0.data(), b0, Kc, G, c, lane, w0);
                 if (b1) put_lane(L->p1.data(), b1, Kc, G, c, lane, w1);
             }
 
-    // headers
+    // headers: one slot per (column group, chunk or super-block, column)
     const uint8_t *d = (const uint8_t *)w->data;
     const size_t nblk = (size_t)k / be;
     for (int G = 0; G < NG; G++)
-        for (int r = 0; r < 16; r++) {
-            const int row = 16 * G + r;
+        for (int r = 0; r < 32; r++) {
+            const int row = 32 * G + r;
             if (row >= n) continue;
             if (qt == MYNAH_ASR_HIP_INT8) {
                 L->h2[row] = w->scales[row];
@@ -209,16 +208,16 @@ int mh_repack(const mynah_asr_hip_wdesc *w, HostLayout *L) {
             }
             if (qt == MYNAH_ASR_HIP_INT4) {
                 for (int b = 0; b < k / 32; b++)
-                    L->h2[(((size_t)G * Kc + b / 4) * 16 + r) * 4 + b % 4] = w->scales[(size_t)row * (k / 32) + b];
+                    L->h2[(((size_t)G * Kc + b / 4) * 32 + r) * 4 + b % 4] = w->scales[(size_t)row * (k / 32) + b];
                 continue;
             }
             for (size_t b = 0; b < nblk; b++) {
                 const uint8_t *blk = d + ((size_t)row * nblk + b) * bb;
                 if (qt == MYNAH_ASR_HIP_Q8_0 || qt == MYNAH_ASR_HIP_Q4_0) {
-                    memcpy(&L->h[(((size_t)G * Kc + b / 4) * 16 + r) * 8 + 2 * (b % 4)], blk, 2);
+                    memcpy(&L->h[(((size_t)G * Kc + b / 4) * 32 + r) * 8 + 2 * (b % 4)], blk, 2);
                     continue;
                 }
-                const size_t u = ((size_t)G * (Kc / 2) + b) * 16 + r;
+                const size_t u = ((size_t)G * (Kc / 2) + b) * 32 + r;
                 uint8_t *hh = &L->h[u * 16];
                 switch (qt) {
                 case MYNAH_ASR_HIP_Q4_K:
