@@ -7,9 +7,13 @@ A step is one pass over the FastConformer-0.6B encoder linear set at
 M = 8 segments x 750 frames = 6000 rows (BASELINE config 2's shapes:
 1024->4096, 4096->1024 and five 1024->1024 for Q, K, V, out, pos), every
 weight Q8_0 (BASELINE's metric), EXACT numerics (the default). Inputs are
-resident in HBM before the timed region; each product is the library's full
-device call (activation prep + GEMM kernel). `value` = dense-equivalent
-2*M*N*K operations per second, summed over the step, in TOPS.
+resident in HBM before the timed region; the products go through the
+library's device entry points the way an encoder layer calls them
+(src/encoder.c): the FFN pair through qffn_dev (the first product prepares
+the intermediate for the second), q/k/v through qqkv_dev (one preparation of
+their shared input), out and pos through qgemm_dev (preparation + product).
+`value` = dense-equivalent 2*M*N*K operations per second, summed over the
+step, in TOPS.
 
 Also reported (not `value`): per-kernel roofline fractions, Q4_K at BASELINE
 config 4's M = 12000 shapes, decoder GEMVs (config 3) in HBM GB/s with >= 512
@@ -102,9 +106,26 @@ def run_encoder_set(B, M_, qt, M, shapes, steps, warmup, seed0):
         ys.append(B.empty(M, n))
     B.sync()
 
+    idx = {name: i for i, (name, _, _) in enumerate(shapes)}
+    fused = {"ffn1", "ffn2"} <= idx.keys()
+    qkv = {"q", "k", "v"} <= idx.keys()
+
     def step():
-        for dw, (name, k, n), y in zip(dws, shapes, ys):
-            dw.gemm(xs[k].data_ptr(), y.data_ptr(), M, 0, B.sp)
+        # the encoder layer's call pattern (src/encoder.c): the FFN through the
+        # fused entry point, q/k/v on one prepared input, the rest one by one
+        done = set()
+        if fused:
+            i1, i2 = idx["ffn1"], idx["ffn2"]
+            M_.ffn_dev(lib, dws[i1], dws[i2], xs[shapes[i1][1]].data_ptr(), ys[i2].data_ptr(), M, B.sp)
+            done |= {i1, i2}
+        if qkv:
+            ii = [idx["q"], idx["k"], idx["v"]]
+            M_.qkv_dev(lib, [dws[i] for i in ii], xs[shapes[ii[0]][1]].data_ptr(), [ys[i].data_ptr() for i in ii],
+                       M, B.sp)
+            done |= set(ii)
+        for i, (dw, (name, k, n), y) in enumerate(zip(dws, shapes, ys)):
+            if i not in done:
+                dw.gemm(xs[k].data_ptr(), y.data_ptr(), M, 0, B.sp)
 
     for _ in range(warmup):
         step()

@@ -144,6 +144,17 @@ int mynah_asr_hip_qgemm_dev(const mynah_asr_hip_weight *w, const float *dx, floa
 int mynah_asr_hip_prep_dev(const mynah_asr_hip_weight *w, const float *dx, int T, void *stream);
 int mynah_asr_hip_qgemm_prepped_dev(const mynah_asr_hip_weight *w, float *dy, int T, int act,
                                     void *stream);
+/* dy = SiLU(dx . W1^T) . W2^T (the device twin of mynah_asr_hip_qffn; dx may
+ * alias dy). On the GEMM path in EXACT numerics the first product hands the
+ * intermediate to the second already prepared (no f32 intermediate is
+ * stored); results are bit-identical to two qgemm_dev calls. */
+int mynah_asr_hip_qffn_dev(const mynah_asr_hip_weight *w1, const mynah_asr_hip_weight *w2, const float *dx,
+                           float *dy, int T, void *stream);
+/* dq, dk, dv = dx . Wq^T, Wk^T, Wv^T with one preparation of dx (the device
+ * twin of mynah_asr_hip_qqkv). */
+int mynah_asr_hip_qqkv_dev(const mynah_asr_hip_weight *wq, const mynah_asr_hip_weight *wk,
+                           const mynah_asr_hip_weight *wv, const float *dx, float *dq, float *dk, float *dv, int T,
+                           void *stream);
 /* dwd[n,k] = dequantized weight. */
 int mynah_asr_hip_dequant_dev(const mynah_asr_hip_weight *w, float *dwd, void *stream);
 

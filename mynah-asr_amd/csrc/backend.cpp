@@ -68,12 +68,18 @@ struct DBuf {
     }
 };
 
+// a prepared input: the buffers and what they hold now
+struct PrepBuf {
+    DBuf xp, xs16, xpf;
+    int T = -1, Kp = 0, xsum = 0, i8 = 0;
+};
+
 struct Ctx {
     int state = 0;  // 0 uninitialised, 1 ok, -1 failed
     hipStream_t st = nullptr;
-    DBuf x, y, h, xp, xs16, xpf;
-    // what the workspace holds now (set by prep)
-    int prep_T = -1, prep_Kp = 0, prep_xsum = 0, prep_i8 = 0;
+    DBuf x, y, h;
+    PrepBuf pa;  // the products' input (prep_dev / qgemm_prepped_dev use this one)
+    PrepBuf pb;  // the FFN's intermediate, prepared by the first product
 };
 thread_local Ctx t_ctx;
 
@@ -154,13 +160,13 @@ int check_numerics_supported(int qtype) {
 // into the calling thread's workspace.
 //   EXACT:   xp = f16 A fragments, xs16 = sub-block sums, xpf = chunk fold factors
 //   INT8ACT: xp = int8 A fragments, xs16 = row scales sx
-int prep_for(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, int T, hipStream_t st) {
+int prep_into(PrepBuf &P, const mynah_asr_hip_weight *W, const float *dx, int T, hipStream_t st) {
     const int Mpad = mh_mpad(T), Kp = W->dw.Kp, k = W->dw.k;
     const bool i8 = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT;
     const bool xsum = !i8 && wants_xsum(W->qtype);
-    uint8_t *xp = (uint8_t *)c->xp.get((size_t)Mpad * Kp * (i8 ? 1 : 4));
-    float *xs16 = (float *)c->xs16.get((size_t)Mpad * (i8 ? 1 : Kp / 16) * sizeof(float));
-    float *xpf = (float *)c->xpf.get((size_t)Mpad * (Kp / 128) * sizeof(float));
+    uint8_t *xp = (uint8_t *)P.xp.get((size_t)Mpad * Kp * (i8 ? 1 : 4));
+    float *xs16 = (float *)P.xs16.get((size_t)Mpad * (i8 ? 1 : Kp / 16) * sizeof(float));
+    float *xpf = (float *)P.xpf.get((size_t)Mpad * (Kp / 128) * sizeof(float));
     if (!xp || !xs16 || !xpf) return fail("workspace allocation failed");
     hipError_t e;
     if (i8) {
@@ -170,30 +176,35 @@ int prep_for(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, int T, hipS
         e = mh_launch_prep(dx, T, k, Kp, Mpad, xp, xs16, xpf, xsum ? 1 : 0, vec, st);
     }
     if (e != hipSuccess) return fail("prep launch failed", hipGetErrorString(e));
-    c->prep_T = T;
-    c->prep_Kp = Kp;
-    c->prep_xsum = xsum ? 1 : 0;
-    c->prep_i8 = i8 ? 1 : 0;
+    P.T = T;
+    P.Kp = Kp;
+    P.xsum = xsum ? 1 : 0;
+    P.i8 = i8 ? 1 : 0;
     return 0;
 }
-
-bool prep_fits(const Ctx *c, const mynah_asr_hip_weight *W, int T) {
-    const bool i8 = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT;
-    return c->prep_T == T && c->prep_Kp == W->dw.Kp && c->prep_i8 == (i8 ? 1 : 0) &&
-           (i8 || !wants_xsum(W->qtype) || c->prep_xsum);
+int prep_for(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, int T, hipStream_t st) {
+    return prep_into(c->pa, W, dx, T, st);
 }
 
-// the product on the prepared input
-int run_prepped(Ctx *c, const mynah_asr_hip_weight *W, float *dy, int T, int act, hipStream_t st) {
+bool fits(const PrepBuf &P, const mynah_asr_hip_weight *W, int T) {
+    const bool i8 = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT;
+    return P.T == T && P.Kp == W->dw.Kp && P.i8 == (i8 ? 1 : 0) && (i8 || !wants_xsum(W->qtype) || P.xsum);
+}
+bool prep_fits(const Ctx *c, const mynah_asr_hip_weight *W, int T) { return fits(c->pa, W, T); }
+
+// the product on a prepared input
+int run_from(const PrepBuf &P, const mynah_asr_hip_weight *W, float *dy, int T, int act, hipStream_t st) {
     hipError_t e;
-    if (c->prep_i8)
-        e = mh_launch_gemm_i8(W->qtype, W->dw, (const uint8_t *)c->xp.p, (const float *)c->xs16.p, dy, T,
-                              act, st);
+    if (P.i8)
+        e = mh_launch_gemm_i8(W->qtype, W->dw, (const uint8_t *)P.xp.p, (const float *)P.xs16.p, dy, T, act, st);
     else
-        e = mh_launch_gemm(W->qtype, W->dw, (const uint8_t *)c->xp.p, (const float *)c->xs16.p,
-                           (const float *)c->xpf.p, dy, T, act, st);
+        e = mh_launch_gemm(W->qtype, W->dw, (const uint8_t *)P.xp.p, (const float *)P.xs16.p,
+                           (const float *)P.xpf.p, dy, T, act, st);
     if (e != hipSuccess) return fail("gemm launch failed", hipGetErrorString(e));
     return 0;
+}
+int run_prepped(Ctx *c, const mynah_asr_hip_weight *W, float *dy, int T, int act, hipStream_t st) {
+    return run_from(c->pa, W, dy, T, act, st);
 }
 
 int gemm_dev(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, float *dy, int T, int act,
@@ -206,6 +217,56 @@ int gemm_dev(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, float *dy, 
     }
     if (prep_for(c, W, dx, T, st)) return -1;
     return run_prepped(c, W, dy, T, act, st);
+}
+
+// out = SiLU(x . W1^T) . W2^T on device buffers (dx may alias dy). In EXACT
+// numerics on the GEMM path, when W2's chunks are W1's column tiles, the
+// first product prepares the intermediate for the second in its epilogue
+// (no f32 intermediate, no preparation pass); otherwise two products.
+int ffn_dev(Ctx *c, const mynah_asr_hip_weight *W1, const mynah_asr_hip_weight *W2, const float *dx, float *dy,
+            int T, hipStream_t st) {
+    const bool fuse = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT && !mh_use_gemv(W1->dw, T) &&
+                      W2->dw.Kp == W1->dw.Np;
+    if (fuse) {
+        if (prep_into(c->pa, W1, dx, T, st)) return -1;
+        PrepBuf &P = c->pb;
+        const int Mpad = mh_mpad(T), Kp = W2->dw.Kp;
+        const int xsum = wants_xsum(W2->qtype) ? 1 : 0;
+        uint8_t *xp = (uint8_t *)P.xp.get((size_t)Mpad * Kp * 4);
+        float *xs16 = (float *)P.xs16.get((size_t)Mpad * (Kp / 16) * sizeof(float));
+        float *xpf = (float *)P.xpf.get((size_t)Mpad * (Kp / 128) * sizeof(float));
+        if (!xp || !xs16 || !xpf) return fail("workspace allocation failed");
+        hipError_t e = mh_launch_gemm_prep_out(W1->qtype, W1->dw, (const uint8_t *)c->pa.xp.p,
+                                               (const float *)c->pa.xs16.p, (const float *)c->pa.xpf.p, T, xp, xs16,
+                                               xpf, Kp / 128, xsum, st);
+        if (e != hipSuccess) return fail("gemm launch failed", hipGetErrorString(e));
+        P.T = T;
+        P.Kp = Kp;
+        P.xsum = xsum;
+        P.i8 = 0;
+        return run_from(P, W2, dy, T, 0, st);
+    }
+    float *dh = (float *)c->h.get((size_t)T * W1->dw.n * sizeof(float));
+    if (!dh) return fail("device buffer allocation failed");
+    if (gemm_dev(c, W1, dx, dh, T, 1, st)) return -1;
+    return gemm_dev(c, W2, dh, dy, T, 0, st);
+}
+
+// three products of one input: prepared once whenever it fits them all
+int qkv_dev(Ctx *c, const mynah_asr_hip_weight *const W[3], const float *dx, float *const dy[3], int T,
+            hipStream_t st) {
+    bool prepared = false;
+    for (int i = 0; i < 3; i++) {
+        if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT && mh_use_gemv(W[i]->dw, T)) {
+            if (gemm_dev(c, W[i], dx, dy[i], T, 0, st)) return -1;
+            continue;
+        }
+        if (!prepared || !prep_fits(c, W[i], T))
+            if (prep_for(c, W[i], dx, T, st)) return -1;
+        prepared = true;
+        if (run_prepped(c, W[i], dy[i], T, 0, st)) return -1;
+    }
+    return 0;
 }
 
 int h2d(Ctx *c, DBuf &b, const float *x, size_t n, float **d) {
@@ -307,6 +368,31 @@ int mynah_asr_hip_qgemm_prepped_dev(const mynah_asr_hip_weight *w, float *dy, in
     return run_prepped(c, w, dy, T, act, pick_stream(stream));
 }
 
+int mynah_asr_hip_qffn_dev(const mynah_asr_hip_weight *w1, const mynah_asr_hip_weight *w2, const float *dx,
+                           float *dy, int T, void *stream) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    if (!w1 || !w2 || !dx || !dy || T < 0 || w2->dw.k != w1->dw.n) return fail("bad argument");
+    if (T == 0) return 0;
+    if (check_numerics_supported(w1->qtype) || check_numerics_supported(w2->qtype)) return -1;
+    return ffn_dev(c, w1, w2, dx, dy, T, pick_stream(stream));
+}
+
+int mynah_asr_hip_qqkv_dev(const mynah_asr_hip_weight *wq, const mynah_asr_hip_weight *wk,
+                           const mynah_asr_hip_weight *wv, const float *dx, float *dq, float *dk, float *dv, int T,
+                           void *stream) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    if (!wq || !wk || !wv || !dx || !dq || !dk || !dv || T < 0 || wk->dw.k != wq->dw.k || wv->dw.k != wq->dw.k)
+        return fail("bad argument");
+    if (T == 0) return 0;
+    const mynah_asr_hip_weight *W[3] = {wq, wk, wv};
+    float *const dy[3] = {dq, dk, dv};
+    for (int i = 0; i < 3; i++)
+        if (check_numerics_supported(W[i]->qtype)) return -1;
+    return qkv_dev(c, W, dx, dy, T, pick_stream(stream));
+}
+
 int mynah_asr_hip_dequant_dev(const mynah_asr_hip_weight *w, float *dwd, void *stream) {
     Ctx *c;
     if (begin(&c)) return -1;
@@ -341,12 +427,10 @@ int mynah_asr_hip_qffn(const mynah_asr_hip_wdesc *w1, const mynah_asr_hip_wdesc 
     if (check_numerics_supported(w1->qtype) || check_numerics_supported(w2->qtype)) return -1;
     const mynah_asr_hip_weight *W1 = resident(w1), *W2 = resident(w2);
     if (!W1 || !W2) return -1;
-    float *dx, *dh = (float *)c->h.get((size_t)T * w1->n * sizeof(float));
-    float *dy = (float *)c->y.get((size_t)T * w2->n * sizeof(float));
-    if (!dh || !dy) return fail("device buffer allocation failed");
+    float *dx, *dy = (float *)c->y.get((size_t)T * w2->n * sizeof(float));
+    if (!dy) return fail("device buffer allocation failed");
     if (h2d(c, c->x, x, (size_t)T * w1->k, &dx)) return -1;  // x is consumed before out is written
-    if (gemm_dev(c, W1, dx, dh, T, 1, c->st)) return -1;
-    if (gemm_dev(c, W2, dh, dy, T, 0, c->st)) return -1;
+    if (ffn_dev(c, W1, W2, dx, dy, T, c->st)) return -1;
     return d2h_sync(c, out, dy, (size_t)T * w2->n);
 }
 

@@ -52,23 +52,8 @@ struct XChunk {
     float p;           // 2^-sh: the chunk's fold factor for this row
 };
 
-__device__ __forceinline__ void split_chunk(const float *__restrict__ x, int M, int K, int m, int c,
-                                            int hh, int vec, XChunk &o) {
-    float v[HSTEPS][8];
-    const bool live = m < M;
-    const float *row = x + (size_t)(live ? m : 0) * K;
-#pragma unroll
-    for (int u = 0; u < HSTEPS; u++) {
-        const int k0 = 128 * c + 16 * u + 8 * hh;
-        if (live && vec && k0 + 8 <= K) {
-            const float4 a = *(const float4 *)(row + k0), b = *(const float4 *)(row + k0 + 4);
-            v[u][0] = a.x; v[u][1] = a.y; v[u][2] = a.z; v[u][3] = a.w;
-            v[u][4] = b.x; v[u][5] = b.y; v[u][6] = b.z; v[u][7] = b.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[u][j] = (live && k0 + j < K) ? row[k0 + j] : 0.0f;
-        }
-    }
+// the split of one chunk's values v[u][j] (element 16u + 8hh + j of row m)
+__device__ __forceinline__ void split_vals(const float (&v)[HSTEPS][8], XChunk &o) {
     float amax = 0.0f;
 #pragma unroll
     for (int u = 0; u < HSTEPS; u++)
@@ -92,6 +77,26 @@ __device__ __forceinline__ void split_chunk(const float *__restrict__ x, int M, 
         }
         o.s8[u] = acc;
     }
+}
+
+__device__ __forceinline__ void split_chunk(const float *__restrict__ x, int M, int K, int m, int c,
+                                            int hh, int vec, XChunk &o) {
+    float v[HSTEPS][8];
+    const bool live = m < M;
+    const float *row = x + (size_t)(live ? m : 0) * K;
+#pragma unroll
+    for (int u = 0; u < HSTEPS; u++) {
+        const int k0 = 128 * c + 16 * u + 8 * hh;
+        if (live && vec && k0 + 8 <= K) {
+            const float4 a = *(const float4 *)(row + k0), b = *(const float4 *)(row + k0 + 4);
+            v[u][0] = a.x; v[u][1] = a.y; v[u][2] = a.z; v[u][3] = a.w;
+            v[u][4] = b.x; v[u][5] = b.y; v[u][6] = b.z; v[u][7] = b.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[u][j] = (live && k0 + j < K) ? row[k0 + j] : 0.0f;
+        }
+    }
+    split_vals(v, o);
 }
 
 // ---------------------------------------------------------------------------
@@ -287,11 +292,25 @@ template <int QT> constexpr int gemm_occ() {
     return (QT == QT_F32 || Fmt<QT>::MINS || Fmt<QT>::SUB16) ? 2 : 3;
 }
 
-template <int QT>
+// Where a product's result goes: EPI_Y stores y (SiLU applied when act);
+// EPI_PREP (the first product of the FFN) applies SiLU and, instead of
+// storing the f32 intermediate, prepares it as the second product's input —
+// the workgroup's 128 output columns are exactly one 128-element chunk of
+// the second product's K, so the chunk's shift, split and sums are formed
+// here by split_vals, the same function the preparation pass runs, on the
+// same f32 values (bit-identical to storing y and preparing it).
+enum { EPI_Y = 0, EPI_PREP = 1 };
+struct PrepOut {
+    uint8_t *xp;
+    float *xs16, *xpf;
+    int Kc, xsum;
+};
+
+template <int QT, int EPI>
 __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint8_t *__restrict__ xp,
                                                  const float *__restrict__ xs16,
                                                  const float *__restrict__ xpf, float *__restrict__ y,
-                                                 int M, int act, int tilesM, int tilesN) {
+                                                 int M, int act, int tilesM, int tilesN, PrepOut po) {
     using F = Fmt<QT>;
     using L = StageLayout<QT>;
     constexpr int WM = 2, WN = 1;
@@ -381,6 +400,45 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
         }
     }
     wait_vm<0>();
+    if constexpr (EPI == EPI_PREP) {
+        // the 64 x 128 SiLU tile through LDS (row stride 129: conflict-free
+        // column writes and row reads), then one lane per (row, half) splits
+        static_assert(2 * L::BYTES >= 64 * 129 * 4, "LDS tile");
+        float *T = (float *)&sbuf[0][0];
+        const int shw = wshift<QT>(W, 32 * (GC0 + wave) + col);  // (the pad columns hold 0)
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < WM; i++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                float v = total[i][0][e];
+                if constexpr (QT == QT_F32) v = ldexpf(v, -shw);
+                T[(32 * i + drow(e, hh)) * 129 + 32 * wave + col] = silu_f(v);
+            }
+        __syncthreads();
+        if (wave < 2) {
+            const int G = G0 + wave;
+            float v[HSTEPS][8];
+#pragma unroll
+            for (int u = 0; u < HSTEPS; u++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[u][j] = T[(32 * wave + col) * 129 + 16 * u + 8 * hh + j];
+            XChunk xc;
+            split_vals(v, xc);
+#pragma unroll
+            for (int u = 0; u < HSTEPS; u++) {
+                uint8_t *o = po.xp + ((((size_t)G * po.Kc + tn) * HSTEPS + u) * 2) * 1024;
+                *(half8 *)(o + lane * 16) = xc.h[u];
+                *(half8 *)(o + (64 + lane) * 16) = xc.l[u];
+                if (po.xsum) {
+                    const float s16 = xc.s8[u] + __shfl_xor(xc.s8[u], 32);
+                    if (hh == 0) po.xs16[((size_t)G * (8 * po.Kc) + 8 * tn + u) * 32 + col] = s16;
+                }
+            }
+            if (hh == 0) po.xpf[((size_t)G * po.Kc + tn) * 32 + col] = xc.p;
+        }
+        return;
+    }
     const int n = 32 * (GC0 + wave) + col;
     if (n >= W.n) return;
     const int shw = wshift<QT>(W, n);
@@ -727,12 +785,18 @@ static hipError_t gemv_t(const DevW &W, const float *x, int M, int vec, float *y
 
 template <int QT>
 static hipError_t gemm_t(const DevW &W, const uint8_t *xp, const float *xs16, const float *xpf, float *y,
-                         int M, int act, hipStream_t st) {
+                         int M, int act, const PrepOut *po, hipStream_t st) {
     const int mpad = mh_mpad(M);
     if (mpad % 64 != 0 || W.Np % 128 != 0) return hipErrorInvalidValue;
     const int tilesM = mpad / 64, tilesN = W.Np / 128;
-    hipLaunchKernelGGL((k_gemm<QT>), dim3(tilesM * tilesN), dim3(256), 0, st, W, xp, xs16, xpf, y, M, act, tilesM,
-                       tilesN);
+    if (po) {
+        if (po->Kc != tilesN) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((k_gemm<QT, EPI_PREP>), dim3(tilesM * tilesN), dim3(256), 0, st, W, xp, xs16, xpf, y, M,
+                           1, tilesM, tilesN, *po);
+    } else {
+        hipLaunchKernelGGL((k_gemm<QT, EPI_Y>), dim3(tilesM * tilesN), dim3(256), 0, st, W, xp, xs16, xpf, y, M,
+                           act, tilesM, tilesN, PrepOut{});
+    }
     return hipGetLastError();
 }
 
@@ -760,7 +824,14 @@ hipError_t mh_launch_gemv(int qtype, const DevW &W, const float *x, int M, int v
 
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
                           const float *xpf, float *y, int M, int act, hipStream_t st) {
-    MH_DISPATCH(gemm_t, qtype, W, xp, xs16, xpf, y, M, act, st)
+    MH_DISPATCH(gemm_t, qtype, W, xp, xs16, xpf, y, M, act, nullptr, st)
+}
+
+hipError_t mh_launch_gemm_prep_out(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
+                                   const float *xpf, int M, uint8_t *oxp, float *oxs16, float *oxpf, int oKc,
+                                   int oxsum, hipStream_t st) {
+    const PrepOut po{oxp, oxs16, oxpf, oKc, oxsum};
+    MH_DISPATCH(gemm_t, qtype, W, xp, xs16, xpf, nullptr, M, 1, &po, st)
 }
 
 hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,

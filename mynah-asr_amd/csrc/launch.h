@@ -18,6 +18,12 @@ hipError_t mh_launch_gemv(int qtype, const DevW &W, const float *x, int M, int v
                           hipStream_t st);
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
                           const float *xpf, float *y, int M, int act, hipStream_t st);
+// The FFN's first product with SiLU, its output prepared as the input of a
+// product with Kp = 128 * oKc (oKc = the first product's column tiles):
+// (oxp, oxs16, oxpf) as mh_launch_prep would write them.
+hipError_t mh_launch_gemm_prep_out(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
+                                   const float *xpf, int M, uint8_t *oxp, float *oxs16, float *oxpf, int oKc,
+                                   int oxsum, hipStream_t st);
 hipError_t mh_launch_dequant(int qtype, const DevW &W, float *out, hipStream_t st);
 hipError_t mh_launch_silu(float *x, size_t n, hipStream_t st);
 

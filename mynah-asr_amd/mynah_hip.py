@@ -36,7 +36,7 @@ HIP_SYMBOLS = [
     "mynah_asr_hip_evict", "mynah_asr_hip_evict_all", "mynah_asr_hip_last_error",
     "mynah_asr_hip_weight_create", "mynah_asr_hip_weight_destroy", "mynah_asr_hip_weight_bytes",
     "mynah_asr_hip_qgemm_dev", "mynah_asr_hip_dequant_dev", "mynah_asr_hip_prep_dev",
-    "mynah_asr_hip_qgemm_prepped_dev",
+    "mynah_asr_hip_qgemm_prepped_dev", "mynah_asr_hip_qffn_dev", "mynah_asr_hip_qqkv_dev",
 ]
 HOST_SYMBOLS = [
     "mynah_asr_set_backend", "mynah_asr_backend", "mynah_asr_gemm_wt", "mynah_asr_silu",
@@ -96,6 +96,9 @@ class HipLib:
         if hasattr(L, "mynah_asr_hip_prep_dev"):  # absent from older builds
             L.mynah_asr_hip_prep_dev.argtypes = [_P, _P, C.c_int, _P]
             L.mynah_asr_hip_qgemm_prepped_dev.argtypes = [_P, _P, C.c_int, C.c_int, _P]
+        if hasattr(L, "mynah_asr_hip_qffn_dev"):
+            L.mynah_asr_hip_qffn_dev.argtypes = [_P, _P, _P, _P, C.c_int, _P]
+            L.mynah_asr_hip_qqkv_dev.argtypes = [_P, _P, _P, _P, _P, _P, _P, C.c_int, _P]
         L.mynah_asr_hip_qgemm.argtypes = [C.POINTER(WDesc), _P, _P, C.c_int]
         L.mynah_asr_hip_qffn.argtypes = [C.POINTER(WDesc), C.POINTER(WDesc), _P, _P, C.c_int]
         L.mynah_asr_hip_qqkv.argtypes = [C.POINTER(WDesc)] * 3 + [_P] * 4 + [C.c_int]
@@ -227,6 +230,17 @@ class DeviceWeight:
     def dequant(self, dwd_ptr: int, stream: int = 0) -> None:
         rc = self.lib.L.mynah_asr_hip_dequant_dev(self.h, dwd_ptr, stream or None)
         self.lib._check(rc, "dequant_dev")
+
+
+def ffn_dev(lib, w1: "DeviceWeight", w2: "DeviceWeight", dx_ptr: int, dy_ptr: int, T: int, stream: int = 0):
+    """dy = SiLU(dx . W1^T) . W2^T on device buffers (mynah_asr_hip_qffn_dev)."""
+    lib._check(lib.L.mynah_asr_hip_qffn_dev(w1.h, w2.h, dx_ptr, dy_ptr, T, stream or None), "qffn_dev")
+
+
+def qkv_dev(lib, ws, dx_ptr: int, dys, T: int, stream: int = 0):
+    """Three products of one input, prepared once (mynah_asr_hip_qqkv_dev)."""
+    rc = lib.L.mynah_asr_hip_qqkv_dev(ws[0].h, ws[1].h, ws[2].h, dx_ptr, dys[0], dys[1], dys[2], T, stream or None)
+    lib._check(rc, "qqkv_dev")
 
 
 def evict(lib: HipLib, w: Weight) -> None:

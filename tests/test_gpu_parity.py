@@ -190,6 +190,43 @@ def test_ffn_and_qkv(gpu, orc):
         assert np.array_equal(o, M.host_qgemm(gpu, w, x))  # evicts w
 
 
+@pytest.mark.parametrize("T", [300, 5])
+@pytest.mark.parametrize("q1,q2", [(M.Q8_0, M.Q8_0), (M.Q4_K, M.Q4_K), (M.Q8_0, M.Q2_K), (M.F32, M.Q4_0)],
+                         ids=lambda q: M.NAMES[q] if isinstance(q, int) else q)
+def test_ffn_dev_matches_two_products(gpu, q1, q2, T):
+    """The fused FFN (first product preparing the second's input in its epilogue)
+    is bit-identical to SiLU product + product; x may alias out."""
+    import torch
+    say("ffn_dev", M.NAMES[q1], M.NAMES[q2], T)
+    k, n1 = 512, 1024
+    w1 = M.DeviceWeight(gpu, M.Weight.make(gpu, q1, gpu.randn(3, 0.02, (n1, k))))
+    w2 = M.DeviceWeight(gpu, M.Weight.make(gpu, q2, gpu.randn(4, 0.02, (k, n1))))
+    x = torch.from_numpy(gpu.randn(5, 1.0, (T, k))).cuda()
+    h = torch.empty((T, n1), dtype=torch.float32, device="cuda")
+    ref = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    w1.gemm(x.data_ptr(), h.data_ptr(), T, act=1)
+    w2.gemm(h.data_ptr(), ref.data_ptr(), T)
+    out = x.clone()
+    torch.cuda.synchronize()
+    M.ffn_dev(gpu, w1, w2, out.data_ptr(), out.data_ptr(), T)
+    torch.cuda.synchronize()
+    a, b = out.cpu().numpy(), ref.cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{int((a != b).sum())} differ"
+    qs = [M.DeviceWeight(gpu, M.Weight.make(gpu, qt, gpu.randn(20 + i, 0.02, (96, k))))
+          for i, qt in enumerate((M.Q8_0, M.Q4_K, M.F32))]
+    ys = [torch.empty((T, 96), dtype=torch.float32, device="cuda") for _ in range(3)]
+    M.qkv_dev(gpu, qs, x.data_ptr(), [y.data_ptr() for y in ys], T)
+    for q, y in zip(qs, ys):
+        r = torch.empty((T, 96), dtype=torch.float32, device="cuda")
+        q.gemm(x.data_ptr(), r.data_ptr(), T)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), r.view(torch.int32)), M.NAMES[q.w.qtype] if hasattr(q, "w") else ""
+        q.close()
+    w1.close()
+    w2.close()
+
+
 class XorShift:
     """The reference self-test's generator (tests/test_qmat.c:13-19)."""
 
