@@ -35,10 +35,13 @@ __device__ __forceinline__ f16v zero16() {
 __device__ __forceinline__ int drow(int e, int hh) { return 8 * (e >> 2) + 4 * hh + (e & 3); }
 
 __device__ __forceinline__ float silu_f(float v) {
-    // the reference's stable sigmoid (src/qmat.h:31-35)
-    if (v >= 0.0f) return v * (1.0f / (1.0f + expf(-v)));
-    const float e = expf(v);
-    return v * (e / (1.0f + e));
+    // x * sigmoid(x) with the reference's stable sigmoid (src/qmat.h:31-35):
+    // exp only of -|x| (never overflows); 1/(1+e) for x >= 0, e/(1+e) below.
+    // Hardware exp2 and reciprocal (~1 ulp each), like the reference's own
+    // -ffast-math build; every kernel applies this same function.
+    const float e = __expf(-fabsf(v));
+    const float r = __builtin_amdgcn_rcpf(1.0f + e);
+    return v * (v >= 0.0f ? r : e * r);
 }
 
 // ---------------------------------------------------------------------------
@@ -52,6 +55,32 @@ struct XChunk {
     float p;           // 2^-sh: the chunk's fold factor for this row
 };
 
+// the chunk shift: sh puts the chunk's largest magnitude in [2^14, 2^15)
+__device__ __forceinline__ int chunk_shift(float amax) {
+    int e = 0;
+    if (amax > 0.0f) (void)frexpf(amax, &e);
+    return amax > 0.0f ? 15 - e : 0;
+}
+
+// the split of NU half-steps' values v[u][j] with shift sh
+template <int NU>
+__device__ __forceinline__ void split_part(const float (&v)[NU][8], int sh, half8 (&h)[NU], half8 (&l)[NU],
+                                           float (&s8)[NU]) {
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float xs = ldexpf(v[u][j], sh);
+            const _Float16 hv = (_Float16)xs;
+            h[u][j] = hv;
+            l[u][j] = (_Float16)(xs - (float)hv);
+            acc += xs;
+        }
+        s8[u] = acc;
+    }
+}
+
 // the split of one chunk's values v[u][j] (element 16u + 8hh + j of row m)
 __device__ __forceinline__ void split_vals(const float (&v)[HSTEPS][8], XChunk &o) {
     float amax = 0.0f;
@@ -60,23 +89,9 @@ __device__ __forceinline__ void split_vals(const float (&v)[HSTEPS][8], XChunk &
 #pragma unroll
         for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[u][j]));
     amax = fmaxf(amax, __shfl_xor(amax, 32));
-    int e = 0;
-    if (amax > 0.0f) (void)frexpf(amax, &e);
-    const int sh = amax > 0.0f ? 15 - e : 0;
+    const int sh = chunk_shift(amax);
     o.p = ldexpf(1.0f, -sh);
-#pragma unroll
-    for (int u = 0; u < HSTEPS; u++) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float xs = ldexpf(v[u][j], sh);
-            const _Float16 h = (_Float16)xs;
-            o.h[u][j] = h;
-            o.l[u][j] = (_Float16)(xs - (float)h);
-            acc += xs;
-        }
-        o.s8[u] = acc;
-    }
+    split_part<HSTEPS>(v, sh, o.h, o.l, o.s8);
 }
 
 __device__ __forceinline__ void split_chunk(const float *__restrict__ x, int M, int K, int m, int c,
@@ -401,10 +416,13 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
     }
     wait_vm<0>();
     if constexpr (EPI == EPI_PREP) {
-        // the 64 x 128 SiLU tile through LDS (row stride 129: conflict-free
-        // column writes and row reads), then one lane per (row, half) splits
-        static_assert(2 * L::BYTES >= 64 * 129 * 4, "LDS tile");
+        // the 64 x 128 SiLU tile through LDS (row stride 132 floats: 16-byte
+        // aligned rows), then wave w splits half-steps 4*(w>>1) .. +3 of row
+        // group w&1; the chunk's row maxima meet in LDS first
+        constexpr int RS = 132;
+        static_assert(2 * L::BYTES >= (64 * RS + 128) * 4, "LDS tile");
         float *T = (float *)&sbuf[0][0];
+        float *amx = T + 64 * RS;  // [2 row groups][2 halves][32 rows]
         const int shw = wshift<QT>(W, 32 * (GC0 + wave) + col);  // (the pad columns hold 0)
         __syncthreads();
 #pragma unroll
@@ -413,30 +431,40 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
             for (int e = 0; e < 16; e++) {
                 float v = total[i][0][e];
                 if constexpr (QT == QT_F32) v = ldexpf(v, -shw);
-                T[(32 * i + drow(e, hh)) * 129 + 32 * wave + col] = silu_f(v);
+                T[(32 * i + drow(e, hh)) * RS + 32 * wave + col] = silu_f(v);
             }
         __syncthreads();
-        if (wave < 2) {
-            const int G = G0 + wave;
-            float v[HSTEPS][8];
+        const int rg = wave & 1, uh = wave >> 1, G = G0 + rg;
+        float v[4][8];
+        float amax = 0.0f;
 #pragma unroll
-            for (int u = 0; u < HSTEPS; u++)
+        for (int u = 0; u < 4; u++) {
+            const float *src = T + (32 * rg + col) * RS + 16 * (4 * uh + u) + 8 * hh;
+            const float4 a0 = *(const float4 *)src, a1 = *(const float4 *)(src + 4);
+            v[u][0] = a0.x; v[u][1] = a0.y; v[u][2] = a0.z; v[u][3] = a0.w;
+            v[u][4] = a1.x; v[u][5] = a1.y; v[u][6] = a1.z; v[u][7] = a1.w;
 #pragma unroll
-                for (int j = 0; j < 8; j++) v[u][j] = T[(32 * wave + col) * 129 + 16 * u + 8 * hh + j];
-            XChunk xc;
-            split_vals(v, xc);
-#pragma unroll
-            for (int u = 0; u < HSTEPS; u++) {
-                uint8_t *o = po.xp + ((((size_t)G * po.Kc + tn) * HSTEPS + u) * 2) * 1024;
-                *(half8 *)(o + lane * 16) = xc.h[u];
-                *(half8 *)(o + (64 + lane) * 16) = xc.l[u];
-                if (po.xsum) {
-                    const float s16 = xc.s8[u] + __shfl_xor(xc.s8[u], 32);
-                    if (hh == 0) po.xs16[((size_t)G * (8 * po.Kc) + 8 * tn + u) * 32 + col] = s16;
-                }
-            }
-            if (hh == 0) po.xpf[((size_t)G * po.Kc + tn) * 32 + col] = xc.p;
+            for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[u][j]));
         }
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        if (hh == 0) amx[(2 * rg + uh) * 32 + col] = amax;
+        __syncthreads();
+        const int sh = chunk_shift(fmaxf(amx[(2 * rg) * 32 + col], amx[(2 * rg + 1) * 32 + col]));
+        half8 xh[4], xl[4];
+        float s8[4];
+        split_part<4>(v, sh, xh, xl, s8);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int uu = 4 * uh + u;
+            uint8_t *o = po.xp + ((((size_t)G * po.Kc + tn) * HSTEPS + uu) * 2) * 1024;
+            *(half8 *)(o + lane * 16) = xh[u];
+            *(half8 *)(o + (64 + lane) * 16) = xl[u];
+            if (po.xsum) {
+                const float s16 = s8[u] + __shfl_xor(s8[u], 32);
+                if (hh == 0) po.xs16[((size_t)G * (8 * po.Kc) + 8 * tn + uu) * 32 + col] = s16;
+            }
+        }
+        if (hh == 0 && uh == 0) po.xpf[((size_t)G * po.Kc + tn) * 32 + col] = ldexpf(1.0f, -sh);
         return;
     }
     const int n = 32 * (GC0 + wave) + col;
