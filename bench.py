@@ -17,7 +17,9 @@ step, in TOPS.
 
 Also reported (not `value`): per-kernel roofline fractions, Q4_K at BASELINE
 config 4's M = 12000 shapes, decoder GEMVs (config 3) in HBM GB/s with >= 512
-MB of rotating weight copies (defeats the 256 MB MALL), the f32-weight GEMM,
+MB of rotating weight copies (defeats the 256 MB MALL), timed as one HIP graph
+of all the launches (kernel_us; call_us = the same launches issued one by one
+from the host), the f32-weight GEMM,
 and the reference CPU path timed on this host (ingot dequant, compiled from
 the reference's sources, + OpenBLAS sgemm, as src/weights.c:103-114 +
 src/backend.c:79 do).
@@ -167,10 +169,32 @@ def run_gemv(B, M_, qt, n, k, Ms, min_bytes=512 << 20, max_copies=512):
             dw.gemm(x.data_ptr(), y.data_ptr(), M, 0, B.sp)
         e1.record(B.stream)
         B.sync()
-        kms = e0.elapsed_time(e1) / copies
+        call_ms = e0.elapsed_time(e1) / copies
+        # the same launches captured once in a HIP graph and replayed: the
+        # GPU-side time per GEMV without the host's launch cost in the way
+        kms = call_ms
+        try:
+            g = torch.cuda.CUDAGraph()
+            cs = torch.cuda.Stream()
+            with torch.cuda.graph(g, stream=cs):
+                for dw in dws:
+                    dw.gemm(x.data_ptr(), y.data_ptr(), M, 0, cs.cuda_stream)
+            with torch.cuda.stream(cs):  # replay on the stream the events mark
+                g.replay()
+                B.sync()
+                e0.record(cs)
+                for _ in range(3):
+                    g.replay()
+                e1.record(cs)
+            B.sync()
+            kms = e0.elapsed_time(e1) / (3 * copies)
+            del g
+        except Exception as ex:  # keep the stream figure
+            log(f"[bench] graph capture failed ({ex}); GEMV time from stream launches")
         nbytes = wb + 4.0 * M * k + 4.0 * M * n
         out.append({"format": M_.NAMES[qt], "M": M, "k": k, "n": n, "copies": copies,
                     "rotated_mb": round(copies * wb / 2**20), "kernel_us": round(kms * 1e3, 2),
+                    "call_us": round(call_ms * 1e3, 2),
                     "kernel_gbps": round(nbytes / (kms * 1e-3) / 1e9, 1),
                     "kernel_hbm_frac": round(nbytes / (kms * 1e-3) / 1e9 / PEAK_HBM, 4)})
     for dw in dws:
@@ -302,7 +326,7 @@ def main():
     achieved = dom_flops / (dom["kernel_us"] * 1e-6) / 1e12
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP16, 4), "traffic": profiled_traffic(),
-                "kernel": f"k_gemm_direct<Q8_0> {dom['gemm']} {dom['k']}->{dom['n']} M={M}"}
+                "kernel": f"k_gemm<Q8_0> {dom['gemm']} {dom['k']}->{dom['n']} M={M}"}
     details = {"encoder_q8_0_m6000": rows}
 
     if not args.no_extras:

@@ -172,7 +172,7 @@ int prep_into(PrepBuf &P, const mynah_asr_hip_weight *W, const float *dx, int T,
     if (i8) {
         e = mh_launch_prep_i8(dx, T, k, Kp, Mpad, xp, xs16, st);
     } else {
-        const int vec = (k % 4 == 0) && (((uintptr_t)dx & 15) == 0);
+        const int vec = (k % 8 == 0) && (((uintptr_t)dx & 15) == 0);
         e = mh_launch_prep(dx, T, k, Kp, Mpad, xp, xs16, xpf, xsum ? 1 : 0, vec, st);
     }
     if (e != hipSuccess) return fail("prep launch failed", hipGetErrorString(e));
@@ -210,7 +210,7 @@ int run_prepped(Ctx *c, const mynah_asr_hip_weight *W, float *dy, int T, int act
 int gemm_dev(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, float *dy, int T, int act,
              hipStream_t st) {
     if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT && mh_use_gemv(W->dw, T)) {
-        const int vec = (W->dw.k % 4 == 0) && (((uintptr_t)dx & 15) == 0);
+        const int vec = (W->dw.k % 8 == 0) && (((uintptr_t)dx & 15) == 0);
         hipError_t e = mh_launch_gemv(W->qtype, W->dw, dx, T, vec, dy, act, st);
         if (e != hipSuccess) return fail("gemv launch failed", hipGetErrorString(e));
         return 0;

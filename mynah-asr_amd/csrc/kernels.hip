@@ -94,16 +94,23 @@ __device__ __forceinline__ void split_vals(const float (&v)[HSTEPS][8], XChunk &
     split_part<HSTEPS>(v, sh, o.h, o.l, o.s8);
 }
 
-__device__ __forceinline__ void split_chunk(const float *__restrict__ x, int M, int K, int m, int c,
-                                            int hh, int vec, XChunk &o) {
+// VEC: K % 8 == 0 and 16-byte aligned rows (each lane's 8 elements are
+// wholly inside or wholly past K), two float4 loads per half-step
+template <bool VEC>
+__device__ __forceinline__ void split_chunk(const float *__restrict__ x, int M, int K, int m, int c, int hh,
+                                            XChunk &o) {
     float v[HSTEPS][8];
     const bool live = m < M;
     const float *row = x + (size_t)(live ? m : 0) * K;
 #pragma unroll
     for (int u = 0; u < HSTEPS; u++) {
         const int k0 = 128 * c + 16 * u + 8 * hh;
-        if (live && vec && k0 + 8 <= K) {
-            const float4 a = *(const float4 *)(row + k0), b = *(const float4 *)(row + k0 + 4);
+        if constexpr (VEC) {
+            float4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
+            if (live && k0 < K) {
+                a = *(const float4 *)(row + k0);
+                b = *(const float4 *)(row + k0 + 4);
+            }
             v[u][0] = a.x; v[u][1] = a.y; v[u][2] = a.z; v[u][3] = a.w;
             v[u][4] = b.x; v[u][5] = b.y; v[u][6] = b.z; v[u][7] = b.w;
         } else {
@@ -489,8 +496,8 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
 // c = w, w+NW, ...; the chunk results of rows 0..15 and their fold factors
 // meet in LDS and are folded in chunk order from zero — the sequence k_gemm
 // runs in registers.
-template <int QT, int NW, int WNG>
-__global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const float *__restrict__ x, int M, int vec,
+template <int QT, int NW, int WNG, bool VEC>
+__global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const float *__restrict__ x, int M,
                                                   float *__restrict__ y, int act) {
     extern __shared__ float part[];  // [Kc][WNG][8][64] chunk results, then pf [Kc][16]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -506,8 +513,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const float *__restric
         BK<QT, WNG> bk[KSTEPS];
 #pragma unroll
         for (int s = 0; s < KSTEPS; s++) load_bk<QT, WNG>(W, Kc, gn, c, s, lane, bk[s]);
+        // the weight loads go out first: their latency overlaps the x split
+        __builtin_amdgcn_sched_barrier(0);
         XChunk xc;
-        split_chunk(x, M, W.k, col, c, hh, vec, xc);
+        split_chunk<VEC>(x, M, W.k, col, c, hh, xc);
         if (hh == 0 && col < 16) pf[c * 16 + col] = xc.p;
         f16v acc[1][WNG];
 #pragma unroll
@@ -562,15 +571,16 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const float *__restric
 //   xp   A fragments of (xh, xl), zero beyond M and K   [G][chunk][u][term][64][16 B]
 //   xs16 per row and 16-element sub-block: (first 8 in order) + (next 8)
 //   xpf  per row group, chunk and row: the fold factor 2^-sh  [G][chunk][32]
+template <bool VEC>
 __global__ __launch_bounds__(256) void k_prep(const float *__restrict__ x, int M, int K, int Kp,
                                               uint8_t *__restrict__ xp, float *__restrict__ xs16,
-                                              float *__restrict__ xpf, int want_xsum, int vec) {
+                                              float *__restrict__ xpf, int want_xsum) {
     const int G = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 31, hh = lane >> 5, m = 32 * G + r;
     const int Kc = Kp / 128;
     for (int c = wave; c < Kc; c += 4) {
         XChunk xc;
-        split_chunk(x, M, K, m, c, hh, vec, xc);
+        split_chunk<VEC>(x, M, K, m, c, hh, xc);
 #pragma unroll
         for (int u = 0; u < HSTEPS; u++) {
             const size_t off = ((((size_t)G * Kc + c) * HSTEPS + u) * 2) * 64 * 16;
@@ -775,20 +785,25 @@ __global__ void k_silu(float *__restrict__ x, size_t n) {
 
 #include "launch.h"
 
-template <int QT, int NW, int WNG>
-static hipError_t launch_gemv(const DevW &W, const float *x, int M, int vec, float *y, int act,
-                              hipStream_t st) {
+template <int QT, int NW, int WNG, bool VEC>
+static hipError_t launch_gemv1(const DevW &W, const float *x, int M, float *y, int act, hipStream_t st) {
     const int Kc = W.Kp / 128;
     const size_t lds = ((size_t)Kc * WNG * 8 * 64 + (size_t)Kc * 16) * sizeof(float);
     static bool attr = false;  // allow dynamic LDS beyond 64 KiB (gfx950 has 160 KiB)
     if (!attr) {
-        (void)hipFuncSetAttribute((const void *)k_gemv<QT, NW, WNG>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        (void)hipFuncSetAttribute((const void *)k_gemv<QT, NW, WNG, VEC>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   160 * 1024);
         attr = true;
     }
-    hipLaunchKernelGGL((k_gemv<QT, NW, WNG>), dim3(W.Np / 32 / WNG), dim3(NW * 64), lds, st, W, x, M, vec,
-                       y, act);
+    hipLaunchKernelGGL((k_gemv<QT, NW, WNG, VEC>), dim3(W.Np / 32 / WNG), dim3(NW * 64), lds, st, W, x, M, y, act);
     return hipGetLastError();
+}
+
+template <int QT, int NW, int WNG>
+static hipError_t launch_gemv(const DevW &W, const float *x, int M, int vec, float *y, int act,
+                              hipStream_t st) {
+    if (vec) return launch_gemv1<QT, NW, WNG, true>(W, x, M, y, act, st);
+    return launch_gemv1<QT, NW, WNG, false>(W, x, M, y, act, st);
 }
 
 // column groups per GEMV workgroup: two for wide outputs, so that each chunk
@@ -864,8 +879,10 @@ hipError_t mh_launch_gemm_prep_out(int qtype, const DevW &W, const uint8_t *xp, 
 
 hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,
                           float *xpf, int want_xsum, int vec, hipStream_t st) {
-    hipLaunchKernelGGL(k_prep, dim3(Mpad / 32), dim3(256), 0, st, x, M, K, Kp, xp, xs16, xpf,
-                       want_xsum, vec);
+    if (vec)
+        hipLaunchKernelGGL(k_prep<true>, dim3(Mpad / 32), dim3(256), 0, st, x, M, K, Kp, xp, xs16, xpf, want_xsum);
+    else
+        hipLaunchKernelGGL(k_prep<false>, dim3(Mpad / 32), dim3(256), 0, st, x, M, K, Kp, xp, xs16, xpf, want_xsum);
     return hipGetLastError();
 }
 
