@@ -240,29 +240,34 @@ __device__ __forceinline__ f16v load_rows16(const float *b) {
 // Global -> LDS copies (global_load_lds: no VGPRs; the LDS destination is
 // wave-uniform, lane l writes bytes [l*size, (l+1)*size) of each piece).
 typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) const void glob_void;
 
+// src is wave-uniform: the address is an SGPR base + the lane's 32-bit offset
+// (+ an immediate), so the copies need no per-lane 64-bit address math
 template <int BYTES>
 __device__ __forceinline__ void dma(const uint8_t *src, uint8_t *dst, int lane) {
+    const glob_void *g = (const glob_void *)src;
     if constexpr (BYTES == 0) {
         return;
     } else if constexpr (BYTES % 1024 == 0) {
 #pragma unroll
         for (int k = 0; k < BYTES / 1024; k++)
-            __builtin_amdgcn_global_load_lds((const void *)(src + k * 1024 + lane * 16), (lds_void *)(dst + k * 1024),
-                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const glob_void *)((const __attribute__((address_space(1))) uint8_t *)g +
+                                                                 k * 1024 + (uint32_t)lane * 16u),
+                                             (lds_void *)(dst + k * 1024), 16, 0, 0);
     } else if constexpr (BYTES % 256 == 0) {
 #pragma unroll
         for (int k = 0; k < BYTES / 256; k++)
-            __builtin_amdgcn_global_load_lds((const void *)(src + k * 256 + lane * 4), (lds_void *)(dst + k * 256), 4,
-                                             0, 0);
+            __builtin_amdgcn_global_load_lds((const glob_void *)((const __attribute__((address_space(1))) uint8_t *)g +
+                                                                 k * 256 + (uint32_t)lane * 4u),
+                                             (lds_void *)(dst + k * 256), 4, 0, 0);
     } else {
         static_assert(BYTES == 128, "staged region size");
-        if (lane < 32) __builtin_amdgcn_global_load_lds((const void *)(src + lane * 4), (lds_void *)dst, 4, 0, 0);
+        if (lane < 32)
+            __builtin_amdgcn_global_load_lds((const glob_void *)((const __attribute__((address_space(1))) uint8_t *)g +
+                                                                 (uint32_t)lane * 4u),
+                                             (lds_void *)dst, 4, 0, 0);
     }
-}
-// number of copy instructions dma<BYTES> issues (each counts once in vmcnt)
-template <int BYTES> constexpr int dma_n() {
-    return BYTES == 0 ? 0 : (BYTES % 1024 == 0 ? BYTES / 1024 : (BYTES % 256 == 0 ? BYTES / 256 : 1));
 }
 
 // the lane's 16 D-layout rows from a staged [32]-row float vector
@@ -296,20 +301,9 @@ template <int QT> struct StageLayout {
     static constexpr int BYTES = XS + (F::MINS ? 2 * 512 : 0);
 };
 
-// ---------------------------------------------------------------------------
-// Large-M GEMM. Workgroup = 4 waves side by side over N, tile 64 x 128: row
-// groups G0, G0+1 and column groups GC0..GC0+3; wave w computes both row
-// groups against column group GC0+w (2 x 1 tiles of 32x32).
-// Everything the MFMAs read goes through LDS in half-chunk stages,
-// double-buffered: the stage for ksteps k+2, k+3 lands while ksteps k, k+1
-// compute. The copies are global_load_lds (no VGPRs hold prefetched data),
-// shared out so that wave w brings its own column group's plane bytes and
-// headers and a quarter of the activation pieces. ~50 KiB of LDS and <= 168
-// VGPRs per wave let three workgroups share a CU: their waves fill each
-// other's stalls and overlap one's VALU epilogue with another's MFMAs.
-// grid = tilesM * tilesN workgroups.
-// workgroups per CU the register budget is sized for: the K-quants (affine
-// sums, sub-block factors) and the f32 pairs need more registers per wave
+// workgroups per CU the register budget is sized for: as many as the LDS
+// ring allows, fewer for the K-quants (affine sums, sub-block factors) and
+// the f32 pairs, which need more registers per wave
 template <int QT> constexpr int gemm_occ() {
     return (QT == QT_F32 || Fmt<QT>::MINS || Fmt<QT>::SUB16) ? 2 : 3;
 }
@@ -319,7 +313,7 @@ template <int QT> constexpr int gemm_occ() {
 // storing the f32 intermediate, prepares it as the second product's input —
 // the workgroup's 128 output columns are exactly one 128-element chunk of
 // the second product's K, so the chunk's shift, split and sums are formed
-// here by split_vals, the same function the preparation pass runs, on the
+// here by split_part, the same function the preparation pass runs, on the
 // same f32 values (bit-identical to storing y and preparing it).
 enum { EPI_Y = 0, EPI_PREP = 1 };
 struct PrepOut {
@@ -328,6 +322,19 @@ struct PrepOut {
     int Kc, xsum;
 };
 
+// ---------------------------------------------------------------------------
+// Large-M GEMM. Workgroup = 4 waves side by side over N, tile 64 x 128: row
+// groups G0, G0+1 and column groups GC0..GC0+3; wave w computes both row
+// groups against column group GC0+w (2 x 1 tiles of 32x32).
+// Everything the MFMAs read goes through LDS in half-chunk stages,
+// double-buffered: the next half's stage lands while the current one
+// computes (a ring of three, two halves of lead, fits only twice per CU and
+// measured 10-15% slower: occupancy hides the copy latency better). The copies are global_load_lds (no VGPRs hold prefetched data),
+// shared out so that wave w brings its own column group's plane bytes and
+// headers and a quarter of the activation pieces. Small LDS and VGPR
+// footprints let two or three workgroups share a CU: their waves fill each
+// other's stalls and overlap one's VALU epilogue with another's MFMAs.
+// grid = tilesM * tilesN workgroups.
 template <int QT, int EPI>
 __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint8_t *__restrict__ xp,
                                                  const float *__restrict__ xs16,
