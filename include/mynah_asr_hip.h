@@ -158,6 +158,24 @@ int mynah_asr_hip_qqkv_dev(const mynah_asr_hip_weight *wq, const mynah_asr_hip_w
 /* dwd[n,k] = dequantized weight. */
 int mynah_asr_hip_dequant_dev(const mynah_asr_hip_weight *w, float *dwd, void *stream);
 
+/* Relative-position self-attention core of one encoder layer on device buffers:
+ * the computation of src/encoder.c:315-410 (left < 0, full attention) and
+ * src/encoder.c:220-313 (left >= 0, chunked-limited attention with chunk =
+ * right + 1) from the point where q, k, v carry their biases and
+ * rk = pe . relk_w^T (encoder.c:336, 233) has been formed:
+ *   ctx[t, h] = sum_j softmax_j(((q[t,h] + bias_u[h]) . k[j,h]
+ *                               + (q[t,h] + bias_v[h]) . rk[T-1+j-t, h]) / sqrt(dk)) v[j,h]
+ * q, k, v, ctx: nseq segments of [T, d] floats each (row stride d, segment
+ * stride T*d); rk: [2T-1, d], shared by the segments; bias_u, bias_v: [d]
+ * (head h at columns h*dk .. h*dk+dk-1, dk = d / H, 64 or 128). nseq > 1 runs
+ * independent equal-length segments in one launch (the reference calls the
+ * layer once per segment). All pointers 16-byte aligned. ctx may not alias
+ * q, k or v. Outputs are f32 sums in another order than the reference's BLAS:
+ * equal within |y - ref| <= 1e-4*|ref| + 1e-5*max|v|. */
+int mynah_asr_hip_relpos_attention_dev(const float *q, const float *k, const float *v, const float *rk,
+                                       const float *bias_u, const float *bias_v, float *ctx, int T, int d,
+                                       int H, int left, int right, int nseq, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

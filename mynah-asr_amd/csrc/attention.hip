@@ -1,0 +1,297 @@
+// attention.hip — the relative-position self-attention core of the FastConformer
+// encoder layer (the reference's src/encoder.c:315-410 for full attention and
+// its banded twin encoder.c:220-313 for chunked-limited attention), on fp32
+// MFMA (v_mfma_f32_16x16x4_f32) for gfx950.
+//
+// Per head h (columns h*DK .. h*DK+DK-1 of the [T, d] buffers):
+//   s[t, j] = ((q[t] + bias_u) . k[j] + (q[t] + bias_v) . rk[T-1 + j - t]) / sqrt(DK)
+//   ctx[t]  = sum_j softmax_j(s[t, j]) v[j],  j over the row's window
+// rk = pe . relk_w^T is [2T-1, d] (the pos projection's output, shared by the
+// segments of one call). The window is all of [0, T) for left < 0, else
+// chunked-limited: chunk = right + 1, lc = left / chunk, row t (chunk t/chunk)
+// sees [(t/chunk - lc) * chunk, (t/chunk + 1) * chunk) clipped to [0, T)
+// (encoder.c:373-381).
+//
+// One workgroup = 4 waves = 64 query rows of one head of one segment; wave w
+// owns rows t0 + 16w .. +15. Keys are visited in tiles of 32 (only the tiles
+// the block's rows can see); each tile's K, V and the 95 rk rows its
+// 64 x 32 (row, key) pairs touch are staged in LDS, and every wave
+//   1. forms the content scores (16 x 32) with its (q + bias_u) held in registers,
+//   2. forms the position scores of its 16 rows against the 47 rk rows of its
+//      band (16 x 48) with (q + bias_v) in registers,
+//   3. applies the rel-shift through a per-wave LDS scratch (row i, key jj
+//      reads band column jj - i + 15),
+//   4. runs an online softmax (running row max and sum, base-2 exponentials of
+//      scores pre-scaled by log2(e)/sqrt(DK)), and
+//   5. multiplies the probabilities (re-laid out as an MFMA A operand through
+//      LDS) by the V tile into its 16 x DK context accumulator.
+// fp32 products and sums throughout: the result is the reference's f32
+// computation up to summation order and the exponential's rounding.
+//
+// MFMA 16x16x4 f32 operand layout (lane l, c = l & 15, g = l >> 4):
+//   A: row c, k-slot g;  B: column c, k-slot g;  D: rows 4g + e (e = 0..3), column c.
+// The reduction index of the score products is permuted so each lane reads a
+// contiguous run: step s, slot g carries feature NS*g + s (NS = DK / 4).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "launch.h"
+
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+constexpr int RB = 64;           // query rows per workgroup
+constexpr int KT = 32;           // keys per tile
+constexpr int NB = RB + KT;      // rk rows staged per tile (the tile touches RB + KT - 1)
+
+template <int DK>
+struct AttnLds {
+    static constexpr int KS = DK + 4;   // K / rk row stride (16-byte rows, conflict-free b128 reads)
+    static constexpr int VS = DK + 2;   // V row stride: the four k-slots of a B read land on disjoint banks
+    static constexpr int BS = 53;       // band scratch row stride
+    static constexpr int PS = 36;       // probability scratch row stride
+    static constexpr int K0 = 0;
+    static constexpr int V0 = K0 + KT * KS;
+    static constexpr int R0 = V0 + KT * VS;
+    static constexpr int W0 = R0 + NB * KS;
+    static constexpr int WB = 16 * BS;
+    static constexpr int WSZ = WB + 16 * PS;
+    static constexpr int TOTAL = W0 + 4 * WSZ;   // floats
+};
+
+__device__ __forceinline__ f4 mfma16(float a, float b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float max16(float x) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+
+__device__ __forceinline__ float sum16(float x) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+
+// Compiler-level ordering of a wave's own LDS writes and reads (the LDS
+// executes one wave's operations in issue order).
+__device__ __forceinline__ void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+struct Window {
+    int lim, chunk, lc, T;
+    __device__ int j0(int t) const { return lim ? max((t / chunk - lc) * chunk, 0) : 0; }
+    __device__ int j1(int t) const { return lim ? min((t / chunk + 1) * chunk, T) : T; }
+};
+
+template <int DK>
+__global__ __launch_bounds__(256, 1) void k_relpos_attn(const float *__restrict__ q, const float *__restrict__ k,
+                                                        const float *__restrict__ v, const float *__restrict__ rk,
+                                                        const float *__restrict__ bu, const float *__restrict__ bv,
+                                                        float *__restrict__ ctx, int T, int d, int left, int right,
+                                                        float kscale) {
+    using L = AttnLds<DK>;
+    constexpr int NS = DK / 4;    // reduction steps of a score product
+    constexpr int NT = DK / 16;   // context column tiles
+    extern __shared__ float lds[];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    const int ho = blockIdx.y * DK;
+    const size_t so = (size_t)blockIdx.z * (size_t)T * (size_t)d;
+    q += so;
+    k += so;
+    v += so;
+    ctx += so;
+    const int t0 = blockIdx.x * RB, tw = t0 + 16 * w;
+    Window win;
+    win.lim = left >= 0;
+    win.chunk = win.lim ? right + 1 : 1;
+    win.lc = win.lim ? left / win.chunk : 0;
+    win.T = T;
+    const int ja = win.j0(t0), jb = win.j1(min(t0 + RB - 1, T - 1));
+
+    // (q + bias_u), (q + bias_v) of query row tw + c, features NS*g .. NS*g + NS-1
+    float qa[NS], qb[NS];
+    {
+        const int t = tw + c;
+        const int f = ho + NS * g;
+#pragma unroll
+        for (int i = 0; i < NS / 4; i++) {
+            f4 x = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
+            if (t < T) {
+                x = *(const f4 *)(q + (size_t)t * d + f + 4 * i);
+                u = x + *(const f4 *)(bu + f + 4 * i);
+                b = x + *(const f4 *)(bv + f + 4 * i);
+            }
+            qa[4 * i + 0] = u.x; qa[4 * i + 1] = u.y; qa[4 * i + 2] = u.z; qa[4 * i + 3] = u.w;
+            qb[4 * i + 0] = b.x; qb[4 * i + 1] = b.y; qb[4 * i + 2] = b.z; qb[4 * i + 3] = b.w;
+        }
+    }
+    // this lane's output rows tw + 4g + e and their windows
+    int rj0[4], rj1[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int t = min(tw + 4 * g + e, T - 1);
+        rj0[e] = win.j0(t);
+        rj1[e] = win.j1(t);
+    }
+    float m[4], l[4];
+    f4 acc[NT];
+#pragma unroll
+    for (int e = 0; e < 4; e++) m[e] = -1e30f, l[e] = 0.f;
+#pragma unroll
+    for (int n = 0; n < NT; n++) acc[n] = f4{0.f, 0.f, 0.f, 0.f};
+
+    float *Ks = lds + L::K0, *Vs = lds + L::V0, *Rs = lds + L::R0;
+    float *Bw = lds + L::W0 + w * L::WSZ, *Pw = Bw + L::WB;
+    const int P = 2 * T - 1;
+
+    for (int jt = ja; jt < jb; jt += KT) {
+        __syncthreads();   // every wave is done with the previous tile
+        for (int i = tid; i < KT * DK / 4; i += 256) {
+            const int r = i / (DK / 4), cc = 4 * (i % (DK / 4));
+            const int j = jt + r;
+            f4 xk = {0.f, 0.f, 0.f, 0.f}, xv = {0.f, 0.f, 0.f, 0.f};
+            if (j < T) {
+                xk = *(const f4 *)(k + (size_t)j * d + ho + cc);
+                xv = *(const f4 *)(v + (size_t)j * d + ho + cc);
+            }
+            *(f4 *)(Ks + r * L::KS + cc) = xk;
+            *(f2 *)(Vs + r * L::VS + cc) = f2{xv.x, xv.y};
+            *(f2 *)(Vs + r * L::VS + cc + 2) = f2{xv.z, xv.w};
+        }
+        const int pbase = T - 1 + jt - t0 - (RB - 1);
+        for (int i = tid; i < NB * DK / 4; i += 256) {
+            const int r = i / (DK / 4), cc = 4 * (i % (DK / 4));
+            const int p = pbase + r;
+            f4 x = {0.f, 0.f, 0.f, 0.f};
+            if (p >= 0 && p < P) x = *(const f4 *)(rk + (size_t)p * d + ho + cc);
+            *(f4 *)(Rs + r * L::KS + cc) = x;
+        }
+        __syncthreads();
+
+        // 1. content scores: 16 rows x 32 keys
+        f4 s[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        // 2. position scores against band rows prow .. prow + 47 (p = pbase + prow + col)
+        f4 bd[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        const int prow = (RB - 16) - 16 * w;
+#pragma unroll
+        for (int i = 0; i < NS / 4; i++) {
+#pragma unroll
+            for (int n = 0; n < 2; n++) {
+                const f4 kb = *(const f4 *)(Ks + (16 * n + c) * L::KS + NS * g + 4 * i);
+                s[n] = mfma16(qa[4 * i + 0], kb.x, s[n]);
+                s[n] = mfma16(qa[4 * i + 1], kb.y, s[n]);
+                s[n] = mfma16(qa[4 * i + 2], kb.z, s[n]);
+                s[n] = mfma16(qa[4 * i + 3], kb.w, s[n]);
+            }
+#pragma unroll
+            for (int n = 0; n < 3; n++) {
+                const f4 rb = *(const f4 *)(Rs + (prow + 16 * n + c) * L::KS + NS * g + 4 * i);
+                bd[n] = mfma16(qb[4 * i + 0], rb.x, bd[n]);
+                bd[n] = mfma16(qb[4 * i + 1], rb.y, bd[n]);
+                bd[n] = mfma16(qb[4 * i + 2], rb.z, bd[n]);
+                bd[n] = mfma16(qb[4 * i + 3], rb.w, bd[n]);
+            }
+        }
+        // 3. rel-shift: row i = 4g + e, key jj = 16n + c takes band column jj - i + 15
+        //    (p = T-1 + jt + jj - (tw + i) = pbase + prow + (jj - i + 15))
+#pragma unroll
+        for (int n = 0; n < 3; n++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) Bw[(4 * g + e) * L::BS + 16 * n + c] = bd[n][e];
+        wave_lds_order();
+        float sv[2][4];
+#pragma unroll
+        for (int n = 0; n < 2; n++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int i = 4 * g + e, j = jt + 16 * n + c;
+                const float x = (s[n][e] + Bw[i * L::BS + 16 * n + c - i + 15]) * kscale;
+                sv[n][e] = (j >= rj0[e] && j < rj1[e]) ? x : -INFINITY;
+            }
+        // 4. online softmax over the tile
+        float alpha[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float mx = max16(fmaxf(sv[0][e], sv[1][e]));
+            const float mn = fmaxf(m[e], mx);
+            alpha[e] = exp2f(m[e] - mn);
+            m[e] = mn;
+            sv[0][e] = exp2f(sv[0][e] - mn);
+            sv[1][e] = exp2f(sv[1][e] - mn);
+            l[e] = l[e] * alpha[e] + sum16(sv[0][e] + sv[1][e]);
+        }
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[n][e] *= alpha[e];
+        // 5. probabilities to the A layout (row c, keys 8g .. 8g+7), then P . V
+#pragma unroll
+        for (int n = 0; n < 2; n++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) Pw[(4 * g + e) * L::PS + 16 * n + c] = sv[n][e];
+        wave_lds_order();
+        const f4 pa0 = *(const f4 *)(Pw + c * L::PS + 8 * g);
+        const f4 pa1 = *(const f4 *)(Pw + c * L::PS + 8 * g + 4);
+        const float pa[8] = {pa0.x, pa0.y, pa0.z, pa0.w, pa1.x, pa1.y, pa1.z, pa1.w};
+#pragma unroll
+        for (int sidx = 0; sidx < 8; sidx++) {
+            const float *vr = Vs + (8 * g + sidx) * L::VS + c;
+#pragma unroll
+            for (int n = 0; n < NT; n++) acc[n] = mfma16(pa[sidx], vr[16 * n], acc[n]);
+        }
+    }
+
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int t = tw + 4 * g + e;
+        if (t < T) {
+            const float inv = 1.0f / l[e];
+            float *o = ctx + (size_t)t * d + ho + c;
+#pragma unroll
+            for (int n = 0; n < NT; n++) o[16 * n] = acc[n][e] * inv;
+        }
+    }
+}
+
+template <int DK>
+hipError_t launch_attn(const float *q, const float *k, const float *v, const float *rk, const float *bu,
+                       const float *bv, float *ctx, int T, int d, int H, int left, int right, int nseq,
+                       hipStream_t st) {
+    const size_t bytes = sizeof(float) * AttnLds<DK>::TOTAL;
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_relpos_attn<DK>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    // exponentials are base 2: scores carry log2(e) / sqrt(DK)
+    const float kscale = (1.0f / sqrtf((float)DK)) * 1.4426950408889634f;
+    dim3 grid((T + RB - 1) / RB, H, nseq);
+    hipLaunchKernelGGL(k_relpos_attn<DK>, grid, dim3(256), bytes, st, q, k, v, rk, bu, bv, ctx, T, d, left,
+                       right, kscale);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool mh_attn_supported(int dk) { return dk == 64 || dk == 128; }
+
+hipError_t mh_launch_relpos_attn(const float *q, const float *k, const float *v, const float *rk,
+                                 const float *bias_u, const float *bias_v, float *ctx, int T, int d, int H,
+                                 int left, int right, int nseq, hipStream_t st) {
+    const int dk = d / H;
+    if (dk == 128) return launch_attn<128>(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, st);
+    if (dk == 64) return launch_attn<64>(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, st);
+    return hipErrorInvalidValue;
+}

@@ -403,6 +403,27 @@ int mynah_asr_hip_dequant_dev(const mynah_asr_hip_weight *w, float *dwd, void *s
     return 0;
 }
 
+int mynah_asr_hip_relpos_attention_dev(const float *q, const float *k, const float *v, const float *rk,
+                                       const float *bias_u, const float *bias_v, float *ctx, int T, int d,
+                                       int H, int left, int right, int nseq, void *stream) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    if (!q || !k || !v || !rk || !bias_u || !bias_v || !ctx || T < 0 || nseq < 0 || H <= 0 || d <= 0 ||
+        d % H != 0)
+        return fail("bad argument");
+    if (!mh_attn_supported(d / H)) return fail("head size must be 64 or 128");
+    if (left >= 0 && right < 0) return fail("chunked attention needs right >= 0");
+    const void *ptrs[7] = {q, k, v, rk, bias_u, bias_v, ctx};
+    for (const void *p : ptrs)
+        if ((uintptr_t)p % 16) return fail("attention buffers must be 16-byte aligned");
+    if (ctx == q || ctx == k || ctx == v) return fail("ctx may not alias q, k or v");
+    if (T == 0 || nseq == 0) return 0;
+    hipError_t e = mh_launch_relpos_attn(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq,
+                                         pick_stream(stream));
+    if (e != hipSuccess) return fail("attention launch failed", hipGetErrorString(e));
+    return 0;
+}
+
 int mynah_asr_hip_qgemm(const mynah_asr_hip_wdesc *w, const float *x, float *out, int T) {
     Ctx *c;
     if (begin(&c)) return -1;

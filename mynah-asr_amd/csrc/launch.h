@@ -33,3 +33,9 @@ hipError_t mh_launch_prep_i8(const float *x, int M, int K, int Kp, int Mpad, uin
                              hipStream_t st);
 hipError_t mh_launch_gemm_i8(int qtype, const DevW &W, const uint8_t *qx, const float *sx, float *y, int M,
                              int act, hipStream_t st);
+
+// Relative-position self-attention core (attention.hip): head size d / H of 64 or 128
+bool mh_attn_supported(int dk);
+hipError_t mh_launch_relpos_attn(const float *q, const float *k, const float *v, const float *rk,
+                                 const float *bias_u, const float *bias_v, float *ctx, int T, int d, int H,
+                                 int left, int right, int nseq, hipStream_t st);

@@ -37,6 +37,7 @@ HIP_SYMBOLS = [
     "mynah_asr_hip_weight_create", "mynah_asr_hip_weight_destroy", "mynah_asr_hip_weight_bytes",
     "mynah_asr_hip_qgemm_dev", "mynah_asr_hip_dequant_dev", "mynah_asr_hip_prep_dev",
     "mynah_asr_hip_qgemm_prepped_dev", "mynah_asr_hip_qffn_dev", "mynah_asr_hip_qqkv_dev",
+    "mynah_asr_hip_relpos_attention_dev",
 ]
 HOST_SYMBOLS = [
     "mynah_asr_set_backend", "mynah_asr_backend", "mynah_asr_gemm_wt", "mynah_asr_silu",
@@ -99,6 +100,8 @@ class HipLib:
         if hasattr(L, "mynah_asr_hip_qffn_dev"):
             L.mynah_asr_hip_qffn_dev.argtypes = [_P, _P, _P, _P, C.c_int, _P]
             L.mynah_asr_hip_qqkv_dev.argtypes = [_P, _P, _P, _P, _P, _P, _P, C.c_int, _P]
+        if hasattr(L, "mynah_asr_hip_relpos_attention_dev"):
+            L.mynah_asr_hip_relpos_attention_dev.argtypes = [_P] * 7 + [C.c_int] * 6 + [_P]
         L.mynah_asr_hip_qgemm.argtypes = [C.POINTER(WDesc), _P, _P, C.c_int]
         L.mynah_asr_hip_qffn.argtypes = [C.POINTER(WDesc), C.POINTER(WDesc), _P, _P, C.c_int]
         L.mynah_asr_hip_qqkv.argtypes = [C.POINTER(WDesc)] * 3 + [_P] * 4 + [C.c_int]
@@ -241,6 +244,15 @@ def qkv_dev(lib, ws, dx_ptr: int, dys, T: int, stream: int = 0):
     """Three products of one input, prepared once (mynah_asr_hip_qqkv_dev)."""
     rc = lib.L.mynah_asr_hip_qqkv_dev(ws[0].h, ws[1].h, ws[2].h, dx_ptr, dys[0], dys[1], dys[2], T, stream or None)
     lib._check(rc, "qqkv_dev")
+
+
+def relpos_attention_dev(lib, q, k, v, rk, bias_u, bias_v, ctx, T: int, d: int, H: int,
+                        left: int = -1, right: int = 0, nseq: int = 1, stream: int = 0):
+    """Relative-position attention core on device pointers
+    (mynah_asr_hip_relpos_attention_dev; src/encoder.c:315-410, 220-313)."""
+    rc = lib.L.mynah_asr_hip_relpos_attention_dev(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right,
+                                                 nseq, stream or None)
+    lib._check(rc, "relpos_attention_dev")
 
 
 def evict(lib: HipLib, w: Weight) -> None:

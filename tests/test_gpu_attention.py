@@ -1,0 +1,104 @@
+"""GPU parity of the relative-position attention core
+(mynah_asr_hip_relpos_attention_dev) against the oracle's float64 restatement
+of src/encoder.c:315-410 (full) and :220-313 (chunked-limited).
+
+Bar: |ctx - ref| <= 1e-4*|ref| + 1e-5*max|v| per element. The kernel computes
+in f32 like the reference, with another summation order and base-2
+exponentials, so a context element near zero (a cancelling weighted sum of v)
+carries an absolute error of order 1e-6 * max|v| — the scale term covers that.
+Inputs: q, k, v, rk N(0, 1) and bias_u, bias_v N(0, 0.1), seeded.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import mynah_hip as M
+from attention import relpos_attention
+
+pytestmark = pytest.mark.gpu
+RTOL, VTOL = 1e-4, 1e-5
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def make(seed, T, d, nseq=1):
+    r = np.random.default_rng(seed)
+    f = lambda *s, sc=1.0: (r.standard_normal(s) * sc).astype(np.float32)
+    return (f(nseq, T, d), f(nseq, T, d), f(nseq, T, d), f(2 * T - 1, d), f(d, sc=0.1), f(d, sc=0.1))
+
+
+def run_gpu(gpu, arrs, T, d, H, left, right, nseq):
+    import torch
+    q, k, v, rk, bu, bv = (torch.from_numpy(a).cuda() for a in arrs)
+    ctx = torch.full((nseq, T, d), float("nan"), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    M.relpos_attention_dev(gpu, q.data_ptr(), k.data_ptr(), v.data_ptr(), rk.data_ptr(), bu.data_ptr(),
+                           bv.data_ptr(), ctx.data_ptr(), T, d, H, left, right, nseq)
+    torch.cuda.synchronize()
+    return ctx.cpu().numpy()
+
+
+def check(out, arrs, H, left, right):
+    q, k, v, rk, bu, bv = arrs
+    for s in range(q.shape[0]):
+        ref = relpos_attention(q[s], k[s], v[s], rk, bu, bv, H, left, right)
+        err = np.abs(out[s] - ref)
+        lim = RTOL * np.abs(ref) + VTOL * np.abs(v[s]).max()
+        assert np.isfinite(out[s]).all()
+        assert (err <= lim).all(), (f"seg {s}: {int((err > lim).sum())} outside, max err {err.max():.3g}, "
+                                    f"worst ratio {(err / lim).max():.3g}")
+
+
+@pytest.mark.parametrize("T,d,H,left,right,nseq", [
+    (1, 128, 2, -1, 0, 1),        # one frame
+    (37, 128, 2, -1, 0, 1),       # dk 64, ragged tiles
+    (64, 256, 2, -1, 0, 1),       # dk 128, one exact row block
+    (65, 256, 2, -1, 0, 2),       # one row past a block, two segments
+    (130, 256, 2, 32, 7, 1),      # chunked: chunk 8, 4 chunks of left context
+    (130, 256, 2, 4, 3, 3),       # chunked: chunk 4, one chunk of left context
+    (200, 512, 4, 0, 0, 1),       # chunk 1, no left context: each row sees itself only
+    (300, 256, 4, 70, 13, 1),     # chunk 14, lc 5, T not a multiple of the chunk
+    (300, 512, 4, 1000, 299, 1),  # one chunk covering all rows: equals full attention
+])
+def test_relpos_attention_matches_oracle(gpu, T, d, H, left, right, nseq):
+    say("attention", T, d, H, left, right, nseq)
+    arrs = make(T * 7 + d, T, d, nseq)
+    out = run_gpu(gpu, arrs, T, d, H, left, right, nseq)
+    check(out, arrs, H, left, right)
+
+
+def test_relpos_attention_fastconformer_segment(gpu):
+    """FastConformer-0.6B: d_model 1024, 8 heads (dk 128), one 750-frame
+    segment, full attention and the streaming chunked-limited window."""
+    T, d, H = 750, 1024, 8
+    arrs = make(11, T, d, 2)
+    for left, right in ((-1, 0), (70, 13)):
+        say("attention fastconformer", T, left, right)
+        out = run_gpu(gpu, arrs, T, d, H, left, right, 2)
+        check(out, arrs, H, left, right)
+
+
+def test_relpos_attention_segments_independent(gpu):
+    """A segment's context does not depend on the other segments of the call
+    (bit-identical to running it alone)."""
+    T, d, H = 97, 256, 2
+    arrs = make(5, T, d, 3)
+    both = run_gpu(gpu, arrs, T, d, H, -1, 0, 3)
+    one = run_gpu(gpu, tuple(a[1:2] if a.ndim == 3 else a for a in arrs), T, d, H, -1, 0, 1)
+    assert np.array_equal(both[1].view(np.uint32), one[0].view(np.uint32))
+
+
+def test_relpos_attention_rejects_bad_arguments(gpu):
+    import torch
+    x = torch.zeros((4, 192), dtype=torch.float32, device="cuda")
+    p = x.data_ptr()
+    with pytest.raises(RuntimeError, match="head size"):
+        M.relpos_attention_dev(gpu, p, p, p, p, p, p, x[1:].data_ptr(), 1, 192, 2)   # dk 96
+    with pytest.raises(RuntimeError, match="right"):
+        M.relpos_attention_dev(gpu, p, p, p, p, p, p, x[1:].data_ptr(), 1, 128, 2, 4, -1)
+    with pytest.raises(RuntimeError, match="alias"):
+        M.relpos_attention_dev(gpu, p, p, p, p, p, p, p, 1, 128, 2)
