@@ -19,8 +19,10 @@ Also reported (not `value`): per-kernel roofline fractions, Q4_K at BASELINE
 config 4's M = 12000 shapes, decoder GEMVs (config 3) in HBM GB/s with >= 512
 MB of rotating weight copies (defeats the 256 MB MALL), timed as one HIP graph
 of all the launches (kernel_us; call_us = the same launches issued one by one
-from the host), the f32-weight GEMM,
-and the reference CPU path timed on this host (ingot dequant, compiled from
+from the host), the f32-weight GEMM, the relative-position attention core at T = 750
+(8 segments, d 1024, 8 heads; full and chunked-limited [70, 13] windows;
+useful flops = 6 * dk per visible (row, key) pair, against the 157.3 TFLOP/s
+fp32 MFMA peak), and the reference CPU path timed on this host (ingot dequant, compiled from
 the reference's sources, + OpenBLAS sgemm, as src/weights.c:103-114 +
 src/backend.c:79 do).
 """
@@ -253,6 +255,51 @@ def cpu_baseline(M_, lib, seconds_budget=20.0):
                       f"{decoder} once + OpenBLAS sgemm per product, {threads} BLAS threads"}
 
 
+PEAK_FP32 = 157.3  # TFLOP/s dense fp32 MFMA (MI355X)
+
+
+def attn_flops(T, H, dk, left, right, nseq):
+    """Useful flops of the attention core: per (row, visible key) pair, the
+    content and position dot products and the context update, 2*dk each."""
+    t = np.arange(T)
+    if left < 0:
+        pairs = T * T
+    else:
+        chunk = right + 1
+        lc = left // chunk
+        pairs = int((np.minimum((t // chunk + 1) * chunk, T) - np.maximum((t // chunk - lc) * chunk, 0)).sum())
+    return 6.0 * dk * pairs * H * nseq
+
+
+def run_attention(B, M_, T=750, d=1024, H=8, nseq=8, reps=10):
+    """The rel-pos attention core (src/encoder.c:315-410 / 220-313) on one
+    layer's q, k, v of nseq segments, full and chunked-limited windows."""
+    torch, lib = B.torch, B.lib
+    q, k, v = (B.dev(lib.randn(300 + i, 1.0, (nseq, T, d))) for i in range(3))
+    rk = B.dev(lib.randn(303, 1.0, (2 * T - 1, d)))
+    bu, bv = B.dev(lib.randn(304, 0.1, (d,))), B.dev(lib.randn(305, 0.1, (d,)))
+    ctx = B.empty(nseq, T, d)
+    out = []
+    for left, right in ((-1, 0), (70, 13)):
+        def call():
+            M_.relpos_attention_dev(lib, q.data_ptr(), k.data_ptr(), v.data_ptr(), rk.data_ptr(), bu.data_ptr(),
+                                    bv.data_ptr(), ctx.data_ptr(), T, d, H, left, right, nseq, B.sp)
+        call()
+        B.sync()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(B.stream)
+        for _ in range(reps):
+            call()
+        e1.record(B.stream)
+        B.sync()
+        ms = e0.elapsed_time(e1) / reps
+        fl = attn_flops(T, H, d // H, left, right, nseq)
+        out.append({"T": T, "d": d, "heads": H, "segments": nseq, "left": left, "right": right,
+                    "kernel_us": round(ms * 1e3, 2), "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
+                    "fp32_mfma_frac": round(fl / (ms * 1e-3) / 1e12 / PEAK_FP32, 4)})
+    return out
+
+
 def profiled_traffic():
     """HBM bytes per launch of the roofline kernel, as measured by the two
     rocprofv3 --pmc passes recorded under profiles/ (None if absent)."""
@@ -337,6 +384,8 @@ def main():
         log("[bench] f32 weights M=6000")
         msf, flf, rowsf = run_encoder_set(B, M_, M_.F32, M, ENC_SHAPES[:2], 3, 1, 200)
         details["f32_m6000"] = {"tflops": round(flf / (msf * 1e-3) / 1e12, 2), "rows": rowsf}
+        log("[bench] rel-pos attention core T=750 x 8 segments")
+        details["relpos_attention"] = run_attention(B, M_)
         log("[bench] decoder GEMVs")
         gv = []
         for qt in (M_.Q8_0, M_.Q4_0):

@@ -50,15 +50,15 @@ constexpr int NB = RB + KT;      // rk rows staged per tile (the tile touches RB
 template <int DK>
 struct AttnLds {
     static constexpr int KS = DK + 4;   // K / rk row stride (16-byte rows, conflict-free b128 reads)
-    static constexpr int VS = DK + 2;   // V row stride: the four k-slots of a B read land on disjoint banks
+    static constexpr int VT = KT + 4;   // V is stored transposed, [DK][VT]: conflict-free b128 reads
     static constexpr int BS = 53;       // band scratch row stride
     static constexpr int PS = 36;       // probability scratch row stride
     static constexpr int K0 = 0;
     static constexpr int V0 = K0 + KT * KS;
-    static constexpr int R0 = V0 + KT * VS;
+    static constexpr int R0 = V0 + DK * VT;
     static constexpr int W0 = R0 + NB * KS;
     static constexpr int WB = 16 * BS;
-    static constexpr int WSZ = WB + 16 * PS;
+    static constexpr int WSZ = WB;      // the probabilities reuse the band scratch
     static constexpr int TOTAL = W0 + 4 * WSZ;   // floats
 };
 
@@ -66,15 +66,27 @@ __device__ __forceinline__ f4 mfma16(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Reductions over the 16 lanes of a DPP row (the lanes holding one score row):
+// swap neighbours, swap pairs, mirror within 8, mirror within 16. Every lane
+// ends with the same value (each step combines a and b symmetrically).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
 __device__ __forceinline__ float max16(float x) {
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+    x = fmaxf(x, dpp<0xB1>(x));    // quad_perm [1,0,3,2]
+    x = fmaxf(x, dpp<0x4E>(x));    // quad_perm [2,3,0,1]
+    x = fmaxf(x, dpp<0x141>(x));   // row_half_mirror
+    x = fmaxf(x, dpp<0x140>(x));   // row_mirror
     return x;
 }
 
 __device__ __forceinline__ float sum16(float x) {
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) x += __shfl_xor(x, o, 64);
+    x += dpp<0xB1>(x);
+    x += dpp<0x4E>(x);
+    x += dpp<0x141>(x);
+    x += dpp<0x140>(x);
     return x;
 }
 
@@ -151,55 +163,81 @@ __global__ __launch_bounds__(256, 1) void k_relpos_attn(const float *__restrict_
     for (int n = 0; n < NT; n++) acc[n] = f4{0.f, 0.f, 0.f, 0.f};
 
     float *Ks = lds + L::K0, *Vs = lds + L::V0, *Rs = lds + L::R0;
-    float *Bw = lds + L::W0 + w * L::WSZ, *Pw = Bw + L::WB;
+    float *Bw = lds + L::W0 + w * L::WSZ, *Pw = Bw;
     const int P = 2 * T - 1;
+
+    // The next tile's K, V and rk rows are loaded into registers while the
+    // current tile computes, then written to LDS between two barriers. Rows
+    // past the ends are clamped, not zeroed: a key j >= T is masked out of
+    // every score, and an rk row p outside [0, 2T-2] only pairs a query row
+    // t >= T (never stored) or a masked key.
+    constexpr int UKV = KT * DK / 4 / 256, UR = NB * DK / 4 / 256;
+    f4 gk[UKV], gv[UKV], gr[UR];
+    auto gload = [&](int jt) {
+#pragma unroll
+        for (int u = 0; u < UKV; u++) {
+            const int i = tid + 256 * u;
+            const int r = i / (DK / 4), cc = 4 * (i % (DK / 4));
+            gk[u] = *(const f4 *)(k + (size_t)min(jt + r, T - 1) * d + ho + cc);
+            const int rv = i % KT, cv = 4 * (i / KT);   // V: lanes along keys (transposed store)
+            gv[u] = *(const f4 *)(v + (size_t)min(jt + rv, T - 1) * d + ho + cv);
+        }
+        const int pbase = T - 1 + jt - t0 - (RB - 1);
+#pragma unroll
+        for (int u = 0; u < UR; u++) {
+            const int i = tid + 256 * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
+            const int p = min(max(pbase + r, 0), P - 1);
+            gr[u] = *(const f4 *)(rk + (size_t)p * d + ho + cc);
+        }
+    };
+    auto lstore = [&]() {
+#pragma unroll
+        for (int u = 0; u < UKV; u++) {
+            const int i = tid + 256 * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
+            *(f4 *)(Ks + r * L::KS + cc) = gk[u];
+            const int rv = i % KT, cv = 4 * (i / KT);
+#pragma unroll
+            for (int e = 0; e < 4; e++) Vs[(cv + e) * L::VT + rv] = gv[u][e];
+        }
+#pragma unroll
+        for (int u = 0; u < UR; u++) {
+            const int i = tid + 256 * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
+            *(f4 *)(Rs + r * L::KS + cc) = gr[u];
+        }
+    };
+    if (ja < jb) gload(ja);
 
     for (int jt = ja; jt < jb; jt += KT) {
         __syncthreads();   // every wave is done with the previous tile
-        for (int i = tid; i < KT * DK / 4; i += 256) {
-            const int r = i / (DK / 4), cc = 4 * (i % (DK / 4));
-            const int j = jt + r;
-            f4 xk = {0.f, 0.f, 0.f, 0.f}, xv = {0.f, 0.f, 0.f, 0.f};
-            if (j < T) {
-                xk = *(const f4 *)(k + (size_t)j * d + ho + cc);
-                xv = *(const f4 *)(v + (size_t)j * d + ho + cc);
-            }
-            *(f4 *)(Ks + r * L::KS + cc) = xk;
-            *(f2 *)(Vs + r * L::VS + cc) = f2{xv.x, xv.y};
-            *(f2 *)(Vs + r * L::VS + cc + 2) = f2{xv.z, xv.w};
-        }
-        const int pbase = T - 1 + jt - t0 - (RB - 1);
-        for (int i = tid; i < NB * DK / 4; i += 256) {
-            const int r = i / (DK / 4), cc = 4 * (i % (DK / 4));
-            const int p = pbase + r;
-            f4 x = {0.f, 0.f, 0.f, 0.f};
-            if (p >= 0 && p < P) x = *(const f4 *)(rk + (size_t)p * d + ho + cc);
-            *(f4 *)(Rs + r * L::KS + cc) = x;
-        }
+        lstore();
         __syncthreads();
+        if (jt + KT < jb) gload(jt + KT);
 
         // 1. content scores: 16 rows x 32 keys
         f4 s[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
         // 2. position scores against band rows prow .. prow + 47 (p = pbase + prow + col)
         f4 bd[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
         const int prow = (RB - 16) - 16 * w;
+        // operands of step group i + 1 are read from LDS while group i multiplies
+        f4 kb[2][2], rb[2][3];
+        auto rd = [&](int i, f4 *kx, f4 *rx) {
+#pragma unroll
+            for (int n = 0; n < 2; n++) kx[n] = *(const f4 *)(Ks + (16 * n + c) * L::KS + NS * g + 4 * i);
+#pragma unroll
+            for (int n = 0; n < 3; n++) rx[n] = *(const f4 *)(Rs + (prow + 16 * n + c) * L::KS + NS * g + 4 * i);
+        };
+        rd(0, kb[0], rb[0]);
 #pragma unroll
         for (int i = 0; i < NS / 4; i++) {
+            if (i + 1 < NS / 4) rd(i + 1, kb[(i + 1) & 1], rb[(i + 1) & 1]);
+            const f4 *kx = kb[i & 1], *rx = rb[i & 1];
 #pragma unroll
-            for (int n = 0; n < 2; n++) {
-                const f4 kb = *(const f4 *)(Ks + (16 * n + c) * L::KS + NS * g + 4 * i);
-                s[n] = mfma16(qa[4 * i + 0], kb.x, s[n]);
-                s[n] = mfma16(qa[4 * i + 1], kb.y, s[n]);
-                s[n] = mfma16(qa[4 * i + 2], kb.z, s[n]);
-                s[n] = mfma16(qa[4 * i + 3], kb.w, s[n]);
-            }
-#pragma unroll
-            for (int n = 0; n < 3; n++) {
-                const f4 rb = *(const f4 *)(Rs + (prow + 16 * n + c) * L::KS + NS * g + 4 * i);
-                bd[n] = mfma16(qb[4 * i + 0], rb.x, bd[n]);
-                bd[n] = mfma16(qb[4 * i + 1], rb.y, bd[n]);
-                bd[n] = mfma16(qb[4 * i + 2], rb.z, bd[n]);
-                bd[n] = mfma16(qb[4 * i + 3], rb.w, bd[n]);
+            for (int u = 0; u < 4; u++) {
+                s[0] = mfma16(qa[4 * i + u], kx[0][u], s[0]);
+                s[1] = mfma16(qa[4 * i + u], kx[1][u], s[1]);
+                bd[0] = mfma16(qb[4 * i + u], rx[0][u], bd[0]);
+                bd[1] = mfma16(qb[4 * i + u], rx[1][u], bd[1]);
+                bd[2] = mfma16(qb[4 * i + u], rx[2][u], bd[2]);
             }
         }
         // 3. rel-shift: row i = 4g + e, key jj = 16n + c takes band column jj - i + 15
@@ -214,9 +252,16 @@ __global__ __launch_bounds__(256, 1) void k_relpos_attn(const float *__restrict_
         for (int n = 0; n < 2; n++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const int i = 4 * g + e, j = jt + 16 * n + c;
-                const float x = (s[n][e] + Bw[i * L::BS + 16 * n + c - i + 15]) * kscale;
-                sv[n][e] = (j >= rj0[e] && j < rj1[e]) ? x : -INFINITY;
+                const int i = 4 * g + e;
+                sv[n][e] = Bw[i * L::BS + 16 * n + c - i + 15];
+            }
+#pragma unroll
+        for (int n = 0; n < 2; n++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int j = jt + 16 * n + c;
+                const float x = (s[n][e] + sv[n][e]) * kscale;
+                sv[n][e] = (unsigned)(j - rj0[e]) < (unsigned)(rj1[e] - rj0[e]) ? x : -INFINITY;
             }
         // 4. online softmax over the tile
         float alpha[4];
@@ -235,6 +280,7 @@ __global__ __launch_bounds__(256, 1) void k_relpos_attn(const float *__restrict_
 #pragma unroll
             for (int e = 0; e < 4; e++) acc[n][e] *= alpha[e];
         // 5. probabilities to the A layout (row c, keys 8g .. 8g+7), then P . V
+        wave_lds_order();   // the band reads above precede these writes
 #pragma unroll
         for (int n = 0; n < 2; n++)
 #pragma unroll
@@ -243,11 +289,20 @@ __global__ __launch_bounds__(256, 1) void k_relpos_attn(const float *__restrict_
         const f4 pa0 = *(const f4 *)(Pw + c * L::PS + 8 * g);
         const f4 pa1 = *(const f4 *)(Pw + c * L::PS + 8 * g + 4);
         const float pa[8] = {pa0.x, pa0.y, pa0.z, pa0.w, pa1.x, pa1.y, pa1.z, pa1.w};
+        // B operand: column 16n + c, keys 8g .. 8g+7 of the transposed V tile
+        f4 vb[2][2];
+        auto rdv = [&](int n, f4 *vx) {
+            const float *vr = Vs + (16 * n + c) * L::VT + 8 * g;
+            vx[0] = *(const f4 *)vr;
+            vx[1] = *(const f4 *)(vr + 4);
+        };
+        rdv(0, vb[0]);
 #pragma unroll
-        for (int sidx = 0; sidx < 8; sidx++) {
-            const float *vr = Vs + (8 * g + sidx) * L::VS + c;
+        for (int n = 0; n < NT; n++) {
+            if (n + 1 < NT) rdv(n + 1, vb[(n + 1) & 1]);
+            const f4 *vx = vb[n & 1];
 #pragma unroll
-            for (int n = 0; n < NT; n++) acc[n] = mfma16(pa[sidx], vr[16 * n], acc[n]);
+            for (int u = 0; u < 8; u++) acc[n] = mfma16(pa[u], vx[u >> 2][u & 3], acc[n]);
         }
     }
 
