@@ -14,11 +14,14 @@
 //
 // One workgroup = 4 waves = 64 query rows of one head of one segment; wave w
 // owns rows t0 + 16w .. +15. Keys are visited in tiles of 32 (only the tiles
-// the block's rows can see); each tile's K, V and the 95 rk rows its
-// 64 x 32 (row, key) pairs touch are staged in LDS, and every wave
+// the block's rows can see); each tile's K, V and the 80 rk rows of the
+// block's new position columns are staged in LDS, and every wave
 //   1. forms the content scores (16 x 32) with its (q + bias_u) held in registers,
-//   2. forms the position scores of its 16 rows against the 47 rk rows of its
-//      band (16 x 48) with (q + bias_v) in registers,
+//   2. forms the position scores (q + bias_v) . rk for its 16 rows in tiles of
+//      16 offsets delta = j - t: a key tile needs 47 offsets (three tiles),
+//      the first of which the previous key tile computed as its last (carried
+//      in registers), so each key tile costs two position tiles, no more MFMA
+//      work than the content scores,
 //   3. applies the rel-shift through a per-wave LDS scratch (row i, key jj
 //      reads band column jj - i + 15),
 //   4. runs an online softmax (running row max and sum, base-2 exponentials of
@@ -45,7 +48,7 @@ typedef float f2 __attribute__((ext_vector_type(2)));
 
 constexpr int RB = 64;           // query rows per workgroup
 constexpr int KT = 32;           // keys per tile
-constexpr int NB = RB + KT;      // rk rows staged per tile (the tile touches RB + KT - 1)
+constexpr int NB = RB + KT - 16; // rk rows staged per tile: the new position columns of all waves
 
 template <int DK>
 struct AttnLds {
@@ -168,9 +171,9 @@ __global__ __launch_bounds__(256, 1) void k_relpos_attn(const float *__restrict_
 
     // The next tile's K, V and rk rows are loaded into registers while the
     // current tile computes, then written to LDS between two barriers. Rows
-    // past the ends are clamped, not zeroed: a key j >= T is masked out of
-    // every score, and an rk row p outside [0, 2T-2] only pairs a query row
-    // t >= T (never stored) or a masked key.
+    // past the ends are clamped, not zeroed: a key j outside [0, T) is masked
+    // out of every score, and an rk row p outside [0, 2T-2] only pairs a query
+    // row t >= T (never stored) or a masked key.
     constexpr int UKV = KT * DK / 4 / 256, UR = NB * DK / 4 / 256;
     f4 gk[UKV], gv[UKV], gr[UR];
     auto gload = [&](int jt) {
@@ -178,11 +181,11 @@ __global__ __launch_bounds__(256, 1) void k_relpos_attn(const float *__restrict_
         for (int u = 0; u < UKV; u++) {
             const int i = tid + 256 * u;
             const int r = i / (DK / 4), cc = 4 * (i % (DK / 4));
-            gk[u] = *(const f4 *)(k + (size_t)min(jt + r, T - 1) * d + ho + cc);
+            gk[u] = *(const f4 *)(k + (size_t)min(max(jt + r, 0), T - 1) * d + ho + cc);
             const int rv = i % KT, cv = 4 * (i / KT);   // V: lanes along keys (transposed store)
-            gv[u] = *(const f4 *)(v + (size_t)min(jt + rv, T - 1) * d + ho + cv);
+            gv[u] = *(const f4 *)(v + (size_t)min(max(jt + rv, 0), T - 1) * d + ho + cv);
         }
-        const int pbase = T - 1 + jt - t0 - (RB - 1);
+        const int pbase = T + jt - t0 - (RB - 16);
 #pragma unroll
         for (int u = 0; u < UR; u++) {
             const int i = tid + 256 * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
@@ -205,7 +208,35 @@ __global__ __launch_bounds__(256, 1) void k_relpos_attn(const float *__restrict_
             *(f4 *)(Rs + r * L::KS + cc) = gr[u];
         }
     };
-    if (ja < jb) gload(ja);
+    // Position columns are computed in tiles of 16 offsets delta = j - t.
+    // For key tile jt the wave needs delta in [b, b+47), b = jt - tw - 15:
+    // tiles D0 = [b, b+16), D1, D2. The next key tile's D0 is this tile's D2,
+    // so it is carried in registers and every tile computes only D1 and D2
+    // (rk rows T-1 + b + 16 .. + 47: staged row (RB - 16) - 16w + col).
+    const int prow = (RB - 16) - 16 * w;
+    auto bd_tiles = [&](f4 *bd, int n0) {
+#pragma unroll
+        for (int i = 0; i < NS / 4; i++) {
+            f4 rx[2];
+#pragma unroll
+            for (int n = n0; n < 2; n++) rx[n] = *(const f4 *)(Rs + (prow + 16 * n + c) * L::KS + NS * g + 4 * i);
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int n = n0; n < 2; n++) bd[n] = mfma16(qb[4 * i + u], rx[n][u], bd[n]);
+        }
+    };
+    f4 carry = {0.f, 0.f, 0.f, 0.f};
+    {
+        // D0 of the first tile = D2 of the tile before it
+        gload(ja - KT);
+        lstore();
+        __syncthreads();
+        f4 bd[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        bd_tiles(bd, 1);
+        carry = bd[1];
+        gload(ja);
+    }
 
     for (int jt = ja; jt < jb; jt += KT) {
         __syncthreads();   // every wave is done with the previous tile
@@ -213,39 +244,33 @@ __global__ __launch_bounds__(256, 1) void k_relpos_attn(const float *__restrict_
         __syncthreads();
         if (jt + KT < jb) gload(jt + KT);
 
-        // 1. content scores: 16 rows x 32 keys
+        // 1. content scores (16 rows x 32 keys), 2. position tiles D1, D2
         f4 s[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        // 2. position scores against band rows prow .. prow + 47 (p = pbase + prow + col)
-        f4 bd[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        const int prow = (RB - 16) - 16 * w;
-        // operands of step group i + 1 are read from LDS while group i multiplies
-        f4 kb[2][2], rb[2][3];
-        auto rd = [&](int i, f4 *kx, f4 *rx) {
+        f4 bd[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int i = 0; i < NS / 4; i++) {
+            f4 kx[2], rx[2];
 #pragma unroll
             for (int n = 0; n < 2; n++) kx[n] = *(const f4 *)(Ks + (16 * n + c) * L::KS + NS * g + 4 * i);
 #pragma unroll
-            for (int n = 0; n < 3; n++) rx[n] = *(const f4 *)(Rs + (prow + 16 * n + c) * L::KS + NS * g + 4 * i);
-        };
-        rd(0, kb[0], rb[0]);
-#pragma unroll
-        for (int i = 0; i < NS / 4; i++) {
-            if (i + 1 < NS / 4) rd(i + 1, kb[(i + 1) & 1], rb[(i + 1) & 1]);
-            const f4 *kx = kb[i & 1], *rx = rb[i & 1];
+            for (int n = 0; n < 2; n++) rx[n] = *(const f4 *)(Rs + (prow + 16 * n + c) * L::KS + NS * g + 4 * i);
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 s[0] = mfma16(qa[4 * i + u], kx[0][u], s[0]);
                 s[1] = mfma16(qa[4 * i + u], kx[1][u], s[1]);
                 bd[0] = mfma16(qb[4 * i + u], rx[0][u], bd[0]);
                 bd[1] = mfma16(qb[4 * i + u], rx[1][u], bd[1]);
-                bd[2] = mfma16(qb[4 * i + u], rx[2][u], bd[2]);
             }
         }
         // 3. rel-shift: row i = 4g + e, key jj = 16n + c takes band column jj - i + 15
-        //    (p = T-1 + jt + jj - (tw + i) = pbase + prow + (jj - i + 15))
+        //    (delta = jt + jj - (tw + i) = b + (jj - i + 15))
 #pragma unroll
-        for (int n = 0; n < 3; n++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) Bw[(4 * g + e) * L::BS + 16 * n + c] = bd[n][e];
+        for (int e = 0; e < 4; e++) {
+            Bw[(4 * g + e) * L::BS + c] = carry[e];
+            Bw[(4 * g + e) * L::BS + 16 + c] = bd[0][e];
+            Bw[(4 * g + e) * L::BS + 32 + c] = bd[1][e];
+        }
+        carry = bd[1];
         wave_lds_order();
         float sv[2][4];
 #pragma unroll
