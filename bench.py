@@ -20,7 +20,7 @@ config 4's M = 12000 shapes, decoder GEMVs (config 3) in HBM GB/s with >= 512
 MB of rotating weight copies (defeats the 256 MB MALL), timed as one HIP graph
 of all the launches (kernel_us; call_us = the same launches issued one by one
 from the host), the f32-weight GEMM, the relative-position attention core at T = 750
-(8 segments, d 1024, 8 heads; full and chunked-limited [70, 13] windows;
+(16 segments as in BASELINE config 5, d 1024, 8 heads; full and chunked-limited [70, 13] windows;
 useful flops = 6 * dk per visible (row, key) pair, against the 157.3 TFLOP/s
 fp32 MFMA peak), and the reference CPU path timed on this host (ingot dequant, compiled from
 the reference's sources, + OpenBLAS sgemm, as src/weights.c:103-114 +
@@ -271,7 +271,7 @@ def attn_flops(T, H, dk, left, right, nseq):
     return 6.0 * dk * pairs * H * nseq
 
 
-def run_attention(B, M_, T=750, d=1024, H=8, nseq=8, reps=10):
+def run_attention(B, M_, T=750, d=1024, H=8, nseq=16, reps=10):
     """The rel-pos attention core (src/encoder.c:315-410 / 220-313) on one
     layer's q, k, v of nseq segments, full and chunked-limited windows."""
     torch, lib = B.torch, B.lib
@@ -384,7 +384,7 @@ def main():
         log("[bench] f32 weights M=6000")
         msf, flf, rowsf = run_encoder_set(B, M_, M_.F32, M, ENC_SHAPES[:2], 3, 1, 200)
         details["f32_m6000"] = {"tflops": round(flf / (msf * 1e-3) / 1e12, 2), "rows": rowsf}
-        log("[bench] rel-pos attention core T=750 x 8 segments")
+        log("[bench] rel-pos attention core T=750 x 16 segments")
         details["relpos_attention"] = run_attention(B, M_)
         log("[bench] decoder GEMVs")
         gv = []

@@ -12,10 +12,10 @@
 // sees [(t/chunk - lc) * chunk, (t/chunk + 1) * chunk) clipped to [0, T)
 // (encoder.c:373-381).
 //
-// One workgroup = 4 waves = 64 query rows of one head of one segment; wave w
-// owns rows t0 + 16w .. +15. Keys are visited in tiles of 32 (only the tiles
-// the block's rows can see); each tile's K, V and the 80 rk rows of the
-// block's new position columns are staged in LDS, and every wave
+// One workgroup = NW waves (4 or 8) = 16 NW query rows of one head of one
+// segment; wave w owns rows t0 + 16w .. +15. Keys are visited in tiles of 32 (only the tiles
+// the block's rows can see); each tile's K, V and the 16 NW + 16 rk rows of
+// the block's new position columns are staged in LDS, and every wave
 //   1. forms the content scores (16 x 32) with its (q + bias_u) held in registers,
 //   2. forms the position scores (q + bias_v) . rk for its 16 rows in tiles of
 //      16 offsets delta = j - t: a key tile needs 47 offsets (three tiles),
@@ -46,12 +46,14 @@ namespace {
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f2 __attribute__((ext_vector_type(2)));
 
-constexpr int RB = 64;           // query rows per workgroup
 constexpr int KT = 32;           // keys per tile
-constexpr int NB = RB + KT - 16; // rk rows staged per tile: the new position columns of all waves
 
-template <int DK>
+// NW waves per workgroup, 16 query rows each
+template <int DK, int NW>
 struct AttnLds {
+    static constexpr int NTH = 64 * NW;
+    static constexpr int RB = 16 * NW;        // query rows per workgroup
+    static constexpr int NB = RB + KT - 16;   // rk rows staged per tile: the new position columns of all waves
     static constexpr int KS = DK + 4;   // K / rk row stride (16-byte rows, conflict-free b128 reads)
     static constexpr int VT = KT + 4;   // V is stored transposed, [DK][VT]: conflict-free b128 reads
     static constexpr int BS = 53;       // band scratch row stride
@@ -62,7 +64,7 @@ struct AttnLds {
     static constexpr int W0 = R0 + NB * KS;
     static constexpr int WB = 16 * BS;
     static constexpr int WSZ = WB;      // the probabilities reuse the band scratch
-    static constexpr int TOTAL = W0 + 4 * WSZ;   // floats
+    static constexpr int TOTAL = W0 + NW * WSZ;   // floats
 };
 
 __device__ __forceinline__ f4 mfma16(float a, float b, f4 c) {
@@ -107,13 +109,14 @@ struct Window {
     __device__ int j1(int t) const { return lim ? min((t / chunk + 1) * chunk, T) : T; }
 };
 
-template <int DK>
-__global__ __launch_bounds__(256, 1) void k_relpos_attn(const float *__restrict__ q, const float *__restrict__ k,
+template <int DK, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restrict__ q, const float *__restrict__ k,
                                                         const float *__restrict__ v, const float *__restrict__ rk,
                                                         const float *__restrict__ bu, const float *__restrict__ bv,
                                                         float *__restrict__ ctx, int T, int d, int left, int right,
                                                         float kscale) {
-    using L = AttnLds<DK>;
+    using L = AttnLds<DK, NW>;
+    constexpr int NTH = L::NTH, RB = L::RB, NB = L::NB;
     constexpr int NS = DK / 4;    // reduction steps of a score product
     constexpr int NT = DK / 16;   // context column tiles
     extern __shared__ float lds[];
@@ -174,12 +177,13 @@ __global__ __launch_bounds__(256, 1) void k_relpos_attn(const float *__restrict_
     // past the ends are clamped, not zeroed: a key j outside [0, T) is masked
     // out of every score, and an rk row p outside [0, 2T-2] only pairs a query
     // row t >= T (never stored) or a masked key.
-    constexpr int UKV = KT * DK / 4 / 256, UR = NB * DK / 4 / 256;
+    constexpr int UKV = KT * DK / 4 / NTH, NR4 = NB * DK / 4, UR = (NR4 + NTH - 1) / NTH;
+    static_assert(UKV * NTH == KT * DK / 4, "staging split");
     f4 gk[UKV], gv[UKV], gr[UR];
     auto gload = [&](int jt) {
 #pragma unroll
         for (int u = 0; u < UKV; u++) {
-            const int i = tid + 256 * u;
+            const int i = tid + NTH * u;
             const int r = i / (DK / 4), cc = 4 * (i % (DK / 4));
             gk[u] = *(const f4 *)(k + (size_t)min(max(jt + r, 0), T - 1) * d + ho + cc);
             const int rv = i % KT, cv = 4 * (i / KT);   // V: lanes along keys (transposed store)
@@ -188,15 +192,15 @@ __global__ __launch_bounds__(256, 1) void k_relpos_attn(const float *__restrict_
         const int pbase = T + jt - t0 - (RB - 16);
 #pragma unroll
         for (int u = 0; u < UR; u++) {
-            const int i = tid + 256 * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
+            const int i = tid + NTH * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
             const int p = min(max(pbase + r, 0), P - 1);
-            gr[u] = *(const f4 *)(rk + (size_t)p * d + ho + cc);
+            if (NR4 % NTH == 0 || i < NR4) gr[u] = *(const f4 *)(rk + (size_t)p * d + ho + cc);
         }
     };
     auto lstore = [&]() {
 #pragma unroll
         for (int u = 0; u < UKV; u++) {
-            const int i = tid + 256 * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
+            const int i = tid + NTH * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
             *(f4 *)(Ks + r * L::KS + cc) = gk[u];
             const int rv = i % KT, cv = 4 * (i / KT);
 #pragma unroll
@@ -204,8 +208,8 @@ __global__ __launch_bounds__(256, 1) void k_relpos_attn(const float *__restrict_
         }
 #pragma unroll
         for (int u = 0; u < UR; u++) {
-            const int i = tid + 256 * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
-            *(f4 *)(Rs + r * L::KS + cc) = gr[u];
+            const int i = tid + NTH * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
+            if (NR4 % NTH == 0 || i < NR4) *(f4 *)(Rs + r * L::KS + cc) = gr[u];
         }
     };
     // Position columns are computed in tiles of 16 offsets delta = j - t.
@@ -343,24 +347,41 @@ __global__ __launch_bounds__(256, 1) void k_relpos_attn(const float *__restrict_
     }
 }
 
-template <int DK>
+template <int DK, int NW>
 hipError_t launch_attn(const float *q, const float *k, const float *v, const float *rk, const float *bu,
                        const float *bv, float *ctx, int T, int d, int H, int left, int right, int nseq,
                        hipStream_t st) {
-    const size_t bytes = sizeof(float) * AttnLds<DK>::TOTAL;
+    using L = AttnLds<DK, NW>;
+    const size_t bytes = sizeof(float) * L::TOTAL;
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_relpos_attn<DK>,
+        hipError_t e = hipFuncSetAttribute((const void *)k_relpos_attn<DK, NW>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
         if (e != hipSuccess) return e;
         attr = true;
     }
     // exponentials are base 2: scores carry log2(e) / sqrt(DK)
     const float kscale = (1.0f / sqrtf((float)DK)) * 1.4426950408889634f;
-    dim3 grid((T + RB - 1) / RB, H, nseq);
-    hipLaunchKernelGGL(k_relpos_attn<DK>, grid, dim3(256), bytes, st, q, k, v, rk, bu, bv, ctx, T, d, left,
-                       right, kscale);
+    dim3 grid((T + L::RB - 1) / L::RB, H, nseq);
+    hipLaunchKernelGGL((k_relpos_attn<DK, NW>), grid, dim3(L::NTH), bytes, st, q, k, v, rk, bu, bv, ctx, T, d,
+                       left, right, kscale);
     return hipGetLastError();
+}
+
+// Eight waves (two per SIMD, one 128-row block) run full attention faster
+// once there are at least two rounds of such blocks for the 256 CUs; with
+// fewer blocks, or chunked windows (whose key range grows with the block),
+// four waves (64 rows) balance better.
+bool use8(int T, int H, int left, int nseq) {
+    return left < 0 && (long)((T + 127) / 128) * H * nseq >= 512;
+}
+
+template <int DK>
+hipError_t launch_dk(const float *q, const float *k, const float *v, const float *rk, const float *bu,
+                     const float *bv, float *ctx, int T, int d, int H, int left, int right, int nseq,
+                     hipStream_t st) {
+    if (use8(T, H, left, nseq)) return launch_attn<DK, 8>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, st);
+    return launch_attn<DK, 4>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, st);
 }
 
 }  // namespace
@@ -371,7 +392,7 @@ hipError_t mh_launch_relpos_attn(const float *q, const float *k, const float *v,
                                  const float *bias_u, const float *bias_v, float *ctx, int T, int d, int H,
                                  int left, int right, int nseq, hipStream_t st) {
     const int dk = d / H;
-    if (dk == 128) return launch_attn<128>(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, st);
-    if (dk == 64) return launch_attn<64>(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, st);
+    if (dk == 128) return launch_dk<128>(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, st);
+    if (dk == 64) return launch_dk<64>(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, st);
     return hipErrorInvalidValue;
 }

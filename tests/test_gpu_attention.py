@@ -82,14 +82,25 @@ def test_relpos_attention_fastconformer_segment(gpu):
         check(out, arrs, H, left, right)
 
 
+@pytest.mark.parametrize("d", [256, 128])
+def test_relpos_attention_many_segments(gpu, d):
+    """Enough segments for the eight-wave (128-row) kernel variant, dk 128 and 64."""
+    T, H, nseq = 200, 2, 128
+    say("attention many segments", T, d, H, nseq)
+    arrs = make(21 + d, T, d, nseq)
+    out = run_gpu(gpu, arrs, T, d, H, -1, 0, nseq)
+    check(out, arrs, H, -1, 0)
+
+
 def test_relpos_attention_segments_independent(gpu):
     """A segment's context does not depend on the other segments of the call
     (bit-identical to running it alone)."""
     T, d, H = 97, 256, 2
-    arrs = make(5, T, d, 3)
-    both = run_gpu(gpu, arrs, T, d, H, -1, 0, 3)
-    one = run_gpu(gpu, tuple(a[1:2] if a.ndim == 3 else a for a in arrs), T, d, H, -1, 0, 1)
-    assert np.array_equal(both[1].view(np.uint32), one[0].view(np.uint32))
+    for nseq in (3, 256):   # the four- and the eight-wave kernel
+        arrs = make(5, T, d, nseq)
+        many = run_gpu(gpu, arrs, T, d, H, -1, 0, nseq)
+        one = run_gpu(gpu, tuple(a[1:2] if a.ndim == 3 else a for a in arrs), T, d, H, -1, 0, 1)
+        assert np.array_equal(many[1].view(np.uint32), one[0].view(np.uint32))
 
 
 def test_relpos_attention_rejects_bad_arguments(gpu):
