@@ -341,6 +341,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extras", action="store_true", help="primary workload only")
+    ap.add_argument("--attention", action="store_true",
+                    help="only the rel-pos attention core (T=750, 16 segments, full and [70, 13] windows), "
+                         "one JSON line")
     ap.add_argument("--profile", action="store_true",
                     help="counter-calibration run for rocprofv3 --pmc: a 256 MiB device copy, then "
                          "the dominant GEMM (Q8_0 4096->1024, M=6000) alone, 3 launches each")
@@ -360,6 +363,9 @@ def main():
     M = 6000
     if args.profile:
         run_profile(B, M_)
+        return
+    if args.attention:
+        print(json.dumps({"relpos_attention": run_attention(B, M_)}), flush=True)
         return
 
     log("[bench] encoder set Q8_0 M=6000")

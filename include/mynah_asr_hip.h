@@ -172,6 +172,12 @@ int mynah_asr_hip_dequant_dev(const mynah_asr_hip_weight *w, float *dwd, void *s
  * layer once per segment). All pointers 16-byte aligned. ctx may not alias
  * q, k or v. Outputs are f32 sums in another order than the reference's BLAS:
  * equal within |y - ref| <= 1e-4*|ref| + 1e-5*max|v|. */
+/* The same on host buffers, one segment (the call encoder.c's attention() and
+ * attention_banded() would make in place of their per-head loops, after rk is
+ * formed): copies in, computes, copies ctx out. d must be a multiple of 4. */
+int mynah_asr_hip_relpos_attention(const float *q, const float *k, const float *v, const float *rk,
+                                   const float *bias_u, const float *bias_v, float *ctx, int T, int d, int H,
+                                   int left, int right);
 int mynah_asr_hip_relpos_attention_dev(const float *q, const float *k, const float *v, const float *rk,
                                        const float *bias_u, const float *bias_v, float *ctx, int T, int d,
                                        int H, int left, int right, int nseq, void *stream);

@@ -78,6 +78,7 @@ struct Ctx {
     int state = 0;  // 0 uninitialised, 1 ok, -1 failed
     hipStream_t st = nullptr;
     DBuf x, y, h;
+    DBuf att;    // the host-pointer attention call's q, k, v, rk, biases and ctx
     PrepBuf pa;  // the products' input (prep_dev / qgemm_prepped_dev use this one)
     PrepBuf pb;  // the FFN's intermediate, prepared by the first product
 };
@@ -422,6 +423,31 @@ int mynah_asr_hip_relpos_attention_dev(const float *q, const float *k, const flo
                                          pick_stream(stream));
     if (e != hipSuccess) return fail("attention launch failed", hipGetErrorString(e));
     return 0;
+}
+
+int mynah_asr_hip_relpos_attention(const float *q, const float *k, const float *v, const float *rk,
+                                   const float *bias_u, const float *bias_v, float *ctx, int T, int d, int H,
+                                   int left, int right) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    if (!q || !k || !v || !rk || !bias_u || !bias_v || !ctx || T < 0 || H <= 0 || d <= 0 || d % H != 0)
+        return fail("bad argument");
+    if (!mh_attn_supported(d / H)) return fail("head size must be 64 or 128");
+    if (T == 0) return 0;
+    const size_t td = (size_t)T * d, pd = (size_t)(2 * T - 1) * d;
+    float *base = (float *)c->att.get((4 * td + pd + 2 * (size_t)d) * sizeof(float));
+    if (!base) return fail("device buffer allocation failed");
+    float *dq = base, *dk = dq + td, *dv = dk + td, *dctx = dv + td, *drk = dctx + td, *dbu = drk + pd,
+          *dbv = dbu + d;
+    const float *src[6] = {q, k, v, rk, bias_u, bias_v};
+    float *dst[6] = {dq, dk, dv, drk, dbu, dbv};
+    const size_t n[6] = {td, td, td, pd, (size_t)d, (size_t)d};
+    for (int i = 0; i < 6; i++)
+        if (hipMemcpyAsync(dst[i], src[i], n[i] * sizeof(float), hipMemcpyHostToDevice, c->st) != hipSuccess)
+            return fail("H2D copy failed");
+    if (mynah_asr_hip_relpos_attention_dev(dq, dk, dv, drk, dbu, dbv, dctx, T, d, H, left, right, 1, c->st))
+        return -1;
+    return d2h_sync(c, ctx, dctx, td);
 }
 
 int mynah_asr_hip_qgemm(const mynah_asr_hip_wdesc *w, const float *x, float *out, int T) {

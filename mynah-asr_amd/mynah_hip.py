@@ -37,7 +37,7 @@ HIP_SYMBOLS = [
     "mynah_asr_hip_weight_create", "mynah_asr_hip_weight_destroy", "mynah_asr_hip_weight_bytes",
     "mynah_asr_hip_qgemm_dev", "mynah_asr_hip_dequant_dev", "mynah_asr_hip_prep_dev",
     "mynah_asr_hip_qgemm_prepped_dev", "mynah_asr_hip_qffn_dev", "mynah_asr_hip_qqkv_dev",
-    "mynah_asr_hip_relpos_attention_dev",
+    "mynah_asr_hip_relpos_attention_dev", "mynah_asr_hip_relpos_attention",
 ]
 HOST_SYMBOLS = [
     "mynah_asr_set_backend", "mynah_asr_backend", "mynah_asr_gemm_wt", "mynah_asr_silu",
@@ -102,6 +102,7 @@ class HipLib:
             L.mynah_asr_hip_qqkv_dev.argtypes = [_P, _P, _P, _P, _P, _P, _P, C.c_int, _P]
         if hasattr(L, "mynah_asr_hip_relpos_attention_dev"):
             L.mynah_asr_hip_relpos_attention_dev.argtypes = [_P] * 7 + [C.c_int] * 6 + [_P]
+            L.mynah_asr_hip_relpos_attention.argtypes = [_P] * 7 + [C.c_int] * 5
         L.mynah_asr_hip_qgemm.argtypes = [C.POINTER(WDesc), _P, _P, C.c_int]
         L.mynah_asr_hip_qffn.argtypes = [C.POINTER(WDesc), C.POINTER(WDesc), _P, _P, C.c_int]
         L.mynah_asr_hip_qqkv.argtypes = [C.POINTER(WDesc)] * 3 + [_P] * 4 + [C.c_int]
@@ -253,6 +254,17 @@ def relpos_attention_dev(lib, q, k, v, rk, bias_u, bias_v, ctx, T: int, d: int, 
     rc = lib.L.mynah_asr_hip_relpos_attention_dev(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right,
                                                  nseq, stream or None)
     lib._check(rc, "relpos_attention_dev")
+
+
+def host_relpos_attention(lib, q, k, v, rk, bias_u, bias_v, H: int, left: int = -1, right: int = 0):
+    """One segment on host arrays (mynah_asr_hip_relpos_attention): ctx [T, d]."""
+    q, k, v, rk, bias_u, bias_v = (np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v, rk, bias_u, bias_v))
+    T, d = q.shape
+    ctx = np.empty((T, d), dtype=np.float32)
+    rc = lib.L.mynah_asr_hip_relpos_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(rk), _ptr(bias_u), _ptr(bias_v),
+                                             _ptr(ctx), T, d, H, left, right)
+    lib._check(rc, "relpos_attention")
+    return ctx
 
 
 def evict(lib: HipLib, w: Weight) -> None:

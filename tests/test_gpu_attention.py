@@ -103,6 +103,17 @@ def test_relpos_attention_segments_independent(gpu):
         assert np.array_equal(many[1].view(np.uint32), one[0].view(np.uint32))
 
 
+def test_relpos_attention_host_entry(gpu):
+    """The host-pointer entry point gives the device entry point's bits."""
+    T, d, H = 150, 256, 2
+    arrs = make(31, T, d, 1)
+    for left, right in ((-1, 0), (20, 4)):
+        dev = run_gpu(gpu, arrs, T, d, H, left, right, 1)[0]
+        q, k, v, rk, bu, bv = arrs
+        host = M.host_relpos_attention(gpu, q[0], k[0], v[0], rk, bu, bv, H, left, right)
+        assert np.array_equal(host.view(np.uint32), dev.view(np.uint32))
+
+
 def test_relpos_attention_rejects_bad_arguments(gpu):
     import torch
     x = torch.zeros((4, 192), dtype=torch.float32, device="cuda")
