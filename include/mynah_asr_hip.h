@@ -182,6 +182,48 @@ int mynah_asr_hip_relpos_attention_dev(const float *q, const float *k, const flo
                                        const float *bias_u, const float *bias_v, float *ctx, int T, int d,
                                        int H, int left, int right, int nseq, void *stream);
 
+/* AED (Canary) decoder on the device: src/decoder_aed.h:12-36 with every
+ * linear a resident weight (mynah_asr_hip_weight_create) and every other tensor
+ * a device pointer. Biases may not be NULL except proj_b. */
+typedef struct {
+    const float *ln_self_w, *ln_self_b;
+    const mynah_asr_hip_weight *sq, *sk, *sv, *so;
+    const float *sq_b, *sk_b, *sv_b, *so_b;
+    const float *ln_cross_w, *ln_cross_b;
+    const mynah_asr_hip_weight *cq, *ck, *cv, *co;
+    const float *cq_b, *ck_b, *cv_b, *co_b;
+    const float *ln_ffn_w, *ln_ffn_b;
+    const mynah_asr_hip_weight *ff1, *ff2;
+    const float *ff1_b, *ff2_b;
+} mynah_asr_hip_aed_layer;
+
+typedef struct {
+    int n_layers, d, n_heads, ffn, vocab, max_seq;
+    const mynah_asr_hip_weight *proj;      /* enc_dec_proj [d, d_enc]; NULL = identity */
+    const float *proj_b;                   /* may be NULL */
+    const float *emb;                      /* [vocab, d] */
+    const float *pos;                      /* [max_seq, d] */
+    const float *embln_w, *embln_b;
+    const float *fin_w, *fin_b;
+    const mynah_asr_hip_weight *head;      /* [vocab, d] */
+    const float *head_b;
+    const mynah_asr_hip_aed_layer *layers; /* host array of n_layers */
+} mynah_asr_hip_aed;
+
+/* Greedy decoding, the device twin of mynah_asr_aed_decode (src/decoder_aed.c:139-232):
+ * enc = device [T, d_enc]; prompt (host, n_prompt >= 1), eos, tokens (host, cap):
+ * returns the generated token count (prompt and EOS excluded) or -1. The self and
+ * cross K/V caches stay on the device; a decoding step is one HIP graph replay
+ * (the step's position and token live in device memory). d <= 4096, head size 64
+ * or 128, EXACT numerics, every linear on the GEMV path (K <= 8192). */
+int mynah_asr_hip_aed_decode_dev(const mynah_asr_hip_aed *a, const float *enc, int T, const int *prompt,
+                                 int n_prompt, int eos, int *tokens, int cap, void *stream);
+/* The same steps over given tokens (host, n <= max_seq): logits (device,
+ * [n, vocab]) of every position, as the decode loop computes them before its
+ * argmax. 0 or -1. */
+int mynah_asr_hip_aed_forced_dev(const mynah_asr_hip_aed *a, const float *enc, int T, const int *tokens, int n,
+                                 float *logits, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

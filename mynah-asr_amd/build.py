@@ -47,7 +47,7 @@ def _run(cmd: list[str]) -> None:
 
 def build_hip() -> str:
     os.makedirs(LIB, exist_ok=True)
-    srcs = [os.path.join(CSRC, f) for f in ("kernels.hip", "attention.hip", "backend.cpp", "repack.cpp")]
+    srcs = [os.path.join(CSRC, f) for f in ("kernels.hip", "attention.hip", "decoder.hip", "backend.cpp", "repack.cpp")]
     objs = []
     for s in srcs:
         o = os.path.join(LIB, os.path.basename(s) + ".o")

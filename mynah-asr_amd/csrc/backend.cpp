@@ -79,6 +79,8 @@ struct Ctx {
     hipStream_t st = nullptr;
     DBuf x, y, h;
     DBuf att;    // the host-pointer attention call's q, k, v, rk, biases and ctx
+    DBuf aed;    // the AED decoder's caches and vectors
+    int *pin = nullptr;   // pinned host int[2]: the step state read back
     PrepBuf pa;  // the products' input (prep_dev / qgemm_prepped_dev use this one)
     PrepBuf pb;  // the FFN's intermediate, prepared by the first product
 };
@@ -286,6 +288,177 @@ int d2h_sync(Ctx *c, float *out, const float *d, size_t n) {
     return 0;
 }
 
+// ---------------------------------------------------------------------------
+// AED decoder (decoder_aed.c:139-232) on the device.
+
+struct AedBufs {
+    float *encp, *ckv, *skv, *x, *xn, *q, *att, *kn, *vn, *ff, *logits, *opart, *ml;
+    int *st, *prompt;
+    int nsplit;
+};
+
+bool gemv_ok(const mynah_asr_hip_weight *W, int n, int k) {
+    return W && W->dw.n == n && W->dw.k == k && mh_use_gemv(W->dw, 1);
+}
+
+int aed_check(const mynah_asr_hip_aed *a, int T) {
+    if (!a || !a->layers || a->n_layers < 0 || a->d <= 0 || a->n_heads <= 0 || a->d % a->n_heads || T <= 0 ||
+        a->vocab <= 0 || a->ffn <= 0 || a->max_seq <= 0)
+        return fail("bad argument");
+    const int d = a->d, dk = d / a->n_heads;
+    if (dk != 64 && dk != 128) return fail("decoder head size must be 64 or 128");
+    if (d > 4096 || d % 4) return fail("decoder width must be a multiple of 4, at most 4096");
+    if (mynah_asr_hip_numerics() != MYNAH_ASR_HIP_EXACT) return fail("the device decoder runs EXACT numerics only");
+    if (!a->emb || !a->pos || !a->embln_w || !a->embln_b || !a->fin_w || !a->fin_b || !a->head_b)
+        return fail("bad argument: a decoder tensor is NULL");
+    if (!gemv_ok(a->head, a->vocab, d)) return fail("head weight shape or GEMV limits");
+    if (a->proj && a->proj->dw.n != d) return fail("proj weight shape");
+    for (int li = 0; li < a->n_layers; li++) {
+        const mynah_asr_hip_aed_layer *L = &a->layers[li];
+        const mynah_asr_hip_weight *sq[8] = {L->sq, L->sk, L->sv, L->so, L->cq, L->ck, L->cv, L->co};
+        for (int i = 0; i < 8; i++)
+            if (!sq[i] || sq[i]->dw.n != d || sq[i]->dw.k != d || (i != 5 && i != 6 && !mh_use_gemv(sq[i]->dw, 1)))
+                return fail("attention weight shape or GEMV limits");
+        if (!gemv_ok(L->ff1, a->ffn, d) || !gemv_ok(L->ff2, d, a->ffn)) return fail("FFN weight shape or GEMV limits");
+        const float *v[16] = {L->ln_self_w, L->ln_self_b, L->sq_b, L->sk_b, L->sv_b, L->so_b, L->ln_cross_w,
+                              L->ln_cross_b, L->cq_b, L->ck_b, L->cv_b, L->co_b, L->ln_ffn_w, L->ln_ffn_b,
+                              L->ff1_b, L->ff2_b};
+        for (int i = 0; i < 16; i++)
+            if (!v[i]) return fail("bad argument: a decoder layer tensor is NULL");
+    }
+    return 0;
+}
+
+int gemv_epi(const mynah_asr_hip_weight *W, const float *x, float *y, int act, const float *bias, const float *res,
+             hipStream_t st) {
+    const int vec = (W->dw.k % 8 == 0) && (((uintptr_t)x & 15) == 0);
+    hipError_t e = mh_launch_gemv_epi(W->qtype, W->dw, x, 1, vec, y, GEpi{act, bias, res}, st);
+    return e == hipSuccess ? 0 : fail("gemv launch failed", hipGetErrorString(e));
+}
+
+#define AED_TRY(expr)                                                             \
+    do {                                                                          \
+        hipError_t e_ = (expr);                                                   \
+        if (e_ != hipSuccess) return fail("decoder launch failed", hipGetErrorString(e_)); \
+    } while (0)
+
+// One decoding position: every launch reads p and the token from b.st.
+int aed_step(const mynah_asr_hip_aed *a, const AedBufs &b, int T, int max_len, int n_prompt, float *logits_out,
+             hipStream_t st) {
+    const int d = a->d, H = a->n_heads;
+    const size_t td = (size_t)T * d, md = (size_t)max_len * d;
+    AED_TRY(mh_launch_embed_ln(a->emb, a->pos, b.prompt, n_prompt, b.st, a->embln_w, a->embln_b, b.x, d, st));
+    for (int li = 0; li < a->n_layers; li++) {
+        const mynah_asr_hip_aed_layer *L = &a->layers[li];
+        float *SK = b.skv + 2 * (size_t)li * md, *SV = SK + md;
+        float *CK = b.ckv + 2 * (size_t)li * td, *CV = CK + td;
+        // causal self attention, its k and v rows appended to the cache at p
+        AED_TRY(mh_launch_ln(b.x, L->ln_self_w, L->ln_self_b, b.xn, d, st));
+        if (gemv_epi(L->sq, b.xn, b.q, 0, L->sq_b, nullptr, st) || gemv_epi(L->sk, b.xn, b.kn, 0, L->sk_b, nullptr, st) ||
+            gemv_epi(L->sv, b.xn, b.vn, 0, L->sv_b, nullptr, st))
+            return -1;
+        AED_TRY(mh_launch_attend1(b.q, SK, SV, b.kn, b.vn, b.st, 0, d, H, b.opart, b.ml, b.nsplit, b.att, st));
+        if (gemv_epi(L->so, b.att, b.x, 0, L->so_b, b.x, st)) return -1;
+        // cross attention over the projected encoder output
+        AED_TRY(mh_launch_ln(b.x, L->ln_cross_w, L->ln_cross_b, b.xn, d, st));
+        if (gemv_epi(L->cq, b.xn, b.q, 0, L->cq_b, nullptr, st)) return -1;
+        AED_TRY(mh_launch_attend1(b.q, CK, CV, nullptr, nullptr, b.st, T, d, H, b.opart, b.ml, b.nsplit, b.att, st));
+        if (gemv_epi(L->co, b.att, b.x, 0, L->co_b, b.x, st)) return -1;
+        // ReLU FFN
+        AED_TRY(mh_launch_ln(b.x, L->ln_ffn_w, L->ln_ffn_b, b.xn, d, st));
+        if (gemv_epi(L->ff1, b.xn, b.ff, 2, L->ff1_b, nullptr, st) || gemv_epi(L->ff2, b.ff, b.x, 0, L->ff2_b, b.x, st))
+            return -1;
+    }
+    AED_TRY(mh_launch_ln(b.x, a->fin_w, a->fin_b, b.xn, d, st));
+    if (gemv_epi(a->head, b.xn, b.logits, 0, a->head_b, nullptr, st)) return -1;
+    AED_TRY(mh_launch_argmax(b.logits, a->vocab, b.st, logits_out, st));
+    return 0;
+}
+
+// Shared body of decode (greedy, tokens != NULL) and forced (logits_out != NULL).
+int aed_run(Ctx *c, const mynah_asr_hip_aed *a, const float *enc, int T, const int *prompt, int n_prompt,
+            int max_len, int eos, int *tokens, int cap, float *logits_out, hipStream_t st) {
+    const int d = a->d, nl = a->n_layers;
+    const size_t td = (size_t)T * d, md = (size_t)max_len * d;
+    AedBufs b;
+    b.nsplit = mh_att_splits(T > max_len ? T : max_len);
+    auto al = [](size_t n) { return (n + 63) / 64 * 64; };   // floats, 256-byte pieces
+    const size_t nenc = a->proj ? al(td) : 0, nckv = al(2 * (size_t)nl * td), nskv = al(2 * (size_t)nl * md);
+    const size_t nvec = 6 * al(d) + al(a->ffn) + al(a->vocab) + al((size_t)b.nsplit * d) +
+                        al((size_t)b.nsplit * a->n_heads * 2) + al(2 + (size_t)n_prompt);
+    float *base = (float *)c->aed.get((nenc + nckv + nskv + nvec) * sizeof(float));
+    if (!base) return fail("device buffer allocation failed");
+    float *cur = base;
+    auto take = [&](size_t n) { float *r = cur; cur += al(n); return r; };
+    b.encp = a->proj ? take(td) : (float *)enc;
+    b.ckv = take(2 * (size_t)nl * td);
+    b.skv = take(2 * (size_t)nl * md);
+    b.x = take(d), b.xn = take(d), b.q = take(d), b.att = take(d), b.kn = take(d), b.vn = take(d);
+    b.ff = take(a->ffn), b.logits = take(a->vocab);
+    b.opart = take((size_t)b.nsplit * d), b.ml = take((size_t)b.nsplit * a->n_heads * 2);
+    b.st = (int *)take(2 + (size_t)n_prompt);
+    b.prompt = b.st + 2;
+    if (!c->pin && hipHostMalloc((void **)&c->pin, 2 * sizeof(int)) != hipSuccess) {
+        c->pin = nullptr;
+        return fail("pinned host allocation failed");
+    }
+
+    // encoder projection and the per-layer cross K/V (decoder_aed.c:150-175)
+    if (a->proj) {
+        if (gemm_dev(c, a->proj, enc, b.encp, T, 0, st)) return -1;
+        if (a->proj_b) AED_TRY(mh_launch_bias_rows(b.encp, a->proj_b, T, d, st));
+    }
+    for (int li = 0; li < nl; li++) {
+        const mynah_asr_hip_aed_layer *L = &a->layers[li];
+        float *CK = b.ckv + 2 * (size_t)li * td, *CV = CK + td;
+        if (gemm_dev(c, L->ck, b.encp, CK, T, 0, st) || gemm_dev(c, L->cv, b.encp, CV, T, 0, st)) return -1;
+        AED_TRY(mh_launch_bias_rows(CK, L->ck_b, T, d, st));
+        AED_TRY(mh_launch_bias_rows(CV, L->cv_b, T, d, st));
+    }
+    if (hipMemcpyAsync(b.prompt, prompt, n_prompt * sizeof(int), hipMemcpyHostToDevice, st) != hipSuccess)
+        return fail("H2D copy failed");
+    AED_TRY(mh_launch_set_state(b.st, 0, prompt[0], st));
+
+    // position 0 eagerly, then the step captured once and replayed
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int n_out = 0, rc = 0;
+    for (int p = 0; p < max_len; p++) {
+        if (p == 0) {
+            if (aed_step(a, b, T, max_len, n_prompt, logits_out, st)) return -1;
+        } else {
+            if (!exec) {
+                if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess)
+                    return fail("stream capture failed");
+                const int r = aed_step(a, b, T, max_len, n_prompt, logits_out, st);
+                hipError_t e = hipStreamEndCapture(st, &graph);
+                if (r || e != hipSuccess) {
+                    if (graph) (void)hipGraphDestroy(graph);
+                    return r ? -1 : fail("stream capture failed", hipGetErrorString(e));
+                }
+                if (hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) {
+                    (void)hipGraphDestroy(graph);
+                    return fail("graph instantiation failed");
+                }
+            }
+            if (hipGraphLaunch(exec, st) != hipSuccess) { rc = fail("graph launch failed"); break; }
+        }
+        if (!tokens || p + 1 < n_prompt) continue;   // prompt positions: no sampling
+        if (hipMemcpyAsync(c->pin, b.st, 2 * sizeof(int), hipMemcpyDeviceToHost, st) != hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess) {
+            rc = fail("token read-back failed");
+            break;
+        }
+        const int best = c->pin[1];
+        if (best == eos || n_out >= cap) break;
+        tokens[n_out++] = best;
+    }
+    if (hipStreamSynchronize(st) != hipSuccess && rc == 0) rc = fail("stream sync failed");
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    return rc ? -1 : n_out;
+}
+
 int begin(Ctx **c) {
     t_err[0] = 0;
     if (!mynah_asr_hip_available()) return fail("no gfx950 device");
@@ -448,6 +621,27 @@ int mynah_asr_hip_relpos_attention(const float *q, const float *k, const float *
     if (mynah_asr_hip_relpos_attention_dev(dq, dk, dv, drk, dbu, dbv, dctx, T, d, H, left, right, 1, c->st))
         return -1;
     return d2h_sync(c, ctx, dctx, td);
+}
+
+int mynah_asr_hip_aed_decode_dev(const mynah_asr_hip_aed *a, const float *enc, int T, const int *prompt,
+                                 int n_prompt, int eos, int *tokens, int cap, void *stream) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    if (aed_check(a, T)) return -1;
+    if (!enc || !prompt || n_prompt <= 0 || !tokens || cap < 0) return fail("bad argument");
+    int max_len = n_prompt + cap;
+    if (max_len > a->max_seq) max_len = a->max_seq;
+    return aed_run(c, a, enc, T, prompt, n_prompt, max_len, eos, tokens, cap, nullptr, pick_stream(stream));
+}
+
+int mynah_asr_hip_aed_forced_dev(const mynah_asr_hip_aed *a, const float *enc, int T, const int *tokens, int n,
+                                 float *logits, void *stream) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    if (aed_check(a, T)) return -1;
+    if (!enc || !tokens || n <= 0 || n > a->max_seq || !logits) return fail("bad argument");
+    const int r = aed_run(c, a, enc, T, tokens, n, n, -1, nullptr, 0, logits, pick_stream(stream));
+    return r < 0 ? -1 : 0;
 }
 
 int mynah_asr_hip_qgemm(const mynah_asr_hip_wdesc *w, const float *x, float *out, int T) {

@@ -1,0 +1,294 @@
+// decoder.hip — the non-GEMV kernels of the AED (Canary) decoder step
+// (the reference's src/decoder_aed.c:139-232), device-resident:
+//
+//   k_embed_ln   x = LN(emb[token] + pos[p])                  decoder_aed.c:183-186
+//   k_ln         y = LN(x)                                    decoder_aed.c:21-28
+//   k_att_part   one query against a split of KC keys, per head: running max,
+//                sum of exponentials and the weighted sum of V rows; with
+//                `append`, the split holding key p first stores this step's
+//                k and v rows into the self-attention cache  decoder_aed.c:124-137, 195-198
+//   k_att_combine the splits of each head merged               (same)
+//   k_argmax     first maximum of the logits, the next token; advances p
+//                                                              decoder_aed.c:217-222
+//   k_bias_rows  y[t] += b                                    decoder_aed.c:132-136
+//
+// The step's position p and its token live in device memory (`st`: st[0] = p,
+// st[1] = the last argmax), so one captured launch sequence serves every
+// step: position p reads prompt[p] while p < n_prompt, else the argmax of the
+// step before (decoder_aed.c:213-222 chooses the same tokens).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "launch.h"
+
+namespace {
+
+constexpr int LN_T = 256;   // threads of the one-workgroup row kernels
+constexpr int LN_V = 16;    // values per thread: d <= 4096
+constexpr int KC = 64;      // keys per attention split
+
+// Sum over the workgroup in double (the reference's ln accumulates in double).
+__device__ double block_sum(double v, double *red) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    double s = 0.0;
+    for (int i = 0; i < LN_T / 64; i++) s += red[i];
+    return s;
+}
+
+// y = LN(v) over d values held LN_V per thread (i = tid + LN_T * u):
+// (float)((x - mean) * inv) * w + b with inv = (float)(1 / sqrt(var + 1e-5))
+__device__ void ln_store(float (&v)[LN_V], int d, const float *w, const float *b, float *y) {
+    __shared__ double red[LN_T / 64];
+    const int tid = threadIdx.x;
+    double s = 0.0;
+#pragma unroll
+    for (int u = 0; u < LN_V; u++)
+        if (tid + LN_T * u < d) s += (double)v[u];
+    const double mu = block_sum(s, red) / d;
+    double q = 0.0;
+#pragma unroll
+    for (int u = 0; u < LN_V; u++)
+        if (tid + LN_T * u < d) {
+            const double c = (double)v[u] - mu;
+            q += c * c;
+        }
+    const double var = block_sum(q, red) / d;
+    const float inv = (float)(1.0 / sqrt(var + 1e-5));
+#pragma unroll
+    for (int u = 0; u < LN_V; u++) {
+        const int i = tid + LN_T * u;
+        if (i < d) {
+            const float t = (float)(((double)v[u] - mu) * (double)inv);
+            y[i] = t * w[i] + b[i];
+        }
+    }
+}
+
+__global__ __launch_bounds__(LN_T) void k_embed_ln(const float *__restrict__ emb, const float *__restrict__ pos,
+                                                   const int *__restrict__ prompt, int n_prompt,
+                                                   const int *__restrict__ st, const float *__restrict__ w,
+                                                   const float *__restrict__ b, float *__restrict__ x, int d) {
+    const int p = st[0];
+    const int tok = p < n_prompt ? prompt[p] : st[1];
+    const float *e = emb + (size_t)tok * d, *pe = pos + (size_t)p * d;
+    float v[LN_V];
+#pragma unroll
+    for (int u = 0; u < LN_V; u++) {
+        const int i = threadIdx.x + LN_T * u;
+        v[u] = i < d ? e[i] + pe[i] : 0.0f;
+    }
+    ln_store(v, d, w, b, x);
+}
+
+__global__ __launch_bounds__(LN_T) void k_ln(const float *__restrict__ x, const float *__restrict__ w,
+                                             const float *__restrict__ b, float *__restrict__ y, int d) {
+    float v[LN_V];
+#pragma unroll
+    for (int u = 0; u < LN_V; u++) {
+        const int i = threadIdx.x + LN_T * u;
+        v[u] = i < d ? x[i] : 0.0f;
+    }
+    ln_store(v, d, w, b, y);
+}
+
+// Workgroup (head h, split s) over keys [s*KC, min((s+1)*KC, n)), n = n_fixed,
+// or p + 1 for self attention (n_fixed = 0). 256 threads: for the scores, 4
+// threads per key (dk/4 features each); for the values, thread = (feature,
+// key group). Writes o[h][s][dk] (unnormalised) and ml[h][s] = (max, sum).
+template <int DK>
+__global__ __launch_bounds__(256) void k_att_part(const float *__restrict__ q, float *K, float *V,
+                                                  const float *__restrict__ kn, const float *__restrict__ vn,
+                                                  const int *__restrict__ st, int n_fixed, int d, float scale,
+                                                  float *__restrict__ o_part, float *__restrict__ ml_part,
+                                                  int nsplit) {
+    __shared__ float qs[DK];
+    __shared__ float sc[KC];
+    __shared__ float red[256 / DK][DK];
+    const int h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
+    const int ho = h * DK;
+    const int p = st[0];
+    const int n = n_fixed > 0 ? n_fixed : p + 1;
+    const int j0 = s * KC, j1 = min(j0 + KC, n);
+    float *op = o_part + ((size_t)h * nsplit + s) * DK;
+    float *mlp = ml_part + ((size_t)h * nsplit + s) * 2;
+    if (j0 >= j1) {   // nothing in this split (uniform per workgroup)
+        if (tid < DK) op[tid] = 0.0f;
+        if (tid == 0) mlp[0] = -INFINITY, mlp[1] = 0.0f;
+        return;
+    }
+    const bool append = n_fixed == 0 && p >= j0 && p < j1;
+    if (append && tid < DK) {   // this step's k, v rows join the cache (read back below from kn, vn)
+        K[(size_t)p * d + ho + tid] = kn[ho + tid];
+        V[(size_t)p * d + ho + tid] = vn[ho + tid];
+    }
+    if (tid < DK) qs[tid] = q[ho + tid];
+    __syncthreads();
+    // scores: key j0 + (tid >> 2), features (tid & 3) * DK/4 ..
+    {
+        const int jj = tid >> 2, part = tid & 3, j = j0 + jj;
+        float acc = 0.0f;
+        if (j < j1) {
+            const float *kr = (append && j == p) ? kn + ho : K + (size_t)j * d + ho;
+#pragma unroll
+            for (int i = 0; i < DK / 4; i += 4) {
+                const float4 kv = *(const float4 *)(kr + part * (DK / 4) + i);
+                const float *qq = qs + part * (DK / 4) + i;
+                acc = fmaf(qq[0], kv.x, acc);
+                acc = fmaf(qq[1], kv.y, acc);
+                acc = fmaf(qq[2], kv.z, acc);
+                acc = fmaf(qq[3], kv.w, acc);
+            }
+        }
+        acc += __shfl_xor(acc, 1, 64);
+        acc += __shfl_xor(acc, 2, 64);
+        if (part == 0 && jj < KC) sc[jj] = j < j1 ? scale * acc : -INFINITY;
+    }
+    __syncthreads();
+    float m = -INFINITY;
+    for (int i = 0; i < KC; i++) m = fmaxf(m, sc[i]);
+    __syncthreads();
+    if (tid < KC) sc[tid] = tid < j1 - j0 ? expf(sc[tid] - m) : 0.0f;
+    __syncthreads();
+    // values: feature f = tid % DK, keys jj = tid / DK, + 256/DK, ...
+    {
+        constexpr int G = 256 / DK;
+        const int f = tid % DK, g = tid / DK;
+        float acc = 0.0f;
+        for (int jj = g; jj < j1 - j0; jj += G) {
+            const int j = j0 + jj;
+            const float *vr = (append && j == p) ? vn + ho : V + (size_t)j * d + ho;
+            acc = fmaf(sc[jj], vr[f], acc);
+        }
+        red[g][f] = acc;
+    }
+    __syncthreads();
+    if (tid < DK) {
+        float o = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 256 / DK; g++) o += red[g][tid];
+        op[tid] = o;
+    }
+    if (tid == 0) {
+        float l = 0.0f;
+        for (int i = 0; i < j1 - j0; i++) l += sc[i];
+        mlp[0] = m;
+        mlp[1] = l;
+    }
+}
+
+// out[h] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M) over the used splits
+template <int DK>
+__global__ __launch_bounds__(DK) void k_att_combine(const float *__restrict__ o_part,
+                                                    const float *__restrict__ ml_part, const int *__restrict__ st,
+                                                    int n_fixed, float *__restrict__ out, int nsplit) {
+    const int h = blockIdx.x, f = threadIdx.x;
+    const int n = n_fixed > 0 ? n_fixed : st[0] + 1;
+    const int ns = min((n + KC - 1) / KC, nsplit);
+    const float *ml = ml_part + (size_t)h * nsplit * 2;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; s++) M = fmaxf(M, ml[2 * s]);
+    float L = 0.0f, o = 0.0f;
+    for (int s = 0; s < ns; s++) {
+        const float c = expf(ml[2 * s] - M);
+        L += ml[2 * s + 1] * c;
+        o += o_part[((size_t)h * nsplit + s) * DK + f] * c;
+    }
+    out[h * DK + f] = o / L;
+}
+
+// First maximum of logits[0..vocab) (the reference's strict > scan) -> st[1];
+// optionally the logits to logits_out[p]; then p + 1 -> st[0].
+__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logits, int vocab, int *st,
+                                                 float *__restrict__ logits_out) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    const int tid = threadIdx.x, p = st[0];
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = tid; i < vocab; i += 1024) {
+        const float v = logits[i];
+        if (v > best) best = v, idx = i;   // i grows: a tie keeps the earlier index
+        if (logits_out) logits_out[(size_t)p * vocab + i] = v;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
+        if (ov > best || (ov == best && oi < idx)) best = ov, idx = oi;
+    }
+    if ((tid & 63) == 0) bv[tid >> 6] = best, bi[tid >> 6] = idx;
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; w++)
+            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) best = bv[w], idx = bi[w];
+        st[1] = idx == 0x7fffffff ? 0 : idx;
+        st[0] = p + 1;
+    }
+}
+
+__global__ void k_bias_rows(float *__restrict__ y, const float *__restrict__ b, size_t rows, int d) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < rows * (size_t)d) y[i] = y[i] + b[i % d];
+}
+
+__global__ void k_set_state(int *st, int p, int cur) {
+    st[0] = p;
+    st[1] = cur;
+}
+
+}  // namespace
+
+int mh_att_splits(int n) { return (n + KC - 1) / KC; }
+
+hipError_t mh_launch_embed_ln(const float *emb, const float *pos, const int *prompt, int n_prompt, const int *st,
+                              const float *w, const float *b, float *x, int d, hipStream_t s) {
+    if (d > LN_T * LN_V) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_embed_ln, dim3(1), dim3(LN_T), 0, s, emb, pos, prompt, n_prompt, st, w, b, x, d);
+    return hipGetLastError();
+}
+
+hipError_t mh_launch_ln(const float *x, const float *w, const float *b, float *y, int d, hipStream_t s) {
+    if (d > LN_T * LN_V) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_ln, dim3(1), dim3(LN_T), 0, s, x, w, b, y, d);
+    return hipGetLastError();
+}
+
+hipError_t mh_launch_attend1(const float *q, float *K, float *V, const float *kn, const float *vn, const int *st,
+                             int n_fixed, int d, int H, float *o_part, float *ml_part, int nsplit, float *out,
+                             hipStream_t s) {
+    const int dk = d / H;
+    const float scale = 1.0f / sqrtf((float)dk);
+    if (dk == 128) {
+        hipLaunchKernelGGL(k_att_part<128>, dim3(H, nsplit), dim3(256), 0, s, q, K, V, kn, vn, st, n_fixed, d, scale,
+                           o_part, ml_part, nsplit);
+        hipLaunchKernelGGL(k_att_combine<128>, dim3(H), dim3(128), 0, s, o_part, ml_part, st, n_fixed, out, nsplit);
+    } else if (dk == 64) {
+        hipLaunchKernelGGL(k_att_part<64>, dim3(H, nsplit), dim3(256), 0, s, q, K, V, kn, vn, st, n_fixed, d, scale,
+                           o_part, ml_part, nsplit);
+        hipLaunchKernelGGL(k_att_combine<64>, dim3(H), dim3(64), 0, s, o_part, ml_part, st, n_fixed, out, nsplit);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t mh_launch_argmax(const float *logits, int vocab, int *st, float *logits_out, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, logits, vocab, st, logits_out);
+    return hipGetLastError();
+}
+
+hipError_t mh_launch_bias_rows(float *y, const float *b, size_t rows, int d, hipStream_t s) {
+    const size_t n = rows * (size_t)d;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_bias_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y, b, rows, d);
+    return hipGetLastError();
+}
+
+hipError_t mh_launch_set_state(int *st, int p, int cur, hipStream_t s) {
+    hipLaunchKernelGGL(k_set_state, dim3(1), dim3(1), 0, s, st, p, cur);
+    return hipGetLastError();
+}

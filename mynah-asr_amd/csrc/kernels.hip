@@ -16,6 +16,7 @@
 // The 32x32x16 MFMA is used throughout: on gfx950 it issues twice the work of
 // the 16x16x32 shape per cycle (measured 2.04 vs 1.19 PFLOP/s f16).
 #include "fmt.h"
+#include "launch.h"
 
 #define KSTEPS 4  // ksteps per chunk
 #define HSTEPS 8  // half-steps per chunk
@@ -505,7 +506,7 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
 // runs in registers.
 template <int QT, int NW, int WNG, bool VEC>
 __global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const float *__restrict__ x, int M,
-                                                  float *__restrict__ y, int act) {
+                                                  float *y, GEpi ep) {
     extern __shared__ float part[];  // [Kc][WNG][8][64] chunk results, then pf [Kc][16]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int hh = lane >> 5, col = lane & 31;
@@ -567,7 +568,13 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const float *__restric
             if (m >= M) continue;
             float v = total[e];
             if constexpr (QT == QT_F32) v = ldexpf(v, -shw);
-            y[(size_t)m * W.n + n] = act ? silu_f(v) : v;
+            // y = act(W x + b) + res, in the order of the reference's mv() and
+            // its callers (decoder_aed.c:15-19, 207-210)
+            if (ep.bias) v = v + ep.bias[n];
+            if (ep.act == 1) v = silu_f(v);
+            else if (ep.act == 2) v = v < 0.0f ? 0.0f : v;
+            if (ep.res) v = ep.res[(size_t)m * W.n + n] + v;
+            y[(size_t)m * W.n + n] = v;
         }
     }
 }
@@ -793,7 +800,7 @@ __global__ void k_silu(float *__restrict__ x, size_t n) {
 #include "launch.h"
 
 template <int QT, int NW, int WNG, bool VEC>
-static hipError_t launch_gemv1(const DevW &W, const float *x, int M, float *y, int act, hipStream_t st) {
+static hipError_t launch_gemv1(const DevW &W, const float *x, int M, float *y, GEpi act, hipStream_t st) {
     const int Kc = W.Kp / 128;
     const size_t lds = ((size_t)Kc * WNG * 8 * 64 + (size_t)Kc * 16) * sizeof(float);
     static bool attr = false;  // allow dynamic LDS beyond 64 KiB (gfx950 has 160 KiB)
@@ -807,7 +814,7 @@ static hipError_t launch_gemv1(const DevW &W, const float *x, int M, float *y, i
 }
 
 template <int QT, int NW, int WNG>
-static hipError_t launch_gemv(const DevW &W, const float *x, int M, int vec, float *y, int act,
+static hipError_t launch_gemv(const DevW &W, const float *x, int M, int vec, float *y, GEpi act,
                               hipStream_t st) {
     if (vec) return launch_gemv1<QT, NW, WNG, true>(W, x, M, y, act, st);
     return launch_gemv1<QT, NW, WNG, false>(W, x, M, y, act, st);
@@ -822,7 +829,7 @@ static int gemv_wng(const DevW &W) {
 }
 
 template <int QT>
-static hipError_t gemv_t(const DevW &W, const float *x, int M, int vec, float *y, int act,
+static hipError_t gemv_t(const DevW &W, const float *x, int M, int vec, float *y, GEpi act,
                          hipStream_t st) {
     const int Kc = W.Kp / 128, wng = gemv_wng(W);
     if (wng == 2) {
@@ -867,9 +874,14 @@ static hipError_t gemm_t(const DevW &W, const uint8_t *xp, const float *xs16, co
 
 bool mh_use_gemv(const DevW &W, int M) { return M <= 16 && (W.Kp / 128) * gemv_wng(W) <= 64; }
 
+hipError_t mh_launch_gemv_epi(int qtype, const DevW &W, const float *x, int M, int vec, float *y, GEpi ep,
+                              hipStream_t st) {
+    MH_DISPATCH(gemv_t, qtype, W, x, M, vec, y, ep, st)
+}
+
 hipError_t mh_launch_gemv(int qtype, const DevW &W, const float *x, int M, int vec, float *y, int act,
                           hipStream_t st) {
-    MH_DISPATCH(gemv_t, qtype, W, x, M, vec, y, act, st)
+    return mh_launch_gemv_epi(qtype, W, x, M, vec, y, GEpi{act, nullptr, nullptr}, st);
 }
 
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,

@@ -16,6 +16,15 @@ hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_
 bool mh_use_gemv(const DevW &W, int M);
 hipError_t mh_launch_gemv(int qtype, const DevW &W, const float *x, int M, int vec, float *y, int act,
                           hipStream_t st);
+// GEMV epilogue: y = act(W x + bias) + res; act 0 none, 1 SiLU, 2 ReLU; bias [n]
+// and res [M, n] may be null; res may alias y
+struct GEpi {
+    int act;
+    const float *bias;
+    const float *res;
+};
+hipError_t mh_launch_gemv_epi(int qtype, const DevW &W, const float *x, int M, int vec, float *y, GEpi ep,
+                              hipStream_t st);
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
                           const float *xpf, float *y, int M, int act, hipStream_t st);
 // The FFN's first product with SiLU, its output prepared as the input of a
@@ -39,3 +48,17 @@ bool mh_attn_supported(int dk);
 hipError_t mh_launch_relpos_attn(const float *q, const float *k, const float *v, const float *rk,
                                  const float *bias_u, const float *bias_v, float *ctx, int T, int d, int H,
                                  int left, int right, int nseq, hipStream_t st);
+
+// AED decoder step kernels (decoder.hip); st = device int[2]: position p, last argmax
+int mh_att_splits(int n);   // attention splits for n keys
+hipError_t mh_launch_embed_ln(const float *emb, const float *pos, const int *prompt, int n_prompt, const int *st,
+                              const float *w, const float *b, float *x, int d, hipStream_t s);
+hipError_t mh_launch_ln(const float *x, const float *w, const float *b, float *y, int d, hipStream_t s);
+// out = attention of q over n keys (n_fixed, or p + 1 with the cache append of kn, vn when n_fixed == 0);
+// o_part [H][nsplit][dk], ml_part [H][nsplit][2]
+hipError_t mh_launch_attend1(const float *q, float *K, float *V, const float *kn, const float *vn, const int *st,
+                             int n_fixed, int d, int H, float *o_part, float *ml_part, int nsplit, float *out,
+                             hipStream_t s);
+hipError_t mh_launch_argmax(const float *logits, int vocab, int *st, float *logits_out, hipStream_t s);
+hipError_t mh_launch_bias_rows(float *y, const float *b, size_t rows, int d, hipStream_t s);
+hipError_t mh_launch_set_state(int *st, int p, int cur, hipStream_t s);

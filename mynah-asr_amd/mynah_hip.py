@@ -38,6 +38,7 @@ HIP_SYMBOLS = [
     "mynah_asr_hip_qgemm_dev", "mynah_asr_hip_dequant_dev", "mynah_asr_hip_prep_dev",
     "mynah_asr_hip_qgemm_prepped_dev", "mynah_asr_hip_qffn_dev", "mynah_asr_hip_qqkv_dev",
     "mynah_asr_hip_relpos_attention_dev", "mynah_asr_hip_relpos_attention",
+    "mynah_asr_hip_aed_decode_dev", "mynah_asr_hip_aed_forced_dev",
 ]
 HOST_SYMBOLS = [
     "mynah_asr_set_backend", "mynah_asr_backend", "mynah_asr_gemm_wt", "mynah_asr_silu",
@@ -49,6 +50,22 @@ HOST_SYMBOLS = [
 ]
 
 _P = C.c_void_p
+
+
+class AedLayerC(C.Structure):
+    """mynah_asr_hip_aed_layer (include/mynah_asr_hip.h)."""
+    _fields_ = [(f, C.c_void_p) for f in (
+        "ln_self_w", "ln_self_b", "sq", "sk", "sv", "so", "sq_b", "sk_b", "sv_b", "so_b",
+        "ln_cross_w", "ln_cross_b", "cq", "ck", "cv", "co", "cq_b", "ck_b", "cv_b", "co_b",
+        "ln_ffn_w", "ln_ffn_b", "ff1", "ff2", "ff1_b", "ff2_b")]
+
+
+class AedC(C.Structure):
+    """mynah_asr_hip_aed (include/mynah_asr_hip.h)."""
+    _fields_ = [("n_layers", C.c_int), ("d", C.c_int), ("n_heads", C.c_int), ("ffn", C.c_int),
+                ("vocab", C.c_int), ("max_seq", C.c_int)] + \
+               [(f, C.c_void_p) for f in ("proj", "proj_b", "emb", "pos", "embln_w", "embln_b", "fin_w", "fin_b",
+                                          "head", "head_b")] + [("layers", C.POINTER(AedLayerC))]
 
 
 class WDesc(C.Structure):
@@ -103,6 +120,10 @@ class HipLib:
         if hasattr(L, "mynah_asr_hip_relpos_attention_dev"):
             L.mynah_asr_hip_relpos_attention_dev.argtypes = [_P] * 7 + [C.c_int] * 6 + [_P]
             L.mynah_asr_hip_relpos_attention.argtypes = [_P] * 7 + [C.c_int] * 5
+        if hasattr(L, "mynah_asr_hip_aed_decode_dev"):
+            L.mynah_asr_hip_aed_decode_dev.argtypes = [C.POINTER(AedC), _P, C.c_int, _P, C.c_int, C.c_int, _P,
+                                                       C.c_int, _P]
+            L.mynah_asr_hip_aed_forced_dev.argtypes = [C.POINTER(AedC), _P, C.c_int, _P, C.c_int, _P, _P]
         L.mynah_asr_hip_qgemm.argtypes = [C.POINTER(WDesc), _P, _P, C.c_int]
         L.mynah_asr_hip_qffn.argtypes = [C.POINTER(WDesc), C.POINTER(WDesc), _P, _P, C.c_int]
         L.mynah_asr_hip_qqkv.argtypes = [C.POINTER(WDesc)] * 3 + [_P] * 4 + [C.c_int]
@@ -265,6 +286,83 @@ def host_relpos_attention(lib, q, k, v, rk, bias_u, bias_v, H: int, left: int = 
                                              _ptr(ctx), T, d, H, left, right)
     lib._check(rc, "relpos_attention")
     return ctx
+
+
+class DeviceAed:
+    """An AED decoder on the device. `params` holds the reference's tensors
+    (src/decoder_aed.h:12-36) as f32 arrays: emb, pos, embln_w/_b, fin_w/_b,
+    head, head_b, optional proj/proj_b, and `layers`, a list of dicts with
+    sq..ff2 ([n, k] weights), their *_b biases and ln_{self,cross,ffn}_{w,b}.
+    Linears are quantized to `qtype` by the library's quantizers and made
+    resident; everything else is copied to device tensors (torch)."""
+
+    LINEARS = ("sq", "sk", "sv", "so", "cq", "ck", "cv", "co", "ff1", "ff2")
+
+    def __init__(self, lib: "HipLib", params: dict, n_heads: int, qtype: int):
+        import torch
+        self.lib, self.torch = lib, torch
+        self._keep = []
+        self.weights = {}       # name -> Weight (host blocks, for the oracle's decoder)
+
+        def dev(a):
+            if a is None:
+                return None
+            t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+            self._keep.append(t)
+            return t.data_ptr()
+
+        def lin(name, w):
+            if w is None:
+                return None
+            hw = Weight.make(lib, qtype, np.asarray(w, np.float32))
+            dw = DeviceWeight(lib, hw)
+            self.weights[name] = hw
+            self._keep.append(dw)
+            return dw.h
+
+        layers = params["layers"]
+        self._layers = (AedLayerC * max(len(layers), 1))()
+        for i, Ld in enumerate(layers):
+            Lc = self._layers[i]
+            for f, _ in AedLayerC._fields_:
+                setattr(Lc, f, lin(f"{i}.{f}", Ld[f]) if f in self.LINEARS else dev(Ld[f]))
+        d = params["emb"].shape[1]
+        self.c = AedC(len(layers), d, n_heads, layers[0]["ff1"].shape[0] if layers else 1,
+                      params["emb"].shape[0], params["pos"].shape[0])
+        self.c.proj = lin("proj", params.get("proj"))
+        self.c.proj_b = dev(params.get("proj_b"))
+        for f in ("emb", "pos", "embln_w", "embln_b", "fin_w", "fin_b", "head_b"):
+            setattr(self.c, f, dev(params[f]))
+        self.c.head = lin("head", params["head"])
+        self.c.layers = self._layers
+        torch.cuda.synchronize()
+
+    def forced(self, enc_ptr: int, T: int, tokens, stream: int = 0) -> np.ndarray:
+        """Logits [n, vocab] of every position (mynah_asr_hip_aed_forced_dev)."""
+        torch = self.torch
+        tok = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = torch.empty((len(tok), self.c.vocab), dtype=torch.float32, device="cuda")
+        rc = self.lib.L.mynah_asr_hip_aed_forced_dev(C.byref(self.c), enc_ptr, T, tok.ctypes.data, len(tok),
+                                                     out.data_ptr(), stream or None)
+        self.lib._check(rc, "aed_forced_dev")
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+
+    def decode(self, enc_ptr: int, T: int, prompt, eos: int, cap: int, stream: int = 0) -> list:
+        """Greedy tokens (mynah_asr_hip_aed_decode_dev)."""
+        pr = np.ascontiguousarray(prompt, dtype=np.int32)
+        toks = np.zeros(max(cap, 1), dtype=np.int32)
+        n = self.lib.L.mynah_asr_hip_aed_decode_dev(C.byref(self.c), enc_ptr, T, pr.ctypes.data, len(pr), eos,
+                                                    toks.ctypes.data, cap, stream or None)
+        if n < 0:
+            raise RuntimeError(f"aed_decode_dev failed: {self.lib.last_error()}")
+        return [int(t) for t in toks[:n]]
+
+    def close(self):
+        for k in self._keep:
+            if isinstance(k, DeviceWeight):
+                k.close()
+        self._keep = []
 
 
 def evict(lib: HipLib, w: Weight) -> None:
