@@ -300,6 +300,53 @@ def run_attention(B, M_, T=750, d=1024, H=8, nseq=16, reps=10):
     return out
 
 
+def run_aed(B, M_, d=1024, H=8, ffn=4096, vocab=16384, n_layers=4, T=750, cap=64, qt=None):
+    """The AED decoder on the device (src/decoder_aed.c:139-232) at BASELINE
+    config 3's shapes: greedy decoding of `cap` tokens after a 4-token prompt
+    (a host read-back per token for the EOS check), and the same steps
+    teacher-forced (no read-back: the graph replays back to back)."""
+    torch, lib = B.torch, B.lib
+    qt = M_.Q8_0 if qt is None else qt
+    r = np.random.default_rng(400)
+    f = lambda *s, sc=0.02: (r.standard_normal(s) * sc).astype(np.float32)
+    layers = []
+    for _ in range(n_layers):
+        L = {nm: f(d, d) for nm in ("sq", "sk", "sv", "so", "cq", "ck", "cv", "co")}
+        L.update({nm + "_b": f(d) for nm in ("sq", "sk", "sv", "so", "cq", "ck", "cv", "co")})
+        L.update(ff1=f(ffn, d), ff1_b=f(ffn), ff2=f(d, ffn), ff2_b=f(d))
+        for nm in ("self", "cross", "ffn"):
+            L[f"ln_{nm}_w"], L[f"ln_{nm}_b"] = 1 + f(d), f(d)
+        layers.append(L)
+    max_seq = 4 + cap + 1
+    params = {"emb": f(vocab, d, sc=1.0), "pos": f(max_seq, d, sc=0.3), "embln_w": 1 + f(d), "embln_b": f(d),
+              "fin_w": 1 + f(d), "fin_b": f(d), "head": f(vocab, d), "head_b": f(vocab), "layers": layers}
+    dev = M_.DeviceAed(lib, params, H, qt)
+    enc = B.dev(f(T, d, sc=1.0))
+    prompt = [1, 2, 3, 4]
+    dev.decode(enc.data_ptr(), T, prompt, -1, 4)   # warm
+    B.sync()
+    t0 = time.perf_counter()
+    toks = dev.decode(enc.data_ptr(), T, prompt, -1, cap)
+    t1 = time.perf_counter()
+    forced = prompt + toks[:cap - 1]
+    dev.forced(enc.data_ptr(), T, forced)
+    t2 = time.perf_counter()
+    dev.forced(enc.data_ptr(), T, forced)
+    t3 = time.perf_counter()
+    positions = len(prompt) - 1 + len(toks)
+    # bytes one position streams: the step's linears, the cross K/V, the self cache (mean length)
+    wb = lambda n, k: M_.weight_bytes(qt, n, k)
+    per_layer = 6 * wb(d, d) + wb(ffn, d) + wb(d, ffn) + 2 * 4 * T * d + 2 * 4 * d * (len(forced) / 2)
+    step_bytes = n_layers * per_layer + wb(vocab, d)
+    us_forced = (t3 - t2) * 1e6 / len(forced)
+    dev.close()
+    return {"d": d, "heads": H, "ffn": ffn, "vocab": vocab, "layers": n_layers, "T": T, "format": M_.NAMES[qt],
+            "tokens": len(toks), "greedy_us_per_token": round((t1 - t0) * 1e6 / positions, 1),
+            "forced_us_per_position": round(us_forced, 1), "bytes_per_position": int(step_bytes),
+            "forced_hbm_gbps": round(step_bytes / (us_forced * 1e-6) / 1e9, 1),
+            "note": "host wall clock around one call (graph capture, cross K/V products and copies included)"}
+
+
 def profiled_traffic():
     """HBM bytes per launch of the roofline kernel, as measured by the two
     rocprofv3 --pmc passes recorded under profiles/ (None if absent)."""
@@ -344,6 +391,8 @@ def main():
     ap.add_argument("--attention", action="store_true",
                     help="only the rel-pos attention core (T=750, 16 segments, full and [70, 13] windows), "
                          "one JSON line")
+    ap.add_argument("--aed", action="store_true",
+                    help="only the AED decoder (config 3 shapes, 4 layers, T=750, Q8_0), one JSON line")
     ap.add_argument("--profile", action="store_true",
                     help="counter-calibration run for rocprofv3 --pmc: a 256 MiB device copy, then "
                          "the dominant GEMM (Q8_0 4096->1024, M=6000) alone, 3 launches each")
@@ -366,6 +415,9 @@ def main():
         return
     if args.attention:
         print(json.dumps({"relpos_attention": run_attention(B, M_)}), flush=True)
+        return
+    if args.aed:
+        print(json.dumps({"aed_decoder": run_aed(B, M_)}), flush=True)
         return
 
     log("[bench] encoder set Q8_0 M=6000")
@@ -392,6 +444,8 @@ def main():
         details["f32_m6000"] = {"tflops": round(flf / (msf * 1e-3) / 1e12, 2), "rows": rowsf}
         log("[bench] rel-pos attention core T=750 x 16 segments")
         details["relpos_attention"] = run_attention(B, M_)
+        log("[bench] AED decoder, config 3 shapes")
+        details["aed_decoder"] = run_aed(B, M_)
         log("[bench] decoder GEMVs")
         gv = []
         for qt in (M_.Q8_0, M_.Q4_0):

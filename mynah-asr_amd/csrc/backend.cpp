@@ -342,7 +342,42 @@ int gemv_epi(const mynah_asr_hip_weight *W, const float *x, float *y, int act, c
         if (e_ != hipSuccess) return fail("decoder launch failed", hipGetErrorString(e_)); \
     } while (0)
 
-// One decoding position: every launch reads p and the token from b.st.
+// One decoding position: every launch reads p and the token from b.st. The
+// layer norms and the merge of the attention splits run as the prologue of
+// the GEMV that consumes them; q, k and v are one launch.
+int aed_gemv(const mynah_asr_hip_weight *const *Ws, float *const *ys, const GEpi *eps, int n, const GPro &pro,
+             const float *x, hipStream_t st) {
+    GJobs J{};
+    for (int i = 0; i < 3; i++) {
+        const int j = i < n ? i : 0;
+        J.W[i] = Ws[j]->dw;
+        J.y[i] = ys[j];
+        J.ep[i] = eps[j];
+    }
+    J.n = n;
+    const int vec = x && (Ws[0]->dw.k % 8 == 0) && (((uintptr_t)x & 15) == 0);
+    hipError_t e = mh_launch_gemv_jobs(Ws[0]->qtype, J, x, 1, vec, pro, st);
+    return e == hipSuccess ? 0 : fail("gemv launch failed", hipGetErrorString(e));
+}
+
+GPro pro_ln(const float *x, const float *w, const float *b) {
+    GPro p{};
+    p.kind = GPRO_LN;
+    p.x = x, p.w = w, p.b = b;
+    return p;
+}
+
+GPro pro_comb(const AedBufs &b, int n_fixed, int H) {
+    GPro p{};
+    p.kind = GPRO_COMB;
+    p.opart = b.opart, p.ml = b.ml, p.st = b.st, p.n_fixed = n_fixed, p.nsplit = b.nsplit, p.H = H;
+    return p;
+}
+
+int aed_one(const mynah_asr_hip_weight *W, float *y, GEpi ep, const GPro &pro, hipStream_t st) {
+    return aed_gemv(&W, &y, &ep, 1, pro, nullptr, st);
+}
+
 int aed_step(const mynah_asr_hip_aed *a, const AedBufs &b, int T, int max_len, int n_prompt, float *logits_out,
              hipStream_t st) {
     const int d = a->d, H = a->n_heads;
@@ -353,24 +388,30 @@ int aed_step(const mynah_asr_hip_aed *a, const AedBufs &b, int T, int max_len, i
         float *SK = b.skv + 2 * (size_t)li * md, *SV = SK + md;
         float *CK = b.ckv + 2 * (size_t)li * td, *CV = CK + td;
         // causal self attention, its k and v rows appended to the cache at p
-        AED_TRY(mh_launch_ln(b.x, L->ln_self_w, L->ln_self_b, b.xn, d, st));
-        if (gemv_epi(L->sq, b.xn, b.q, 0, L->sq_b, nullptr, st) || gemv_epi(L->sk, b.xn, b.kn, 0, L->sk_b, nullptr, st) ||
-            gemv_epi(L->sv, b.xn, b.vn, 0, L->sv_b, nullptr, st))
-            return -1;
-        AED_TRY(mh_launch_attend1(b.q, SK, SV, b.kn, b.vn, b.st, 0, d, H, b.opart, b.ml, b.nsplit, b.att, st));
-        if (gemv_epi(L->so, b.att, b.x, 0, L->so_b, b.x, st)) return -1;
+        const mynah_asr_hip_weight *qkv[3] = {L->sq, L->sk, L->sv};
+        float *const qkv_y[3] = {b.q, b.kn, b.vn};
+        const GEpi qkv_ep[3] = {{0, L->sq_b, nullptr}, {0, L->sk_b, nullptr}, {0, L->sv_b, nullptr}};
+        const bool same = L->sk->qtype == L->sq->qtype && L->sv->qtype == L->sq->qtype;
+        const GPro ln_self = pro_ln(b.x, L->ln_self_w, L->ln_self_b);
+        if (same) {
+            if (aed_gemv(qkv, qkv_y, qkv_ep, 3, ln_self, nullptr, st)) return -1;
+        } else {
+            for (int i = 0; i < 3; i++)
+                if (aed_one(qkv[i], qkv_y[i], qkv_ep[i], ln_self, st)) return -1;
+        }
+        AED_TRY(mh_launch_attend1(b.q, SK, SV, b.kn, b.vn, b.st, 0, d, H, b.opart, b.ml, b.nsplit, nullptr, st));
+        if (aed_one(L->so, b.x, GEpi{0, L->so_b, b.x}, pro_comb(b, 0, H), st)) return -1;
         // cross attention over the projected encoder output
-        AED_TRY(mh_launch_ln(b.x, L->ln_cross_w, L->ln_cross_b, b.xn, d, st));
-        if (gemv_epi(L->cq, b.xn, b.q, 0, L->cq_b, nullptr, st)) return -1;
-        AED_TRY(mh_launch_attend1(b.q, CK, CV, nullptr, nullptr, b.st, T, d, H, b.opart, b.ml, b.nsplit, b.att, st));
-        if (gemv_epi(L->co, b.att, b.x, 0, L->co_b, b.x, st)) return -1;
+        if (aed_one(L->cq, b.q, GEpi{0, L->cq_b, nullptr}, pro_ln(b.x, L->ln_cross_w, L->ln_cross_b), st)) return -1;
+        AED_TRY(mh_launch_attend1(b.q, CK, CV, nullptr, nullptr, b.st, T, d, H, b.opart, b.ml, b.nsplit, nullptr, st));
+        if (aed_one(L->co, b.x, GEpi{0, L->co_b, b.x}, pro_comb(b, T, H), st)) return -1;
         // ReLU FFN
-        AED_TRY(mh_launch_ln(b.x, L->ln_ffn_w, L->ln_ffn_b, b.xn, d, st));
-        if (gemv_epi(L->ff1, b.xn, b.ff, 2, L->ff1_b, nullptr, st) || gemv_epi(L->ff2, b.ff, b.x, 0, L->ff2_b, b.x, st))
+        const GEpi ff2_ep{0, L->ff2_b, b.x};
+        if (aed_one(L->ff1, b.ff, GEpi{2, L->ff1_b, nullptr}, pro_ln(b.x, L->ln_ffn_w, L->ln_ffn_b), st) ||
+            aed_gemv(&L->ff2, &b.x, &ff2_ep, 1, GPro{}, b.ff, st))
             return -1;
     }
-    AED_TRY(mh_launch_ln(b.x, a->fin_w, a->fin_b, b.xn, d, st));
-    if (gemv_epi(a->head, b.xn, b.logits, 0, a->head_b, nullptr, st)) return -1;
+    if (aed_one(a->head, b.logits, GEpi{0, a->head_b, nullptr}, pro_ln(b.x, a->fin_w, a->fin_b), st)) return -1;
     AED_TRY(mh_launch_argmax(b.logits, a->vocab, b.st, logits_out, st));
     return 0;
 }

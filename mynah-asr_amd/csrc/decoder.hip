@@ -2,12 +2,12 @@
 // (the reference's src/decoder_aed.c:139-232), device-resident:
 //
 //   k_embed_ln   x = LN(emb[token] + pos[p])                  decoder_aed.c:183-186
-//   k_ln         y = LN(x)                                    decoder_aed.c:21-28
 //   k_att_part   one query against a split of KC keys, per head: running max,
 //                sum of exponentials and the weighted sum of V rows; with
 //                `append`, the split holding key p first stores this step's
 //                k and v rows into the self-attention cache  decoder_aed.c:124-137, 195-198
-//   k_att_combine the splits of each head merged               (same)
+//   k_att_combine the splits of each head merged (the decoder step merges them
+//                instead in the prologue of the GEMV that reads the result)
 //   k_argmax     first maximum of the logits, the next token; advances p
 //                                                              decoder_aed.c:217-222
 //   k_bias_rows  y[t] += b                                    decoder_aed.c:132-136
@@ -26,7 +26,7 @@ namespace {
 
 constexpr int LN_T = 256;   // threads of the one-workgroup row kernels
 constexpr int LN_V = 16;    // values per thread: d <= 4096
-constexpr int KC = 64;      // keys per attention split
+constexpr int KC = MH_ATT_KC;   // keys per attention split
 
 // Sum over the workgroup in double (the reference's ln accumulates in double).
 __device__ double block_sum(double v, double *red) {
@@ -85,17 +85,6 @@ __global__ __launch_bounds__(LN_T) void k_embed_ln(const float *__restrict__ emb
     ln_store(v, d, w, b, x);
 }
 
-__global__ __launch_bounds__(LN_T) void k_ln(const float *__restrict__ x, const float *__restrict__ w,
-                                             const float *__restrict__ b, float *__restrict__ y, int d) {
-    float v[LN_V];
-#pragma unroll
-    for (int u = 0; u < LN_V; u++) {
-        const int i = threadIdx.x + LN_T * u;
-        v[u] = i < d ? x[i] : 0.0f;
-    }
-    ln_store(v, d, w, b, y);
-}
-
 // Workgroup (head h, split s) over keys [s*KC, min((s+1)*KC, n)), n = n_fixed,
 // or p + 1 for self attention (n_fixed = 0). 256 threads: for the scores, 4
 // threads per key (dk/4 features each); for the values, thread = (feature,
@@ -149,20 +138,32 @@ __global__ __launch_bounds__(256) void k_att_part(const float *__restrict__ q, f
         if (part == 0 && jj < KC) sc[jj] = j < j1 ? scale * acc : -INFINITY;
     }
     __syncthreads();
-    float m = -INFINITY;
-    for (int i = 0; i < KC; i++) m = fmaxf(m, sc[i]);
+    // max and sum of exponentials over the split: one wave, one key per lane
+    static_assert(KC == 64, "one key per lane of a wave");
+    __shared__ float mls[2];
+    if (tid < 64) {
+        float m = sc[tid];
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float e = tid < j1 - j0 ? expf(sc[tid] - m) : 0.0f;
+        sc[tid] = e;
+        float l = e;
+        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+        if (tid == 0) mls[0] = m, mls[1] = l;
+    }
     __syncthreads();
-    if (tid < KC) sc[tid] = tid < j1 - j0 ? expf(sc[tid] - m) : 0.0f;
-    __syncthreads();
-    // values: feature f = tid % DK, keys jj = tid / DK, + 256/DK, ...
+    // values: feature f = tid % DK, keys jj = tid / DK, + 256/DK, ... (all loads in flight)
     {
         constexpr int G = 256 / DK;
-        const int f = tid % DK, g = tid / DK;
+        const int f = tid % DK, g = tid / DK, cnt = j1 - j0;
         float acc = 0.0f;
-        for (int jj = g; jj < j1 - j0; jj += G) {
-            const int j = j0 + jj;
-            const float *vr = (append && j == p) ? vn + ho : V + (size_t)j * d + ho;
-            acc = fmaf(sc[jj], vr[f], acc);
+#pragma unroll
+        for (int t = 0; t < KC / G; t++) {
+            const int jj = g + G * t;
+            if (jj < cnt) {
+                const int j = j0 + jj;
+                const float *vr = (append && j == p) ? vn + ho : V + (size_t)j * d + ho;
+                acc = fmaf(sc[jj], vr[f], acc);
+            }
         }
         red[g][f] = acc;
     }
@@ -173,12 +174,7 @@ __global__ __launch_bounds__(256) void k_att_part(const float *__restrict__ q, f
         for (int g = 0; g < 256 / DK; g++) o += red[g][tid];
         op[tid] = o;
     }
-    if (tid == 0) {
-        float l = 0.0f;
-        for (int i = 0; i < j1 - j0; i++) l += sc[i];
-        mlp[0] = m;
-        mlp[1] = l;
-    }
+    if (tid == 0) mlp[0] = mls[0], mlp[1] = mls[1];
 }
 
 // out[h] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M) over the used splits
@@ -242,18 +238,12 @@ __global__ void k_set_state(int *st, int p, int cur) {
 
 }  // namespace
 
-int mh_att_splits(int n) { return (n + KC - 1) / KC; }
+int mh_att_splits(int n) { return mh_att_splits_dev(n); }
 
 hipError_t mh_launch_embed_ln(const float *emb, const float *pos, const int *prompt, int n_prompt, const int *st,
                               const float *w, const float *b, float *x, int d, hipStream_t s) {
     if (d > LN_T * LN_V) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_embed_ln, dim3(1), dim3(LN_T), 0, s, emb, pos, prompt, n_prompt, st, w, b, x, d);
-    return hipGetLastError();
-}
-
-hipError_t mh_launch_ln(const float *x, const float *w, const float *b, float *y, int d, hipStream_t s) {
-    if (d > LN_T * LN_V) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_ln, dim3(1), dim3(LN_T), 0, s, x, w, b, y, d);
     return hipGetLastError();
 }
 
@@ -265,11 +255,13 @@ hipError_t mh_launch_attend1(const float *q, float *K, float *V, const float *kn
     if (dk == 128) {
         hipLaunchKernelGGL(k_att_part<128>, dim3(H, nsplit), dim3(256), 0, s, q, K, V, kn, vn, st, n_fixed, d, scale,
                            o_part, ml_part, nsplit);
-        hipLaunchKernelGGL(k_att_combine<128>, dim3(H), dim3(128), 0, s, o_part, ml_part, st, n_fixed, out, nsplit);
+        if (out)
+            hipLaunchKernelGGL(k_att_combine<128>, dim3(H), dim3(128), 0, s, o_part, ml_part, st, n_fixed, out, nsplit);
     } else if (dk == 64) {
         hipLaunchKernelGGL(k_att_part<64>, dim3(H, nsplit), dim3(256), 0, s, q, K, V, kn, vn, st, n_fixed, d, scale,
                            o_part, ml_part, nsplit);
-        hipLaunchKernelGGL(k_att_combine<64>, dim3(H), dim3(64), 0, s, o_part, ml_part, st, n_fixed, out, nsplit);
+        if (out)
+            hipLaunchKernelGGL(k_att_combine<64>, dim3(H), dim3(64), 0, s, o_part, ml_part, st, n_fixed, out, nsplit);
     } else {
         return hipErrorInvalidValue;
     }

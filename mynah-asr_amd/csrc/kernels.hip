@@ -504,17 +504,113 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
 // c = w, w+NW, ...; the chunk results of rows 0..15 and their fold factors
 // meet in LDS and are folded in chunk order from zero — the sequence k_gemm
 // runs in registers.
+//
+// A launch may carry up to three products of one input (jobs of the same
+// format and shape: the workgroups of job i follow those of job i-1), and for
+// M = 1 a prologue may build the input row in LDS, per workgroup: the layer
+// norm of x, or the merge of attention splits (GPro).
+
+// sum over the workgroup's threads in double
+template <int NT>
+__device__ double wg_sum(double v, double *red) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < NT / 64; i++) s += red[i];
+    return s;
+}
+
+// xs[0..Kp) = the prologue's row (zero past K); K <= 4096
+template <int NT>
+__device__ void gemv_prologue(const GPro &pro, int K, int Kp, float *xs) {
+    __shared__ double red[NT / 64];
+    __shared__ float hm[64], hl[64];
+    constexpr int V = 4096 / NT;
+    const int tid = threadIdx.x;
+    if (pro.kind == GPRO_LN) {
+        // (float)((x - mean) * inv) * w + b, inv = (float)(1 / sqrt(var + 1e-5)): decoder_aed.c:21-28
+        float v[V];
+#pragma unroll
+        for (int u = 0; u < V; u++) {
+            const int i = tid + NT * u;
+            v[u] = i < K ? pro.x[i] : 0.0f;
+        }
+        double s = 0.0;
+#pragma unroll
+        for (int u = 0; u < V; u++) s += (double)v[u];
+        const double mu = wg_sum<NT>(s, red) / K;
+        double q = 0.0;
+#pragma unroll
+        for (int u = 0; u < V; u++)
+            if (tid + NT * u < K) {
+                const double c = (double)v[u] - mu;
+                q += c * c;
+            }
+        const double var = wg_sum<NT>(q, red) / K;
+        const float inv = (float)(1.0 / sqrt(var + 1e-5));
+#pragma unroll
+        for (int u = 0; u < V; u++) {
+            const int i = tid + NT * u;
+            if (i < K) {
+                const float t = (float)(((double)v[u] - mu) * (double)inv);
+                xs[i] = t * pro.w[i] + pro.b[i];
+            }
+        }
+        for (int i = K + tid; i < Kp; i += NT) xs[i] = 0.0f;
+    } else {
+        // attention splits merged per head: sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M)
+        const int dk = K / pro.H;
+        const int n = pro.n_fixed > 0 ? pro.n_fixed : pro.st[0] + 1;
+        const int ns = min(mh_att_splits_dev(n), pro.nsplit);
+        if (tid < pro.H) {
+            const float *ml = pro.ml + (size_t)tid * pro.nsplit * 2;
+            float Mx = -INFINITY;
+            for (int s2 = 0; s2 < ns; s2++) Mx = fmaxf(Mx, ml[2 * s2]);
+            float L = 0.0f;
+            for (int s2 = 0; s2 < ns; s2++) L += ml[2 * s2 + 1] * expf(ml[2 * s2] - Mx);
+            hm[tid] = Mx;
+            hl[tid] = L;
+        }
+        __syncthreads();
+        for (int i = tid; i < Kp; i += NT) {
+            float v = 0.0f;
+            if (i < K) {
+                const int h = i / dk, f = i - h * dk;
+                const float *ml = pro.ml + (size_t)h * pro.nsplit * 2;
+                const float Mx = hm[h];
+                float o = 0.0f;
+                for (int s2 = 0; s2 < ns; s2++)
+                    o += pro.opart[((size_t)h * pro.nsplit + s2) * dk + f] * expf(ml[2 * s2] - Mx);
+                v = o / hl[h];
+            }
+            xs[i] = v;
+        }
+    }
+}
+
 template <int QT, int NW, int WNG, bool VEC>
-__global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const float *__restrict__ x, int M,
-                                                  float *y, GEpi ep) {
-    extern __shared__ float part[];  // [Kc][WNG][8][64] chunk results, then pf [Kc][16]
+__global__ __launch_bounds__(NW * 64) void k_gemv(GJobs J, const float *__restrict__ x, int M, GPro pro) {
+    extern __shared__ float part[];  // [Kc][WNG][8][64] chunk results, pf [Kc][16], prologue row [Kp]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int hh = lane >> 5, col = lane & 31;
+    const int gpj = J.W[0].Np / 32 / WNG;   // workgroups per job
+    const int job = blockIdx.x / gpj, bx = blockIdx.x - job * gpj;
+    const DevW W = job == 0 ? J.W[0] : (job == 1 ? J.W[1] : J.W[2]);
+    float *y = job == 0 ? J.y[0] : (job == 1 ? J.y[1] : J.y[2]);
+    const GEpi ep = job == 0 ? J.ep[0] : (job == 1 ? J.ep[1] : J.ep[2]);
     const int Kc = W.Kp / 128;
     float *pf = part + (size_t)Kc * WNG * 8 * 64;
+    float *xs = pf + (size_t)Kc * 16;
+    if (pro.kind != GPRO_NONE) {
+        gemv_prologue<NW * 64>(pro, W.k, W.Kp, xs);
+        __syncthreads();
+    }
     int gn[WNG];
 #pragma unroll
-    for (int j = 0; j < WNG; j++) gn[j] = blockIdx.x * WNG + j;
+    for (int j = 0; j < WNG; j++) gn[j] = bx * WNG + j;
     for (int c = wave; c < Kc; c += NW) {
         BH<QT, WNG> hd;
         load_bh<QT, WNG>(W, Kc, gn, c, lane, hd);
@@ -524,7 +620,16 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const float *__restric
         // the weight loads go out first: their latency overlaps the x split
         __builtin_amdgcn_sched_barrier(0);
         XChunk xc;
-        split_chunk<VEC>(x, M, W.k, col, c, hh, xc);
+        if (pro.kind != GPRO_NONE) {   // M = 1: row 0 from the prologue's row
+            float v[HSTEPS][8];
+#pragma unroll
+            for (int u = 0; u < HSTEPS; u++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[u][j] = col == 0 ? xs[128 * c + 16 * u + 8 * hh + j] : 0.0f;
+            split_vals(v, xc);
+        } else {
+            split_chunk<VEC>(x, M, W.k, col, c, hh, xc);
+        }
         if (hh == 0 && col < 16) pf[c * 16 + col] = xc.p;
         f16v acc[1][WNG];
 #pragma unroll
@@ -800,24 +905,28 @@ __global__ void k_silu(float *__restrict__ x, size_t n) {
 #include "launch.h"
 
 template <int QT, int NW, int WNG, bool VEC>
-static hipError_t launch_gemv1(const DevW &W, const float *x, int M, float *y, GEpi act, hipStream_t st) {
+static hipError_t launch_gemv1(const GJobs &J, const float *x, int M, const GPro &pro, hipStream_t st) {
+    const DevW &W = J.W[0];
     const int Kc = W.Kp / 128;
-    const size_t lds = ((size_t)Kc * WNG * 8 * 64 + (size_t)Kc * 16) * sizeof(float);
-    static bool attr = false;  // allow dynamic LDS beyond 64 KiB (gfx950 has 160 KiB)
+    const size_t lds = ((size_t)Kc * WNG * 8 * 64 + (size_t)Kc * 16 + (pro.kind ? (size_t)W.Kp : 0)) * sizeof(float);
+    // allow dynamic LDS beyond 64 KiB: gfx950 has 160 KiB, less the prologue's
+    // static reduction scratch
+    static bool attr = false;
     if (!attr) {
-        (void)hipFuncSetAttribute((const void *)k_gemv<QT, NW, WNG, VEC>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  160 * 1024);
+        hipError_t e = hipFuncSetAttribute((const void *)k_gemv<QT, NW, WNG, VEC>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024);
+        if (e != hipSuccess) return e;
         attr = true;
     }
-    hipLaunchKernelGGL((k_gemv<QT, NW, WNG, VEC>), dim3(W.Np / 32 / WNG), dim3(NW * 64), lds, st, W, x, M, y, act);
+    hipLaunchKernelGGL((k_gemv<QT, NW, WNG, VEC>), dim3(W.Np / 32 / WNG * J.n), dim3(NW * 64), lds, st, J, x, M,
+                       pro);
     return hipGetLastError();
 }
 
 template <int QT, int NW, int WNG>
-static hipError_t launch_gemv(const DevW &W, const float *x, int M, int vec, float *y, GEpi act,
-                              hipStream_t st) {
-    if (vec) return launch_gemv1<QT, NW, WNG, true>(W, x, M, y, act, st);
-    return launch_gemv1<QT, NW, WNG, false>(W, x, M, y, act, st);
+static hipError_t launch_gemv(const GJobs &J, const float *x, int M, int vec, const GPro &pro, hipStream_t st) {
+    if (vec) return launch_gemv1<QT, NW, WNG, true>(J, x, M, pro, st);
+    return launch_gemv1<QT, NW, WNG, false>(J, x, M, pro, st);
 }
 
 // column groups per GEMV workgroup: two for wide outputs, so that each chunk
@@ -829,15 +938,15 @@ static int gemv_wng(const DevW &W) {
 }
 
 template <int QT>
-static hipError_t gemv_t(const DevW &W, const float *x, int M, int vec, float *y, GEpi act,
-                         hipStream_t st) {
+static hipError_t gemv_t(const GJobs &J, const float *x, int M, int vec, const GPro &pro, hipStream_t st) {
+    const DevW &W = J.W[0];
     const int Kc = W.Kp / 128, wng = gemv_wng(W);
     if (wng == 2) {
-        if (Kc >= 8) return launch_gemv<QT, 8, 2>(W, x, M, vec, y, act, st);
-        return launch_gemv<QT, 4, 2>(W, x, M, vec, y, act, st);
+        if (Kc >= 8) return launch_gemv<QT, 8, 2>(J, x, M, vec, pro, st);
+        return launch_gemv<QT, 4, 2>(J, x, M, vec, pro, st);
     }
-    if (Kc >= 8) return launch_gemv<QT, 8, 1>(W, x, M, vec, y, act, st);
-    return launch_gemv<QT, 4, 1>(W, x, M, vec, y, act, st);
+    if (Kc >= 8) return launch_gemv<QT, 8, 1>(J, x, M, vec, pro, st);
+    return launch_gemv<QT, 4, 1>(J, x, M, vec, pro, st);
 }
 
 template <int QT>
@@ -874,9 +983,22 @@ static hipError_t gemm_t(const DevW &W, const uint8_t *xp, const float *xs16, co
 
 bool mh_use_gemv(const DevW &W, int M) { return M <= 16 && (W.Kp / 128) * gemv_wng(W) <= 64; }
 
+hipError_t mh_launch_gemv_jobs(int qtype, const GJobs &J, const float *x, int M, int vec, const GPro &pro,
+                               hipStream_t st) {
+    if (J.n < 1 || J.n > 3 || (pro.kind != GPRO_NONE && (M != 1 || J.W[0].k > 4096))) return hipErrorInvalidValue;
+    for (int i = 1; i < J.n; i++)
+        if (J.W[i].Np != J.W[0].Np || J.W[i].Kp != J.W[0].Kp || J.W[i].k != J.W[0].k) return hipErrorInvalidValue;
+    MH_DISPATCH(gemv_t, qtype, J, x, M, vec, pro, st)
+}
+
 hipError_t mh_launch_gemv_epi(int qtype, const DevW &W, const float *x, int M, int vec, float *y, GEpi ep,
                               hipStream_t st) {
-    MH_DISPATCH(gemv_t, qtype, W, x, M, vec, y, ep, st)
+    GJobs J{};
+    J.W[0] = J.W[1] = J.W[2] = W;
+    J.y[0] = y;
+    J.ep[0] = ep;
+    J.n = 1;
+    return mh_launch_gemv_jobs(qtype, J, x, M, vec, GPro{}, st);
 }
 
 hipError_t mh_launch_gemv(int qtype, const DevW &W, const float *x, int M, int vec, float *y, int act,

@@ -4,7 +4,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-struct DevW;
+#include "fmt.h"   // DevW
 
 // Rows the prepared-activation buffer must hold for an M-row product: the
 // kernels read whole row groups up to this count.
@@ -25,6 +25,29 @@ struct GEpi {
 };
 hipError_t mh_launch_gemv_epi(int qtype, const DevW &W, const float *x, int M, int vec, float *y, GEpi ep,
                               hipStream_t st);
+// The input row of a one-row GEMV built per workgroup: GPRO_LN = the layer norm
+// of x (w, b); GPRO_COMB = the attention splits merged (opart [H][nsplit][dk],
+// ml [H][nsplit][2], n keys = n_fixed, or st[0] + 1 when n_fixed == 0).
+enum { GPRO_NONE = 0, GPRO_LN = 1, GPRO_COMB = 2 };
+struct GPro {
+    int kind;
+    const float *x, *w, *b;
+    const float *opart, *ml;
+    const int *st;
+    int n_fixed, nsplit, H;
+};
+// up to three products of one input, same format and shape
+struct GJobs {
+    DevW W[3];
+    float *y[3];
+    GEpi ep[3];
+    int n;
+};
+hipError_t mh_launch_gemv_jobs(int qtype, const GJobs &J, const float *x, int M, int vec, const GPro &pro,
+                               hipStream_t st);
+// keys per attention split of the decoder step
+constexpr int MH_ATT_KC = 64;
+__host__ __device__ inline int mh_att_splits_dev(int n) { return (n + MH_ATT_KC - 1) / MH_ATT_KC; }
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
                           const float *xpf, float *y, int M, int act, hipStream_t st);
 // The FFN's first product with SiLU, its output prepared as the input of a
@@ -53,8 +76,8 @@ hipError_t mh_launch_relpos_attn(const float *q, const float *k, const float *v,
 int mh_att_splits(int n);   // attention splits for n keys
 hipError_t mh_launch_embed_ln(const float *emb, const float *pos, const int *prompt, int n_prompt, const int *st,
                               const float *w, const float *b, float *x, int d, hipStream_t s);
-hipError_t mh_launch_ln(const float *x, const float *w, const float *b, float *y, int d, hipStream_t s);
 // out = attention of q over n keys (n_fixed, or p + 1 with the cache append of kn, vn when n_fixed == 0);
+// out == NULL: the splits only (merged by a GPRO_COMB prologue);
 // o_part [H][nsplit][dk], ml_part [H][nsplit][2]
 hipError_t mh_launch_attend1(const float *q, float *K, float *V, const float *kn, const float *vn, const int *st,
                              int n_fixed, int d, int H, float *o_part, float *ml_part, int nsplit, float *out,
