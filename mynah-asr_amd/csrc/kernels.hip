@@ -591,20 +591,17 @@ __device__ void gemv_prologue(const GPro &pro, int K, int Kp, float *xs) {
     }
 }
 
-template <int QT, int NW, int WNG, bool VEC>
-__global__ __launch_bounds__(NW * 64) void k_gemv(GJobs J, const float *__restrict__ x, int M, GPro pro) {
+// the GEMV of workgroup bx of one product (shared by k_gemv and k_gemv_jobs)
+template <int QT, int NW, int WNG, bool VEC, bool PRO>
+__device__ __forceinline__ void gemv_body(const DevW &W, const float *__restrict__ x, int M, float *y,
+                                          const GEpi &ep, const GPro &pro, int bx) {
     extern __shared__ float part[];  // [Kc][WNG][8][64] chunk results, pf [Kc][16], prologue row [Kp]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int hh = lane >> 5, col = lane & 31;
-    const int gpj = J.W[0].Np / 32 / WNG;   // workgroups per job
-    const int job = blockIdx.x / gpj, bx = blockIdx.x - job * gpj;
-    const DevW W = job == 0 ? J.W[0] : (job == 1 ? J.W[1] : J.W[2]);
-    float *y = job == 0 ? J.y[0] : (job == 1 ? J.y[1] : J.y[2]);
-    const GEpi ep = job == 0 ? J.ep[0] : (job == 1 ? J.ep[1] : J.ep[2]);
     const int Kc = W.Kp / 128;
     float *pf = part + (size_t)Kc * WNG * 8 * 64;
     float *xs = pf + (size_t)Kc * 16;
-    if (pro.kind != GPRO_NONE) {
+    if constexpr (PRO) {
         gemv_prologue<NW * 64>(pro, W.k, W.Kp, xs);
         __syncthreads();
     }
@@ -620,7 +617,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GJobs J, const float *__restri
         // the weight loads go out first: their latency overlaps the x split
         __builtin_amdgcn_sched_barrier(0);
         XChunk xc;
-        if (pro.kind != GPRO_NONE) {   // M = 1: row 0 from the prologue's row
+        if constexpr (PRO) {   // M = 1: row 0 from the prologue's row
             float v[HSTEPS][8];
 #pragma unroll
             for (int u = 0; u < HSTEPS; u++)
@@ -682,6 +679,23 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GJobs J, const float *__restri
             y[(size_t)m * W.n + n] = v;
         }
     }
+}
+
+// one product: the compact argument block of the encoder and decoder GEMVs
+template <int QT, int NW, int WNG, bool VEC>
+__global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const float *__restrict__ x, int M, float *y, GEpi ep) {
+    gemv_body<QT, NW, WNG, VEC, false>(W, x, M, y, ep, GPro{}, blockIdx.x);
+}
+
+// up to three products of one prologue-built row (the decoder step)
+template <int QT, int NW, int WNG>
+__global__ __launch_bounds__(NW * 64) void k_gemv_jobs(GJobs J, GPro pro) {
+    const int gpj = J.W[0].Np / 32 / WNG;   // workgroups per job
+    const int job = blockIdx.x / gpj, bx = blockIdx.x - job * gpj;
+    const DevW W = job == 0 ? J.W[0] : (job == 1 ? J.W[1] : J.W[2]);
+    float *y = job == 0 ? J.y[0] : (job == 1 ? J.y[1] : J.y[2]);
+    const GEpi ep = job == 0 ? J.ep[0] : (job == 1 ? J.ep[1] : J.ep[2]);
+    gemv_body<QT, NW, WNG, false, true>(W, nullptr, 1, y, ep, pro, bx);
 }
 
 // ---------------------------------------------------------------------------
@@ -904,29 +918,43 @@ __global__ void k_silu(float *__restrict__ x, size_t n) {
 
 #include "launch.h"
 
-template <int QT, int NW, int WNG, bool VEC>
+template <typename F>
+static hipError_t allow_lds(F *f) {
+    // dynamic LDS beyond 64 KiB: gfx950 has 160 KiB, less the prologue's static scratch
+    return hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024);
+}
+
+template <int QT, int NW, int WNG, bool VEC, bool PRO>
 static hipError_t launch_gemv1(const GJobs &J, const float *x, int M, const GPro &pro, hipStream_t st) {
     const DevW &W = J.W[0];
     const int Kc = W.Kp / 128;
-    const size_t lds = ((size_t)Kc * WNG * 8 * 64 + (size_t)Kc * 16 + (pro.kind ? (size_t)W.Kp : 0)) * sizeof(float);
-    // allow dynamic LDS beyond 64 KiB: gfx950 has 160 KiB, less the prologue's
-    // static reduction scratch
+    const size_t lds = ((size_t)Kc * WNG * 8 * 64 + (size_t)Kc * 16 + (PRO ? (size_t)W.Kp : 0)) * sizeof(float);
     static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_gemv<QT, NW, WNG, VEC>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024);
-        if (e != hipSuccess) return e;
-        attr = true;
+    if constexpr (PRO) {
+        if (!attr) {
+            hipError_t e = allow_lds(k_gemv_jobs<QT, NW, WNG>);
+            if (e != hipSuccess) return e;
+            attr = true;
+        }
+        hipLaunchKernelGGL((k_gemv_jobs<QT, NW, WNG>), dim3(W.Np / 32 / WNG * J.n), dim3(NW * 64), lds, st, J, pro);
+    } else {
+        if (!attr) {
+            hipError_t e = allow_lds(k_gemv<QT, NW, WNG, VEC>);
+            if (e != hipSuccess) return e;
+            attr = true;
+        }
+        if (J.n != 1) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((k_gemv<QT, NW, WNG, VEC>), dim3(W.Np / 32 / WNG), dim3(NW * 64), lds, st, W, x, M, J.y[0],
+                           J.ep[0]);
     }
-    hipLaunchKernelGGL((k_gemv<QT, NW, WNG, VEC>), dim3(W.Np / 32 / WNG * J.n), dim3(NW * 64), lds, st, J, x, M,
-                       pro);
     return hipGetLastError();
 }
 
 template <int QT, int NW, int WNG>
 static hipError_t launch_gemv(const GJobs &J, const float *x, int M, int vec, const GPro &pro, hipStream_t st) {
-    if (vec) return launch_gemv1<QT, NW, WNG, true>(J, x, M, pro, st);
-    return launch_gemv1<QT, NW, WNG, false>(J, x, M, pro, st);
+    if (pro.kind != GPRO_NONE) return launch_gemv1<QT, NW, WNG, false, true>(J, x, M, pro, st);
+    if (vec) return launch_gemv1<QT, NW, WNG, true, false>(J, x, M, pro, st);
+    return launch_gemv1<QT, NW, WNG, false, false>(J, x, M, pro, st);
 }
 
 // column groups per GEMV workgroup: two for wide outputs, so that each chunk
@@ -985,7 +1013,9 @@ bool mh_use_gemv(const DevW &W, int M) { return M <= 16 && (W.Kp / 128) * gemv_w
 
 hipError_t mh_launch_gemv_jobs(int qtype, const GJobs &J, const float *x, int M, int vec, const GPro &pro,
                                hipStream_t st) {
-    if (J.n < 1 || J.n > 3 || (pro.kind != GPRO_NONE && (M != 1 || J.W[0].k > 4096))) return hipErrorInvalidValue;
+    if (J.n < 1 || J.n > 3 || (pro.kind != GPRO_NONE && (M != 1 || J.W[0].k > 4096)) ||
+        (pro.kind == GPRO_NONE && J.n != 1))
+        return hipErrorInvalidValue;
     for (int i = 1; i < J.n; i++)
         if (J.W[i].Np != J.W[0].Np || J.W[i].Kp != J.W[0].Kp || J.W[i].k != J.W[0].k) return hipErrorInvalidValue;
     MH_DISPATCH(gemv_t, qtype, J, x, M, vec, pro, st)
