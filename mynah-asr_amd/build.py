@@ -60,7 +60,7 @@ def build_hip() -> str:
 
 
 def build_host() -> str:
-    srcs = [os.path.join(HOST, f) for f in ("qmat.c", "backend.c", "synth.c")]
+    srcs = [os.path.join(HOST, f) for f in ("qmat.c", "backend.c", "synth.c", "gguf.c")]
     if not all(os.path.exists(s) for s in srcs):
         return ""
     _run(["gcc", "-std=c11", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", "-ffp-contract=off",

@@ -47,6 +47,8 @@ HOST_SYMBOLS = [
     "mynah_asr_qmat_mul", "mynah_asr_qmat_ffn", "mynah_asr_qmat_qkv", "mynah_asr_qmat_dequant",
     "mynah_asr_quantize_int8", "mynah_asr_quantize_int4",
     "mynah_synth_randn", "mynah_synth_quantize", "mynah_synth_nbytes",
+    "mynah_gguf_open", "mynah_gguf_close", "mynah_gguf_version", "mynah_gguf_alignment", "mynah_gguf_count",
+    "mynah_gguf_at", "mynah_gguf_find", "mynah_asr_qmat_init_gguf",
 ]
 
 _P = C.c_void_p
@@ -78,6 +80,12 @@ class QMat(C.Structure):
     _fields_ = [("f32", C.c_void_p), ("q8", C.c_void_p), ("q4", C.c_void_p),
                 ("scales", C.c_void_p), ("owned_q", C.c_void_p), ("owned_s", C.c_void_p),
                 ("qtype", C.c_int), ("n", C.c_int), ("k", C.c_int), ("blocks", C.c_void_p)]
+
+
+class GgufTensor(C.Structure):
+    """mynah_gguf_tensor (host/gguf.h)."""
+    _fields_ = [("name", C.c_char_p), ("ggml_type", C.c_int), ("rank", C.c_int), ("ne", C.c_int64 * 4),
+                ("data", C.c_void_p), ("nbytes", C.c_uint64)]
 
 
 def _ptr(a: np.ndarray):
@@ -138,6 +146,20 @@ class HipLib:
         H.mynah_asr_set_backend.argtypes = [C.c_char_p]
         H.mynah_asr_qmat_init.argtypes = [C.POINTER(QMat), _P, C.c_int, C.c_int, C.c_int]
         H.mynah_asr_qmat_init_blocks.argtypes = [C.POINTER(QMat), _P, C.c_int, C.c_int, C.c_int]
+        H.mynah_gguf_open.restype = _P
+        H.mynah_gguf_open.argtypes = [C.c_char_p, C.c_char_p, C.c_size_t]
+        H.mynah_gguf_close.argtypes = [_P]
+        H.mynah_gguf_version.restype = C.c_uint32
+        H.mynah_gguf_version.argtypes = [_P]
+        H.mynah_gguf_alignment.restype = C.c_uint64
+        H.mynah_gguf_alignment.argtypes = [_P]
+        H.mynah_gguf_count.restype = C.c_size_t
+        H.mynah_gguf_count.argtypes = [_P]
+        H.mynah_gguf_at.restype = C.POINTER(GgufTensor)
+        H.mynah_gguf_at.argtypes = [_P, C.c_size_t]
+        H.mynah_gguf_find.restype = C.POINTER(GgufTensor)
+        H.mynah_gguf_find.argtypes = [_P, C.c_char_p]
+        H.mynah_asr_qmat_init_gguf.argtypes = [C.POINTER(QMat), _P, C.c_char_p]
         H.mynah_asr_qmat_free.argtypes = [C.POINTER(QMat)]
         H.mynah_asr_qmat_mul.argtypes = [C.POINTER(QMat), _P, _P, C.c_int]
         H.mynah_asr_qmat_ffn.argtypes = [C.POINTER(QMat), C.POINTER(QMat), _P, _P, C.c_int, _P]
@@ -286,6 +308,43 @@ def host_relpos_attention(lib, q, k, v, rk, bias_u, bias_v, H: int, left: int = 
                                              _ptr(ctx), T, d, H, left, right)
     lib._check(rc, "relpos_attention")
     return ctx
+
+
+class Gguf:
+    """A mapped GGUF file (host/gguf.h): `tensors()` lists (name, ggml type,
+    ne, bytes); `qmat(name)` is the zero-copy qmat of one weight."""
+
+    def __init__(self, lib: "HipLib", path: str):
+        self.lib = lib
+        err = C.create_string_buffer(256)
+        self.h = lib.H.mynah_gguf_open(path.encode(), err, 256)
+        if not self.h:
+            raise ValueError(err.value.decode())
+
+    def version(self) -> int:
+        return int(self.lib.H.mynah_gguf_version(self.h))
+
+    def alignment(self) -> int:
+        return int(self.lib.H.mynah_gguf_alignment(self.h))
+
+    def tensors(self):
+        out = []
+        for i in range(self.lib.H.mynah_gguf_count(self.h)):
+            t = self.lib.H.mynah_gguf_at(self.h, i).contents
+            raw = C.string_at(t.data, t.nbytes) if t.nbytes else b""
+            out.append((t.name.decode(), t.ggml_type, tuple(t.ne[:t.rank]), raw, t.data))
+        return out
+
+    def qmat(self, name: str) -> QMat:
+        m = QMat()
+        if self.lib.H.mynah_asr_qmat_init_gguf(C.byref(m), self.h, name.encode()) != 0:
+            raise KeyError(name)
+        return m
+
+    def close(self):
+        if self.h:
+            self.lib.H.mynah_gguf_close(self.h)
+            self.h = None
 
 
 class DeviceAed:

@@ -18,7 +18,7 @@ GOLDEN = os.path.join(ROOT, "tests", "golden")
 def _declared(header):
     txt = open(header).read()
     txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
-    return sorted(set(re.findall(r"\b(mynah_(?:asr|synth)_\w+)\s*\(", txt)) - {"mynah_asr_sigmoid"})
+    return sorted(set(re.findall(r"\b(mynah_(?:asr|synth|gguf)_\w+)\s*\(", txt)) - {"mynah_asr_sigmoid"})
 
 
 def test_hip_library_exports_every_declared_symbol(lib):
@@ -32,7 +32,7 @@ def test_hip_library_exports_every_declared_symbol(lib):
 def test_host_library_exports_every_declared_symbol(lib):
     host = os.path.join(ROOT, "mynah-asr_amd", "host")
     names = []
-    for h in ("qmat.h", "backend.h", "synth.h"):
+    for h in ("qmat.h", "backend.h", "synth.h", "gguf.h"):
         names += _declared(os.path.join(host, h))
     assert sorted(names) == sorted(M.HOST_SYMBOLS)
     for n in names:
