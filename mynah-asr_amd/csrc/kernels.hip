@@ -303,10 +303,11 @@ template <int QT> struct StageLayout {
 };
 
 // workgroups per CU the register budget is sized for: as many as the LDS
-// ring allows, fewer for the K-quants (affine sums, sub-block factors) and
-// the f32 pairs, which need more registers per wave
+// ring allows, fewer for the K-quants (affine sums, sub-block factors, more
+// registers per wave); f32 weights (two f16 planes, 4 bytes per element)
+// stage 48 KiB per half-chunk, so one double-buffered workgroup fills the LDS
 template <int QT> constexpr int gemm_occ() {
-    return (QT == QT_F32 || Fmt<QT>::MINS || Fmt<QT>::SUB16) ? 2 : 3;
+    return QT == QT_F32 ? 1 : ((Fmt<QT>::MINS || Fmt<QT>::SUB16) ? 2 : 3);
 }
 
 // Where a product's result goes: EPI_Y stores y (SiLU applied when act);
@@ -359,7 +360,6 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
     const int hh = lane >> 5, col = lane & 31;
     const int Kc = W.Kp / 128, Kp16 = W.Kp / 16;
     const int G0 = tm * 2, GC0 = tn * 4;
-    const int gj[WN] = {wave};
 
     auto stage = [&](int c, int h, uint8_t *B) {
         const int rg = wave >> 1, gc = GC0 + wave;
@@ -711,7 +711,9 @@ __global__ __launch_bounds__(256) void k_prep(const float *__restrict__ x, int M
     const int G = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 31, hh = lane >> 5, m = 32 * G + r;
     const int Kc = Kp / 128;
-    for (int c = wave; c < Kc; c += 4) {
+    // workgroup (G, y): chunks 4y .. 4y+3, one per wave (enough waves to fill
+    // the chip at encoder sizes: M/32 row groups alone are fewer than the CUs)
+    for (int c = 4 * blockIdx.y + wave; c < Kc; c += 4 * gridDim.y) {
         XChunk xc;
         split_chunk<VEC>(x, M, K, m, c, hh, xc);
 #pragma unroll
@@ -1050,10 +1052,11 @@ hipError_t mh_launch_gemm_prep_out(int qtype, const DevW &W, const uint8_t *xp, 
 
 hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,
                           float *xpf, int want_xsum, int vec, hipStream_t st) {
+    const dim3 grid(Mpad / 32, (Kp / 128 + 3) / 4);
     if (vec)
-        hipLaunchKernelGGL(k_prep<true>, dim3(Mpad / 32), dim3(256), 0, st, x, M, K, Kp, xp, xs16, xpf, want_xsum);
+        hipLaunchKernelGGL(k_prep<true>, grid, dim3(256), 0, st, x, M, K, Kp, xp, xs16, xpf, want_xsum);
     else
-        hipLaunchKernelGGL(k_prep<false>, dim3(Mpad / 32), dim3(256), 0, st, x, M, K, Kp, xp, xs16, xpf, want_xsum);
+        hipLaunchKernelGGL(k_prep<false>, grid, dim3(256), 0, st, x, M, K, Kp, xp, xs16, xpf, want_xsum);
     return hipGetLastError();
 }
 
