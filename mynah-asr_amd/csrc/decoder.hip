@@ -116,6 +116,17 @@ __global__ __launch_bounds__(256) void k_att_part(const float *__restrict__ q, f
         V[(size_t)p * d + ho + tid] = vn[ho + tid];
     }
     if (tid < DK) qs[tid] = q[ho + tid];
+    // the V values this thread weighs later (feature tid % DK, keys tid / DK
+    // + G t): loaded now, so their latency overlaps the scores
+    constexpr int G = 256 / DK;
+    const int f = tid % DK, g = tid / DK, cnt = j1 - j0;
+    float vv[KC / G];
+#pragma unroll
+    for (int t = 0; t < KC / G; t++) {
+        const int jj = g + G * t, j = j0 + jj;
+        vv[t] = 0.0f;
+        if (jj < cnt) vv[t] = ((append && j == p) ? vn + ho : V + (size_t)j * d + ho)[f];
+    }
     __syncthreads();
     // scores: key j0 + (tid >> 2), features (tid & 3) * DK/4 ..
     {
@@ -151,19 +162,13 @@ __global__ __launch_bounds__(256) void k_att_part(const float *__restrict__ q, f
         if (tid == 0) mls[0] = m, mls[1] = l;
     }
     __syncthreads();
-    // values: feature f = tid % DK, keys jj = tid / DK, + 256/DK, ... (all loads in flight)
+    // values: feature f, keys g + G t
     {
-        constexpr int G = 256 / DK;
-        const int f = tid % DK, g = tid / DK, cnt = j1 - j0;
         float acc = 0.0f;
 #pragma unroll
         for (int t = 0; t < KC / G; t++) {
             const int jj = g + G * t;
-            if (jj < cnt) {
-                const int j = j0 + jj;
-                const float *vr = (append && j == p) ? vn + ho : V + (size_t)j * d + ho;
-                acc = fmaf(sc[jj], vr[f], acc);
-            }
+            if (jj < cnt) acc = fmaf(sc[jj], vv[t], acc);
         }
         red[g][f] = acc;
     }

@@ -601,19 +601,25 @@ __device__ __forceinline__ void gemv_body(const DevW &W, const float *__restrict
     const int Kc = W.Kp / 128;
     float *pf = part + (size_t)Kc * WNG * 8 * 64;
     float *xs = pf + (size_t)Kc * 16;
-    if constexpr (PRO) {
-        gemv_prologue<NW * 64>(pro, W.k, W.Kp, xs);
-        __syncthreads();
-    }
     int gn[WNG];
 #pragma unroll
     for (int j = 0; j < WNG; j++) gn[j] = bx * WNG + j;
-    for (int c = wave; c < Kc; c += NW) {
-        BH<QT, WNG> hd;
+    BH<QT, WNG> hd;
+    BK<QT, WNG> bk[KSTEPS];
+    auto load = [&](int c) {
         load_bh<QT, WNG>(W, Kc, gn, c, lane, hd);
-        BK<QT, WNG> bk[KSTEPS];
 #pragma unroll
         for (int s = 0; s < KSTEPS; s++) load_bk<QT, WNG>(W, Kc, gn, c, s, lane, bk[s]);
+    };
+    if constexpr (PRO) {
+        // the first chunk's weight loads go out before the prologue builds the row
+        if (wave < Kc) load(wave);
+        __builtin_amdgcn_sched_barrier(0);
+        gemv_prologue<NW * 64>(pro, W.k, W.Kp, xs);
+        __syncthreads();
+    }
+    for (int c = wave; c < Kc; c += NW) {
+        if (!PRO || c != wave) load(c);
         // the weight loads go out first: their latency overlaps the x split
         __builtin_amdgcn_sched_barrier(0);
         XChunk xc;
