@@ -15,8 +15,9 @@ their shared input), out and pos through qgemm_dev (preparation + product).
 `value` = dense-equivalent 2*M*N*K operations per second, summed over the
 step, in TOPS.
 
-Also reported (not `value`): per-kernel roofline fractions, Q4_K at BASELINE
-config 4's M = 12000 shapes, decoder GEMVs (config 3) in HBM GB/s with >= 512
+Also reported (not `value`): per-kernel roofline fractions, the same step in
+INT8ACT numerics (int8 activations on the i8 MFMA, against 5.0 POP/s), Q4_K at
+BASELINE config 4's M = 12000 shapes, decoder GEMVs (config 3) in HBM GB/s with >= 512
 MB of rotating weight copies (defeats the 256 MB MALL), timed as one HIP graph
 of all the launches (kernel_us; call_us = the same launches issued one by one
 from the host), the f32-weight GEMM, the relative-position attention core at T = 750
@@ -41,6 +42,7 @@ sys.path.insert(0, os.path.join(ROOT, "mynah-asr_amd"))
 
 PEAK_FP16 = 2500.0  # TFLOP/s dense (MI355X)
 PEAK_HBM = 8000.0   # GB/s
+PEAK_INT8 = 5000.0  # TOPS dense int8 (MI355X)
 METRIC = "Q8_0/Q4_K GEMM TOPS & % roofline at FastConformer-0.6B shapes; GEMV HBM GB/s"
 
 ENC_SHAPES = [("ffn1", 1024, 4096), ("ffn2", 4096, 1024), ("q", 1024, 1024), ("k", 1024, 1024),
@@ -439,6 +441,18 @@ def main():
         ms4, fl4, rows4 = run_encoder_set(B, M_, M_.Q4_K, 12000, KQ_SHAPES, 3, 1, 100)
         details["kquant_q4_k_m12000"] = {"tops_per_layer_set": round(fl4 / (ms4 * 1e-3) / 1e12, 2),
                                          "ms_per_layer_set": round(ms4, 3), "rows": rows4}
+        log("[bench] INT8ACT numerics, Q8_0 encoder set M=6000")
+        lib.set_numerics(1)
+        try:
+            ms8, fl8, rows8 = run_encoder_set(B, M_, M_.Q8_0, M, ENC_SHAPES, 5, 2, 0)
+        finally:
+            lib.set_numerics(0)
+        details["int8act_q8_0_m6000"] = {
+            "tops": round(fl8 / (ms8 * 1e-3) / 1e12, 2), "ms_per_step": round(ms8, 4),
+            "int8_mfma_frac": round(fl8 / (ms8 * 1e-3) / 1e12 / PEAK_INT8, 4),
+            "note": "per-row int8 activations and exact integer block sums (the reference's int8 path, "
+                    "qmat.c:186-202, 508-552, 606-643); outputs match that path, not the f32 product",
+            "rows": rows8}
         log("[bench] f32 weights M=6000")
         msf, flf, rowsf = run_encoder_set(B, M_, M_.F32, M, ENC_SHAPES[:2], 3, 1, 200)
         details["f32_m6000"] = {"tflops": round(flf / (msf * 1e-3) / 1e12, 2), "rows": rowsf}

@@ -763,20 +763,26 @@ __device__ __forceinline__ int act_q8(float v, float inv) {
 }
 
 // one workgroup (4 waves) per 32-row group
-__global__ __launch_bounds__(256) void k_prep_i8(const float *__restrict__ x, int M, int K, int Kp,
-                                                 uint8_t *__restrict__ qx, float *__restrict__ sx) {
+// 16 waves per 32-row group: two rows each for the row maxima, then the
+// ksteps split over the waves (a 32-row group per 4 waves left the chip idle)
+constexpr int PREP_I8_NW = 16;
+template <bool VEC>
+__global__ __launch_bounds__(PREP_I8_NW * 64) void k_prep_i8(const float *__restrict__ x, int M, int K, int Kp,
+                                                             uint8_t *__restrict__ qx, float *__restrict__ sx) {
     __shared__ float invs[32];
     const int G = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int rr = 0; rr < 8; rr++) {
-        const int m = 32 * G + 8 * wave + rr;
+    constexpr int RPW = 32 / PREP_I8_NW;
+    for (int rr = 0; rr < RPW; rr++) {
+        const int m = 32 * G + RPW * wave + rr;
         float amax = 0.0f;
         if (m < M) {
             const float *row = x + (size_t)m * K;
+#pragma unroll 4
             for (int j = lane; j < K; j += 64) amax = fmaxf(amax, fabsf(row[j]));
         }
         for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
         if (lane == 0) {
-            invs[8 * wave + rr] = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+            invs[RPW * wave + rr] = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
             sx[m] = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 0.0f;
         }
     }
@@ -788,14 +794,27 @@ __global__ __launch_bounds__(256) void k_prep_i8(const float *__restrict__ x, in
     const int S = Kp / 32;
     static const int kWord[8] = {0, 0, 1, 1, 0, 0, 1, 1};
     static const int kByte[8] = {0, 2, 0, 2, 1, 3, 1, 3};
-    for (int s = wave; s < S; s += 4) {
+    for (int s = wave; s < S; s += PREP_I8_NW) {
         uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int kh = 0; kh < 2; kh++) {
             const int k0 = 32 * s + 16 * kh + 8 * hh;
+            float v[8];
+            if constexpr (VEC) {   // K % 8 == 0, 16-byte rows: the lane's 8 elements in two loads
+                float4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
+                if (live && k0 < K) {
+                    a = *(const float4 *)(row + k0);
+                    b = *(const float4 *)(row + k0 + 4);
+                }
+                v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+                v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = (live && k0 + j < K) ? row[k0 + j] : 0.0f;
+            }
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const int q = (live && k0 + j < K) ? act_q8(row[k0 + j], inv) : 0;
+                const int q = (live && k0 + j < K) ? act_q8(v[j], inv) : 0;
                 w[2 * kh + kWord[j]] |= ((uint32_t)q & 0xffu) << (8 * kByte[j]);
             }
         }
@@ -1086,7 +1105,10 @@ bool mh_i8_supported(int qtype) {
 
 hipError_t mh_launch_prep_i8(const float *x, int M, int K, int Kp, int Mpad, uint8_t *qx, float *sx,
                              hipStream_t st) {
-    hipLaunchKernelGGL(k_prep_i8, dim3(Mpad / 32), dim3(256), 0, st, x, M, K, Kp, qx, sx);
+    if (K % 8 == 0 && ((uintptr_t)x & 15) == 0)
+        hipLaunchKernelGGL(k_prep_i8<true>, dim3(Mpad / 32), dim3(PREP_I8_NW * 64), 0, st, x, M, K, Kp, qx, sx);
+    else
+        hipLaunchKernelGGL(k_prep_i8<false>, dim3(Mpad / 32), dim3(PREP_I8_NW * 64), 0, st, x, M, K, Kp, qx, sx);
     return hipGetLastError();
 }
 
