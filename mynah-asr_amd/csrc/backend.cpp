@@ -670,6 +670,8 @@ int mynah_asr_hip_aed_decode_dev(const mynah_asr_hip_aed *a, const float *enc, i
     if (begin(&c)) return -1;
     if (aed_check(a, T)) return -1;
     if (!enc || !prompt || n_prompt <= 0 || !tokens || cap < 0) return fail("bad argument");
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= a->vocab) return fail("prompt token outside the vocabulary");
     int max_len = n_prompt + cap;
     if (max_len > a->max_seq) max_len = a->max_seq;
     return aed_run(c, a, enc, T, prompt, n_prompt, max_len, eos, tokens, cap, nullptr, pick_stream(stream));
@@ -681,6 +683,8 @@ int mynah_asr_hip_aed_forced_dev(const mynah_asr_hip_aed *a, const float *enc, i
     if (begin(&c)) return -1;
     if (aed_check(a, T)) return -1;
     if (!enc || !tokens || n <= 0 || n > a->max_seq || !logits) return fail("bad argument");
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= a->vocab) return fail("token outside the vocabulary");
     const int r = aed_run(c, a, enc, T, tokens, n, n, -1, nullptr, 0, logits, pick_stream(stream));
     return r < 0 ? -1 : 0;
 }

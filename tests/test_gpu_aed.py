@@ -146,3 +146,13 @@ def test_aed_rejects_unsupported(gpu):
     with pytest.raises(RuntimeError, match="head size"):
         dev.forced(enc.data_ptr(), 4, [1, 2])
     dev.close()
+    params = make_params(2, 128, 2, 128, 100, 1, 8)
+    dev = M.DeviceAed(gpu, params, 2, M.F32)
+    enc = torch.zeros((4, 128), device="cuda")
+    with pytest.raises(RuntimeError, match="vocabulary"):
+        dev.forced(enc.data_ptr(), 4, [1, 100])
+    with pytest.raises(RuntimeError, match="vocabulary"):
+        dev.decode(enc.data_ptr(), 4, [-1], eos=0, cap=2)
+    with pytest.raises(RuntimeError, match="bad argument"):
+        dev.forced(enc.data_ptr(), 4, list(range(9)))      # more positions than max_seq
+    dev.close()
