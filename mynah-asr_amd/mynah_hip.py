@@ -332,7 +332,7 @@ class Gguf:
         for i in range(self.lib.H.mynah_gguf_count(self.h)):
             t = self.lib.H.mynah_gguf_at(self.h, i).contents
             raw = C.string_at(t.data, t.nbytes) if t.nbytes else b""
-            out.append((t.name.decode(), t.ggml_type, tuple(t.ne[:t.rank]), raw, t.data))
+            out.append((t.name.decode("utf-8", "replace"), t.ggml_type, tuple(t.ne[:t.rank]), raw, t.data))
         return out
 
     def qmat(self, name: str) -> QMat:

@@ -117,7 +117,8 @@ def ingot_read(L, path):
     for i in range(L.ingot_gguf_count(g)):
         tp = L.ingot_gguf_at(g, i)
         t = tp.contents
-        out.append((t.name.decode(), t.type, tuple(t.ne[:t.rank]), C.string_at(L.ingot_gguf_data(g, tp), t.nbytes)))
+        out.append((t.name.decode("utf-8", "replace"), t.type, tuple(t.ne[:t.rank]),
+                    C.string_at(L.ingot_gguf_data(g, tp), t.nbytes)))
     L.ingot_gguf_close(g)
     return out
 
@@ -251,3 +252,51 @@ def test_gguf_weights_on_the_device(gpu, orc, tmp_path):
         H.mynah_asr_qmat_free(C.byref(m))
         H.mynah_asr_qmat_free(C.byref(m2))
     g.close()
+
+
+def test_mutated_files_never_read_outside(lib, tmp_path):
+    """Seeded mutation fuzz (as the reference fuzzes its reader,
+    third_party/ingot/tests/fuzz_mutate.c): flipped bytes, overwritten
+    length fields and truncations are either refused or parsed into tensors
+    whose bytes lie inside the file; where both readers accept a file they
+    agree on it."""
+    L = ingot_lib() if O.IngotRef.available() else None
+    tens = sample_tensors(lib)[:3]
+    good = str(tmp_path / "seed.gguf")
+    write_gguf(good, tens, [("general.name", 8, "x"), ("arr", 9, (8, ["a", "b"]))], alignment=64)
+    blob = bytearray(open(good, "rb").read())
+    rng = np.random.default_rng(1234)
+    accepted = 0
+    for i in range(300):
+        b = bytearray(blob)
+        kind = i % 3
+        if kind == 0:                      # a few random byte flips in the header and tables
+            for _ in range(rng.integers(1, 4)):
+                b[rng.integers(0, min(len(b), 600))] ^= int(rng.integers(1, 256))
+        elif kind == 1:                    # a huge or odd value over an 8-byte field
+            o = int(rng.integers(8, min(len(b), 600) - 8))
+            vals = [0, 1, 1 << 31, 1 << 40, (1 << 64) - 1]
+            b[o:o + 8] = struct.pack("<Q", vals[int(rng.integers(0, len(vals)))])
+        else:                              # truncation
+            b = b[:int(rng.integers(0, len(b)))]
+        p = str(tmp_path / f"m{i}.gguf")
+        with open(p, "wb") as f:
+            f.write(bytes(b))
+        try:
+            g = M.Gguf(lib, p)
+        except ValueError:
+            continue
+        accepted += 1
+        for name, typ, ne, raw, ptr in g.tensors():
+            assert len(raw) <= len(b)
+        g.close()
+        if L is not None:
+            gi = C.c_void_p()
+            err = C.create_string_buffer(256)
+            if L.ingot_gguf_open(C.byref(gi), p.encode(), err, 256) == 0:
+                L.ingot_gguf_close(gi)
+                ours_t, _, _ = ours(lib, p)
+                theirs = ingot_read(L, p)
+                # names, types and shapes agree wherever both read every tensor
+                assert [(n, t, ne) for n, t, ne, _ in ours_t] == [(n, t, ne) for n, t, ne, _ in theirs]
+    assert accepted > 0   # some mutations (in payload bytes, unused fields) still parse

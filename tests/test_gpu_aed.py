@@ -156,3 +156,20 @@ def test_aed_rejects_unsupported(gpu):
     with pytest.raises(RuntimeError, match="bad argument"):
         dev.forced(enc.data_ptr(), 4, list(range(9)))      # more positions than max_seq
     dev.close()
+
+
+@pytest.mark.parametrize("nl,T", [(0, 5), (1, 1)])
+def test_aed_edge_shapes(gpu, orc, nl, T):
+    """No decoder layers (embedding, final norm and head only); a one-frame
+    encoder output (cross attention over a single key)."""
+    import torch
+    say("aed edge", nl, T)
+    d, H, ffn, vocab, max_seq = 128, 2, 256, 300, 16
+    params = make_params(40 + nl, d, H, ffn, vocab, nl, max_seq)
+    dev = M.DeviceAed(gpu, params, H, M.Q8_0)
+    enc = np.random.default_rng(41).standard_normal((T, d)).astype(np.float32)
+    denc = torch.from_numpy(enc).cuda()
+    toks = [3, 1, 4, 1, 5, 9, 2, 6]
+    got = dev.forced(denc.data_ptr(), T, toks)
+    check_logits(got, oracle_model(orc, dev, params, H).forced(enc, toks), f"edge layers={nl} T={T}")
+    dev.close()
