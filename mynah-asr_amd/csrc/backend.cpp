@@ -98,8 +98,11 @@ hipStream_t pick_stream(void *s) {
     return c ? c->st : nullptr;
 }
 
-bool wants_xsum(int qtype) {
-    return qtype == MYNAH_ASR_HIP_Q4_K || qtype == MYNAH_ASR_HIP_Q5_K || qtype == MYNAH_ASR_HIP_Q2_K;
+// row sums of x the EXACT products with this format read: 0 none, 1 per
+// 16-element sub-block (Q2_K), 2 per 32-element sub-block (Q4_K, Q5_K)
+int wants_xsum(int qtype) {
+    if (qtype == MYNAH_ASR_HIP_Q2_K) return 1;
+    return qtype == MYNAH_ASR_HIP_Q4_K || qtype == MYNAH_ASR_HIP_Q5_K ? 2 : 0;
 }
 
 mynah_asr_hip_weight *upload(const mynah_asr_hip_wdesc *w) {
@@ -161,12 +164,13 @@ int check_numerics_supported(int qtype) {
 
 // Prepare x (device) for products with weight W in the current numerics mode,
 // into the calling thread's workspace.
-//   EXACT:   xp = f16 A fragments, xs16 = sub-block sums, xpf = chunk fold factors
+//   EXACT:   xp = f16 A fragments, xs16 = sub-block sums (16- or 32-element,
+//            as the format reads them), xpf = chunk fold factors
 //   INT8ACT: xp = int8 A fragments, xs16 = row scales sx
 int prep_into(PrepBuf &P, const mynah_asr_hip_weight *W, const float *dx, int T, hipStream_t st) {
     const int Mpad = mh_mpad(T), Kp = W->dw.Kp, k = W->dw.k;
     const bool i8 = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT;
-    const bool xsum = !i8 && wants_xsum(W->qtype);
+    const int xsum = i8 ? 0 : wants_xsum(W->qtype);
     uint8_t *xp = (uint8_t *)P.xp.get((size_t)Mpad * Kp * (i8 ? 1 : 4));
     float *xs16 = (float *)P.xs16.get((size_t)Mpad * (i8 ? 1 : Kp / 16) * sizeof(float));
     float *xpf = (float *)P.xpf.get((size_t)Mpad * (Kp / 128) * sizeof(float));
@@ -176,12 +180,12 @@ int prep_into(PrepBuf &P, const mynah_asr_hip_weight *W, const float *dx, int T,
         e = mh_launch_prep_i8(dx, T, k, Kp, Mpad, xp, xs16, st);
     } else {
         const int vec = (k % 8 == 0) && (((uintptr_t)dx & 15) == 0);
-        e = mh_launch_prep(dx, T, k, Kp, Mpad, xp, xs16, xpf, xsum ? 1 : 0, vec, st);
+        e = mh_launch_prep(dx, T, k, Kp, Mpad, xp, xs16, xpf, xsum, vec, st);
     }
     if (e != hipSuccess) return fail("prep launch failed", hipGetErrorString(e));
     P.T = T;
     P.Kp = Kp;
-    P.xsum = xsum ? 1 : 0;
+    P.xsum = xsum;
     P.i8 = i8 ? 1 : 0;
     return 0;
 }
@@ -191,7 +195,7 @@ int prep_for(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, int T, hipS
 
 bool fits(const PrepBuf &P, const mynah_asr_hip_weight *W, int T) {
     const bool i8 = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT;
-    return P.T == T && P.Kp == W->dw.Kp && P.i8 == (i8 ? 1 : 0) && (i8 || !wants_xsum(W->qtype) || P.xsum);
+    return P.T == T && P.Kp == W->dw.Kp && P.i8 == (i8 ? 1 : 0) && (i8 || !wants_xsum(W->qtype) || P.xsum == wants_xsum(W->qtype));
 }
 bool prep_fits(const Ctx *c, const mynah_asr_hip_weight *W, int T) { return fits(c->pa, W, T); }
 
@@ -234,7 +238,7 @@ int ffn_dev(Ctx *c, const mynah_asr_hip_weight *W1, const mynah_asr_hip_weight *
         if (prep_into(c->pa, W1, dx, T, st)) return -1;
         PrepBuf &P = c->pb;
         const int Mpad = mh_mpad(T), Kp = W2->dw.Kp;
-        const int xsum = wants_xsum(W2->qtype) ? 1 : 0;
+        const int xsum = wants_xsum(W2->qtype);
         uint8_t *xp = (uint8_t *)P.xp.get((size_t)Mpad * Kp * 4);
         float *xs16 = (float *)P.xs16.get((size_t)Mpad * (Kp / 16) * sizeof(float));
         float *xpf = (float *)P.xpf.get((size_t)Mpad * (Kp / 128) * sizeof(float));

@@ -142,10 +142,18 @@ __device__ __forceinline__ void load_bk(const DevW &W, int Kc, const int (&gn)[W
 // A fragments of one kstep for WM row groups: the two f16 terms of its two
 // half-steps, and (affine formats) the 16-element sub-block sums of the
 // lane's 16 D-layout rows.
+// A fragments of one kstep; xs = the rows' sub-block sums of x: for the
+// 16-element sub-blocks (SUB16) one per half-step, else (32-element
+// sub-blocks) the kstep's sum in xs[i][0]
 template <int WM> struct AK {
     half8 h[WM][2], l[WM][2];
     f16v xs[WM][2];
 };
+
+// Affine formats whose sub-blocks are 32 elements (one kstep): the
+// preparation stores each row's 32-element sum (the two 16-element sums
+// added, the same float addition the kernels would do)
+template <int QT> constexpr bool xs32_fmt() { return Fmt<QT>::MINS && !Fmt<QT>::SUB16; }
 
 // The exact product of one kstep, folded into the chunk accumulator
 // (acc = fma(sc, t, acc) [- mn * sum_x]). The float operations each output
@@ -184,8 +192,7 @@ __device__ __forceinline__ void kstep(const AK<WM> &a, const BK<QT, WN> &b, cons
                 for (int e = 0; e < 16; e++) acc[i][j][e] = __builtin_fmaf(sc, t[e], acc[i][j][e]);
                 if constexpr (F::MINS) {
 #pragma unroll
-                    for (int e = 0; e < 16; e++)
-                        acc[i][j][e] = __builtin_fmaf(-mn, a.xs[i][0][e] + a.xs[i][1][e], acc[i][j][e]);
+                    for (int e = 0; e < 16; e++) acc[i][j][e] = __builtin_fmaf(-mn, a.xs[i][0][e], acc[i][j][e]);
                 }
             }
         }
@@ -299,7 +306,7 @@ template <int QT> struct StageLayout {
     static constexpr int H2 = HB + 4 * F::HB;                     // [4 cg][F::H2]
     static constexpr int PF = H2 + 4 * F::H2;                     // [2 rg][32 floats]
     static constexpr int XS = PF + 2 * 128;                       // [2 rg][4 sub-blocks][32 floats]
-    static constexpr int BYTES = XS + (F::MINS ? 2 * 512 : 0);
+    static constexpr int BYTES = XS + (F::MINS ? (F::SUB16 ? 2 * 512 : 2 * 256) : 0);
 };
 
 // workgroups per CU the register budget is sized for: as many as the LDS
@@ -320,8 +327,8 @@ template <int QT> constexpr int gemm_occ() {
 enum { EPI_Y = 0, EPI_PREP = 1 };
 struct PrepOut {
     uint8_t *xp;
-    float *xs16, *xpf;
-    int Kc, xsum;
+    float *xs, *xpf;
+    int Kc, xsum;   // xsum: 0 none, 1 16-element sums, 2 32-element sums
 };
 
 // ---------------------------------------------------------------------------
@@ -339,7 +346,7 @@ struct PrepOut {
 // grid = tilesM * tilesN workgroups.
 template <int QT, int EPI>
 __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint8_t *__restrict__ xp,
-                                                 const float *__restrict__ xs16,
+                                                 const float *__restrict__ xs,
                                                  const float *__restrict__ xpf, float *__restrict__ y,
                                                  int M, int act, int tilesM, int tilesN, PrepOut po) {
     using F = Fmt<QT>;
@@ -358,7 +365,7 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int hh = lane >> 5, col = lane & 31;
-    const int Kc = W.Kp / 128, Kp16 = W.Kp / 16;
+    const int Kc = W.Kp / 128, Kps = W.Kp / (xs32_fmt<QT>() ? 32 : 16);   // sums per row
     const int G0 = tm * 2, GC0 = tn * 4;
 
     auto stage = [&](int c, int h, uint8_t *B) {
@@ -373,8 +380,11 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
         if constexpr (F::H2 > 0) dma<F::H2>(F::h2_src(W, Kc, gc, c), B + L::H2 + wave * F::H2, lane);
         if (wave < 2) {
             dma<128>((const uint8_t *)(xpf + ((size_t)(G0 + wave) * Kc + c) * 32), B + L::PF + wave * 128, lane);
-            if constexpr (F::MINS)
-                dma<512>((const uint8_t *)(xs16 + ((size_t)(G0 + wave) * Kp16 + 8 * c + 4 * h) * 32),
+            if constexpr (xs32_fmt<QT>())
+                dma<256>((const uint8_t *)(xs + ((size_t)(G0 + wave) * Kps + 4 * c + 2 * h) * 32),
+                         B + L::XS + wave * 256, lane);
+            else if constexpr (F::MINS)
+                dma<512>((const uint8_t *)(xs + ((size_t)(G0 + wave) * Kps + 8 * c + 4 * h) * 32),
                          B + L::XS + wave * 512, lane);
         }
     };
@@ -393,7 +403,11 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
                     const uint8_t *pp = B + L::A + i * 8192 + ((2 * sl + kh) * 2) * 1024 + lane * 16;
                     a.h[i][kh] = *(const half8 *)pp;
                     a.l[i][kh] = *(const half8 *)(pp + 1024);
-                    if constexpr (F::MINS) a.xs[i][kh] = lds_rows16(B + L::XS + i * 512 + (2 * sl + kh) * 128, hh);
+                    if constexpr (xs32_fmt<QT>()) {
+                        if (kh == 0) a.xs[i][0] = lds_rows16(B + L::XS + i * 256 + sl * 128, hh);
+                    } else if constexpr (F::MINS) {
+                        a.xs[i][kh] = lds_rows16(B + L::XS + i * 512 + (2 * sl + kh) * 128, hh);
+                    }
                 }
             BK<QT, WN> b;
             F::k_lds(B + L::P0 + wave * L::B0S, B + L::P1 + wave * L::B1S, s, lane, b.r[0]);
@@ -474,9 +488,17 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
             uint8_t *o = po.xp + ((((size_t)G * po.Kc + tn) * HSTEPS + uu) * 2) * 1024;
             *(half8 *)(o + lane * 16) = xh[u];
             *(half8 *)(o + (64 + lane) * 16) = xl[u];
-            if (po.xsum) {
+            if (po.xsum == 1) {
                 const float s16 = s8[u] + __shfl_xor(s8[u], 32);
-                if (hh == 0) po.xs16[((size_t)G * (8 * po.Kc) + 8 * tn + uu) * 32 + col] = s16;
+                if (hh == 0) po.xs[((size_t)G * (8 * po.Kc) + 8 * tn + uu) * 32 + col] = s16;
+            }
+        }
+        if (po.xsum == 2) {   // 32-element sums: half-steps (2b, 2b+1) added in that order
+#pragma unroll
+            for (int u = 0; u < 4; u += 2) {
+                const float s0 = s8[u] + __shfl_xor(s8[u], 32), s1 = s8[u + 1] + __shfl_xor(s8[u + 1], 32);
+                const int b = (4 * uh + u) / 2;
+                if (hh == 0) po.xs[((size_t)G * (4 * po.Kc) + 4 * tn + b) * 32 + col] = s0 + s1;
             }
         }
         if (hh == 0 && uh == 0) po.xpf[((size_t)G * po.Kc + tn) * 32 + col] = ldexpf(1.0f, -sh);
@@ -644,12 +666,19 @@ __device__ __forceinline__ void gemv_body(const DevW &W, const float *__restrict
             for (int kh = 0; kh < 2; kh++) {
                 a.h[0][kh] = xc.h[2 * s + kh];
                 a.l[0][kh] = xc.l[2 * s + kh];
-                if constexpr (Fmt<QT>::MINS) {
+                if constexpr (Fmt<QT>::MINS && !xs32_fmt<QT>()) {
                     // sub-block sums of the D-layout rows (rows >= 16 are not live)
                     const float s16 = xc.s8[2 * s + kh] + __shfl_xor(xc.s8[2 * s + kh], 32);
 #pragma unroll
                     for (int e = 0; e < 16; e++) a.xs[0][kh][e] = e < 8 ? __shfl(s16, drow(e, hh)) : 0.0f;
                 }
+            }
+            if constexpr (xs32_fmt<QT>()) {   // the kstep's 32-element sums, as the preparation adds them
+                const float s0 = xc.s8[2 * s] + __shfl_xor(xc.s8[2 * s], 32);
+                const float s1 = xc.s8[2 * s + 1] + __shfl_xor(xc.s8[2 * s + 1], 32);
+                const float s32 = s0 + s1;
+#pragma unroll
+                for (int e = 0; e < 16; e++) a.xs[0][0][e] = e < 8 ? __shfl(s32, drow(e, hh)) : 0.0f;
             }
             kstep<QT, 1, WNG>(a, bk[s], hd, s, acc);
         }
@@ -708,11 +737,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_jobs(GJobs J, GPro pro) {
 // Activation preparation for k_gemm: one workgroup (4 waves) per 32-row
 // group; wave w splits chunks c = w, w+4, ... with split_chunk and stores
 //   xp   A fragments of (xh, xl), zero beyond M and K   [G][chunk][u][term][64][16 B]
-//   xs16 per row and 16-element sub-block: (first 8 in order) + (next 8)
+//   xs   per row and 16-element sub-block: (first 8 in order) + (next 8)
+//        (want_xsum 1), or per 32-element sub-block the two added (want_xsum 2)
 //   xpf  per row group, chunk and row: the fold factor 2^-sh  [G][chunk][32]
 template <bool VEC>
 __global__ __launch_bounds__(256) void k_prep(const float *__restrict__ x, int M, int K, int Kp,
-                                              uint8_t *__restrict__ xp, float *__restrict__ xs16,
+                                              uint8_t *__restrict__ xp, float *__restrict__ xs,
                                               float *__restrict__ xpf, int want_xsum) {
     const int G = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 31, hh = lane >> 5, m = 32 * G + r;
@@ -727,9 +757,17 @@ __global__ __launch_bounds__(256) void k_prep(const float *__restrict__ x, int M
             const size_t off = ((((size_t)G * Kc + c) * HSTEPS + u) * 2) * 64 * 16;
             *(half8 *)(xp + off + lane * 16) = xc.h[u];
             *(half8 *)(xp + off + (64 + lane) * 16) = xc.l[u];
-            if (want_xsum) {
+            if (want_xsum == 1) {
                 const float s16 = xc.s8[u] + __shfl_xor(xc.s8[u], 32);
-                if (hh == 0) xs16[((size_t)G * (Kp / 16) + 8 * c + u) * 32 + r] = s16;
+                if (hh == 0) xs[((size_t)G * (Kp / 16) + 8 * c + u) * 32 + r] = s16;
+            }
+        }
+        if (want_xsum == 2) {
+#pragma unroll
+            for (int b = 0; b < HSTEPS / 2; b++) {
+                const float s0 = xc.s8[2 * b] + __shfl_xor(xc.s8[2 * b], 32);
+                const float s1 = xc.s8[2 * b + 1] + __shfl_xor(xc.s8[2 * b + 1], 32);
+                if (hh == 0) xs[((size_t)G * (Kp / 32) + 4 * c + b) * 32 + r] = s0 + s1;
             }
         }
         if (hh == 0) xpf[((size_t)G * Kc + c) * 32 + r] = xc.p;
