@@ -39,6 +39,7 @@
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
@@ -65,6 +66,23 @@ __device__ __forceinline__ half8 pairs_to_half8(uint32_t a, uint32_t b, uint32_t
     half2v v2 = __builtin_bit_cast(half2v, c), v3 = __builtin_bit_cast(half2v, d);
     const half2v nb = {(_Float16)-bias, (_Float16)-bias};
     v0 += nb; v1 += nb; v2 += nb; v3 += nb;
+    half8 r;
+    r[0] = v0[0]; r[1] = v0[1]; r[2] = v1[0]; r[3] = v1[1];
+    r[4] = v2[0]; r[5] = v2[1]; r[6] = v3[0]; r[7] = v3[1];
+    return r;
+}
+
+// the same pairs (1024 + code) times an integer sub-block factor f: one
+// packed f16 fma per pair, v*f - 1024*f, whose exact value (code*f) is an
+// f16 integer below 2048, so the single rounding is exact
+__device__ __forceinline__ half8 pairs_to_half8_f(uint32_t a, uint32_t b, uint32_t c, uint32_t d, half2v f) {
+    const half2v nb = f * (half2v){(_Float16)-1024.0f, (_Float16)-1024.0f};   // exact: 2^10 * f
+    half2v v0 = __builtin_bit_cast(half2v, a), v1 = __builtin_bit_cast(half2v, b);
+    half2v v2 = __builtin_bit_cast(half2v, c), v3 = __builtin_bit_cast(half2v, d);
+    v0 = __builtin_elementwise_fma(v0, f, nb);
+    v1 = __builtin_elementwise_fma(v1, f, nb);
+    v2 = __builtin_elementwise_fma(v2, f, nb);
+    v3 = __builtin_elementwise_fma(v3, f, nb);
     half8 r;
     r[0] = v0[0]; r[1] = v0[1]; r[2] = v1[0]; r[3] = v1[1];
     r[4] = v2[0]; r[5] = v2[1]; r[6] = v3[0]; r[7] = v3[1];
@@ -175,7 +193,20 @@ __device__ __forceinline__ half8 dec_nib(uint32_t w, _Float16 bias) {
 //   scale(hdr, s, hh, &sc, &mn)           factor (and min) of kstep s's
 //                                         sub-block hh (0 unless SUB16)
 // The factors are computed exactly as the reference decoders do, so that
-// sc*q - mn (or sc*q) reproduces their f32 values bit for bit.
+// sc*q - mn (or sc*q) reproduces their f32 values bit for bit (the dequant
+// kernel).
+//
+// Formats whose sub-block factors are small integers under one f32 (or f16)
+// super-block factor — Q2_K, Q3_K, Q4_K, Q5_K — also carry, for the product
+// kernels:
+//   FHdr                  the chunk's integer sub-block factors as f16 pairs
+//                         (sf), the super-block factor d, and for the affine
+//                         ones dm = 32 * dmin and the integer mins as the B
+//                         operand of one MFMA (mb: slot j = min of sub-block j,
+//                         in both lane halves)
+//   load_fhdr / fhdr_lds  as load_hdr / hdr_lds
+//   decode_f(raw, s, kh, fh)  half8 of q * (integer factor) of half-step
+//                         2s+kh: exact f16 integers (|q*f| < 2048)
 // ---------------------------------------------------------------------------
 template <int QT> struct Fmt;
 
@@ -298,10 +329,8 @@ template <> struct Fmt<QT_Q4_0> {
 
 // Q4_K / Q5_K super-block header: f16 d, f16 dmin, 12 bytes of packed 6-bit
 // scales and mins (ingot dequant.c:59-68 unpacking).
-__device__ __forceinline__ void k4_scale_min(const uint32_t (&hd)[4], int j, float &sc, float &mn) {
-    const float d = h2f(hd[0] & 0xffff), dmin = h2f(hd[0] >> 16);
+__device__ __forceinline__ void k4_ints(const uint32_t (&hd)[4], int j, uint32_t &s, uint32_t &m) {
     auto byte = [&](int i) -> uint32_t { return (sel4(hd, 1 + (i >> 2)) >> (8 * (i & 3))) & 0xffu; };
-    uint32_t s, m;
     if (j < 4) {
         s = byte(j) & 63u;
         m = byte(j + 4) & 63u;
@@ -309,8 +338,39 @@ __device__ __forceinline__ void k4_scale_min(const uint32_t (&hd)[4], int j, flo
         s = (byte(j + 4) & 15u) | ((byte(j - 4) >> 6) << 4);
         m = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
     }
+}
+__device__ __forceinline__ void k4_scale_min(const uint32_t (&hd)[4], int j, float &sc, float &mn) {
+    const float d = h2f(hd[0] & 0xffff), dmin = h2f(hd[0] >> 16);
+    uint32_t s, m;
+    k4_ints(hd, j, s, m);
     sc = d * (float)s;
     mn = dmin * (float)m;
+}
+
+// folded factors of NS sub-blocks per chunk (see the trait notes)
+template <int NS> struct FoldHdr {
+    half2v sf[NS];
+    float d, dm;
+    half8 mb;
+};
+__device__ __forceinline__ half2v h2pair(int v) {
+    const _Float16 f = (_Float16)(float)v;
+    return (half2v){f, f};
+}
+__device__ __forceinline__ void k4fhdr_from(const uint8_t *p, int c, FoldHdr<4> &H) {
+    const uint4 v = *(const uint4 *)p;
+    const uint32_t hd[4] = {v.x, v.y, v.z, v.w};
+    H.d = h2f(hd[0] & 0xffff);
+    H.dm = h2f(hd[0] >> 16) * 32.0f;
+#pragma unroll
+    for (int s = 0; s < 8; s++) H.mb[s] = (_Float16)0.0f;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        uint32_t sc, mn;
+        k4_ints(hd, 4 * (c & 1) + s, sc, mn);
+        H.sf[s] = h2pair((int)sc);
+        H.mb[s] = (_Float16)(float)mn;
+    }
 }
 
 // the chunk's four sub-block factors and mins, decoded once per chunk
@@ -346,6 +406,18 @@ template <> struct Fmt<QT_Q4_K> {
         sc = H.sc[s];
         mn = H.mn[s];
     }
+    using FHdr = FoldHdr<4>;
+    static __device__ __forceinline__ void load_fhdr(const DevW &W, int Kc, int G, int c, int lane, FHdr &H) {
+        k4fhdr_from(W.h + hdr(G, Kc / 2, c / 2, lane) * 16, c, H);
+    }
+    static __device__ __forceinline__ void fhdr_lds(const uint8_t *hb, const uint8_t *, int c, int lane, FHdr &H) {
+        k4fhdr_from(hb + (lane & 31) * 16, c, H);
+    }
+    static __device__ __forceinline__ half8 decode_f(const RawK &R, int s, int kh, const FHdr &H) {
+        const uint32_t w = R.w[kh];
+        return pairs_to_half8_f(nib_pair(w, 0) | MAGIC, nib_pair(w, 1) | MAGIC, nib_pair(w, 2) | MAGIC,
+                                nib_pair(w, 3) | MAGIC, H.sf[s]);
+    }
 };
 
 template <> struct Fmt<QT_Q5_K> {
@@ -380,6 +452,21 @@ template <> struct Fmt<QT_Q5_K> {
     static __device__ __forceinline__ void scale(const Hdr &H, int s, int, float &sc, float &mn) {
         sc = H.sc[s];
         mn = H.mn[s];
+    }
+    using FHdr = FoldHdr<4>;
+    static __device__ __forceinline__ void load_fhdr(const DevW &W, int Kc, int G, int c, int lane, FHdr &H) {
+        k4fhdr_from(W.h + hdr(G, Kc / 2, c / 2, lane) * 16, c, H);
+    }
+    static __device__ __forceinline__ void fhdr_lds(const uint8_t *hb, const uint8_t *, int c, int lane, FHdr &H) {
+        k4fhdr_from(hb + (lane & 31) * 16, c, H);
+    }
+    static __device__ __forceinline__ half8 decode_f(const RawK &R, int s, int kh, const FHdr &H) {
+        const int u = 2 * s + kh;
+        const uint32_t w = R.w[kh], h = R.hb[0];
+        uint32_t p[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) p[t] = nib_pair(w, t) | (bit_pair(h, u, t) << 4) | MAGIC;
+        return pairs_to_half8_f(p[0], p[1], p[2], p[3], H.sf[s]);
     }
 };
 
@@ -482,6 +569,42 @@ template <> struct Fmt<QT_Q3_K> {
         sc = H.sc[2 * s + hh];
         mn = 0.0f;
     }
+    // folded: factor lo | hi << 4 minus 32 (|q*f| <= 128); no mins
+    using FHdr = FoldHdr<8>;
+    static __device__ __forceinline__ void ffrom(const uint8_t *p, float d, int c, FHdr &H) {
+        const uint4 v = *(const uint4 *)p;
+        const uint32_t sc[4] = {v.x, v.y, v.z, v.w};
+        auto byte = [&](int i) -> int { return (int)((sel4(sc, i >> 2) >> (8 * (i & 3))) & 0xffu); };
+        H.d = d;
+        H.dm = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int j = 8 * (c & 1) + q;
+            const int lo = j < 8 ? (byte(j) & 15) : (byte(j - 8) >> 4);
+            const int hi = (byte(8 + (j & 3)) >> (2 * (j >> 2))) & 3;
+            H.sf[q] = h2pair((lo | (hi << 4)) - 32);
+            H.mb[q] = (_Float16)0.0f;
+        }
+    }
+    static __device__ __forceinline__ void load_fhdr(const DevW &W, int Kc, int G, int c, int lane, FHdr &H) {
+        const size_t u = hdr(G, Kc / 2, c / 2, lane);
+        ffrom(W.h + u * 16, W.h2[u], c, H);
+    }
+    static __device__ __forceinline__ void fhdr_lds(const uint8_t *hb, const uint8_t *h2b, int c, int lane, FHdr &H) {
+        ffrom(hb + (lane & 31) * 16, ((const float *)h2b)[lane & 31], c, H);
+    }
+    static __device__ __forceinline__ half8 decode_f(const RawK &R, int s, int kh, const FHdr &H) {
+        const half8 q = decode(R, s, kh);
+        const half2v f = H.sf[2 * s + kh];
+        half8 r;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const half2v v = (half2v){q[2 * t], q[2 * t + 1]} * f;
+            r[2 * t] = v[0];
+            r[2 * t + 1] = v[1];
+        }
+        return r;
+    }
 };
 
 // Q2_K: header unit = 16 scale|min bytes per column, h2 = (d, dmin) (f32 pair).
@@ -530,6 +653,33 @@ template <> struct Fmt<QT_Q2_K> {
     static __device__ __forceinline__ void scale(const Hdr &H, int s, int hh, float &sc, float &mn) {
         sc = H.sc[2 * s + hh];
         mn = H.mn[2 * s + hh];
+    }
+    using FHdr = FoldHdr<8>;
+    static __device__ __forceinline__ void ffrom(const uint8_t *p, float2 dd, int c, FHdr &H) {
+        const uint4 v = *(const uint4 *)p;
+        const uint32_t sc[4] = {v.x, v.y, v.z, v.w};
+        H.d = dd.x;
+        H.dm = dd.y * 32.0f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int j = 8 * (c & 1) + q;
+            const uint32_t b = (sel4(sc, j >> 2) >> (8 * (j & 3))) & 0xffu;
+            H.sf[q] = h2pair((int)(b & 15u));
+            H.mb[q] = (_Float16)(float)(b >> 4);
+        }
+    }
+    static __device__ __forceinline__ void load_fhdr(const DevW &W, int Kc, int G, int c, int lane, FHdr &H) {
+        const size_t u = hdr(G, Kc / 2, c / 2, lane);
+        ffrom(W.h + u * 16, *(const float2 *)(W.h2 + 2 * u), c, H);
+    }
+    static __device__ __forceinline__ void fhdr_lds(const uint8_t *hb, const uint8_t *h2b, int c, int lane, FHdr &H) {
+        ffrom(hb + (lane & 31) * 16, *(const float2 *)(h2b + (lane & 31) * 8), c, H);
+    }
+    static __device__ __forceinline__ half8 decode_f(const RawK &R, int s, int kh, const FHdr &H) {
+        const int u = 2 * s + kh;
+        const uint32_t w = R.w[0];
+        return pairs_to_half8_f(crumb_pair(w, u, 0) | MAGIC, crumb_pair(w, u, 1) | MAGIC,
+                                crumb_pair(w, u, 2) | MAGIC, crumb_pair(w, u, 3) | MAGIC, H.sf[u]);
     }
 };
 

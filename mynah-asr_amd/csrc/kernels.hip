@@ -9,6 +9,9 @@
 //     sub-block factor is applied in f32: a = fma(sc, t, a) [; a = fma(-mn,
 //     sum_x, a) for the affine formats], a starting at zero in every chunk;
 //   * total = fma(2^-sh, a, total), chunks in order from zero. y = total.
+// Q2_K, Q3_K, Q4_K and Q5_K fold their integer sub-block factors f into the
+// decoded quants (q*f, exact in f16): a = the chunk's MFMAs straight through,
+// then a = d*a - 32*dmin*(mins MFMA over the rows' split sub-block sums).
 // Every step depends only on row m's own data and on K — never on M, on the
 // tile the row lands in, or on the kernel (GEMM or GEMV) that runs it — so
 // each row's bits are the same whatever the batch size.
@@ -124,13 +127,26 @@ __device__ __forceinline__ void split_chunk(const float *__restrict__ x, int M, 
 
 // ---------------------------------------------------------------------------
 // Weight fragments of WN column groups: per-chunk headers and per-kstep words.
-template <int QT, int WN> struct BH { typename Fmt<QT>::Hdr h[WN]; };
+// Formats whose integer sub-block factors fold into the decoded weights (the
+// FHdr traits): a chunk's MFMAs then accumulate straight through its four
+// ksteps, and the factors d (and the mins, through one more MFMA) apply once
+// per chunk instead of once per sub-block
+template <int QT> constexpr bool fold_fmt() {
+    return QT == QT_Q2_K || QT == QT_Q3_K || QT == QT_Q4_K || QT == QT_Q5_K;
+}
+template <int QT, bool FOLD = fold_fmt<QT>()> struct KHdr { using T = typename Fmt<QT>::Hdr; };
+template <int QT> struct KHdr<QT, true> { using T = typename Fmt<QT>::FHdr; };
+
+template <int QT, int WN> struct BH { typename KHdr<QT>::T h[WN]; };
 template <int QT, int WN> struct BK { typename Fmt<QT>::RawK r[WN]; };
 
 template <int QT, int WN>
 __device__ __forceinline__ void load_bh(const DevW &W, int Kc, const int (&gn)[WN], int c, int lane, BH<QT, WN> &b) {
 #pragma unroll
-    for (int j = 0; j < WN; j++) Fmt<QT>::load_hdr(W, Kc, gn[j], c, lane, b.h[j]);
+    for (int j = 0; j < WN; j++) {
+        if constexpr (fold_fmt<QT>()) Fmt<QT>::load_fhdr(W, Kc, gn[j], c, lane, b.h[j]);
+        else Fmt<QT>::load_hdr(W, Kc, gn[j], c, lane, b.h[j]);
+    }
 }
 template <int QT, int WN>
 __device__ __forceinline__ void load_bk(const DevW &W, int Kc, const int (&gn)[WN], int c, int s, int lane,
@@ -140,29 +156,33 @@ __device__ __forceinline__ void load_bk(const DevW &W, int Kc, const int (&gn)[W
 }
 
 // A fragments of one kstep for WM row groups: the two f16 terms of its two
-// half-steps, and (affine formats) the 16-element sub-block sums of the
-// lane's 16 D-layout rows.
-// A fragments of one kstep; xs = the rows' sub-block sums of x: for the
-// 16-element sub-blocks (SUB16) one per half-step, else (32-element
-// sub-blocks) the kstep's sum in xs[i][0]
+// half-steps
 template <int WM> struct AK {
     half8 h[WM][2], l[WM][2];
-    f16v xs[WM][2];
 };
 
-// Affine formats whose sub-blocks are 32 elements (one kstep): the
-// preparation stores each row's 32-element sum (the two 16-element sums
-// added, the same float addition the kernels would do)
-template <int QT> constexpr bool xs32_fmt() { return Fmt<QT>::MINS && !Fmt<QT>::SUB16; }
-
-// The exact product of one kstep, folded into the chunk accumulator
-// (acc = fma(sc, t, acc) [- mn * sum_x]). The float operations each output
-// sees, and their order, are the same in every caller.
+// The exact product of one kstep into the chunk accumulator. Folded formats:
+// acc += xh*(q f) + xl*(q f) for both half-steps, MFMA after MFMA; the others:
+// t = the kstep's MFMAs from zero, acc = fma(sc, t, acc) per sub-block. The
+// float operations each output sees, and their order, are the same in every
+// caller.
 template <int QT, int WM, int WN>
 __device__ __forceinline__ void kstep(const AK<WM> &a, const BK<QT, WN> &b, const BH<QT, WN> &hd, int s,
                                       f16v (&acc)[WM][WN]) {
     using F = Fmt<QT>;
-    if constexpr (QT == QT_F32) {
+    if constexpr (fold_fmt<QT>()) {
+#pragma unroll
+        for (int j = 0; j < WN; j++) {
+            const half8 b0 = F::decode_f(b.r[j], s, 0, hd.h[j]), b1 = F::decode_f(b.r[j], s, 1, hd.h[j]);
+#pragma unroll
+            for (int i = 0; i < WM; i++) {
+                acc[i][j] = mfma32(a.h[i][0], b0, acc[i][j]);
+                acc[i][j] = mfma32(a.h[i][1], b1, acc[i][j]);
+                acc[i][j] = mfma32(a.l[i][0], b0, acc[i][j]);
+                acc[i][j] = mfma32(a.l[i][1], b1, acc[i][j]);
+            }
+        }
+    } else if constexpr (QT == QT_F32) {
         // f32 weights: resident as (wh, wl) f16 pairs scaled per row by
         // 2^shw_n; acc += xh*wh + xh*wl + xl*wh straight into the chunk
         // accumulator (no per-kstep factor)
@@ -177,6 +197,7 @@ __device__ __forceinline__ void kstep(const AK<WM> &a, const BK<QT, WN> &b, cons
                     acc[i][j] = mfma32(a.l[i][kh], b.r[j].h[kh], acc[i][j]);
                 }
     } else if constexpr (!F::SUB16) {
+        static_assert(!F::MINS, "affine formats fold");
 #pragma unroll
         for (int j = 0; j < WN; j++) {
             const half8 b0 = F::decode(b.r[j], s, 0), b1 = F::decode(b.r[j], s, 1);
@@ -190,13 +211,10 @@ __device__ __forceinline__ void kstep(const AK<WM> &a, const BK<QT, WN> &b, cons
                 t = mfma32(a.l[i][1], b1, t);
 #pragma unroll
                 for (int e = 0; e < 16; e++) acc[i][j][e] = __builtin_fmaf(sc, t[e], acc[i][j][e]);
-                if constexpr (F::MINS) {
-#pragma unroll
-                    for (int e = 0; e < 16; e++) acc[i][j][e] = __builtin_fmaf(-mn, a.xs[i][0][e], acc[i][j][e]);
-                }
             }
         }
     } else {
+        static_assert(!F::MINS, "affine formats fold");
 #pragma unroll
         for (int j = 0; j < WN; j++) {
             const half8 b0 = F::decode(b.r[j], s, 0), b1 = F::decode(b.r[j], s, 1);
@@ -214,15 +232,47 @@ __device__ __forceinline__ void kstep(const AK<WM> &a, const BK<QT, WN> &b, cons
                     acc[i][j][e] = __builtin_fmaf(sc0, t0[e], acc[i][j][e]);
                     acc[i][j][e] = __builtin_fmaf(sc1, t1[e], acc[i][j][e]);
                 }
-                if constexpr (F::MINS) {
-#pragma unroll
-                    for (int e = 0; e < 16; e++) {
-                        acc[i][j][e] = __builtin_fmaf(-mn0, a.xs[i][0][e], acc[i][j][e]);
-                        acc[i][j][e] = __builtin_fmaf(-mn1, a.xs[i][1][e], acc[i][j][e]);
-                    }
-                }
             }
         }
+    }
+}
+
+// The affine folded formats' row sums as the A operand of the chunk's mins
+// MFMA: sub-block sum x_j (NS per chunk: the 16-element sums (first 8 in
+// order) + (next 8), for 32-element sub-blocks two of them added) scaled by
+// 2^-5 (|x_j| < 2^20, so the result fits f16) and split into f16 hi_j + lo_j;
+// lane half 0 carries hi_j in slot j, half 1 lo_j, slots >= NS are zero. The
+// mins product is then sum_j (hi_j + lo_j) * m_j = 2^-5 * sum_j x_j m_j.
+__device__ __forceinline__ _Float16 xm_part(float xsum, int hh) {
+    const float v = xsum * 0.03125f;
+    const _Float16 hi = (_Float16)v;
+    return hh ? (_Float16)(v - (float)hi) : hi;
+}
+template <int NS>
+__device__ __forceinline__ half8 xm_frag(const float (&s8)[HSTEPS], int hh) {
+    float s16[HSTEPS];
+#pragma unroll
+    for (int u = 0; u < HSTEPS; u++) s16[u] = s8[u] + __shfl_xor(s8[u], 32);
+    half8 r;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        if (j < NS) r[j] = xm_part(NS == 8 ? s16[j] : s16[2 * j] + s16[2 * j + 1], hh);
+        else r[j] = (_Float16)0.0f;
+    }
+    return r;
+}
+
+// End of a chunk of a folded format: acc (= sum of x * q f over the chunk)
+// becomes d * acc - dm * (mins product), the chunk result the fold takes
+template <int QT>
+__device__ __forceinline__ void fold_finish(const half8 &xm, const typename KHdr<QT>::T &H, f16v &acc) {
+    if constexpr (Fmt<QT>::MINS) {
+        const f16v t2 = mfma32(xm, H.mb, zero16());
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[e] = __builtin_fmaf(-H.dm, t2[e], H.d * acc[e]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[e] = H.d * acc[e];
     }
 }
 
@@ -305,16 +355,17 @@ template <int QT> struct StageLayout {
     static constexpr int HB = P1 + 4 * B1S;                       // [4 cg][F::HB]
     static constexpr int H2 = HB + 4 * F::HB;                     // [4 cg][F::H2]
     static constexpr int PF = H2 + 4 * F::H2;                     // [2 rg][32 floats]
-    static constexpr int XS = PF + 2 * 128;                       // [2 rg][4 sub-blocks][32 floats]
-    static constexpr int BYTES = XS + (F::MINS ? (F::SUB16 ? 2 * 512 : 2 * 256) : 0);
+    static constexpr int XS = PF + 2 * 128;                       // [2 rg][64 lanes][16 B] mins A operand
+    static constexpr int BYTES = XS + (F::MINS ? 2 * 1024 : 0);
 };
 
 // workgroups per CU the register budget is sized for: as many as the LDS
-// ring allows, fewer for the K-quants (affine sums, sub-block factors, more
-// registers per wave); f32 weights (two f16 planes, 4 bytes per element)
-// stage 48 KiB per half-chunk, so one double-buffered workgroup fills the LDS
+// ring allows (three double-buffered workgroups for every quantized format),
+// two for Q6_K (its eight per-half-step f32 factors need more registers);
+// f32 weights (two f16 planes, 4 bytes per element) stage 48 KiB per
+// half-chunk, so one double-buffered workgroup fills the LDS
 template <int QT> constexpr int gemm_occ() {
-    return QT == QT_F32 ? 1 : ((Fmt<QT>::MINS || Fmt<QT>::SUB16) ? 2 : 3);
+    return QT == QT_F32 ? 1 : (QT == QT_Q6_K ? 2 : 3);
 }
 
 // Where a product's result goes: EPI_Y stores y (SiLU applied when act);
@@ -326,9 +377,9 @@ template <int QT> constexpr int gemm_occ() {
 // same f32 values (bit-identical to storing y and preparing it).
 enum { EPI_Y = 0, EPI_PREP = 1 };
 struct PrepOut {
-    uint8_t *xp;
-    float *xs, *xpf;
-    int Kc, xsum;   // xsum: 0 none, 1 16-element sums, 2 32-element sums
+    uint8_t *xp, *xm;
+    float *xpf;
+    int Kc, xsum;   // mins A operands (xm_frag): 0 none, 1 of 8 sub-blocks, 2 of 4
 };
 
 // ---------------------------------------------------------------------------
@@ -346,7 +397,7 @@ struct PrepOut {
 // grid = tilesM * tilesN workgroups.
 template <int QT, int EPI>
 __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint8_t *__restrict__ xp,
-                                                 const float *__restrict__ xs,
+                                                 const uint8_t *__restrict__ xm,
                                                  const float *__restrict__ xpf, float *__restrict__ y,
                                                  int M, int act, int tilesM, int tilesN, PrepOut po) {
     using F = Fmt<QT>;
@@ -365,7 +416,7 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int hh = lane >> 5, col = lane & 31;
-    const int Kc = W.Kp / 128, Kps = W.Kp / (xs32_fmt<QT>() ? 32 : 16);   // sums per row
+    const int Kc = W.Kp / 128;
     const int G0 = tm * 2, GC0 = tn * 4;
 
     auto stage = [&](int c, int h, uint8_t *B) {
@@ -380,18 +431,13 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
         if constexpr (F::H2 > 0) dma<F::H2>(F::h2_src(W, Kc, gc, c), B + L::H2 + wave * F::H2, lane);
         if (wave < 2) {
             dma<128>((const uint8_t *)(xpf + ((size_t)(G0 + wave) * Kc + c) * 32), B + L::PF + wave * 128, lane);
-            if constexpr (xs32_fmt<QT>())
-                dma<256>((const uint8_t *)(xs + ((size_t)(G0 + wave) * Kps + 4 * c + 2 * h) * 32),
-                         B + L::XS + wave * 256, lane);
-            else if constexpr (F::MINS)
-                dma<512>((const uint8_t *)(xs + ((size_t)(G0 + wave) * Kps + 8 * c + 4 * h) * 32),
-                         B + L::XS + wave * 512, lane);
+            // the mins operand is read at the chunk's end, from the second half
+            if constexpr (F::MINS)
+                if (h == 1) dma<1024>(xm + ((size_t)(G0 + wave) * Kc + c) * 1024, B + L::XS + wave * 1024, lane);
         }
     };
 
-    auto compute = [&](const uint8_t *B, int c, int h, f16v (&acc)[WM][WN]) {
-        BH<QT, WN> hd;
-        F::hdr_lds(B + L::HB + wave * F::HB, B + L::H2 + wave * F::H2, c, lane, hd.h[0]);
+    auto compute = [&](const uint8_t *B, int h, const BH<QT, WN> &hd, f16v (&acc)[WM][WN]) {
 #pragma unroll
         for (int sl = 0; sl < 2; sl++) {
             const int s = 2 * h + sl;
@@ -403,18 +449,10 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
                     const uint8_t *pp = B + L::A + i * 8192 + ((2 * sl + kh) * 2) * 1024 + lane * 16;
                     a.h[i][kh] = *(const half8 *)pp;
                     a.l[i][kh] = *(const half8 *)(pp + 1024);
-                    if constexpr (xs32_fmt<QT>()) {
-                        if (kh == 0) a.xs[i][0] = lds_rows16(B + L::XS + i * 256 + sl * 128, hh);
-                    } else if constexpr (F::MINS) {
-                        a.xs[i][kh] = lds_rows16(B + L::XS + i * 512 + (2 * sl + kh) * 128, hh);
-                    }
                 }
             BK<QT, WN> b;
             F::k_lds(B + L::P0 + wave * L::B0S, B + L::P1 + wave * L::B1S, s, lane, b.r[0]);
             kstep<QT, WM, WN>(a, b, hd, s, acc);
-            // the affine formats' sub-block sums would otherwise be hoisted a
-            // kstep ahead, past the register budget
-            if constexpr (F::MINS) __builtin_amdgcn_sched_barrier(0);
         }
     };
 
@@ -428,14 +466,28 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
         wait_vm<0>();
         __syncthreads();
         stage(c, 1, sbuf[1]);
+        // the chunk's factors, from its headers (staged with either half)
+        BH<QT, WN> hd;
+        if constexpr (fold_fmt<QT>())
+            F::fhdr_lds(sbuf[0] + L::HB + wave * F::HB, sbuf[0] + L::H2 + wave * F::H2, c, lane, hd.h[0]);
+        else
+            F::hdr_lds(sbuf[0] + L::HB + wave * F::HB, sbuf[0] + L::H2 + wave * F::H2, c, lane, hd.h[0]);
         f16v acc[WM][WN];
 #pragma unroll
         for (int i = 0; i < WM; i++) acc[i][0] = zero16();
-        compute(sbuf[0], c, 0, acc);
+        compute(sbuf[0], 0, hd, acc);
         wait_vm<0>();
         __syncthreads();
         if (c + 1 < Kc) stage(c + 1, 0, sbuf[0]);
-        compute(sbuf[1], c, 1, acc);
+        compute(sbuf[1], 1, hd, acc);
+        if constexpr (fold_fmt<QT>()) {
+#pragma unroll
+            for (int i = 0; i < WM; i++) {
+                half8 xmv = {};
+                if constexpr (F::MINS) xmv = *(const half8 *)(sbuf[1] + L::XS + i * 1024 + lane * 16);
+                fold_finish<QT>(xmv, hd.h[0], acc[i][0]);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < WM; i++) {
             const f16v pv = lds_rows16(sbuf[1] + L::PF + i * 128, hh);
@@ -488,17 +540,23 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
             uint8_t *o = po.xp + ((((size_t)G * po.Kc + tn) * HSTEPS + uu) * 2) * 1024;
             *(half8 *)(o + lane * 16) = xh[u];
             *(half8 *)(o + (64 + lane) * 16) = xl[u];
-            if (po.xsum == 1) {
-                const float s16 = s8[u] + __shfl_xor(s8[u], 32);
-                if (hh == 0) po.xs[((size_t)G * (8 * po.Kc) + 8 * tn + uu) * 32 + col] = s16;
-            }
         }
-        if (po.xsum == 2) {   // 32-element sums: half-steps (2b, 2b+1) added in that order
+        if (po.xsum) {
+            // this wave's sub-blocks of the mins operand (xm_frag's slots,
+            // the same arithmetic): half-steps 4uh .. 4uh+3
+            float s16[4];
 #pragma unroll
-            for (int u = 0; u < 4; u += 2) {
-                const float s0 = s8[u] + __shfl_xor(s8[u], 32), s1 = s8[u + 1] + __shfl_xor(s8[u + 1], 32);
-                const int b = (4 * uh + u) / 2;
-                if (hh == 0) po.xs[((size_t)G * (4 * po.Kc) + 4 * tn + b) * 32 + col] = s0 + s1;
+            for (int u = 0; u < 4; u++) s16[u] = s8[u] + __shfl_xor(s8[u], 32);
+            uint8_t *rec = po.xm + (((size_t)G * po.Kc + tn) * 64 + lane) * 16;
+            if (po.xsum == 1) {   // 16-element sub-blocks 4uh .. 4uh+3
+                half4v v;
+#pragma unroll
+                for (int u = 0; u < 4; u++) v[u] = xm_part(s16[u], hh);
+                *(half4v *)(rec + 8 * uh) = v;
+            } else {              // 32-element sub-blocks 2uh, 2uh+1; slots 4..7 zero
+                const half2v v = {xm_part(s16[0] + s16[1], hh), xm_part(s16[2] + s16[3], hh)};
+                *(half2v *)(rec + 4 * uh) = v;
+                if (uh == 1) *(uint2 *)(rec + 8) = make_uint2(0u, 0u);
             }
         }
         if (hh == 0 && uh == 0) po.xpf[((size_t)G * po.Kc + tn) * 32 + col] = ldexpf(1.0f, -sh);
@@ -666,21 +724,15 @@ __device__ __forceinline__ void gemv_body(const DevW &W, const float *__restrict
             for (int kh = 0; kh < 2; kh++) {
                 a.h[0][kh] = xc.h[2 * s + kh];
                 a.l[0][kh] = xc.l[2 * s + kh];
-                if constexpr (Fmt<QT>::MINS && !xs32_fmt<QT>()) {
-                    // sub-block sums of the D-layout rows (rows >= 16 are not live)
-                    const float s16 = xc.s8[2 * s + kh] + __shfl_xor(xc.s8[2 * s + kh], 32);
-#pragma unroll
-                    for (int e = 0; e < 16; e++) a.xs[0][kh][e] = e < 8 ? __shfl(s16, drow(e, hh)) : 0.0f;
-                }
-            }
-            if constexpr (xs32_fmt<QT>()) {   // the kstep's 32-element sums, as the preparation adds them
-                const float s0 = xc.s8[2 * s] + __shfl_xor(xc.s8[2 * s], 32);
-                const float s1 = xc.s8[2 * s + 1] + __shfl_xor(xc.s8[2 * s + 1], 32);
-                const float s32 = s0 + s1;
-#pragma unroll
-                for (int e = 0; e < 16; e++) a.xs[0][0][e] = e < 8 ? __shfl(s32, drow(e, hh)) : 0.0f;
             }
             kstep<QT, 1, WNG>(a, bk[s], hd, s, acc);
+        }
+        if constexpr (fold_fmt<QT>()) {
+            // the mins operand from this chunk's own sums, as the preparation forms it
+            half8 xmv = {};
+            if constexpr (Fmt<QT>::MINS) xmv = xm_frag<Fmt<QT>::SUB16 ? 8 : 4>(xc.s8, hh);
+#pragma unroll
+            for (int j = 0; j < WNG; j++) fold_finish<QT>(xmv, hd.h[j], acc[0][j]);
         }
 #pragma unroll
         for (int j = 0; j < WNG; j++)
@@ -737,12 +789,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_jobs(GJobs J, GPro pro) {
 // Activation preparation for k_gemm: one workgroup (4 waves) per 32-row
 // group; wave w splits chunks c = w, w+4, ... with split_chunk and stores
 //   xp   A fragments of (xh, xl), zero beyond M and K   [G][chunk][u][term][64][16 B]
-//   xs   per row and 16-element sub-block: (first 8 in order) + (next 8)
-//        (want_xsum 1), or per 32-element sub-block the two added (want_xsum 2)
+//   xm   the affine folded formats' mins A operand (xm_frag) of 8 (want_xsum
+//        1) or 4 (want_xsum 2) sub-blocks       [G][chunk][64][16 B]
 //   xpf  per row group, chunk and row: the fold factor 2^-sh  [G][chunk][32]
 template <bool VEC>
 __global__ __launch_bounds__(256) void k_prep(const float *__restrict__ x, int M, int K, int Kp,
-                                              uint8_t *__restrict__ xp, float *__restrict__ xs,
+                                              uint8_t *__restrict__ xp, uint8_t *__restrict__ xm,
                                               float *__restrict__ xpf, int want_xsum) {
     const int G = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 31, hh = lane >> 5, m = 32 * G + r;
@@ -757,18 +809,10 @@ __global__ __launch_bounds__(256) void k_prep(const float *__restrict__ x, int M
             const size_t off = ((((size_t)G * Kc + c) * HSTEPS + u) * 2) * 64 * 16;
             *(half8 *)(xp + off + lane * 16) = xc.h[u];
             *(half8 *)(xp + off + (64 + lane) * 16) = xc.l[u];
-            if (want_xsum == 1) {
-                const float s16 = xc.s8[u] + __shfl_xor(xc.s8[u], 32);
-                if (hh == 0) xs[((size_t)G * (Kp / 16) + 8 * c + u) * 32 + r] = s16;
-            }
         }
-        if (want_xsum == 2) {
-#pragma unroll
-            for (int b = 0; b < HSTEPS / 2; b++) {
-                const float s0 = xc.s8[2 * b] + __shfl_xor(xc.s8[2 * b], 32);
-                const float s1 = xc.s8[2 * b + 1] + __shfl_xor(xc.s8[2 * b + 1], 32);
-                if (hh == 0) xs[((size_t)G * (Kp / 32) + 4 * c + b) * 32 + r] = s0 + s1;
-            }
+        if (want_xsum) {
+            const half8 v = want_xsum == 1 ? xm_frag<8>(xc.s8, hh) : xm_frag<4>(xc.s8, hh);
+            *(half8 *)(xm + (((size_t)G * Kc + c) * 64 + lane) * 16) = v;
         }
         if (hh == 0) xpf[((size_t)G * Kc + c) * 32 + r] = xc.p;
     }
@@ -1050,10 +1094,10 @@ static hipError_t gemm_t(const DevW &W, const uint8_t *xp, const float *xs16, co
     const int tilesM = mpad / 64, tilesN = W.Np / 128;
     if (po) {
         if (po->Kc != tilesN) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_gemm<QT, EPI_PREP>), dim3(tilesM * tilesN), dim3(256), 0, st, W, xp, xs16, xpf, y, M,
+        hipLaunchKernelGGL((k_gemm<QT, EPI_PREP>), dim3(tilesM * tilesN), dim3(256), 0, st, W, xp, (const uint8_t *)xs16, xpf, y, M,
                            1, tilesM, tilesN, *po);
     } else {
-        hipLaunchKernelGGL((k_gemm<QT, EPI_Y>), dim3(tilesM * tilesN), dim3(256), 0, st, W, xp, xs16, xpf, y, M,
+        hipLaunchKernelGGL((k_gemm<QT, EPI_Y>), dim3(tilesM * tilesN), dim3(256), 0, st, W, xp, (const uint8_t *)xs16, xpf, y, M,
                            act, tilesM, tilesN, PrepOut{});
     }
     return hipGetLastError();
@@ -1109,7 +1153,7 @@ hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const flo
 hipError_t mh_launch_gemm_prep_out(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
                                    const float *xpf, int M, uint8_t *oxp, float *oxs16, float *oxpf, int oKc,
                                    int oxsum, hipStream_t st) {
-    const PrepOut po{oxp, oxs16, oxpf, oKc, oxsum};
+    const PrepOut po{oxp, (uint8_t *)oxs16, oxpf, oKc, oxsum};
     MH_DISPATCH(gemm_t, qtype, W, xp, xs16, xpf, nullptr, M, 1, &po, st)
 }
 
@@ -1117,9 +1161,9 @@ hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_
                           float *xpf, int want_xsum, int vec, hipStream_t st) {
     const dim3 grid(Mpad / 32, (Kp / 128 + 3) / 4);
     if (vec)
-        hipLaunchKernelGGL(k_prep<true>, grid, dim3(256), 0, st, x, M, K, Kp, xp, xs16, xpf, want_xsum);
+        hipLaunchKernelGGL(k_prep<true>, grid, dim3(256), 0, st, x, M, K, Kp, xp, (uint8_t *)xs16, xpf, want_xsum);
     else
-        hipLaunchKernelGGL(k_prep<false>, grid, dim3(256), 0, st, x, M, K, Kp, xp, xs16, xpf, want_xsum);
+        hipLaunchKernelGGL(k_prep<false>, grid, dim3(256), 0, st, x, M, K, Kp, xp, (uint8_t *)xs16, xpf, want_xsum);
     return hipGetLastError();
 }
 

@@ -10,6 +10,9 @@
 // kernels read whole row groups up to this count.
 static inline int mh_mpad(int M) { return (M + 63) / 64 * 64; }
 
+// x -> prepared activations: xp (f16 A fragments), xpf (fold factors) and,
+// for want_xsum 1 / 2, in xs16 (Mpad * Kp / 4 bytes) the mins operands of the
+// affine formats with 16- / 32-element sub-blocks
 hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,
                           float *xpf, int want_xsum, int vec, hipStream_t st);
 // M <= 16 (and K small enough for the LDS partials): the preparation-free GEMV
