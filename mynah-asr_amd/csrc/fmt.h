@@ -90,6 +90,11 @@ __device__ __forceinline__ half8 pairs_to_half8_f(uint32_t a, uint32_t b, uint32
 }
 
 #define MAGIC 0x64006400u
+// (a & b) | c as one v_bitop3_b32 (truth table over sources 0xF0, 0xCC, 0xAA:
+// (0xF0 & 0xCC) | 0xAA = 0xEA); the compiler would emit an and and an or
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_bitop3_b32(a, b, c, 0xEA);
+}
 __device__ __forceinline__ uint32_t nib_pair(uint32_t w, int t) { return (w >> (4 * t)) & 0x000F000Fu; }
 // pair t of half-step u in a crumb dword / a bit dword
 __device__ __forceinline__ uint32_t crumb_pair(uint32_t w, int u, int t) {
@@ -170,9 +175,42 @@ __device__ __forceinline__ void lds_kpart(const uint8_t *r, int s, int lane, uin
     }
 }
 
+// A nibble dword as four f16 pairs, with one shift: pairs 0 and 2 are the low
+// nibbles of the bytes of w and w >> 8 (value 1024 + q), pairs 1 and 3 their
+// high nibbles left in place (1024 + 16 q, still an exact f16 integer).
+struct NibPairs { half2v lo0, hi0, lo1, hi1; };
+__device__ __forceinline__ NibPairs nib_pairs(uint32_t w) {
+    const uint32_t w8 = w >> 8;
+    return {__builtin_bit_cast(half2v, and_or(w, 0x000F000Fu, MAGIC)), __builtin_bit_cast(half2v, and_or(w, 0x00F000F0u, MAGIC)),
+            __builtin_bit_cast(half2v, and_or(w8, 0x000F000Fu, MAGIC)),
+            __builtin_bit_cast(half2v, and_or(w8, 0x00F000F0u, MAGIC))};
+}
+__device__ __forceinline__ half8 pack_pairs(half2v v0, half2v v1, half2v v2, half2v v3) {
+    half8 r;
+    r[0] = v0[0]; r[1] = v0[1]; r[2] = v1[0]; r[3] = v1[1];
+    r[4] = v2[0]; r[5] = v2[1]; r[6] = v3[0]; r[7] = v3[1];
+    return r;
+}
+// q - (bias - 1024): exact packed adds, and for the in-place pairs
+// (1024 + 16 q) / 16 - (bias - 960) by one packed fma (1/16 is exact)
 __device__ __forceinline__ half8 dec_nib(uint32_t w, _Float16 bias) {
-    return pairs_to_half8(nib_pair(w, 0) | MAGIC, nib_pair(w, 1) | MAGIC, nib_pair(w, 2) | MAGIC,
-                          nib_pair(w, 3) | MAGIC, bias);
+    const NibPairs p = nib_pairs(w);
+    const half2v nb = {(_Float16)-bias, (_Float16)-bias};
+    const half2v r16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const _Float16 b16 = (_Float16)(960.0f - (float)bias);
+    const half2v nb16 = {b16, b16};
+    return pack_pairs(p.lo0 + nb, __builtin_elementwise_fma(p.hi0, r16, nb16), p.lo1 + nb,
+                      __builtin_elementwise_fma(p.hi1, r16, nb16));
+}
+// q * f for an integer factor f: v*f - 1024 f, and (1024 + 16 q) * (f/16) - 64 f
+// (every constant and the exact results are f16 integers or 2^-4 multiples)
+__device__ __forceinline__ half8 dec_nib_f(uint32_t w, half2v f) {
+    const NibPairs p = nib_pairs(w);
+    const half2v nb = f * (half2v){(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const half2v f16th = f * (half2v){(_Float16)0.0625f, (_Float16)0.0625f};
+    const half2v nb16 = f * (half2v){(_Float16)-64.0f, (_Float16)-64.0f};
+    return pack_pairs(__builtin_elementwise_fma(p.lo0, f, nb), __builtin_elementwise_fma(p.hi0, f16th, nb16),
+                      __builtin_elementwise_fma(p.lo1, f, nb), __builtin_elementwise_fma(p.hi1, f16th, nb16));
 }
 
 // ---------------------------------------------------------------------------
@@ -414,9 +452,7 @@ template <> struct Fmt<QT_Q4_K> {
         k4fhdr_from(hb + (lane & 31) * 16, c, H);
     }
     static __device__ __forceinline__ half8 decode_f(const RawK &R, int s, int kh, const FHdr &H) {
-        const uint32_t w = R.w[kh];
-        return pairs_to_half8_f(nib_pair(w, 0) | MAGIC, nib_pair(w, 1) | MAGIC, nib_pair(w, 2) | MAGIC,
-                                nib_pair(w, 3) | MAGIC, H.sf[s]);
+        return dec_nib_f(R.w[kh], H.sf[s]);
     }
 };
 
