@@ -16,8 +16,8 @@ their shared input), out and pos through qgemm_dev (preparation + product).
 step, in TOPS.
 
 Also reported (not `value`): per-kernel roofline fractions, the same step in
-INT8ACT numerics (int8 activations on the i8 MFMA, against 5.0 POP/s), Q4_K at
-BASELINE config 4's M = 12000 shapes, decoder GEMVs (config 3) in HBM GB/s with >= 512
+INT8ACT numerics (int8 activations on the i8 MFMA, against 5.0 POP/s), each of
+Q2_K, Q3_K, Q4_K, Q5_K and Q6_K at BASELINE config 4's M = 12000 shapes, decoder GEMVs (config 3) in HBM GB/s with >= 512
 MB of rotating weight copies (defeats the 256 MB MALL), timed as one HIP graph
 of all the launches (kernel_us; call_us = the same launches issued one by one
 from the host), the f32-weight GEMM, the relative-position attention core at T = 750
@@ -437,10 +437,13 @@ def main():
     details = {"encoder_q8_0_m6000": rows}
 
     if not args.no_extras:
-        log("[bench] K-quant Q4_K M=12000")
-        ms4, fl4, rows4 = run_encoder_set(B, M_, M_.Q4_K, 12000, KQ_SHAPES, 3, 1, 100)
-        details["kquant_q4_k_m12000"] = {"tops_per_layer_set": round(fl4 / (ms4 * 1e-3) / 1e12, 2),
-                                         "ms_per_layer_set": round(ms4, 3), "rows": rows4}
+        kq = {}
+        for qt in (M_.Q2_K, M_.Q3_K, M_.Q4_K, M_.Q5_K, M_.Q6_K):
+            log(f"[bench] K-quant {M_.NAMES[qt]} M=12000")
+            ms4, fl4, rows4 = run_encoder_set(B, M_, qt, 12000, KQ_SHAPES, 3, 1, 100)
+            kq[M_.NAMES[qt]] = {"tops_per_layer_set": round(fl4 / (ms4 * 1e-3) / 1e12, 2),
+                                "ms_per_layer_set": round(ms4, 3), "rows": rows4}
+        details["kquant_m12000"] = kq
         log("[bench] INT8ACT numerics, Q8_0 encoder set M=6000")
         lib.set_numerics(1)
         try:
