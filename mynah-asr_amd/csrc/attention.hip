@@ -14,8 +14,9 @@
 //
 // One workgroup = NW waves (4 or 8) = 16 NW query rows of one head of one
 // segment; wave w owns rows t0 + 16w .. +15. Keys are visited in tiles of 32 (only the tiles
-// the block's rows can see); each tile's K, V and the 16 NW + 16 rk rows of
-// the block's new position columns are staged in LDS, and every wave
+// the block's rows can see); each tile's K and V are staged in LDS, and the
+// 16 NW + 16 rk rows of the block's position columns stay in an LDS ring that
+// takes 32 new rows per tile; every wave
 //   1. forms the content scores (16 x 32) with its (q + bias_u) held in registers,
 //   2. forms the position scores (q + bias_v) . rk for its 16 rows in tiles of
 //      16 offsets delta = j - t: a key tile needs 47 offsets (three tiles),
@@ -53,7 +54,7 @@ template <int DK, int NW>
 struct AttnLds {
     static constexpr int NTH = 64 * NW;
     static constexpr int RB = 16 * NW;        // query rows per workgroup
-    static constexpr int NB = RB + KT - 16;   // rk rows staged per tile: the new position columns of all waves
+    static constexpr int NB = RB + KT - 16;   // rk rows a key tile reads (all waves' position columns): the ring
     static constexpr int KS = DK + 4;   // K / rk row stride (16-byte rows, conflict-free b128 reads)
     static constexpr int VT = KT + 4;   // V is stored transposed, [DK][VT]: conflict-free b128 reads
     static constexpr int BS = 53;       // band scratch row stride
@@ -177,10 +178,16 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     // past the ends are clamped, not zeroed: a key j outside [0, T) is masked
     // out of every score, and an rk row p outside [0, 2T-2] only pairs a query
     // row t >= T (never stored) or a masked key.
-    constexpr int UKV = KT * DK / 4 / NTH, NR4 = NB * DK / 4, UR = (NR4 + NTH - 1) / NTH;
+    //
+    // The rk rows form a ring of NB rows: key tile ti (0 = the tile before
+    // the first) reads window rows 32 ti .. 32 ti + NB - 1 (absolute rk row
+    // pb0 + v for window row v), in slot v mod NB; moving to the next tile
+    // retires the 32 lowest and stages 32 new ones into their slots.
+    constexpr int UKV = KT * DK / 4 / NTH, UR = KT * DK / 4 / NTH;
     static_assert(UKV * NTH == KT * DK / 4, "staging split");
     f4 gk[UKV], gv[UKV], gr[UR];
-    auto gload = [&](int jt) {
+    const int pb0 = T + (ja - KT) - t0 - (RB - 16);
+    auto gload = [&](int jt, int ti) {
 #pragma unroll
         for (int u = 0; u < UKV; u++) {
             const int i = tid + NTH * u;
@@ -189,15 +196,14 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
             const int rv = i % KT, cv = 4 * (i / KT);   // V: lanes along keys (transposed store)
             gv[u] = *(const f4 *)(v + (size_t)min(max(jt + rv, 0), T - 1) * d + ho + cv);
         }
-        const int pbase = T + jt - t0 - (RB - 16);
 #pragma unroll
         for (int u = 0; u < UR; u++) {
             const int i = tid + NTH * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
-            const int p = min(max(pbase + r, 0), P - 1);
-            if (NR4 % NTH == 0 || i < NR4) gr[u] = *(const f4 *)(rk + (size_t)p * d + ho + cc);
+            const int p = min(max(pb0 + 32 * ti + NB - 32 + r, 0), P - 1);
+            gr[u] = *(const f4 *)(rk + (size_t)p * d + ho + cc);
         }
     };
-    auto lstore = [&]() {
+    auto lstore = [&](int ti) {
 #pragma unroll
         for (int u = 0; u < UKV; u++) {
             const int i = tid + NTH * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
@@ -209,7 +215,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
 #pragma unroll
         for (int u = 0; u < UR; u++) {
             const int i = tid + NTH * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
-            if (NR4 % NTH == 0 || i < NR4) *(f4 *)(Rs + r * L::KS + cc) = gr[u];
+            *(f4 *)(Rs + ((32 * ti + NB - 32 + r) % NB) * L::KS + cc) = gr[u];
         }
     };
     // Position columns are computed in tiles of 16 offsets delta = j - t.
@@ -218,12 +224,14 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     // so it is carried in registers and every tile computes only D1 and D2
     // (rk rows T-1 + b + 16 .. + 47: staged row (RB - 16) - 16w + col).
     const int prow = (RB - 16) - 16 * w;
-    auto bd_tiles = [&](f4 *bd, int n0) {
+    // ring slots of this lane's window rows prow + 16n + c at tile ti
+    auto rrow = [&](int ti, int n) { return (32 * ti + prow + 16 * n + c) % NB; };
+    auto bd_tiles = [&](f4 *bd, int n0) {   // tile 0
 #pragma unroll
         for (int i = 0; i < NS / 4; i++) {
             f4 rx[2];
 #pragma unroll
-            for (int n = n0; n < 2; n++) rx[n] = *(const f4 *)(Rs + (prow + 16 * n + c) * L::KS + NS * g + 4 * i);
+            for (int n = n0; n < 2; n++) rx[n] = *(const f4 *)(Rs + rrow(0, n) * L::KS + NS * g + 4 * i);
 #pragma unroll
             for (int u = 0; u < 4; u++)
 #pragma unroll
@@ -232,21 +240,25 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     };
     f4 carry = {0.f, 0.f, 0.f, 0.f};
     {
-        // D0 of the first tile = D2 of the tile before it
-        gload(ja - KT);
-        lstore();
+        // D0 of the first tile = D2 of the tile before it: tile 0's whole
+        // window of rk rows (slots 0 .. NB-1), then its position tile D2
+        for (int i = tid; i < NB * DK / 4; i += NTH) {
+            const int r = i / (DK / 4), cc = 4 * (i % (DK / 4));
+            const int p = min(max(pb0 + r, 0), P - 1);
+            *(f4 *)(Rs + r * L::KS + cc) = *(const f4 *)(rk + (size_t)p * d + ho + cc);
+        }
         __syncthreads();
         f4 bd[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
         bd_tiles(bd, 1);
         carry = bd[1];
-        gload(ja);
+        gload(ja, 1);
     }
 
-    for (int jt = ja; jt < jb; jt += KT) {
+    for (int jt = ja, ti = 1; jt < jb; jt += KT, ti++) {
         __syncthreads();   // every wave is done with the previous tile
-        lstore();
+        lstore(ti);
         __syncthreads();
-        if (jt + KT < jb) gload(jt + KT);
+        if (jt + KT < jb) gload(jt + KT, ti + 1);
 
         // 1. content scores (16 rows x 32 keys), 2. position tiles D1, D2
         f4 s[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -257,7 +269,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
 #pragma unroll
             for (int n = 0; n < 2; n++) kx[n] = *(const f4 *)(Ks + (16 * n + c) * L::KS + NS * g + 4 * i);
 #pragma unroll
-            for (int n = 0; n < 2; n++) rx[n] = *(const f4 *)(Rs + (prow + 16 * n + c) * L::KS + NS * g + 4 * i);
+            for (int n = 0; n < 2; n++) rx[n] = *(const f4 *)(Rs + rrow(ti, n) * L::KS + NS * g + 4 * i);
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 s[0] = mfma16(qa[4 * i + u], kx[0][u], s[0]);
