@@ -1082,6 +1082,12 @@ static hipError_t gemv_t(const GJobs &J, const float *x, int M, int vec, const G
         if (Kc >= 8) return launch_gemv<QT, 8, 2>(J, x, M, vec, pro, st);
         return launch_gemv<QT, 4, 2>(J, x, M, vec, pro, st);
     }
+    // K >= 4096 over few column groups: 16 waves take two chunks each rather
+    // than 8 taking four (each chunk's loads wait a full memory latency);
+    // within the 128 registers a 1024-thread workgroup allows, except the
+    // formats whose GEMV needs more
+    if constexpr (QT != QT_F32 && QT != QT_Q4_K && QT != QT_Q5_K)
+        if (Kc >= 32) return launch_gemv<QT, 16, 1>(J, x, M, vec, pro, st);
     if (Kc >= 8) return launch_gemv<QT, 8, 1>(J, x, M, vec, pro, st);
     return launch_gemv<QT, 4, 1>(J, x, M, vec, pro, st);
 }
