@@ -645,12 +645,21 @@ __device__ void gemv_prologue(const GPro &pro, int K, int Kp, float *xs) {
         const int dk = K / pro.H;
         const int n = pro.n_fixed > 0 ? pro.n_fixed : pro.st[0] + 1;
         const int ns = min(mh_att_splits_dev(n), pro.nsplit);
+        // the split weights e^(m_s - M) once per (head, split), not per element
+        // (up to PW of them; beyond that each element recomputes its own)
+        constexpr int PW = 1024;
+        __shared__ float hw[PW];
+        const bool pre = pro.H * ns <= PW;
         if (tid < pro.H) {
             const float *ml = pro.ml + (size_t)tid * pro.nsplit * 2;
             float Mx = -INFINITY;
             for (int s2 = 0; s2 < ns; s2++) Mx = fmaxf(Mx, ml[2 * s2]);
             float L = 0.0f;
-            for (int s2 = 0; s2 < ns; s2++) L += ml[2 * s2 + 1] * expf(ml[2 * s2] - Mx);
+            for (int s2 = 0; s2 < ns; s2++) {
+                const float e = expf(ml[2 * s2] - Mx);
+                if (pre) hw[tid * ns + s2] = e;
+                L += ml[2 * s2 + 1] * e;
+            }
             hm[tid] = Mx;
             hl[tid] = L;
         }
@@ -663,7 +672,8 @@ __device__ void gemv_prologue(const GPro &pro, int K, int Kp, float *xs) {
                 const float Mx = hm[h];
                 float o = 0.0f;
                 for (int s2 = 0; s2 < ns; s2++)
-                    o += pro.opart[((size_t)h * pro.nsplit + s2) * dk + f] * expf(ml[2 * s2] - Mx);
+                    o += pro.opart[((size_t)h * pro.nsplit + s2) * dk + f] *
+                         (pre ? hw[h * ns + s2] : expf(ml[2 * s2] - Mx));
                 v = o / hl[h];
             }
             xs[i] = v;
@@ -1029,8 +1039,9 @@ __global__ void k_silu(float *__restrict__ x, size_t n) {
 
 template <typename F>
 static hipError_t allow_lds(F *f) {
-    // dynamic LDS beyond 64 KiB: gfx950 has 160 KiB, less the prologue's static scratch
-    return hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024);
+    // dynamic LDS beyond 64 KiB: gfx950 has 160 KiB, less the prologue's static
+    // scratch (about 5 KiB); the largest GEMV request is about 130 KiB
+    return hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, 154 * 1024);
 }
 
 template <int QT, int NW, int WNG, bool VEC, bool PRO>
