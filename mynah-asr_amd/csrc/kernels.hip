@@ -344,13 +344,21 @@ template <int N> __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// LDS stage of k_gemm: half a chunk (2 ksteps) of everything the workgroup
-// reads, for its 2 row groups and 4 column groups.
+// LDS stage of k_gemm: SPS ksteps (half a chunk; one kstep for f32 weights,
+// whose two f16 planes make a half-chunk stage 48 KiB) of everything the
+// workgroup reads, for its 2 row groups and 4 column groups. Planes of 32 or
+// more bytes per lane and chunk stage the stage's own part; narrower ones the
+// whole (column group, chunk) block.
 template <int QT> struct StageLayout {
     using F = Fmt<QT>;
-    static constexpr int A = 0;                                   // [2 rg][4 u][2 term][1 KiB]
-    static constexpr int B0S = Stage<F::B0>::BYTES, B1S = Stage<F::B1>::BYTES;
-    static constexpr int P0 = A + 2 * 8192;                       // [4 cg][B0S]
+    static constexpr int SPS = QT == QT_F32 ? 1 : 2;              // ksteps per stage
+    static constexpr int NST = KSTEPS / SPS;                      // stages per chunk
+    static constexpr int AR = SPS * 4096;                         // activation bytes per row group
+    template <int B> static constexpr int plane() { return B == 0 ? 0 : (B >= 32 ? SPS * 16 * B : 64 * B); }
+    template <int B> static __device__ int plane_off(int q) { return B >= 32 ? q * SPS * 16 * B : 0; }
+    static constexpr int A = 0;                                   // [2 rg][2 SPS u][2 term][1 KiB]
+    static constexpr int B0S = plane<F::B0>(), B1S = plane<F::B1>();
+    static constexpr int P0 = A + 2 * AR;                         // [4 cg][B0S]
     static constexpr int P1 = P0 + 4 * B0S;                       // [4 cg][B1S]
     static constexpr int HB = P1 + 4 * B1S;                       // [4 cg][F::HB]
     static constexpr int H2 = HB + 4 * F::HB;                     // [4 cg][F::H2]
@@ -360,13 +368,10 @@ template <int QT> struct StageLayout {
 };
 
 // workgroups per CU the register budget is sized for: as many as the LDS
-// ring allows (three double-buffered workgroups for every quantized format),
-// two for Q6_K (its eight per-half-step f32 factors need more registers);
-// f32 weights (two f16 planes, 4 bytes per element) stage 48 KiB per
-// half-chunk, so one double-buffered workgroup fills the LDS
-template <int QT> constexpr int gemm_occ() {
-    return QT == QT_F32 ? 1 : (QT == QT_Q6_K ? 2 : 3);
-}
+// ring allows (three double-buffered workgroups: 25-27 KiB stages, 24 KiB
+// one-kstep stages for f32 weights), two for Q6_K (its eight per-half-step
+// f32 factors need more registers)
+template <int QT> constexpr int gemm_occ() { return QT == QT_Q6_K ? 2 : 3; }
 
 // Where a product's result goes: EPI_Y stores y (SiLU applied when act);
 // EPI_PREP (the first product of the FFN) applies SiLU and, instead of
@@ -419,39 +424,41 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
     const int Kc = W.Kp / 128;
     const int G0 = tm * 2, GC0 = tn * 4;
 
-    auto stage = [&](int c, int h, uint8_t *B) {
+    auto stage = [&](int c, int q, uint8_t *B) {
         const int rg = wave >> 1, gc = GC0 + wave;
-        dma<4096>(xp + (((size_t)(G0 + rg) * Kc + c) * 16 + 8 * h + 4 * (wave & 1)) * 1024,
-                  B + L::A + rg * 8192 + (wave & 1) * 4096, lane);
-        dma<L::B0S>(W.p0 + ((size_t)gc * Kc + c) * 64 * F::B0 + Stage<F::B0>::off(h), B + L::P0 + wave * L::B0S, lane);
+        dma<L::AR / 2>(xp + (((size_t)(G0 + rg) * Kc + c) * 16 + 4 * L::SPS * q + 2 * L::SPS * (wave & 1)) * 1024,
+                       B + L::A + rg * L::AR + (wave & 1) * (L::AR / 2), lane);
+        dma<L::B0S>(W.p0 + ((size_t)gc * Kc + c) * 64 * F::B0 + L::template plane_off<F::B0>(q),
+                    B + L::P0 + wave * L::B0S, lane);
         if constexpr (F::B1 > 0)
-            dma<L::B1S>(W.p1 + ((size_t)gc * Kc + c) * 64 * F::B1 + Stage<F::B1>::off(h), B + L::P1 + wave * L::B1S,
-                        lane);
+            dma<L::B1S>(W.p1 + ((size_t)gc * Kc + c) * 64 * F::B1 + L::template plane_off<F::B1>(q),
+                        B + L::P1 + wave * L::B1S, lane);
         if constexpr (F::HB > 0) dma<F::HB>(F::hb_src(W, Kc, gc, c), B + L::HB + wave * F::HB, lane);
         if constexpr (F::H2 > 0) dma<F::H2>(F::h2_src(W, Kc, gc, c), B + L::H2 + wave * F::H2, lane);
         if (wave < 2) {
             dma<128>((const uint8_t *)(xpf + ((size_t)(G0 + wave) * Kc + c) * 32), B + L::PF + wave * 128, lane);
-            // the mins operand is read at the chunk's end, from the second half
+            // the mins operand is read at the chunk's end, from its last stage
             if constexpr (F::MINS)
-                if (h == 1) dma<1024>(xm + ((size_t)(G0 + wave) * Kc + c) * 1024, B + L::XS + wave * 1024, lane);
+                if (q == L::NST - 1) dma<1024>(xm + ((size_t)(G0 + wave) * Kc + c) * 1024, B + L::XS + wave * 1024, lane);
         }
     };
 
-    auto compute = [&](const uint8_t *B, int h, const BH<QT, WN> &hd, f16v (&acc)[WM][WN]) {
+    auto compute = [&](const uint8_t *B, int q, const BH<QT, WN> &hd, f16v (&acc)[WM][WN]) {
 #pragma unroll
-        for (int sl = 0; sl < 2; sl++) {
-            const int s = 2 * h + sl;
+        for (int sl = 0; sl < L::SPS; sl++) {
+            const int s = L::SPS * q + sl;
             AK<WM> a;
 #pragma unroll
             for (int i = 0; i < WM; i++)
 #pragma unroll
                 for (int kh = 0; kh < 2; kh++) {
-                    const uint8_t *pp = B + L::A + i * 8192 + ((2 * sl + kh) * 2) * 1024 + lane * 16;
+                    const uint8_t *pp = B + L::A + i * L::AR + ((2 * sl + kh) * 2) * 1024 + lane * 16;
                     a.h[i][kh] = *(const half8 *)pp;
                     a.l[i][kh] = *(const half8 *)(pp + 1024);
                 }
             BK<QT, WN> b;
-            F::k_lds(B + L::P0 + wave * L::B0S, B + L::P1 + wave * L::B1S, s, lane, b.r[0]);
+            // (one-kstep stages hold only kstep s: its local index is 0)
+            F::k_lds(B + L::P0 + wave * L::B0S, B + L::P1 + wave * L::B1S, L::SPS == 1 ? 0 : s, lane, b.r[0]);
             kstep<QT, WM, WN>(a, b, hd, s, acc);
         }
     };
@@ -461,25 +468,29 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
     for (int i = 0; i < WM; i++) total[i][0] = zero16();
     stage(0, 0, sbuf[0]);
     for (int c = 0; c < Kc; c++) {
-        // the stage (issued one half ago) has landed for every wave, and every
-        // wave is done reading the buffer the next stage overwrites
-        wait_vm<0>();
-        __syncthreads();
-        stage(c, 1, sbuf[1]);
-        // the chunk's factors, from its headers (staged with either half)
         BH<QT, WN> hd;
-        if constexpr (fold_fmt<QT>())
-            F::fhdr_lds(sbuf[0] + L::HB + wave * F::HB, sbuf[0] + L::H2 + wave * F::H2, c, lane, hd.h[0]);
-        else
-            F::hdr_lds(sbuf[0] + L::HB + wave * F::HB, sbuf[0] + L::H2 + wave * F::H2, c, lane, hd.h[0]);
         f16v acc[WM][WN];
 #pragma unroll
         for (int i = 0; i < WM; i++) acc[i][0] = zero16();
-        compute(sbuf[0], 0, hd, acc);
-        wait_vm<0>();
-        __syncthreads();
-        if (c + 1 < Kc) stage(c + 1, 0, sbuf[0]);
-        compute(sbuf[1], 1, hd, acc);
+        // NST (even) stages per chunk, alternating buffers: stage 0 of every
+        // chunk is in sbuf[0], the last in sbuf[1]
+#pragma unroll
+        for (int q = 0; q < L::NST; q++) {
+            // the stage (issued one stage ago) has landed for every wave, and
+            // every wave is done reading the buffer the next stage overwrites
+            wait_vm<0>();
+            __syncthreads();
+            if (q + 1 < L::NST) stage(c, q + 1, sbuf[(q + 1) & 1]);
+            else if (c + 1 < Kc) stage(c + 1, 0, sbuf[0]);
+            if (q == 0) {
+                // the chunk's factors, from its headers (staged with every stage)
+                if constexpr (fold_fmt<QT>())
+                    F::fhdr_lds(sbuf[0] + L::HB + wave * F::HB, sbuf[0] + L::H2 + wave * F::H2, c, lane, hd.h[0]);
+                else
+                    F::hdr_lds(sbuf[0] + L::HB + wave * F::HB, sbuf[0] + L::H2 + wave * F::H2, c, lane, hd.h[0]);
+            }
+            compute(sbuf[q & 1], q, hd, acc);
+        }
         if constexpr (fold_fmt<QT>()) {
 #pragma unroll
             for (int i = 0; i < WM; i++) {
