@@ -382,8 +382,9 @@ hipError_t launch_attn(const float *q, const float *k, const float *v, const flo
 
 // Eight waves (two per SIMD, one 128-row block) run full attention faster
 // once there are at least two rounds of such blocks for the 256 CUs; with
-// fewer blocks, or chunked windows (whose key range grows with the block),
-// four waves (64 rows) balance better.
+// fewer blocks four waves (64 rows) balance better. Chunked windows take two
+// waves (32 rows): a block visits the union of its rows' windows, so
+// narrower blocks skip more of the keys their rows cannot see.
 bool use8(int T, int H, int left, int nseq) {
     return left < 0 && (long)((T + 127) / 128) * H * nseq >= 512;
 }
@@ -393,6 +394,7 @@ hipError_t launch_dk(const float *q, const float *k, const float *v, const float
                      const float *bv, float *ctx, int T, int d, int H, int left, int right, int nseq,
                      hipStream_t st) {
     if (use8(T, H, left, nseq)) return launch_attn<DK, 8>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, st);
+    if (left >= 0) return launch_attn<DK, 2>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, st);
     return launch_attn<DK, 4>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, st);
 }
 
