@@ -80,6 +80,7 @@ struct Ctx {
     DBuf x, y, h;
     DBuf att;    // the host-pointer attention call's q, k, v, rk, biases and ctx
     DBuf aed;    // the AED decoder's caches and vectors
+    DBuf gs;     // split-K GEMV workspace
     int *pin = nullptr;   // pinned host int[2]: the step state read back
     PrepBuf pa;  // the products' input (prep_dev / qgemm_prepped_dev use this one)
     PrepBuf pb;  // the FFN's intermediate, prepared by the first product
@@ -214,11 +215,17 @@ int run_prepped(Ctx *c, const mynah_asr_hip_weight *W, float *dy, int T, int act
     return run_from(c->pa, W, dy, T, act, st);
 }
 
+// the calling thread's split-K GEMV workspace for W (null: the one-launch GEMV)
+float *gemv_ws(Ctx *c, const mynah_asr_hip_weight *W) {
+    const size_t n = mh_gemv_ws_floats(W->dw);
+    return n ? (float *)c->gs.get(n * sizeof(float)) : nullptr;
+}
+
 int gemm_dev(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, float *dy, int T, int act,
              hipStream_t st) {
     if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT && mh_use_gemv(W->dw, T)) {
         const int vec = (W->dw.k % 8 == 0) && (((uintptr_t)dx & 15) == 0);
-        hipError_t e = mh_launch_gemv(W->qtype, W->dw, dx, T, vec, dy, act, st);
+        hipError_t e = mh_launch_gemv(W->qtype, W->dw, dx, T, vec, dy, act, gemv_ws(c, W), st);
         if (e != hipSuccess) return fail("gemv launch failed", hipGetErrorString(e));
         return 0;
     }
@@ -336,7 +343,9 @@ int aed_check(const mynah_asr_hip_aed *a, int T) {
 int gemv_epi(const mynah_asr_hip_weight *W, const float *x, float *y, int act, const float *bias, const float *res,
              hipStream_t st) {
     const int vec = (W->dw.k % 8 == 0) && (((uintptr_t)x & 15) == 0);
-    hipError_t e = mh_launch_gemv_epi(W->qtype, W->dw, x, 1, vec, y, GEpi{act, bias, res}, st);
+    Ctx *c = ctx();
+    hipError_t e = mh_launch_gemv_epi(W->qtype, W->dw, x, 1, vec, y, GEpi{act, bias, res},
+                                      c ? gemv_ws(c, W) : nullptr, st);
     return e == hipSuccess ? 0 : fail("gemv launch failed", hipGetErrorString(e));
 }
 
@@ -360,7 +369,12 @@ int aed_gemv(const mynah_asr_hip_weight *const *Ws, float *const *ys, const GEpi
     }
     J.n = n;
     const int vec = x && (Ws[0]->dw.k % 8 == 0) && (((uintptr_t)x & 15) == 0);
-    hipError_t e = mh_launch_gemv_jobs(Ws[0]->qtype, J, x, 1, vec, pro, st);
+    Ctx *c = ctx();
+    // one product of a plain input may split K (ff2); the workspace is sized by
+    // the eager first step, before the step is captured
+    float *ws = n == 1 && pro.kind == GPRO_NONE && c ? gemv_ws(c, Ws[0]) : nullptr;
+    hipError_t e = ws ? mh_launch_gemv_epi(Ws[0]->qtype, J.W[0], x, 1, vec, J.y[0], J.ep[0], ws, st)
+                      : mh_launch_gemv_jobs(Ws[0]->qtype, J, x, 1, vec, pro, st);
     return e == hipSuccess ? 0 : fail("gemv launch failed", hipGetErrorString(e));
 }
 

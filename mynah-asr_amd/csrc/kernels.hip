@@ -692,6 +692,27 @@ __device__ void gemv_prologue(const GPro &pro, int K, int Kp, float *xs) {
     }
 }
 
+// y = act(W x + b) + res for output column n and the lane's 8 rows, in the
+// order of the reference's mv() and its callers (decoder_aed.c:15-19, 207-210)
+template <int QT>
+__device__ __forceinline__ void gemv_store(const DevW &W, int n, int M, int hh, const float (&total)[8],
+                                           const GEpi &ep, float *y) {
+    if (n >= W.n) return;
+    const int shw = wshift<QT>(W, n);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const int m = drow(e, hh);
+        if (m >= M) continue;
+        float v = total[e];
+        if constexpr (QT == QT_F32) v = ldexpf(v, -shw);
+        if (ep.bias) v = v + ep.bias[n];
+        if (ep.act == 1) v = silu_f(v);
+        else if (ep.act == 2) v = v < 0.0f ? 0.0f : v;
+        if (ep.res) v = ep.res[(size_t)m * W.n + n] + v;
+        y[(size_t)m * W.n + n] = v;
+    }
+}
+
 // the GEMV of workgroup bx of one product (shared by k_gemv and k_gemv_jobs)
 template <int QT, int NW, int WNG, bool VEC, bool PRO>
 __device__ __forceinline__ void gemv_body(const DevW &W, const float *__restrict__ x, int M, float *y,
@@ -769,24 +790,87 @@ __device__ __forceinline__ void gemv_body(const DevW &W, const float *__restrict
 #pragma unroll
             for (int e = 0; e < 8; e++)
                 total[e] = __builtin_fmaf(pf[c * 16 + drow(e, hh)], part[((c * WNG + j) * 8 + e) * 64 + lane], total[e]);
-        const int n = 32 * gn[j] + col;
-        if (n >= W.n) continue;
-        const int shw = wshift<QT>(W, n);
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const int m = drow(e, hh);
-            if (m >= M) continue;
-            float v = total[e];
-            if constexpr (QT == QT_F32) v = ldexpf(v, -shw);
-            // y = act(W x + b) + res, in the order of the reference's mv() and
-            // its callers (decoder_aed.c:15-19, 207-210)
-            if (ep.bias) v = v + ep.bias[n];
-            if (ep.act == 1) v = silu_f(v);
-            else if (ep.act == 2) v = v < 0.0f ? 0.0f : v;
-            if (ep.res) v = ep.res[(size_t)m * W.n + n] + v;
-            y[(size_t)m * W.n + n] = v;
-        }
+        gemv_store<QT>(W, 32 * gn[j] + col, M, hh, total, ep, y);
     }
+}
+
+// Split-K GEMV for long K over few column groups (K >= 2048, N <= 2048: 32
+// to 64 workgroups would each run many chunks in turn, one memory latency per
+// chunk). Part 1: workgroup (column group bx, split ks) runs chunks
+// ks*NW .. ks*NW+NW-1, one per wave, and writes each chunk's result rows
+// (the values gemv_body keeps in LDS) to part[bx][c][8][64] and the fold
+// factors to pfg[c][16]. Part 2 (k_gemv_fold) folds them in chunk order from
+// zero: the same operations, so the rows are bit-identical to gemv_body's.
+template <int QT, int NW, bool VEC>
+__global__ __launch_bounds__(NW * 64) void k_gemv_part(DevW W, const float *__restrict__ x, int M,
+                                                       float *__restrict__ part, float *__restrict__ pfg) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int hh = lane >> 5, col = lane & 31;
+    const int Kc = W.Kp / 128, c = blockIdx.y * NW + wave, bx = blockIdx.x;
+    if (c >= Kc) return;   // (no barrier follows)
+    const int gn[1] = {bx};
+    BH<QT, 1> hd;
+    BK<QT, 1> bk[KSTEPS];
+    load_bh<QT, 1>(W, Kc, gn, c, lane, hd);
+#pragma unroll
+    for (int s = 0; s < KSTEPS; s++) load_bk<QT, 1>(W, Kc, gn, c, s, lane, bk[s]);
+    __builtin_amdgcn_sched_barrier(0);
+    XChunk xc;
+    split_chunk<VEC>(x, M, W.k, col, c, hh, xc);
+    if (bx == 0 && hh == 0 && col < 16) pfg[c * 16 + col] = xc.p;
+    f16v acc[1][1];
+    acc[0][0] = zero16();
+#pragma unroll
+    for (int s = 0; s < KSTEPS; s++) {
+        AK<1> a;
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++) {
+            a.h[0][kh] = xc.h[2 * s + kh];
+            a.l[0][kh] = xc.l[2 * s + kh];
+        }
+        kstep<QT, 1, 1>(a, bk[s], hd, s, acc);
+    }
+    if constexpr (fold_fmt<QT>()) {
+        half8 xmv = {};
+        if constexpr (Fmt<QT>::MINS) xmv = xm_frag<Fmt<QT>::SUB16 ? 8 : 4>(xc.s8, hh);
+        fold_finish<QT>(xmv, hd.h[0], acc[0][0]);
+    }
+    float *o = part + ((size_t)bx * Kc + c) * 8 * 64;
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e * 64 + lane] = acc[0][0][e];
+}
+
+template <int QT>
+__global__ __launch_bounds__(64) void k_gemv_fold(DevW W, const float *__restrict__ part,
+                                                  const float *__restrict__ pfg, int M, float *y, GEpi ep) {
+    const int lane = threadIdx.x, hh = lane >> 5, col = lane & 31, bx = blockIdx.x;
+    const int Kc = W.Kp / 128;
+    const float *pp = part + (size_t)bx * Kc * 8 * 64;
+    float total[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) total[e] = 0.0f;
+    // Kc is a multiple of 2 (Kp of 256): eight chunks' loads at a time go out
+    // ahead of the (sequential) fma chain
+    int c = 0;
+    for (; c + 8 <= Kc; c += 8) {
+        float pv[8][8], fv[8][8];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                pv[u][e] = pp[((size_t)(c + u) * 8 + e) * 64 + lane];
+                fv[u][e] = pfg[(c + u) * 16 + drow(e, hh)];
+            }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) total[e] = __builtin_fmaf(fv[u][e], pv[u][e], total[e]);
+    }
+    for (; c < Kc; c++)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            total[e] = __builtin_fmaf(pfg[c * 16 + drow(e, hh)], pp[((size_t)c * 8 + e) * 64 + lane], total[e]);
+    gemv_store<QT>(W, 32 * bx + col, M, hh, total, ep, y);
 }
 
 // one product: the compact argument block of the encoder and decoder GEMVs
@@ -1158,8 +1242,34 @@ hipError_t mh_launch_gemv_jobs(int qtype, const GJobs &J, const float *x, int M,
     MH_DISPATCH(gemv_t, qtype, J, x, M, vec, pro, st)
 }
 
+// the split-K GEMV: K >= 2048 over at most 64 column groups (N <= 2048)
+static bool gemv_split(const DevW &W) { return W.Kp / 128 >= 16 && W.Np / 32 <= 64; }
+
+size_t mh_gemv_ws_floats(const DevW &W) {
+    const size_t Kc = W.Kp / 128;
+    return gemv_split(W) ? (size_t)(W.Np / 32) * Kc * 512 + Kc * 16 : 0;
+}
+
+template <int QT>
+static hipError_t gemv_split_t(const DevW &W, const float *x, int M, int vec, float *y, GEpi ep, float *ws,
+                               hipStream_t st) {
+    constexpr int NW = 4;
+    const int Kc = W.Kp / 128, G = W.Np / 32;
+    float *part = ws, *pfg = ws + (size_t)G * Kc * 512;
+    const dim3 grid(G, (Kc + NW - 1) / NW);
+    if (vec)
+        hipLaunchKernelGGL((k_gemv_part<QT, NW, true>), grid, dim3(NW * 64), 0, st, W, x, M, part, pfg);
+    else
+        hipLaunchKernelGGL((k_gemv_part<QT, NW, false>), grid, dim3(NW * 64), 0, st, W, x, M, part, pfg);
+    hipLaunchKernelGGL((k_gemv_fold<QT>), dim3(G), dim3(64), 0, st, W, part, pfg, M, y, ep);
+    return hipGetLastError();
+}
+
 hipError_t mh_launch_gemv_epi(int qtype, const DevW &W, const float *x, int M, int vec, float *y, GEpi ep,
-                              hipStream_t st) {
+                              float *ws, hipStream_t st) {
+    if (ws && gemv_split(W)) {
+        MH_DISPATCH(gemv_split_t, qtype, W, x, M, vec, y, ep, ws, st)
+    }
     GJobs J{};
     J.W[0] = J.W[1] = J.W[2] = W;
     J.y[0] = y;
@@ -1169,8 +1279,8 @@ hipError_t mh_launch_gemv_epi(int qtype, const DevW &W, const float *x, int M, i
 }
 
 hipError_t mh_launch_gemv(int qtype, const DevW &W, const float *x, int M, int vec, float *y, int act,
-                          hipStream_t st) {
-    return mh_launch_gemv_epi(qtype, W, x, M, vec, y, GEpi{act, nullptr, nullptr}, st);
+                          float *ws, hipStream_t st) {
+    return mh_launch_gemv_epi(qtype, W, x, M, vec, y, GEpi{act, nullptr, nullptr}, ws, st);
 }
 
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,

@@ -17,8 +17,14 @@ hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_
                           float *xpf, int want_xsum, int vec, hipStream_t st);
 // M <= 16 (and K small enough for the LDS partials): the preparation-free GEMV
 bool mh_use_gemv(const DevW &W, int M);
+// Floats of device workspace that let a GEMV of W split K over workgroups (0:
+// it never does). The launchers below take such a workspace (or null) in `ws`;
+// with it, K >= 2048 over N <= 2048 runs as two launches (chunk results, then
+// their fold in chunk order: the same bits as without). Calls sharing one
+// workspace must be ordered on one stream.
+size_t mh_gemv_ws_floats(const DevW &W);
 hipError_t mh_launch_gemv(int qtype, const DevW &W, const float *x, int M, int vec, float *y, int act,
-                          hipStream_t st);
+                          float *ws, hipStream_t st);
 // GEMV epilogue: y = act(W x + bias) + res; act 0 none, 1 SiLU, 2 ReLU; bias [n]
 // and res [M, n] may be null; res may alias y
 struct GEpi {
@@ -27,7 +33,7 @@ struct GEpi {
     const float *res;
 };
 hipError_t mh_launch_gemv_epi(int qtype, const DevW &W, const float *x, int M, int vec, float *y, GEpi ep,
-                              hipStream_t st);
+                              float *ws, hipStream_t st);
 // The input row of a one-row GEMV built per workgroup: GPRO_LN = the layer norm
 // of x (w, b); GPRO_COMB = the attention splits merged (opart [H][nsplit][dk],
 // ml [H][nsplit][2], n keys = n_fixed, or st[0] + 1 when n_fixed == 0).

@@ -86,6 +86,7 @@ CASES = [
     (256, 2, 512, 1000, 2, 37, M.F32, None),     # head size 128
     (256, 4, 512, 1000, 2, 70, M.Q8_0, 128),     # head size 64, encoder projection
     (512, 4, 1024, 2048, 3, 130, M.Q4_K, None),  # K-quant linears, 3 splits of cross keys
+    (256, 2, 2048, 500, 1, 20, M.Q8_0, None),    # ff2 with K = 2048: the split-K GEMV
 ]
 
 
