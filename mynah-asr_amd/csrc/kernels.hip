@@ -846,30 +846,53 @@ __global__ __launch_bounds__(64) void k_gemv_fold(DevW W, const float *__restric
     const int lane = threadIdx.x, hh = lane >> 5, col = lane & 31, bx = blockIdx.x;
     const int Kc = W.Kp / 128;
     const float *pp = part + (size_t)bx * Kc * 8 * 64;
+    // The fma chain of each row runs in chunk order from zero; what varies is
+    // how far its loads go out ahead of it.
     float total[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) total[e] = 0.0f;
-    // Kc is a multiple of 2 (Kp of 256): eight chunks' loads at a time go out
-    // ahead of the (sequential) fma chain
-    int c = 0;
-    for (; c + 8 <= Kc; c += 8) {
-        float pv[8][8], fv[8][8];
+    if (M <= 2) {
+        // one or two live rows (on the lanes of half 0): a row at a time, 32
+        // chunks' loads together
 #pragma unroll
-        for (int u = 0; u < 8; u++)
+        for (int e = 0; e < 2; e++) {
+            const int row = drow(e, hh);
+            if (row >= M) continue;
+            for (int c0 = 0; c0 < Kc; c0 += 32) {
+                float pv[32], fv[32];
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                pv[u][e] = pp[((size_t)(c + u) * 8 + e) * 64 + lane];
-                fv[u][e] = pfg[(c + u) * 16 + drow(e, hh)];
+                for (int u = 0; u < 32; u++)
+                    if (c0 + u < Kc) {
+                        pv[u] = pp[((size_t)(c0 + u) * 8 + e) * 64 + lane];
+                        fv[u] = pfg[(c0 + u) * 16 + row];
+                    }
+#pragma unroll
+                for (int u = 0; u < 32; u++)
+                    if (c0 + u < Kc) total[e] = __builtin_fmaf(fv[u], pv[u], total[e]);
             }
+        }
+    } else {
+        // all rows, eight chunks' loads at a time (Kc is even: Kp of 256)
+        int c = 0;
+        for (; c + 8 <= Kc; c += 8) {
+            float pv[8][8], fv[8][8];
 #pragma unroll
-        for (int u = 0; u < 8; u++)
+            for (int u = 0; u < 8; u++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) total[e] = __builtin_fmaf(fv[u][e], pv[u][e], total[e]);
+                for (int e = 0; e < 8; e++) {
+                    pv[u][e] = pp[((size_t)(c + u) * 8 + e) * 64 + lane];
+                    fv[u][e] = pfg[(c + u) * 16 + drow(e, hh)];
+                }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) total[e] = __builtin_fmaf(fv[u][e], pv[u][e], total[e]);
+        }
+        for (; c < Kc; c++)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                total[e] = __builtin_fmaf(pfg[c * 16 + drow(e, hh)], pp[((size_t)c * 8 + e) * 64 + lane], total[e]);
     }
-    for (; c < Kc; c++)
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-            total[e] = __builtin_fmaf(pfg[c * 16 + drow(e, hh)], pp[((size_t)c * 8 + e) * 64 + lane], total[e]);
     gemv_store<QT>(W, 32 * bx + col, M, hh, total, ep, y);
 }
 
