@@ -396,11 +396,13 @@ int aed_one(const mynah_asr_hip_weight *W, float *y, GEpi ep, const GPro &pro, h
     return aed_gemv(&W, &y, &ep, 1, pro, nullptr, st);
 }
 
+// One position. Its input row x is formed by the previous step's argmax
+// kernel, so only the first step (first = true) embeds its own.
 int aed_step(const mynah_asr_hip_aed *a, const AedBufs &b, int T, int max_len, int n_prompt, float *logits_out,
-             hipStream_t st) {
+             bool first, hipStream_t st) {
     const int d = a->d, H = a->n_heads;
     const size_t td = (size_t)T * d, md = (size_t)max_len * d;
-    AED_TRY(mh_launch_embed_ln(a->emb, a->pos, b.prompt, n_prompt, b.st, a->embln_w, a->embln_b, b.x, d, st));
+    if (first) AED_TRY(mh_launch_embed_ln(a->emb, a->pos, b.prompt, n_prompt, b.st, a->embln_w, a->embln_b, b.x, d, st));
     for (int li = 0; li < a->n_layers; li++) {
         const mynah_asr_hip_aed_layer *L = &a->layers[li];
         float *SK = b.skv + 2 * (size_t)li * md, *SV = SK + md;
@@ -430,7 +432,8 @@ int aed_step(const mynah_asr_hip_aed *a, const AedBufs &b, int T, int max_len, i
             return -1;
     }
     if (aed_one(a->head, b.logits, GEpi{0, a->head_b, nullptr}, pro_ln(b.x, a->fin_w, a->fin_b), st)) return -1;
-    AED_TRY(mh_launch_argmax(b.logits, a->vocab, b.st, logits_out, st));
+    const MhEmbNext en{a->emb, a->pos, b.prompt, n_prompt, max_len, a->embln_w, a->embln_b, b.x, d};
+    AED_TRY(mh_launch_argmax(b.logits, a->vocab, b.st, logits_out, &en, st));
     return 0;
 }
 
@@ -484,12 +487,12 @@ int aed_run(Ctx *c, const mynah_asr_hip_aed *a, const float *enc, int T, const i
     int n_out = 0, rc = 0;
     for (int p = 0; p < max_len; p++) {
         if (p == 0) {
-            if (aed_step(a, b, T, max_len, n_prompt, logits_out, st)) return -1;
+            if (aed_step(a, b, T, max_len, n_prompt, logits_out, true, st)) return -1;
         } else {
             if (!exec) {
                 if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess)
                     return fail("stream capture failed");
-                const int r = aed_step(a, b, T, max_len, n_prompt, logits_out, st);
+                const int r = aed_step(a, b, T, max_len, n_prompt, logits_out, false, st);
                 hipError_t e = hipStreamEndCapture(st, &graph);
                 if (r || e != hipSuccess) {
                     if (graph) (void)hipGraphDestroy(graph);

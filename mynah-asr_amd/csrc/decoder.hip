@@ -8,8 +8,9 @@
 //                k and v rows into the self-attention cache  decoder_aed.c:124-137, 195-198
 //   k_att_combine the splits of each head merged (the decoder step merges them
 //                instead in the prologue of the GEMV that reads the result)
-//   k_argmax     first maximum of the logits, the next token; advances p
-//                                                              decoder_aed.c:217-222
+//   k_argmax     first maximum of the logits, the next token; advances p and
+//                forms the next position's x as k_embed_ln would (so only
+//                the first position launches k_embed_ln)   decoder_aed.c:217-222
 //   k_bias_rows  y[t] += b                                    decoder_aed.c:132-136
 //
 // The step's position p and its token live in device memory (`st`: st[0] = p,
@@ -28,7 +29,9 @@ constexpr int LN_T = 256;   // threads of the one-workgroup row kernels
 constexpr int LN_V = 16;    // values per thread: d <= 4096
 constexpr int KC = MH_ATT_KC;   // keys per attention split
 
-// Sum over the workgroup in double (the reference's ln accumulates in double).
+// Sum over the NT threads of the workgroup in double (the reference's ln
+// accumulates in double).
+template <int NT>
 __device__ double block_sum(double v, double *red) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -36,32 +39,33 @@ __device__ double block_sum(double v, double *red) {
     if (lane == 0) red[w] = v;
     __syncthreads();
     double s = 0.0;
-    for (int i = 0; i < LN_T / 64; i++) s += red[i];
+    for (int i = 0; i < NT / 64; i++) s += red[i];
     return s;
 }
 
-// y = LN(v) over d values held LN_V per thread (i = tid + LN_T * u):
+// y = LN(v) over d values held V per thread (i = tid + NT * u):
 // (float)((x - mean) * inv) * w + b with inv = (float)(1 / sqrt(var + 1e-5))
-__device__ void ln_store(float (&v)[LN_V], int d, const float *w, const float *b, float *y) {
-    __shared__ double red[LN_T / 64];
+template <int NT, int V>
+__device__ void ln_store(float (&v)[V], int d, const float *w, const float *b, float *y) {
+    __shared__ double red[NT / 64];
     const int tid = threadIdx.x;
     double s = 0.0;
 #pragma unroll
-    for (int u = 0; u < LN_V; u++)
-        if (tid + LN_T * u < d) s += (double)v[u];
-    const double mu = block_sum(s, red) / d;
+    for (int u = 0; u < V; u++)
+        if (tid + NT * u < d) s += (double)v[u];
+    const double mu = block_sum<NT>(s, red) / d;
     double q = 0.0;
 #pragma unroll
-    for (int u = 0; u < LN_V; u++)
-        if (tid + LN_T * u < d) {
+    for (int u = 0; u < V; u++)
+        if (tid + NT * u < d) {
             const double c = (double)v[u] - mu;
             q += c * c;
         }
-    const double var = block_sum(q, red) / d;
+    const double var = block_sum<NT>(q, red) / d;
     const float inv = (float)(1.0 / sqrt(var + 1e-5));
 #pragma unroll
-    for (int u = 0; u < LN_V; u++) {
-        const int i = tid + LN_T * u;
+    for (int u = 0; u < V; u++) {
+        const int i = tid + NT * u;
         if (i < d) {
             const float t = (float)(((double)v[u] - mu) * (double)inv);
             y[i] = t * w[i] + b[i];
@@ -82,7 +86,7 @@ __global__ __launch_bounds__(LN_T) void k_embed_ln(const float *__restrict__ emb
         const int i = threadIdx.x + LN_T * u;
         v[u] = i < d ? e[i] + pe[i] : 0.0f;
     }
-    ln_store(v, d, w, b, x);
+    ln_store<LN_T, LN_V>(v, d, w, b, x);
 }
 
 // Workgroup (head h, split s) over keys [s*KC, min((s+1)*KC, n)), n = n_fixed,
@@ -205,9 +209,10 @@ __global__ __launch_bounds__(DK) void k_att_combine(const float *__restrict__ o_
 // First maximum of logits[0..vocab) (the reference's strict > scan) -> st[1];
 // optionally the logits to logits_out[p]; then p + 1 -> st[0].
 __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logits, int vocab, int *st,
-                                                 float *__restrict__ logits_out) {
+                                                 float *__restrict__ logits_out, MhEmbNext en) {
     __shared__ float bv[16];
     __shared__ int bi[16];
+    __shared__ int nxt;
     const int tid = threadIdx.x, p = st[0];
     float best = -INFINITY;
     int idx = 0x7fffffff;
@@ -228,7 +233,21 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logit
             if (bv[w] > best || (bv[w] == best && bi[w] < idx)) best = bv[w], idx = bi[w];
         st[1] = idx == 0x7fffffff ? 0 : idx;
         st[0] = p + 1;
+        nxt = st[1];
     }
+    // the next position's input row, as k_embed_ln would form it
+    const int q = p + 1;
+    if (!en.emb || q >= en.max_pos) return;   // (uniform)
+    __syncthreads();
+    const int tok = q < en.n_prompt ? en.prompt[q] : nxt;
+    const float *e = en.emb + (size_t)tok * en.d, *pe = en.pos + (size_t)q * en.d;
+    float v[4];   // d <= 4096
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int i = tid + 1024 * u;
+        v[u] = i < en.d ? e[i] + pe[i] : 0.0f;
+    }
+    ln_store<1024, 4>(v, en.d, en.w, en.b, en.x);
 }
 
 __global__ void k_bias_rows(float *__restrict__ y, const float *__restrict__ b, size_t rows, int d) {
@@ -273,8 +292,10 @@ hipError_t mh_launch_attend1(const float *q, float *K, float *V, const float *kn
     return hipGetLastError();
 }
 
-hipError_t mh_launch_argmax(const float *logits, int vocab, int *st, float *logits_out, hipStream_t s) {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, logits, vocab, st, logits_out);
+hipError_t mh_launch_argmax(const float *logits, int vocab, int *st, float *logits_out, const MhEmbNext *en,
+                            hipStream_t s) {
+    if (en && en->emb && en->d > 4096) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, logits, vocab, st, logits_out, en ? *en : MhEmbNext{});
     return hipGetLastError();
 }
 

@@ -91,6 +91,20 @@ hipError_t mh_launch_embed_ln(const float *emb, const float *pos, const int *pro
 hipError_t mh_launch_attend1(const float *q, float *K, float *V, const float *kn, const float *vn, const int *st,
                              int n_fixed, int d, int H, float *o_part, float *ml_part, int nsplit, float *out,
                              hipStream_t s);
-hipError_t mh_launch_argmax(const float *logits, int vocab, int *st, float *logits_out, hipStream_t s);
+// The next position's input row, formed by the argmax kernel once it has the
+// token: x = LN(emb[tok] + pos[q]) for q = p + 1 < max_pos, tok = prompt[q]
+// while q < n_prompt, else the argmax (d <= 4096)
+struct MhEmbNext {
+    const float *emb, *pos;
+    const int *prompt;
+    int n_prompt, max_pos;
+    const float *w, *b;
+    float *x;
+    int d;
+};
+// first maximum of the logits into st[1], st[0] advanced; logits_out (if not
+// null) receives row p of the logits; en (if not null) as above
+hipError_t mh_launch_argmax(const float *logits, int vocab, int *st, float *logits_out, const MhEmbNext *en,
+                            hipStream_t s);
 hipError_t mh_launch_bias_rows(float *y, const float *b, size_t rows, int d, hipStream_t s);
 hipError_t mh_launch_set_state(int *st, int p, int cur, hipStream_t s);
