@@ -202,6 +202,38 @@ __device__ __forceinline__ half8 dec_nib(uint32_t w, _Float16 bias) {
     return pack_pairs(p.lo0 + nb, __builtin_elementwise_fma(p.hi0, r16, nb16), p.lo1 + nb,
                       __builtin_elementwise_fma(p.hi1, r16, nb16));
 }
+// Nibble pairs with extra high bits: pairs 0 and 2 (low nibbles) take them at
+// bit 4 (value 1024 + q), pairs 1 and 3 (high nibbles, in place) at bit 8
+// (value 1024 + 16 q). hm[t] = MAGIC | pair t's extra bits at that place.
+__device__ __forceinline__ NibPairs nib_pairs_hi(uint32_t w, const uint32_t (&hm)[4]) {
+    const uint32_t w8 = w >> 8;
+    return {__builtin_bit_cast(half2v, and_or(w, 0x000F000Fu, hm[0])),
+            __builtin_bit_cast(half2v, and_or(w, 0x00F000F0u, hm[1])),
+            __builtin_bit_cast(half2v, and_or(w8, 0x000F000Fu, hm[2])),
+            __builtin_bit_cast(half2v, and_or(w8, 0x00F000F0u, hm[3]))};
+}
+// x << sh for sh >= 0, else x >> -sh (constant after unrolling)
+__device__ __forceinline__ uint32_t shift_by(uint32_t x, int sh) { return sh >= 0 ? x << sh : x >> -sh; }
+// hm for extra bits of width NB (1: a bit plane, 2: a crumb plane) whose pair
+// t sits at bit pos(t) (+16) of h: moved to bit 4 (t even) or 8 (t odd)
+template <int NB>
+__device__ __forceinline__ void extra_bits(uint32_t h, int pos0, int step, uint32_t (&hm)[4]) {
+    constexpr uint32_t m = NB == 1 ? 0x00010001u : 0x00030003u;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int to = (t & 1) ? 8 : 4;
+        hm[t] = and_or(shift_by(h, to - (pos0 + step * t)), m << to, MAGIC);
+    }
+}
+// q * f from such pairs (the factor form of dec_nib_f)
+__device__ __forceinline__ half8 nibs_f(const NibPairs &p, half2v f) {
+    const half2v nb = f * (half2v){(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const half2v f16th = f * (half2v){(_Float16)0.0625f, (_Float16)0.0625f};
+    const half2v nb16 = f * (half2v){(_Float16)-64.0f, (_Float16)-64.0f};
+    return pack_pairs(__builtin_elementwise_fma(p.lo0, f, nb), __builtin_elementwise_fma(p.hi0, f16th, nb16),
+                      __builtin_elementwise_fma(p.lo1, f, nb), __builtin_elementwise_fma(p.hi1, f16th, nb16));
+}
+
 // q * f for an integer factor f: v*f - 1024 f, and (1024 + 16 q) * (f/16) - 64 f
 // (every constant and the exact results are f16 integers or 2^-4 multiples)
 __device__ __forceinline__ half8 dec_nib_f(uint32_t w, half2v f) {
@@ -497,12 +529,10 @@ template <> struct Fmt<QT_Q5_K> {
         k4fhdr_from(hb + (lane & 31) * 16, c, H);
     }
     static __device__ __forceinline__ half8 decode_f(const RawK &R, int s, int kh, const FHdr &H) {
-        const int u = 2 * s + kh;
-        const uint32_t w = R.w[kh], h = R.hb[0];
-        uint32_t p[4];
-#pragma unroll
-        for (int t = 0; t < 4; t++) p[t] = nib_pair(w, t) | (bit_pair(h, u, t) << 4) | MAGIC;
-        return pairs_to_half8_f(p[0], p[1], p[2], p[3], H.sf[s]);
+        // the 5th bit of pair t of half-step u is bit 4 (u & 3) + t of hb
+        uint32_t hm[4];
+        extra_bits<1>(R.hb[0], 4 * ((2 * s + kh) & 3), 1, hm);
+        return nibs_f(nib_pairs_hi(R.w[kh], hm), H.sf[s]);
     }
 };
 
@@ -550,6 +580,17 @@ template <> struct Fmt<QT_Q6_K> {
 #pragma unroll
         for (int t = 0; t < 4; t++) p[t] = nib_pair(w, t) | (crumb_pair(h, u, t) << 4) | MAGIC;
         return pairs_to_half8(p[0], p[1], p[2], p[3], (_Float16)1056.0f);
+    }
+    // the same values: the crumbs (bits 8 (u & 1) + 2t of hi) joined in place,
+    // q - 32 by a packed add (low nibbles) or (1024 + 16 q) / 16 - 96 (high)
+    static __device__ __forceinline__ half8 decode_fast(const RawK &R, int s, int kh) {
+        uint32_t hm[4];
+        extra_bits<2>(R.hi[0], 8 * ((2 * s + kh) & 1), 2, hm);
+        const NibPairs p = nib_pairs_hi(R.w[kh], hm);
+        const half2v nb = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+        const half2v r16 = {(_Float16)0.0625f, (_Float16)0.0625f}, nb16 = {(_Float16)-96.0f, (_Float16)-96.0f};
+        return pack_pairs(p.lo0 + nb, __builtin_elementwise_fma(p.hi0, r16, nb16), p.lo1 + nb,
+                          __builtin_elementwise_fma(p.hi1, r16, nb16));
     }
     static __device__ __forceinline__ void scale(const Hdr &H, int s, int hh, float &sc, float &mn) {
         sc = H.sc[2 * s + hh];

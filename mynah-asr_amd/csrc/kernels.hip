@@ -217,7 +217,14 @@ __device__ __forceinline__ void kstep(const AK<WM> &a, const BK<QT, WN> &b, cons
         static_assert(!F::MINS, "affine formats fold");
 #pragma unroll
         for (int j = 0; j < WN; j++) {
-            const half8 b0 = F::decode(b.r[j], s, 0), b1 = F::decode(b.r[j], s, 1);
+            half8 b0, b1;
+            if constexpr (QT == QT_Q6_K) {   // the same values, fewer instructions
+                b0 = F::decode_fast(b.r[j], s, 0);
+                b1 = F::decode_fast(b.r[j], s, 1);
+            } else {
+                b0 = F::decode(b.r[j], s, 0);
+                b1 = F::decode(b.r[j], s, 1);
+            }
             float sc0, mn0, sc1, mn1;
             F::scale(hd.h[j], s, 0, sc0, mn0);
             F::scale(hd.h[j], s, 1, sc1, mn1);
