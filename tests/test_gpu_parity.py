@@ -160,6 +160,31 @@ def test_rows_bit_identical_across_M(gpu, orc, qt, n, k):
     dw.close()
 
 
+@pytest.mark.parametrize("qt", ALL, ids=lambda q: M.NAMES[q])
+def test_split_k_gemv_rows_match_gemm(gpu, orc, qt):
+    """K = 2048 over N = 96 (4 column groups): M <= 16 runs the split-K GEMV
+    (chunk results, then their fold in chunk order), M = 40 the GEMM. Every
+    format's rows must be the same bits either way, and right."""
+    import torch
+    say("split-K GEMV rows", M.NAMES[qt])
+    n, k = 96, 2048
+    w = M.Weight.make(gpu, qt, gpu.randn(3, 0.02, (n, k)))
+    dw = M.DeviceWeight(gpu, w)
+    x = gpu.randn(4, 1.0, (40, k))
+    xd = torch.from_numpy(x).cuda()
+    outs = {}
+    for T in (40, 16, 3, 1):
+        yd = torch.empty((T, n), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        dw.gemm(xd.data_ptr(), yd.data_ptr(), T)
+        torch.cuda.synchronize()
+        outs[T] = yd.cpu().numpy()
+    for T in (16, 3, 1):
+        assert np.array_equal(outs[T].view(np.uint32), outs[40][:T].view(np.uint32)), T
+    check_close(outs[40], orc.gemm_f64(x, oracle_dequant(orc, w)), f"{M.NAMES[qt]} K=2048")
+    dw.close()
+
+
 # ------------------------------------------------------ fused entry points
 def test_ffn_and_qkv(gpu, orc):
     import ctypes as C
