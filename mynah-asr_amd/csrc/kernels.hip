@@ -699,11 +699,26 @@ __device__ void gemv_prologue(const GPro &pro, int K, int Kp, float *xs) {
     }
 }
 
+// The epilogue operands of a one-row product (the decoder's), loaded when the
+// kernel starts so that their latency is not at its end: bias[n], res[0][n].
+struct EpiPre {
+    float b, r;
+};
+__device__ __forceinline__ EpiPre epi_pre(const DevW &W, int n, int M, int hh, const GEpi &ep) {
+    EpiPre p{0.0f, 0.0f};
+    if (M == 1 && hh == 0 && n < W.n) {
+        if (ep.bias) p.b = ep.bias[n];
+        if (ep.res) p.r = ep.res[n];
+    }
+    return p;
+}
+
 // y = act(W x + b) + res for output column n and the lane's 8 rows, in the
-// order of the reference's mv() and its callers (decoder_aed.c:15-19, 207-210)
+// order of the reference's mv() and its callers (decoder_aed.c:15-19, 207-210);
+// for M = 1, b and res from pre
 template <int QT>
 __device__ __forceinline__ void gemv_store(const DevW &W, int n, int M, int hh, const float (&total)[8],
-                                           const GEpi &ep, float *y) {
+                                           const GEpi &ep, const EpiPre &pre, float *y) {
     if (n >= W.n) return;
     const int shw = wshift<QT>(W, n);
 #pragma unroll
@@ -712,10 +727,10 @@ __device__ __forceinline__ void gemv_store(const DevW &W, int n, int M, int hh, 
         if (m >= M) continue;
         float v = total[e];
         if constexpr (QT == QT_F32) v = ldexpf(v, -shw);
-        if (ep.bias) v = v + ep.bias[n];
+        if (ep.bias) v = v + (M == 1 ? pre.b : ep.bias[n]);
         if (ep.act == 1) v = silu_f(v);
         else if (ep.act == 2) v = v < 0.0f ? 0.0f : v;
-        if (ep.res) v = ep.res[(size_t)m * W.n + n] + v;
+        if (ep.res) v = (M == 1 ? pre.r : ep.res[(size_t)m * W.n + n]) + v;
         y[(size_t)m * W.n + n] = v;
     }
 }
@@ -740,6 +755,8 @@ __device__ __forceinline__ void gemv_body(const DevW &W, const float *__restrict
 #pragma unroll
         for (int s = 0; s < KSTEPS; s++) load_bk<QT, WNG>(W, Kc, gn, c, s, lane, bk[s]);
     };
+    // (the waves w < WNG store column group w)
+    const EpiPre pre = wave < WNG ? epi_pre(W, 32 * (bx * WNG + wave) + col, M, hh, ep) : EpiPre{0.0f, 0.0f};
     if constexpr (PRO) {
         // the first chunk's weight loads go out before the prologue builds the row
         if (wave < Kc) load(wave);
@@ -797,7 +814,7 @@ __device__ __forceinline__ void gemv_body(const DevW &W, const float *__restrict
 #pragma unroll
             for (int e = 0; e < 8; e++)
                 total[e] = __builtin_fmaf(pf[c * 16 + drow(e, hh)], part[((c * WNG + j) * 8 + e) * 64 + lane], total[e]);
-        gemv_store<QT>(W, 32 * gn[j] + col, M, hh, total, ep, y);
+        gemv_store<QT>(W, 32 * gn[j] + col, M, hh, total, ep, pre, y);
     }
 }
 
@@ -852,6 +869,7 @@ __global__ __launch_bounds__(64) void k_gemv_fold(DevW W, const float *__restric
                                                   const float *__restrict__ pfg, int M, float *y, GEpi ep) {
     const int lane = threadIdx.x, hh = lane >> 5, col = lane & 31, bx = blockIdx.x;
     const int Kc = W.Kp / 128;
+    const EpiPre pre = epi_pre(W, 32 * bx + col, M, hh, ep);
     const float *pp = part + (size_t)bx * Kc * 8 * 64;
     // The fma chain of each row runs in chunk order from zero; what varies is
     // how far its loads go out ahead of it.
@@ -900,7 +918,7 @@ __global__ __launch_bounds__(64) void k_gemv_fold(DevW W, const float *__restric
             for (int e = 0; e < 8; e++)
                 total[e] = __builtin_fmaf(pfg[c * 16 + drow(e, hh)], pp[((size_t)c * 8 + e) * 64 + lane], total[e]);
     }
-    gemv_store<QT>(W, 32 * bx + col, M, hh, total, ep, y);
+    gemv_store<QT>(W, 32 * bx + col, M, hh, total, ep, pre, y);
 }
 
 // one product: the compact argument block of the encoder and decoder GEMVs
@@ -1222,7 +1240,7 @@ static hipError_t gemv_t(const GJobs &J, const float *x, int M, int vec, const G
     // than 8 taking four (each chunk's loads wait a full memory latency);
     // within the 128 registers a 1024-thread workgroup allows, except the
     // formats whose GEMV needs more
-    if constexpr (QT != QT_F32 && QT != QT_Q4_K && QT != QT_Q5_K)
+    if constexpr (QT != QT_F32 && QT != QT_Q4_K && QT != QT_Q5_K && QT != QT_Q6_K)
         if (Kc >= 32) return launch_gemv<QT, 16, 1>(J, x, M, vec, pro, st);
     if (Kc >= 8) return launch_gemv<QT, 8, 1>(J, x, M, vec, pro, st);
     return launch_gemv<QT, 4, 1>(J, x, M, vec, pro, st);
