@@ -4,7 +4,8 @@
 // quant bits each lane of a wave feeds into v_mfma_f32_32x32x16_f16 sit at
 // consecutive addresses, so one wave-wide load of 4/8/16 bytes per lane moves a
 // contiguous 256 B/512 B/1 KiB block. Nothing is widened: the planes hold the
-// same bits as the ggml blocks (or the qmat INT8/INT4 arrays), only reordered.
+// same bits as the ggml blocks (or the qmat INT8/INT4 arrays), only reordered
+// (Q8_0's bytes with their top bit flipped: offset binary, q + 128).
 //
 // Geometry shared by every kernel:
 //   column group G = 32 weight rows (the B/N side of one MFMA)
@@ -108,6 +109,15 @@ __device__ __forceinline__ uint32_t bit_pair(uint32_t w, int u, int t) {
 __device__ __forceinline__ half8 dec_bytes(uint32_t w0, uint32_t w1) {
     const uint32_t a = (w0 & 0x00FF00FFu) ^ 0x64806480u, b = (w1 & 0x00FF00FFu) ^ 0x64806480u;
     const uint32_t c = ((w0 >> 8) & 0x00FF00FFu) ^ 0x64806480u, d = ((w1 >> 8) & 0x00FF00FFu) ^ 0x64806480u;
+    return pairs_to_half8(a, b, c, d, (_Float16)1152.0f);
+}
+
+// offset-binary bytes (q + 128) -> half8 of q: each f16 pair 1024 + (q + 128)
+// assembled by one byte permute with the exponent byte 0x64, then -1152
+__device__ __forceinline__ half8 dec_bytes_ob(uint32_t w0, uint32_t w1) {
+    const uint32_t E = 0x64646464u;
+    const uint32_t a = __builtin_amdgcn_perm(E, w0, 0x04020400u), b = __builtin_amdgcn_perm(E, w1, 0x04020400u);
+    const uint32_t c = __builtin_amdgcn_perm(E, w0, 0x04030401u), d = __builtin_amdgcn_perm(E, w1, 0x04030401u);
     return pairs_to_half8(a, b, c, d, (_Float16)1152.0f);
 }
 
@@ -368,7 +378,8 @@ template <> struct Fmt<QT_Q8_0> {
     static __device__ __forceinline__ void k_lds(const uint8_t *r0, const uint8_t *, int s, int lane, RawK &R) {
         lds_kpart<64>(r0, s, lane, R.w);
     }
-    static __device__ __forceinline__ half8 decode(const RawK &R, int, int kh) { return dec_bytes(R.w[2 * kh], R.w[2 * kh + 1]); }
+    // the plane holds q + 128 (offset binary; see repack.cpp)
+    static __device__ __forceinline__ half8 decode(const RawK &R, int, int kh) { return dec_bytes_ob(R.w[2 * kh], R.w[2 * kh + 1]); }
     static __device__ __forceinline__ void scale(const Hdr &H, int s, int, float &sc, float &mn) { blk_scale(H, s, sc, mn); }
 };
 

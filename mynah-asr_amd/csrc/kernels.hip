@@ -1083,19 +1083,35 @@ __global__ __launch_bounds__(256) void k_gemm_i8(DevW W, const uint8_t *__restri
 #pragma unroll
     for (int e = 0; e < 16; e++) zi[e] = 0;
     const i4v minus8 = {(int)0xF8F8F8F8u, (int)0xF8F8F8F8u, (int)0xF8F8F8F8u, (int)0xF8F8F8F8u};
+    // the kstep's plane words, loaded one kstep ahead of their use
+    auto ldw = [&](int ks) -> uint4 {
+        const size_t tile = (size_t)G * Kc + (ks >> 2);
+        const int s = ks & 3;
+        if constexpr (NIB) {
+            const uint2 v = *(const uint2 *)(W.p0 + ((tile * 2 + (s >> 1)) * 64 + lane) * 16 + 8 * (s & 1));
+            return make_uint4(v.x, v.y, 0u, 0u);
+        } else {
+            return *(const uint4 *)(W.p0 + ((tile * 4 + s) * 64 + lane) * 16);
+        }
+    };
+    uint4 nxt = ldw(0);
     for (int ks = 0; ks < S; ks++) {
         const int c = ks >> 2, s = ks & 3;
         const size_t tile = (size_t)G * Kc + c;
+        const uint4 v = nxt;
+        if (ks + 1 < S) nxt = ldw(ks + 1);
         uint32_t b[4];
         if constexpr (NIB) {
-            const uint2 v = *(const uint2 *)(W.p0 + ((tile * 2 + (s >> 1)) * 64 + lane) * 16 + 8 * (s & 1));
             b[0] = v.x & 0x0F0F0F0Fu;
             b[1] = (v.x >> 4) & 0x0F0F0F0Fu;
             b[2] = v.y & 0x0F0F0F0Fu;
             b[3] = (v.y >> 4) & 0x0F0F0F0Fu;
         } else {
-            const uint4 v = *(const uint4 *)(W.p0 + ((tile * 4 + s) * 64 + lane) * 16);
             b[0] = v.x; b[1] = v.y; b[2] = v.z; b[3] = v.w;
+            if constexpr (QT == QT_Q8_0) {   // the plane is offset binary: back to int8
+#pragma unroll
+                for (int i = 0; i < 4; i++) b[i] ^= 0x80808080u;
+            }
         }
         float d = 0.f;
         if constexpr (QT == QT_Q8_0 || QT == QT_Q4_0) {

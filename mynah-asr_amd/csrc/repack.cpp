@@ -178,7 +178,10 @@ int mh_repack(const mynah_asr_hip_wdesc *w, HostLayout *L) {
                             // dword 2u: elements {0,4,1,5}; dword 2u+1: {2,6,3,7}
                             static const int kWord[8] = {0, 0, 1, 1, 0, 0, 1, 1};
                             static const int kByte[8] = {0, 2, 0, 2, 1, 3, 1, 3};
-                            w0[2 * u + kWord[j]] |= (code & 0xffu) << (8 * kByte[j]);
+                            // Q8_0 bytes offset-binary (q + 128): the decoder then
+                            // builds each f16 pair with one byte permute
+                            const uint32_t byte = qt == MYNAH_ASR_HIP_Q8_0 ? (code ^ 0x80u) & 0xffu : code & 0xffu;
+                            w0[2 * u + kWord[j]] |= byte << (8 * kByte[j]);
                         } else if (nib) {
                             w0[u] |= (code & 15u) << (16 * v + 4 * t);
                             if (qt == MYNAH_ASR_HIP_Q5_K)
