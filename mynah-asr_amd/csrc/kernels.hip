@@ -939,22 +939,24 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_jobs(GJobs J, GPro pro) {
 }
 
 // ---------------------------------------------------------------------------
-// Activation preparation for k_gemm: one workgroup (4 waves) per 32-row
-// group; wave w splits chunks c = w, w+4, ... with split_chunk and stores
+// Activation preparation for k_gemm: workgroups of NWP waves per 32-row
+// group (the launch uses one wave per chunk); a wave splits its chunks with
+// split_chunk and stores
 //   xp   A fragments of (xh, xl), zero beyond M and K   [G][chunk][u][term][64][16 B]
 //   xm   the affine folded formats' mins A operand (xm_frag) of 8 (want_xsum
 //        1) or 4 (want_xsum 2) sub-blocks       [G][chunk][64][16 B]
 //   xpf  per row group, chunk and row: the fold factor 2^-sh  [G][chunk][32]
-template <bool VEC>
-__global__ __launch_bounds__(256) void k_prep(const float *__restrict__ x, int M, int K, int Kp,
+template <bool VEC, int NWP>
+__global__ __launch_bounds__(64 * NWP) void k_prep(const float *__restrict__ x, int M, int K, int Kp,
                                               uint8_t *__restrict__ xp, uint8_t *__restrict__ xm,
                                               float *__restrict__ xpf, int want_xsum) {
     const int G = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 31, hh = lane >> 5, m = 32 * G + r;
     const int Kc = Kp / 128;
-    // workgroup (G, y): chunks 4y .. 4y+3, one per wave (enough waves to fill
-    // the chip at encoder sizes: M/32 row groups alone are fewer than the CUs)
-    for (int c = 4 * blockIdx.y + wave; c < Kc; c += 4 * gridDim.y) {
+    // workgroup (G, y): chunks NWP y .. NWP y + NWP-1, one per wave (enough
+    // waves to fill the chip at encoder sizes: M/32 row groups alone are fewer
+    // than the CUs)
+    for (int c = NWP * blockIdx.y + wave; c < Kc; c += NWP * gridDim.y) {
         XChunk xc;
         split_chunk<VEC>(x, M, K, m, c, hh, xc);
 #pragma unroll
@@ -1361,11 +1363,12 @@ hipError_t mh_launch_gemm_prep_out(int qtype, const DevW &W, const uint8_t *xp, 
 
 hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,
                           float *xpf, int want_xsum, int vec, hipStream_t st) {
-    const dim3 grid(Mpad / 32, (Kp / 128 + 3) / 4);
+    constexpr int NWP = 1;
+    const dim3 grid(Mpad / 32, (Kp / 128 + NWP - 1) / NWP);
     if (vec)
-        hipLaunchKernelGGL(k_prep<true>, grid, dim3(256), 0, st, x, M, K, Kp, xp, (uint8_t *)xs16, xpf, want_xsum);
+        hipLaunchKernelGGL((k_prep<true, NWP>), grid, dim3(64 * NWP), 0, st, x, M, K, Kp, xp, (uint8_t *)xs16, xpf, want_xsum);
     else
-        hipLaunchKernelGGL(k_prep<false>, grid, dim3(256), 0, st, x, M, K, Kp, xp, (uint8_t *)xs16, xpf, want_xsum);
+        hipLaunchKernelGGL((k_prep<false, NWP>), grid, dim3(64 * NWP), 0, st, x, M, K, Kp, xp, (uint8_t *)xs16, xpf, want_xsum);
     return hipGetLastError();
 }
 
