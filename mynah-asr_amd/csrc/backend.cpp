@@ -269,6 +269,29 @@ int ffn_dev(Ctx *c, const mynah_asr_hip_weight *W1, const mynah_asr_hip_weight *
 // three products of one input: prepared once whenever it fits them all
 int qkv_dev(Ctx *c, const mynah_asr_hip_weight *const W[3], const float *dx, float *const dy[3], int T,
             hipStream_t st) {
+    // EXACT GEMMs of one format and shape: one preparation, one launch
+    if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT && !mh_use_gemv(W[0]->dw, T) &&
+        W[1]->qtype == W[0]->qtype && W[2]->qtype == W[0]->qtype && W[1]->dw.n == W[0]->dw.n &&
+        W[2]->dw.n == W[0]->dw.n && W[1]->dw.k == W[0]->dw.k && W[2]->dw.k == W[0]->dw.k &&
+        W[1]->dw.Np == W[0]->dw.Np && W[2]->dw.Np == W[0]->dw.Np) {
+        if (prep_for(c, W[0], dx, T, st)) return -1;
+        if (c->pa.i8) {
+            for (int i = 0; i < 3; i++)
+                if (run_prepped(c, W[i], dy[i], T, 0, st)) return -1;
+            return 0;
+        }
+        GemmJobs J{};
+        for (int i = 0; i < 3; i++) {
+            J.W[i] = W[i]->dw;
+            J.y[i] = dy[i];
+        }
+        J.n = 3;
+        const PrepBuf &P = c->pa;
+        hipError_t e = mh_launch_gemm_jobs(W[0]->qtype, J, (const uint8_t *)P.xp.p, (const float *)P.xs16.p,
+                                           (const float *)P.xpf.p, T, st);
+        if (e != hipSuccess) return fail("gemm launch failed", hipGetErrorString(e));
+        return 0;
+    }
     bool prepared = false;
     for (int i = 0; i < 3; i++) {
         if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT && mh_use_gemv(W[i]->dw, T)) {

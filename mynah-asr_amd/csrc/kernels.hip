@@ -408,9 +408,9 @@ struct PrepOut {
 // other's stalls and overlap one's VALU epilogue with another's MFMAs.
 // grid = tilesM * tilesN workgroups.
 template <int QT, int EPI>
-__global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint8_t *__restrict__ xp,
+__global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const uint8_t *__restrict__ xp,
                                                  const uint8_t *__restrict__ xm,
-                                                 const float *__restrict__ xpf, float *__restrict__ y,
+                                                 const float *__restrict__ xpf,
                                                  int M, int act, int tilesM, int tilesN, PrepOut po) {
     using F = Fmt<QT>;
     using L = StageLayout<QT>;
@@ -421,10 +421,16 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(DevW W, const uint
     // tiles in row-band-major order, so that the N tiles of a row band — which
     // all read the same activations, the largest operand — share one L2
     // instead of fetching the band from HBM once per XCD.
-    const int ntiles = tilesM * tilesN, bid = blockIdx.x;
+    // Several products of one input (J.n jobs) share the row bands: the tiles
+    // of band tm are (job, column tile) pairs, so one XCD runs all of a band's
+    // products and reads its activations into its L2 once.
+    const int nj = J.n, ntiles = nj * tilesM * tilesN, bid = blockIdx.x;
     const int q = ntiles / 8, rem = ntiles % 8, xcd = bid % 8, loc = bid / 8;
     const int t = xcd < rem ? xcd * (q + 1) + loc : rem * (q + 1) + (xcd - rem) * q + loc;
-    const int tm = t / tilesN, tn = t % tilesN;
+    const int tm = t / (nj * tilesN), tr = t - tm * nj * tilesN;
+    const int job = tr / tilesN, tn = tr - job * tilesN;
+    const DevW W = job == 0 ? J.W[0] : (job == 1 ? J.W[1] : J.W[2]);
+    float *__restrict__ y = job == 0 ? J.y[0] : (job == 1 ? J.y[1] : J.y[2]);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int hh = lane >> 5, col = lane & 31;
@@ -1265,17 +1271,20 @@ static hipError_t gemv_t(const GJobs &J, const float *x, int M, int vec, const G
 }
 
 template <int QT>
-static hipError_t gemm_t(const DevW &W, const uint8_t *xp, const float *xs16, const float *xpf, float *y,
-                         int M, int act, const PrepOut *po, hipStream_t st) {
+static hipError_t gemm_t(const GemmJobs &J, const uint8_t *xp, const float *xs16, const float *xpf, int M,
+                         int act, const PrepOut *po, hipStream_t st) {
+    const DevW &W = J.W[0];
     const int mpad = mh_mpad(M);
-    if (mpad % 64 != 0 || W.Np % 128 != 0) return hipErrorInvalidValue;
-    const int tilesM = mpad / 64, tilesN = W.Np / 128;
+    if (mpad % 64 != 0 || W.Np % 128 != 0 || J.n < 1 || J.n > 3) return hipErrorInvalidValue;
+    for (int i = 1; i < J.n; i++)
+        if (J.W[i].Np != W.Np || J.W[i].Kp != W.Kp || J.W[i].n != W.n) return hipErrorInvalidValue;
+    const int tilesM = mpad / 64, tilesN = W.Np / 128, grid = J.n * tilesM * tilesN;
     if (po) {
-        if (po->Kc != tilesN) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_gemm<QT, EPI_PREP>), dim3(tilesM * tilesN), dim3(256), 0, st, W, xp, (const uint8_t *)xs16, xpf, y, M,
+        if (po->Kc != tilesN || J.n != 1) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((k_gemm<QT, EPI_PREP>), dim3(grid), dim3(256), 0, st, J, xp, (const uint8_t *)xs16, xpf, M,
                            1, tilesM, tilesN, *po);
     } else {
-        hipLaunchKernelGGL((k_gemm<QT, EPI_Y>), dim3(tilesM * tilesN), dim3(256), 0, st, W, xp, (const uint8_t *)xs16, xpf, y, M,
+        hipLaunchKernelGGL((k_gemm<QT, EPI_Y>), dim3(grid), dim3(256), 0, st, J, xp, (const uint8_t *)xs16, xpf, M,
                            act, tilesM, tilesN, PrepOut{});
     }
     return hipGetLastError();
@@ -1351,14 +1360,26 @@ hipError_t mh_launch_gemv(int qtype, const DevW &W, const float *x, int M, int v
 
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
                           const float *xpf, float *y, int M, int act, hipStream_t st) {
-    MH_DISPATCH(gemm_t, qtype, W, xp, xs16, xpf, y, M, act, nullptr, st)
+    GemmJobs J{};
+    J.W[0] = J.W[1] = J.W[2] = W;
+    J.y[0] = J.y[1] = J.y[2] = y;
+    J.n = 1;
+    MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, act, nullptr, st)
+}
+
+hipError_t mh_launch_gemm_jobs(int qtype, const GemmJobs &J, const uint8_t *xp, const float *xs16,
+                               const float *xpf, int M, hipStream_t st) {
+    MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, 0, nullptr, st)
 }
 
 hipError_t mh_launch_gemm_prep_out(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
                                    const float *xpf, int M, uint8_t *oxp, float *oxs16, float *oxpf, int oKc,
                                    int oxsum, hipStream_t st) {
     const PrepOut po{oxp, (uint8_t *)oxs16, oxpf, oKc, oxsum};
-    MH_DISPATCH(gemm_t, qtype, W, xp, xs16, xpf, nullptr, M, 1, &po, st)
+    GemmJobs J{};
+    J.W[0] = J.W[1] = J.W[2] = W;
+    J.n = 1;
+    MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, 1, &po, st)
 }
 
 hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,

@@ -59,6 +59,14 @@ constexpr int MH_ATT_KC = 64;
 __host__ __device__ inline int mh_att_splits_dev(int n) { return (n + MH_ATT_KC - 1) / MH_ATT_KC; }
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
                           const float *xpf, float *y, int M, int act, hipStream_t st);
+// up to three products (same shape) of one prepared input in one launch
+struct GemmJobs {
+    DevW W[3];
+    float *y[3];
+    int n;
+};
+hipError_t mh_launch_gemm_jobs(int qtype, const GemmJobs &J, const uint8_t *xp, const float *xs16,
+                               const float *xpf, int M, hipStream_t st);
 // The FFN's first product with SiLU, its output prepared as the input of a
 // product with Kp = 128 * oKc (oKc = the first product's column tiles):
 // (oxp, oxs16, oxpf) as mh_launch_prep would write them.

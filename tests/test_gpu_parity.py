@@ -252,6 +252,29 @@ def test_ffn_dev_matches_two_products(gpu, q1, q2, T):
     w2.close()
 
 
+@pytest.mark.parametrize("qt", ALL, ids=lambda q: M.NAMES[q])
+def test_qkv_one_launch_matches_products(gpu, qt):
+    """Three weights of one format and shape run as one GEMM launch over one
+    prepared input; each output is bit-identical to the weight's own product
+    (two row counts: several row bands, and a ragged last band; N = 200 pads)."""
+    import torch
+    say("qkv one launch", M.NAMES[qt])
+    k, n = 512, 200
+    qs = [M.DeviceWeight(gpu, M.Weight.make(gpu, qt, gpu.randn(30 + i, 0.02, (n, k)))) for i in range(3)]
+    for T in (700, 70):
+        x = torch.from_numpy(gpu.randn(T, 1.0, (T, k))).cuda()
+        ys = [torch.full((T, n), float("nan"), dtype=torch.float32, device="cuda") for _ in range(3)]
+        torch.cuda.synchronize()
+        M.qkv_dev(gpu, qs, x.data_ptr(), [y.data_ptr() for y in ys], T)
+        for i, (q, y) in enumerate(zip(qs, ys)):
+            r = torch.empty((T, n), dtype=torch.float32, device="cuda")
+            q.gemm(x.data_ptr(), r.data_ptr(), T)
+            torch.cuda.synchronize()
+            assert torch.equal(y.view(torch.int32), r.view(torch.int32)), f"T={T} output {i}"
+    for q in qs:
+        q.close()
+
+
 class XorShift:
     """The reference self-test's generator (tests/test_qmat.c:13-19)."""
 
