@@ -49,6 +49,13 @@ template <int NT, int V>
 __device__ void ln_store(float (&v)[V], int d, const float *w, const float *b, float *y) {
     __shared__ double red[NT / 64];
     const int tid = threadIdx.x;
+    float lw[V], lb[V];   // loaded before the sums, so their latency overlaps them
+#pragma unroll
+    for (int u = 0; u < V; u++) {
+        const int i = tid + NT * u;
+        lw[u] = i < d ? w[i] : 0.0f;
+        lb[u] = i < d ? b[i] : 0.0f;
+    }
     double s = 0.0;
 #pragma unroll
     for (int u = 0; u < V; u++)
@@ -68,7 +75,7 @@ __device__ void ln_store(float (&v)[V], int d, const float *w, const float *b, f
         const int i = tid + NT * u;
         if (i < d) {
             const float t = (float)(((double)v[u] - mu) * (double)inv);
-            y[i] = t * w[i] + b[i];
+            y[i] = t * lw[u] + lb[u];
         }
     }
 }
@@ -104,7 +111,7 @@ __global__ __launch_bounds__(256) void k_att_part(const float *__restrict__ q, f
     __shared__ float red[256 / DK][DK];
     const int h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
     const int ho = h * DK;
-    const int p = st[0];
+    const int p = n_fixed > 0 ? -1 : st[0];   // (cross attention does not wait for st)
     const int n = n_fixed > 0 ? n_fixed : p + 1;
     const int j0 = s * KC, j1 = min(j0 + KC, n);
     float *op = o_part + ((size_t)h * nsplit + s) * DK;
@@ -131,21 +138,26 @@ __global__ __launch_bounds__(256) void k_att_part(const float *__restrict__ q, f
         vv[t] = 0.0f;
         if (jj < cnt) vv[t] = ((append && j == p) ? vn + ho : V + (size_t)j * d + ho)[f];
     }
-    __syncthreads();
-    // scores: key j0 + (tid >> 2), features (tid & 3) * DK/4 ..
+    // scores: key j0 + (tid >> 2), features (tid & 3) * DK/4 ..; the key row
+    // is loaded before the barrier, with the V values
     {
         const int jj = tid >> 2, part = tid & 3, j = j0 + jj;
-        float acc = 0.0f;
+        float4 kv[DK / 16];
         if (j < j1) {
             const float *kr = (append && j == p) ? kn + ho : K + (size_t)j * d + ho;
 #pragma unroll
-            for (int i = 0; i < DK / 4; i += 4) {
-                const float4 kv = *(const float4 *)(kr + part * (DK / 4) + i);
-                const float *qq = qs + part * (DK / 4) + i;
-                acc = fmaf(qq[0], kv.x, acc);
-                acc = fmaf(qq[1], kv.y, acc);
-                acc = fmaf(qq[2], kv.z, acc);
-                acc = fmaf(qq[3], kv.w, acc);
+            for (int i = 0; i < DK / 16; i++) kv[i] = *(const float4 *)(kr + part * (DK / 4) + 4 * i);
+        }
+        __syncthreads();
+        float acc = 0.0f;
+        if (j < j1) {
+#pragma unroll
+            for (int i = 0; i < DK / 16; i++) {
+                const float *qq = qs + part * (DK / 4) + 4 * i;
+                acc = fmaf(qq[0], kv[i].x, acc);
+                acc = fmaf(qq[1], kv[i].y, acc);
+                acc = fmaf(qq[2], kv[i].z, acc);
+                acc = fmaf(qq[3], kv[i].w, acc);
             }
         }
         acc += __shfl_xor(acc, 1, 64);
@@ -213,13 +225,40 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logit
     __shared__ float bv[16];
     __shared__ int bi[16];
     __shared__ int nxt;
+    constexpr int AV = 16;   // logits per thread per batch: all of them go out at once
     const int tid = threadIdx.x, p = st[0];
+    // the next position's rows that do not depend on this argmax go out first
+    const int q = p + 1;
+    const bool next = en.emb && q < en.max_pos;   // (uniform)
+    float pv[4], ev[4];   // d <= 4096
+    const bool in_prompt = next && q < en.n_prompt;
+    if (next) {
+        const float *pe = en.pos + (size_t)q * en.d;
+        const float *e = in_prompt ? en.emb + (size_t)en.prompt[q] * en.d : nullptr;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = tid + 1024 * u;
+            pv[u] = i < en.d ? pe[i] : 0.0f;
+            ev[u] = in_prompt && i < en.d ? e[i] : 0.0f;
+        }
+    }
     float best = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = tid; i < vocab; i += 1024) {
-        const float v = logits[i];
-        if (v > best) best = v, idx = i;   // i grows: a tie keeps the earlier index
-        if (logits_out) logits_out[(size_t)p * vocab + i] = v;
+    for (int i0 = 0; i0 < vocab; i0 += 1024 * AV) {
+        float v[AV];
+#pragma unroll
+        for (int u = 0; u < AV; u++) {
+            const int i = i0 + tid + 1024 * u;
+            v[u] = i < vocab ? logits[i] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < AV; u++) {
+            const int i = i0 + tid + 1024 * u;
+            if (i < vocab) {
+                if (v[u] > best) best = v[u], idx = i;   // i grows: a tie keeps the earlier index
+                if (logits_out) logits_out[(size_t)p * vocab + i] = v[u];
+            }
+        }
     }
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(best, o, 64);
@@ -236,17 +275,19 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logit
         nxt = st[1];
     }
     // the next position's input row, as k_embed_ln would form it
-    const int q = p + 1;
-    if (!en.emb || q >= en.max_pos) return;   // (uniform)
+    if (!next) return;
     __syncthreads();
-    const int tok = q < en.n_prompt ? en.prompt[q] : nxt;
-    const float *e = en.emb + (size_t)tok * en.d, *pe = en.pos + (size_t)q * en.d;
-    float v[4];   // d <= 4096
+    if (!in_prompt) {
+        const float *e = en.emb + (size_t)nxt * en.d;
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int i = tid + 1024 * u;
-        v[u] = i < en.d ? e[i] + pe[i] : 0.0f;
+        for (int u = 0; u < 4; u++) {
+            const int i = tid + 1024 * u;
+            ev[u] = i < en.d ? e[i] : 0.0f;
+        }
     }
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) v[u] = ev[u] + pv[u];
     ln_store<1024, 4>(v, en.d, en.w, en.b, en.x);
 }
 

@@ -636,11 +636,14 @@ __device__ void gemv_prologue(const GPro &pro, int K, int Kp, float *xs) {
     const int tid = threadIdx.x;
     if (pro.kind == GPRO_LN) {
         // (float)((x - mean) * inv) * w + b, inv = (float)(1 / sqrt(var + 1e-5)): decoder_aed.c:21-28
-        float v[V];
+        // w and b load with x: their latency is not after the two sums
+        float v[V], lw[V], lb[V];
 #pragma unroll
         for (int u = 0; u < V; u++) {
             const int i = tid + NT * u;
             v[u] = i < K ? pro.x[i] : 0.0f;
+            lw[u] = i < K ? pro.w[i] : 0.0f;
+            lb[u] = i < K ? pro.b[i] : 0.0f;
         }
         double s = 0.0;
 #pragma unroll
@@ -660,7 +663,7 @@ __device__ void gemv_prologue(const GPro &pro, int K, int Kp, float *xs) {
             const int i = tid + NT * u;
             if (i < K) {
                 const float t = (float)(((double)v[u] - mu) * (double)inv);
-                xs[i] = t * pro.w[i] + pro.b[i];
+                xs[i] = t * lw[u] + lb[u];
             }
         }
         for (int i = K + tid; i < Kp; i += NT) xs[i] = 0.0f;
@@ -674,15 +677,29 @@ __device__ void gemv_prologue(const GPro &pro, int K, int Kp, float *xs) {
         constexpr int PW = 1024;
         __shared__ float hw[PW];
         const bool pre = pro.H * ns <= PW;
+        // loads go out MB splits at a time (a loop over a run-time count
+        // would wait for each before issuing the next); the sums keep split order
+        constexpr int MB = 8;
         if (tid < pro.H) {
-            const float *ml = pro.ml + (size_t)tid * pro.nsplit * 2;
-            float Mx = -INFINITY;
-            for (int s2 = 0; s2 < ns; s2++) Mx = fmaxf(Mx, ml[2 * s2]);
-            float L = 0.0f;
-            for (int s2 = 0; s2 < ns; s2++) {
-                const float e = expf(ml[2 * s2] - Mx);
-                if (pre) hw[tid * ns + s2] = e;
-                L += ml[2 * s2 + 1] * e;
+            const float2 *ml = (const float2 *)(pro.ml + (size_t)tid * pro.nsplit * 2);
+            float Mx = -INFINITY, L = 0.0f;
+            float2 mlv[MB];
+            for (int s0 = 0; s0 < ns; s0 += MB) {
+#pragma unroll
+                for (int u = 0; u < MB; u++) mlv[u] = s0 + u < ns ? ml[s0 + u] : float2{-INFINITY, 0.0f};
+#pragma unroll
+                for (int u = 0; u < MB; u++) Mx = fmaxf(Mx, mlv[u].x);
+            }
+            for (int s0 = 0; s0 < ns; s0 += MB) {
+#pragma unroll
+                for (int u = 0; u < MB; u++) mlv[u] = s0 + u < ns ? ml[s0 + u] : float2{-INFINITY, 0.0f};
+#pragma unroll
+                for (int u = 0; u < MB; u++)
+                    if (s0 + u < ns) {
+                        const float e = expf(mlv[u].x - Mx);
+                        if (pre) hw[tid * ns + s0 + u] = e;
+                        L += mlv[u].y * e;
+                    }
             }
             hm[tid] = Mx;
             hl[tid] = L;
@@ -693,11 +710,17 @@ __device__ void gemv_prologue(const GPro &pro, int K, int Kp, float *xs) {
             if (i < K) {
                 const int h = i / dk, f = i - h * dk;
                 const float *ml = pro.ml + (size_t)h * pro.nsplit * 2;
+                const float *op = pro.opart + (size_t)h * pro.nsplit * dk + f;
                 const float Mx = hm[h];
                 float o = 0.0f;
-                for (int s2 = 0; s2 < ns; s2++)
-                    o += pro.opart[((size_t)h * pro.nsplit + s2) * dk + f] *
-                         (pre ? hw[h * ns + s2] : expf(ml[2 * s2] - Mx));
+                for (int s0 = 0; s0 < ns; s0 += MB) {
+                    float ov[MB];
+#pragma unroll
+                    for (int u = 0; u < MB; u++) ov[u] = s0 + u < ns ? op[(size_t)(s0 + u) * dk] : 0.0f;
+#pragma unroll
+                    for (int u = 0; u < MB; u++)
+                        if (s0 + u < ns) o += ov[u] * (pre ? hw[h * ns + s0 + u] : expf(ml[2 * (s0 + u)] - Mx));
+                }
                 v = o / hl[h];
             }
             xs[i] = v;
