@@ -100,6 +100,53 @@ def test_gemm_matches_oracle(gpu, orc, qt, T):
     check_close(y, ref, f"{M.NAMES[qt]} T={T}")
 
 
+def _sweep_cases(n_cases=40, seed=2024):
+    """Seeded random shapes: every format, ragged n, several K per format (block
+    multiples for the block formats, any K for F32 / INT8), M on both sides of
+    the GEMV / GEMM boundary, weight scales small and large, and activations
+    with or without outliers (one entry in 64 scaled by 300: a wide range
+    inside each 128-chunk for its shift and split)."""
+    r = np.random.default_rng(seed)
+    ks = {M.F32: [7, 100, 1000], M.INT8: [13, 256, 1100], M.INT4: [32, 224, 1056],
+          M.Q4_0: [32, 96, 544, 2080], M.Q8_0: [32, 96, 544, 2080]}
+    kq = [256, 768, 2304]
+    out = []
+    for i in range(n_cases):
+        qt = ALL[i % len(ALL)]
+        k = int(r.choice(ks.get(qt, kq)))
+        n = int(r.integers(1, 700))
+        T = int(r.choice([1, 2, 5, 16, 17, 31, 64, 129, 777]))
+        out.append((i, qt, n, k, T, float(r.choice([0.02, 3.0])), bool(r.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("i,qt,n,k,T,wsc,outliers", _sweep_cases())
+def test_gemm_shape_sweep(gpu, orc, i, qt, n, k, T, wsc, outliers):
+    say("sweep", i, M.NAMES[qt], "n", n, "k", k, "T", T, "wsc", wsc, "outliers", outliers)
+    w = M.Weight.make(gpu, qt, gpu.randn(100 + i, wsc, (n, k)))
+    x = gpu.randn(200 + i, 1.0, (T, k))
+    if outliers:
+        x[:, ::64] *= 300.0
+    y = M.host_qgemm(gpu, w, x)
+    wd = oracle_dequant(orc, w)
+    ref = orc.gemm_f64(x, wd)
+    # Large weights and outliers make outputs that cancel: there the f32
+    # rounding of the terms, not the result's own size, sets what any f32
+    # product can reach. The reference's product (f32 sgemm over the
+    # dequantized weights) misses 1e-4*|ref| + 1e-6 on such elements too, by up
+    # to 18.5 * 2^-24 * sum_k |x||w| on these cases (measured with numpy's
+    # float32 matmul), and this backend by up to 30.1 (its activations carry 22
+    # bits as an f16 pair). So the bar adds 64 * 2^-24 * sum_k |x||w|.
+    floor = 64 * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(wd).astype(np.float64).T)
+    err = np.abs(y.astype(np.float64) - ref)
+    bound = RTOL * np.abs(ref) + ATOL + floor
+    ratio = float((err / (floor / 64)).max())
+    say(f"  worst err / (2^-24 sum|x||w|) = {ratio:.3g}")
+    bad = err > bound
+    assert not bad.any(), (f"sweep {i} {M.NAMES[qt]} n={n} k={k} T={T}: {int(bad.sum())} outside; "
+                           f"worst ratio {ratio:.3g}")
+
+
 def test_gemm_zero_and_tiny_rows(gpu, orc):
     say("gemm special rows")
     w = M.Weight.make(gpu, M.Q8_0, gpu.randn(0, 0.02, (64, 256)))
