@@ -408,3 +408,75 @@ def test_qmat_api_mirror(gpu, orc):
     H.mynah_asr_qmat_mul(C.byref(m), x.ctypes.data, out.ctypes.data, 48)
     check_close(out, orc.gemm_f64(x, orc.dequant(O.Q4_K, raw, 96 * 1024).reshape(96, 1024)), "blocks")
     H.mynah_asr_qmat_free(C.byref(m))
+
+
+# ------------------------------------------------------------- threading
+def test_concurrent_callers_match_serial(gpu, orc):
+    """The reference calls the qmat entry points from several threads at once
+    (server workers, and segment workers inside parallel_for:
+    src/encoder.c:928,934; the CUDA unit keeps a per-thread stream and buffers,
+    src/cuda_gemm.cu:50-90, and locks only its weight cache, :92-130). Six
+    threads call the host-pointer qgemm and qqkv entry points on shared
+    weights, each first uploaded while the threads contend for it, and on
+    inputs of their own (M = 1, 5, 40, 300). Every result must carry the same
+    bits as the same call made from one thread."""
+    import ctypes as C
+    import threading
+    say("concurrent callers")
+    k = 512
+    ws = [M.Weight.make(gpu, qt, gpu.randn(60 + i, 0.02, (192, k))) for i, qt in
+          enumerate((M.Q8_0, M.Q4_K, M.F32, M.Q6_K))]
+    qkv = [M.Weight.make(gpu, M.Q8_0, gpu.randn(70 + i, 0.02, (128, k))) for i in range(3)]
+    Ts = (1, 5, 40, 300)
+    cases = [(t, j) for t in range(6) for j in range(8)]
+
+    def inputs(t, j):
+        return gpu.randn(1000 + 8 * t + j, 1.0, (Ts[(t + j) % 4], k))
+
+    def run_qkv(x):
+        outs = [np.empty((x.shape[0], 128), np.float32) for _ in range(3)]
+        rc = gpu.L.mynah_asr_hip_qqkv(*[C.byref(w.desc) for w in qkv], x.ctypes.data,
+                                      *[o.ctypes.data for o in outs], x.shape[0])
+        return rc, outs
+
+    # one thread (weights evicted after each call, so the threads upload them again)
+    serial = {}
+    for t, j in cases:
+        x = inputs(t, j)
+        if j % 4 == 3:
+            rc, outs = run_qkv(x)
+            assert rc == 0, gpu.last_error()
+            serial[(t, j)] = outs
+            for w in qkv:
+                M.evict(gpu, w)
+        else:
+            serial[(t, j)] = [M.host_qgemm(gpu, ws[(t + j) % 4], x)]
+
+    got, errors = {}, []
+
+    def worker(t):
+        try:
+            for j in range(8):
+                x = inputs(t, j)
+                if j % 4 == 3:
+                    rc, outs = run_qkv(x)
+                    if rc != 0:
+                        raise RuntimeError(gpu.last_error())
+                    got[(t, j)] = outs
+                else:
+                    got[(t, j)] = [M.host_qgemm(gpu, ws[(t + j) % 4], x, keep=True)]
+        except Exception as e:  # reported by the main thread
+            errors.append(f"thread {t}: {e!r}")
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(6)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=60)
+    assert not any(th.is_alive() for th in threads), "a caller thread did not finish"
+    for w in ws + qkv:
+        M.evict(gpu, w)
+    assert not errors, errors
+    for key in cases:
+        for a, b in zip(got[key], serial[key]):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"case {key} differs"
