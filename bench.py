@@ -465,7 +465,7 @@ def main():
         details["aed_decoder"] = run_aed(B, M_)
         log("[bench] decoder GEMVs")
         gv = []
-        for qt in (M_.Q8_0, M_.Q4_0):
+        for qt in (M_.Q8_0, M_.Q4_0, M_.Q4_K):
             for n, k in [(s[1], s[0]) for s in GEMV_SHAPES]:
                 gv += run_gemv(B, M_, qt, n, k, (1, 4, 16))
         details["gemv"] = gv
