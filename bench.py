@@ -1,12 +1,12 @@
 #!/usr/bin/env python3
-"""bench.py — throughput of the MI355X linear-layer backend on BASELINE's shapes.
+"""bench.py — throughput of the MI355X linear-layer backend on the benchmark's shapes.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 
 A step is one pass over the FastConformer-0.6B encoder linear set at
-M = 8 segments x 750 frames = 6000 rows (BASELINE config 2's shapes:
+M = 8 segments x 750 frames = 6000 rows (benchmark config 2's shapes:
 1024->4096, 4096->1024 and five 1024->1024 for Q, K, V, out, pos), every
-weight Q8_0 (BASELINE's metric), EXACT numerics (the default). Inputs are
+weight Q8_0 (the headline metric), EXACT numerics (the default). Inputs are
 resident in HBM before the timed region; the products go through the
 library's device entry points the way an encoder layer calls them
 (src/encoder.c): the FFN pair through qffn_dev (the first product prepares
@@ -17,11 +17,11 @@ step, in TOPS.
 
 Also reported (not `value`): per-kernel roofline fractions, the same step in
 INT8ACT numerics (int8 activations on the i8 MFMA, against 5.0 POP/s), each of
-Q2_K, Q3_K, Q4_K, Q5_K and Q6_K at BASELINE config 4's M = 12000 shapes, decoder GEMVs (config 3) in HBM GB/s with >= 512
+Q2_K, Q3_K, Q4_K, Q5_K and Q6_K at benchmark config 4's M = 12000 shapes, decoder GEMVs (config 3) in HBM GB/s with >= 512
 MB of rotating weight copies (defeats the 256 MB MALL), timed as one HIP graph
 of all the launches (kernel_us; call_us = the same launches issued one by one
 from the host), the f32-weight GEMM, the relative-position attention core at T = 750
-(16 segments as in BASELINE config 5, d 1024, 8 heads; full and chunked-limited [70, 13] windows;
+(16 segments as in benchmark config 5, d 1024, 8 heads; full and chunked-limited [70, 13] windows;
 useful flops = 6 * dk per visible (row, key) pair, against the 157.3 TFLOP/s
 fp32 MFMA peak), and the reference CPU path timed on this host (ingot dequant, compiled from
 the reference's sources, + OpenBLAS sgemm, as src/weights.c:103-114 +
@@ -303,7 +303,7 @@ def run_attention(B, M_, T=750, d=1024, H=8, nseq=16, reps=10):
 
 
 def run_aed(B, M_, d=1024, H=8, ffn=4096, vocab=16384, n_layers=4, T=750, cap=64, qt=None):
-    """The AED decoder on the device (src/decoder_aed.c:139-232) at BASELINE
+    """The AED decoder on the device (src/decoder_aed.c:139-232) at benchmark
     config 3's shapes: greedy decoding of `cap` tokens after a 4-token prompt
     (a host read-back per token for the EOS check), and the same steps
     teacher-forced (no read-back: the graph replays back to back)."""

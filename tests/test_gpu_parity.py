@@ -166,7 +166,7 @@ def test_gemm_zero_and_tiny_rows(gpu, orc):
 @pytest.mark.parametrize("n,k", [(1024, 4096), (4096, 1024), (16384, 1024)])
 @pytest.mark.parametrize("qt", [M.Q8_0, M.Q4_0], ids=lambda q: M.NAMES[q])
 def test_decoder_gemv_shapes(gpu, orc, qt, n, k):
-    """BASELINE config 3 shapes at M in {1, 4, 16}."""
+    """Benchmark config 3 shapes at M in {1, 4, 16}."""
     say("gemv", M.NAMES[qt], n, k)
     w = M.Weight.make(gpu, qt, gpu.randn(0, 0.02, (n, k)))
     wd = oracle_dequant(orc, w)
