@@ -81,6 +81,7 @@ struct Ctx {
     DBuf att;    // the host-pointer attention call's q, k, v, rk, biases and ctx
     DBuf aed;    // the AED decoder's caches and vectors
     DBuf gs;     // split-K GEMV workspace
+    DBuf gk;     // split-K GEMM workspace (chunk results)
     int *pin = nullptr;   // pinned host int[2]: the step state read back
     PrepBuf pa;  // the products' input (prep_dev / qgemm_prepped_dev use this one)
     PrepBuf pb;  // the FFN's intermediate, prepared by the first product
@@ -201,18 +202,22 @@ bool fits(const PrepBuf &P, const mynah_asr_hip_weight *W, int T) {
 bool prep_fits(const Ctx *c, const mynah_asr_hip_weight *W, int T) { return fits(c->pa, W, T); }
 
 // the product on a prepared input
-int run_from(const PrepBuf &P, const mynah_asr_hip_weight *W, float *dy, int T, int act, hipStream_t st) {
+int run_from(Ctx *c, const PrepBuf &P, const mynah_asr_hip_weight *W, float *dy, int T, int act, hipStream_t st) {
     hipError_t e;
-    if (P.i8)
+    if (P.i8) {
         e = mh_launch_gemm_i8(W->qtype, W->dw, (const uint8_t *)P.xp.p, (const float *)P.xs16.p, dy, T, act, st);
-    else
+    } else {
+        // few tiles: K split over workgroups, through the calling thread's workspace
+        const size_t n = mh_gemm_ws_floats(W->dw, T);
+        float *ws = n ? (float *)c->gk.get(n * sizeof(float)) : nullptr;
         e = mh_launch_gemm(W->qtype, W->dw, (const uint8_t *)P.xp.p, (const float *)P.xs16.p,
-                           (const float *)P.xpf.p, dy, T, act, st);
+                           (const float *)P.xpf.p, dy, T, act, ws, st);
+    }
     if (e != hipSuccess) return fail("gemm launch failed", hipGetErrorString(e));
     return 0;
 }
 int run_prepped(Ctx *c, const mynah_asr_hip_weight *W, float *dy, int T, int act, hipStream_t st) {
-    return run_from(c->pa, W, dy, T, act, st);
+    return run_from(c, c->pa, W, dy, T, act, st);
 }
 
 // the calling thread's split-K GEMV workspace for W (null: the one-launch GEMV)
@@ -258,7 +263,7 @@ int ffn_dev(Ctx *c, const mynah_asr_hip_weight *W1, const mynah_asr_hip_weight *
         P.Kp = Kp;
         P.xsum = xsum;
         P.i8 = 0;
-        return run_from(P, W2, dy, T, 0, st);
+        return run_from(c, P, W2, dy, T, 0, st);
     }
     float *dh = (float *)c->h.get((size_t)T * W1->dw.n * sizeof(float));
     if (!dh) return fail("device buffer allocation failed");

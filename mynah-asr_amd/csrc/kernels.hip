@@ -387,7 +387,11 @@ template <int QT> constexpr int gemm_occ() { return QT == QT_Q6_K ? 2 : 3; }
 // the second product's K, so the chunk's shift, split and sums are formed
 // here by split_part, the same function the preparation pass runs, on the
 // same f32 values (bit-identical to storing y and preparing it).
-enum { EPI_Y = 0, EPI_PREP = 1 };
+enum { EPI_Y = 0, EPI_PREP = 1, EPI_PART = 2 };
+// EPI_PART (launches with few tiles): workgroup (tile, split) runs one range
+// of chunks and stores each chunk's result to part[c][Mpad][Np] instead of
+// folding it; k_gemm_fold then folds them in chunk order from zero, with the
+// prepared input's fold factors: the operations the fold in registers runs.
 struct PrepOut {
     uint8_t *xp, *xm;
     float *xpf;
@@ -411,7 +415,8 @@ template <int QT, int EPI>
 __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const uint8_t *__restrict__ xp,
                                                  const uint8_t *__restrict__ xm,
                                                  const float *__restrict__ xpf,
-                                                 int M, int act, int tilesM, int tilesN, PrepOut po) {
+                                                 int M, int act, int tilesM, int tilesN, PrepOut po,
+                                                 float *__restrict__ part, int ksplit) {
     using F = Fmt<QT>;
     using L = StageLayout<QT>;
     constexpr int WM = 2, WN = 1;
@@ -424,10 +429,13 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
     // Several products of one input (J.n jobs) share the row bands: the tiles
     // of band tm are (job, column tile) pairs, so one XCD runs all of a band's
     // products and reads its activations into its L2 once.
-    const int nj = J.n, ntiles = nj * tilesM * tilesN, bid = blockIdx.x;
+    // With EPI_PART, a band's splits follow each other (band, split, tile).
+    const int KS = EPI == EPI_PART ? ksplit : 1;
+    const int nj = J.n, ntiles = nj * tilesM * tilesN * KS, bid = blockIdx.x;
     const int q = ntiles / 8, rem = ntiles % 8, xcd = bid % 8, loc = bid / 8;
     const int t = xcd < rem ? xcd * (q + 1) + loc : rem * (q + 1) + (xcd - rem) * q + loc;
-    const int tm = t / (nj * tilesN), tr = t - tm * nj * tilesN;
+    const int tm = t / (nj * tilesN * KS), ts = t - tm * nj * tilesN * KS;
+    const int ks = ts / (nj * tilesN), tr = ts - ks * nj * tilesN;
     const int job = tr / tilesN, tn = tr - job * tilesN;
     const DevW W = job == 0 ? J.W[0] : (job == 1 ? J.W[1] : J.W[2]);
     float *__restrict__ y = job == 0 ? J.y[0] : (job == 1 ? J.y[1] : J.y[2]);
@@ -436,6 +444,8 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
     const int hh = lane >> 5, col = lane & 31;
     const int Kc = W.Kp / 128;
     const int G0 = tm * 2, GC0 = tn * 4;
+    const int cps = (Kc + KS - 1) / KS;
+    const int c0 = EPI == EPI_PART ? ks * cps : 0, c1 = EPI == EPI_PART ? min(c0 + cps, Kc) : Kc;
 
     auto stage = [&](int c, int q, uint8_t *B) {
         const int rg = wave >> 1, gc = GC0 + wave;
@@ -479,8 +489,8 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
     f16v total[WM][WN];
 #pragma unroll
     for (int i = 0; i < WM; i++) total[i][0] = zero16();
-    stage(0, 0, sbuf[0]);
-    for (int c = 0; c < Kc; c++) {
+    if (EPI != EPI_PART || c0 < c1) stage(c0, 0, sbuf[0]);
+    for (int c = c0; c < c1; c++) {
         BH<QT, WN> hd;
         f16v acc[WM][WN];
 #pragma unroll
@@ -494,7 +504,7 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
             wait_vm<0>();
             __syncthreads();
             if (q + 1 < L::NST) stage(c, q + 1, sbuf[(q + 1) & 1]);
-            else if (c + 1 < Kc) stage(c + 1, 0, sbuf[0]);
+            else if (c + 1 < c1) stage(c + 1, 0, sbuf[0]);
             if (q == 0) {
                 // the chunk's factors, from its headers (staged with every stage)
                 if constexpr (fold_fmt<QT>())
@@ -512,6 +522,15 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
                 fold_finish<QT>(xmv, hd.h[0], acc[i][0]);
             }
         }
+        if constexpr (EPI == EPI_PART) {
+            const size_t Mp = (size_t)tilesM * 64;
+            float *pc = part + (size_t)c * Mp * W.Np + 32 * (GC0 + wave) + col;
+#pragma unroll
+            for (int i = 0; i < WM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) pc[(size_t)(32 * (G0 + i) + drow(e, hh)) * W.Np] = acc[i][0][e];
+            continue;
+        }
 #pragma unroll
         for (int i = 0; i < WM; i++) {
             const f16v pv = lds_rows16(sbuf[1] + L::PF + i * 128, hh);
@@ -520,6 +539,7 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
         }
     }
     wait_vm<0>();
+    if constexpr (EPI == EPI_PART) return;
     if constexpr (EPI == EPI_PREP) {
         // the 64 x 128 SiLU tile through LDS (row stride 132 floats: 16-byte
         // aligned rows), then wave w splits half-steps 4*(w>>1) .. +3 of row
@@ -599,6 +619,49 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
             if constexpr (QT == QT_F32) v = ldexpf(v, -shw);
             y[(size_t)m * W.n + n] = act ? silu_f(v) : v;
         }
+}
+
+// The fold of EPI_PART's chunk results: y[m][n] from part[c][m][n], c in
+// order from zero, with factor xpf[m/32][c][m%32] (what k_gemm stages as the
+// chunk's fold factors), then k_gemm's own epilogue. Thread = (row m, four
+// columns); the loads go out eight chunks at a time.
+template <int QT>
+__global__ __launch_bounds__(256) void k_gemm_fold(DevW W, const float *__restrict__ part,
+                                                   const float *__restrict__ xpf, float *__restrict__ y, int M,
+                                                   int Mp, int act) {
+    const int n4 = W.Np / 4;
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    const int m = idx / n4, n = 4 * (idx - m * n4);
+    if (m >= M) return;
+    const int Kc = W.Kp / 128;
+    const float *pf = xpf + (size_t)(m >> 5) * Kc * 32 + (m & 31);
+    const float *pp = part + (size_t)m * W.Np + n;
+    float total[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c0 = 0; c0 < Kc; c0 += 8) {
+        float4 pv[8];
+        float fv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (c0 + u < Kc) {
+                pv[u] = *(const float4 *)(pp + (size_t)(c0 + u) * Mp * W.Np);
+                fv[u] = pf[(c0 + u) * 32];
+            }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (c0 + u < Kc) {
+                total[0] = __builtin_fmaf(fv[u], pv[u].x, total[0]);
+                total[1] = __builtin_fmaf(fv[u], pv[u].y, total[1]);
+                total[2] = __builtin_fmaf(fv[u], pv[u].z, total[2]);
+                total[3] = __builtin_fmaf(fv[u], pv[u].w, total[3]);
+            }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        if (n + j >= W.n) return;
+        float v = total[j];
+        if constexpr (QT == QT_F32) v = ldexpf(v, -wshift<QT>(W, n + j));
+        y[(size_t)m * W.n + n + j] = act ? silu_f(v) : v;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1293,9 +1356,30 @@ static hipError_t gemv_t(const GJobs &J, const float *x, int M, int vec, const G
     return launch_gemv<QT, 4, 1>(J, x, M, vec, pro, st);
 }
 
+// K split for a launch of few tiles (at most one workgroup per CU otherwise,
+// each running its chunks as one long dependent chain): enough (tile, split)
+// workgroups for three per CU, none of them empty. 1: no split. It pays when
+// the chain it shortens is long (16 chunks or more) or the chunk results the
+// fold reads back are few (outputs of at most 512K elements); measured on
+// 1024 -> 1024 at M = 750 (8 chunks, 786K outputs) it does not.
+static int gemm_ksplit(int Kc, int tiles, size_t outs) {
+    if (tiles > 256 || Kc < 2 || (Kc < 16 && outs > ((size_t)512 << 10))) return 1;
+    int s = (768 + tiles - 1) / tiles;
+    if (s > Kc) s = Kc;
+    const int cps = (Kc + s - 1) / s;
+    return (Kc + cps - 1) / cps;
+}
+
+size_t mh_gemm_ws_floats(const DevW &W, int M) {
+    const int Kc = W.Kp / 128, tilesM = mh_mpad(M) / 64;
+    const size_t outs = (size_t)tilesM * 64 * W.Np;
+    if (W.Np % 128 != 0 || gemm_ksplit(Kc, tilesM * (W.Np / 128), outs) == 1) return 0;
+    return (size_t)Kc * outs;
+}
+
 template <int QT>
 static hipError_t gemm_t(const GemmJobs &J, const uint8_t *xp, const float *xs16, const float *xpf, int M,
-                         int act, const PrepOut *po, hipStream_t st) {
+                         int act, const PrepOut *po, float *ws, hipStream_t st) {
     const DevW &W = J.W[0];
     const int mpad = mh_mpad(M);
     if (mpad % 64 != 0 || W.Np % 128 != 0 || J.n < 1 || J.n > 3) return hipErrorInvalidValue;
@@ -1305,10 +1389,19 @@ static hipError_t gemm_t(const GemmJobs &J, const uint8_t *xp, const float *xs16
     if (po) {
         if (po->Kc != tilesN || J.n != 1) return hipErrorInvalidValue;
         hipLaunchKernelGGL((k_gemm<QT, EPI_PREP>), dim3(grid), dim3(256), 0, st, J, xp, (const uint8_t *)xs16, xpf, M,
-                           1, tilesM, tilesN, *po);
+                           1, tilesM, tilesN, *po, nullptr, 1);
+        return hipGetLastError();
+    }
+    const int ks = J.n == 1 && ws ? gemm_ksplit(W.Kp / 128, grid, (size_t)mpad * W.Np) : 1;
+    if (ks > 1) {
+        hipLaunchKernelGGL((k_gemm<QT, EPI_PART>), dim3(grid * ks), dim3(256), 0, st, J, xp, (const uint8_t *)xs16,
+                           xpf, M, act, tilesM, tilesN, PrepOut{}, ws, ks);
+        const int threads = M * (W.Np / 4);
+        hipLaunchKernelGGL((k_gemm_fold<QT>), dim3((threads + 255) / 256), dim3(256), 0, st, W, (const float *)ws, xpf,
+                           J.y[0], M, mpad, act);
     } else {
         hipLaunchKernelGGL((k_gemm<QT, EPI_Y>), dim3(grid), dim3(256), 0, st, J, xp, (const uint8_t *)xs16, xpf, M,
-                           act, tilesM, tilesN, PrepOut{});
+                           act, tilesM, tilesN, PrepOut{}, nullptr, 1);
     }
     return hipGetLastError();
 }
@@ -1382,17 +1475,17 @@ hipError_t mh_launch_gemv(int qtype, const DevW &W, const float *x, int M, int v
 }
 
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
-                          const float *xpf, float *y, int M, int act, hipStream_t st) {
+                          const float *xpf, float *y, int M, int act, float *ws, hipStream_t st) {
     GemmJobs J{};
     J.W[0] = J.W[1] = J.W[2] = W;
     J.y[0] = J.y[1] = J.y[2] = y;
     J.n = 1;
-    MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, act, nullptr, st)
+    MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, act, nullptr, ws, st)
 }
 
 hipError_t mh_launch_gemm_jobs(int qtype, const GemmJobs &J, const uint8_t *xp, const float *xs16,
                                const float *xpf, int M, hipStream_t st) {
-    MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, 0, nullptr, st)
+    MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, 0, nullptr, nullptr, st)
 }
 
 hipError_t mh_launch_gemm_prep_out(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
@@ -1402,7 +1495,7 @@ hipError_t mh_launch_gemm_prep_out(int qtype, const DevW &W, const uint8_t *xp, 
     GemmJobs J{};
     J.W[0] = J.W[1] = J.W[2] = W;
     J.n = 1;
-    MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, 1, &po, st)
+    MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, 1, &po, nullptr, st)
 }
 
 hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,

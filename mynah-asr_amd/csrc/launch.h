@@ -57,8 +57,14 @@ hipError_t mh_launch_gemv_jobs(int qtype, const GJobs &J, const float *x, int M,
 // keys per attention split of the decoder step
 constexpr int MH_ATT_KC = 64;
 __host__ __device__ inline int mh_att_splits_dev(int n) { return (n + MH_ATT_KC - 1) / MH_ATT_KC; }
+// Floats of device workspace that let a product of W over M rows split K over
+// workgroups (0: it never does). It does when the product has at most 256
+// tiles of 64 x 128 (one workgroup per CU or fewer): each chunk's results go
+// to the workspace and a second launch folds them in chunk order (the same
+// bits as without). Calls sharing one workspace must be ordered on one stream.
+size_t mh_gemm_ws_floats(const DevW &W, int M);
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
-                          const float *xpf, float *y, int M, int act, hipStream_t st);
+                          const float *xpf, float *y, int M, int act, float *ws, hipStream_t st);
 // up to three products (same shape) of one prepared input in one launch
 struct GemmJobs {
     DevW W[3];

@@ -232,6 +232,34 @@ def test_split_k_gemv_rows_match_gemm(gpu, orc, qt):
     dw.close()
 
 
+@pytest.mark.parametrize("qt", ALL, ids=lambda q: M.NAMES[q])
+def test_split_k_gemm_rows_match_gemm(gpu, orc, qt):
+    """A product with few tiles splits K over workgroups (chunk results to a
+    workspace, then their fold in chunk order); its rows must carry the bits
+    of the same rows in a product with enough tiles to run unsplit. K = 2048,
+    N = 1024: M = 40 and 700 split (8 and 88 tiles), M = 2100 does not (264
+    tiles); with and without SiLU."""
+    import torch
+    say("split-K gemm", M.NAMES[qt])
+    k, n = 2048, 1024
+    dw = M.DeviceWeight(gpu, M.Weight.make(gpu, qt, gpu.randn(80, 0.02, (n, k))))
+    x = torch.from_numpy(gpu.randn(81, 1.0, (2100, k))).cuda()
+    for act in (0, 1):
+        ys = {}
+        for T in (2100, 700, 40):
+            y = torch.full((T, n), float("nan"), dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+            dw.gemm(x.data_ptr(), y.data_ptr(), T, act)
+            torch.cuda.synchronize()
+            ys[T] = y
+        for T in (700, 40):
+            assert torch.equal(ys[T].view(torch.int32), ys[2100][:T].view(torch.int32)), f"M={T} act={act}"
+    if qt == M.Q8_0:
+        ref = orc.gemm_f64(x[:40].cpu().numpy(), oracle_dequant(orc, dw.w))
+        check_close(ys[40].cpu().numpy(), ref / (1.0 + np.exp(-ref)), "split-K Q8_0 SiLU")
+    dw.close()
+
+
 # ------------------------------------------------------ fused entry points
 def test_ffn_and_qkv(gpu, orc):
     import ctypes as C
