@@ -1364,6 +1364,7 @@ static hipError_t gemv_t(const GJobs &J, const float *x, int M, int vec, const G
 // 1024 -> 1024 at M = 750 (8 chunks, 786K outputs) it does not.
 static int gemm_ksplit(int Kc, int tiles, size_t outs) {
     if (tiles > 256 || Kc < 2 || (Kc < 16 && outs > ((size_t)512 << 10))) return 1;
+    if ((size_t)Kc * outs > ((size_t)64 << 20)) return 1;   // workspace above 256 MiB: unsplit
     int s = (768 + tiles - 1) / tiles;
     if (s > Kc) s = Kc;
     const int cps = (Kc + s - 1) / s;
