@@ -20,7 +20,8 @@ INT8ACT numerics (int8 activations on the i8 MFMA, against 5.0 POP/s), each of
 Q2_K, Q3_K, Q4_K, Q5_K and Q6_K at benchmark config 4's M = 12000 shapes, decoder GEMVs (config 3) in HBM GB/s with >= 512
 MB of rotating weight copies (defeats the 256 MB MALL), timed as one HIP graph
 of all the launches (kernel_us; call_us = the same launches issued one by one
-from the host), the f32-weight GEMM, the relative-position attention core at T = 750
+from the host), products of 16 to 750 rows on one stream (qgemm_dev calls: few tiles,
+K split over workgroups), the f32-weight GEMM, the relative-position attention core at T = 750
 (16 segments as in benchmark config 5, d 1024, 8 heads; full and chunked-limited [70, 13] windows;
 useful flops = 6 * dk per visible (row, key) pair, against the 157.3 TFLOP/s
 fp32 MFMA peak), and the reference CPU path timed on this host (ingot dequant, compiled from
@@ -273,6 +274,34 @@ def attn_flops(T, H, dk, left, right, nseq):
     return 6.0 * dk * pairs * H * nseq
 
 
+def run_small_m(B, M_, reps=50):
+    """Products of few rows on one stream (the streaming encoder's chunks, one
+    segment's out / pos products, the decoder's cross K/V): qgemm_dev calls
+    (preparation + product, K split over workgroups where the product has few
+    tiles), HIP events on the stream, Q8_0 weights."""
+    torch = B.torch
+    lib = B.lib
+    out = []
+    for (k, n) in [(1024, 1024), (4096, 1024), (1024, 4096)]:
+        dw = M_.DeviceWeight(lib, M_.Weight.make(lib, M_.Q8_0, lib.randn(0, 0.02, (n, k))))
+        for M in (16, 17, 64, 256, 750):
+            x = B.dev(lib.randn(1, 1.0, (M, k)))
+            y = B.empty(M, n)
+            for _ in range(5):
+                dw.gemm(x.data_ptr(), y.data_ptr(), M, 0, B.sp)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(B.stream)
+            for _ in range(reps):
+                dw.gemm(x.data_ptr(), y.data_ptr(), M, 0, B.sp)
+            e1.record(B.stream)
+            B.sync()
+            us = e0.elapsed_time(e1) / reps * 1e3
+            out.append({"M": M, "k": k, "n": n, "format": "Q8_0", "call_us": round(us, 2),
+                        "tflops": round(2.0 * M * n * k / us / 1e6, 2)})
+        dw.close()
+    return out
+
+
 def run_attention(B, M_, T=750, d=1024, H=8, nseq=16, reps=10):
     """The rel-pos attention core (src/encoder.c:315-410 / 220-313) on one
     layer's q, k, v of nseq segments, full and chunked-limited windows."""
@@ -471,6 +500,8 @@ def main():
         details["gemv"] = gv
         big = [g for g in gv if g["n"] * g["k"] >= 4 << 20]
         details["gemv_hbm_frac_mean_large"] = round(float(np.mean([g["kernel_hbm_frac"] for g in big])), 4)
+        log("[bench] few-row products (one stream)")
+        details["gemm_small_m"] = run_small_m(B, M_)
 
     cpu = None
     if not args.no_cpu:
