@@ -422,6 +422,8 @@ def main():
     ap.add_argument("--attention", action="store_true",
                     help="only the rel-pos attention core (T=750, 16 segments, full and [70, 13] windows), "
                          "one JSON line")
+    ap.add_argument("--small-m", action="store_true",
+                    help="only the few-row products on one stream (M = 16 .. 750), one JSON line")
     ap.add_argument("--aed", action="store_true",
                     help="only the AED decoder (config 3 shapes, 4 layers, T=750, Q8_0), one JSON line")
     ap.add_argument("--profile", action="store_true",
@@ -446,6 +448,9 @@ def main():
         return
     if args.attention:
         print(json.dumps({"relpos_attention": run_attention(B, M_)}), flush=True)
+        return
+    if args.small_m:
+        print(json.dumps({"gemm_small_m": run_small_m(B, M_)}), flush=True)
         return
     if args.aed:
         print(json.dumps({"aed_decoder": run_aed(B, M_)}), flush=True)
