@@ -292,8 +292,10 @@ int qkv_dev(Ctx *c, const mynah_asr_hip_weight *const W[3], const float *dx, flo
         }
         J.n = 3;
         const PrepBuf &P = c->pa;
+        const size_t n = mh_gemm_ws_floats(W[0]->dw, T, 3);
+        float *ws = n ? (float *)c->gk.get(n * sizeof(float)) : nullptr;
         hipError_t e = mh_launch_gemm_jobs(W[0]->qtype, J, (const uint8_t *)P.xp.p, (const float *)P.xs16.p,
-                                           (const float *)P.xpf.p, T, st);
+                                           (const float *)P.xpf.p, T, ws, st);
         if (e != hipSuccess) return fail("gemm launch failed", hipGetErrorString(e));
         return 0;
     }

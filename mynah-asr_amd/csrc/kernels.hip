@@ -524,7 +524,7 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
         }
         if constexpr (EPI == EPI_PART) {
             const size_t Mp = (size_t)tilesM * 64;
-            float *pc = part + (size_t)c * Mp * W.Np + 32 * (GC0 + wave) + col;
+            float *pc = part + ((size_t)job * Kc + c) * Mp * W.Np + 32 * (GC0 + wave) + col;
 #pragma unroll
             for (int i = 0; i < WM; i++)
 #pragma unroll
@@ -621,21 +621,23 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
         }
 }
 
-// The fold of EPI_PART's chunk results: y[m][n] from part[c][m][n], c in
-// order from zero, with factor xpf[m/32][c][m%32] (what k_gemm stages as the
-// chunk's fold factors), then k_gemm's own epilogue. Thread = (row m, four
-// columns); the loads go out eight chunks at a time.
+// The fold of EPI_PART's chunk results: y[m][n] from part[job][c][m][n], c
+// in order from zero, with factor xpf[m/32][c][m%32] (what k_gemm stages as
+// the chunk's fold factors), then k_gemm's own epilogue. Thread = (row m, four
+// columns), blockIdx.y = job; the loads go out eight chunks at a time.
 template <int QT>
-__global__ __launch_bounds__(256) void k_gemm_fold(DevW W, const float *__restrict__ part,
-                                                   const float *__restrict__ xpf, float *__restrict__ y, int M,
-                                                   int Mp, int act) {
+__global__ __launch_bounds__(256) void k_gemm_fold(GemmJobs J, const float *__restrict__ part,
+                                                   const float *__restrict__ xpf, int M, int Mp, int act) {
+    const int job = blockIdx.y;
+    const DevW W = job == 0 ? J.W[0] : (job == 1 ? J.W[1] : J.W[2]);
+    float *__restrict__ y = job == 0 ? J.y[0] : (job == 1 ? J.y[1] : J.y[2]);
     const int n4 = W.Np / 4;
     const int idx = blockIdx.x * 256 + threadIdx.x;
     const int m = idx / n4, n = 4 * (idx - m * n4);
     if (m >= M) return;
     const int Kc = W.Kp / 128;
     const float *pf = xpf + (size_t)(m >> 5) * Kc * 32 + (m & 31);
-    const float *pp = part + (size_t)m * W.Np + n;
+    const float *pp = part + (size_t)job * Kc * Mp * W.Np + (size_t)m * W.Np + n;
     float total[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int c0 = 0; c0 < Kc; c0 += 8) {
         float4 pv[8];
@@ -1360,8 +1362,9 @@ static hipError_t gemv_t(const GJobs &J, const float *x, int M, int vec, const G
 // each running its chunks as one long dependent chain): enough (tile, split)
 // workgroups for three per CU, none of them empty. 1: no split. It pays when
 // the chain it shortens is long (16 chunks or more) or the chunk results the
-// fold reads back are few (outputs of at most 512K elements); measured on
-// 1024 -> 1024 at M = 750 (8 chunks, 786K outputs) it does not.
+// fold reads back are few (outputs of at most 512K elements over all jobs);
+// measured on 1024 -> 1024 at M = 750 (8 chunks, 786K outputs), and on three
+// such products at M = 256, it does not.
 static int gemm_ksplit(int Kc, int tiles, size_t outs) {
     if (tiles > 256 || Kc < 2 || (Kc < 16 && outs > ((size_t)512 << 10))) return 1;
     if ((size_t)Kc * outs > ((size_t)64 << 20)) return 1;   // workspace above 256 MiB: unsplit
@@ -1371,10 +1374,10 @@ static int gemm_ksplit(int Kc, int tiles, size_t outs) {
     return (Kc + cps - 1) / cps;
 }
 
-size_t mh_gemm_ws_floats(const DevW &W, int M) {
+size_t mh_gemm_ws_floats(const DevW &W, int M, int jobs) {
     const int Kc = W.Kp / 128, tilesM = mh_mpad(M) / 64;
-    const size_t outs = (size_t)tilesM * 64 * W.Np;
-    if (W.Np % 128 != 0 || gemm_ksplit(Kc, tilesM * (W.Np / 128), outs) == 1) return 0;
+    const size_t outs = (size_t)jobs * tilesM * 64 * W.Np;   // over all jobs
+    if (W.Np % 128 != 0 || gemm_ksplit(Kc, jobs * tilesM * (W.Np / 128), outs) == 1) return 0;
     return (size_t)Kc * outs;
 }
 
@@ -1393,13 +1396,13 @@ static hipError_t gemm_t(const GemmJobs &J, const uint8_t *xp, const float *xs16
                            1, tilesM, tilesN, *po, nullptr, 1);
         return hipGetLastError();
     }
-    const int ks = J.n == 1 && ws ? gemm_ksplit(W.Kp / 128, grid, (size_t)mpad * W.Np) : 1;
+    const int ks = ws ? gemm_ksplit(W.Kp / 128, grid, (size_t)J.n * mpad * W.Np) : 1;
     if (ks > 1) {
         hipLaunchKernelGGL((k_gemm<QT, EPI_PART>), dim3(grid * ks), dim3(256), 0, st, J, xp, (const uint8_t *)xs16,
                            xpf, M, act, tilesM, tilesN, PrepOut{}, ws, ks);
         const int threads = M * (W.Np / 4);
-        hipLaunchKernelGGL((k_gemm_fold<QT>), dim3((threads + 255) / 256), dim3(256), 0, st, W, (const float *)ws, xpf,
-                           J.y[0], M, mpad, act);
+        hipLaunchKernelGGL((k_gemm_fold<QT>), dim3((threads + 255) / 256, J.n), dim3(256), 0, st, J, (const float *)ws,
+                           xpf, M, mpad, act);
     } else {
         hipLaunchKernelGGL((k_gemm<QT, EPI_Y>), dim3(grid), dim3(256), 0, st, J, xp, (const uint8_t *)xs16, xpf, M,
                            act, tilesM, tilesN, PrepOut{}, nullptr, 1);
@@ -1485,8 +1488,8 @@ hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const flo
 }
 
 hipError_t mh_launch_gemm_jobs(int qtype, const GemmJobs &J, const uint8_t *xp, const float *xs16,
-                               const float *xpf, int M, hipStream_t st) {
-    MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, 0, nullptr, nullptr, st)
+                               const float *xpf, int M, float *ws, hipStream_t st) {
+    MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, 0, nullptr, ws, st)
 }
 
 hipError_t mh_launch_gemm_prep_out(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,

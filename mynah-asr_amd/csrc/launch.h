@@ -62,7 +62,7 @@ __host__ __device__ inline int mh_att_splits_dev(int n) { return (n + MH_ATT_KC 
 // tiles of 64 x 128 (one workgroup per CU or fewer): each chunk's results go
 // to the workspace and a second launch folds them in chunk order (the same
 // bits as without). Calls sharing one workspace must be ordered on one stream.
-size_t mh_gemm_ws_floats(const DevW &W, int M);
+size_t mh_gemm_ws_floats(const DevW &W, int M, int jobs = 1);
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
                           const float *xpf, float *y, int M, int act, float *ws, hipStream_t st);
 // up to three products (same shape) of one prepared input in one launch
@@ -71,8 +71,9 @@ struct GemmJobs {
     float *y[3];
     int n;
 };
+// (ws: as for mh_launch_gemm, sized by mh_gemm_ws_floats(W, M, J.n), or null)
 hipError_t mh_launch_gemm_jobs(int qtype, const GemmJobs &J, const uint8_t *xp, const float *xs16,
-                               const float *xpf, int M, hipStream_t st);
+                               const float *xpf, int M, float *ws, hipStream_t st);
 // The FFN's first product with SiLU, its output prepared as the input of a
 // product with Kp = 128 * oKc (oKc = the first product's column tiles):
 // (oxp, oxs16, oxpf) as mh_launch_prep would write them.
