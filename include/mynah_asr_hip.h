@@ -155,6 +155,24 @@ int mynah_asr_hip_qffn_dev(const mynah_asr_hip_weight *w1, const mynah_asr_hip_w
 int mynah_asr_hip_qqkv_dev(const mynah_asr_hip_weight *wq, const mynah_asr_hip_weight *wk,
                            const mynah_asr_hip_weight *wv, const float *dx, float *dq, float *dk, float *dv, int T,
                            void *stream);
+/* qgemm_dev without any allocation, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). No counterpart in the reference. The same product and
+ * the same bits as mynah_asr_hip_qgemm_dev; the prepared input goes to a
+ * 32 MiB device array that each GPU holds from the library's first such call
+ * until the process ends, and K is never split over workgroups (the split-K
+ * launches need a workspace of their own). `stream` is used as given (NULL =
+ * the null stream; no per-thread stream is created). Returns -1 when the
+ * prepared input of T rows does not fit the 32 MiB (see
+ * mynah_asr_hip_noalloc_bytes). Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (two streams, two threads) race, so the
+ * caller orders them. */
+int mynah_asr_hip_qgemm_noalloc_dev(const mynah_asr_hip_weight *w, const float *dx, float *dy, int T, int act,
+                                    void *stream);
+/* Scratch bytes qgemm_noalloc_dev needs for w over T rows in the current
+ * numerics mode (0 for the GEMV path, M <= 16, which needs none); calls above
+ * 32 MiB (33554432) are refused. */
+size_t mynah_asr_hip_noalloc_bytes(const mynah_asr_hip_weight *w, int T);
 /* dwd[n,k] = dequantized weight. */
 int mynah_asr_hip_dequant_dev(const mynah_asr_hip_weight *w, float *dwd, void *stream);
 

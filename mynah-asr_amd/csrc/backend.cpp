@@ -551,6 +551,85 @@ int aed_run(Ctx *c, const mynah_asr_hip_aed *a, const float *enc, int T, const i
     return rc ? -1 : n_out;
 }
 
+// ---------------------------------------------------------------------------
+// The allocation-free product (mynah_asr_hip_qgemm_noalloc_dev). Its prepared
+// input lives in `scratch`, a file-scope device array: every device the
+// library runs on holds one copy, at its own address, until the process ends.
+// In host code `scratch` names a host-side stand-in, never the device memory:
+// the device address comes from hipGetSymbolAddress, once per device, and is
+// the only form host code passes to kernels.
+constexpr size_t kNoAllocBytes = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+
+constexpr int kMaxDevices = 64;
+void *g_scratch_dev[kMaxDevices];   // device address of `scratch` per device (null: not yet looked up)
+
+// the scratch address on the current device (null + t_err on failure)
+uint8_t *noalloc_scratch() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        fail("no current device for the scratch buffer");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_scratch_dev[dev]) {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            fail("hipGetSymbolAddress(scratch) failed", hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_dev[dev] = ptr;
+    }
+    return (uint8_t *)g_scratch_dev[dev];
+}
+
+inline size_t al256(size_t b) { return (b + 255) / 256 * 256; }
+
+// Bytes of scratch a product of W over T rows needs in the current numerics
+// mode (0: the GEMV path, which uses none); what prep_into would allocate.
+size_t noalloc_need(const mynah_asr_hip_weight *W, int T, size_t *o_xs16, size_t *o_xpf) {
+    const bool i8 = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT;
+    if (!i8 && mh_use_gemv(W->dw, T)) return 0;
+    const size_t Mpad = (size_t)mh_mpad(T), Kp = (size_t)W->dw.Kp;
+    const size_t xp = al256(Mpad * Kp * (i8 ? 1 : 4));
+    const size_t xs16 = al256(Mpad * (i8 ? 1 : Kp / 16) * sizeof(float));
+    const size_t xpf = al256(Mpad * (Kp / 128) * sizeof(float));
+    *o_xs16 = xp;
+    *o_xpf = xp + xs16;
+    return xp + xs16 + xpf;
+}
+
+// qgemm_dev's product with its prepared input in `scratch` and K unsplit (the
+// split-K launches need a workspace of their own): the same kernels on the
+// same data, so the same bits.
+int gemm_noalloc(const mynah_asr_hip_weight *W, const float *dx, float *dy, int T, int act, hipStream_t st) {
+    size_t o_xs16 = 0, o_xpf = 0;
+    const size_t need = noalloc_need(W, T, &o_xs16, &o_xpf);
+    const bool i8 = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT;
+    hipError_t e;
+    if (need == 0) {
+        const int vec = (W->dw.k % 8 == 0) && (((uintptr_t)dx & 15) == 0);
+        e = mh_launch_gemv(W->qtype, W->dw, dx, T, vec, dy, act, nullptr, st);
+        return e == hipSuccess ? 0 : fail("gemv launch failed", hipGetErrorString(e));
+    }
+    if (need > kNoAllocBytes) return fail("input too large for the 32 MiB no-allocation scratch");
+    uint8_t *base = noalloc_scratch();
+    if (!base) return -1;
+    uint8_t *xp = base;
+    float *xs16 = (float *)(base + o_xs16), *xpf = (float *)(base + o_xpf);
+    const int Mpad = mh_mpad(T), Kp = W->dw.Kp, k = W->dw.k;
+    if (i8) {
+        e = mh_launch_prep_i8(dx, T, k, Kp, Mpad, xp, xs16, st);
+        if (e == hipSuccess) e = mh_launch_gemm_i8(W->qtype, W->dw, xp, xs16, dy, T, act, st);
+    } else {
+        const int vec = (k % 8 == 0) && (((uintptr_t)dx & 15) == 0);
+        e = mh_launch_prep(dx, T, k, Kp, Mpad, xp, xs16, xpf, wants_xsum(W->qtype), vec, st);
+        if (e == hipSuccess) e = mh_launch_gemm(W->qtype, W->dw, xp, xs16, xpf, dy, T, act, nullptr, st);
+    }
+    return e == hipSuccess ? 0 : fail("launch failed", hipGetErrorString(e));
+}
+
 int begin(Ctx **c) {
     t_err[0] = 0;
     if (!mynah_asr_hip_available()) return fail("no gfx950 device");
@@ -614,6 +693,24 @@ int mynah_asr_hip_qgemm_dev(const mynah_asr_hip_weight *w, const float *dx, floa
     if (T == 0) return 0;
     if (check_numerics_supported(w->qtype)) return -1;
     return gemm_dev(c, w, dx, dy, T, act, pick_stream(stream));
+}
+
+int mynah_asr_hip_qgemm_noalloc_dev(const mynah_asr_hip_weight *w, const float *dx, float *dy, int T, int act,
+                                    void *stream) {
+    // no begin(): that creates the thread's stream; this call uses `stream`
+    // as given (NULL = the null stream) and allocates nothing
+    t_err[0] = 0;
+    if (!mynah_asr_hip_available()) return fail("no gfx950 device");
+    if (!w || !dx || !dy || T < 0) return fail("bad argument");
+    if (T == 0) return 0;
+    if (check_numerics_supported(w->qtype)) return -1;
+    return gemm_noalloc(w, dx, dy, T, act, (hipStream_t)stream);
+}
+
+size_t mynah_asr_hip_noalloc_bytes(const mynah_asr_hip_weight *w, int T) {
+    if (!w || T <= 0) return 0;
+    size_t a, b;
+    return noalloc_need(w, T, &a, &b);
 }
 
 int mynah_asr_hip_prep_dev(const mynah_asr_hip_weight *w, const float *dx, int T, void *stream) {

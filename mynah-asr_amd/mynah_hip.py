@@ -39,6 +39,7 @@ HIP_SYMBOLS = [
     "mynah_asr_hip_qgemm_prepped_dev", "mynah_asr_hip_qffn_dev", "mynah_asr_hip_qqkv_dev",
     "mynah_asr_hip_relpos_attention_dev", "mynah_asr_hip_relpos_attention",
     "mynah_asr_hip_aed_decode_dev", "mynah_asr_hip_aed_forced_dev",
+    "mynah_asr_hip_qgemm_noalloc_dev", "mynah_asr_hip_noalloc_bytes",
 ]
 HOST_SYMBOLS = [
     "mynah_asr_set_backend", "mynah_asr_backend", "mynah_asr_gemm_wt", "mynah_asr_silu",
@@ -119,6 +120,10 @@ class HipLib:
         L.mynah_asr_hip_weight_bytes.argtypes = [_P]
         L.mynah_asr_hip_qgemm_dev.argtypes = [_P, _P, _P, C.c_int, C.c_int, _P]
         L.mynah_asr_hip_dequant_dev.argtypes = [_P, _P, _P]
+        if hasattr(L, "mynah_asr_hip_qgemm_noalloc_dev"):
+            L.mynah_asr_hip_qgemm_noalloc_dev.argtypes = [_P, _P, _P, C.c_int, C.c_int, _P]
+            L.mynah_asr_hip_noalloc_bytes.restype = C.c_size_t
+            L.mynah_asr_hip_noalloc_bytes.argtypes = [_P, C.c_int]
         if hasattr(L, "mynah_asr_hip_prep_dev"):  # absent from older builds
             L.mynah_asr_hip_prep_dev.argtypes = [_P, _P, C.c_int, _P]
             L.mynah_asr_hip_qgemm_prepped_dev.argtypes = [_P, _P, C.c_int, C.c_int, _P]
@@ -266,6 +271,14 @@ class DeviceWeight:
     def gemm(self, dx_ptr: int, dy_ptr: int, T: int, act: int = 0, stream: int = 0) -> None:
         rc = self.lib.L.mynah_asr_hip_qgemm_dev(self.h, dx_ptr, dy_ptr, T, act, stream or None)
         self.lib._check(rc, "qgemm_dev")
+
+    def gemm_noalloc(self, dx_ptr: int, dy_ptr: int, T: int, act: int = 0, stream: int = 0) -> None:
+        """qgemm_dev through the allocation-free entry point (its scratch array)."""
+        rc = self.lib.L.mynah_asr_hip_qgemm_noalloc_dev(self.h, dx_ptr, dy_ptr, T, act, stream or None)
+        self.lib._check(rc, "qgemm_noalloc_dev")
+
+    def noalloc_bytes(self, T: int) -> int:
+        return int(self.lib.L.mynah_asr_hip_noalloc_bytes(self.h, T))
 
     def prep(self, dx_ptr: int, T: int, stream: int = 0) -> None:
         self.lib._check(self.lib.L.mynah_asr_hip_prep_dev(self.h, dx_ptr, T, stream or None), "prep_dev")
