@@ -50,6 +50,19 @@ int fail(const char *msg, const char *detail = nullptr) {
     return -1;
 }
 
+// Set once the calling thread has issued a _dev call on a stream under capture:
+// a HIP graph may then hold pointers into this thread's buffers, so a buffer
+// that grows afterwards keeps its old allocation alive (t_retired, held until
+// the process ends) instead of freeing it, and the graph's replays keep
+// writing and reading memory of their own.
+thread_local bool t_captured = false;
+thread_local std::vector<void *> t_retired;
+
+void note_capture(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs == hipStreamCaptureStatusActive) t_captured = true;
+}
+
 // grow-only device buffer
 struct DBuf {
     void *p = nullptr;
@@ -59,7 +72,10 @@ struct DBuf {
         if (p && cap >= bytes) return p;
         size_t want = cap ? cap : ((size_t)1 << 20);
         while (want < bytes) want *= 2;
-        if (p) (void)hipFree(p);
+        if (p) {
+            if (t_captured) t_retired.push_back(p);
+            else (void)hipFree(p);
+        }
         p = nullptr;
         cap = 0;
         if (hipMalloc(&p, want) != hipSuccess) { p = nullptr; return nullptr; }
@@ -689,6 +705,7 @@ int mynah_asr_hip_qgemm_dev(const mynah_asr_hip_weight *w, const float *dx, floa
                             void *stream) {
     Ctx *c;
     if (begin(&c)) return -1;
+    note_capture(pick_stream(stream));
     if (!w || !dx || !dy || T < 0) return fail("bad argument");
     if (T == 0) return 0;
     if (check_numerics_supported(w->qtype)) return -1;
@@ -716,6 +733,7 @@ size_t mynah_asr_hip_noalloc_bytes(const mynah_asr_hip_weight *w, int T) {
 int mynah_asr_hip_prep_dev(const mynah_asr_hip_weight *w, const float *dx, int T, void *stream) {
     Ctx *c;
     if (begin(&c)) return -1;
+    note_capture(pick_stream(stream));
     if (!w || !dx || T <= 0) return fail("bad argument");
     if (check_numerics_supported(w->qtype)) return -1;
     return prep_for(c, w, dx, T, pick_stream(stream));
@@ -725,6 +743,7 @@ int mynah_asr_hip_qgemm_prepped_dev(const mynah_asr_hip_weight *w, float *dy, in
                                     void *stream) {
     Ctx *c;
     if (begin(&c)) return -1;
+    note_capture(pick_stream(stream));
     if (!w || !dy || T <= 0) return fail("bad argument");
     if (check_numerics_supported(w->qtype)) return -1;
     if (!prep_fits(c, w, T)) return fail("the prepared input does not fit this weight");
@@ -735,6 +754,7 @@ int mynah_asr_hip_qffn_dev(const mynah_asr_hip_weight *w1, const mynah_asr_hip_w
                            float *dy, int T, void *stream) {
     Ctx *c;
     if (begin(&c)) return -1;
+    note_capture(pick_stream(stream));
     if (!w1 || !w2 || !dx || !dy || T < 0 || w2->dw.k != w1->dw.n) return fail("bad argument");
     if (T == 0) return 0;
     if (check_numerics_supported(w1->qtype) || check_numerics_supported(w2->qtype)) return -1;
@@ -746,6 +766,7 @@ int mynah_asr_hip_qqkv_dev(const mynah_asr_hip_weight *wq, const mynah_asr_hip_w
                            void *stream) {
     Ctx *c;
     if (begin(&c)) return -1;
+    note_capture(pick_stream(stream));
     if (!wq || !wk || !wv || !dx || !dq || !dk || !dv || T < 0 || wk->dw.k != wq->dw.k || wv->dw.k != wq->dw.k)
         return fail("bad argument");
     if (T == 0) return 0;

@@ -105,7 +105,8 @@ static int skip_value(cur_t *c, uint32_t type, int depth) {
     return sb < 0 ? -1 : take(c, (uint64_t)sb, &b);
 }
 
-/* bytes of `nelem` elements of ggml `type` (0 when not sized here) */
+/* bytes of `nelem` elements of ggml `type` (0 when not sized here, UINT64_MAX when
+ * beyond 64 bits) */
 static uint64_t type_nbytes(int type, uint64_t nelem) {
     uint64_t bs = 0, be = 1;
     switch (type) {
@@ -132,6 +133,8 @@ static uint64_t type_nbytes(int type, uint64_t nelem) {
     default: return 0;
     }
     if (nelem % be) return 0;
+    /* a size past 2^64 cannot lie inside any file: UINT64_MAX fails the bounds check */
+    if (nelem / be > UINT64_MAX / bs) return UINT64_MAX;
     return nelem / be * bs;
 }
 

@@ -193,6 +193,14 @@ def test_malformed_files_are_refused(lib, tmp_path):
     bad_align = str(tmp_path / "align.gguf")
     write_gguf(bad_align, tens, [], alignment=48)
     cases["alignment48"] = open(bad_align, "rb").read()
+    # element counts whose byte size passes 2^64 (2^63 f32 elements: 2^65 bytes,
+    # which wraps to 0 in 64 bits) over a zero-length payload
+    wrap = str(tmp_path / "wrap.gguf")
+    write_gguf(wrap, [("wrap", GGML["F32"], (1 << 62, 2, 1), b"")], [])
+    cases["size_wraps"] = open(wrap, "rb").read()
+    wrapq = str(tmp_path / "wrapq.gguf")
+    write_gguf(wrapq, [("wrapq", GGML["Q8_0"], (1 << 58, 32), b"")], [])
+    cases["block_size_wraps"] = open(wrapq, "rb").read()
     for what, data in cases.items():
         p = str(tmp_path / f"bad_{what}.gguf")
         with open(p, "wb") as f:
