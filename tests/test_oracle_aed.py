@@ -107,3 +107,85 @@ def test_decode_follows_forced_argmax():
     # positions stop at max_seq: the last prompt position already yields the first token
     toks3, _ = m.decode(enc, prompt, eos=-1, cap=5, max_seq=5)
     assert toks3 == toks[:5 - len(prompt) + 1]
+
+
+# ------------------------------------------------------ closed-form layers
+def _ln(x, w, b):
+    # written out again (not aed.ln): mean, biased variance, eps 1e-5
+    c = x - x.sum() / x.size
+    return c / np.sqrt((c * c).sum() / x.size + 1e-5) * w + b
+
+
+def _one_layer(seed, keep):
+    """One layer whose sublayers outside `keep` have zero output projections."""
+    m = make_model(seed, n_layers=1)
+    L = m.layers[0]
+    for sub, (w, b) in (("self", ("so", "so_b")), ("cross", ("co", "co_b")), ("ffn", ("ff2", "ff2_b"))):
+        if sub not in keep:
+            L[w] = np.zeros_like(L[w])
+            L[b] = np.zeros_like(L[b])
+    return m, L
+
+
+def _logits(m, x):
+    return m.head @ _ln(x, m.fin_w, m.fin_b) + m.head_b
+
+
+def test_ffn_sublayer_closed_form():
+    """decoder_aed.c:205-210: x + W2 relu(W1 LN_ffn(x) + b1) + b2, with the
+    norm before the sublayer (pre-LN) and ReLU, not SiLU or GELU."""
+    m, L = _one_layer(20, {"ffn"})
+    enc = rnd(21, 5, 16)
+    for p, t in enumerate([4, 9, 2]):
+        x = _ln(m.emb[t] + m.pos[p], m.embln_w, m.embln_b)
+        h = L["ff1"] @ _ln(x, L["ln_ffn_w"], L["ln_ffn_b"]) + L["ff1_b"]
+        x = x + L["ff2"] @ np.where(h > 0, h, 0.0) + L["ff2_b"]
+        np.testing.assert_allclose(m.forced(enc, [4, 9, 2][:p + 1])[p], _logits(m, x), rtol=1e-12, atol=1e-12)
+
+
+def test_self_attention_at_position_zero_closed_form():
+    """decoder_aed.c:186-198 at p = 0: one key (the position's own), so the
+    attention output is its value: x + Wo (Wv LN_self(x) + bv) + bo."""
+    m, L = _one_layer(22, {"self"})
+    enc = rnd(23, 5, 16)
+    t = 7
+    x = _ln(m.emb[t] + m.pos[0], m.embln_w, m.embln_b)
+    v = L["sv"] @ _ln(x, L["ln_self_w"], L["ln_self_b"]) + L["sv_b"]
+    x = x + L["so"] @ v + L["so_b"]
+    np.testing.assert_allclose(m.forced(enc, [t])[0], _logits(m, x), rtol=1e-12, atol=1e-12)
+
+
+def test_cross_attention_one_frame_closed_form():
+    """decoder_aed.c:199-204 over one encoder frame: the attention output is
+    that frame's value, whatever the query: x + Wco (Wcv e + bcv) + bco."""
+    m, L = _one_layer(24, {"cross"})
+    e = rnd(25, 1, 16)
+    toks = [3, 8]
+    got = m.forced(e, toks)
+    for p, t in enumerate(toks):
+        x = _ln(m.emb[t] + m.pos[p], m.embln_w, m.embln_b)
+        x = x + L["co"] @ (L["cv"] @ e[0] + L["cv_b"]) + L["co_b"]
+        np.testing.assert_allclose(got[p], _logits(m, x), rtol=1e-12, atol=1e-12)
+
+
+def test_layer_composition_order_closed_form():
+    """All three sublayers at p = 0 over one encoder frame: self, then cross,
+    then FFN, each pre-LN with a residual (decoder_aed.c:186-210). A swapped
+    self/cross order or a post-LN layer gives other values."""
+    m, L = _one_layer(26, {"self", "cross", "ffn"})
+    e = rnd(27, 1, 16)
+    t = 5
+    x = _ln(m.emb[t] + m.pos[0], m.embln_w, m.embln_b)
+    x = x + L["so"] @ (L["sv"] @ _ln(x, L["ln_self_w"], L["ln_self_b"]) + L["sv_b"]) + L["so_b"]
+    x = x + L["co"] @ (L["cv"] @ e[0] + L["cv_b"]) + L["co_b"]
+    h = L["ff1"] @ _ln(x, L["ln_ffn_w"], L["ln_ffn_b"]) + L["ff1_b"]
+    x = x + L["ff2"] @ np.maximum(h, 0.0) + L["ff2_b"]
+    want = _logits(m, x)
+    np.testing.assert_allclose(m.forced(e, [t])[0], want, rtol=1e-12, atol=1e-12)
+    # the swapped order is a different function here (so the test can tell)
+    y = _ln(m.emb[t] + m.pos[0], m.embln_w, m.embln_b)
+    y = y + L["co"] @ (L["cv"] @ e[0] + L["cv_b"]) + L["co_b"]
+    y = y + L["so"] @ (L["sv"] @ _ln(y, L["ln_self_w"], L["ln_self_b"]) + L["sv_b"]) + L["so_b"]
+    h = L["ff1"] @ _ln(y, L["ln_ffn_w"], L["ln_ffn_b"]) + L["ff1_b"]
+    y = y + L["ff2"] @ np.maximum(h, 0.0) + L["ff2_b"]
+    assert not np.allclose(_logits(m, y), want)
