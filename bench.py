@@ -153,6 +153,36 @@ def run_encoder_set(B, M_, qt, M, shapes, steps, warmup, seed0):
     return ms_step, flops, rows
 
 
+def run_int8act(B, M_, M):
+    """INT8ACT numerics: the Q8_0 encoder set at M = 6000 (per-row int8
+    activations, qmat.c:186-202) and the Q4_K / Q5_K layer sets at config 4's
+    M = 12000 (per-super-block int8 activations, ingot's int8 path,
+    third_party/ingot/src/kernels.c:719-750, 1649-1795). The products run on
+    the f16 MFMA with the int8 values as single exact terms; the fractions
+    are given against both the int8 (5.0 POP/s) and the f16 (2.5 PF) peak."""
+    lib = B.lib
+    out = {}
+    lib.set_numerics(1)
+    try:
+        for name, qt, MM, shapes, seed in (("int8act_q8_0_m6000", M_.Q8_0, M, ENC_SHAPES, 0),
+                                           ("int8act_q4_k_m12000", M_.Q4_K, 12000, KQ_SHAPES, 100),
+                                           ("int8act_q5_k_m12000", M_.Q5_K, 12000, KQ_SHAPES, 100)):
+            log(f"[bench] INT8ACT numerics, {name}")
+            ms8, fl8, rows8 = run_encoder_set(B, M_, qt, MM, shapes, 5, 2, seed)
+            tops = fl8 / (ms8 * 1e-3) / 1e12
+            for r in rows8:
+                r["int8_mfma_frac"] = round(r["tflops"] / PEAK_INT8, 4)
+            out[name] = {"tops": round(tops, 2), "ms_per_step": round(ms8, 4),
+                         "int8_mfma_frac": round(tops / PEAK_INT8, 4), "f16_mfma_frac": round(tops / PEAK_FP16, 4),
+                         "rows": rows8}
+    finally:
+        lib.set_numerics(0)
+    out["int8act_note"] = ("int8 activations (Q8_0: per row as qmat.c:186-202; K-quants: per 256-element "
+                           "super-block as ingot's int8 path), exact integer sums, f32 combine; outputs match "
+                           "that path (ingot's 5e-3 budget against the f32 product), not the f32 product")
+    return out
+
+
 def run_gemv(B, M_, qt, n, k, Ms, min_bytes=512 << 20, max_copies=512):
     lib = B.lib
     w = M_.Weight.make(lib, qt, lib.randn(0, 0.02, (n, k)))
@@ -426,6 +456,8 @@ def main():
                     help="only the few-row products on one stream (M = 16 .. 750), one JSON line")
     ap.add_argument("--aed", action="store_true",
                     help="only the AED decoder (config 3 shapes, 4 layers, T=750, Q8_0), one JSON line")
+    ap.add_argument("--int8act", action="store_true",
+                    help="only the INT8ACT layer sets (Q8_0 M=6000, Q4_K and Q5_K M=12000), one JSON line")
     ap.add_argument("--profile", action="store_true",
                     help="counter-calibration run for rocprofv3 --pmc: a 256 MiB device copy, then "
                          "the dominant GEMM (Q8_0 4096->1024, M=6000) alone, 3 launches each")
@@ -455,6 +487,9 @@ def main():
     if args.aed:
         print(json.dumps({"aed_decoder": run_aed(B, M_)}), flush=True)
         return
+    if args.int8act:
+        print(json.dumps(run_int8act(B, M_, M)), flush=True)
+        return
 
     log("[bench] encoder set Q8_0 M=6000")
     ms_step, flops, rows = run_encoder_set(B, M_, M_.Q8_0, M, ENC_SHAPES, args.steps, args.warmup, 0)
@@ -478,18 +513,7 @@ def main():
             kq[M_.NAMES[qt]] = {"tops_per_layer_set": round(fl4 / (ms4 * 1e-3) / 1e12, 2),
                                 "ms_per_layer_set": round(ms4, 3), "rows": rows4}
         details["kquant_m12000"] = kq
-        log("[bench] INT8ACT numerics, Q8_0 encoder set M=6000")
-        lib.set_numerics(1)
-        try:
-            ms8, fl8, rows8 = run_encoder_set(B, M_, M_.Q8_0, M, ENC_SHAPES, 5, 2, 0)
-        finally:
-            lib.set_numerics(0)
-        details["int8act_q8_0_m6000"] = {
-            "tops": round(fl8 / (ms8 * 1e-3) / 1e12, 2), "ms_per_step": round(ms8, 4),
-            "int8_mfma_frac": round(fl8 / (ms8 * 1e-3) / 1e12 / PEAK_INT8, 4),
-            "note": "per-row int8 activations and exact integer block sums (the reference's int8 path, "
-                    "qmat.c:186-202, 508-552, 606-643); outputs match that path, not the f32 product",
-            "rows": rows8}
+        details.update(run_int8act(B, M_, M))
         log("[bench] f32 weights M=6000")
         msf, flf, rowsf = run_encoder_set(B, M_, M_.F32, M, ENC_SHAPES[:2], 3, 1, 200)
         details["f32_m6000"] = {"tflops": round(flf / (msf * 1e-3) / 1e12, 2), "rows": rowsf}

@@ -10,10 +10,12 @@
  *   EXACT (default): every output row matches an f32 GEMM over the
  *     dequantized weights to |y - ref| <= 1e-4*|ref| + 1e-6 (ref accumulated in
  *     double), and a row's bits never depend on how many rows share the call.
- *   INT8ACT: activations quantized per row to int8 exactly as qmat.c:186-202;
- *     integer block sums are exact and the f32 combine follows qmat.c's order
- *     (the reference's small-T path, qmat.c:508-552), for every M. Supported
- *     for INT8, INT4, Q8_0 and Q4_0 weights (other formats return -1).
+ *   INT8ACT: int8 activations and exact integer sums, for every M.
+ *     INT8 / INT4: the reference's small-T path (qmat.c:186-202, 508-552),
+ *     its f32 combine order included. Q8_0 / Q4_0: activations per row as
+ *     qmat.c:186-202. Q2_K..Q6_K: activations per 256-element super-block as
+ *     ingot's int8 path (third_party/ingot/src/kernels.c:719-750, 1649-1795),
+ *     within its 5e-3 budget of the f32 product. F32 weights return -1.
  *
  * Return values: 0 = done, -1 = not done (the caller runs its CPU path);
  * mynah_asr_hip_last_error() names the reason for the calling thread.

@@ -84,7 +84,8 @@ struct DBuf {
     }
 };
 
-// a prepared input: the buffers and what they hold now
+// a prepared input: the buffers and what they hold now (i8: 0 = EXACT, else
+// the INT8ACT activation form, MH_I8_QMAT / _ROW / _SB)
 struct PrepBuf {
     DBuf xp, xs16, xpf;
     int T = -1, Kp = 0, xsum = 0, i8 = 0;
@@ -177,34 +178,54 @@ const mynah_asr_hip_weight *resident(const mynah_asr_hip_wdesc *w) {
 int check_numerics_supported(int qtype) {
     if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT) return 0;
     if (mh_i8_supported(qtype)) return 0;
-    return fail("INT8ACT numerics: supported for INT8, INT4, Q8_0 and Q4_0 weights only");
+    return fail("INT8ACT numerics: f32 weights have no int8 form (the reference multiplies them in f32)");
 }
 
-// Prepare x (device) for products with weight W in the current numerics mode,
-// into the calling thread's workspace.
-//   EXACT:   xp = f16 A fragments, xs16 = sub-block sums (16- or 32-element,
-//            as the format reads them), xpf = chunk fold factors
-//   INT8ACT: xp = int8 A fragments, xs16 = row scales sx
-int prep_into(PrepBuf &P, const mynah_asr_hip_weight *W, const float *dx, int T, hipStream_t st) {
+// the prepared-input form a product of this format reads in the current mode
+int prep_kind(int qtype) {
+    return mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT ? mh_i8_kind(qtype) : 0;
+}
+
+// bytes of the three prepared-input buffers (xp, xs16, xpf) for one form
+void prep_sizes(int kind, int Mpad, int Kp, size_t b[3]) {
+    b[0] = (size_t)Mpad * Kp * (kind == MH_I8_QMAT ? 1 : (kind ? 2 : 4));
+    b[1] = (size_t)Mpad * (kind == MH_I8_QMAT ? 1 : Kp / 16) * sizeof(float);
+    b[2] = (size_t)Mpad * (Kp / 128) * sizeof(float);
+}
+
+// Launch the preparation of x for products of W's format and inner size into
+// (xp, xs16, xpf), sized by prep_sizes:
+//   EXACT:           xp = f16 (hi, lo) A fragments, xs16 = the mins operand of
+//                    the affine formats, xpf = chunk fold factors
+//   INT8ACT QMAT:    xp = int8 A fragments, xs16 = row scales sx
+//   INT8ACT ROW/SB:  xp = int8 values as f16 A fragments, xpf = their scales
+//                    per chunk, xs16 = the mins operand of the affine formats
+hipError_t launch_prep(int kind, const mynah_asr_hip_weight *W, const float *dx, int T, uint8_t *xp, float *xs16,
+                       float *xpf, hipStream_t st) {
     const int Mpad = mh_mpad(T), Kp = W->dw.Kp, k = W->dw.k;
-    const bool i8 = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT;
-    const int xsum = i8 ? 0 : wants_xsum(W->qtype);
-    uint8_t *xp = (uint8_t *)P.xp.get((size_t)Mpad * Kp * (i8 ? 1 : 4));
-    float *xs16 = (float *)P.xs16.get((size_t)Mpad * (i8 ? 1 : Kp / 16) * sizeof(float));
-    float *xpf = (float *)P.xpf.get((size_t)Mpad * (Kp / 128) * sizeof(float));
+    if (kind == MH_I8_QMAT) return mh_launch_prep_i8(dx, T, k, Kp, Mpad, xp, xs16, st);
+    if (kind) return mh_launch_prep_a1(kind, dx, T, k, Kp, Mpad, xp, xs16, xpf, wants_xsum(W->qtype), st);
+    const int vec = (k % 8 == 0) && (((uintptr_t)dx & 15) == 0);
+    return mh_launch_prep(dx, T, k, Kp, Mpad, xp, xs16, xpf, wants_xsum(W->qtype), vec, st);
+}
+
+// Prepare x for products with W in the current numerics mode into the
+// calling thread's workspace P.
+int prep_into(PrepBuf &P, const mynah_asr_hip_weight *W, const float *dx, int T, hipStream_t st) {
+    const int Mpad = mh_mpad(T), Kp = W->dw.Kp;
+    const int kind = prep_kind(W->qtype);
+    size_t b[3];
+    prep_sizes(kind, Mpad, Kp, b);
+    uint8_t *xp = (uint8_t *)P.xp.get(b[0]);
+    float *xs16 = (float *)P.xs16.get(b[1]);
+    float *xpf = (float *)P.xpf.get(b[2]);
     if (!xp || !xs16 || !xpf) return fail("workspace allocation failed");
-    hipError_t e;
-    if (i8) {
-        e = mh_launch_prep_i8(dx, T, k, Kp, Mpad, xp, xs16, st);
-    } else {
-        const int vec = (k % 8 == 0) && (((uintptr_t)dx & 15) == 0);
-        e = mh_launch_prep(dx, T, k, Kp, Mpad, xp, xs16, xpf, xsum, vec, st);
-    }
+    hipError_t e = launch_prep(kind, W, dx, T, xp, xs16, xpf, st);
     if (e != hipSuccess) return fail("prep launch failed", hipGetErrorString(e));
     P.T = T;
     P.Kp = Kp;
-    P.xsum = xsum;
-    P.i8 = i8 ? 1 : 0;
+    P.xsum = kind == MH_I8_QMAT ? 0 : wants_xsum(W->qtype);
+    P.i8 = kind;
     return 0;
 }
 int prep_for(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, int T, hipStream_t st) {
@@ -212,22 +233,23 @@ int prep_for(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, int T, hipS
 }
 
 bool fits(const PrepBuf &P, const mynah_asr_hip_weight *W, int T) {
-    const bool i8 = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT;
-    return P.T == T && P.Kp == W->dw.Kp && P.i8 == (i8 ? 1 : 0) && (i8 || !wants_xsum(W->qtype) || P.xsum == wants_xsum(W->qtype));
+    const int kind = prep_kind(W->qtype);
+    return P.T == T && P.Kp == W->dw.Kp && P.i8 == kind &&
+           (kind == MH_I8_QMAT || !wants_xsum(W->qtype) || P.xsum == wants_xsum(W->qtype));
 }
 bool prep_fits(const Ctx *c, const mynah_asr_hip_weight *W, int T) { return fits(c->pa, W, T); }
 
 // the product on a prepared input
 int run_from(Ctx *c, const PrepBuf &P, const mynah_asr_hip_weight *W, float *dy, int T, int act, hipStream_t st) {
     hipError_t e;
-    if (P.i8) {
+    if (P.i8 == MH_I8_QMAT) {
         e = mh_launch_gemm_i8(W->qtype, W->dw, (const uint8_t *)P.xp.p, (const float *)P.xs16.p, dy, T, act, st);
     } else {
         // few tiles: K split over workgroups, through the calling thread's workspace
         const size_t n = mh_gemm_ws_floats(W->dw, T);
         float *ws = n ? (float *)c->gk.get(n * sizeof(float)) : nullptr;
         e = mh_launch_gemm(W->qtype, W->dw, (const uint8_t *)P.xp.p, (const float *)P.xs16.p,
-                           (const float *)P.xpf.p, dy, T, act, ws, st);
+                           (const float *)P.xpf.p, dy, T, act, ws, st, P.i8 != 0);
     }
     if (e != hipSuccess) return fail("gemm launch failed", hipGetErrorString(e));
     return 0;
@@ -290,13 +312,14 @@ int ffn_dev(Ctx *c, const mynah_asr_hip_weight *W1, const mynah_asr_hip_weight *
 // three products of one input: prepared once whenever it fits them all
 int qkv_dev(Ctx *c, const mynah_asr_hip_weight *const W[3], const float *dx, float *const dy[3], int T,
             hipStream_t st) {
-    // EXACT GEMMs of one format and shape: one preparation, one launch
-    if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT && !mh_use_gemv(W[0]->dw, T) &&
+    // GEMMs of one format and shape: one preparation, one launch
+    const bool exact = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT;
+    if ((!exact || !mh_use_gemv(W[0]->dw, T)) &&
         W[1]->qtype == W[0]->qtype && W[2]->qtype == W[0]->qtype && W[1]->dw.n == W[0]->dw.n &&
         W[2]->dw.n == W[0]->dw.n && W[1]->dw.k == W[0]->dw.k && W[2]->dw.k == W[0]->dw.k &&
         W[1]->dw.Np == W[0]->dw.Np && W[2]->dw.Np == W[0]->dw.Np) {
         if (prep_for(c, W[0], dx, T, st)) return -1;
-        if (c->pa.i8) {
+        if (c->pa.i8 == MH_I8_QMAT) {
             for (int i = 0; i < 3; i++)
                 if (run_prepped(c, W[i], dy[i], T, 0, st)) return -1;
             return 0;
@@ -311,7 +334,7 @@ int qkv_dev(Ctx *c, const mynah_asr_hip_weight *const W[3], const float *dx, flo
         const size_t n = mh_gemm_ws_floats(W[0]->dw, T, 3);
         float *ws = n ? (float *)c->gk.get(n * sizeof(float)) : nullptr;
         hipError_t e = mh_launch_gemm_jobs(W[0]->qtype, J, (const uint8_t *)P.xp.p, (const float *)P.xs16.p,
-                                           (const float *)P.xpf.p, T, ws, st);
+                                           (const float *)P.xpf.p, T, ws, st, P.i8 != 0);
         if (e != hipSuccess) return fail("gemm launch failed", hipGetErrorString(e));
         return 0;
     }
@@ -605,12 +628,11 @@ inline size_t al256(size_t b) { return (b + 255) / 256 * 256; }
 // Bytes of scratch a product of W over T rows needs in the current numerics
 // mode (0: the GEMV path, which uses none); what prep_into would allocate.
 size_t noalloc_need(const mynah_asr_hip_weight *W, int T, size_t *o_xs16, size_t *o_xpf) {
-    const bool i8 = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT;
-    if (!i8 && mh_use_gemv(W->dw, T)) return 0;
-    const size_t Mpad = (size_t)mh_mpad(T), Kp = (size_t)W->dw.Kp;
-    const size_t xp = al256(Mpad * Kp * (i8 ? 1 : 4));
-    const size_t xs16 = al256(Mpad * (i8 ? 1 : Kp / 16) * sizeof(float));
-    const size_t xpf = al256(Mpad * (Kp / 128) * sizeof(float));
+    const int kind = prep_kind(W->qtype);
+    if (!kind && mh_use_gemv(W->dw, T)) return 0;
+    size_t b[3];
+    prep_sizes(kind, mh_mpad(T), W->dw.Kp, b);
+    const size_t xp = al256(b[0]), xs16 = al256(b[1]), xpf = al256(b[2]);
     *o_xs16 = xp;
     *o_xpf = xp + xs16;
     return xp + xs16 + xpf;
@@ -622,7 +644,7 @@ size_t noalloc_need(const mynah_asr_hip_weight *W, int T, size_t *o_xs16, size_t
 int gemm_noalloc(const mynah_asr_hip_weight *W, const float *dx, float *dy, int T, int act, hipStream_t st) {
     size_t o_xs16 = 0, o_xpf = 0;
     const size_t need = noalloc_need(W, T, &o_xs16, &o_xpf);
-    const bool i8 = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT;
+    const int kind = prep_kind(W->qtype);
     hipError_t e;
     if (need == 0) {
         const int vec = (W->dw.k % 8 == 0) && (((uintptr_t)dx & 15) == 0);
@@ -634,14 +656,10 @@ int gemm_noalloc(const mynah_asr_hip_weight *W, const float *dx, float *dy, int 
     if (!base) return -1;
     uint8_t *xp = base;
     float *xs16 = (float *)(base + o_xs16), *xpf = (float *)(base + o_xpf);
-    const int Mpad = mh_mpad(T), Kp = W->dw.Kp, k = W->dw.k;
-    if (i8) {
-        e = mh_launch_prep_i8(dx, T, k, Kp, Mpad, xp, xs16, st);
-        if (e == hipSuccess) e = mh_launch_gemm_i8(W->qtype, W->dw, xp, xs16, dy, T, act, st);
-    } else {
-        const int vec = (k % 8 == 0) && (((uintptr_t)dx & 15) == 0);
-        e = mh_launch_prep(dx, T, k, Kp, Mpad, xp, xs16, xpf, wants_xsum(W->qtype), vec, st);
-        if (e == hipSuccess) e = mh_launch_gemm(W->qtype, W->dw, xp, xs16, xpf, dy, T, act, nullptr, st);
+    e = launch_prep(kind, W, dx, T, xp, xs16, xpf, st);
+    if (e == hipSuccess) {
+        if (kind == MH_I8_QMAT) e = mh_launch_gemm_i8(W->qtype, W->dw, xp, xs16, dy, T, act, st);
+        else e = mh_launch_gemm(W->qtype, W->dw, xp, xs16, xpf, dy, T, act, nullptr, st, kind != 0);
     }
     return e == hipSuccess ? 0 : fail("launch failed", hipGetErrorString(e));
 }

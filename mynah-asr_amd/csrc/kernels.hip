@@ -166,7 +166,11 @@ template <int WM> struct AK {
 // t = the kstep's MFMAs from zero, acc = fma(sc, t, acc) per sub-block. The
 // float operations each output sees, and their order, are the same in every
 // caller.
-template <int QT, int WM, int WN>
+//
+// A1 (INT8ACT numerics): the activations are int8 values held as f16 (exact),
+// one term: the xl MFMAs drop out, and every sum the MFMAs form is an exact
+// integer (the kernels keep each accumulation below 2^24 in magnitude).
+template <int QT, int WM, int WN, bool A1 = false>
 __device__ __forceinline__ void kstep(const AK<WM> &a, const BK<QT, WN> &b, const BH<QT, WN> &hd, int s,
                                       f16v (&acc)[WM][WN]) {
     using F = Fmt<QT>;
@@ -178,11 +182,14 @@ __device__ __forceinline__ void kstep(const AK<WM> &a, const BK<QT, WN> &b, cons
             for (int i = 0; i < WM; i++) {
                 acc[i][j] = mfma32(a.h[i][0], b0, acc[i][j]);
                 acc[i][j] = mfma32(a.h[i][1], b1, acc[i][j]);
-                acc[i][j] = mfma32(a.l[i][0], b0, acc[i][j]);
-                acc[i][j] = mfma32(a.l[i][1], b1, acc[i][j]);
+                if constexpr (!A1) {
+                    acc[i][j] = mfma32(a.l[i][0], b0, acc[i][j]);
+                    acc[i][j] = mfma32(a.l[i][1], b1, acc[i][j]);
+                }
             }
         }
     } else if constexpr (QT == QT_F32) {
+        static_assert(!A1, "f32 weights have no int8-activation form");
         // f32 weights: resident as (wh, wl) f16 pairs scaled per row by
         // 2^shw_n; acc += xh*wh + xh*wl + xl*wh straight into the chunk
         // accumulator (no per-kstep factor)
@@ -207,8 +214,10 @@ __device__ __forceinline__ void kstep(const AK<WM> &a, const BK<QT, WN> &b, cons
             for (int i = 0; i < WM; i++) {
                 f16v t = mfma32(a.h[i][0], b0, zero16());
                 t = mfma32(a.h[i][1], b1, t);
-                t = mfma32(a.l[i][0], b0, t);
-                t = mfma32(a.l[i][1], b1, t);
+                if constexpr (!A1) {
+                    t = mfma32(a.l[i][0], b0, t);
+                    t = mfma32(a.l[i][1], b1, t);
+                }
 #pragma unroll
                 for (int e = 0; e < 16; e++) acc[i][j][e] = __builtin_fmaf(sc, t[e], acc[i][j][e]);
             }
@@ -231,9 +240,9 @@ __device__ __forceinline__ void kstep(const AK<WM> &a, const BK<QT, WN> &b, cons
 #pragma unroll
             for (int i = 0; i < WM; i++) {
                 f16v t0 = mfma32(a.h[i][0], b0, zero16());
-                t0 = mfma32(a.l[i][0], b0, t0);
+                if constexpr (!A1) t0 = mfma32(a.l[i][0], b0, t0);
                 f16v t1 = mfma32(a.h[i][1], b1, zero16());
-                t1 = mfma32(a.l[i][1], b1, t1);
+                if constexpr (!A1) t1 = mfma32(a.l[i][1], b1, t1);
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
                     acc[i][j][e] = __builtin_fmaf(sc0, t0[e], acc[i][j][e]);
@@ -356,14 +365,15 @@ template <int N> __device__ __forceinline__ void wait_vm() {
 // workgroup reads, for its 2 row groups and 4 column groups. Planes of 32 or
 // more bytes per lane and chunk stage the stage's own part; narrower ones the
 // whole (column group, chunk) block.
-template <int QT> struct StageLayout {
+template <int QT, bool A1 = false> struct StageLayout {
     using F = Fmt<QT>;
     static constexpr int SPS = QT == QT_F32 ? 1 : 2;              // ksteps per stage
     static constexpr int NST = KSTEPS / SPS;                      // stages per chunk
-    static constexpr int AR = SPS * 4096;                         // activation bytes per row group
+    static constexpr int TERMS = A1 ? 1 : 2;                      // activation f16 terms
+    static constexpr int AR = SPS * 2048 * TERMS;                 // activation bytes per row group
     template <int B> static constexpr int plane() { return B == 0 ? 0 : (B >= 32 ? SPS * 16 * B : 64 * B); }
     template <int B> static __device__ int plane_off(int q) { return B >= 32 ? q * SPS * 16 * B : 0; }
-    static constexpr int A = 0;                                   // [2 rg][2 SPS u][2 term][1 KiB]
+    static constexpr int A = 0;                                   // [2 rg][2 SPS u][TERMS][1 KiB]
     static constexpr int B0S = plane<F::B0>(), B1S = plane<F::B1>();
     static constexpr int P0 = A + 2 * AR;                         // [4 cg][B0S]
     static constexpr int P1 = P0 + 4 * B0S;                       // [4 cg][B1S]
@@ -411,14 +421,19 @@ struct PrepOut {
 // footprints let two or three workgroups share a CU: their waves fill each
 // other's stalls and overlap one's VALU epilogue with another's MFMAs.
 // grid = tilesM * tilesN workgroups.
-template <int QT, int EPI>
+// A1: INT8ACT numerics (int8 activations as single f16 terms, xpf = their
+// scales); Q5_K then sums each chunk as two exact halves (its products reach
+// 127 * 1953, so a whole chunk could pass 2^24) joined in int32.
+template <int QT, int EPI, bool A1 = false>
 __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const uint8_t *__restrict__ xp,
                                                  const uint8_t *__restrict__ xm,
                                                  const float *__restrict__ xpf,
                                                  int M, int act, int tilesM, int tilesN, PrepOut po,
                                                  float *__restrict__ part, int ksplit) {
     using F = Fmt<QT>;
-    using L = StageLayout<QT>;
+    using L = StageLayout<QT, A1>;
+    static_assert(!(A1 && EPI == EPI_PREP), "the fused FFN hand-off is EXACT only");
+    constexpr bool HALVES = A1 && QT == QT_Q5_K;
     constexpr int WM = 2, WN = 1;
     __shared__ __attribute__((aligned(16))) uint8_t sbuf[2][L::BYTES];
     // XCD-aware tile order: workgroups are dealt to the 8 XCDs round-robin
@@ -449,7 +464,8 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
 
     auto stage = [&](int c, int q, uint8_t *B) {
         const int rg = wave >> 1, gc = GC0 + wave;
-        dma<L::AR / 2>(xp + (((size_t)(G0 + rg) * Kc + c) * 16 + 4 * L::SPS * q + 2 * L::SPS * (wave & 1)) * 1024,
+        dma<L::AR / 2>(xp + (((size_t)(G0 + rg) * Kc + c) * 8 * L::TERMS + 2 * L::SPS * L::TERMS * q +
+                             L::SPS * L::TERMS * (wave & 1)) * 1024,
                        B + L::A + rg * L::AR + (wave & 1) * (L::AR / 2), lane);
         dma<L::B0S>(W.p0 + ((size_t)gc * Kc + c) * 64 * F::B0 + L::template plane_off<F::B0>(q),
                     B + L::P0 + wave * L::B0S, lane);
@@ -475,14 +491,14 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
             for (int i = 0; i < WM; i++)
 #pragma unroll
                 for (int kh = 0; kh < 2; kh++) {
-                    const uint8_t *pp = B + L::A + i * L::AR + ((2 * sl + kh) * 2) * 1024 + lane * 16;
+                    const uint8_t *pp = B + L::A + i * L::AR + ((2 * sl + kh) * L::TERMS) * 1024 + lane * 16;
                     a.h[i][kh] = *(const half8 *)pp;
-                    a.l[i][kh] = *(const half8 *)(pp + 1024);
+                    if constexpr (!A1) a.l[i][kh] = *(const half8 *)(pp + 1024);
                 }
             BK<QT, WN> b;
             // (one-kstep stages hold only kstep s: its local index is 0)
             F::k_lds(B + L::P0 + wave * L::B0S, B + L::P1 + wave * L::B1S, L::SPS == 1 ? 0 : s, lane, b.r[0]);
-            kstep<QT, WM, WN>(a, b, hd, s, acc);
+            kstep<QT, WM, WN, A1>(a, b, hd, s, acc);
         }
     };
 
@@ -493,6 +509,7 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
     for (int c = c0; c < c1; c++) {
         BH<QT, WN> hd;
         f16v acc[WM][WN];
+        int half0[HALVES ? WM : 1][HALVES ? 16 : 1];
 #pragma unroll
         for (int i = 0; i < WM; i++) acc[i][0] = zero16();
         // NST (even) stages per chunk, alternating buffers: stage 0 of every
@@ -513,6 +530,23 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
                     F::hdr_lds(sbuf[0] + L::HB + wave * F::HB, sbuf[0] + L::H2 + wave * F::H2, c, lane, hd.h[0]);
             }
             compute(sbuf[q & 1], q, hd, acc);
+            if constexpr (HALVES) {
+                if (q == L::NST / 2 - 1) {
+#pragma unroll
+                    for (int i = 0; i < WM; i++)
+#pragma unroll
+                        for (int e = 0; e < 16; e++) {
+                            half0[i][e] = (int)acc[i][0][e];
+                            acc[i][0][e] = 0.0f;
+                        }
+                }
+            }
+        }
+        if constexpr (HALVES) {
+#pragma unroll
+            for (int i = 0; i < WM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[i][0][e] = (float)(half0[i][e] + (int)acc[i][0][e]);
         }
         if constexpr (fold_fmt<QT>()) {
 #pragma unroll
@@ -1153,6 +1187,148 @@ __global__ __launch_bounds__(PREP_I8_NW * 64) void k_prep_i8(const float *__rest
     }
 }
 
+// ---------------------------------------------------------------------------
+// INT8ACT activations for the ggml block formats, as the A1 GEMM reads them:
+//   xp   int8 values as single f16 terms (exact)   [G][chunk][u][64][16 B]
+//   xpf  the activation scale of each row and chunk [G][chunk][32]
+//   xm   the affine formats' mins A operand from the exact integer sums of
+//        the int8 values (xm_frag, want_xsum 1 / 2)  [G][chunk][64][16 B]
+// PA1_ROW (Q8_0, Q4_0): one scale per row, quantized exactly as
+//   quantize_act_int8 (src/qmat.c:186-202), the reference's int8 path.
+// PA1_SB (the K-quants): one scale per 256-element super-block, quantized as
+//   ingot's q4_k_quantize_activation (third_party/ingot/src/kernels.c:719-750):
+//   scale = amax/127, q = round-to-nearest-even(x * (127/amax)), saturated.
+enum { PA1_ROW = 0, PA1_SB = 1 };
+
+__device__ __forceinline__ int act_q8_rne(float v, float inv) {
+    const int q = __float2int_rn(__fmul_rn(v, inv));
+    return q > 127 ? 127 : (q < -128 ? -128 : q);
+}
+
+// the lane's 8 values of half-step u of chunk c (zero past M or K)
+template <bool VEC>
+__device__ __forceinline__ void load8(const float *row, bool live, int K, int k0, float (&v)[8]) {
+    if constexpr (VEC) {
+        float4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
+        if (live && k0 < K) {
+            a = *(const float4 *)(row + k0);
+            b = *(const float4 *)(row + k0 + 4);
+        }
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = (live && k0 + j < K) ? row[k0 + j] : 0.0f;
+    }
+}
+
+// one chunk's quantized values of the lane into the A1 layout, their 8-element
+// sums into s8 (exact integers)
+__device__ __forceinline__ void a1_store(uint8_t *xp, int G, int Kc, int c, int lane, const int (&q)[HSTEPS][8],
+                                         float (&s8)[HSTEPS]) {
+#pragma unroll
+    for (int u = 0; u < HSTEPS; u++) {
+        half8 h;
+        int sum = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            h[j] = (_Float16)(float)q[u][j];
+            sum += q[u][j];
+        }
+        s8[u] = (float)sum;
+        *(half8 *)(xp + ((((size_t)G * Kc + c) * HSTEPS + u) * 64 + lane) * 16) = h;
+    }
+}
+
+__device__ __forceinline__ void a1_store_xm(uint8_t *xm, int G, int Kc, int c, int lane, int hh,
+                                            const float (&s8)[HSTEPS], int want_xsum) {
+    if (!want_xsum) return;
+    const half8 v = want_xsum == 1 ? xm_frag<8>(s8, hh) : xm_frag<4>(s8, hh);
+    *(half8 *)(xm + (((size_t)G * Kc + c) * 64 + lane) * 16) = v;
+}
+
+// PA1_SB: workgroup (row group G, super-block b) = one wave over chunks 2b, 2b+1
+template <bool VEC>
+__global__ __launch_bounds__(64) void k_prep_a1_sb(const float *__restrict__ x, int M, int K, int Kp,
+                                                   uint8_t *__restrict__ xp, uint8_t *__restrict__ xm,
+                                                   float *__restrict__ xpf, int want_xsum) {
+    const int G = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+    const int r = lane & 31, hh = lane >> 5, m = 32 * G + r;
+    const int Kc = Kp / 128;
+    const bool live = m < M;
+    const float *row = x + (size_t)(live ? m : 0) * K;
+    float v[2][HSTEPS][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int u = 0; u < HSTEPS; u++) {
+            load8<VEC>(row, live, K, 256 * b + 128 * h + 16 * u + 8 * hh, v[h][u]);
+#pragma unroll
+            for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[h][u][j]));
+        }
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    const bool nz = amax > 0.0f;
+    const float inv = nz ? __fdiv_rn(127.0f, amax) : 0.0f;
+    const float scale = nz ? __fdiv_rn(amax, 127.0f) : 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int c = 2 * b + h;
+        int q[HSTEPS][8];
+#pragma unroll
+        for (int u = 0; u < HSTEPS; u++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) q[u][j] = nz ? act_q8_rne(v[h][u][j], inv) : 0;
+        float s8[HSTEPS];
+        a1_store(xp, G, Kc, c, lane, q, s8);
+        a1_store_xm(xm, G, Kc, c, lane, hh, s8, want_xsum);
+        if (hh == 0) xpf[((size_t)G * Kc + c) * 32 + r] = scale;
+    }
+}
+
+// PA1_ROW: workgroup = one 32-row group; 16 waves find the row maxima (two
+// rows each), then take the chunks in turn
+template <bool VEC>
+__global__ __launch_bounds__(PREP_I8_NW * 64) void k_prep_a1_row(const float *__restrict__ x, int M, int K, int Kp,
+                                                                 uint8_t *__restrict__ xp, float *__restrict__ xpf) {
+    __shared__ float invs[32], sxs[32];
+    const int G = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int RPW = 32 / PREP_I8_NW;
+    for (int rr = 0; rr < RPW; rr++) {
+        const int m = 32 * G + RPW * wave + rr;
+        float amax = 0.0f;
+        if (m < M) {
+            const float *row = x + (size_t)m * K;
+#pragma unroll 4
+            for (int j = lane; j < K; j += 64) amax = fmaxf(amax, fabsf(row[j]));
+        }
+        for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+        if (lane == 0) {
+            invs[RPW * wave + rr] = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+            sxs[RPW * wave + rr] = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 0.0f;
+        }
+    }
+    __syncthreads();
+    const int r = lane & 31, hh = lane >> 5, m = 32 * G + r;
+    const float inv = invs[r], sx = sxs[r];
+    const bool live = m < M && inv > 0.0f;
+    const float *row = x + (size_t)(m < M ? m : 0) * K;
+    const int Kc = Kp / 128;
+    for (int c = wave; c < Kc; c += PREP_I8_NW) {
+        int q[HSTEPS][8];
+#pragma unroll
+        for (int u = 0; u < HSTEPS; u++) {
+            float v[8];
+            load8<VEC>(row, live, K, 128 * c + 16 * u + 8 * hh, v);
+#pragma unroll
+            for (int j = 0; j < 8; j++) q[u][j] = (live && 128 * c + 16 * u + 8 * hh + j < K) ? act_q8(v[j], inv) : 0;
+        }
+        float s8[HSTEPS];
+        a1_store(xp, G, Kc, c, lane, q, s8);
+        if (hh == 0) xpf[((size_t)G * Kc + c) * 32 + r] = sx;
+    }
+}
+
 // 4 waves per workgroup, one 32-column group each, WM row groups per wave.
 template <int QT, int WM>
 __global__ __launch_bounds__(256) void k_gemm_i8(DevW W, const uint8_t *__restrict__ qx,
@@ -1381,9 +1557,9 @@ size_t mh_gemm_ws_floats(const DevW &W, int M, int jobs) {
     return (size_t)Kc * outs;
 }
 
-template <int QT>
-static hipError_t gemm_t(const GemmJobs &J, const uint8_t *xp, const float *xs16, const float *xpf, int M,
-                         int act, const PrepOut *po, float *ws, hipStream_t st) {
+template <int QT, bool A1>
+static hipError_t gemm_launch(const GemmJobs &J, const uint8_t *xp, const float *xs16, const float *xpf, int M,
+                              int act, const PrepOut *po, float *ws, hipStream_t st) {
     const DevW &W = J.W[0];
     const int mpad = mh_mpad(M);
     if (mpad % 64 != 0 || W.Np % 128 != 0 || J.n < 1 || J.n > 3) return hipErrorInvalidValue;
@@ -1391,23 +1567,41 @@ static hipError_t gemm_t(const GemmJobs &J, const uint8_t *xp, const float *xs16
         if (J.W[i].Np != W.Np || J.W[i].Kp != W.Kp || J.W[i].n != W.n) return hipErrorInvalidValue;
     const int tilesM = mpad / 64, tilesN = W.Np / 128, grid = J.n * tilesM * tilesN;
     if (po) {
-        if (po->Kc != tilesN || J.n != 1) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_gemm<QT, EPI_PREP>), dim3(grid), dim3(256), 0, st, J, xp, (const uint8_t *)xs16, xpf, M,
-                           1, tilesM, tilesN, *po, nullptr, 1);
-        return hipGetLastError();
+        if constexpr (A1) {
+            return hipErrorInvalidValue;
+        } else {
+            if (po->Kc != tilesN || J.n != 1) return hipErrorInvalidValue;
+            hipLaunchKernelGGL((k_gemm<QT, EPI_PREP>), dim3(grid), dim3(256), 0, st, J, xp, (const uint8_t *)xs16,
+                               xpf, M, 1, tilesM, tilesN, *po, nullptr, 1);
+            return hipGetLastError();
+        }
     }
     const int ks = ws ? gemm_ksplit(W.Kp / 128, grid, (size_t)J.n * mpad * W.Np) : 1;
     if (ks > 1) {
-        hipLaunchKernelGGL((k_gemm<QT, EPI_PART>), dim3(grid * ks), dim3(256), 0, st, J, xp, (const uint8_t *)xs16,
-                           xpf, M, act, tilesM, tilesN, PrepOut{}, ws, ks);
+        hipLaunchKernelGGL((k_gemm<QT, EPI_PART, A1>), dim3(grid * ks), dim3(256), 0, st, J, xp,
+                           (const uint8_t *)xs16, xpf, M, act, tilesM, tilesN, PrepOut{}, ws, ks);
         const int threads = M * (W.Np / 4);
         hipLaunchKernelGGL((k_gemm_fold<QT>), dim3((threads + 255) / 256, J.n), dim3(256), 0, st, J, (const float *)ws,
                            xpf, M, mpad, act);
     } else {
-        hipLaunchKernelGGL((k_gemm<QT, EPI_Y>), dim3(grid), dim3(256), 0, st, J, xp, (const uint8_t *)xs16, xpf, M,
-                           act, tilesM, tilesN, PrepOut{}, nullptr, 1);
+        hipLaunchKernelGGL((k_gemm<QT, EPI_Y, A1>), dim3(grid), dim3(256), 0, st, J, xp, (const uint8_t *)xs16, xpf,
+                           M, act, tilesM, tilesN, PrepOut{}, nullptr, 1);
     }
     return hipGetLastError();
+}
+
+// a1: the INT8ACT form (int8 activations from mh_launch_prep_a1); the qmat
+// formats INT8 / INT4 and f32 weights have none
+template <int QT>
+static hipError_t gemm_t(const GemmJobs &J, const uint8_t *xp, const float *xs16, const float *xpf, int M,
+                         int act, const PrepOut *po, float *ws, hipStream_t st, bool a1 = false) {
+    if constexpr (QT == QT_F32 || QT == QT_INT8 || QT == QT_INT4) {
+        if (a1) return hipErrorInvalidValue;
+        return gemm_launch<QT, false>(J, xp, xs16, xpf, M, act, po, ws, st);
+    } else {
+        if (a1) return gemm_launch<QT, true>(J, xp, xs16, xpf, M, act, po, ws, st);
+        return gemm_launch<QT, false>(J, xp, xs16, xpf, M, act, po, ws, st);
+    }
 }
 
 #define MH_DISPATCH(fn, qtype, ...)                                  \
@@ -1479,17 +1673,17 @@ hipError_t mh_launch_gemv(int qtype, const DevW &W, const float *x, int M, int v
 }
 
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
-                          const float *xpf, float *y, int M, int act, float *ws, hipStream_t st) {
+                          const float *xpf, float *y, int M, int act, float *ws, hipStream_t st, bool a1) {
     GemmJobs J{};
     J.W[0] = J.W[1] = J.W[2] = W;
     J.y[0] = J.y[1] = J.y[2] = y;
     J.n = 1;
-    MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, act, nullptr, ws, st)
+    MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, act, nullptr, ws, st, a1)
 }
 
 hipError_t mh_launch_gemm_jobs(int qtype, const GemmJobs &J, const uint8_t *xp, const float *xs16,
-                               const float *xpf, int M, float *ws, hipStream_t st) {
-    MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, 0, nullptr, ws, st)
+                               const float *xpf, int M, float *ws, hipStream_t st, bool a1) {
+    MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, 0, nullptr, ws, st, a1)
 }
 
 hipError_t mh_launch_gemm_prep_out(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
@@ -1527,8 +1721,33 @@ hipError_t mh_launch_dequant(int qtype, const DevW &W, float *out, hipStream_t s
     MH_DISPATCH(launch_dq, qtype, W, out, st)
 }
 
-bool mh_i8_supported(int qtype) {
-    return qtype == QT_INT8 || qtype == QT_INT4 || qtype == QT_Q8_0 || qtype == QT_Q4_0;
+bool mh_i8_supported(int qtype) { return qtype != QT_F32; }
+
+int mh_i8_kind(int qtype) {
+    if (qtype == QT_INT8 || qtype == QT_INT4) return MH_I8_QMAT;
+    if (qtype == QT_Q8_0 || qtype == QT_Q4_0) return MH_I8_ROW;
+    return MH_I8_SB;
+}
+
+hipError_t mh_launch_prep_a1(int kind, const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,
+                             float *xpf, int want_xsum, hipStream_t st) {
+    const bool vec = K % 8 == 0 && ((uintptr_t)x & 15) == 0;
+    if (kind == MH_I8_ROW) {
+        if (vec)
+            hipLaunchKernelGGL(k_prep_a1_row<true>, dim3(Mpad / 32), dim3(PREP_I8_NW * 64), 0, st, x, M, K, Kp, xp, xpf);
+        else
+            hipLaunchKernelGGL(k_prep_a1_row<false>, dim3(Mpad / 32), dim3(PREP_I8_NW * 64), 0, st, x, M, K, Kp, xp, xpf);
+    } else if (kind == MH_I8_SB) {
+        if (Kp % 256 != 0) return hipErrorInvalidValue;
+        const dim3 grid(Mpad / 32, Kp / 256);
+        if (vec)
+            hipLaunchKernelGGL(k_prep_a1_sb<true>, grid, dim3(64), 0, st, x, M, K, Kp, xp, (uint8_t *)xs16, xpf, want_xsum);
+        else
+            hipLaunchKernelGGL(k_prep_a1_sb<false>, grid, dim3(64), 0, st, x, M, K, Kp, xp, (uint8_t *)xs16, xpf, want_xsum);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 hipError_t mh_launch_prep_i8(const float *x, int M, int K, int Kp, int Mpad, uint8_t *qx, float *sx,

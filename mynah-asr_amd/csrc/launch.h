@@ -63,8 +63,9 @@ __host__ __device__ inline int mh_att_splits_dev(int n) { return (n + MH_ATT_KC 
 // to the workspace and a second launch folds them in chunk order (the same
 // bits as without). Calls sharing one workspace must be ordered on one stream.
 size_t mh_gemm_ws_floats(const DevW &W, int M, int jobs = 1);
+// a1: the INT8ACT form of the product, on activations prepared by mh_launch_prep_a1
 hipError_t mh_launch_gemm(int qtype, const DevW &W, const uint8_t *xp, const float *xs16,
-                          const float *xpf, float *y, int M, int act, float *ws, hipStream_t st);
+                          const float *xpf, float *y, int M, int act, float *ws, hipStream_t st, bool a1 = false);
 // up to three products (same shape) of one prepared input in one launch
 struct GemmJobs {
     DevW W[3];
@@ -73,7 +74,7 @@ struct GemmJobs {
 };
 // (ws: as for mh_launch_gemm, sized by mh_gemm_ws_floats(W, M, J.n), or null)
 hipError_t mh_launch_gemm_jobs(int qtype, const GemmJobs &J, const uint8_t *xp, const float *xs16,
-                               const float *xpf, int M, float *ws, hipStream_t st);
+                               const float *xpf, int M, float *ws, hipStream_t st, bool a1 = false);
 // The FFN's first product with SiLU, its output prepared as the input of a
 // product with Kp = 128 * oKc (oKc = the first product's column tiles):
 // (oxp, oxs16, oxpf) as mh_launch_prep would write them.
@@ -83,8 +84,20 @@ hipError_t mh_launch_gemm_prep_out(int qtype, const DevW &W, const uint8_t *xp, 
 hipError_t mh_launch_dequant(int qtype, const DevW &W, float *out, hipStream_t st);
 hipError_t mh_launch_silu(float *x, size_t n, hipStream_t st);
 
-// INT8ACT numerics (formats INT8, INT4, Q8_0, Q4_0)
+// INT8ACT numerics (every format but F32). Three activation forms:
+//   MH_I8_QMAT (INT8, INT4): int8 bytes for k_gemm_i8, one scale per row
+//     (mh_launch_prep_i8), the reference's qmat int8 path;
+//   MH_I8_ROW (Q8_0, Q4_0): int8 values as f16 for the A1 GEMM, one scale per
+//     row, quantized as the qmat path quantizes;
+//   MH_I8_SB (the K-quants): the same, one scale per 256-element super-block
+//     (ingot's int8-activation semantics).
+enum { MH_I8_QMAT = 1, MH_I8_ROW = 2, MH_I8_SB = 3 };
 bool mh_i8_supported(int qtype);
+int mh_i8_kind(int qtype);
+// xp: Mpad * Kp * 2 bytes; xpf: Mpad * Kp / 128 floats; xs16: the mins operand
+// (Mpad * Kp / 4 bytes) when want_xsum (MH_I8_SB only)
+hipError_t mh_launch_prep_a1(int kind, const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,
+                             float *xpf, int want_xsum, hipStream_t st);
 hipError_t mh_launch_prep_i8(const float *x, int M, int K, int Kp, int Mpad, uint8_t *qx, float *sx,
                              hipStream_t st);
 hipError_t mh_launch_gemm_i8(int qtype, const DevW &W, const uint8_t *qx, const float *sx, float *y, int M,

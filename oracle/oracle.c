@@ -586,33 +586,178 @@ void orc_qmat_int8_path(int qtype, const void *qv, const float *scales, int n, i
     free(qx);
 }
 
-void orc_block_int8_path(int type, const void *blocks, int n, int k, const float *x, int T,
-                         float *out, int32_t *int_sums) {
-    const int bb = type == ORC_Q8_0 ? 34 : 18;
-    const int G = k / 32;
-    int8_t *qx = (int8_t *)malloc((size_t)k);
-    const unsigned char *w = (const unsigned char *)blocks;
-    for (int t = 0; t < T; t++) {
-        const float sx = orc_act_quant_int8(x + (size_t)t * k, k, qx);
-        for (int r = 0; r < n; r++) {
-            float acc = 0.0f;
-            for (int g = 0; g < G; g++) {
-                const unsigned char *blk = w + ((size_t)r * G + g) * bb;
-                const float d = h2f(blk);
-                int64_t ib = 0;
-                for (int i = 0; i < 32; i++) {
-                    int qv;
-                    if (type == ORC_Q8_0) qv = (signed char)blk[2 + i];
-                    else qv = (i < 16 ? (blk[2 + i] & 15) : (blk[2 + i - 16] >> 4)) - 8;
-                    ib += (int64_t)qv * qx[32 * g + i];
-                }
-                if (int_sums) int_sums[((size_t)t * n + r) * G + g] = (int32_t)ib;
-                acc += (float)(int32_t)ib * d;
+/* ------------------------------------------ INT8ACT over ggml block formats
+ * Integer form of one K-quant super-block: quant q[e] (offsets applied, e.g.
+ * Q3_K q - 4*!hbit, Q6_K q - 32), sub-block factor f and min m of the
+ * sub-block holding e (16 elements for Q2_K, Q3_K, Q6_K; 32 for Q4_K, Q5_K),
+ * super-block factors d, dmin. The decoders above are these integers put
+ * together in f32: (d * f) * q - dmin * m (Q2_K, Q4_K, Q5_K), (d * f) * q
+ * (Q3_K, Q6_K); orc_kquant_ints returns them so that a test can rebuild the
+ * decoder's output from them bit for bit. */
+static int kq_sub(int type) { return (type == ORC_Q4_K || type == ORC_Q5_K) ? 32 : 16; }
+
+int orc_kquant_ints(int type, const void *block, int32_t *q, int32_t *f, int32_t *m, float *d, float *dmin) {
+    const unsigned char *s = (const unsigned char *)block;
+    switch (type) {
+    case ORC_Q2_K:
+        *d = h2f(s + 80), *dmin = h2f(s + 82);
+        for (int e = 0; e < 256; e++) {
+            const int h = e / 128, r = e % 128, fi = r / 32, l = r % 32;
+            q[e] = (s[16 + 32 * h + l] >> (2 * fi)) & 3;
+        }
+        for (int j = 0; j < 16; j++) f[j] = s[j] & 15, m[j] = s[j] >> 4;
+        return 0;
+    case ORC_Q3_K:
+        *d = h2f(s + 108), *dmin = 0.0f;
+        for (int e = 0; e < 256; e++) {
+            const int h = e / 128, r = e % 128, fi = r / 32, l = r % 32;
+            const int v = (s[32 + 32 * h + l] >> (2 * fi)) & 3;
+            q[e] = v - (((s[l] >> (4 * h + fi)) & 1) ? 0 : 4);
+        }
+        for (int j = 0; j < 16; j++) f[j] = q3k_scale(s + 96, j), m[j] = 0;
+        return 0;
+    case ORC_Q4_K:
+    case ORC_Q5_K: {
+        *d = h2f(s), *dmin = h2f(s + 2);
+        const unsigned char *qs = s + (type == ORC_Q4_K ? 16 : 48);
+        for (int j = 0; j < 8; j++) {
+            int sc, mn;
+            k4_sm(s + 4, j, &sc, &mn);
+            f[j] = sc, m[j] = mn;
+            for (int i = 0; i < 32; i++) {
+                int v = (j & 1) ? (qs[32 * (j / 2) + i] >> 4) : (qs[32 * (j / 2) + i] & 15);
+                if (type == ORC_Q5_K && ((s[16 + i] >> j) & 1)) v += 16;
+                q[32 * j + i] = v;
             }
-            out[(size_t)t * n + r] = acc * sx;
+        }
+        return 0;
+    }
+    case ORC_Q6_K:
+        *d = h2f(s + 208), *dmin = 0.0f;
+        for (int e = 0; e < 256; e++) {
+            const int h = e / 128, r = e % 128, fi = r / 32, l = r % 32;
+            const unsigned char lb = s[64 * h + 32 * (fi & 1) + l];
+            const int lo = (fi >= 2) ? (lb >> 4) : (lb & 15);
+            const int hi = (s[128 + 32 * h + l] >> (2 * fi)) & 3;
+            q[e] = (lo | (hi << 4)) - 32;
+        }
+        for (int j = 0; j < 16; j++) f[j] = (signed char)s[192 + j], m[j] = 0;
+        return 0;
+    }
+    return -1;
+}
+
+/* ingot's int8 activations for the K-quants (third_party/ingot/src/kernels.c:
+ * 719-750, q4_k_quantize_activation): per 256-element super-block, scale =
+ * amax/127, q = round-to-nearest-even(x * (127/amax)) saturated to int8
+ * (CVTPS2DQ and the saturating packs); an all-zero block gives q = 0, scale 0.
+ * Returns the scale. */
+float orc_act_quant_sb(const float *x, int8_t *qx) {
+    float amax = 0.0f;
+    for (int i = 0; i < 256; i++) if (fabsf(x[i]) > amax) amax = fabsf(x[i]);
+    if (!(amax > 0.0f)) { memset(qx, 0, 256); return 0.0f; }
+    const float inv = 127.0f / amax;
+    for (int i = 0; i < 256; i++) qx[i] = (int8_t)clampi((int)nearbyintf(x[i] * inv), -128, 127);
+    return amax / 127.0f;
+}
+
+/* INT8ACT over the ggml block formats, in the order the HIP unit evaluates it
+ * (this build's definition: the reference has an int8 path over ggml blocks
+ * only for Q4_K/Q5_K, kernels.c:1649-1795, whose f32 combine runs in another
+ * order; that path is the check against the reference, within its own budget).
+ * K is cut into chunks of 128 (4 blocks of 32, or half a super-block).
+ *   Q8_0 / Q4_0: activations per row as quantize_act_int8 (scale sx); per chunk
+ *     acc = 0, acc = fmaf(d_b, (float)t_b, acc) over its blocks, t_b = sum
+ *     q_w * q_x (exact); total = fmaf(sx, acc, total), chunks in order.
+ *   K-quants: activations per super-block (orc_act_quant_sb, scale s_B); per
+ *     chunk the exact integers A = sum_j f_j sum_{e in j} q_e qx_e and
+ *     Bm = sum_j m_j * xsum_j (xsum_j = sum of qx over sub-block j), then
+ *       Q2_K, Q4_K, Q5_K: acc = fmaf(-(32 dmin), (float)Bm / 32, d * (float)A)
+ *       Q3_K:             acc = d * (float)A
+ *       Q6_K:             acc = 0, acc = fmaf(d * f_j, (float)t_j, acc) over
+ *                         its 16-element sub-blocks j in order
+ *     ((float)A is exact: |A| < 2^24; for Q5_K A is the int32 sum of the
+ *     chunk's two 64-element halves, each below 2^24, converted once);
+ *     total = fmaf(s_B, acc, total), chunks in order.
+ * chunk_ints (optional) [T, n, k/128, 2] receives (A, Bm) of the K-quants. */
+void orc_int8act_blocks(int type, const void *blocks, int n, int k, const float *x, int T, float *out,
+                        int64_t *chunk_ints) {
+    int be, bb;
+    orc_geometry(type, &be, &bb);
+    const int nblk = k / be, Kc = (k + 127) / 128;
+    const unsigned char *w = (const unsigned char *)blocks;
+    int8_t *qx = (int8_t *)calloc((size_t)Kc * 128 + 256, 1);
+    float *xs = (float *)calloc((size_t)nblk + 1, sizeof(float));
+    int32_t qi[256], fi[16], mi[16];
+    for (int t = 0; t < T; t++) {
+        const float *xr = x + (size_t)t * k;
+        float sx = 0.0f;
+        if (be == 32) {
+            memset(qx, 0, (size_t)Kc * 128);
+            sx = orc_act_quant_int8(xr, k, qx);
+        } else {
+            for (int b = 0; b < nblk; b++) xs[b] = orc_act_quant_sb(xr + 256 * b, qx + 256 * b);
+        }
+        for (int r = 0; r < n; r++) {
+            const unsigned char *row = w + (size_t)r * nblk * bb;
+            float total = 0.0f;
+            if (be == 32) {
+                for (int c = 0; c < Kc; c++) {
+                    float acc = 0.0f;
+                    for (int b = 4 * c; b < 4 * c + 4 && b < nblk; b++) {
+                        const unsigned char *blk = row + (size_t)b * bb;
+                        const float d = h2f(blk);
+                        int64_t tb = 0;
+                        for (int i = 0; i < 32; i++) {
+                            const int qv = type == ORC_Q8_0 ? (signed char)blk[2 + i]
+                                                            : (i < 16 ? (blk[2 + i] & 15) : (blk[2 + i - 16] >> 4)) - 8;
+                            tb += (int64_t)qv * qx[32 * b + i];
+                        }
+                        acc = fmaf(d, (float)tb, acc);
+                    }
+                    total = fmaf(sx, acc, total);
+                }
+            } else {
+                const int sub = kq_sub(type);
+                float d = 0.0f, dmin = 0.0f;
+                for (int c = 0; c < Kc; c++) {
+                    const int B = c / 2, e0 = 128 * (c & 1);
+                    orc_kquant_ints(type, row + (size_t)B * bb, qi, fi, mi, &d, &dmin);
+                    const int8_t *xq = qx + 256 * B;
+                    float acc = 0.0f;
+                    if (type == ORC_Q6_K) {
+                        for (int j = e0 / 16; j < e0 / 16 + 8; j++) {
+                            int64_t tj = 0;
+                            for (int i = 16 * j; i < 16 * j + 16; i++) tj += (int64_t)qi[i] * xq[i];
+                            acc = fmaf(d * (float)fi[j], (float)tj, acc);
+                        }
+                    } else {
+                        int64_t A0 = 0, A1 = 0, Bm = 0;
+                        for (int e = e0; e < e0 + 128; e++) {
+                            const int64_t p = (int64_t)qi[e] * fi[e / sub] * xq[e];
+                            if (e < e0 + 64) A0 += p; else A1 += p;
+                        }
+                        for (int j = e0 / sub; j < (e0 + 128) / sub; j++) {
+                            int64_t xsum = 0;
+                            for (int i = sub * j; i < sub * j + sub; i++) xsum += xq[i];
+                            Bm += (int64_t)mi[j] * xsum;
+                        }
+                        const float Af = type == ORC_Q5_K ? (float)(int32_t)(A0 + A1) : (float)(A0 + A1);
+                        if (type == ORC_Q3_K) acc = d * Af;
+                        else acc = fmaf(-(dmin * 32.0f), (float)((double)Bm / 32.0), d * Af);
+                        if (chunk_ints) {
+                            chunk_ints[(((size_t)t * n + r) * Kc + c) * 2] = A0 + A1;
+                            chunk_ints[(((size_t)t * n + r) * Kc + c) * 2 + 1] = Bm;
+                        }
+                    }
+                    total = fmaf(xs[B], acc, total);
+                }
+            }
+            out[(size_t)t * n + r] = total;
         }
     }
     free(qx);
+    free(xs);
 }
 
 /* ---------------------------------------------------- double reference GEMM
@@ -651,4 +796,42 @@ void orc_gemm_f64(const float *x, const float *wd, int T, int n, int k, double *
         pthread_create(&tid[i], NULL, gemm_rows, &job[i]);
     }
     for (int i = 0; i < threads; i++) pthread_join(tid[i], NULL);
+}
+
+/* ----------------------------------------- a thread pool for oracle/_ref
+ * ingot runs its row loops through a parallel_for its host installs
+ * (ingot_set_parallel_for, third_party/ingot/src/cpu.c:217-230; serial by
+ * default). For timing the reference's CPU kernels on all host cores, this
+ * installs one that splits [0, count) into `threads` contiguous ranges, each
+ * on its own thread. */
+typedef void (*orc_range_fn)(size_t begin, size_t end, void *user);
+typedef void (*orc_set_pf_fn)(void (*)(size_t, orc_range_fn, void *));
+static int g_pool_threads = 1;
+typedef struct { orc_range_fn fn; void *user; size_t b, e; } orc_range_job;
+static void *orc_range_run(void *a) {
+    const orc_range_job *j = (const orc_range_job *)a;
+    if (j->b < j->e) j->fn(j->b, j->e, j->user);
+    return NULL;
+}
+static void orc_parallel_for(size_t count, orc_range_fn fn, void *user) {
+    int nt = g_pool_threads;
+    if ((size_t)nt > count) nt = (int)count;
+    if (nt <= 1) { if (count) fn(0, count, user); return; }
+    pthread_t th[256];
+    orc_range_job jobs[256];
+    if (nt > 256) nt = 256;
+    for (int i = 0; i < nt; i++) {
+        jobs[i].fn = fn, jobs[i].user = user;
+        jobs[i].b = count * (size_t)i / (size_t)nt, jobs[i].e = count * (size_t)(i + 1) / (size_t)nt;
+    }
+    int started = 1;
+    for (int i = 1; i < nt; i++, started++)
+        if (pthread_create(&th[i], NULL, orc_range_run, &jobs[i]) != 0) break;
+    orc_range_run(&jobs[0]);
+    for (int i = started; i < nt; i++) orc_range_run(&jobs[i]);   /* any thread that did not start */
+    for (int i = 1; i < started; i++) pthread_join(th[i], NULL);
+}
+void orc_ingot_install_pool(void *set_parallel_for, int threads) {
+    g_pool_threads = threads < 1 ? 1 : threads;
+    ((orc_set_pf_fn)set_parallel_for)(orc_parallel_for);
 }

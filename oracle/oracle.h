@@ -51,15 +51,22 @@ float orc_act_quant_int8(const float *x, int k, int8_t *qx);
 void orc_qmat_int8_path(int qtype, const void *q, const float *scales, int n, int k,
                         const float *x, int T, float *out, int32_t *int_sums);
 
-/* int8-activation product over 32-element ggml blocks (Q8_0, Q4_0), the
- * semantics the HIP int8 mode defines for them: per block ib = sum q_w*q_x
- * (exact int32), acc = acc + (float)ib * d (two roundings, blocks in order),
- * out = acc * sx. int_sums (optional) [T, n, k/32]. */
-void orc_block_int8_path(int type, const void *blocks, int n, int k, const float *x, int T,
-                         float *out, int32_t *int_sums);
+/* K-quant super-block as integers (quants with offsets, sub-block factors
+ * and mins, d, dmin); 0 or -1 for other types */
+int orc_kquant_ints(int type, const void *block, int32_t *q, int32_t *f, int32_t *m, float *d, float *dmin);
+/* ingot's per-super-block int8 activation quantizer (256 values); returns the scale */
+float orc_act_quant_sb(const float *x, int8_t *qx);
+/* INT8ACT over ggml blocks in the HIP unit's evaluation order (see oracle.c);
+ * chunk_ints (optional) [T, n, k/128, 2] = the K-quants' exact chunk integers */
+void orc_int8act_blocks(int type, const void *blocks, int n, int k, const float *x, int T, float *out,
+                        int64_t *chunk_ints);
 
 /* out[T, n] = x[T, k] . wd[n, k]^T accumulated in double (threads: 0 = all) */
 void orc_gemm_f64(const float *x, const float *wd, int T, int n, int k, double *out,
                   int threads);
+
+/* install a pthread parallel_for of `threads` ranges into an ingot build
+ * (set_parallel_for = that library's ingot_set_parallel_for) */
+void orc_ingot_install_pool(void *set_parallel_for, int threads);
 
 #endif

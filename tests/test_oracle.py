@@ -182,27 +182,6 @@ def test_int8_path_sums_brute(orc, qtype):
                     assert sums[t, r, g] == int((vals[32 * g:32 * g + 32] * qx[32 * g:32 * g + 32]).sum())
 
 
-def test_block_int8_path_sums_brute(orc):
-    rng = np.random.default_rng(12)
-    n, k, T = 4, 128, 2
-    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
-    x = rng.standard_normal((T, k)).astype(np.float32)
-    for t in (O.Q8_0, O.Q4_0):
-        raw = orc.quantize(t, w.ravel())
-        _, sums = orc.block_int8_path(t, raw, n, k, x)
-        wd = orc.dequant(t, raw, n * k).reshape(n, k)
-        d = np.repeat(np.array([raw.reshape(n, k // 32, -1)[r, b, :2].view(np.float16)[0]
-                                for r in range(n) for b in range(k // 32)],
-                               dtype=np.float32).reshape(n, k // 32), 32, axis=1)
-        qw = np.rint(np.where(d != 0, wd / np.where(d != 0, d, 1), 0)).astype(np.int64)
-        for tt in range(T):
-            qx, _ = orc.act_quant_int8(x[tt])
-            for r in range(n):
-                for g in range(k // 32):
-                    sl = slice(32 * g, 32 * g + 32)
-                    assert sums[tt, r, g] == int((qw[r, sl] * qx[sl].astype(np.int64)).sum())
-
-
 def test_gemm_f64_closed_forms(orc):
     rng = np.random.default_rng(1)
     x = rng.standard_normal((6, 40)).astype(np.float32)
