@@ -408,22 +408,37 @@ def run_aed(B, M_, d=1024, H=8, ffn=4096, vocab=16384, n_layers=4, T=750, cap=64
             "note": "host wall clock around one call (graph capture, cross K/V products and copies included)"}
 
 
-def profiled_traffic():
-    """HBM bytes per launch of the roofline kernel, as measured by the two
-    rocprofv3 --pmc passes recorded under profiles/ (None if absent)."""
-    path = os.path.join(ROOT, "profiles", "gemm_q8_0_4096to1024_m6000_traffic.md")
+COUNTERS = os.path.join(ROOT, "profiles", "counters_q8_0_gemm_and_gemv.md")
+
+
+def profiled_counters() -> dict:
+    """Per-kernel counter figures recorded by the rocprofv3 --pmc passes under
+    profiles/ (MFMA busy %, useful MFMA %, HBM MB read / written per launch,
+    GB/s): {name: {field: value}}; {} if absent."""
+    out = {}
     try:
-        for line in open(path):
-            if "traffic_bytes_per_launch:" in line:
-                return int(line.split("traffic_bytes_per_launch:")[1].split()[0])
+        for line in open(COUNTERS):
+            if line.startswith("counter ") and ":" in line:
+                name, rest = line[len("counter "):].split(":", 1)
+                out[name.strip()] = {k: float(v) for k, v in (f.split("=") for f in rest.split())}
     except OSError:
         pass
-    return None
+    return out
+
+
+def profiled_traffic():
+    """HBM bytes per launch of the roofline kernel (ffn2), from the counters."""
+    c = profiled_counters().get("ffn2")
+    return int((c["hbm_read_mb"] + c["hbm_write_mb"]) * 1e6) if c else None
 
 
 def run_profile(B, M_):
-    """Copy of known size (calibrates FETCH_SIZE / WRITE_SIZE), then the
-    dominant kernel alone on a prepared input."""
+    """Counter runs for rocprofv3 --pmc: a 256 MiB device copy (calibrates
+    FETCH_SIZE / WRITE_SIZE), then each kernel the bench line reports, three
+    launches each on inputs prepared once: the EXACT Q8_0 products at M = 6000
+    (1024->4096, 4096->1024, 1024->1024), the INT8ACT Q4_K 4096->1024 product at
+    M = 12000, and the decoder GEMVs (Q8_0, M = 1: 1024->16384, 4096->1024
+    split K, 1024->1024) over rotating weight copies."""
     torch, lib = B.torch, B.lib
     src = torch.empty(64 << 20, dtype=torch.float32, device="cuda").fill_(1.0)
     dst = torch.empty_like(src)
@@ -431,15 +446,31 @@ def run_profile(B, M_):
         for _ in range(3):
             dst.copy_(src)
     B.sync()
-    k, n, M = 4096, 1024, 6000
-    w = M_.Weight.make(lib, M_.Q8_0, lib.randn(1, 0.02, (n, k)))
-    dw = M_.DeviceWeight(lib, w)
-    x, y = B.dev(lib.randn(1, 1.0, (M, k))), B.empty(M, n)
-    dw.prep(x.data_ptr(), M, B.sp)
-    for _ in range(3):
-        dw.gemm_prepped(y.data_ptr(), M, 0, B.sp)
-    B.sync()
-    log("[bench] profile run: copy 256 MiB x3, Q8_0 4096->1024 M=6000 x3")
+    del src, dst
+    for qt, k, n, M, num in ((M_.Q8_0, 1024, 4096, 6000, 0), (M_.Q8_0, 4096, 1024, 6000, 0),
+                             (M_.Q8_0, 1024, 1024, 6000, 0), (M_.Q4_K, 4096, 1024, 12000, 1)):
+        lib.set_numerics(num)
+        try:
+            dw = M_.DeviceWeight(lib, M_.Weight.make(lib, qt, lib.randn(1, 0.02, (n, k))))
+            x, y = B.dev(lib.randn(1, 1.0, (M, k))), B.empty(M, n)
+            dw.prep(x.data_ptr(), M, B.sp)
+            for _ in range(3):
+                dw.gemm_prepped(y.data_ptr(), M, 0, B.sp)
+            B.sync()
+            dw.close()
+        finally:
+            lib.set_numerics(0)
+        log(f"[bench] profile: {M_.NAMES[qt]} {k}->{n} M={M} numerics={num} x3")
+    for k, n in ((1024, 16384), (4096, 1024), (1024, 1024)):
+        w = M_.Weight.make(lib, M_.Q8_0, lib.randn(0, 0.02, (n, k)))
+        dws = [M_.DeviceWeight(lib, w) for _ in range(3)]
+        x, y = B.dev(lib.randn(1, 1.0, (1, k))), B.empty(1, n)
+        for dw in dws:
+            dw.gemm(x.data_ptr(), y.data_ptr(), 1, 0, B.sp)
+        B.sync()
+        for dw in dws:
+            dw.close()
+        log(f"[bench] profile: GEMV Q8_0 {k}->{n} M=1 x3")
 
 
 def main():
@@ -459,8 +490,8 @@ def main():
     ap.add_argument("--int8act", action="store_true",
                     help="only the INT8ACT layer sets (Q8_0 M=6000, Q4_K and Q5_K M=12000), one JSON line")
     ap.add_argument("--profile", action="store_true",
-                    help="counter-calibration run for rocprofv3 --pmc: a 256 MiB device copy, then "
-                         "the dominant GEMM (Q8_0 4096->1024, M=6000) alone, 3 launches each")
+                    help="counter run for rocprofv3 --pmc: a 256 MiB device copy, then each kernel the "
+                         "bench line reports (GEMMs and decoder GEMVs), 3 launches each")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are out of scope "
@@ -495,15 +526,22 @@ def main():
     ms_step, flops, rows = run_encoder_set(B, M_, M_.Q8_0, M, ENC_SHAPES, args.steps, args.warmup, 0)
     value = flops / (ms_step * 1e-3) / 1e12
     # the roofline entry follows the 4096->1024 product: with 1024->4096 the
-    # longest launch of the step, and the one whose HBM traffic is measured
-    # under profiles/ (gemm_q8_0_4096to1024_m6000_traffic.md)
+    # longest launch of the step; its HBM traffic and MFMA busy fraction are
+    # measured under profiles/ (counters_q8_0_gemm_and_gemv.md)
     dom = next(r for r in rows if r["gemm"] == "ffn2")
     dom_flops = 2.0 * M * dom["n"] * dom["k"]
     achieved = dom_flops / (dom["kernel_us"] * 1e-6) / 1e12
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP16, 4), "traffic": profiled_traffic(),
                 "kernel": f"k_gemm<Q8_0> {dom['gemm']} {dom['k']}->{dom['n']} M={M}"}
-    details = {"encoder_q8_0_m6000": rows}
+    counters = profiled_counters()
+    for r in rows:
+        c = counters.get("qkvo" if r["gemm"] in ("q", "k", "v", "out", "pos") else r["gemm"])
+        if c:
+            r["counter_mfma_busy_pct"], r["counter_useful_mfma_pct"] = c["mfma_util"], c["useful_mfma"]
+    details = {"encoder_q8_0_m6000": rows, "counters": {
+        "source": "profiles/counters_q8_0_gemm_and_gemv.md (rocprofv3 --pmc passes over bench.py --profile)",
+        "kernels": counters}}
 
     if not args.no_extras:
         kq = {}
