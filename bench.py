@@ -183,6 +183,86 @@ def run_int8act(B, M_, M):
     return out
 
 
+def run_config5(B, M_, reps=3):
+    """The parts of one FastConformer-0.6B encoder layer this build runs, at
+    benchmark config 5's batch (16 segments x 750 frames = 12000 rows, d 1024,
+    FFN 4096, 8 heads; src/encoder.c:901-946 for the layer's order), Q8_0
+    weights, EXACT numerics, one stream: the two macaron FFNs (qffn_dev),
+    q/k/v (qqkv_dev), the attention output projection, the pos projection
+    (2T-1 = 1499 rows of the sinusoidal table: the reference forms it per
+    segment, 16 x 1499 rows; one product over the 1499 shared rows gives the
+    same values), the relative-position attention core over the 16 segments,
+    and the conv module's pointwise convolutions (1024->2048 before the GLU,
+    1024->1024 after). Not built here: layer norms, GLU, depthwise conv, batch
+    norm, residual adds, subsampling. Each call is timed with HIP events on the
+    stream (preparation included); the layer's time is their sum, the
+    forward's 24 times that; RTF over 16 x 60 s of audio."""
+    torch, lib = B.torch, B.lib
+    Mr, T, nseq, d, H = 12000, 750, 16, 1024, 8
+    mk = lambda seed, n, k: M_.DeviceWeight(lib, M_.Weight.make(lib, M_.Q8_0, lib.randn(seed, 0.02, (n, k))))
+    W = {"ffa1": mk(500, 4096, d), "ffa2": mk(501, d, 4096), "ffb1": mk(502, 4096, d), "ffb2": mk(503, d, 4096),
+         "q": mk(504, d, d), "k": mk(505, d, d), "v": mk(506, d, d), "out": mk(507, d, d), "pos": mk(508, d, d),
+         "pw1": mk(509, 2 * d, d), "pw2": mk(510, d, d)}
+    x = B.dev(lib.randn(511, 1.0, (Mr, d)))
+    pe = B.dev(lib.randn(512, 1.0, (2 * T - 1, d)))
+    y, q, kk, v, ctx = (B.empty(Mr, d) for _ in range(5))
+    rk = B.empty(2 * T - 1, d)
+    y2 = B.empty(Mr, 2 * d)
+    bu, bv = B.dev(lib.randn(513, 0.1, (d,))), B.dev(lib.randn(514, 0.1, (d,)))
+    sp = B.sp
+    steps = [
+        ("ffn_a (1024->4096->1024)", 2 * Mr * 2 * 4096 * d,
+         lambda: M_.ffn_dev(lib, W["ffa1"], W["ffa2"], x.data_ptr(), y.data_ptr(), Mr, sp)),
+        ("q/k/v (3 x 1024->1024)", 3 * 2 * Mr * d * d,
+         lambda: M_.qkv_dev(lib, [W["q"], W["k"], W["v"]], x.data_ptr(), [q.data_ptr(), kk.data_ptr(), v.data_ptr()],
+                            Mr, sp)),
+        ("pos (1499 x 1024->1024)", 2 * (2 * T - 1) * d * d,
+         lambda: W["pos"].gemm(pe.data_ptr(), rk.data_ptr(), 2 * T - 1, 0, sp)),
+        ("rel-pos attention core (16 x 750)", attn_flops(T, H, d // H, -1, 0, nseq),
+         lambda: M_.relpos_attention_dev(lib, q.data_ptr(), kk.data_ptr(), v.data_ptr(), rk.data_ptr(), bu.data_ptr(),
+                                         bv.data_ptr(), ctx.data_ptr(), T, d, H, -1, 0, nseq, sp)),
+        ("out (1024->1024)", 2 * Mr * d * d, lambda: W["out"].gemm(ctx.data_ptr(), y.data_ptr(), Mr, 0, sp)),
+        ("conv pw1 (1024->2048)", 2 * Mr * 2 * d * d, lambda: W["pw1"].gemm(x.data_ptr(), y2.data_ptr(), Mr, 0, sp)),
+        ("conv pw2 (1024->1024)", 2 * Mr * d * d, lambda: W["pw2"].gemm(x.data_ptr(), y.data_ptr(), Mr, 0, sp)),
+        ("ffn_b (1024->4096->1024)", 2 * Mr * 2 * 4096 * d,
+         lambda: M_.ffn_dev(lib, W["ffb1"], W["ffb2"], x.data_ptr(), y.data_ptr(), Mr, sp)),
+    ]
+    for _, _, f in steps:
+        f()
+    B.sync()
+    rows, total = [], 0.0
+    for name, fl, f in steps:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(B.stream)
+        for _ in range(reps):
+            f()
+        e1.record(B.stream)
+        B.sync()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        total += us
+        peak = PEAK_FP32 if "attention" in name else PEAK_FP16
+        rows.append({"step": name, "us": round(us, 1), "gflop": round(fl / 1e9, 1),
+                     "tflops": round(fl / us / 1e6, 1), "mfma_frac": round(fl / us / 1e6 / peak, 4),
+                     "peak": "fp32 MFMA 157.3" if "attention" in name else "f16 MFMA 2500"})
+    # the whole layer as one back-to-back sequence
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(B.stream)
+    for _ in range(reps):
+        for _, _, f in steps:
+            f()
+    e1.record(B.stream)
+    B.sync()
+    seq_us = e0.elapsed_time(e1) / reps * 1e3
+    for w in W.values():
+        w.close()
+    fwd_ms = 24 * seq_us / 1e3
+    return {"rows": Mr, "segments": nseq, "frames": T, "layers": 24, "format": "Q8_0", "numerics": "EXACT",
+            "steps": rows, "layer_us_sum_of_steps": round(total, 1), "layer_us_sequence": round(seq_us, 1),
+            "forward_ms_built_parts": round(fwd_ms, 2), "rtf_built_parts": float(f"{fwd_ms / 1e3 / 960.0:.3g}"),
+            "note": "linears + pos projection + attention core of 24 layers only (layer norms, GLU, depthwise "
+                    "conv, batch norm, residuals and subsampling are outside this build); RTF over 960 s of audio"}
+
+
 def run_gemv(B, M_, qt, n, k, Ms, min_bytes=512 << 20, max_copies=512):
     lib = B.lib
     w = M_.Weight.make(lib, qt, lib.randn(0, 0.02, (n, k)))
@@ -237,12 +317,54 @@ def run_gemv(B, M_, qt, n, k, Ms, min_bytes=512 << 20, max_copies=512):
     return out
 
 
+def host_cpu() -> dict:
+    """The host's CPU model, the logical CPUs this process may use, and the
+    physical cores among them (from /proc/cpuinfo)."""
+    model, cores, allowed = "unknown", set(), sorted(os.sched_getaffinity(0))
+    try:
+        phys = core = proc = None
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "processor":
+                proc = int(v)
+            elif k == "model name":
+                model = v
+            elif k == "physical id":
+                phys = v
+            elif k == "core id":
+                core = v
+                if proc in allowed:
+                    cores.add((phys, core))
+    except OSError:
+        pass
+    return {"model": model, "logical_cpus": len(allowed), "physical_cores": len(cores) or None}
+
+
+def _median_time(fn, budget_s, max_reps=5, min_reps=1):
+    t_all, start = [], time.perf_counter()
+    while len(t_all) < max_reps and (len(t_all) < min_reps or time.perf_counter() - start < budget_s):
+        t0 = time.perf_counter()
+        fn()
+        t_all.append(time.perf_counter() - t0)
+    return float(np.median(t_all)), len(t_all)
+
+
 def cpu_baseline(M_, lib, seconds_budget=20.0):
-    """The reference CPU path for Q8_0 weights: ingot decodes the blocks to f32
-    once (src/weights.c:103-114; here oracle/_ref, the reference's ingot
-    sources compiled unmodified, or the oracle's restatement when _ref is
-    absent), then every product is cblas_sgemm (src/backend.c:79; here the
-    OpenBLAS numpy links). Timed on a bounded sample of the same step."""
+    """The reference CPU path on this host's cores, on bounded samples of the
+    benchmark's workloads. `value`: the Q8_0 encoder set at M = 6000 as the
+    reference runs GGUF weights: ingot decodes the blocks to f32 once
+    (src/weights.c:103-114; oracle/_ref is the reference's ingot sources
+    compiled unmodified, or the oracle's restatement when _ref is absent),
+    then every product is cblas_sgemm (src/backend.c:79; numpy's OpenBLAS).
+    `variants`: the same at one thread; qmat's INT8 large-T default (per-call
+    dequant + sgemm, src/qmat.c:644-650) at config 1; the reference's own
+    SIMD CPU GEMMs straight off the blocks (ingot_q8_0_matmat,
+    ingot_q4_k_matmat_exact, and the int8-activation ingot_q4_k_matmat,
+    third_party/ingot/src/kernels.c:1758-1795, 2392-2400; built with its x86
+    SIMD flags) at config 1; and the decoder GEMVs (config 3, M = 1) as the
+    reference runs them (f32 weights through sgemv) and through ingot's Q8_0
+    matvec, with the AED step's linears summed."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     kind = "reference"
@@ -253,17 +375,19 @@ def cpu_baseline(M_, lib, seconds_budget=20.0):
         dec = O.Oracle()
         kind = "port"
         decoder = "oracle restatement of ingot dequant"
+    host = host_cpu()
     try:
         from threadpoolctl import threadpool_info, threadpool_limits
         threads = max([i.get("num_threads", 1) for i in threadpool_info()
                        if i.get("user_api") == "blas"] or [1])
     except Exception:
         threadpool_limits = None
-        threads = os.cpu_count()
+        threads = host["logical_cpus"]
     M = 6000
-    wd = {}
+    wd, raws = {}, {}
     for i, (name, k, n) in enumerate(ENC_SHAPES):
         raw = lib.quantize(M_.Q8_0, lib.randn(i, 0.02, (n, k)))
+        raws[name] = raw
         wd[name] = dec.dequant(O.Q8_0, raw, n * k).reshape(n, k)
     xs = {k: lib.randn(1, 1.0, (M, k)) for k in (1024, 4096)}
 
@@ -271,21 +395,67 @@ def cpu_baseline(M_, lib, seconds_budget=20.0):
         for name, k, n in ENC_SHAPES:
             np.matmul(xs[k][:rows], wd[name].T)
 
-    # bounded sample: whole steps at M = 6000 while within the budget
     step(750)  # warm the BLAS pool
-    t_all, reps = [], 0
-    start = time.perf_counter()
-    while reps < 5 and time.perf_counter() - start < seconds_budget:
-        t0 = time.perf_counter()
-        step(M)
-        t_all.append(time.perf_counter() - t0)
-        reps += 1
-    med = float(np.median(t_all))
     flops = sum(2.0 * M * n * k for _, k, n in ENC_SHAPES)
+    med, reps = _median_time(lambda: step(M), seconds_budget * 0.4)
+    variants = []
+    if threadpool_limits is not None:
+        with threadpool_limits(limits=1, user_api="blas"):
+            med1, _ = _median_time(lambda: step(M), 0.0, max_reps=1)
+        variants.append({"variant": "ingot dequant once + OpenBLAS sgemm, encoder set M=6000", "threads": 1,
+                         "ms": round(med1 * 1e3, 1), "tops": round(flops / med1 / 1e12, 4)})
+    # config 1: Q8_0 M=750, 1024 -> 4096
+    c1x = xs[1024][:750]
+    c1f = 2.0 * 750 * 4096 * 1024
+    raw1, wd1 = raws["ffn1"], wd["ffn1"]
+    q8, s8 = O.Oracle().qmat_quantize_int8(wd1)
+    orc = O.Oracle()
+
+    def qmat_default():   # qmat.c:644-650: dequant_row per call (one thread), then sgemm
+        np.matmul(c1x, orc.qmat_dequant(1, q8, s8, 4096, 1024).T)
+
+    t, _ = _median_time(qmat_default, 2.0, max_reps=3)
+    variants.append({"variant": "qmat INT8 per-call dequant + OpenBLAS sgemm (qmat.c:644-650), config 1 M=750 "
+                                "1024->4096 (dequant: oracle restatement, one thread)", "threads": int(threads),
+                     "kind": "port", "ms": round(t * 1e3, 2), "gflops": round(c1f / t / 1e9, 1)})
+    gemv_cpu = []
+    if os.path.exists(O.REF_AVX2_PATH):
+        R = O.IngotRef(O.REF_AVX2_PATH)
+        R.set_threads(host["logical_cpus"])
+        raw4 = lib.quantize(M_.Q4_K, lib.randn(0, 0.02, (4096, 1024)))
+        for name, raw, label in (("ingot_q8_0_matmat", raw1, "Q8_0"), ("ingot_q4_k_matmat_exact", raw4, "Q4_K"),
+                                 ("ingot_q4_k_matmat", raw4, "Q4_K int8 activations")):
+            R.kernel(name, raw, 4096, 1024, c1x[:64])
+            t, _ = _median_time(lambda: R.kernel(name, raw, 4096, 1024, c1x), 3.0, max_reps=3)
+            variants.append({"variant": f"{name} ({label}), config 1 M=750 1024->4096", "kind": "reference",
+                             "threads": host["logical_cpus"], "ms": round(t * 1e3, 2),
+                             "gflops": round(c1f / t / 1e9, 1)})
+        # decoder GEMVs: M = 1 (ingot's Q8_0 matvec) and M = 4, 16 (its matmat)
+        for k, n in [(s[0], s[1]) for s in GEMV_SHAPES]:
+            raw = lib.quantize(M_.Q8_0, lib.randn(0, 0.02, (n, k)))
+            wf = dec.dequant(O.Q8_0, raw, n * k).reshape(n, k)
+            xg = lib.randn(1, 1.0, (16, k))
+            for Mg in (1, 4, 16):
+                t_s, _ = _median_time(lambda: np.matmul(xg[:Mg], wf.T), 0.3, max_reps=20, min_reps=5)
+                t_i, _ = _median_time(lambda: R.kernel("ingot_q8_0_matmat", raw, n, k, xg[:Mg]), 0.3, max_reps=20,
+                                      min_reps=5)
+                qb = M_.weight_bytes(M_.Q8_0, n, k) + 4.0 * Mg * (k + n)
+                gemv_cpu.append({"M": Mg, "k": k, "n": n, "sgemv_f32_us": round(t_s * 1e6, 1),
+                                 "ingot_q8_0_us": round(t_i * 1e6, 1),
+                                 "ingot_q8_0_gbps": round(qb / t_i / 1e9, 1)})
+    # the AED step's linears at M = 1 through sgemv (4 layers of 6 x 1024^2 +
+    # 1024x4096 + 4096x1024, then the 16384-row head): the CPU floor of a step
+    sg = {(g["k"], g["n"]): g["sgemv_f32_us"] for g in gemv_cpu if g["M"] == 1}
+    aed_us = None
+    if sg:
+        aed_us = round(4 * (6 * sg[(1024, 1024)] + sg[(1024, 4096)] + sg[(4096, 1024)]) + sg[(1024, 16384)], 1)
     return {"value": round(flops / med / 1e12, 4), "unit": "TOPS", "cores": int(threads),
-            "kind": kind,
+            "kind": kind, "host": host,
             "sample": f"{reps} whole steps (7 GEMMs at M=6000, median {med*1e3:.0f} ms): "
-                      f"{decoder} once + OpenBLAS sgemm per product, {threads} BLAS threads"}
+                      f"{decoder} once + OpenBLAS sgemm per product, {threads} BLAS threads on "
+                      f"{host['logical_cpus']} logical CPUs ({host['physical_cores']} physical cores) of {host['model']}",
+            "variants": variants, "gemv": gemv_cpu,
+            "aed_step_linears_sgemv_us": aed_us}
 
 
 PEAK_FP32 = 157.3  # TFLOP/s dense fp32 MFMA (MI355X)
@@ -489,6 +659,8 @@ def main():
                     help="only the AED decoder (config 3 shapes, 4 layers, T=750, Q8_0), one JSON line")
     ap.add_argument("--int8act", action="store_true",
                     help="only the INT8ACT layer sets (Q8_0 M=6000, Q4_K and Q5_K M=12000), one JSON line")
+    ap.add_argument("--config5", action="store_true",
+                    help="only the built parts of one encoder layer at config 5's batch (M=12000), one JSON line")
     ap.add_argument("--profile", action="store_true",
                     help="counter run for rocprofv3 --pmc: a 256 MiB device copy, then each kernel the "
                          "bench line reports (GEMMs and decoder GEMVs), 3 launches each")
@@ -520,6 +692,9 @@ def main():
         return
     if args.int8act:
         print(json.dumps(run_int8act(B, M_, M)), flush=True)
+        return
+    if args.config5:
+        print(json.dumps({"config5_layer": run_config5(B, M_)}), flush=True)
         return
 
     log("[bench] encoder set Q8_0 M=6000")
@@ -569,6 +744,8 @@ def main():
         details["gemv_hbm_frac_mean_large"] = round(float(np.mean([g["kernel_hbm_frac"] for g in big])), 4)
         log("[bench] few-row products (one stream)")
         details["gemm_small_m"] = run_small_m(B, M_)
+        log("[bench] config 5: one encoder layer's built parts at M=12000")
+        details["config5_layer"] = run_config5(B, M_)
 
     cpu = None
     if not args.no_cpu:
