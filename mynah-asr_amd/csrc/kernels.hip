@@ -365,7 +365,7 @@ template <int N> __device__ __forceinline__ void wait_vm() {
 // workgroup reads, for its 2 row groups and 4 column groups. Planes of 32 or
 // more bytes per lane and chunk stage the stage's own part; narrower ones the
 // whole (column group, chunk) block.
-template <int QT, bool A1 = false> struct StageLayout {
+template <int QT, bool A1 = false, int NCG = 4, int NRG = 2> struct StageLayout {
     using F = Fmt<QT>;
     static constexpr int SPS = QT == QT_F32 ? 1 : 2;              // ksteps per stage
     static constexpr int NST = KSTEPS / SPS;                      // stages per chunk
@@ -373,22 +373,26 @@ template <int QT, bool A1 = false> struct StageLayout {
     static constexpr int AR = SPS * 2048 * TERMS;                 // activation bytes per row group
     template <int B> static constexpr int plane() { return B == 0 ? 0 : (B >= 32 ? SPS * 16 * B : 64 * B); }
     template <int B> static __device__ int plane_off(int q) { return B >= 32 ? q * SPS * 16 * B : 0; }
-    static constexpr int A = 0;                                   // [2 rg][2 SPS u][TERMS][1 KiB]
+    static constexpr int A = 0;                                   // [NRG rg][2 SPS u][TERMS][1 KiB]
     static constexpr int B0S = plane<F::B0>(), B1S = plane<F::B1>();
-    static constexpr int P0 = A + 2 * AR;                         // [4 cg][B0S]
-    static constexpr int P1 = P0 + 4 * B0S;                       // [4 cg][B1S]
-    static constexpr int HB = P1 + 4 * B1S;                       // [4 cg][F::HB]
-    static constexpr int H2 = HB + 4 * F::HB;                     // [4 cg][F::H2]
-    static constexpr int PF = H2 + 4 * F::H2;                     // [2 rg][32 floats]
-    static constexpr int XS = PF + 2 * 128;                       // [2 rg][64 lanes][16 B] mins A operand
-    static constexpr int BYTES = XS + (F::MINS ? 2 * 1024 : 0);
+    static constexpr int P0 = A + NRG * AR;                       // [NCG cg][B0S]
+    static constexpr int P1 = P0 + NCG * B0S;                     // [NCG cg][B1S]
+    static constexpr int HB = P1 + NCG * B1S;                     // [NCG cg][F::HB]
+    static constexpr int H2 = HB + NCG * F::HB;                   // [NCG cg][F::H2]
+    static constexpr int PF = H2 + NCG * F::H2;                   // [NRG rg][32 floats]
+    static constexpr int XS = PF + NRG * 128;                     // [NRG rg][64 lanes][16 B] mins A operand
+    static constexpr int BYTES = XS + (F::MINS ? NRG * 1024 : 0);
 };
 
 // workgroups per CU the register budget is sized for: as many as the LDS
 // ring allows (three double-buffered workgroups: 25-27 KiB stages, 24 KiB
 // one-kstep stages for f32 weights), two for Q6_K (its eight per-half-step
 // f32 factors need more registers)
-template <int QT> constexpr int gemm_occ() { return QT == QT_Q6_K ? 2 : 3; }
+template <int QT, bool A1 = false, int WN = 1, int WM = 2> constexpr int gemm_occ() {
+    if (WN > 1) return 2;
+    if (WM == 1) return QT == QT_Q6_K ? 3 : 4;
+    return QT == QT_Q6_K ? 2 : 3;
+}
 
 // Where a product's result goes: EPI_Y stores y (SiLU applied when act);
 // EPI_PREP (the first product of the FFN) applies SiLU and, instead of
@@ -424,17 +428,22 @@ struct PrepOut {
 // A1: INT8ACT numerics (int8 activations as single f16 terms, xpf = their
 // scales); Q5_K then sums each chunk as two exact halves (its products reach
 // 127 * 1953, so a whole chunk could pass 2^24) joined in int32.
-template <int QT, int EPI, bool A1 = false>
-__global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const uint8_t *__restrict__ xp,
+// WN: column groups per wave (1: tile 64 x 128 per workgroup; 2: 64 x 256,
+// each wave 64 x 64, which halves the activation reads from LDS per MFMA).
+// WM: row groups per wave and workgroup (2: tiles of 64 rows; 1: of 32 rows,
+// twice the workgroups for products of few row bands).
+template <int QT, int EPI, bool A1 = false, int WN = 1, int WM = 2>
+__global__ __launch_bounds__(256, (gemm_occ<QT, A1, WN, WM>())) void k_gemm(GemmJobs J, const uint8_t *__restrict__ xp,
                                                  const uint8_t *__restrict__ xm,
                                                  const float *__restrict__ xpf,
                                                  int M, int act, int tilesM, int tilesN, PrepOut po,
-                                                 float *__restrict__ part, int ksplit) {
+                                                 float *__restrict__ part, int ksplit, int ngrp) {
     using F = Fmt<QT>;
-    using L = StageLayout<QT, A1>;
+    using L = StageLayout<QT, A1, 4 * WN, WM>;
     static_assert(!(A1 && EPI == EPI_PREP), "the fused FFN hand-off is EXACT only");
+    static_assert((WN == 1 && WM == 2) || EPI != EPI_PREP, "the fused FFN hand-off takes 64 x 128 tiles");
     constexpr bool HALVES = A1 && QT == QT_Q5_K;
-    constexpr int WM = 2, WN = 1;
+    constexpr int WPR = 4 / WM;   // waves copying one row group's activations
     __shared__ __attribute__((aligned(16))) uint8_t sbuf[2][L::BYTES];
     // XCD-aware tile order: workgroups are dealt to the 8 XCDs round-robin
     // (bid % 8), each XCD with its own L2. Give every XCD a contiguous run of
@@ -445,12 +454,28 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
     // of band tm are (job, column tile) pairs, so one XCD runs all of a band's
     // products and reads its activations into its L2 once.
     // With EPI_PART, a band's splits follow each other (band, split, tile).
+    // Without a K split, the order is N-group-major with ngrp groups of
+    // column tiles (ngrp divides nj * tilesN), band-major inside a group: an
+    // XCD's run then covers the bands of one group only, so the group's
+    // slice of the weights can stay in its L2 while the bands stream past
+    // (the host picks ngrp from the operand sizes; 1 = plain band-major).
     const int KS = EPI == EPI_PART ? ksplit : 1;
-    const int nj = J.n, ntiles = nj * tilesM * tilesN * KS, bid = blockIdx.x;
+    const int nj = J.n, nt = nj * tilesN, ntiles = nt * tilesM * KS, bid = blockIdx.x;
     const int q = ntiles / 8, rem = ntiles % 8, xcd = bid % 8, loc = bid / 8;
     const int t = xcd < rem ? xcd * (q + 1) + loc : rem * (q + 1) + (xcd - rem) * q + loc;
-    const int tm = t / (nj * tilesN * KS), ts = t - tm * nj * tilesN * KS;
-    const int ks = ts / (nj * tilesN), tr = ts - ks * nj * tilesN;
+    int tm, ks, tr;
+    if (EPI == EPI_PART) {
+        tm = t / (nt * KS);
+        const int ts = t - tm * nt * KS;
+        ks = ts / nt;
+        tr = ts - ks * nt;
+    } else {
+        const int ntg = nt / ngrp, per = tilesM * ntg;
+        const int g = t / per, r = t - g * per;
+        tm = r / ntg;
+        tr = g * ntg + (r - tm * ntg);
+        ks = 0;
+    }
     const int job = tr / tilesN, tn = tr - job * tilesN;
     const DevW W = job == 0 ? J.W[0] : (job == 1 ? J.W[1] : J.W[2]);
     float *__restrict__ y = job == 0 ? J.y[0] : (job == 1 ? J.y[1] : J.y[2]);
@@ -458,23 +483,27 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int hh = lane >> 5, col = lane & 31;
     const int Kc = W.Kp / 128;
-    const int G0 = tm * 2, GC0 = tn * 4;
+    const int G0 = tm * WM, GC0 = tn * 4 * WN;   // wave w: column groups GC0 + WN w + j
     const int cps = (Kc + KS - 1) / KS;
     const int c0 = EPI == EPI_PART ? ks * cps : 0, c1 = EPI == EPI_PART ? min(c0 + cps, Kc) : Kc;
 
     auto stage = [&](int c, int q, uint8_t *B) {
-        const int rg = wave >> 1, gc = GC0 + wave;
-        dma<L::AR / 2>(xp + (((size_t)(G0 + rg) * Kc + c) * 8 * L::TERMS + 2 * L::SPS * L::TERMS * q +
-                             L::SPS * L::TERMS * (wave & 1)) * 1024,
-                       B + L::A + rg * L::AR + (wave & 1) * (L::AR / 2), lane);
-        dma<L::B0S>(W.p0 + ((size_t)gc * Kc + c) * 64 * F::B0 + L::template plane_off<F::B0>(q),
-                    B + L::P0 + wave * L::B0S, lane);
-        if constexpr (F::B1 > 0)
-            dma<L::B1S>(W.p1 + ((size_t)gc * Kc + c) * 64 * F::B1 + L::template plane_off<F::B1>(q),
-                        B + L::P1 + wave * L::B1S, lane);
-        if constexpr (F::HB > 0) dma<F::HB>(F::hb_src(W, Kc, gc, c), B + L::HB + wave * F::HB, lane);
-        if constexpr (F::H2 > 0) dma<F::H2>(F::h2_src(W, Kc, gc, c), B + L::H2 + wave * F::H2, lane);
-        if (wave < 2) {
+        const int rg = wave / WPR, pw = wave % WPR;
+        dma<L::AR / WPR>(xp + (((size_t)(G0 + rg) * Kc + c) * 8 * L::TERMS + 2 * L::SPS * L::TERMS * q) * 1024 +
+                             (size_t)pw * (L::AR / WPR),
+                         B + L::A + rg * L::AR + pw * (L::AR / WPR), lane);
+#pragma unroll
+        for (int j = 0; j < WN; j++) {
+            const int gc = GC0 + WN * wave + j, slot = WN * wave + j;
+            dma<L::B0S>(W.p0 + ((size_t)gc * Kc + c) * 64 * F::B0 + L::template plane_off<F::B0>(q),
+                        B + L::P0 + slot * L::B0S, lane);
+            if constexpr (F::B1 > 0)
+                dma<L::B1S>(W.p1 + ((size_t)gc * Kc + c) * 64 * F::B1 + L::template plane_off<F::B1>(q),
+                            B + L::P1 + slot * L::B1S, lane);
+            if constexpr (F::HB > 0) dma<F::HB>(F::hb_src(W, Kc, gc, c), B + L::HB + slot * F::HB, lane);
+            if constexpr (F::H2 > 0) dma<F::H2>(F::h2_src(W, Kc, gc, c), B + L::H2 + slot * F::H2, lane);
+        }
+        if (wave < WM) {
             dma<128>((const uint8_t *)(xpf + ((size_t)(G0 + wave) * Kc + c) * 32), B + L::PF + wave * 128, lane);
             // the mins operand is read at the chunk's end, from its last stage
             if constexpr (F::MINS)
@@ -497,21 +526,28 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
                 }
             BK<QT, WN> b;
             // (one-kstep stages hold only kstep s: its local index is 0)
-            F::k_lds(B + L::P0 + wave * L::B0S, B + L::P1 + wave * L::B1S, L::SPS == 1 ? 0 : s, lane, b.r[0]);
+#pragma unroll
+            for (int j = 0; j < WN; j++)
+                F::k_lds(B + L::P0 + (WN * wave + j) * L::B0S, B + L::P1 + (WN * wave + j) * L::B1S,
+                         L::SPS == 1 ? 0 : s, lane, b.r[j]);
             kstep<QT, WM, WN, A1>(a, b, hd, s, acc);
         }
     };
 
     f16v total[WM][WN];
 #pragma unroll
-    for (int i = 0; i < WM; i++) total[i][0] = zero16();
+    for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int j = 0; j < WN; j++) total[i][j] = zero16();
     if (EPI != EPI_PART || c0 < c1) stage(c0, 0, sbuf[0]);
     for (int c = c0; c < c1; c++) {
         BH<QT, WN> hd;
         f16v acc[WM][WN];
-        int half0[HALVES ? WM : 1][HALVES ? 16 : 1];
+        int half0[HALVES ? WM : 1][HALVES ? WN : 1][HALVES ? 16 : 1];
 #pragma unroll
-        for (int i = 0; i < WM; i++) acc[i][0] = zero16();
+        for (int i = 0; i < WM; i++)
+#pragma unroll
+            for (int j = 0; j < WN; j++) acc[i][j] = zero16();
         // NST (even) stages per chunk, alternating buffers: stage 0 of every
         // chunk is in sbuf[0], the last in sbuf[1]
 #pragma unroll
@@ -524,10 +560,14 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
             else if (c + 1 < c1) stage(c + 1, 0, sbuf[0]);
             if (q == 0) {
                 // the chunk's factors, from its headers (staged with every stage)
-                if constexpr (fold_fmt<QT>())
-                    F::fhdr_lds(sbuf[0] + L::HB + wave * F::HB, sbuf[0] + L::H2 + wave * F::H2, c, lane, hd.h[0]);
-                else
-                    F::hdr_lds(sbuf[0] + L::HB + wave * F::HB, sbuf[0] + L::H2 + wave * F::H2, c, lane, hd.h[0]);
+#pragma unroll
+                for (int j = 0; j < WN; j++) {
+                    const int slot = WN * wave + j;
+                    if constexpr (fold_fmt<QT>())
+                        F::fhdr_lds(sbuf[0] + L::HB + slot * F::HB, sbuf[0] + L::H2 + slot * F::H2, c, lane, hd.h[j]);
+                    else
+                        F::hdr_lds(sbuf[0] + L::HB + slot * F::HB, sbuf[0] + L::H2 + slot * F::H2, c, lane, hd.h[j]);
+                }
             }
             compute(sbuf[q & 1], q, hd, acc);
             if constexpr (HALVES) {
@@ -535,10 +575,12 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
 #pragma unroll
                     for (int i = 0; i < WM; i++)
 #pragma unroll
-                        for (int e = 0; e < 16; e++) {
-                            half0[i][e] = (int)acc[i][0][e];
-                            acc[i][0][e] = 0.0f;
-                        }
+                        for (int j = 0; j < WN; j++)
+#pragma unroll
+                            for (int e = 0; e < 16; e++) {
+                                half0[i][j][e] = (int)acc[i][j][e];
+                                acc[i][j][e] = 0.0f;
+                            }
                 }
             }
         }
@@ -546,30 +588,38 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
 #pragma unroll
             for (int i = 0; i < WM; i++)
 #pragma unroll
-                for (int e = 0; e < 16; e++) acc[i][0][e] = (float)(half0[i][e] + (int)acc[i][0][e]);
+                for (int j = 0; j < WN; j++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) acc[i][j][e] = (float)(half0[i][j][e] + (int)acc[i][j][e]);
         }
         if constexpr (fold_fmt<QT>()) {
 #pragma unroll
             for (int i = 0; i < WM; i++) {
                 half8 xmv = {};
                 if constexpr (F::MINS) xmv = *(const half8 *)(sbuf[1] + L::XS + i * 1024 + lane * 16);
-                fold_finish<QT>(xmv, hd.h[0], acc[i][0]);
+#pragma unroll
+                for (int j = 0; j < WN; j++) fold_finish<QT>(xmv, hd.h[j], acc[i][j]);
             }
         }
         if constexpr (EPI == EPI_PART) {
-            const size_t Mp = (size_t)tilesM * 64;
-            float *pc = part + ((size_t)job * Kc + c) * Mp * W.Np + 32 * (GC0 + wave) + col;
+            const size_t Mp = (size_t)tilesM * 32 * WM;
 #pragma unroll
-            for (int i = 0; i < WM; i++)
+            for (int j = 0; j < WN; j++) {
+                float *pc = part + ((size_t)job * Kc + c) * Mp * W.Np + 32 * (GC0 + WN * wave + j) + col;
 #pragma unroll
-                for (int e = 0; e < 16; e++) pc[(size_t)(32 * (G0 + i) + drow(e, hh)) * W.Np] = acc[i][0][e];
+                for (int i = 0; i < WM; i++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) pc[(size_t)(32 * (G0 + i) + drow(e, hh)) * W.Np] = acc[i][j][e];
+            }
             continue;
         }
 #pragma unroll
         for (int i = 0; i < WM; i++) {
             const f16v pv = lds_rows16(sbuf[1] + L::PF + i * 128, hh);
 #pragma unroll
-            for (int e = 0; e < 16; e++) total[i][0][e] = __builtin_fmaf(pv[e], acc[i][0][e], total[i][0][e]);
+            for (int j = 0; j < WN; j++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) total[i][j][e] = __builtin_fmaf(pv[e], acc[i][j][e], total[i][j][e]);
         }
     }
     wait_vm<0>();
@@ -640,19 +690,22 @@ __global__ __launch_bounds__(256, gemm_occ<QT>()) void k_gemm(GemmJobs J, const 
         if (hh == 0 && uh == 0) po.xpf[((size_t)G * po.Kc + tn) * 32 + col] = ldexpf(1.0f, -sh);
         return;
     }
-    const int n = 32 * (GC0 + wave) + col;
-    if (n >= W.n) return;
-    const int shw = wshift<QT>(W, n);
 #pragma unroll
-    for (int i = 0; i < WM; i++)
+    for (int j = 0; j < WN; j++) {
+        const int n = 32 * (GC0 + WN * wave + j) + col;
+        if (n >= W.n) continue;
+        const int shw = wshift<QT>(W, n);
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const int m = 32 * (G0 + i) + drow(e, hh);
-            if (m >= M) continue;
-            float v = total[i][0][e];
-            if constexpr (QT == QT_F32) v = ldexpf(v, -shw);
-            y[(size_t)m * W.n + n] = act ? silu_f(v) : v;
-        }
+        for (int i = 0; i < WM; i++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int m = 32 * (G0 + i) + drow(e, hh);
+                if (m >= M) continue;
+                float v = total[i][j][e];
+                if constexpr (QT == QT_F32) v = ldexpf(v, -shw);
+                y[(size_t)m * W.n + n] = act ? silu_f(v) : v;
+            }
+    }
 }
 
 // The fold of EPI_PART's chunk results: y[m][n] from part[job][c][m][n], c
@@ -1557,6 +1610,51 @@ size_t mh_gemm_ws_floats(const DevW &W, int M, int jobs) {
     return (size_t)Kc * outs;
 }
 
+// Weight bytes per element of the resident layout (planes and headers)
+template <int QT> constexpr float w_bpe() {
+    return QT == QT_F32 ? 4.0f : QT == QT_INT8 ? 1.0f : QT == QT_INT4 ? 0.5625f : QT == QT_Q4_0 ? 0.5625f
+         : QT == QT_Q8_0 ? 1.0625f : QT == QT_Q2_K ? 0.33f : QT == QT_Q3_K ? 0.43f : QT == QT_Q4_K ? 0.5625f
+         : QT == QT_Q5_K ? 0.6875f : 0.82f;
+}
+
+// Column-tile groups of the tile order (k_gemm's ngrp): the count in {1, 2, 4}
+// that minimises a model of the L2 misses. Each XCD runs about 96 tiles at a
+// time (32 CUs x 3) out of an L2 of 4 MB. A group's weight slice that fits
+// beside the bands in flight is read once per XCD; one that does not is read
+// again for every round of tiles. Every extra group reads the activations
+// once more.
+static int gemm_ngroups(float wbytes, float abytes, int tilesM, int nt) {
+    const float l2 = 4.0f * 1048576.0f, conc = 96.0f;
+    const float band = abytes / (float)tilesM, rounds = fmaxf(1.0f, (float)tilesM * nt / 8.0f / conc);
+    int best = 1;
+    float best_cost = 0.0f;
+    for (int S = 1; S <= 4; S *= 2) {
+        if (nt % S) continue;
+        const float wslice = wbytes / S, bands_in_flight = fminf((float)tilesM, conc * S / nt);
+        const bool fits = wslice + bands_in_flight * band <= l2;
+        const float cost = S * abytes + 8.0f * wslice * (fits ? 1.0f : rounds);
+        if (S == 1 || cost < best_cost) best = S, best_cost = cost;
+    }
+    return best;
+}
+
+// 32 x 128 workgroup tiles when the 64 x 128 ones give at most two per CU;
+// measured on 750 rows: 1024->4096 (384 tiles) 25.9 -> 23.4 us, 1024->1024
+// (96) 17.7 -> 13.3 us; at 6000 rows 1024->1024 (752) 36 -> 40 us and at 1500
+// rows 1024->4096 (768) 36.6 -> 39.7 us, so there the 64-row tiles stay. The
+// same bits either way.
+static bool gemm_narrow(int grid) { return grid <= 512; }
+
+// 64 x 256 workgroup tiles (two column groups per wave, two workgroups per
+// CU) for the folded affine K-quants in EXACT numerics when there are enough
+// of them: measured at 12000 rows, Q4_K 1024->4096 294 -> 278 us, Q2_K
+// 4096->1024 280 -> 264 us (Q5_K 1%; Q3_K, Q8_0 and the A1 forms slower).
+template <int QT, bool A1>
+static bool gemm_wide(const DevW &W, int tilesM, int jobs) {
+    if (A1 || !(QT == QT_Q2_K || QT == QT_Q4_K || QT == QT_Q5_K) || W.Np % 256 != 0) return false;
+    return tilesM * (W.Np / 256) * jobs >= 512;
+}
+
 template <int QT, bool A1>
 static hipError_t gemm_launch(const GemmJobs &J, const uint8_t *xp, const float *xs16, const float *xpf, int M,
                               int act, const PrepOut *po, float *ws, hipStream_t st) {
@@ -1566,26 +1664,36 @@ static hipError_t gemm_launch(const GemmJobs &J, const uint8_t *xp, const float 
     for (int i = 1; i < J.n; i++)
         if (J.W[i].Np != W.Np || J.W[i].Kp != W.Kp || J.W[i].n != W.n) return hipErrorInvalidValue;
     const int tilesM = mpad / 64, tilesN = W.Np / 128, grid = J.n * tilesM * tilesN;
+    const int ngrp = gemm_ngroups(w_bpe<QT>() * W.Np * W.Kp * J.n, (A1 ? 2.0f : 4.0f) * mpad * W.Kp, tilesM,
+                                  J.n * tilesN);
     if (po) {
         if constexpr (A1) {
             return hipErrorInvalidValue;
         } else {
             if (po->Kc != tilesN || J.n != 1) return hipErrorInvalidValue;
             hipLaunchKernelGGL((k_gemm<QT, EPI_PREP>), dim3(grid), dim3(256), 0, st, J, xp, (const uint8_t *)xs16,
-                               xpf, M, 1, tilesM, tilesN, *po, nullptr, 1);
+                               xpf, M, 1, tilesM, tilesN, *po, nullptr, 1, ngrp);
             return hipGetLastError();
         }
     }
     const int ks = ws ? gemm_ksplit(W.Kp / 128, grid, (size_t)J.n * mpad * W.Np) : 1;
     if (ks > 1) {
         hipLaunchKernelGGL((k_gemm<QT, EPI_PART, A1>), dim3(grid * ks), dim3(256), 0, st, J, xp,
-                           (const uint8_t *)xs16, xpf, M, act, tilesM, tilesN, PrepOut{}, ws, ks);
+                           (const uint8_t *)xs16, xpf, M, act, tilesM, tilesN, PrepOut{}, ws, ks, 1);
         const int threads = M * (W.Np / 4);
         hipLaunchKernelGGL((k_gemm_fold<QT>), dim3((threads + 255) / 256, J.n), dim3(256), 0, st, J, (const float *)ws,
                            xpf, M, mpad, act);
+    } else if (gemm_narrow(grid)) {
+        hipLaunchKernelGGL((k_gemm<QT, EPI_Y, A1, 1, 1>), dim3(2 * grid), dim3(256), 0, st, J, xp,
+                           (const uint8_t *)xs16, xpf, M, act, 2 * tilesM, tilesN, PrepOut{}, nullptr, 1, ngrp);
+    } else if (gemm_wide<QT, A1>(W, tilesM, J.n)) {
+        const int tN2 = W.Np / 256, ng2 = gemm_ngroups(w_bpe<QT>() * W.Np * W.Kp * J.n, (A1 ? 2.0f : 4.0f) * mpad * W.Kp,
+                                                      tilesM, J.n * tN2);
+        hipLaunchKernelGGL((k_gemm<QT, EPI_Y, A1, 2>), dim3(J.n * tilesM * tN2), dim3(256), 0, st, J, xp,
+                           (const uint8_t *)xs16, xpf, M, act, tilesM, tN2, PrepOut{}, nullptr, 1, ng2);
     } else {
         hipLaunchKernelGGL((k_gemm<QT, EPI_Y, A1>), dim3(grid), dim3(256), 0, st, J, xp, (const uint8_t *)xs16, xpf,
-                           M, act, tilesM, tilesN, PrepOut{}, nullptr, 1);
+                           M, act, tilesM, tilesN, PrepOut{}, nullptr, 1, ngrp);
     }
     return hipGetLastError();
 }
