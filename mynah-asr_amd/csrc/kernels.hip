@@ -66,6 +66,19 @@ __device__ __forceinline__ int chunk_shift(float amax) {
     return amax > 0.0f ? 15 - e : 0;
 }
 
+// f16(x0 - h.lo), f16(x1 - h.hi) as one packed pair: x - h is exact in f32
+// (h is x rounded to f16), and v_fma_mixlo / v_fma_mixhi form it with h read as f16 in place
+// and rounds it to f16 once: the value of (_Float16)(x - (float)h), in two
+// instructions per pair instead of six.
+__device__ __forceinline__ uint32_t lo_pair(uint32_t hpair, float x0, float x1) {
+    uint32_t r;
+    asm volatile("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(hpair), "v"(x0));
+    asm volatile("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+                 : "+v"(r)
+                 : "v"(hpair), "v"(x1));
+    return r;
+}
+
 // the split of NU half-steps' values v[u][j] with shift sh
 template <int NU>
 __device__ __forceinline__ void split_part(const float (&v)[NU][8], int sh, half8 (&h)[NU], half8 (&l)[NU],
@@ -73,15 +86,19 @@ __device__ __forceinline__ void split_part(const float (&v)[NU][8], int sh, half
 #pragma unroll
     for (int u = 0; u < NU; u++) {
         float acc = 0.0f;
+        float xs[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const float xs = ldexpf(v[u][j], sh);
-            const _Float16 hv = (_Float16)xs;
-            h[u][j] = hv;
-            l[u][j] = (_Float16)(xs - (float)hv);
-            acc += xs;
+            xs[j] = ldexpf(v[u][j], sh);
+            h[u][j] = (_Float16)xs[j];
+            acc += xs[j];
         }
         s8[u] = acc;
+        uint32_t hw[4], lw[4];
+        __builtin_memcpy(hw, &h[u], 16);
+#pragma unroll
+        for (int t = 0; t < 4; t++) lw[t] = lo_pair(hw[t], xs[2 * t], xs[2 * t + 1]);
+        __builtin_memcpy(&l[u], lw, 16);
     }
 }
 
@@ -101,9 +118,8 @@ __device__ __forceinline__ void split_vals(const float (&v)[HSTEPS][8], XChunk &
 // VEC: K % 8 == 0 and 16-byte aligned rows (each lane's 8 elements are
 // wholly inside or wholly past K), two float4 loads per half-step
 template <bool VEC>
-__device__ __forceinline__ void split_chunk(const float *__restrict__ x, int M, int K, int m, int c, int hh,
-                                            XChunk &o) {
-    float v[HSTEPS][8];
+__device__ __forceinline__ void load_chunk(const float *__restrict__ x, int M, int K, int m, int c, int hh,
+                                           float (&v)[HSTEPS][8]) {
     const bool live = m < M;
     const float *row = x + (size_t)(live ? m : 0) * K;
 #pragma unroll
@@ -122,6 +138,13 @@ __device__ __forceinline__ void split_chunk(const float *__restrict__ x, int M, 
             for (int j = 0; j < 8; j++) v[u][j] = (live && k0 + j < K) ? row[k0 + j] : 0.0f;
         }
     }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void split_chunk(const float *__restrict__ x, int M, int K, int m, int c, int hh,
+                                            XChunk &o) {
+    float v[HSTEPS][8];
+    load_chunk<VEC>(x, M, K, m, c, hh, v);
     split_vals(v, o);
 }
 
@@ -946,8 +969,13 @@ __device__ __forceinline__ void gemv_body(const DevW &W, const float *__restrict
         __syncthreads();
     }
     for (int c = wave; c < Kc; c += NW) {
+        // x's chunk (a few KiB, in L2) goes out before the weights: vector
+        // loads complete in issue order, so the split can start as soon as
+        // x lands, while the weight bytes are still on their way
+        float xv[HSTEPS][8];
+        if constexpr (!PRO) load_chunk<VEC>(x, M, W.k, col, c, hh, xv);
+        __builtin_amdgcn_sched_barrier(0);
         if (!PRO || c != wave) load(c);
-        // the weight loads go out first: their latency overlaps the x split
         __builtin_amdgcn_sched_barrier(0);
         XChunk xc;
         if constexpr (PRO) {   // M = 1: row 0 from the prologue's row
@@ -958,7 +986,7 @@ __device__ __forceinline__ void gemv_body(const DevW &W, const float *__restrict
                 for (int j = 0; j < 8; j++) v[u][j] = col == 0 ? xs[128 * c + 16 * u + 8 * hh + j] : 0.0f;
             split_vals(v, xc);
         } else {
-            split_chunk<VEC>(x, M, W.k, col, c, hh, xc);
+            split_vals(xv, xc);
         }
         if (hh == 0 && col < 16) pf[c * 16 + col] = xc.p;
         f16v acc[1][WNG];
@@ -1016,12 +1044,16 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_part(DevW W, const float *__re
     const int gn[1] = {bx};
     BH<QT, 1> hd;
     BK<QT, 1> bk[KSTEPS];
+    // x first: its loads complete before the weights' (issue order)
+    float xv[HSTEPS][8];
+    load_chunk<VEC>(x, M, W.k, col, c, hh, xv);
+    __builtin_amdgcn_sched_barrier(0);
     load_bh<QT, 1>(W, Kc, gn, c, lane, hd);
 #pragma unroll
     for (int s = 0; s < KSTEPS; s++) load_bk<QT, 1>(W, Kc, gn, c, s, lane, bk[s]);
     __builtin_amdgcn_sched_barrier(0);
     XChunk xc;
-    split_chunk<VEC>(x, M, W.k, col, c, hh, xc);
+    split_vals(xv, xc);
     if (bx == 0 && hh == 0 && col < 16) pfg[c * 16 + col] = xc.p;
     f16v acc[1][1];
     acc[0][0] = zero16();
