@@ -388,7 +388,9 @@ template <int N> __device__ __forceinline__ void wait_vm() {
 // workgroup reads, for its 2 row groups and 4 column groups. Planes of 32 or
 // more bytes per lane and chunk stage the stage's own part; narrower ones the
 // whole (column group, chunk) block.
-template <int QT, bool A1 = false, int NCG = 4, int NRG = 2> struct StageLayout {
+// BD: the weight planes go global -> registers instead of through LDS (each
+// wave reads only its own column groups' planes, so LDS brings no reuse)
+template <int QT, bool A1 = false, int NCG = 4, int NRG = 2, bool BD = false> struct StageLayout {
     using F = Fmt<QT>;
     static constexpr int SPS = QT == QT_F32 ? 1 : 2;              // ksteps per stage
     static constexpr int NST = KSTEPS / SPS;                      // stages per chunk
@@ -397,7 +399,7 @@ template <int QT, bool A1 = false, int NCG = 4, int NRG = 2> struct StageLayout 
     template <int B> static constexpr int plane() { return B == 0 ? 0 : (B >= 32 ? SPS * 16 * B : 64 * B); }
     template <int B> static __device__ int plane_off(int q) { return B >= 32 ? q * SPS * 16 * B : 0; }
     static constexpr int A = 0;                                   // [NRG rg][2 SPS u][TERMS][1 KiB]
-    static constexpr int B0S = plane<F::B0>(), B1S = plane<F::B1>();
+    static constexpr int B0S = BD ? 0 : plane<F::B0>(), B1S = BD ? 0 : plane<F::B1>();
     static constexpr int P0 = A + NRG * AR;                       // [NCG cg][B0S]
     static constexpr int P1 = P0 + NCG * B0S;                     // [NCG cg][B1S]
     static constexpr int HB = P1 + NCG * B1S;                     // [NCG cg][F::HB]
@@ -462,7 +464,12 @@ __global__ __launch_bounds__(256, (gemm_occ<QT, A1, WN, WM>())) void k_gemm(Gemm
                                                  int M, int act, int tilesM, int tilesN, PrepOut po,
                                                  float *__restrict__ part, int ksplit, int ngrp) {
     using F = Fmt<QT>;
-    using L = StageLayout<QT, A1, 4 * WN, WM>;
+    // the weight planes go straight to registers, one stage ahead (measured
+    // 3-6% faster than through LDS on every format: less LDS traffic);
+    // f32 weights' two f16 planes stay in LDS
+    constexpr bool BD = QT != QT_F32;
+    using L = StageLayout<QT, A1, 4 * WN, WM, BD>;
+    typename F::RawK rb[2][WN][L::SPS];   // BD: the weight planes of the stage in flight and the current one
     static_assert(!(A1 && EPI == EPI_PREP), "the fused FFN hand-off is EXACT only");
     static_assert((WN == 1 && WM == 2) || EPI != EPI_PREP, "the fused FFN hand-off takes 64 x 128 tiles");
     constexpr bool HALVES = A1 && QT == QT_Q5_K;
@@ -518,11 +525,16 @@ __global__ __launch_bounds__(256, (gemm_occ<QT, A1, WN, WM>())) void k_gemm(Gemm
 #pragma unroll
         for (int j = 0; j < WN; j++) {
             const int gc = GC0 + WN * wave + j, slot = WN * wave + j;
-            dma<L::B0S>(W.p0 + ((size_t)gc * Kc + c) * 64 * F::B0 + L::template plane_off<F::B0>(q),
-                        B + L::P0 + slot * L::B0S, lane);
-            if constexpr (F::B1 > 0)
-                dma<L::B1S>(W.p1 + ((size_t)gc * Kc + c) * 64 * F::B1 + L::template plane_off<F::B1>(q),
-                            B + L::P1 + slot * L::B1S, lane);
+            if constexpr (BD) {
+#pragma unroll
+                for (int sl = 0; sl < L::SPS; sl++) F::load_k(W, Kc, gc, c, L::SPS * q + sl, lane, rb[q & 1][j][sl]);
+            } else {
+                dma<L::B0S>(W.p0 + ((size_t)gc * Kc + c) * 64 * F::B0 + L::template plane_off<F::B0>(q),
+                            B + L::P0 + slot * L::B0S, lane);
+                if constexpr (F::B1 > 0)
+                    dma<L::B1S>(W.p1 + ((size_t)gc * Kc + c) * 64 * F::B1 + L::template plane_off<F::B1>(q),
+                                B + L::P1 + slot * L::B1S, lane);
+            }
             if constexpr (F::HB > 0) dma<F::HB>(F::hb_src(W, Kc, gc, c), B + L::HB + slot * F::HB, lane);
             if constexpr (F::H2 > 0) dma<F::H2>(F::h2_src(W, Kc, gc, c), B + L::H2 + slot * F::H2, lane);
         }
@@ -550,9 +562,12 @@ __global__ __launch_bounds__(256, (gemm_occ<QT, A1, WN, WM>())) void k_gemm(Gemm
             BK<QT, WN> b;
             // (one-kstep stages hold only kstep s: its local index is 0)
 #pragma unroll
-            for (int j = 0; j < WN; j++)
-                F::k_lds(B + L::P0 + (WN * wave + j) * L::B0S, B + L::P1 + (WN * wave + j) * L::B1S,
-                         L::SPS == 1 ? 0 : s, lane, b.r[j]);
+            for (int j = 0; j < WN; j++) {
+                if constexpr (BD) b.r[j] = rb[q & 1][j][sl];
+                else
+                    F::k_lds(B + L::P0 + (WN * wave + j) * L::B0S, B + L::P1 + (WN * wave + j) * L::B1S,
+                             L::SPS == 1 ? 0 : s, lane, b.r[j]);
+            }
             kstep<QT, WM, WN, A1>(a, b, hd, s, acc);
         }
     };
