@@ -193,7 +193,11 @@ template <int WM> struct AK {
 // A1 (INT8ACT numerics): the activations are int8 values held as f16 (exact),
 // one term: the xl MFMAs drop out, and every sum the MFMAs form is an exact
 // integer (the kernels keep each accumulation below 2^24 in magnitude).
-template <int QT, int WM, int WN, bool A1 = false>
+//
+// NE: the per-element f32 work covers accumulator elements e < NE only (the
+// GEMV of M rows reads elements 0 .. NE-1: rows drow(e, hh) below M); the
+// elements it covers see the same operations at every NE.
+template <int QT, int WM, int WN, bool A1 = false, int NE = 16>
 __device__ __forceinline__ void kstep(const AK<WM> &a, const BK<QT, WN> &b, const BH<QT, WN> &hd, int s,
                                       f16v (&acc)[WM][WN]) {
     using F = Fmt<QT>;
@@ -242,7 +246,7 @@ __device__ __forceinline__ void kstep(const AK<WM> &a, const BK<QT, WN> &b, cons
                     t = mfma32(a.l[i][1], b1, t);
                 }
 #pragma unroll
-                for (int e = 0; e < 16; e++) acc[i][j][e] = __builtin_fmaf(sc, t[e], acc[i][j][e]);
+                for (int e = 0; e < NE; e++) acc[i][j][e] = __builtin_fmaf(sc, t[e], acc[i][j][e]);
             }
         }
     } else {
@@ -267,7 +271,7 @@ __device__ __forceinline__ void kstep(const AK<WM> &a, const BK<QT, WN> &b, cons
                 f16v t1 = mfma32(a.h[i][1], b1, zero16());
                 if constexpr (!A1) t1 = mfma32(a.l[i][1], b1, t1);
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
+                for (int e = 0; e < NE; e++) {
                     acc[i][j][e] = __builtin_fmaf(sc0, t0[e], acc[i][j][e]);
                     acc[i][j][e] = __builtin_fmaf(sc1, t1[e], acc[i][j][e]);
                 }
@@ -303,15 +307,15 @@ __device__ __forceinline__ half8 xm_frag(const float (&s8)[HSTEPS], int hh) {
 
 // End of a chunk of a folded format: acc (= sum of x * q f over the chunk)
 // becomes d * acc - dm * (mins product), the chunk result the fold takes
-template <int QT>
+template <int QT, int NE = 16>
 __device__ __forceinline__ void fold_finish(const half8 &xm, const typename KHdr<QT>::T &H, f16v &acc) {
     if constexpr (Fmt<QT>::MINS) {
         const f16v t2 = mfma32(xm, H.mb, zero16());
 #pragma unroll
-        for (int e = 0; e < 16; e++) acc[e] = __builtin_fmaf(-H.dm, t2[e], H.d * acc[e]);
+        for (int e = 0; e < NE; e++) acc[e] = __builtin_fmaf(-H.dm, t2[e], H.d * acc[e]);
     } else {
 #pragma unroll
-        for (int e = 0; e < 16; e++) acc[e] = H.d * acc[e];
+        for (int e = 0; e < NE; e++) acc[e] = H.d * acc[e];
     }
 }
 
@@ -934,14 +938,14 @@ __device__ __forceinline__ EpiPre epi_pre(const DevW &W, int n, int M, int hh, c
 
 // y = act(W x + b) + res for output column n and the lane's 8 rows, in the
 // order of the reference's mv() and its callers (decoder_aed.c:15-19, 207-210);
-// for M = 1, b and res from pre
-template <int QT>
+// for M = 1, b and res from pre; elements e < NE hold rows
+template <int QT, int NE = 8>
 __device__ __forceinline__ void gemv_store(const DevW &W, int n, int M, int hh, const float (&total)[8],
                                            const GEpi &ep, const EpiPre &pre, float *y) {
     if (n >= W.n) return;
     const int shw = wshift<QT>(W, n);
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
+    for (int e = 0; e < NE; e++) {
         const int m = drow(e, hh);
         if (m >= M) continue;
         float v = total[e];
@@ -954,8 +958,10 @@ __device__ __forceinline__ void gemv_store(const DevW &W, int n, int M, int hh, 
     }
 }
 
-// the GEMV of workgroup bx of one product (shared by k_gemv and k_gemv_jobs)
-template <int QT, int NW, int WNG, bool VEC, bool PRO>
+// the GEMV of workgroup bx of one product (shared by k_gemv and k_gemv_jobs).
+// NE: accumulator elements carried (1 for M = 1, 8 for M <= 16): rows
+// drow(e, hh) for e < NE cover every row below M.
+template <int QT, int NW, int WNG, bool VEC, bool PRO, int NE>
 __device__ __forceinline__ void gemv_body(const DevW &W, const float *__restrict__ x, int M, float *y,
                                           const GEpi &ep, const GPro &pro, int bx) {
     extern __shared__ float part[];  // [Kc][WNG][8][64] chunk results, pf [Kc][16], prologue row [Kp]
@@ -1015,19 +1021,19 @@ __device__ __forceinline__ void gemv_body(const DevW &W, const float *__restrict
                 a.h[0][kh] = xc.h[2 * s + kh];
                 a.l[0][kh] = xc.l[2 * s + kh];
             }
-            kstep<QT, 1, WNG>(a, bk[s], hd, s, acc);
+            kstep<QT, 1, WNG, false, NE>(a, bk[s], hd, s, acc);
         }
         if constexpr (fold_fmt<QT>()) {
             // the mins operand from this chunk's own sums, as the preparation forms it
             half8 xmv = {};
             if constexpr (Fmt<QT>::MINS) xmv = xm_frag<Fmt<QT>::SUB16 ? 8 : 4>(xc.s8, hh);
 #pragma unroll
-            for (int j = 0; j < WNG; j++) fold_finish<QT>(xmv, hd.h[j], acc[0][j]);
+            for (int j = 0; j < WNG; j++) fold_finish<QT, NE>(xmv, hd.h[j], acc[0][j]);
         }
 #pragma unroll
         for (int j = 0; j < WNG; j++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) part[((c * WNG + j) * 8 + e) * 64 + lane] = acc[0][j][e];
+            for (int e = 0; e < NE; e++) part[((c * WNG + j) * 8 + e) * 64 + lane] = acc[0][j][e];
     }
     __syncthreads();
     for (int j = wave; j < WNG; j += NW) {
@@ -1036,9 +1042,9 @@ __device__ __forceinline__ void gemv_body(const DevW &W, const float *__restrict
         for (int e = 0; e < 8; e++) total[e] = 0.0f;
         for (int c = 0; c < Kc; c++)
 #pragma unroll
-            for (int e = 0; e < 8; e++)
+            for (int e = 0; e < NE; e++)
                 total[e] = __builtin_fmaf(pf[c * 16 + drow(e, hh)], part[((c * WNG + j) * 8 + e) * 64 + lane], total[e]);
-        gemv_store<QT>(W, 32 * gn[j] + col, M, hh, total, ep, pre, y);
+        gemv_store<QT, NE>(W, 32 * gn[j] + col, M, hh, total, ep, pre, y);
     }
 }
 
@@ -1049,7 +1055,7 @@ __device__ __forceinline__ void gemv_body(const DevW &W, const float *__restrict
 // (the values gemv_body keeps in LDS) to part[bx][c][8][64] and the fold
 // factors to pfg[c][16]. Part 2 (k_gemv_fold) folds them in chunk order from
 // zero: the same operations, so the rows are bit-identical to gemv_body's.
-template <int QT, int NW, bool VEC>
+template <int QT, int NW, bool VEC, int NE>
 __global__ __launch_bounds__(NW * 64) void k_gemv_part(DevW W, const float *__restrict__ x, int M,
                                                        float *__restrict__ part, float *__restrict__ pfg) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1080,16 +1086,16 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_part(DevW W, const float *__re
             a.h[0][kh] = xc.h[2 * s + kh];
             a.l[0][kh] = xc.l[2 * s + kh];
         }
-        kstep<QT, 1, 1>(a, bk[s], hd, s, acc);
+        kstep<QT, 1, 1, false, NE>(a, bk[s], hd, s, acc);
     }
     if constexpr (fold_fmt<QT>()) {
         half8 xmv = {};
         if constexpr (Fmt<QT>::MINS) xmv = xm_frag<Fmt<QT>::SUB16 ? 8 : 4>(xc.s8, hh);
-        fold_finish<QT>(xmv, hd.h[0], acc[0][0]);
+        fold_finish<QT, NE>(xmv, hd.h[0], acc[0][0]);
     }
     float *o = part + ((size_t)bx * Kc + c) * 8 * 64;
 #pragma unroll
-    for (int e = 0; e < 8; e++) o[e * 64 + lane] = acc[0][0][e];
+    for (int e = 0; e < NE; e++) o[e * 64 + lane] = acc[0][0][e];
 }
 
 template <int QT>
@@ -1150,9 +1156,9 @@ __global__ __launch_bounds__(64) void k_gemv_fold(DevW W, const float *__restric
 }
 
 // one product: the compact argument block of the encoder and decoder GEMVs
-template <int QT, int NW, int WNG, bool VEC>
+template <int QT, int NW, int WNG, bool VEC, int NE>
 __global__ __launch_bounds__(NW * 64) void k_gemv(DevW W, const float *__restrict__ x, int M, float *y, GEpi ep) {
-    gemv_body<QT, NW, WNG, VEC, false>(W, x, M, y, ep, GPro{}, blockIdx.x);
+    gemv_body<QT, NW, WNG, VEC, false, NE>(W, x, M, y, ep, GPro{}, blockIdx.x);
 }
 
 // up to three products of one prologue-built row (the decoder step)
@@ -1163,7 +1169,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_jobs(GJobs J, GPro pro) {
     const DevW W = job == 0 ? J.W[0] : (job == 1 ? J.W[1] : J.W[2]);
     float *y = job == 0 ? J.y[0] : (job == 1 ? J.y[1] : J.y[2]);
     const GEpi ep = job == 0 ? J.ep[0] : (job == 1 ? J.ep[1] : J.ep[2]);
-    gemv_body<QT, NW, WNG, false, true>(W, nullptr, 1, y, ep, pro, bx);
+    gemv_body<QT, NW, WNG, false, true, 1>(W, nullptr, 1, y, ep, pro, bx);
 }
 
 // ---------------------------------------------------------------------------
@@ -1566,6 +1572,8 @@ __global__ void k_silu(float *__restrict__ x, size_t n) {
 // Host-side launchers (C++ linkage inside the library).
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "launch.h"
 
 template <typename F>
@@ -1590,13 +1598,23 @@ static hipError_t launch_gemv1(const GJobs &J, const float *x, int M, const GPro
         hipLaunchKernelGGL((k_gemv_jobs<QT, NW, WNG>), dim3(W.Np / 32 / WNG * J.n), dim3(NW * 64), lds, st, J, pro);
     } else {
         if (!attr) {
-            hipError_t e = allow_lds(k_gemv<QT, NW, WNG, VEC>);
+            hipError_t e = allow_lds(k_gemv<QT, NW, WNG, VEC, 1>);
+            if (e == hipSuccess) e = allow_lds(k_gemv<QT, NW, WNG, VEC, 4>);
+            if (e == hipSuccess) e = allow_lds(k_gemv<QT, NW, WNG, VEC, 8>);
             if (e != hipSuccess) return e;
             attr = true;
         }
         if (J.n != 1) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_gemv<QT, NW, WNG, VEC>), dim3(W.Np / 32 / WNG), dim3(NW * 64), lds, st, W, x, M, J.y[0],
-                           J.ep[0]);
+        // accumulator elements the M rows need (rows drow(e, hh) < M)
+        if (M == 1)
+            hipLaunchKernelGGL((k_gemv<QT, NW, WNG, VEC, 1>), dim3(W.Np / 32 / WNG), dim3(NW * 64), lds, st, W, x, M,
+                               J.y[0], J.ep[0]);
+        else if (M <= 8)
+            hipLaunchKernelGGL((k_gemv<QT, NW, WNG, VEC, 4>), dim3(W.Np / 32 / WNG), dim3(NW * 64), lds, st, W, x, M,
+                               J.y[0], J.ep[0]);
+        else
+            hipLaunchKernelGGL((k_gemv<QT, NW, WNG, VEC, 8>), dim3(W.Np / 32 / WNG), dim3(NW * 64), lds, st, W, x, M,
+                               J.y[0], J.ep[0]);
     }
     return hipGetLastError();
 }
@@ -1801,10 +1819,17 @@ static hipError_t gemv_split_t(const DevW &W, const float *x, int M, int vec, fl
     const int Kc = W.Kp / 128, G = W.Np / 32;
     float *part = ws, *pfg = ws + (size_t)G * Kc * 512;
     const dim3 grid(G, (Kc + NW - 1) / NW);
-    if (vec)
-        hipLaunchKernelGGL((k_gemv_part<QT, NW, true>), grid, dim3(NW * 64), 0, st, W, x, M, part, pfg);
-    else
-        hipLaunchKernelGGL((k_gemv_part<QT, NW, false>), grid, dim3(NW * 64), 0, st, W, x, M, part, pfg);
+    // chunk results of the rows below M only (the fold reads no other row)
+    auto part_k = [&](auto ne) {
+        constexpr int NE = decltype(ne)::value;
+        if (vec)
+            hipLaunchKernelGGL((k_gemv_part<QT, NW, true, NE>), grid, dim3(NW * 64), 0, st, W, x, M, part, pfg);
+        else
+            hipLaunchKernelGGL((k_gemv_part<QT, NW, false, NE>), grid, dim3(NW * 64), 0, st, W, x, M, part, pfg);
+    };
+    if (M == 1) part_k(std::integral_constant<int, 1>{});
+    else if (M <= 8) part_k(std::integral_constant<int, 4>{});
+    else part_k(std::integral_constant<int, 8>{});
     hipLaunchKernelGGL((k_gemv_fold<QT>), dim3(G), dim3(64), 0, st, W, part, pfg, M, y, ep);
     return hipGetLastError();
 }
