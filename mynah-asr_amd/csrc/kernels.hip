@@ -413,16 +413,6 @@ template <int QT, bool A1 = false, int NCG = 4, int NRG = 2, bool BD = false> st
     static constexpr int BYTES = XS + (F::MINS ? NRG * 1024 : 0);
 };
 
-// workgroups per CU the register budget is sized for: as many as the LDS
-// ring allows (three double-buffered workgroups: 25-27 KiB stages, 24 KiB
-// one-kstep stages for f32 weights), two for Q6_K (its eight per-half-step
-// f32 factors need more registers)
-template <int QT, bool A1 = false, int WN = 1, int WM = 2> constexpr int gemm_occ() {
-    if (WN > 1) return 2;
-    if (WM == 1) return QT == QT_Q6_K ? 3 : 4;
-    return QT == QT_Q6_K ? 2 : 3;
-}
-
 // Where a product's result goes: EPI_Y stores y (SiLU applied when act);
 // EPI_PREP (the first product of the FFN) applies SiLU and, instead of
 // storing the f32 intermediate, prepares it as the second product's input —
@@ -440,6 +430,19 @@ struct PrepOut {
     float *xpf;
     int Kc, xsum;   // mins A operands (xm_frag): 0 none, 1 of 8 sub-blocks, 2 of 4
 };
+
+// workgroups per CU the register budget is sized for: as many as the LDS
+// ring allows (three double-buffered workgroups: 25-27 KiB stages, 24 KiB
+// one-kstep stages for f32 weights), two for Q6_K (its eight per-half-step
+// f32 factors need more registers), and two for the split-K form of the
+// formats whose chunk-result stores would otherwise spill (INT4; Q5_K with
+// int8 activations, whose chunk halves join in int32)
+template <int QT, int EPI, bool A1 = false, int WN = 1, int WM = 2> constexpr int gemm_occ() {
+    if (WN > 1) return 2;
+    if (WM == 1) return QT == QT_Q6_K ? 3 : 4;
+    if (EPI == EPI_PART && (QT == QT_INT4 || (A1 && QT == QT_Q5_K))) return 2;
+    return QT == QT_Q6_K ? 2 : 3;
+}
 
 // ---------------------------------------------------------------------------
 // Large-M GEMM. Workgroup = 4 waves side by side over N, tile 64 x 128: row
@@ -462,7 +465,7 @@ struct PrepOut {
 // WM: row groups per wave and workgroup (2: tiles of 64 rows; 1: of 32 rows,
 // twice the workgroups for products of few row bands).
 template <int QT, int EPI, bool A1 = false, int WN = 1, int WM = 2>
-__global__ __launch_bounds__(256, (gemm_occ<QT, A1, WN, WM>())) void k_gemm(GemmJobs J, const uint8_t *__restrict__ xp,
+__global__ __launch_bounds__(256, (gemm_occ<QT, EPI, A1, WN, WM>())) void k_gemm(GemmJobs J, const uint8_t *__restrict__ xp,
                                                  const uint8_t *__restrict__ xm,
                                                  const float *__restrict__ xpf,
                                                  int M, int act, int tilesM, int tilesN, PrepOut po,
@@ -470,8 +473,10 @@ __global__ __launch_bounds__(256, (gemm_occ<QT, A1, WN, WM>())) void k_gemm(Gemm
     using F = Fmt<QT>;
     // the weight planes go straight to registers, one stage ahead (measured
     // 3-6% faster than through LDS on every format: less LDS traffic);
-    // f32 weights' two f16 planes stay in LDS
-    constexpr bool BD = QT != QT_F32;
+    // f32 weights' two f16 planes stay in LDS, and so do the planes of the
+    // split-K form (its chunk-result stores leave no registers for them:
+    // with them it spilled, and 4096->1024 at 750 rows took 129 us, not 50)
+    constexpr bool BD = QT != QT_F32 && EPI != EPI_PART;
     using L = StageLayout<QT, A1, 4 * WN, WM, BD>;
     typename F::RawK rb[2][WN][L::SPS];   // BD: the weight planes of the stage in flight and the current one
     static_assert(!(A1 && EPI == EPI_PREP), "the fused FFN hand-off is EXACT only");
@@ -1714,9 +1719,12 @@ static bool gemm_narrow(int grid) { return grid <= 512; }
 // CU) for the folded affine K-quants in EXACT numerics when there are enough
 // of them: measured at 12000 rows, Q4_K 1024->4096 294 -> 278 us, Q2_K
 // 4096->1024 280 -> 264 us (Q5_K 1%; Q3_K, Q8_0 and the A1 forms slower).
+template <int QT, bool A1> constexpr bool wide_fmt() {
+    return !A1 && (QT == QT_Q2_K || QT == QT_Q4_K || QT == QT_Q5_K);
+}
 template <int QT, bool A1>
 static bool gemm_wide(const DevW &W, int tilesM, int jobs) {
-    if (A1 || !(QT == QT_Q2_K || QT == QT_Q4_K || QT == QT_Q5_K) || W.Np % 256 != 0) return false;
+    if (!wide_fmt<QT, A1>() || W.Np % 256 != 0) return false;
     return tilesM * (W.Np / 256) * jobs >= 512;
 }
 
@@ -1752,10 +1760,12 @@ static hipError_t gemm_launch(const GemmJobs &J, const uint8_t *xp, const float 
         hipLaunchKernelGGL((k_gemm<QT, EPI_Y, A1, 1, 1>), dim3(2 * grid), dim3(256), 0, st, J, xp,
                            (const uint8_t *)xs16, xpf, M, act, 2 * tilesM, tilesN, PrepOut{}, nullptr, 1, ngrp);
     } else if (gemm_wide<QT, A1>(W, tilesM, J.n)) {
-        const int tN2 = W.Np / 256, ng2 = gemm_ngroups(w_bpe<QT>() * W.Np * W.Kp * J.n, (A1 ? 2.0f : 4.0f) * mpad * W.Kp,
-                                                      tilesM, J.n * tN2);
-        hipLaunchKernelGGL((k_gemm<QT, EPI_Y, A1, 2>), dim3(J.n * tilesM * tN2), dim3(256), 0, st, J, xp,
-                           (const uint8_t *)xs16, xpf, M, act, tilesM, tN2, PrepOut{}, nullptr, 1, ng2);
+        if constexpr (wide_fmt<QT, A1>()) {   // (the other formats never instantiate it)
+            const int tN2 = W.Np / 256, ng2 = gemm_ngroups(w_bpe<QT>() * W.Np * W.Kp * J.n,
+                                                          (A1 ? 2.0f : 4.0f) * mpad * W.Kp, tilesM, J.n * tN2);
+            hipLaunchKernelGGL((k_gemm<QT, EPI_Y, A1, 2>), dim3(J.n * tilesM * tN2), dim3(256), 0, st, J, xp,
+                               (const uint8_t *)xs16, xpf, M, act, tilesM, tN2, PrepOut{}, nullptr, 1, ng2);
+        }
     } else {
         hipLaunchKernelGGL((k_gemm<QT, EPI_Y, A1>), dim3(grid), dim3(256), 0, st, J, xp, (const uint8_t *)xs16, xpf,
                            M, act, tilesM, tilesN, PrepOut{}, nullptr, 1, ngrp);
