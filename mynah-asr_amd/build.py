@@ -33,26 +33,49 @@ HIP_FLAGS = ["-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC", "-ffp-contra
              "-Wall", "-Wno-unused-function", "-I", INC, "-I", CSRC]
 
 
-def _run(cmd: list[str]) -> None:
+def _run(cmd: list[str]) -> list[str]:
+    """Runs one compiler command; returns the kernels that spill registers
+    (from the kernel-resource-usage remarks, which are not echoed)."""
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature: harmless
     noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in r.stderr.splitlines() if noise not in l)
+    lines, spills, kernel, in_remark = [], [], "", False
+    for l in r.stderr.splitlines():
+        if "remark:" in l and "kernel-resource-usage" in l:
+            in_remark = True
+            body = l.split("remark:", 1)[1].strip()
+            if body.startswith("Function Name:"):
+                kernel = body.split(":", 1)[1].split("[")[0].strip()
+            elif body.startswith("VGPRs Spill:") and body.split(":", 1)[1].split("[")[0].strip() != "0":
+                spills.append(f"{kernel} ({body.split(':', 1)[1].split('[')[0].strip()} VGPRs)")
+            continue
+        if in_remark and (l.lstrip()[:1].isdigit() or l.strip().startswith(("|", "^"))):
+            continue   # the source lines a remark quotes
+        in_remark = False
+        if noise not in l:
+            lines.append(l)
+    err = "\n".join(lines)
     if r.returncode != 0:
         sys.stderr.write(err + "\n")
         raise RuntimeError(f"build failed: {' '.join(cmd[:3])} ...")
     if err.strip():
         sys.stderr.write(err + "\n")
+    return spills
 
 
 def build_hip() -> str:
     os.makedirs(LIB, exist_ok=True)
     srcs = [os.path.join(CSRC, f) for f in ("kernels.hip", "attention.hip", "decoder.hip", "backend.cpp", "repack.cpp")]
     objs = []
+    spills = []
     for s in srcs:
         o = os.path.join(LIB, os.path.basename(s) + ".o")
-        _run([HIPCC, *HIP_FLAGS, "-x", "hip", "-c", s, "-o", o])
+        spills += _run([HIPCC, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-x", "hip", "-c", s, "-o", o])
         objs.append(o)
+    # a kernel that spills runs from scratch memory: say which, so a change
+    # that pushes one over its register budget does not go unnoticed
+    for k in spills:
+        sys.stderr.write(f"build.py: register spill in {k}\n")
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", HIP_LIB, *objs])
     for o in objs:
         os.remove(o)

@@ -433,13 +433,14 @@ struct PrepOut {
 
 // workgroups per CU the register budget is sized for: as many as the LDS
 // ring allows (three double-buffered workgroups: 25-27 KiB stages, 24 KiB
-// one-kstep stages for f32 weights), two for Q6_K (its eight per-half-step
-// f32 factors need more registers), and two for the split-K form of the
+// one-kstep stages for f32 weights; four of 32-row tiles, three for f32
+// weights), two for Q6_K (its eight per-half-step f32 factors need more
+// registers), and two for the split-K form of the
 // formats whose chunk-result stores would otherwise spill (INT4; Q5_K with
 // int8 activations, whose chunk halves join in int32)
 template <int QT, int EPI, bool A1 = false, int WN = 1, int WM = 2> constexpr int gemm_occ() {
     if (WN > 1) return 2;
-    if (WM == 1) return QT == QT_Q6_K ? 3 : 4;
+    if (WM == 1) return QT == QT_Q6_K || QT == QT_F32 ? 3 : 4;
     if (EPI == EPI_PART && (QT == QT_INT4 || (A1 && QT == QT_Q5_K))) return 2;
     return QT == QT_Q6_K ? 2 : 3;
 }
@@ -1650,8 +1651,8 @@ static hipError_t gemv_t(const GJobs &J, const float *x, int M, int vec, const G
     // K >= 4096 over few column groups: 16 waves take two chunks each rather
     // than 8 taking four (each chunk's loads wait a full memory latency);
     // within the 128 registers a 1024-thread workgroup allows, except the
-    // formats whose GEMV needs more
-    if constexpr (QT != QT_F32 && QT != QT_Q4_K && QT != QT_Q5_K && QT != QT_Q6_K)
+    // formats whose GEMV needs more (Q2_K spilled 60 registers there)
+    if constexpr (QT != QT_F32 && QT != QT_Q2_K && QT != QT_Q4_K && QT != QT_Q5_K && QT != QT_Q6_K)
         if (Kc >= 32) return launch_gemv<QT, 16, 1>(J, x, M, vec, pro, st);
     if (Kc >= 8) return launch_gemv<QT, 8, 1>(J, x, M, vec, pro, st);
     return launch_gemv<QT, 4, 1>(J, x, M, vec, pro, st);
