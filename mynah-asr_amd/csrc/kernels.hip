@@ -811,121 +811,148 @@ __global__ __launch_bounds__(256) void k_gemm_fold(GemmJobs J, const float *__re
 //
 // A launch may carry up to three products of one input (jobs of the same
 // format and shape: the workgroups of job i follow those of job i-1), and for
-// M = 1 a prologue may build the input row in LDS, per workgroup: the layer
-// norm of x, or the merge of attention splits (GPro).
+// M = 1 each wave may form its chunks of the input row itself: the layer norm
+// of x, or the merge of attention splits (GPro).
 
-// sum over the workgroup's threads in double
-template <int NT>
-__device__ double wg_sum(double v, double *red) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    double s = 0.0;
+// The input row of a one-row product built by each wave for its own chunks,
+// with no workgroup barrier (the row's statistics are formed by every wave
+// alone): lane l forms elements 128c + 2l, +1 of chunk c, and the wave moves
+// them to the A-fragment layout through its own 128 floats of LDS. All the
+// row's loads for the wave's first chunk go out before that chunk's weight
+// loads: vector loads complete in issue order, so the row is formed while the
+// weight bytes are still on their way.
+//
+//   GPRO_LN   (float)(((double)x - mean) * (double)inv) * w + b with inv =
+//             (float)(1 / sqrt(var + 1e-5)), mean and var over the K values in
+//             double (decoder_aed.c:21-28; the sums in one pass)
+//   GPRO_COMB the attention splits of the element's head merged:
+//             sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M), in split order
+constexpr int PRO_XB = 8;   // chunks of x per batch of the layer-norm sums (1024 values)
+constexpr int PRO_MB = 8;   // attention splits per batch of the merge
+static_assert(PRO_XB == PRO_MB, "the two kinds share their load registers");
+struct WaveRow {
+    // GPRO_LN: a = the first PRO_XB chunks of x (float2 per lane and chunk),
+    // then mu and inv; GPRO_COMB: n = the keys, a / b = (m, l) and the lane's
+    // two partial outputs of the chunk's first PRO_MB splits
+    float2 a[PRO_MB], b[PRO_MB];
+    double mu;
+    float inv;
+    bool have;
+    int n;
+    float2 xc, wc, bc;   // (GPRO_LN) this chunk's own operands
+};
+
+__device__ __forceinline__ float2 ld2(const float *p) { return *(const float2 *)p; }
+
+// issued once per wave, before anything else of the row
+__device__ __forceinline__ void wave_row_begin(const GPro &pro, int K, int lane, WaveRow &r) {
+    r.have = false;
+    if (pro.kind == GPRO_LN) {
 #pragma unroll
-    for (int i = 0; i < NT / 64; i++) s += red[i];
-    return s;
+        for (int u = 0; u < PRO_XB; u++) {
+            const int e = 128 * u + 2 * lane;
+            r.a[u] = e < K ? ld2(pro.x + e) : float2{0.0f, 0.0f};
+        }
+    } else {
+        r.n = pro.n_fixed > 0 ? pro.n_fixed : pro.st[0] + 1;
+    }
 }
 
-// xs[0..Kp) = the prologue's row (zero past K); K <= 4096
-template <int NT>
-__device__ void gemv_prologue(const GPro &pro, int K, int Kp, float *xs) {
-    __shared__ double red[NT / 64];
-    __shared__ float hm[64], hl[64];
-    constexpr int V = 4096 / NT;
-    const int tid = threadIdx.x;
+// chunk c's own loads (before its weight loads)
+__device__ __forceinline__ void wave_row_issue(const GPro &pro, int K, int c, int lane, WaveRow &r) {
+    const int e = 128 * c + 2 * lane;
+    const bool live = e < K;
     if (pro.kind == GPRO_LN) {
-        // (float)((x - mean) * inv) * w + b, inv = (float)(1 / sqrt(var + 1e-5)): decoder_aed.c:21-28
-        // w and b load with x: their latency is not after the two sums
-        float v[V], lw[V], lb[V];
-#pragma unroll
-        for (int u = 0; u < V; u++) {
-            const int i = tid + NT * u;
-            v[u] = i < K ? pro.x[i] : 0.0f;
-            lw[u] = i < K ? pro.w[i] : 0.0f;
-            lb[u] = i < K ? pro.b[i] : 0.0f;
-        }
-        double s = 0.0;
-#pragma unroll
-        for (int u = 0; u < V; u++) s += (double)v[u];
-        const double mu = wg_sum<NT>(s, red) / K;
-        double q = 0.0;
-#pragma unroll
-        for (int u = 0; u < V; u++)
-            if (tid + NT * u < K) {
-                const double c = (double)v[u] - mu;
-                q += c * c;
-            }
-        const double var = wg_sum<NT>(q, red) / K;
-        const float inv = (float)(1.0 / sqrt(var + 1e-5));
-#pragma unroll
-        for (int u = 0; u < V; u++) {
-            const int i = tid + NT * u;
-            if (i < K) {
-                const float t = (float)(((double)v[u] - mu) * (double)inv);
-                xs[i] = t * lw[u] + lb[u];
-            }
-        }
-        for (int i = K + tid; i < Kp; i += NT) xs[i] = 0.0f;
+        r.xc = live ? ld2(pro.x + e) : float2{0.0f, 0.0f};
+        r.wc = live ? ld2(pro.w + e) : float2{0.0f, 0.0f};
+        r.bc = live ? ld2(pro.b + e) : float2{0.0f, 0.0f};
     } else {
-        // attention splits merged per head: sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M)
-        const int dk = K / pro.H;
-        const int n = pro.n_fixed > 0 ? pro.n_fixed : pro.st[0] + 1;
-        const int ns = min(mh_att_splits_dev(n), pro.nsplit);
-        // the split weights e^(m_s - M) once per (head, split), not per element
-        // (up to PW of them; beyond that each element recomputes its own)
-        constexpr int PW = 1024;
-        __shared__ float hw[PW];
-        const bool pre = pro.H * ns <= PW;
-        // loads go out MB splits at a time (a loop over a run-time count
-        // would wait for each before issuing the next); the sums keep split order
-        constexpr int MB = 8;
-        if (tid < pro.H) {
-            const float2 *ml = (const float2 *)(pro.ml + (size_t)tid * pro.nsplit * 2);
-            float Mx = -INFINITY, L = 0.0f;
-            float2 mlv[MB];
-            for (int s0 = 0; s0 < ns; s0 += MB) {
+        const int dk = K / pro.H, h = live ? e / dk : 0, f = live ? e - h * dk : 0;
+        const float *ml = pro.ml + (size_t)h * pro.nsplit * 2;
+        const float *op = pro.opart + (size_t)h * pro.nsplit * dk + f;
 #pragma unroll
-                for (int u = 0; u < MB; u++) mlv[u] = s0 + u < ns ? ml[s0 + u] : float2{-INFINITY, 0.0f};
-#pragma unroll
-                for (int u = 0; u < MB; u++) Mx = fmaxf(Mx, mlv[u].x);
-            }
-            for (int s0 = 0; s0 < ns; s0 += MB) {
-#pragma unroll
-                for (int u = 0; u < MB; u++) mlv[u] = s0 + u < ns ? ml[s0 + u] : float2{-INFINITY, 0.0f};
-#pragma unroll
-                for (int u = 0; u < MB; u++)
-                    if (s0 + u < ns) {
-                        const float e = expf(mlv[u].x - Mx);
-                        if (pre) hw[tid * ns + s0 + u] = e;
-                        L += mlv[u].y * e;
-                    }
-            }
-            hm[tid] = Mx;
-            hl[tid] = L;
-        }
-        __syncthreads();
-        for (int i = tid; i < Kp; i += NT) {
-            float v = 0.0f;
-            if (i < K) {
-                const int h = i / dk, f = i - h * dk;
-                const float *ml = pro.ml + (size_t)h * pro.nsplit * 2;
-                const float *op = pro.opart + (size_t)h * pro.nsplit * dk + f;
-                const float Mx = hm[h];
-                float o = 0.0f;
-                for (int s0 = 0; s0 < ns; s0 += MB) {
-                    float ov[MB];
-#pragma unroll
-                    for (int u = 0; u < MB; u++) ov[u] = s0 + u < ns ? op[(size_t)(s0 + u) * dk] : 0.0f;
-#pragma unroll
-                    for (int u = 0; u < MB; u++)
-                        if (s0 + u < ns) o += ov[u] * (pre ? hw[h * ns + s0 + u] : expf(ml[2 * (s0 + u)] - Mx));
-                }
-                v = o / hl[h];
-            }
-            xs[i] = v;
+        for (int u = 0; u < PRO_MB; u++) {
+            const bool ok = live && u < pro.nsplit;
+            r.a[u] = ok ? ld2(ml + 2 * u) : float2{-INFINITY, 0.0f};
+            r.b[u] = ok ? ld2(op + (size_t)u * dk) : float2{0.0f, 0.0f};
         }
     }
+}
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// the lane's two elements of chunk c (zero past K)
+__device__ __forceinline__ float2 wave_row_values(const GPro &pro, int K, int c, int lane, WaveRow &r) {
+    const int e = 128 * c + 2 * lane;
+    const bool live = e < K;
+    if (pro.kind == GPRO_LN) {
+        if (!r.have) {
+            double s = 0.0, q = 0.0;
+#pragma unroll
+            for (int u = 0; u < PRO_XB; u++) {
+                s += (double)r.a[u].x + (double)r.a[u].y;
+                q += (double)r.a[u].x * (double)r.a[u].x + (double)r.a[u].y * (double)r.a[u].y;
+            }
+            for (int c0 = PRO_XB; 128 * c0 < K; c0 += PRO_XB)   // K > 1024: further batches
+#pragma unroll
+                for (int u = 0; u < PRO_XB; u++) {
+                    const int ee = 128 * (c0 + u) + 2 * lane;
+                    const float2 v = ee < K ? ld2(pro.x + ee) : float2{0.0f, 0.0f};
+                    s += (double)v.x + (double)v.y;
+                    q += (double)v.x * (double)v.x + (double)v.y * (double)v.y;
+                }
+            s = wave_sum(s);
+            q = wave_sum(q);
+            r.mu = s / K;
+            const double var = fmax(q / K - r.mu * r.mu, 0.0);
+            r.inv = (float)(1.0 / sqrt(var + 1e-5));
+            r.have = true;
+        }
+        if (!live) return float2{0.0f, 0.0f};
+        const float t0 = (float)(((double)r.xc.x - r.mu) * (double)r.inv);
+        const float t1 = (float)(((double)r.xc.y - r.mu) * (double)r.inv);
+        return float2{t0 * r.wc.x + r.bc.x, t1 * r.wc.y + r.bc.y};
+    }
+    const int dk = K / pro.H, h = live ? e / dk : 0, f = live ? e - h * dk : 0;
+    const int ns = min(mh_att_splits_dev(r.n), pro.nsplit);
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < PRO_MB; u++)
+        if (u < ns) Mx = fmaxf(Mx, r.a[u].x);
+    const float *ml = pro.ml + (size_t)h * pro.nsplit * 2;
+    const float *op = pro.opart + (size_t)h * pro.nsplit * dk + f;
+    for (int s0 = PRO_MB; s0 < ns; s0++) Mx = fmaxf(Mx, ml[2 * s0]);
+    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+    for (int u = 0; u < PRO_MB; u++)
+        if (u < ns) {
+            const float w = expf(r.a[u].x - Mx);
+            L += r.a[u].y * w;
+            o0 += r.b[u].x * w;
+            o1 += r.b[u].y * w;
+        }
+    for (int s0 = PRO_MB; s0 < ns; s0 += PRO_MB) {   // further splits, PRO_MB loads at a time
+        float2 mv[PRO_MB], ov[PRO_MB];
+#pragma unroll
+        for (int u = 0; u < PRO_MB; u++) {
+            mv[u] = s0 + u < ns ? ld2(ml + 2 * (s0 + u)) : float2{-INFINITY, 0.0f};
+            ov[u] = s0 + u < ns ? ld2(op + (size_t)(s0 + u) * dk) : float2{0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int u = 0; u < PRO_MB; u++)
+            if (s0 + u < ns) {
+                const float w = expf(mv[u].x - Mx);
+                L += mv[u].y * w;
+                o0 += ov[u].x * w;
+                o1 += ov[u].y * w;
+            }
+    }
+    if (!live) return float2{0.0f, 0.0f};
+    return float2{o0 / L, o1 / L};
 }
 
 // The epilogue operands of a one-row product (the decoder's), loaded when the
@@ -988,24 +1015,27 @@ __device__ __forceinline__ void gemv_body(const DevW &W, const float *__restrict
     };
     // (the waves w < WNG store column group w)
     const EpiPre pre = wave < WNG ? epi_pre(W, 32 * (bx * WNG + wave) + col, M, hh, ep) : EpiPre{0.0f, 0.0f};
-    if constexpr (PRO) {
-        // the first chunk's weight loads go out before the prologue builds the row
-        if (wave < Kc) load(wave);
-        __builtin_amdgcn_sched_barrier(0);
-        gemv_prologue<NW * 64>(pro, W.k, W.Kp, xs);
-        __syncthreads();
-    }
+    WaveRow wr;
+    if constexpr (PRO) wave_row_begin(pro, W.k, lane, wr);
     for (int c = wave; c < Kc; c += NW) {
         // x's chunk (a few KiB, in L2) goes out before the weights: vector
         // loads complete in issue order, so the split can start as soon as
         // x lands, while the weight bytes are still on their way
         float xv[HSTEPS][8];
         if constexpr (!PRO) load_chunk<VEC>(x, M, W.k, col, c, hh, xv);
+        else wave_row_issue(pro, W.k, c, lane, wr);
         __builtin_amdgcn_sched_barrier(0);
-        if (!PRO || c != wave) load(c);
+        load(c);
         __builtin_amdgcn_sched_barrier(0);
         XChunk xc;
-        if constexpr (PRO) {   // M = 1: row 0 from the prologue's row
+        if constexpr (PRO) {
+            // M = 1: row 0, formed by this wave; its 128 values go to the
+            // A-fragment layout (lanes 0 and 32) through the chunk's own LDS
+            const float2 val = wave_row_values(pro, W.k, c, lane, wr);
+            *(float2 *)(xs + 128 * c + 2 * lane) = val;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             float v[HSTEPS][8];
 #pragma unroll
             for (int u = 0; u < HSTEPS; u++)
@@ -1625,9 +1655,13 @@ static hipError_t launch_gemv1(const GJobs &J, const float *x, int M, const GPro
     return hipGetLastError();
 }
 
-template <int QT, int NW, int WNG>
+template <int QT, int NW, int WNG, bool WITH_PRO = true>
 static hipError_t launch_gemv(const GJobs &J, const float *x, int M, int vec, const GPro &pro, hipStream_t st) {
-    if (pro.kind != GPRO_NONE) return launch_gemv1<QT, NW, WNG, false, true>(J, x, M, pro, st);
+    if constexpr (WITH_PRO) {
+        if (pro.kind != GPRO_NONE) return launch_gemv1<QT, NW, WNG, false, true>(J, x, M, pro, st);
+    } else {
+        if (pro.kind != GPRO_NONE) return hipErrorInvalidValue;
+    }
     if (vec) return launch_gemv1<QT, NW, WNG, true, false>(J, x, M, pro, st);
     return launch_gemv1<QT, NW, WNG, false, false>(J, x, M, pro, st);
 }
@@ -1644,16 +1678,20 @@ template <int QT>
 static hipError_t gemv_t(const GJobs &J, const float *x, int M, int vec, const GPro &pro, hipStream_t st) {
     const DevW &W = J.W[0];
     const int Kc = W.Kp / 128, wng = gemv_wng(W);
-    if (wng == 2) {
-        if (Kc >= 8) return launch_gemv<QT, 8, 2>(J, x, M, vec, pro, st);
-        return launch_gemv<QT, 4, 2>(J, x, M, vec, pro, st);
+    // (f32 weights form their row with one column group per wave: the two
+    // f16 planes of two groups beside the row registers spill)
+    constexpr bool PRO2 = QT != QT_F32;
+    if (wng == 2 && (PRO2 || pro.kind == GPRO_NONE)) {
+        if (Kc >= 8) return launch_gemv<QT, 8, 2, PRO2>(J, x, M, vec, pro, st);
+        return launch_gemv<QT, 4, 2, PRO2>(J, x, M, vec, pro, st);
     }
     // K >= 4096 over few column groups: 16 waves take two chunks each rather
     // than 8 taking four (each chunk's loads wait a full memory latency);
     // within the 128 registers a 1024-thread workgroup allows, except the
-    // formats whose GEMV needs more (Q2_K spilled 60 registers there)
+    // formats whose GEMV needs more (Q2_K spilled 60 registers there), and
+    // except the row-forming form (its per-wave row registers)
     if constexpr (QT != QT_F32 && QT != QT_Q2_K && QT != QT_Q4_K && QT != QT_Q5_K && QT != QT_Q6_K)
-        if (Kc >= 32) return launch_gemv<QT, 16, 1>(J, x, M, vec, pro, st);
+        if (Kc >= 32 && pro.kind == GPRO_NONE) return launch_gemv<QT, 16, 1, false>(J, x, M, vec, pro, st);
     if (Kc >= 8) return launch_gemv<QT, 8, 1>(J, x, M, vec, pro, st);
     return launch_gemv<QT, 4, 1>(J, x, M, vec, pro, st);
 }
