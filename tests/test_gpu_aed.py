@@ -87,6 +87,9 @@ CASES = [
     (256, 4, 512, 1000, 2, 70, M.Q8_0, 128),     # head size 64, encoder projection
     (512, 4, 1024, 2048, 3, 130, M.Q4_K, None),  # K-quant linears, 3 splits of cross keys
     (256, 2, 2048, 500, 1, 20, M.Q8_0, None),    # ff2 with K = 2048: the split-K GEMV
+    # d = 2048: each wave forms two chunks of the row and sums the layer norm
+    # over two batches of x; 600 keys = 10 splits: the merge's second batch
+    (2048, 16, 2048, 700, 1, 600, M.Q8_0, None),
 ]
 
 
