@@ -118,6 +118,59 @@ def test_config2_f32_rows_bit_identical(gpu, orc, n, k):
         dw.close()
 
 
+# Benchmark config 5: one FastConformer-0.6B layer's linears at 16 x 750 rows
+# as the encoder calls them (encoder.c:901-946): the conv module's pointwise
+# 1024 -> 2048 (the one shape no other config has) against the oracle, the
+# FFN pair through qffn_dev and q/k/v through qqkv_dev, rows bit-identical at
+# every batch size.
+def test_config5_layer_linears_m12000(gpu, orc):
+    import torch
+    Mr = 16 * 750
+    say("config 5 Q8_0 layer linears M", Mr)
+    x = gpu.randn(1, 1.0, (Mr, 1024))
+    xd = torch.from_numpy(x).cuda()
+    rows = np.r_[0:16, 6000:6008, 11968:12000]
+    dws = []
+    try:
+        wp = M.Weight.make(gpu, M.Q8_0, gpu.randn(20, 0.02, (2048, 1024)))
+        pw1 = M.DeviceWeight(gpu, wp)
+        dws.append(pw1)
+        y = _gemm(torch, pw1, xd, Mr, 2048)
+        wd = orc.dequant(O.Q8_0, wp.data, 2048 * 1024).reshape(2048, 1024)
+        check_close_floor(y[rows], x[rows], wd, orc.gemm_f64(x[rows], wd), "Q8_0 1024->2048 M=12000")
+        for T in (750, 1):
+            assert np.array_equal(_gemm(torch, pw1, xd, T, 2048).view(np.uint32), y[:T].view(np.uint32)), T
+
+        w1 = M.DeviceWeight(gpu, M.Weight.make(gpu, M.Q8_0, gpu.randn(21, 0.02, (4096, 1024))))
+        w2 = M.DeviceWeight(gpu, M.Weight.make(gpu, M.Q8_0, gpu.randn(22, 0.02, (1024, 4096))))
+        dws += [w1, w2]
+
+        def ffn(T, src):
+            out = torch.full((T, 1024), float("nan"), dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+            M.ffn_dev(gpu, w1, w2, src.data_ptr(), out.data_ptr(), T)
+            torch.cuda.synchronize()
+            return out.cpu().numpy()
+        yf = ffn(Mr, xd)
+        assert np.isfinite(yf).all()
+        assert np.array_equal(ffn(750, xd).view(np.uint32), yf[:750].view(np.uint32)), "ffn M=750"
+        assert np.array_equal(ffn(1, xd[Mr - 1:]).view(np.uint32), yf[Mr - 1:].view(np.uint32)), "ffn last row"
+
+        qkv = [M.DeviceWeight(gpu, M.Weight.make(gpu, M.Q8_0, gpu.randn(23 + i, 0.02, (1024, 1024))))
+               for i in range(3)]
+        dws += qkv
+        ys = [torch.full((Mr, 1024), float("nan"), dtype=torch.float32, device="cuda") for _ in range(3)]
+        torch.cuda.synchronize()
+        M.qkv_dev(gpu, qkv, xd.data_ptr(), [t.data_ptr() for t in ys], Mr)
+        torch.cuda.synchronize()
+        for i in range(3):
+            single = _gemm(torch, qkv[i], xd, Mr, 1024)
+            assert np.array_equal(ys[i].cpu().numpy().view(np.uint32), single.view(np.uint32)), f"qkv output {i}"
+    finally:
+        for dw in dws:
+            dw.close()
+
+
 # ---------------------------------------------------- backend.h f32 entries
 def _ptr(a):
     return a.ctypes.data_as(C.c_void_p)
