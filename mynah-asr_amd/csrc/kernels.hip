@@ -824,7 +824,7 @@ __global__ __launch_bounds__(256) void k_gemm_fold(GemmJobs J, const float *__re
 //
 //   GPRO_LN   (float)(((double)x - mean) * (double)inv) * w + b with inv =
 //             (float)(1 / sqrt(var + 1e-5)), mean and var over the K values in
-//             double (decoder_aed.c:21-28; the sums in one pass)
+//             double, two passes (decoder_aed.c:21-28)
 //   GPRO_COMB the attention splits of the element's head merged:
 //             sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M), in split order
 constexpr int PRO_XB = 8;   // chunks of x per batch of the layer-norm sums (1024 values)
@@ -891,25 +891,36 @@ __device__ __forceinline__ float2 wave_row_values(const GPro &pro, int K, int c,
     const bool live = e < K;
     if (pro.kind == GPRO_LN) {
         if (!r.have) {
-            double s = 0.0, q = 0.0;
+            // two passes in double, as ln(): the mean, then the sum of (x - mean)^2
+            double s = 0.0;
 #pragma unroll
-            for (int u = 0; u < PRO_XB; u++) {
-                s += (double)r.a[u].x + (double)r.a[u].y;
-                q += (double)r.a[u].x * (double)r.a[u].x + (double)r.a[u].y * (double)r.a[u].y;
-            }
+            for (int u = 0; u < PRO_XB; u++) s += (double)r.a[u].x + (double)r.a[u].y;
             for (int c0 = PRO_XB; 128 * c0 < K; c0 += PRO_XB)   // K > 1024: further batches
 #pragma unroll
                 for (int u = 0; u < PRO_XB; u++) {
                     const int ee = 128 * (c0 + u) + 2 * lane;
                     const float2 v = ee < K ? ld2(pro.x + ee) : float2{0.0f, 0.0f};
                     s += (double)v.x + (double)v.y;
-                    q += (double)v.x * (double)v.x + (double)v.y * (double)v.y;
                 }
-            s = wave_sum(s);
-            q = wave_sum(q);
-            r.mu = s / K;
-            const double var = fmax(q / K - r.mu * r.mu, 0.0);
-            r.inv = (float)(1.0 / sqrt(var + 1e-5));
+            r.mu = wave_sum(s) / K;
+            double q = 0.0;
+#pragma unroll
+            for (int u = 0; u < PRO_XB; u++)
+                if (128 * u + 2 * lane < K) {
+                    const double d0 = (double)r.a[u].x - r.mu, d1 = (double)r.a[u].y - r.mu;
+                    q += d0 * d0 + d1 * d1;
+                }
+            for (int c0 = PRO_XB; 128 * c0 < K; c0 += PRO_XB)
+#pragma unroll
+                for (int u = 0; u < PRO_XB; u++) {
+                    const int ee = 128 * (c0 + u) + 2 * lane;
+                    if (ee < K) {
+                        const float2 v = ld2(pro.x + ee);
+                        const double d0 = (double)v.x - r.mu, d1 = (double)v.y - r.mu;
+                        q += d0 * d0 + d1 * d1;
+                    }
+                }
+            r.inv = (float)(1.0 / sqrt(wave_sum(q) / K + 1e-5));
             r.have = true;
         }
         if (!live) return float2{0.0f, 0.0f};
