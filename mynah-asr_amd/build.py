@@ -33,14 +33,14 @@ HIP_FLAGS = ["-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC", "-ffp-contra
              "-Wall", "-Wno-unused-function", "-I", INC, "-I", CSRC]
 
 
-def _run(cmd: list[str]) -> list[str]:
-    """Runs one compiler command; returns the kernels that spill registers
-    (from the kernel-resource-usage remarks, which are not echoed)."""
-    r = subprocess.run(cmd, capture_output=True, text=True)
+def _check(cmd: list[str], returncode: int, stderr: str) -> list[str]:
+    """One finished compiler command: raises on failure, echoes its warnings,
+    returns the kernels that spill registers (from the kernel-resource-usage
+    remarks, which are not echoed)."""
     # hipcc's host pass warns that it does not know the packed-fp32 feature: harmless
     noise = "is not a recognized feature for this target"
     lines, spills, kernel, in_remark = [], [], "", False
-    for l in r.stderr.splitlines():
+    for l in stderr.splitlines():
         if "remark:" in l and "kernel-resource-usage" in l:
             in_remark = True
             body = l.split("remark:", 1)[1].strip()
@@ -55,7 +55,7 @@ def _run(cmd: list[str]) -> list[str]:
         if noise not in l:
             lines.append(l)
     err = "\n".join(lines)
-    if r.returncode != 0:
+    if returncode != 0:
         sys.stderr.write(err + "\n")
         raise RuntimeError(f"build failed: {' '.join(cmd[:3])} ...")
     if err.strip():
@@ -63,15 +63,26 @@ def _run(cmd: list[str]) -> list[str]:
     return spills
 
 
+def _run(cmd: list[str]) -> list[str]:
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    return _check(cmd, r.returncode, r.stderr)
+
+
 def build_hip() -> str:
     os.makedirs(LIB, exist_ok=True)
     srcs = [os.path.join(CSRC, f) for f in ("kernels.hip", "attention.hip", "decoder.hip", "backend.cpp", "repack.cpp")]
     objs = []
-    spills = []
+    # the units compile side by side (each hipcc runs one device pass)
+    jobs = []
     for s in srcs:
         o = os.path.join(LIB, os.path.basename(s) + ".o")
-        spills += _run([HIPCC, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-x", "hip", "-c", s, "-o", o])
+        cmd = [HIPCC, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-x", "hip", "-c", s, "-o", o]
+        jobs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE, text=True)))
         objs.append(o)
+    spills = []
+    for cmd, pr in jobs:
+        _, err = pr.communicate()
+        spills += _check(cmd, pr.returncode, err)
     # a kernel that spills runs from scratch memory: say which, so a change
     # that pushes one over its register budget does not go unnoticed
     for k in spills:

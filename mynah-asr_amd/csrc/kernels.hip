@@ -1666,7 +1666,9 @@ static hipError_t launch_gemv1(const GJobs &J, const float *x, int M, const GPro
     return hipGetLastError();
 }
 
-template <int QT, int NW, int WNG, bool WITH_PRO = true>
+// WITH_PRO / WITH_SCALAR: whether the row-forming form and the form for
+// unaligned x (element loads) exist at this shape (callers route around them)
+template <int QT, int NW, int WNG, bool WITH_PRO = true, bool WITH_SCALAR = true>
 static hipError_t launch_gemv(const GJobs &J, const float *x, int M, int vec, const GPro &pro, hipStream_t st) {
     if constexpr (WITH_PRO) {
         if (pro.kind != GPRO_NONE) return launch_gemv1<QT, NW, WNG, false, true>(J, x, M, pro, st);
@@ -1674,7 +1676,8 @@ static hipError_t launch_gemv(const GJobs &J, const float *x, int M, int vec, co
         if (pro.kind != GPRO_NONE) return hipErrorInvalidValue;
     }
     if (vec) return launch_gemv1<QT, NW, WNG, true, false>(J, x, M, pro, st);
-    return launch_gemv1<QT, NW, WNG, false, false>(J, x, M, pro, st);
+    if constexpr (WITH_SCALAR) return launch_gemv1<QT, NW, WNG, false, false>(J, x, M, pro, st);
+    return hipErrorInvalidValue;
 }
 
 // column groups per GEMV workgroup: two for wide outputs, so that each chunk
@@ -1699,10 +1702,11 @@ static hipError_t gemv_t(const GJobs &J, const float *x, int M, int vec, const G
     // K >= 4096 over few column groups: 16 waves take two chunks each rather
     // than 8 taking four (each chunk's loads wait a full memory latency);
     // within the 128 registers a 1024-thread workgroup allows, except the
-    // formats whose GEMV needs more (Q2_K spilled 60 registers there), and
-    // except the row-forming form (its per-wave row registers)
+    // formats whose GEMV needs more (Q2_K spilled 60 registers there), the
+    // row-forming form (its per-wave row registers) and unaligned x (Q8_0's
+    // element loads spilled 4)
     if constexpr (QT != QT_F32 && QT != QT_Q2_K && QT != QT_Q4_K && QT != QT_Q5_K && QT != QT_Q6_K)
-        if (Kc >= 32 && pro.kind == GPRO_NONE) return launch_gemv<QT, 16, 1, false>(J, x, M, vec, pro, st);
+        if (Kc >= 32 && pro.kind == GPRO_NONE && vec) return launch_gemv<QT, 16, 1, false, false>(J, x, M, vec, pro, st);
     if (Kc >= 8) return launch_gemv<QT, 8, 1>(J, x, M, vec, pro, st);
     return launch_gemv<QT, 4, 1>(J, x, M, vec, pro, st);
 }
