@@ -473,11 +473,12 @@ __global__ __launch_bounds__(256, (gemm_occ<QT, EPI, A1, WN, WM>())) void k_gemm
                                                  float *__restrict__ part, int ksplit, int ngrp) {
     using F = Fmt<QT>;
     // the weight planes go straight to registers, one stage ahead (measured
-    // 3-6% faster than through LDS on every format: less LDS traffic);
-    // f32 weights' two f16 planes stay in LDS, and so do the planes of the
-    // split-K form (its chunk-result stores leave no registers for them:
-    // with them it spilled, and 4096->1024 at 750 rows took 129 us, not 50)
-    constexpr bool BD = QT != QT_F32 && EPI != EPI_PART;
+    // 3-6% faster than through LDS on every format: less LDS traffic), except
+    // in the split-K form (its chunk-result stores leave no registers for
+    // them: with them it spilled, and 4096->1024 at 750 rows took 129 us, not
+    // 50) and, for f32 weights, in the FFN's fused form (its epilogue's LDS
+    // tile needs the larger stages)
+    constexpr bool BD = EPI != EPI_PART && (QT != QT_F32 || EPI == EPI_Y);
     using L = StageLayout<QT, A1, 4 * WN, WM, BD>;
     typename F::RawK rb[2][WN][L::SPS];   // BD: the weight planes of the stage in flight and the current one
     static_assert(!(A1 && EPI == EPI_PREP), "the fused FFN hand-off is EXACT only");
