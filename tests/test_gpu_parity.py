@@ -165,6 +165,25 @@ def test_gemm_zero_and_tiny_rows(gpu, orc):
         check_close((y[r] / np.float32(scale)).astype(np.float32), ref[r] / scale, f"row {r}")
 
 
+@pytest.mark.parametrize("T", [3, 40])
+def test_gemm_nonfinite_rows_stay_in_their_rows(gpu, orc, T):
+    """A row holding NaN or +-inf gives non-finite outputs (NaN for a NaN, as
+    the f32 product; for an infinity the f32 product's +-inf or NaN, here NaN:
+    the infinity's f16 pair is inf + NaN) and leaves every other row's bits
+    as they are without it (GEMV at T = 3, GEMM at T = 40)."""
+    say("gemm non-finite rows T", T)
+    w = M.Weight.make(gpu, M.Q8_0, gpu.randn(0, 0.02, (64, 512)))
+    x = gpu.randn(1, 1.0, (T, 512))
+    clean = M.host_qgemm(gpu, w, x, keep=True)
+    x[0, 7] = np.nan
+    x[2, 300] = np.inf
+    y = M.host_qgemm(gpu, w, x)
+    assert np.isnan(y[0]).all()
+    assert not np.isfinite(y[2]).any()
+    others = [r for r in range(T) if r not in (0, 2)]
+    assert np.array_equal(y[others].view(np.uint32), clean[others].view(np.uint32))
+
+
 @pytest.mark.parametrize("n,k", [(1024, 4096), (4096, 1024), (16384, 1024)])
 @pytest.mark.parametrize("qt", [M.Q8_0, M.Q4_0], ids=lambda q: M.NAMES[q])
 def test_decoder_gemv_shapes(gpu, orc, qt, n, k):
