@@ -97,19 +97,23 @@ __global__ __launch_bounds__(LN_T) void k_embed_ln(const float *__restrict__ emb
 }
 
 // Workgroup (head h, split s) over keys [s*KC, min((s+1)*KC, n)), n = n_fixed,
-// or p + 1 for self attention (n_fixed = 0). 256 threads: for the scores, 4
-// threads per key (dk/4 features each); for the values, thread = (feature,
-// key group). Writes o[h][s][dk] (unnormalised) and ml[h][s] = (max, sum).
+// or p + 1 for self attention (n_fixed = 0). Four waves, wave w the keys
+// 16w .. 16w+15 of the split: for the scores 4 lanes per key (DK/4 features
+// each, q read by every lane from global); for the values lane = features
+// DK/64 per lane over the wave's 16 keys. Two workgroup barriers: the waves'
+// score maxima, then their partial outputs and sums, which wave 0 adds in
+// wave order. Writes o[h][s][dk] (unnormalised) and ml[h][s] = (max, sum).
 template <int DK>
 __global__ __launch_bounds__(256) void k_att_part(const float *__restrict__ q, float *K, float *V,
                                                   const float *__restrict__ kn, const float *__restrict__ vn,
                                                   const int *__restrict__ st, int n_fixed, int d, float scale,
                                                   float *__restrict__ o_part, float *__restrict__ ml_part,
                                                   int nsplit) {
-    __shared__ float qs[DK];
-    __shared__ float sc[KC];
-    __shared__ float red[256 / DK][DK];
-    const int h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
+    static_assert(KC == 64, "four waves of 16 keys");
+    constexpr int FPL = DK / 64;   // value features per lane
+    __shared__ float wm[4], wl[4];
+    __shared__ float wo[4][DK];
+    const int h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int ho = h * DK;
     const int p = n_fixed > 0 ? -1 : st[0];   // (cross attention does not wait for st)
     const int n = n_fixed > 0 ? n_fixed : p + 1;
@@ -122,80 +126,73 @@ __global__ __launch_bounds__(256) void k_att_part(const float *__restrict__ q, f
         return;
     }
     const bool append = n_fixed == 0 && p >= j0 && p < j1;
-    if (append && tid < DK) {   // this step's k, v rows join the cache (read back below from kn, vn)
+    if (append && tid < DK) {   // this step's k, v rows join the cache (read below from kn, vn)
         K[(size_t)p * d + ho + tid] = kn[ho + tid];
         V[(size_t)p * d + ho + tid] = vn[ho + tid];
     }
-    if (tid < DK) qs[tid] = q[ho + tid];
-    // the V values this thread weighs later (feature tid % DK, keys tid / DK
-    // + G t): loaded now, so their latency overlaps the scores
-    constexpr int G = 256 / DK;
-    const int f = tid % DK, g = tid / DK, cnt = j1 - j0;
-    float vv[KC / G];
+    const int cnt = j1 - j0;
+    // the V values of this lane's features for the wave's 16 keys, loaded now
+    // so that their latency overlaps the scores
+    float vv[16][FPL];
 #pragma unroll
-    for (int t = 0; t < KC / G; t++) {
-        const int jj = g + G * t, j = j0 + jj;
-        vv[t] = 0.0f;
-        if (jj < cnt) vv[t] = ((append && j == p) ? vn + ho : V + (size_t)j * d + ho)[f];
+    for (int t = 0; t < 16; t++) {
+        const int jj = 16 * w + t, j = j0 + jj;
+        const float *vr = (append && j == p) ? vn + ho : V + (size_t)j * d + ho;
+#pragma unroll
+        for (int i = 0; i < FPL; i++) vv[t][i] = jj < cnt ? vr[lane + 64 * i] : 0.0f;
     }
-    // scores: key j0 + (tid >> 2), features (tid & 3) * DK/4 ..; the key row
-    // is loaded before the barrier, with the V values
-    {
-        const int jj = tid >> 2, part = tid & 3, j = j0 + jj;
-        float4 kv[DK / 16];
-        if (j < j1) {
-            const float *kr = (append && j == p) ? kn + ho : K + (size_t)j * d + ho;
+    // scores: key 16w + (lane >> 2), features (lane & 3) * DK/4 ..
+    const int kq = lane >> 2, part = lane & 3, jj = 16 * w + kq, j = j0 + jj;
+    const bool live = jj < cnt;
+    float acc = 0.0f;
+    if (live) {
+        const float *kr = (append && j == p) ? kn + ho : K + (size_t)j * d + ho;
 #pragma unroll
-            for (int i = 0; i < DK / 16; i++) kv[i] = *(const float4 *)(kr + part * (DK / 4) + 4 * i);
+        for (int i = 0; i < DK / 16; i++) {
+            const float4 kv = *(const float4 *)(kr + part * (DK / 4) + 4 * i);
+            const float4 qv = *(const float4 *)(q + ho + part * (DK / 4) + 4 * i);
+            acc = fmaf(qv.x, kv.x, acc);
+            acc = fmaf(qv.y, kv.y, acc);
+            acc = fmaf(qv.z, kv.z, acc);
+            acc = fmaf(qv.w, kv.w, acc);
         }
-        __syncthreads();
-        float acc = 0.0f;
-        if (j < j1) {
+    }
+    acc += __shfl_xor(acc, 1, 64);
+    acc += __shfl_xor(acc, 2, 64);
+    const float sc = live ? scale * acc : -INFINITY;
+    // the split's maximum: the wave's (every lane of a key holds its score), then the workgroup's
+    float m = sc;
 #pragma unroll
-            for (int i = 0; i < DK / 16; i++) {
-                const float *qq = qs + part * (DK / 4) + 4 * i;
-                acc = fmaf(qq[0], kv[i].x, acc);
-                acc = fmaf(qq[1], kv[i].y, acc);
-                acc = fmaf(qq[2], kv[i].z, acc);
-                acc = fmaf(qq[3], kv[i].w, acc);
-            }
+    for (int o = 4; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if (lane == 0) wm[w] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    const float e = live ? expf(sc - m) : 0.0f;
+    float l = part == 0 ? e : 0.0f;   // one lane per key
+#pragma unroll
+    for (int o = 4; o < 64; o <<= 1) l += __shfl_xor(l, o, 64);
+    // values: this lane's features over the wave's keys, in key order
+    float o[FPL];
+#pragma unroll
+    for (int i = 0; i < FPL; i++) o[i] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 16; t++) {
+        const float pt = __shfl(e, 4 * t, 64);   // (zero past cnt)
+#pragma unroll
+        for (int i = 0; i < FPL; i++) o[i] = fmaf(pt, vv[t][i], o[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < FPL; i++) wo[w][lane + 64 * i] = o[i];
+    if (lane == 0) wl[w] = l;
+    __syncthreads();
+    if (w == 0) {
+#pragma unroll
+        for (int i = 0; i < FPL; i++) {
+            const int f = lane + 64 * i;
+            op[f] = ((wo[0][f] + wo[1][f]) + wo[2][f]) + wo[3][f];
         }
-        acc += __shfl_xor(acc, 1, 64);
-        acc += __shfl_xor(acc, 2, 64);
-        if (part == 0 && jj < KC) sc[jj] = j < j1 ? scale * acc : -INFINITY;
+        if (lane == 0) mlp[0] = m, mlp[1] = ((wl[0] + wl[1]) + wl[2]) + wl[3];
     }
-    __syncthreads();
-    // max and sum of exponentials over the split: one wave, one key per lane
-    static_assert(KC == 64, "one key per lane of a wave");
-    __shared__ float mls[2];
-    if (tid < 64) {
-        float m = sc[tid];
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        const float e = tid < j1 - j0 ? expf(sc[tid] - m) : 0.0f;
-        sc[tid] = e;
-        float l = e;
-        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
-        if (tid == 0) mls[0] = m, mls[1] = l;
-    }
-    __syncthreads();
-    // values: feature f, keys g + G t
-    {
-        float acc = 0.0f;
-#pragma unroll
-        for (int t = 0; t < KC / G; t++) {
-            const int jj = g + G * t;
-            if (jj < cnt) acc = fmaf(sc[jj], vv[t], acc);
-        }
-        red[g][f] = acc;
-    }
-    __syncthreads();
-    if (tid < DK) {
-        float o = 0.0f;
-#pragma unroll
-        for (int g = 0; g < 256 / DK; g++) o += red[g][tid];
-        op[tid] = o;
-    }
-    if (tid == 0) mlp[0] = mls[0], mlp[1] = mls[1];
 }
 
 // out[h] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M) over the used splits
