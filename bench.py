@@ -263,6 +263,39 @@ def run_config5(B, M_, reps=3):
                     "conv, batch norm, residuals and subsampling are outside this build); RTF over 960 s of audio"}
 
 
+def read_floor_us(B, nbytes, copies):
+    """The one-launch floor for nbytes: a plain streaming read of that many
+    bytes (mynah_asr_hip_read_floor_dev, no compute), over `copies` distinct
+    buffers in turn, replayed from one HIP graph as the GEMVs are."""
+    torch = B.torch
+    try:
+        buf = torch.empty(copies * nbytes // 4, dtype=torch.float32, device="cuda")
+        buf.zero_()
+        g = torch.cuda.CUDAGraph()
+        cs = torch.cuda.Stream()
+        with torch.cuda.graph(g, stream=cs):
+            for i in range(copies):
+                B.lib.read_floor(buf.data_ptr() + i * nbytes, nbytes, cs.cuda_stream)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(cs):
+            g.replay()
+            B.sync()
+            e0.record(cs)
+            for _ in range(3):
+                g.replay()
+            e1.record(cs)
+        B.sync()
+        us = e0.elapsed_time(e1) / (3 * copies) * 1e3
+        del g, buf
+        return round(us, 2)
+    except Exception as ex:
+        log(f"[bench] read floor not measured ({ex})")
+        return None
+
+
+floor = {}
+
+
 def run_gemv(B, M_, qt, n, k, Ms, min_bytes=512 << 20, max_copies=512):
     lib = B.lib
     w = M_.Weight.make(lib, qt, lib.randn(0, 0.02, (n, k)))
@@ -307,7 +340,11 @@ def run_gemv(B, M_, qt, n, k, Ms, min_bytes=512 << 20, max_copies=512):
         except Exception as ex:  # keep the stream figure
             log(f"[bench] graph capture failed ({ex}); GEMV time from stream launches")
         nbytes = wb + 4.0 * M * k + 4.0 * M * n
+        fus = floor.get(int(nbytes) // 16 * 16)
+        if fus is None:
+            fus = floor[int(nbytes) // 16 * 16] = read_floor_us(B, int(nbytes) // 16 * 16, copies)
         out.append({"format": M_.NAMES[qt], "M": M, "k": k, "n": n, "copies": copies,
+                    "read_floor_us": fus, "kernel_vs_floor": round(fus / (kms * 1e3), 3) if fus else None,
                     "rotated_mb": round(copies * wb / 2**20), "kernel_us": round(kms * 1e3, 2),
                     "call_us": round(call_ms * 1e3, 2),
                     "kernel_gbps": round(nbytes / (kms * 1e-3) / 1e9, 1),
@@ -742,6 +779,9 @@ def main():
         details["gemv"] = gv
         big = [g for g in gv if g["n"] * g["k"] >= 4 << 20]
         details["gemv_hbm_frac_mean_large"] = round(float(np.mean([g["kernel_hbm_frac"] for g in big])), 4)
+        vf = [g["kernel_vs_floor"] for g in big if g.get("kernel_vs_floor")]
+        if vf:   # the same GEMVs against a plain streaming read of their bytes, one launch each
+            details["gemv_vs_read_floor_mean_large"] = round(float(np.mean(vf)), 3)
         log("[bench] few-row products (one stream)")
         details["gemm_small_m"] = run_small_m(B, M_)
         log("[bench] config 5: one encoder layer's built parts at M=12000")

@@ -177,6 +177,11 @@ int mynah_asr_hip_qgemm_noalloc_dev(const mynah_asr_hip_weight *w, const float *
 size_t mynah_asr_hip_noalloc_bytes(const mynah_asr_hip_weight *w, int T);
 /* dwd[n,k] = dequantized weight. */
 int mynah_asr_hip_dequant_dev(const mynah_asr_hip_weight *w, float *dwd, void *stream);
+/* No counterpart in the reference: a measurement aid for benchmarks. One
+ * launch that streams `bytes` from device memory at p (16-byte aligned, size a
+ * multiple of 16) and computes nothing from them: the one-launch floor a
+ * memory-bound product over the same bytes (a decoder GEMV) is compared with. */
+int mynah_asr_hip_read_floor_dev(const void *p, size_t bytes, void *stream);
 
 /* Relative-position self-attention core of one encoder layer on device buffers:
  * the computation of src/encoder.c:315-410 (left < 0, full attention) and

@@ -805,6 +805,15 @@ int mynah_asr_hip_dequant_dev(const mynah_asr_hip_weight *w, float *dwd, void *s
     return 0;
 }
 
+int mynah_asr_hip_read_floor_dev(const void *p, size_t bytes, void *stream) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    if (!p || ((uintptr_t)p & 15) || (bytes & 15)) return fail("bad argument: 16-byte aligned pointer and size");
+    hipError_t e = mh_launch_read_floor(p, bytes, pick_stream(stream));
+    if (e != hipSuccess) return fail("read launch failed", hipGetErrorString(e));
+    return 0;
+}
+
 int mynah_asr_hip_relpos_attention_dev(const float *q, const float *k, const float *v, const float *rk,
                                        const float *bias_u, const float *bias_v, float *ctx, int T, int d,
                                        int H, int left, int right, int nseq, void *stream) {

@@ -1624,6 +1624,24 @@ __global__ void k_silu(float *__restrict__ x, size_t n) {
 
 #include "launch.h"
 
+// A plain streaming read of `n4` float4 (the one-launch floor a memory-bound
+// kernel of the same bytes is measured against: no compute, nothing written
+// unless the data sum to a value they never do). Four loads per thread per
+// round, all issued before their sums.
+__device__ float g_read_sink;
+__global__ __launch_bounds__(256) void k_read_floor(const float4 *__restrict__ p, size_t n4) {
+    const size_t stride = (size_t)gridDim.x * 256;
+    float s = 0.0f;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += 4 * stride) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = i + u * stride < n4 ? p[i + u * stride] : float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 4; u++) s += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+    }
+    if (s == -1.2345e-37f) g_read_sink = s;
+}
+
 template <typename F>
 static hipError_t allow_lds(F *f) {
     // dynamic LDS beyond 64 KiB: gfx950 has 160 KiB, less the prologue's static
@@ -1939,6 +1957,16 @@ hipError_t mh_launch_gemm_prep_out(int qtype, const DevW &W, const uint8_t *xp, 
     J.W[0] = J.W[1] = J.W[2] = W;
     J.n = 1;
     MH_DISPATCH(gemm_t, qtype, J, xp, xs16, xpf, M, 1, &po, nullptr, st)
+}
+
+hipError_t mh_launch_read_floor(const void *p, size_t bytes, hipStream_t st) {
+    const size_t n4 = bytes / 16;
+    if (n4 == 0) return hipSuccess;
+    // enough threads for four float4 each per round, at most 2048 workgroups
+    const size_t wgs = (n4 + 4 * 256 - 1) / (4 * 256);
+    hipLaunchKernelGGL(k_read_floor, dim3((unsigned)(wgs < 2048 ? wgs : 2048)), dim3(256), 0, st,
+                       (const float4 *)p, n4);
+    return hipGetLastError();
 }
 
 hipError_t mh_launch_prep(const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,

@@ -82,6 +82,8 @@ hipError_t mh_launch_gemm_prep_out(int qtype, const DevW &W, const uint8_t *xp, 
                                    const float *xpf, int M, uint8_t *oxp, float *oxs16, float *oxpf, int oKc,
                                    int oxsum, hipStream_t st);
 hipError_t mh_launch_dequant(int qtype, const DevW &W, float *out, hipStream_t st);
+// a plain streaming read of `bytes` (16-byte aligned), nothing written
+hipError_t mh_launch_read_floor(const void *p, size_t bytes, hipStream_t st);
 hipError_t mh_launch_silu(float *x, size_t n, hipStream_t st);
 
 // INT8ACT numerics (every format but F32). Three activation forms:

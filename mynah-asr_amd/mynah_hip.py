@@ -39,7 +39,7 @@ HIP_SYMBOLS = [
     "mynah_asr_hip_qgemm_prepped_dev", "mynah_asr_hip_qffn_dev", "mynah_asr_hip_qqkv_dev",
     "mynah_asr_hip_relpos_attention_dev", "mynah_asr_hip_relpos_attention",
     "mynah_asr_hip_aed_decode_dev", "mynah_asr_hip_aed_forced_dev",
-    "mynah_asr_hip_qgemm_noalloc_dev", "mynah_asr_hip_noalloc_bytes",
+    "mynah_asr_hip_qgemm_noalloc_dev", "mynah_asr_hip_noalloc_bytes", "mynah_asr_hip_read_floor_dev",
 ]
 HOST_SYMBOLS = [
     "mynah_asr_set_backend", "mynah_asr_backend", "mynah_asr_gemm_wt", "mynah_asr_silu",
@@ -124,6 +124,8 @@ class HipLib:
             L.mynah_asr_hip_qgemm_noalloc_dev.argtypes = [_P, _P, _P, C.c_int, C.c_int, _P]
             L.mynah_asr_hip_noalloc_bytes.restype = C.c_size_t
             L.mynah_asr_hip_noalloc_bytes.argtypes = [_P, C.c_int]
+        if hasattr(L, "mynah_asr_hip_read_floor_dev"):
+            L.mynah_asr_hip_read_floor_dev.argtypes = [_P, C.c_size_t, _P]
         if hasattr(L, "mynah_asr_hip_prep_dev"):  # absent from older builds
             L.mynah_asr_hip_prep_dev.argtypes = [_P, _P, C.c_int, _P]
             L.mynah_asr_hip_qgemm_prepped_dev.argtypes = [_P, _P, C.c_int, C.c_int, _P]
@@ -180,6 +182,10 @@ class HipLib:
 
     def last_error(self) -> str:
         return self.L.mynah_asr_hip_last_error().decode()
+
+    def read_floor(self, ptr: int, nbytes: int, stream: int = 0) -> None:
+        """One streaming read of nbytes at a device pointer (a measurement aid)."""
+        self._check(self.L.mynah_asr_hip_read_floor_dev(ptr, nbytes, stream or None), "read_floor_dev")
 
     def set_numerics(self, mode: int) -> int:
         return self.L.mynah_asr_hip_set_numerics(mode)
