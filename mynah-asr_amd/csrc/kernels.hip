@@ -880,9 +880,25 @@ __device__ __forceinline__ void wave_row_issue(const GPro &pro, int K, int c, in
     }
 }
 
+// a double moved between lanes by one DPP pattern (its two halves)
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double x) {
+    const long long b = __double_as_longlong(x);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)b, CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, 0xF, 0xF, false);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+// The wave's sum in every lane: within each row of 16 lanes by DPP (swap
+// neighbours, swap pairs, mirror within 8, mirror within 16: each step adds
+// two values symmetrically, so every lane holds the same sum), then across
+// the four rows.
 __device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v += dpp_d<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_d<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_d<0x141>(v);   // row_half_mirror
+    v += dpp_d<0x140>(v);   // row_mirror
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
     return v;
 }
 
