@@ -167,7 +167,7 @@ def run_int8act(B, M_, M):
         for name, qt, MM, shapes, seed in (("int8act_q8_0_m6000", M_.Q8_0, M, ENC_SHAPES, 0),
                                            ("int8act_q4_k_m12000", M_.Q4_K, 12000, KQ_SHAPES, 100),
                                            ("int8act_q5_k_m12000", M_.Q5_K, 12000, KQ_SHAPES, 100)):
-            log(f"[bench] INT8ACT numerics, {name}")
+            log(f"[bench] {name}")
             ms8, fl8, rows8 = run_encoder_set(B, M_, qt, MM, shapes, 5, 2, seed)
             tops = fl8 / (ms8 * 1e-3) / 1e12
             for r in rows8:
@@ -357,7 +357,7 @@ def run_gemv(B, M_, qt, n, k, Ms, min_bytes=512 << 20, max_copies=512):
 def host_cpu() -> dict:
     """The host's CPU model, the logical CPUs this process may use, and the
     physical cores among them (from /proc/cpuinfo)."""
-    model, cores, allowed = "unknown", set(), sorted(os.sched_getaffinity(0))
+    model, cores, allowed, ids = "unknown", set(), sorted(os.sched_getaffinity(0)), {}
     try:
         phys = core = proc = None
         for line in open("/proc/cpuinfo"):
@@ -367,6 +367,8 @@ def host_cpu() -> dict:
                 proc = int(v)
             elif k == "model name":
                 model = v
+            elif k in ("vendor_id", "cpu family", "model", "stepping") and k not in ids:
+                ids[k] = v
             elif k == "physical id":
                 phys = v
             elif k == "core id":
@@ -375,7 +377,9 @@ def host_cpu() -> dict:
                     cores.add((phys, core))
     except OSError:
         pass
-    return {"model": model, "logical_cpus": len(allowed), "physical_cores": len(cores) or None}
+    # the model name a VM reports can be bare ("AMD EPYC"); family/model/stepping pin the part
+    cpuid = " ".join(f"{k}={v}" for k, v in ids.items())
+    return {"model": model, "cpuid": cpuid, "logical_cpus": len(allowed), "physical_cores": len(cores) or None}
 
 
 def _median_time(fn, budget_s, max_reps=5, min_reps=1):
@@ -474,12 +478,20 @@ def cpu_baseline(M_, lib, seconds_budget=20.0):
             xg = lib.randn(1, 1.0, (16, k))
             for Mg in (1, 4, 16):
                 t_s, _ = _median_time(lambda: np.matmul(xg[:Mg], wf.T), 0.3, max_reps=20, min_reps=5)
-                t_i, _ = _median_time(lambda: R.kernel("ingot_q8_0_matmat", raw, n, k, xg[:Mg]), 0.3, max_reps=20,
-                                      min_reps=5)
                 qb = M_.weight_bytes(M_.Q8_0, n, k) + 4.0 * Mg * (k + n)
-                gemv_cpu.append({"M": Mg, "k": k, "n": n, "sgemv_f32_us": round(t_s * 1e6, 1),
-                                 "ingot_q8_0_us": round(t_i * 1e6, 1),
-                                 "ingot_q8_0_gbps": round(qb / t_i / 1e9, 1)})
+                row = {"M": Mg, "k": k, "n": n, "sgemv_f32_us": round(t_s * 1e6, 1)}
+                # ingot's own thread split (a persistent pool: no thread
+                # creation per call); M = 1 is its serial matvec at any count
+                for th in (1, host["logical_cpus"]):
+                    R.set_threads(th)
+                    R.kernel("ingot_q8_0_matmat", raw, n, k, xg[:Mg])
+                    t_i, _ = _median_time(lambda: R.kernel("ingot_q8_0_matmat", raw, n, k, xg[:Mg]), 0.3,
+                                          max_reps=20, min_reps=5)
+                    tag = "1t" if th == 1 else f"{th}t"
+                    row[f"ingot_q8_0_{tag}_us"] = round(t_i * 1e6, 1)
+                    row[f"ingot_q8_0_{tag}_gbps"] = round(qb / t_i / 1e9, 2)
+                gemv_cpu.append(row)
+        R.set_threads(host["logical_cpus"])
     # the AED step's linears at M = 1 through sgemv (4 layers of 6 x 1024^2 +
     # 1024x4096 + 4096x1024, then the 16384-row head): the CPU floor of a step
     sg = {(g["k"], g["n"]): g["sgemv_f32_us"] for g in gemv_cpu if g["M"] == 1}
@@ -490,12 +502,32 @@ def cpu_baseline(M_, lib, seconds_budget=20.0):
             "kind": kind, "host": host,
             "sample": f"{reps} whole steps (7 GEMMs at M=6000, median {med*1e3:.0f} ms): "
                       f"{decoder} once + OpenBLAS sgemm per product, {threads} BLAS threads on "
-                      f"{host['logical_cpus']} logical CPUs ({host['physical_cores']} physical cores) of {host['model']}",
+                      f"{host['logical_cpus']} logical CPUs ({host['physical_cores']} physical cores) of {host['model']} ({host['cpuid']})",
+            "sample_short": f"{reps} steps (7 GEMMs, M=6000): ingot dequant once + OpenBLAS sgemm, "
+                            f"{threads} threads, {host['model']} ({host['cpuid']})",
             "variants": variants, "gemv": gemv_cpu,
             "aed_step_linears_sgemv_us": aed_us}
 
 
 PEAK_FP32 = 157.3  # TFLOP/s dense fp32 MFMA (MI355X)
+
+
+def headline_summary(details: dict, rows: list) -> dict:
+    """A few figures from the detail tree, small enough for the contract line."""
+    s = {"gemm_us": {r["gemm"]: round(r["kernel_us"], 1) for r in rows if r["gemm"] in ("ffn1", "ffn2", "q")}}
+    if "gemv_hbm_frac_mean_large" in details:
+        s["gemv_hbm_frac_large"] = details["gemv_hbm_frac_mean_large"]
+        g1 = [g for g in details["gemv"] if g["format"] == "Q8_0" and g["M"] == 1 and g["n"] == 16384]
+        if g1:
+            s["gemv_q8_0_1024x16384_m1_us"] = g1[0]["kernel_us"]
+    if "aed_decoder" in details:
+        s["aed_us_per_pos"] = details["aed_decoder"].get("forced_us_per_position")
+    if "gemm_small_m" in details:
+        c1 = [r for r in details["gemm_small_m"] if r.get("M") == 750 and r.get("k") == 1024
+              and r.get("n") == 4096]
+        if c1:
+            s["config1_us_per_call"] = c1[0].get("call_us")
+    return s
 
 
 def attn_flops(T, H, dk, left, right, nseq):
@@ -734,7 +766,7 @@ def main():
         print(json.dumps({"config5_layer": run_config5(B, M_)}), flush=True)
         return
 
-    log("[bench] encoder set Q8_0 M=6000")
+    log("[bench] q8_0 set")
     ms_step, flops, rows = run_encoder_set(B, M_, M_.Q8_0, M, ENC_SHAPES, args.steps, args.warmup, 0)
     value = flops / (ms_step * 1e-3) / 1e12
     # the roofline entry follows the 4096->1024 product: with 1024->4096 the
@@ -758,20 +790,20 @@ def main():
     if not args.no_extras:
         kq = {}
         for qt in (M_.Q2_K, M_.Q3_K, M_.Q4_K, M_.Q5_K, M_.Q6_K):
-            log(f"[bench] K-quant {M_.NAMES[qt]} M=12000")
+            log(f"[bench] {M_.NAMES[qt]}")
             ms4, fl4, rows4 = run_encoder_set(B, M_, qt, 12000, KQ_SHAPES, 3, 1, 100)
             kq[M_.NAMES[qt]] = {"tops_per_layer_set": round(fl4 / (ms4 * 1e-3) / 1e12, 2),
                                 "ms_per_layer_set": round(ms4, 3), "rows": rows4}
         details["kquant_m12000"] = kq
         details.update(run_int8act(B, M_, M))
-        log("[bench] f32 weights M=6000")
+        log("[bench] f32")
         msf, flf, rowsf = run_encoder_set(B, M_, M_.F32, M, ENC_SHAPES[:2], 3, 1, 200)
         details["f32_m6000"] = {"tflops": round(flf / (msf * 1e-3) / 1e12, 2), "rows": rowsf}
-        log("[bench] rel-pos attention core T=750 x 16 segments")
+        log("[bench] attention")
         details["relpos_attention"] = run_attention(B, M_)
-        log("[bench] AED decoder, config 3 shapes")
+        log("[bench] aed")
         details["aed_decoder"] = run_aed(B, M_)
-        log("[bench] decoder GEMVs")
+        log("[bench] gemv")
         gv = []
         for qt in (M_.Q8_0, M_.Q4_0, M_.Q4_K):
             for n, k in [(s[1], s[0]) for s in GEMV_SHAPES]:
@@ -782,14 +814,14 @@ def main():
         vf = [g["kernel_vs_floor"] for g in big if g.get("kernel_vs_floor")]
         if vf:   # the same GEMVs against a plain streaming read of their bytes, one launch each
             details["gemv_vs_read_floor_mean_large"] = round(float(np.mean(vf)), 3)
-        log("[bench] few-row products (one stream)")
+        log("[bench] small m")
         details["gemm_small_m"] = run_small_m(B, M_)
-        log("[bench] config 5: one encoder layer's built parts at M=12000")
+        log("[bench] config5")
         details["config5_layer"] = run_config5(B, M_)
 
     cpu = None
     if not args.no_cpu:
-        log("[bench] CPU baseline")
+        log("[bench] cpu")
         cpu = cpu_baseline(M_, lib)
 
     line = {"metric": METRIC, "value": round(value, 3), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
@@ -799,9 +831,24 @@ def main():
             "config": {"workload": "FastConformer-0.6B encoder linear set, Q8_0 weights, M=6000 "
                                    "(1024->4096, 4096->1024, 5x 1024->1024), EXACT numerics",
                        "M": M, "weights": "Q8_0"},
-            "roofline": roofline, "cpu_baseline": cpu, "details": details}
-    print(json.dumps(line), flush=True)
-
+            "roofline": roofline, "cpu_baseline": cpu}
+    # The full tree goes to a file (gpurun_out/ when the run has one); stdout
+    # gets the contract line alone, kept short (about 1 KB) so that a reader
+    # of the output's last lines gets all of it.
+    full = dict(line, details=details)
+    path = os.path.join(ROOT, "gpurun_out", "bench_details.json")
+    try:
+        os.makedirs(os.path.dirname(path), exist_ok=True)
+        with open(path, "w") as f:
+            json.dump(full, f)
+        log(f"[bench] details: {os.path.relpath(path, ROOT)}")
+    except OSError as ex:
+        log(f"[bench] details not written ({ex})")
+    line["summary"] = headline_summary(details, rows)
+    if cpu is not None:
+        line["cpu_baseline"] = {k: cpu[k] for k in ("value", "unit", "cores", "kind")}
+        line["cpu_baseline"]["sample"] = cpu["sample_short"]
+    print(json.dumps(line, separators=(",", ":")), flush=True)
 
 if __name__ == "__main__":
     main()

@@ -365,13 +365,10 @@ hipError_t launch_attn(const float *q, const float *k, const float *v, const flo
                        hipStream_t st) {
     using L = AttnLds<DK, NW>;
     const size_t bytes = sizeof(float) * L::TOTAL;
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_relpos_attn<DK, NW>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    // set once per instantiation (thread-safe static initialisation)
+    static const hipError_t attr = hipFuncSetAttribute((const void *)k_relpos_attn<DK, NW>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (attr != hipSuccess) return attr;
     // exponentials are base 2: scores carry log2(e) / sqrt(DK)
     const float kscale = (1.0f / sqrtf((float)DK)) * 1.4426950408889634f;
     dim3 grid((T + L::RB - 1) / L::RB, H, nseq);

@@ -1670,22 +1670,22 @@ static hipError_t launch_gemv1(const GJobs &J, const float *x, int M, const GPro
     const DevW &W = J.W[0];
     const int Kc = W.Kp / 128;
     const size_t lds = ((size_t)Kc * WNG * 8 * 64 + (size_t)Kc * 16 + (PRO ? (size_t)W.Kp : 0)) * sizeof(float);
-    static bool attr = false;
-    if constexpr (PRO) {
-        if (!attr) {
-            hipError_t e = allow_lds(k_gemv_jobs<QT, NW, WNG>);
-            if (e != hipSuccess) return e;
-            attr = true;
-        }
-        hipLaunchKernelGGL((k_gemv_jobs<QT, NW, WNG>), dim3(W.Np / 32 / WNG * J.n), dim3(NW * 64), lds, st, J, pro);
-    } else {
-        if (!attr) {
+    // set once per instantiation; a function-local static's initialisation is
+    // thread-safe, so concurrent first calls wait for the one that runs it
+    static const hipError_t attr = []() {
+        if constexpr (PRO) {
+            return allow_lds(k_gemv_jobs<QT, NW, WNG>);
+        } else {
             hipError_t e = allow_lds(k_gemv<QT, NW, WNG, VEC, 1>);
             if (e == hipSuccess) e = allow_lds(k_gemv<QT, NW, WNG, VEC, 4>);
             if (e == hipSuccess) e = allow_lds(k_gemv<QT, NW, WNG, VEC, 8>);
-            if (e != hipSuccess) return e;
-            attr = true;
+            return e;
         }
+    }();
+    if (attr != hipSuccess) return attr;
+    if constexpr (PRO) {
+        hipLaunchKernelGGL((k_gemv_jobs<QT, NW, WNG>), dim3(W.Np / 32 / WNG * J.n), dim3(NW * 64), lds, st, J, pro);
+    } else {
         if (J.n != 1) return hipErrorInvalidValue;
         // accumulator elements the M rows need (rows drow(e, hh) < M)
         if (M == 1)

@@ -25,6 +25,7 @@
 
 #include <math.h>
 #include <pthread.h>
+#include <stdatomic.h>
 #include <stdlib.h>
 #include <string.h>
 #include <unistd.h>
@@ -802,36 +803,87 @@ void orc_gemm_f64(const float *x, const float *wd, int T, int n, int k, double *
  * ingot runs its row loops through a parallel_for its host installs
  * (ingot_set_parallel_for, third_party/ingot/src/cpu.c:217-230; serial by
  * default). For timing the reference's CPU kernels on all host cores, this
- * installs one that splits [0, count) into `threads` contiguous ranges, each
- * on its own thread. */
+ * installs one that splits [0, count) into `threads` contiguous ranges. The
+ * workers are started once and stay alive; they spin on a generation counter
+ * for a while after each job, then sleep on a condition variable, so a call
+ * costs a wake-up, not a thread creation, and an idle pool uses no CPU. The calling
+ * thread runs range 0 itself. Calls are serialised by the caller (timing runs
+ * one kernel at a time). */
 typedef void (*orc_range_fn)(size_t begin, size_t end, void *user);
 typedef void (*orc_set_pf_fn)(void (*)(size_t, orc_range_fn, void *));
-static int g_pool_threads = 1;
-typedef struct { orc_range_fn fn; void *user; size_t b, e; } orc_range_job;
-static void *orc_range_run(void *a) {
-    const orc_range_job *j = (const orc_range_job *)a;
-    if (j->b < j->e) j->fn(j->b, j->e, j->user);
+#define ORC_POOL_MAX 256
+static struct {
+    int threads;                 /* workers + the caller */
+    int started;                 /* workers running */
+    _Atomic unsigned long gen;   /* bumped per job */
+    _Atomic int pending;         /* workers still on the current job */
+    orc_range_fn fn;
+    void *user;
+    size_t count;
+    int nt;                      /* ranges of the current job */
+    pthread_t th[ORC_POOL_MAX];
+    pthread_mutex_t mu;
+    pthread_cond_t cv;
+} g_pool = {1, 0, 0, 0, NULL, NULL, 0, 1, {0}, PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER};
+
+static void *orc_pool_worker(void *arg) {
+    const int id = (int)(size_t)arg;          /* 1 .. threads-1 */
+    unsigned long seen = 0;
+    for (;;) {
+        unsigned long g;
+        int spins = 0;
+        while ((g = atomic_load_explicit(&g_pool.gen, memory_order_acquire)) == seen) {
+            if (++spins > 200000) {
+                pthread_mutex_lock(&g_pool.mu);
+                while ((g = atomic_load_explicit(&g_pool.gen, memory_order_acquire)) == seen)
+                    pthread_cond_wait(&g_pool.cv, &g_pool.mu);
+                pthread_mutex_unlock(&g_pool.mu);
+                break;
+            }
+        }
+        seen = g;
+        if (id < g_pool.nt) {
+            const size_t b = g_pool.count * (size_t)id / (size_t)g_pool.nt;
+            const size_t e = g_pool.count * (size_t)(id + 1) / (size_t)g_pool.nt;
+            if (b < e) g_pool.fn(b, e, g_pool.user);
+        }
+        atomic_fetch_sub_explicit(&g_pool.pending, 1, memory_order_acq_rel);
+    }
     return NULL;
 }
+
 static void orc_parallel_for(size_t count, orc_range_fn fn, void *user) {
-    int nt = g_pool_threads;
+    int nt = g_pool.threads < g_pool.started + 1 ? g_pool.threads : g_pool.started + 1;
     if ((size_t)nt > count) nt = (int)count;
     if (nt <= 1) { if (count) fn(0, count, user); return; }
-    pthread_t th[256];
-    orc_range_job jobs[256];
-    if (nt > 256) nt = 256;
-    for (int i = 0; i < nt; i++) {
-        jobs[i].fn = fn, jobs[i].user = user;
-        jobs[i].b = count * (size_t)i / (size_t)nt, jobs[i].e = count * (size_t)(i + 1) / (size_t)nt;
-    }
-    int started = 1;
-    for (int i = 1; i < nt; i++, started++)
-        if (pthread_create(&th[i], NULL, orc_range_run, &jobs[i]) != 0) break;
-    orc_range_run(&jobs[0]);
-    for (int i = started; i < nt; i++) orc_range_run(&jobs[i]);   /* any thread that did not start */
-    for (int i = 1; i < started; i++) pthread_join(th[i], NULL);
+    g_pool.fn = fn, g_pool.user = user, g_pool.count = count, g_pool.nt = nt;
+    atomic_store_explicit(&g_pool.pending, g_pool.started, memory_order_relaxed);
+    atomic_fetch_add_explicit(&g_pool.gen, 1, memory_order_release);
+    pthread_mutex_lock(&g_pool.mu);
+    pthread_cond_broadcast(&g_pool.cv);
+    pthread_mutex_unlock(&g_pool.mu);
+    fn(0, count / (size_t)nt, user);
+    while (atomic_load_explicit(&g_pool.pending, memory_order_acquire) > 0) { }
 }
+
+static void orc_pool_grow(int threads) {
+    if (threads > ORC_POOL_MAX) threads = ORC_POOL_MAX;
+    while (g_pool.started + 1 < threads) {
+        const int id = g_pool.started + 1;
+        if (pthread_create(&g_pool.th[id], NULL, orc_pool_worker, (void *)(size_t)id) != 0) break;
+        g_pool.started++;
+    }
+}
+
+/* Range count of the next jobs: at most the threads started so far (workers
+ * are never stopped; a smaller count leaves the extra workers idle). */
+static void orc_pool_use(int threads) {
+    if (threads < 1) threads = 1;
+    orc_pool_grow(threads);
+    g_pool.threads = threads;
+}
+
 void orc_ingot_install_pool(void *set_parallel_for, int threads) {
-    g_pool_threads = threads < 1 ? 1 : threads;
+    orc_pool_use(threads);
     ((orc_set_pf_fn)set_parallel_for)(orc_parallel_for);
 }
