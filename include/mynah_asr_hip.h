@@ -12,10 +12,17 @@
  *     double), and a row's bits never depend on how many rows share the call.
  *   INT8ACT: int8 activations and exact integer sums, for every M.
  *     INT8 / INT4: the reference's small-T path (qmat.c:186-202, 508-552),
- *     its f32 combine order included. Q8_0 / Q4_0: activations per row as
- *     qmat.c:186-202. Q2_K..Q6_K: activations per 256-element super-block as
- *     ingot's int8 path (third_party/ingot/src/kernels.c:719-750, 1649-1795),
- *     within its 5e-3 budget of the f32 product. F32 weights return -1.
+ *     its f32 combine order included. Q4_K / Q5_K: ingot's int8 path
+ *     (third_party/ingot/src/kernels.c:719-750, 1767-1791, 2325-2353;
+ *     activations per 256-element super-block), within 1e-7 of it. Q8_0 /
+ *     Q4_0 (activations per row as qmat.c:186-202) and Q2_K, Q3_K, Q6_K (per
+ *     super-block, as Q4_K): this unit's own extension; the reference has no
+ *     int8 path for them (its matmat is exact f32 there). Error against the
+ *     f32 product, measured on the reference's own int8 test case
+ *     (tests/test_quant.c:157-205, uniform(-1, 1) activations): 3.9e-3
+ *     relative L2 for every block format, under that test's 5e-3 budget; this
+ *     is a measurement on that case, not a bound (N(0, 1) activations at
+ *     K = 1024 give 6.9e-3 to 7.8e-3). F32 weights return -1.
  *
  * Return values: 0 = done, -1 = not done (the caller runs its CPU path);
  * mynah_asr_hip_last_error() names the reason for the calling thread.

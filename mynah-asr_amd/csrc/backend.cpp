@@ -860,10 +860,24 @@ int mynah_asr_hip_relpos_attention(const float *q, const float *k, const float *
     return d2h_sync(c, ctx, dctx, td);
 }
 
+// The decoder entry points cannot run under a caller's graph capture: each
+// captures (and replays) its own step graph on the stream, reads tokens back
+// on the host (decode) and grows its thread buffers between calls. Refused
+// up front with a clear message rather than failing inside the capture.
+static int aed_refuse_capture(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) return fail("stream capture query failed");
+    if (cs != hipStreamCaptureStatusNone)
+        return fail("the AED decoder entry points cannot be called under stream capture (they capture their own "
+                    "step graph)");
+    return 0;
+}
+
 int mynah_asr_hip_aed_decode_dev(const mynah_asr_hip_aed *a, const float *enc, int T, const int *prompt,
                                  int n_prompt, int eos, int *tokens, int cap, void *stream) {
     Ctx *c;
     if (begin(&c)) return -1;
+    if (aed_refuse_capture(pick_stream(stream))) return -1;
     if (aed_check(a, T)) return -1;
     if (!enc || !prompt || n_prompt <= 0 || !tokens || cap < 0) return fail("bad argument");
     for (int i = 0; i < n_prompt; i++)
@@ -877,6 +891,7 @@ int mynah_asr_hip_aed_forced_dev(const mynah_asr_hip_aed *a, const float *enc, i
                                  float *logits, void *stream) {
     Ctx *c;
     if (begin(&c)) return -1;
+    if (aed_refuse_capture(pick_stream(stream))) return -1;
     if (aed_check(a, T)) return -1;
     if (!enc || !tokens || n <= 0 || n > a->max_seq || !logits) return fail("bad argument");
     for (int i = 0; i < n; i++)

@@ -438,7 +438,14 @@ struct PrepOut {
 // registers), and two for the split-K form of the
 // formats whose chunk-result stores would otherwise spill (INT4; Q5_K with
 // int8 activations, whose chunk halves join in int32)
+#ifndef GQ_V
+#define GQ_V 0
+#endif
+#ifndef GQ_OCC
+#define GQ_OCC 3
+#endif
 template <int QT, int EPI, bool A1 = false, int WN = 1, int WM = 2> constexpr int gemm_occ() {
+    if (QT == QT_Q8_0 && !A1 && WN == 1 && WM == 2 && EPI != EPI_PART) return GQ_OCC;
     if (WN > 1) return 2;
     if (WM == 1) return QT == QT_Q6_K || QT == QT_F32 ? 3 : 4;
     if (EPI == EPI_PART && (QT == QT_INT4 || (A1 && QT == QT_Q5_K))) return 2;
@@ -558,9 +565,25 @@ __global__ __launch_bounds__(256, (gemm_occ<QT, EPI, A1, WN, WM>())) void k_gemm
     };
 
     auto compute = [&](const uint8_t *B, int q, const BH<QT, WN> &hd, f16v (&acc)[WM][WN]) {
+#if GQ_V & 1
+        AK<WM> aa[L::SPS];
+#pragma unroll
+        for (int sl = 0; sl < L::SPS; sl++)
+#pragma unroll
+            for (int i = 0; i < WM; i++)
+#pragma unroll
+                for (int kh = 0; kh < 2; kh++) {
+                    const uint8_t *pp = B + L::A + i * L::AR + ((2 * sl + kh) * L::TERMS) * 1024 + lane * 16;
+                    aa[sl].h[i][kh] = *(const half8 *)pp;
+                    if constexpr (!A1) aa[sl].l[i][kh] = *(const half8 *)(pp + 1024);
+                }
+#endif
 #pragma unroll
         for (int sl = 0; sl < L::SPS; sl++) {
             const int s = L::SPS * q + sl;
+#if GQ_V & 1
+            const AK<WM> &a = aa[sl];
+#else
             AK<WM> a;
 #pragma unroll
             for (int i = 0; i < WM; i++)
@@ -570,6 +593,7 @@ __global__ __launch_bounds__(256, (gemm_occ<QT, EPI, A1, WN, WM>())) void k_gemm
                     a.h[i][kh] = *(const half8 *)pp;
                     if constexpr (!A1) a.l[i][kh] = *(const half8 *)(pp + 1024);
                 }
+#endif
             BK<QT, WN> b;
             // (one-kstep stages hold only kstep s: its local index is 0)
 #pragma unroll
@@ -580,6 +604,15 @@ __global__ __launch_bounds__(256, (gemm_occ<QT, EPI, A1, WN, WM>())) void k_gemm
                              L::SPS == 1 ? 0 : s, lane, b.r[j]);
             }
             kstep<QT, WM, WN, A1>(a, b, hd, s, acc);
+#if GQ_V & 2
+            if constexpr (QT == QT_Q8_0 && !A1 && WN == 1 && WM == 2) {
+#pragma unroll
+                for (int g = 0; g < 8; g++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // VALU
+                }
+            }
+#endif
         }
     };
 

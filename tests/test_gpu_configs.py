@@ -67,12 +67,15 @@ def _gemm(torch, dw, xd, T, n):
 
 # Benchmark config 4: K-quant GEMMs at FastConformer-1.1B shapes, M = 16 x 750
 CFG4_M = 12000
-# rows checked against the oracle: the first band, rows mid-run, and the last
-# band, which is ragged (12000 = 187 x 64 + 32)
-CFG4_ROWS = np.r_[0:16, 5000:5008, 9001:9009, 11968:12000]
+# rows checked against the oracle: the first band, one row of every 64-row
+# band at a different offset in each, rows mid-run, and the last band, which
+# is ragged (12000 = 187 x 64 + 32): 249 rows
+CFG4_ROWS = np.unique(np.r_[0:16, np.arange(0, 11968, 64) + np.arange(187) % 64, 5000:5008, 9001:9009,
+                            11968:12000])
 
 
-@pytest.mark.parametrize("n,k", [(4096, 1024), (1024, 4096)], ids=["1024to4096", "4096to1024"])
+@pytest.mark.parametrize("n,k", [(4096, 1024), (1024, 4096), (1024, 1024)],
+                         ids=["1024to4096", "4096to1024", "1024to1024"])
 @pytest.mark.parametrize("qt", KQ, ids=lambda q: M.NAMES[q])
 def test_config4_kquant_m12000(gpu, orc, qt, n, k):
     import torch
@@ -86,7 +89,7 @@ def test_config4_kquant_m12000(gpu, orc, qt, n, k):
         wd = orc.dequant(TO_ORC[qt], w.data, n * k).reshape(n, k)
         check_close_floor(y[CFG4_ROWS], x[CFG4_ROWS], wd, orc.gemm_f64(x[CFG4_ROWS], wd),
                           f"{M.NAMES[qt]} {k}->{n} M={CFG4_M}")
-        # rows carry the same bits at M = 750 (GEMM, split K at 4096->1024) and M = 1 (GEMV)
+        # rows carry the same bits at M = 750 (GEMM; split K at 4096->1024) and M = 1 (GEMV)
         for T in (750, 1):
             yt = _gemm(torch, dw, xd, T, n)
             assert np.array_equal(yt.view(np.uint32), y[:T].view(np.uint32)), f"M={T}"

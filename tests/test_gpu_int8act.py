@@ -102,27 +102,33 @@ def test_int8act_large_products_bit_exact(int8act, orc, qt):
         dw.close()
 
 
-def test_int8act_reference_budget(int8act, orc):
-    """test_quant.c:157-205: Q4_K, 37 rows of 0.02 * uniform(-1, 1), 131 tokens
-    of uniform(-1, 1), 256 columns: relative L2 against the exact product
-    below the reference's int8 budget, 5e-3."""
-    say("int8act budget")
+@pytest.mark.parametrize("name", ["Q4_K", "Q5_K", "Q8_0", "Q4_0", "Q2_K", "Q3_K", "Q6_K"])
+def test_int8act_reference_budget(int8act, orc, name):
+    """test_quant.c:157-205: 37 rows of 0.02 * uniform(-1, 1), 131 tokens of
+    uniform(-1, 1), 256 columns: relative L2 against the exact product below
+    the reference's int8 budget, 5e-3. The reference has this path for Q4_K
+    and Q5_K only (checked against it below when oracle/_ref is built); for
+    the other formats INT8ACT is this build's extension and the budget is
+    the check that pins it. Q4_K through the reference's own quantizer
+    (restated in the oracle), the others through the build's."""
+    say("int8act budget", name)
     gpu = int8act
     r = np.random.default_rng(0xC0FFEE)
     wf = (0.02 * r.uniform(-1, 1, (37, 256))).astype(np.float32)
-    raw = orc.quantize(O.Q4_K, wf)
+    oq, mq = getattr(O, name), getattr(M, name)
+    raw = orc.quantize(O.Q4_K, wf) if name == "Q4_K" else gpu.quantize(mq, wf)
     x = r.uniform(-1, 1, (131, 256)).astype(np.float32)
-    w = M.Weight(M.Q4_K, 37, 256, raw)
+    w = M.Weight(mq, 37, 256, raw)
     y = M.host_qgemm(gpu, w, x)
-    ex = orc.gemm_f64(x, orc.dequant(O.Q4_K, raw, 37 * 256).reshape(37, 256))
+    ex = orc.gemm_f64(x, orc.dequant(oq, raw, 37 * 256).reshape(37, 256))
     rel = float(np.linalg.norm(y - ex) / np.linalg.norm(ex))
     say(f"  rel L2 vs exact {rel:.3g}")
     assert rel < 5e-3
     ref_path = os.path.join(os.path.dirname(O.__file__), "_ref", "libingot_ref_avx2.so")
-    if os.path.exists(ref_path):
+    if name in ("Q4_K", "Q5_K") and os.path.exists(ref_path):
         R = O.IngotRef(ref_path)
         if not R.is_exact(131):
-            ri = R.kernel("ingot_q4_k_matmat", raw, 37, 256, x)
+            ri = R.kernel("ingot_%s_matmat" % name.lower(), raw, 37, 256, x)
             rel_i = float(np.linalg.norm(y - ri) / np.linalg.norm(ri))
             say(f"  rel L2 vs the reference's int8 path {rel_i:.3g}")
             assert rel_i < 1e-6

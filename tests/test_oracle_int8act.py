@@ -207,3 +207,41 @@ def test_int8act_budget_on_reference_case(orc):
     ex = orc.gemm_f64(x, orc.dequant(O.Q4_K, raw, 37 * 256).reshape(37, 256))
     rel = np.linalg.norm(ours - ex) / np.linalg.norm(ex)
     assert rel < 5e-3, rel
+
+
+BLOCK_FORMATS = ["Q8_0", "Q4_0", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K"]
+
+
+def _budget_case(orc, lib, name, rows, cols, tokens, weights, acts):
+    import mynah_hip as M
+    raw = lib.quantize(getattr(M, name), weights)
+    oq = getattr(O, name)
+    ours, _ = orc.int8act_blocks(oq, raw, rows, cols, acts)
+    ex = orc.gemm_f64(acts, orc.dequant(oq, raw, rows * cols).reshape(rows, cols))
+    return float(np.linalg.norm(ours - ex) / np.linalg.norm(ex))
+
+
+@pytest.mark.parametrize("name", BLOCK_FORMATS)
+def test_int8act_budget_every_block_format(orc, name):
+    """The reference's int8 precision contract (test_quant.c:157-205: 37 rows
+    of 0.02 * uniform(-1, 1), 131 tokens of uniform(-1, 1), 256 columns,
+    relative L2 against the exact product below 5e-3) for every block format.
+    Only Q4_K and Q5_K have an int8 path in the reference
+    (kernels.c:1767-1791, 2325-2353); for Q8_0, Q4_0, Q2_K, Q3_K and Q6_K the
+    INT8ACT form is this build's own extension, and this is the check that
+    pins its error. Weights through the build's quantizers (host/synth.c).
+    Measured: 3.86e-3 for every format. The same activations drawn N(0, 1) at
+    K = 1024 give 6.9e-3 (K-quants, per-256 activation scales) and 7.8e-3
+    (Q8_0 / Q4_0, per-row scales): the 5e-3 figure holds for the reference's
+    case, not for any input; that second case is bounded at 1e-2 here."""
+    import mynah_hip as M
+    lib = M.HipLib()
+    r = np.random.default_rng(0xC0FFEE)
+    w = (0.02 * r.uniform(-1, 1, (37, 256))).astype(np.float32)
+    x = r.uniform(-1, 1, (131, 256)).astype(np.float32)
+    rel = _budget_case(orc, lib, name, 37, 256, 131, w, x)
+    assert rel < 5e-3, rel
+    w2 = lib.randn(0, 0.02, (64, 1024))
+    x2 = lib.randn(1, 1.0, (64, 1024))
+    rel2 = _budget_case(orc, lib, name, 64, 1024, 64, w2, x2)
+    assert 5e-3 < rel2 < 1e-2, rel2

@@ -38,9 +38,12 @@ def _run(torch, dw, x, T, n, act, noalloc):
 
 
 # (format, n, k, first M, second M): GEMM sizes on both calls, one pair that
-# would split K in qgemm_dev (M = 40 at K = 4096), one pair crossing to the GEMV
+# would split K in qgemm_dev (M = 40 at K = 4096), pairs crossing to the GEMV
+# (Q8_0 4096 -> 1024 at M = 4: qgemm_dev runs the split-K GEMV there, the
+# allocation-free entry the one-launch GEMV, which must give the same bits)
 CASES = [
     (M.Q8_0, 1024, 1024, 2000, 300),
+    (M.Q8_0, 1024, 4096, 300, 4),
     (M.Q4_K, 512, 4096, 700, 40),
     (M.F32, 256, 1024, 600, 17),
     (M.Q6_K, 256, 1024, 130, 9),
@@ -65,15 +68,19 @@ def test_noalloc_matches_qgemm_dev(gpu, qt, n, k, m1, m2):
         dw.close()
 
 
-def test_noalloc_int8act_matches_qgemm_dev(gpu):
+# INT8ACT's three activation forms: per-row (Q8_0), per-super-block with the
+# mins operand (Q4_K), and the qmat INT4 form on the i8 MFMA; calls of 900, 33
+# and 5 rows in a row (the last takes the M <= 16 path)
+@pytest.mark.parametrize("qt", [M.Q8_0, M.Q4_K, M.INT4], ids=lambda q: M.NAMES[q])
+def test_noalloc_int8act_matches_qgemm_dev(gpu, qt):
     import torch
-    say("noalloc INT8ACT Q8_0")
-    w = M.Weight.make(gpu, M.Q8_0, gpu.randn(0, 0.02, (512, 1024)))
+    say("noalloc INT8ACT", M.NAMES[qt])
+    w = M.Weight.make(gpu, qt, gpu.randn(0, 0.02, (512, 1024)))
     dw = M.DeviceWeight(gpu, w)
     x = torch.from_numpy(gpu.randn(8, 1.0, (900, 1024))).cuda()
     gpu.set_numerics(M.INT8ACT)
     try:
-        for T in (900, 33):
+        for T in (900, 33, 5):
             ref = _run(torch, dw, x, T, 512, 0, False)
             got = _run(torch, dw, x, T, 512, 0, True)
             assert torch.equal(got.view(torch.int32), ref.view(torch.int32)), f"M={T}"
