@@ -159,6 +159,24 @@ def test_aed_rejects_unsupported(gpu):
         dev.decode(enc.data_ptr(), 4, [-1], eos=0, cap=2)
     with pytest.raises(RuntimeError, match="bad argument"):
         dev.forced(enc.data_ptr(), 4, list(range(9)))      # more positions than max_seq
+    # under a caller's stream capture both entry points refuse up front (they
+    # capture their own step graph); the capture itself stays valid
+    g, s = torch.cuda.CUDAGraph(), torch.cuda.Stream()
+    z = torch.zeros(4, device="cuda")
+    msgs = []
+    with torch.cuda.graph(g, stream=s):
+        z.add_(1.0)
+        for call in (lambda: dev.forced(enc.data_ptr(), 4, [1, 2], stream=s.cuda_stream),
+                     lambda: dev.decode(enc.data_ptr(), 4, [1], eos=0, cap=2, stream=s.cuda_stream)):
+            try:
+                call()
+                msgs.append("no error")
+            except RuntimeError as ex:
+                msgs.append(str(ex))
+    g.replay()
+    torch.cuda.synchronize()
+    assert all("stream capture" in m for m in msgs), msgs
+    assert torch.equal(z, torch.ones(4, device="cuda"))
     dev.close()
 
 
