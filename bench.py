@@ -522,6 +522,10 @@ def headline_summary(details: dict, rows: list) -> dict:
             s["gemv_q8_0_1024x16384_m1_us"] = g1[0]["kernel_us"]
     if "aed_decoder" in details:
         s["aed_us_per_pos"] = details["aed_decoder"].get("forced_us_per_position")
+    if "vendor_gemm" in details:
+        v = {r["gemm"]: r["us"] for r in details["vendor_gemm"] if r["dtype"] == "f16" and "volume" in r["gemm"]}
+        if v:
+            s["hipblaslt_f16_same_mfma_us"] = v
     if "gemm_small_m" in details:
         c1 = [r for r in details["gemm_small_m"] if r.get("M") == 750 and r.get("k") == 1024
               and r.get("n") == 4096]
@@ -568,6 +572,38 @@ def run_small_m(B, M_, reps=50):
             out.append({"M": M, "k": k, "n": n, "format": "Q8_0", "call_us": round(us, 2),
                         "tflops": round(2.0 * M * n * k / us / 1e6, 2)})
         dw.close()
+    return out
+
+
+def run_vendor_gemm(B, reps=50):
+    """The vendor's plain GEMM (torch.matmul -> hipBLASLt) at the MFMA volume of
+    this build's EXACT products: a plain f16 / bf16 GEMM with K doubled issues
+    the same MFMA work as two f16 terms per useful product (ffn2: M=6000,
+    K=2*4096, N=1024; ffn1: K=2*1024, N=4096), and the single-term shapes
+    themselves. A calibration of what this box's MFMA sustains on these
+    shapes, not a parity path (no rounding contract, no row stability)."""
+    torch = B.torch
+    out = []
+    for name, (M, K, N) in (("ffn2 volume", (6000, 8192, 1024)), ("ffn1 volume", (6000, 2048, 4096)),
+                            ("4096->1024 plain", (6000, 4096, 1024)), ("1024->4096 plain", (6000, 1024, 4096))):
+        for dt, dn in ((torch.float16, "f16"), (torch.bfloat16, "bf16")):
+            g = torch.Generator(device="cuda").manual_seed(5)
+            a = torch.randn(M, K, device="cuda", dtype=dt, generator=g)
+            b = torch.randn(K, N, device="cuda", dtype=dt, generator=g)
+            with torch.cuda.stream(B.stream):
+                for _ in range(5):
+                    c = a @ b
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(B.stream)
+                for _ in range(reps):
+                    c = a @ b
+                e1.record(B.stream)
+            B.sync()
+            us = e0.elapsed_time(e1) / reps * 1e3
+            tf = 2.0 * M * N * K / us / 1e6
+            out.append({"gemm": name, "M": M, "K": K, "N": N, "dtype": dn, "us": round(us, 2),
+                        "tflops": round(tf, 1), "mfma_frac": round(tf / PEAK_FP16, 4)})
+            del a, b, c
     return out
 
 
@@ -728,6 +764,9 @@ def main():
                     help="only the AED decoder (config 3 shapes, 4 layers, T=750, Q8_0), one JSON line")
     ap.add_argument("--int8act", action="store_true",
                     help="only the INT8ACT layer sets (Q8_0 M=6000, Q4_K and Q5_K M=12000), one JSON line")
+    ap.add_argument("--vendor", action="store_true",
+                    help="only the vendor GEMM calibration (torch.matmul / hipBLASLt at the EXACT products' "
+                         "MFMA volume), one JSON line")
     ap.add_argument("--config5", action="store_true",
                     help="only the built parts of one encoder layer at config 5's batch (M=12000), one JSON line")
     ap.add_argument("--profile", action="store_true",
@@ -764,6 +803,9 @@ def main():
         return
     if args.config5:
         print(json.dumps({"config5_layer": run_config5(B, M_)}), flush=True)
+        return
+    if args.vendor:
+        print(json.dumps({"vendor_gemm": run_vendor_gemm(B)}), flush=True)
         return
 
     log("[bench] q8_0 set")
@@ -818,6 +860,8 @@ def main():
         details["gemm_small_m"] = run_small_m(B, M_)
         log("[bench] config5")
         details["config5_layer"] = run_config5(B, M_)
+        log("[bench] vendor gemm")
+        details["vendor_gemm"] = run_vendor_gemm(B)
 
     cpu = None
     if not args.no_cpu:

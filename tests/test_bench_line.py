@@ -28,7 +28,10 @@ def _fake_details():
     return rows, {"gemv": gemv, "gemv_hbm_frac_mean_large": 0.1103,
                   "aed_decoder": {"forced_us_per_position": 248.3},
                   "gemm_small_m": [{"M": 750, "k": 1024, "n": 4096, "call_us": 27.59}],
-                  "kquant_m12000": {"Q4_K": {"tops_per_layer_set": 332.0}}}
+                  "kquant_m12000": {"Q4_K": {"tops_per_layer_set": 332.0}},
+                  "vendor_gemm": [{"gemm": g, "dtype": d, "us": 125.43} for g in ("ffn2 volume", "ffn1 volume",
+                                                                             "4096->1024 plain")
+                                  for d in ("f16", "bf16")]}
 
 
 def test_contract_line_is_short():
