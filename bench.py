@@ -585,7 +585,8 @@ def run_vendor_gemm(B, reps=50):
     torch = B.torch
     out = []
     for name, (M, K, N) in (("ffn2 volume", (6000, 8192, 1024)), ("ffn1 volume", (6000, 2048, 4096)),
-                            ("4096->1024 plain", (6000, 4096, 1024)), ("1024->4096 plain", (6000, 1024, 4096))):
+                            ("4096->1024 plain", (6000, 4096, 1024)), ("1024->4096 plain", (6000, 1024, 4096)),
+                            ("config 1 volume", (750, 2048, 4096)), ("4096->1024 M=750 volume", (750, 8192, 1024))):
         for dt, dn in ((torch.float16, "f16"), (torch.bfloat16, "bf16")):
             g = torch.Generator(device="cuda").manual_seed(5)
             a = torch.randn(M, K, device="cuda", dtype=dt, generator=g)
