@@ -529,3 +529,67 @@ def test_concurrent_callers_match_serial(gpu, orc):
     for key in cases:
         for a, b in zip(got[key], serial[key]):
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"case {key} differs"
+
+
+# ------------------------------------------------- largest K, empty inputs
+@pytest.mark.parametrize("qt", [M.Q8_0, M.Q4_K, M.INT8], ids=lambda q: M.NAMES[q])
+def test_largest_k(gpu, orc, qt):
+    """K = 8192 (QMAT_K_MAX, the reference's largest K for its native int8
+    paths, src/qmat.c:181, 515-517) and beyond it (K = 8448, where the
+    reference's small-T path leaves SIMD for its scalar loop, the same
+    arithmetic): the GEMV (M = 1, 16, K split over workgroups) and the GEMM
+    (M = 40, split K; M = 300) against the oracle in EXACT numerics; the
+    qmat INT8 format also bit-exact with the reference's small-T int8 path in
+    INT8ACT numerics; rows bit-identical across M.
+    Bar: 1e-4*|ref| + 1e-6 plus 4 * 2^-24 * sum_k |x||w| per element: at
+    K = 8192 some outputs cancel to far below their terms, and there no f32
+    product meets the plain bar (the reference's own sgemm misses it at
+    K = 4096 by up to 3.3 of these units; tests/test_gpu_configs.py)."""
+    say("largest K", M.NAMES[qt])
+    for k in (8192, 8448):
+        w = M.Weight.make(gpu, qt, gpu.randn(3, 0.02, (96, k)))
+        x = gpu.randn(4, 1.0, (300, k))
+        wd = oracle_dequant(orc, w)
+        y300 = M.host_qgemm(gpu, w, x, keep=True)
+        ref = orc.gemm_f64(x[:24], wd)
+        unit = 2.0 ** -24 * (np.abs(x[:24]).astype(np.float64) @ np.abs(wd).astype(np.float64).T)
+        err = np.abs(y300[:24].astype(np.float64) - ref)
+        say(f"  K={k}: worst err / (2^-24 sum|x||w|) = {float((err / unit).max()):.3g}")
+        assert (err <= RTOL * np.abs(ref) + ATOL + 4.0 * unit).all(), f"K={k} M=300"
+        for T in (1, 16, 40):
+            yT = M.host_qgemm(gpu, w, x[:T], keep=True)
+            assert np.array_equal(yT.view(np.uint32), y300[:T].view(np.uint32)), f"K={k} M={T}"
+        if qt == M.INT8:
+            assert gpu.set_numerics(M.INT8ACT) == M.INT8ACT
+            try:
+                for T in (1, 16, 300):
+                    y8 = M.host_qgemm(gpu, w, x[:T], keep=True)
+                    ref, _ = orc.qmat_int8_path(w.qtype, w.data, w.scales, w.n, w.k, x[:T])
+                    assert np.array_equal(y8.view(np.uint32), ref.view(np.uint32)), f"INT8ACT K={k} M={T}"
+            finally:
+                gpu.set_numerics(M.EXACT)
+        M.evict(gpu, w)
+
+
+def test_empty_inputs(gpu):
+    """T = 0 is done (0) and touches nothing, through the host-pointer and the
+    device-pointer entry points, as the reference's loops do nothing for it."""
+    import ctypes as C
+    import torch
+    say("empty inputs")
+    w = M.Weight.make(gpu, M.Q8_0, gpu.randn(0, 0.02, (64, 256)))
+    out = np.full((1, 64), 7.0, np.float32)
+    x = np.zeros((1, 256), np.float32)
+    assert gpu.L.mynah_asr_hip_qgemm(C.byref(w.desc), x.ctypes.data, out.ctypes.data, 0) == 0
+    assert (out == 7.0).all()
+    dw = M.DeviceWeight(gpu, w)
+    try:
+        xd = torch.zeros((1, 256), device="cuda")
+        yd = torch.full((1, 64), 7.0, device="cuda")
+        torch.cuda.synchronize()
+        assert gpu.L.mynah_asr_hip_qgemm_dev(dw.h, xd.data_ptr(), yd.data_ptr(), 0, 0, None) == 0
+        torch.cuda.synchronize()
+        assert bool((yd == 7.0).all())
+    finally:
+        dw.close()
+    M.evict(gpu, w)
