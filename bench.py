@@ -523,7 +523,8 @@ def headline_summary(details: dict, rows: list) -> dict:
     if "aed_decoder" in details:
         s["aed_us_per_pos"] = details["aed_decoder"].get("forced_us_per_position")
     if "vendor_gemm" in details:
-        v = {r["gemm"]: r["us"] for r in details["vendor_gemm"] if r["dtype"] == "f16" and "volume" in r["gemm"]}
+        v = {r["gemm"].split()[0]: r["us"] for r in details["vendor_gemm"]
+             if r["dtype"] == "f16" and r["gemm"] in ("ffn2 volume", "ffn1 volume")}
         if v:
             s["hipblaslt_f16_same_mfma_us"] = v
     if "gemm_small_m" in details:
