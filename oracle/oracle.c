@@ -826,9 +826,13 @@ static struct {
     pthread_cond_t cv;
 } g_pool = {1, 0, 0, 0, NULL, NULL, 0, 1, {0}, PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER};
 
+/* a worker's id and the generation current when it was created: the next
+ * job published is the first it joins */
+static struct { int id; unsigned long gen0; } g_pool_start[ORC_POOL_MAX];
+
 static void *orc_pool_worker(void *arg) {
-    const int id = (int)(size_t)arg;          /* 1 .. threads-1 */
-    unsigned long seen = 0;
+    const int id = ((const int *)arg)[0];     /* 1 .. threads-1 */
+    unsigned long seen = g_pool_start[id].gen0;
     for (;;) {
         unsigned long g;
         int spins = 0;
@@ -870,7 +874,10 @@ static void orc_pool_grow(int threads) {
     if (threads > ORC_POOL_MAX) threads = ORC_POOL_MAX;
     while (g_pool.started + 1 < threads) {
         const int id = g_pool.started + 1;
-        if (pthread_create(&g_pool.th[id], NULL, orc_pool_worker, (void *)(size_t)id) != 0) break;
+        /* no job is in flight here (the caller is between jobs) */
+        g_pool_start[id].id = id;
+        g_pool_start[id].gen0 = atomic_load_explicit(&g_pool.gen, memory_order_relaxed);
+        if (pthread_create(&g_pool.th[id], NULL, orc_pool_worker, &g_pool_start[id].id) != 0) break;
         g_pool.started++;
     }
 }

@@ -74,6 +74,11 @@ def test_persistent_pool_matches_serial():
     for th in (4, 3, 8, 2):   # grow, shrink, grow again: workers stay, ranges follow the count
         R.set_threads(th)
         outs.append(R.kernel("ingot_q8_0_matmat", raw, 96, 512, x))
+    for i in range(200):   # many short jobs, the count changing between them
+        R.set_threads(1 + i % 6)
+        o = R.kernel("ingot_q8_0_matmat", raw, 96, 512, x)
+        if i % 50 == 0:
+            outs.append(o)
     R.set_threads(1)
     for o in outs:
         assert np.array_equal(o.view(np.uint32), one.view(np.uint32))
