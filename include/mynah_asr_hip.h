@@ -54,7 +54,7 @@ enum {
     MYNAH_ASR_HIP_Q6_K = 30
 };
 
-enum { MYNAH_ASR_HIP_EXACT = 0, MYNAH_ASR_HIP_INT8ACT = 1 };
+enum { MYNAH_ASR_HIP_EXACT = 0, MYNAH_ASR_HIP_INT8ACT = 1, MYNAH_ASR_HIP_QMAT = 2 };
 
 /* A weight matrix as the caller holds it in host memory: the fields of
  * mynah_asr_qmat (src/qmat.h:39-47) plus the raw ggml block pointer. `data` is
@@ -71,11 +71,20 @@ typedef struct {
  * mynah_asr_cuda_available (src/cuda_gemm.cu:62, declared src/backend.c:24). */
 int mynah_asr_hip_available(void);
 
-/* Process-wide numerics mode (MYNAH_ASR_HIP_EXACT / _INT8ACT). Returns the
- * mode now in force. The environment variable MYNAH_ASR_HIP_NUMERICS=int8
- * selects INT8ACT at first use. No reference counterpart: it exposes the
- * choice qmat.c makes by row count (src/qmat.c:180, 508, 644) as a fixed
- * setting, so a row's result never depends on the batch size. */
+/* Process-wide numerics mode (MYNAH_ASR_HIP_EXACT / _INT8ACT / _QMAT). Returns
+ * the mode now in force. The environment variable MYNAH_ASR_HIP_NUMERICS=int8
+ * selects INT8ACT at first use, =qmat QMAT. No reference counterpart: EXACT
+ * and INT8ACT expose the choice qmat.c makes by row count (src/qmat.c:180,
+ * 508, 644) as a fixed setting, so a row's result never depends on the batch
+ * size. QMAT instead makes that choice per product as qmat.c does
+ * (src/qmat.c:503-651): INT8/INT4 weights with K <= 8192 take the
+ * int8-activation path (INT8ACT's, bit-exact with the reference's) for
+ * T <= 16, and for every T when MYNAH_ASR_QGEMM=1 is set (qmat.c:598-643;
+ * read at each product, where qmat.c reads it once); every other product is
+ * EXACT (the reference's dequant + sgemm,
+ * to the tolerance above). Like the reference it is not row-stable across
+ * T = 16 for INT8/INT4 weights. The device AED decoder refuses INT8/INT4
+ * weights in QMAT (their one-row products would take the int8 path). */
 int mynah_asr_hip_set_numerics(int mode);
 int mynah_asr_hip_numerics(void);
 

@@ -175,15 +175,38 @@ const mynah_asr_hip_weight *resident(const mynah_asr_hip_wdesc *w) {
     return W;
 }
 
-int check_numerics_supported(int qtype) {
-    if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT) return 0;
+// The numerics of the product being run. The process mode (set_numerics)
+// applies as it is, except MYNAH_ASR_HIP_QMAT, which follows the reference's
+// qmat.c dispatch per product (src/qmat.c:508-552, 598-650): INT8 / INT4
+// weights with K <= 8192 (QMAT_K_MAX, :181) take the int8-activation path
+// for T <= 16 (QMAT_SMALL_T, :180) and, with MYNAH_ASR_QGEMM=1 in the
+// environment (:607-611; read at each call here, once per process there),
+// for every T; every other product runs EXACT. Entry points set the effective mode for the call (NumScope).
+thread_local int t_num = -1;
+int num_now() { return t_num >= 0 ? t_num : mynah_asr_hip_numerics(); }
+int eff_num(int qtype, int k, int T) {
+    const int m = mynah_asr_hip_numerics();
+    if (m != MYNAH_ASR_HIP_QMAT) return m;
+    if ((qtype != MYNAH_ASR_HIP_INT8 && qtype != MYNAH_ASR_HIP_INT4) || k > 8192) return MYNAH_ASR_HIP_EXACT;
+    if (T <= 16) return MYNAH_ASR_HIP_INT8ACT;
+    const char *e = getenv("MYNAH_ASR_QGEMM");
+    return (e && e[0] == '1') ? MYNAH_ASR_HIP_INT8ACT : MYNAH_ASR_HIP_EXACT;
+}
+struct NumScope {
+    int prev;
+    explicit NumScope(int m) : prev(t_num) { t_num = m; }
+    ~NumScope() { t_num = prev; }
+};
+
+int check_numerics_supported(int qtype, int k, int T) {
+    if (eff_num(qtype, k, T) == MYNAH_ASR_HIP_EXACT) return 0;
     if (mh_i8_supported(qtype)) return 0;
     return fail("INT8ACT numerics: f32 weights have no int8 form (the reference multiplies them in f32)");
 }
 
 // the prepared-input form a product of this format reads in the current mode
 int prep_kind(int qtype) {
-    return mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT ? mh_i8_kind(qtype) : 0;
+    return num_now() == MYNAH_ASR_HIP_INT8ACT ? mh_i8_kind(qtype) : 0;
 }
 
 // bytes of the three prepared-input buffers (xp, xs16, xpf) for one form
@@ -266,7 +289,7 @@ float *gemv_ws(Ctx *c, const mynah_asr_hip_weight *W) {
 
 int gemm_dev(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, float *dy, int T, int act,
              hipStream_t st) {
-    if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT && mh_use_gemv(W->dw, T)) {
+    if (num_now() == MYNAH_ASR_HIP_EXACT && mh_use_gemv(W->dw, T)) {
         const int vec = (W->dw.k % 8 == 0) && (((uintptr_t)dx & 15) == 0);
         hipError_t e = mh_launch_gemv(W->qtype, W->dw, dx, T, vec, dy, act, gemv_ws(c, W), st);
         if (e != hipSuccess) return fail("gemv launch failed", hipGetErrorString(e));
@@ -282,7 +305,20 @@ int gemm_dev(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, float *dy, 
 // (no f32 intermediate, no preparation pass); otherwise two products.
 int ffn_dev(Ctx *c, const mynah_asr_hip_weight *W1, const mynah_asr_hip_weight *W2, const float *dx, float *dy,
             int T, hipStream_t st) {
-    const bool fuse = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT && !mh_use_gemv(W1->dw, T) &&
+    const int n1 = eff_num(W1->qtype, W1->dw.k, T), n2 = eff_num(W2->qtype, W2->dw.k, T);
+    if (n1 != n2) {
+        // (QMAT numerics: each product in its own mode, as qmat_ffn's two qmat_mul calls)
+        float *dh = (float *)c->h.get((size_t)T * W1->dw.n * sizeof(float));
+        if (!dh) return fail("device buffer allocation failed");
+        {
+            NumScope s1(n1);
+            if (gemm_dev(c, W1, dx, dh, T, 1, st)) return -1;
+        }
+        NumScope s2(n2);
+        return gemm_dev(c, W2, dh, dy, T, 0, st);
+    }
+    NumScope sc(n1);
+    const bool fuse = num_now() == MYNAH_ASR_HIP_EXACT && !mh_use_gemv(W1->dw, T) &&
                       W2->dw.Kp == W1->dw.Np;
     if (fuse) {
         if (prep_into(c->pa, W1, dx, T, st)) return -1;
@@ -312,8 +348,18 @@ int ffn_dev(Ctx *c, const mynah_asr_hip_weight *W1, const mynah_asr_hip_weight *
 // three products of one input: prepared once whenever it fits them all
 int qkv_dev(Ctx *c, const mynah_asr_hip_weight *const W[3], const float *dx, float *const dy[3], int T,
             hipStream_t st) {
+    const int nq = eff_num(W[0]->qtype, W[0]->dw.k, T);
+    if (eff_num(W[1]->qtype, W[1]->dw.k, T) != nq || eff_num(W[2]->qtype, W[2]->dw.k, T) != nq) {
+        // (QMAT numerics: each product in its own mode, as qmat_qkv's three qmat_mul calls)
+        for (int i = 0; i < 3; i++) {
+            NumScope si(eff_num(W[i]->qtype, W[i]->dw.k, T));
+            if (gemm_dev(c, W[i], dx, dy[i], T, 0, st)) return -1;
+        }
+        return 0;
+    }
+    NumScope sc(nq);
     // GEMMs of one format and shape: one preparation, one launch
-    const bool exact = mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT;
+    const bool exact = num_now() == MYNAH_ASR_HIP_EXACT;
     if ((!exact || !mh_use_gemv(W[0]->dw, T)) &&
         W[1]->qtype == W[0]->qtype && W[2]->qtype == W[0]->qtype && W[1]->dw.n == W[0]->dw.n &&
         W[2]->dw.n == W[0]->dw.n && W[1]->dw.k == W[0]->dw.k && W[2]->dw.k == W[0]->dw.k &&
@@ -340,7 +386,7 @@ int qkv_dev(Ctx *c, const mynah_asr_hip_weight *const W[3], const float *dx, flo
     }
     bool prepared = false;
     for (int i = 0; i < 3; i++) {
-        if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT && mh_use_gemv(W[i]->dw, T)) {
+        if (num_now() == MYNAH_ASR_HIP_EXACT && mh_use_gemv(W[i]->dw, T)) {
             if (gemm_dev(c, W[i], dx, dy[i], T, 0, st)) return -1;
             continue;
         }
@@ -388,7 +434,7 @@ int aed_check(const mynah_asr_hip_aed *a, int T) {
     const int d = a->d, dk = d / a->n_heads;
     if (dk != 64 && dk != 128) return fail("decoder head size must be 64 or 128");
     if (d > 4096 || d % 4) return fail("decoder width must be a multiple of 4, at most 4096");
-    if (mynah_asr_hip_numerics() != MYNAH_ASR_HIP_EXACT) return fail("the device decoder runs EXACT numerics only");
+    if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_INT8ACT) return fail("the device decoder runs EXACT numerics only");
     if (!a->emb || !a->pos || !a->embln_w || !a->embln_b || !a->fin_w || !a->fin_b || !a->head_b)
         return fail("bad argument: a decoder tensor is NULL");
     if (!gemv_ok(a->head, a->vocab, d)) return fail("head weight shape or GEMV limits");
@@ -405,6 +451,22 @@ int aed_check(const mynah_asr_hip_aed *a, int T) {
                               L->ff1_b, L->ff2_b};
         for (int i = 0; i < 16; i++)
             if (!v[i]) return fail("bad argument: a decoder layer tensor is NULL");
+    }
+    // QMAT numerics: the decoder's one-row products of INT8/INT4 weights would
+    // take the reference's int8 path, which the device decoder does not run
+    if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_QMAT) {
+        auto int8_path = [](const mynah_asr_hip_weight *W) {
+            return W && eff_num(W->qtype, W->dw.k, 1) != MYNAH_ASR_HIP_EXACT;
+        };
+        bool any = int8_path(a->head) || int8_path(a->proj);
+        for (int li = 0; li < a->n_layers && !any; li++) {
+            const mynah_asr_hip_aed_layer *L = &a->layers[li];
+            const mynah_asr_hip_weight *ws[10] = {L->sq, L->sk, L->sv, L->so, L->cq, L->ck, L->cv, L->co, L->ff1, L->ff2};
+            for (int i = 0; i < 10; i++) any = any || int8_path(ws[i]);
+        }
+        if (any)
+            return fail("QMAT numerics: INT8/INT4 decoder weights take the reference's int8 path, which the device "
+                        "decoder does not run");
     }
     return 0;
 }
@@ -691,14 +753,16 @@ int mynah_asr_hip_available(void) {
 }
 
 int mynah_asr_hip_set_numerics(int mode) {
-    if (mode == MYNAH_ASR_HIP_EXACT || mode == MYNAH_ASR_HIP_INT8ACT) g_numerics = mode;
+    if (mode == MYNAH_ASR_HIP_EXACT || mode == MYNAH_ASR_HIP_INT8ACT || mode == MYNAH_ASR_HIP_QMAT) g_numerics = mode;
     return mynah_asr_hip_numerics();
 }
 
 int mynah_asr_hip_numerics(void) {
     if (g_numerics < 0) {
         const char *e = getenv("MYNAH_ASR_HIP_NUMERICS");
-        g_numerics = (e && strcmp(e, "int8") == 0) ? MYNAH_ASR_HIP_INT8ACT : MYNAH_ASR_HIP_EXACT;
+        g_numerics = (e && strcmp(e, "int8") == 0)   ? MYNAH_ASR_HIP_INT8ACT
+                     : (e && strcmp(e, "qmat") == 0) ? MYNAH_ASR_HIP_QMAT
+                                                     : MYNAH_ASR_HIP_EXACT;
     }
     return g_numerics;
 }
@@ -726,7 +790,8 @@ int mynah_asr_hip_qgemm_dev(const mynah_asr_hip_weight *w, const float *dx, floa
     note_capture(pick_stream(stream));
     if (!w || !dx || !dy || T < 0) return fail("bad argument");
     if (T == 0) return 0;
-    if (check_numerics_supported(w->qtype)) return -1;
+    if (check_numerics_supported(w->qtype, w->dw.k, T)) return -1;
+    NumScope sc(eff_num(w->qtype, w->dw.k, T));
     return gemm_dev(c, w, dx, dy, T, act, pick_stream(stream));
 }
 
@@ -738,12 +803,14 @@ int mynah_asr_hip_qgemm_noalloc_dev(const mynah_asr_hip_weight *w, const float *
     if (!mynah_asr_hip_available()) return fail("no gfx950 device");
     if (!w || !dx || !dy || T < 0) return fail("bad argument");
     if (T == 0) return 0;
-    if (check_numerics_supported(w->qtype)) return -1;
+    if (check_numerics_supported(w->qtype, w->dw.k, T)) return -1;
+    NumScope sc(eff_num(w->qtype, w->dw.k, T));
     return gemm_noalloc(w, dx, dy, T, act, (hipStream_t)stream);
 }
 
 size_t mynah_asr_hip_noalloc_bytes(const mynah_asr_hip_weight *w, int T) {
     if (!w || T <= 0) return 0;
+    NumScope sc(eff_num(w->qtype, w->dw.k, T));
     size_t a, b;
     return noalloc_need(w, T, &a, &b);
 }
@@ -753,7 +820,8 @@ int mynah_asr_hip_prep_dev(const mynah_asr_hip_weight *w, const float *dx, int T
     if (begin(&c)) return -1;
     note_capture(pick_stream(stream));
     if (!w || !dx || T <= 0) return fail("bad argument");
-    if (check_numerics_supported(w->qtype)) return -1;
+    if (check_numerics_supported(w->qtype, w->dw.k, T)) return -1;
+    NumScope sc(eff_num(w->qtype, w->dw.k, T));
     return prep_for(c, w, dx, T, pick_stream(stream));
 }
 
@@ -763,7 +831,8 @@ int mynah_asr_hip_qgemm_prepped_dev(const mynah_asr_hip_weight *w, float *dy, in
     if (begin(&c)) return -1;
     note_capture(pick_stream(stream));
     if (!w || !dy || T <= 0) return fail("bad argument");
-    if (check_numerics_supported(w->qtype)) return -1;
+    if (check_numerics_supported(w->qtype, w->dw.k, T)) return -1;
+    NumScope sc(eff_num(w->qtype, w->dw.k, T));
     if (!prep_fits(c, w, T)) return fail("the prepared input does not fit this weight");
     return run_prepped(c, w, dy, T, act, pick_stream(stream));
 }
@@ -775,7 +844,7 @@ int mynah_asr_hip_qffn_dev(const mynah_asr_hip_weight *w1, const mynah_asr_hip_w
     note_capture(pick_stream(stream));
     if (!w1 || !w2 || !dx || !dy || T < 0 || w2->dw.k != w1->dw.n) return fail("bad argument");
     if (T == 0) return 0;
-    if (check_numerics_supported(w1->qtype) || check_numerics_supported(w2->qtype)) return -1;
+    if (check_numerics_supported(w1->qtype, w1->dw.k, T) || check_numerics_supported(w2->qtype, w2->dw.k, T)) return -1;
     return ffn_dev(c, w1, w2, dx, dy, T, pick_stream(stream));
 }
 
@@ -791,7 +860,7 @@ int mynah_asr_hip_qqkv_dev(const mynah_asr_hip_weight *wq, const mynah_asr_hip_w
     const mynah_asr_hip_weight *W[3] = {wq, wk, wv};
     float *const dy[3] = {dq, dk, dv};
     for (int i = 0; i < 3; i++)
-        if (check_numerics_supported(W[i]->qtype)) return -1;
+        if (check_numerics_supported(W[i]->qtype, W[i]->dw.k, T)) return -1;
     return qkv_dev(c, W, dx, dy, T, pick_stream(stream));
 }
 
@@ -879,6 +948,7 @@ int mynah_asr_hip_aed_decode_dev(const mynah_asr_hip_aed *a, const float *enc, i
     if (begin(&c)) return -1;
     if (aed_refuse_capture(pick_stream(stream))) return -1;
     if (aed_check(a, T)) return -1;
+    NumScope sc(MYNAH_ASR_HIP_EXACT);
     if (!enc || !prompt || n_prompt <= 0 || !tokens || cap < 0) return fail("bad argument");
     for (int i = 0; i < n_prompt; i++)
         if (prompt[i] < 0 || prompt[i] >= a->vocab) return fail("prompt token outside the vocabulary");
@@ -893,6 +963,7 @@ int mynah_asr_hip_aed_forced_dev(const mynah_asr_hip_aed *a, const float *enc, i
     if (begin(&c)) return -1;
     if (aed_refuse_capture(pick_stream(stream))) return -1;
     if (aed_check(a, T)) return -1;
+    NumScope sc(MYNAH_ASR_HIP_EXACT);
     if (!enc || !tokens || n <= 0 || n > a->max_seq || !logits) return fail("bad argument");
     for (int i = 0; i < n; i++)
         if (tokens[i] < 0 || tokens[i] >= a->vocab) return fail("token outside the vocabulary");
@@ -905,7 +976,8 @@ int mynah_asr_hip_qgemm(const mynah_asr_hip_wdesc *w, const float *x, float *out
     if (begin(&c)) return -1;
     if (!w || !x || !out || T < 0) return fail("bad argument");
     if (T == 0) return 0;
-    if (check_numerics_supported(w->qtype)) return -1;
+    if (check_numerics_supported(w->qtype, w->k, T)) return -1;
+    NumScope sc(eff_num(w->qtype, w->k, T));
     const mynah_asr_hip_weight *W = resident(w);
     if (!W) return -1;
     float *dx, *dy = (float *)c->y.get((size_t)T * w->n * sizeof(float));
@@ -921,7 +993,7 @@ int mynah_asr_hip_qffn(const mynah_asr_hip_wdesc *w1, const mynah_asr_hip_wdesc 
     if (begin(&c)) return -1;
     if (!w1 || !w2 || !x || !out || T < 0 || w2->k != w1->n) return fail("bad argument");
     if (T == 0) return 0;
-    if (check_numerics_supported(w1->qtype) || check_numerics_supported(w2->qtype)) return -1;
+    if (check_numerics_supported(w1->qtype, w1->k, T) || check_numerics_supported(w2->qtype, w2->k, T)) return -1;
     const mynah_asr_hip_weight *W1 = resident(w1), *W2 = resident(w2);
     if (!W1 || !W2) return -1;
     float *dx, *dy = (float *)c->y.get((size_t)T * w2->n * sizeof(float));
@@ -943,7 +1015,7 @@ int mynah_asr_hip_qqkv(const mynah_asr_hip_wdesc *wq, const mynah_asr_hip_wdesc 
     float *outs[3] = {oq, ok, ov};
     const mynah_asr_hip_weight *W[3];
     for (int i = 0; i < 3; i++) {
-        if (check_numerics_supported(ws[i]->qtype)) return -1;
+        if (check_numerics_supported(ws[i]->qtype, ws[i]->k, T)) return -1;
         if (!(W[i] = resident(ws[i]))) return -1;
     }
     float *dx;
@@ -953,7 +1025,8 @@ int mynah_asr_hip_qqkv(const mynah_asr_hip_wdesc *wq, const mynah_asr_hip_wdesc 
     for (int i = 0; i < 3; i++) {
         float *dy = (float *)c->y.get((size_t)T * ws[i]->n * sizeof(float));
         if (!dy) return fail("device buffer allocation failed");
-        if (mynah_asr_hip_numerics() == MYNAH_ASR_HIP_EXACT && mh_use_gemv(W[i]->dw, T)) {
+        NumScope si(eff_num(ws[i]->qtype, ws[i]->k, T));
+        if (num_now() == MYNAH_ASR_HIP_EXACT && mh_use_gemv(W[i]->dw, T)) {
             if (gemm_dev(c, W[i], dx, dy, T, 0, c->st)) return -1;
         } else {
             if (!prepared || !prep_fits(c, W[i], T))

@@ -26,7 +26,7 @@ NAMES = {F32: "F32", INT8: "INT8", INT4: "INT4", Q4_0: "Q4_0", Q8_0: "Q8_0", Q2_
 # bits per weight as stored (algorithmic HBM bytes of a weight = n*k*bits/8)
 BITS = {F32: 32.0, INT8: 8.0, INT4: 5.0, Q4_0: 4.5, Q8_0: 8.5, Q2_K: 2.625, Q3_K: 3.4375,
         Q4_K: 4.5, Q5_K: 5.5, Q6_K: 6.5625}
-EXACT, INT8ACT = 0, 1
+EXACT, INT8ACT, QMAT = 0, 1, 2
 
 # every symbol include/mynah_asr_hip.h declares
 HIP_SYMBOLS = [
@@ -189,6 +189,9 @@ class HipLib:
 
     def set_numerics(self, mode: int) -> int:
         return self.L.mynah_asr_hip_set_numerics(mode)
+
+    def numerics(self) -> int:
+        return self.L.mynah_asr_hip_numerics()
 
     def _check(self, rc: int, what: str) -> None:
         if rc != 0:
