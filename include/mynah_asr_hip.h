@@ -6,7 +6,7 @@
  * -1 (src/backend.c:74-77). Every entry point takes plain host pointers and
  * sizes; nothing here exposes a HIP or torch type (streams travel as void*).
  *
- * Numerics. Two modes, chosen process-wide with mynah_asr_hip_set_numerics():
+ * Numerics. Three modes, chosen process-wide with mynah_asr_hip_set_numerics():
  *   EXACT (default): every output row matches an f32 GEMM over the
  *     dequantized weights to |y - ref| <= 1e-4*|ref| + 1e-6 (ref accumulated in
  *     double), and a row's bits never depend on how many rows share the call.
@@ -23,6 +23,10 @@
  *     relative L2 for every block format, under that test's 5e-3 budget; this
  *     is a measurement on that case, not a bound (N(0, 1) activations at
  *     K = 1024 give 6.9e-3 to 7.8e-3). F32 weights return -1.
+ *   QMAT: qmat.c's own choice per product (src/qmat.c:503-651): INT8ACT for
+ *     INT8/INT4 weights with K <= 8192 at T <= 16 (and at every T with
+ *     MYNAH_ASR_QGEMM=1), EXACT for everything else. Bit-exact with the
+ *     reference wherever it computes in int8; not row-stable across T = 16.
  *
  * Return values: 0 = done, -1 = not done (the caller runs its CPU path);
  * mynah_asr_hip_last_error() names the reason for the calling thread.
