@@ -1838,11 +1838,12 @@ static int gemm_ngroups(float wbytes, float abytes, int tilesM, int nt) {
 static bool gemm_narrow(int grid) { return grid <= 512; }
 
 // 64 x 256 workgroup tiles (two column groups per wave, two workgroups per
-// CU) for the folded affine K-quants in EXACT numerics when there are enough
-// of them: measured at 12000 rows, Q4_K 1024->4096 294 -> 278 us, Q2_K
-// 4096->1024 280 -> 264 us (Q5_K 1%; Q3_K, Q8_0 and the A1 forms slower).
+// CU) for the folded affine K-quants and f32 weights in EXACT numerics when
+// there are enough of them: measured at 12000 rows, Q4_K 1024->4096 294 ->
+// 278 us, Q2_K 4096->1024 280 -> 264 us (Q5_K 1%; Q3_K, Q8_0 and the A1 forms
+// slower); f32 weights 1024->4096 at 6000 rows 176 -> 164 us.
 template <int QT, bool A1> constexpr bool wide_fmt() {
-    return !A1 && (QT == QT_Q2_K || QT == QT_Q4_K || QT == QT_Q5_K);
+    return !A1 && (QT == QT_Q2_K || QT == QT_Q4_K || QT == QT_Q5_K || QT == QT_F32);
 }
 template <int QT, bool A1>
 static bool gemm_wide(const DevW &W, int tilesM, int jobs) {
