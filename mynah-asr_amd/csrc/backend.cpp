@@ -99,7 +99,8 @@ struct Ctx {
     DBuf aed;    // the AED decoder's caches and vectors
     DBuf gs;     // split-K GEMV workspace
     DBuf gk;     // split-K GEMM workspace (chunk results)
-    int *pin = nullptr;   // pinned host int[2]: the step state read back
+    int *pin = nullptr;   // pinned host int[2][2]: the step state of two positions read back
+    hipEvent_t pev[2] = {nullptr, nullptr};   // their copies' completion
     PrepBuf pa;  // the products' input (prep_dev / qgemm_prepped_dev use this one)
     PrepBuf pb;  // the FFN's intermediate, prepared by the first product
 };
@@ -591,10 +592,15 @@ int aed_run(Ctx *c, const mynah_asr_hip_aed *a, const float *enc, int T, const i
     b.opart = take((size_t)b.nsplit * d), b.ml = take((size_t)b.nsplit * a->n_heads * 2);
     b.st = (int *)take(2 + (size_t)n_prompt);
     b.prompt = b.st + 2;
-    if (!c->pin && hipHostMalloc((void **)&c->pin, 2 * sizeof(int)) != hipSuccess) {
+    if (!c->pin && hipHostMalloc((void **)&c->pin, 4 * sizeof(int)) != hipSuccess) {
         c->pin = nullptr;
         return fail("pinned host allocation failed");
     }
+    for (int i = 0; i < 2; i++)
+        if (!c->pev[i] && hipEventCreateWithFlags(&c->pev[i], hipEventDisableTiming) != hipSuccess) {
+            c->pev[i] = nullptr;
+            return fail("event creation failed");
+        }
 
     // encoder projection and the per-layer cross K/V (decoder_aed.c:150-175)
     if (a->proj) {
@@ -612,11 +618,27 @@ int aed_run(Ctx *c, const mynah_asr_hip_aed *a, const float *enc, int T, const i
         return fail("H2D copy failed");
     AED_TRY(mh_launch_set_state(b.st, 0, prompt[0], st));
 
-    // position 0 eagerly, then the step captured once and replayed
+    // position 0 eagerly, then the step captured once and replayed. Greedy
+    // decoding reads each position's token back while the next position runs:
+    // the step's argmax already formed the next input row on the device, so
+    // position p+1 is enqueued before the host sees p's token (a position
+    // enqueued past an EOS or the cap only extends the internal cache by one
+    // row, within max_len, and its token is never read).
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
-    int n_out = 0, rc = 0;
-    for (int p = 0; p < max_len; p++) {
+    int n_out = 0, rc = 0, pending = -1;
+    bool stop = false;
+    auto resolve = [&](int q) {   // position q's token: the loop's EOS / cap test (decoder_aed.c:215-221)
+        if (hipEventSynchronize(c->pev[q & 1]) != hipSuccess) {
+            rc = fail("token read-back failed");
+            return true;
+        }
+        const int best = c->pin[2 * (q & 1) + 1];
+        if (best == eos || n_out >= cap) return true;
+        tokens[n_out++] = best;
+        return false;
+    };
+    for (int p = 0; p < max_len && !stop; p++) {
         if (p == 0) {
             if (aed_step(a, b, T, max_len, n_prompt, logits_out, true, st)) return -1;
         } else {
@@ -637,15 +659,15 @@ int aed_run(Ctx *c, const mynah_asr_hip_aed *a, const float *enc, int T, const i
             if (hipGraphLaunch(exec, st) != hipSuccess) { rc = fail("graph launch failed"); break; }
         }
         if (!tokens || p + 1 < n_prompt) continue;   // prompt positions: no sampling
-        if (hipMemcpyAsync(c->pin, b.st, 2 * sizeof(int), hipMemcpyDeviceToHost, st) != hipSuccess ||
-            hipStreamSynchronize(st) != hipSuccess) {
+        if (hipMemcpyAsync(c->pin + 2 * (p & 1), b.st, 2 * sizeof(int), hipMemcpyDeviceToHost, st) != hipSuccess ||
+            hipEventRecord(c->pev[p & 1], st) != hipSuccess) {
             rc = fail("token read-back failed");
             break;
         }
-        const int best = c->pin[1];
-        if (best == eos || n_out >= cap) break;
-        tokens[n_out++] = best;
+        if (pending >= 0) stop = resolve(pending);
+        pending = p;
     }
+    if (pending >= 0 && !stop && rc == 0) resolve(pending);
     if (hipStreamSynchronize(st) != hipSuccess && rc == 0) rc = fail("stream sync failed");
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
