@@ -15,6 +15,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -34,7 +35,9 @@ namespace {
 
 std::mutex g_mu;
 int g_ready = -1;
-int g_numerics = -1;
+// the process-wide numerics mode (-1: not yet read from the environment);
+// atomic: set_numerics may run while other threads' calls read it
+std::atomic<int> g_numerics{-1};
 
 struct CacheEnt {
     const void *key;
@@ -775,18 +778,22 @@ int mynah_asr_hip_available(void) {
 }
 
 int mynah_asr_hip_set_numerics(int mode) {
-    if (mode == MYNAH_ASR_HIP_EXACT || mode == MYNAH_ASR_HIP_INT8ACT || mode == MYNAH_ASR_HIP_QMAT) g_numerics = mode;
+    if (mode == MYNAH_ASR_HIP_EXACT || mode == MYNAH_ASR_HIP_INT8ACT || mode == MYNAH_ASR_HIP_QMAT)
+        g_numerics.store(mode, std::memory_order_relaxed);
     return mynah_asr_hip_numerics();
 }
 
 int mynah_asr_hip_numerics(void) {
-    if (g_numerics < 0) {
+    int m = g_numerics.load(std::memory_order_relaxed);
+    if (m < 0) {
         const char *e = getenv("MYNAH_ASR_HIP_NUMERICS");
-        g_numerics = (e && strcmp(e, "int8") == 0)   ? MYNAH_ASR_HIP_INT8ACT
-                     : (e && strcmp(e, "qmat") == 0) ? MYNAH_ASR_HIP_QMAT
-                                                     : MYNAH_ASR_HIP_EXACT;
+        m = (e && strcmp(e, "int8") == 0)   ? MYNAH_ASR_HIP_INT8ACT
+            : (e && strcmp(e, "qmat") == 0) ? MYNAH_ASR_HIP_QMAT
+                                            : MYNAH_ASR_HIP_EXACT;
+        int expect = -1;   // a concurrent first call or set_numerics may have won: keep theirs
+        if (!g_numerics.compare_exchange_strong(expect, m, std::memory_order_relaxed)) m = expect;
     }
-    return g_numerics;
+    return m;
 }
 
 const char *mynah_asr_hip_last_error(void) { return t_err; }
