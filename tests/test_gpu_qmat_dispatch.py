@@ -211,3 +211,35 @@ def test_device_decoder_in_qmat_mode(qmat_mode):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     finally:
         devq.close()
+
+
+def test_threads_each_get_their_products_mode(qmat_mode, orc):
+    """Four threads at once, INT8 weights at T = 4 (int8 path) and T = 40
+    (EXACT) interleaved: each call's mode is its own (the effective mode is
+    per call and per thread), so every result matches its serial twin."""
+    import threading
+    say("qmat dispatch, concurrent callers")
+    gpu = qmat_mode
+    w = M.Weight.make(gpu, M.INT8, gpu.randn(0, 0.02, (128, 1024)))
+    x = gpu.randn(1, 1.0, (40, 1024))
+    want = {4: int8_ref(orc, w, x[:4]), 40: in_mode(gpu, M.EXACT, w, x[:40])}
+    gpu.set_numerics(M.QMAT)
+    errors = []
+
+    def work(i):
+        try:
+            for r in range(6):
+                T = 4 if (i + r) % 2 == 0 else 40
+                y = M.host_qgemm(gpu, w, x[:T], keep=True)
+                if not np.array_equal(y.view(np.uint32), want[T].view(np.uint32)):
+                    errors.append((i, r, T))
+        except Exception as ex:   # surfaced below
+            errors.append((i, repr(ex)))
+
+    th = [threading.Thread(target=work, args=(i,)) for i in range(4)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    M.evict(gpu, w)
+    assert not errors, errors
