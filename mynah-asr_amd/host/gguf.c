@@ -268,6 +268,34 @@ const mynah_gguf_tensor *mynah_gguf_find(const mynah_gguf *g, const char *name) 
     return NULL;
 }
 
+/* IEEE binary16 -> binary32, exact for every input (subnormals normalised,
+ * inf / NaN kept) */
+static float half_to_f32(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    int e = (int)((h >> 10) & 31);
+    uint32_t mant = h & 0x3ffu, b;
+    if (e == 0) {
+        if (mant == 0) b = sign;
+        else {
+            e = 1;
+            while (!(mant & 0x400u)) { mant <<= 1; e--; }
+            b = sign | ((uint32_t)(e + 112) << 23) | ((mant & 0x3ffu) << 13);
+        }
+    } else if (e == 31) b = sign | 0x7f800000u | (mant << 13);
+    else b = sign | ((uint32_t)(e + 112) << 23) | (mant << 13);
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+/* bfloat16 is the top half of a binary32 */
+static float bf16_to_f32(uint32_t h) {
+    const uint32_t b = h << 16;
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
 int mynah_asr_qmat_init_gguf(mynah_asr_qmat *m, const mynah_gguf *g, const char *name) {
     memset(m, 0, sizeof(*m));
     const mynah_gguf_tensor *t = mynah_gguf_find(g, name);
@@ -275,6 +303,25 @@ int mynah_asr_qmat_init_gguf(mynah_asr_qmat *m, const mynah_gguf *g, const char 
     const int k = (int)t->ne[0], n = (int)t->ne[1];
     if (t->ggml_type == 0) {                 /* F32: borrowed, as qmat_init with F32 */
         m->f32 = (const float *)t->data;
+        m->qtype = MYNAH_ASR_Q_F32;
+        m->n = n;
+        m->k = k;
+        return 0;
+    }
+    if (t->ggml_type == 1 || t->ggml_type == 30) {
+        /* F16 / BF16: decoded to an owned f32 copy at load, as the reference's
+         * loader does for every non-F32 GGUF tensor (src/weights.c:90-104) */
+        const size_t ne = (size_t)n * (size_t)k;
+        if (t->nbytes < ne * 2) return -1;
+        float *f = (float *)malloc(ne * sizeof(float));
+        if (!f) return -1;
+        const unsigned char *p = (const unsigned char *)t->data;
+        for (size_t i = 0; i < ne; i++) {
+            const uint32_t h = (uint32_t)p[2 * i] | ((uint32_t)p[2 * i + 1] << 8);
+            f[i] = t->ggml_type == 1 ? half_to_f32(h) : bf16_to_f32(h);
+        }
+        m->owned_q = f;
+        m->f32 = f;
         m->qtype = MYNAH_ASR_Q_F32;
         m->n = n;
         m->k = k;

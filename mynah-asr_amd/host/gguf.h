@@ -46,7 +46,9 @@ const mynah_gguf_tensor *mynah_gguf_find(const mynah_gguf *g, const char *name);
 /* The qmat_init_st of a GGUF (src/qmat.c:114-143 for safetensors): a 2-D
  * tensor [n, k] (ne = {k, n}) of a block type the unit runs (Q4_0, Q8_0,
  * Q2_K..Q6_K) becomes a block qmat over the mapped bytes (zero-copy, borrowed:
- * the mapping must outlive m); an F32 tensor becomes an F32 qmat (borrowed).
+ * the mapping must outlive m); an F32 tensor becomes an F32 qmat (borrowed);
+ * an F16 or BF16 tensor is decoded to an owned f32 copy (src/weights.c:90-104
+ * decodes every non-F32 GGUF tensor at load), freed by mynah_asr_qmat_free.
  * 0 ok, -1 missing or unsupported. */
 int mynah_asr_qmat_init_gguf(mynah_asr_qmat *m, const mynah_gguf *g, const char *name);
 

@@ -15,7 +15,7 @@ import pytest
 import mynah_hip as M
 import oracle as O
 
-GGML = {"F32": 0, "F16": 1, "Q4_0": 2, "Q8_0": 8, "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+GGML = {"F32": 0, "F16": 1, "BF16": 30, "Q4_0": 2, "Q8_0": 8, "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
 QT_OF = {GGML["Q4_0"]: M.Q4_0, GGML["Q8_0"]: M.Q8_0, GGML["Q4_K"]: M.Q4_K, GGML["Q6_K"]: M.Q6_K,
          GGML["Q2_K"]: M.Q2_K}
 
@@ -230,6 +230,37 @@ def test_qmat_from_gguf_is_zero_copy(lib, tmp_path):
     g.close()
 
 
+def test_half_tensors_decode_to_owned_f32(lib, tmp_path):
+    """F16 and BF16 tensors become F32 qmats over an owned decoded copy, as
+    the reference's loader decodes every non-F32 GGUF tensor at load
+    (src/weights.c:90-104). The decoded values are checked against numpy's
+    float16 conversion and, for BF16, against the f32 whose top half it is;
+    every f16 bit pattern appears once (subnormals, infinities, NaNs)."""
+    import ctypes as C
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16).reshape(256, 256)
+    f = np.random.default_rng(5).standard_normal((32, 64)).astype(np.float32)
+    bf = (f.view(np.uint32) >> 16).astype(np.uint16)
+    path = str(tmp_path / "h.gguf")
+    write_gguf(path, [("h", GGML["F16"], (256, 256), h.tobytes()),
+                      ("b", GGML["BF16"], (64, 32), bf.tobytes())])
+    g = M.Gguf(lib, path)
+    ptrs = {n: p for n, _, _, _, p in g.tensors()}
+    for name, shape, want in (("h", (256, 256), h.view(np.float16).astype(np.float32)),
+                              ("b", (32, 64), (bf.astype(np.uint32) << 16).view(np.float32))):
+        m = g.qmat(name)
+        try:
+            assert (m.qtype, m.n, m.k) == (M.F32, shape[0], shape[1])
+            assert m.f32 and m.f32 != ptrs[name]          # an owned copy, not the mapping
+            got = np.ctypeslib.as_array(C.cast(m.f32, C.POINTER(C.c_uint32)), shape=shape).copy()
+            nan = np.isnan(want)
+            assert np.array_equal(got[~nan], want.view(np.uint32)[~nan])
+            assert np.isnan(got.view(np.float32)[nan]).all()
+            assert np.array_equal(got[nan] >> 31, want.view(np.uint32)[nan] >> 31)
+        finally:
+            lib.H.mynah_asr_qmat_free(C.byref(m))
+    g.close()
+
+
 @pytest.mark.gpu
 def test_gguf_weights_on_the_device(gpu, orc, tmp_path):
     """Products from GGUF-mapped blocks equal the oracle's product over the
@@ -259,6 +290,17 @@ def test_gguf_weights_on_the_device(gpu, orc, tmp_path):
         assert (err <= 1e-4 * np.abs(ref) + 1e-6).all(), name
         H.mynah_asr_qmat_free(C.byref(m))
         H.mynah_asr_qmat_free(C.byref(m2))
+    g.close()
+    # an F16 tensor: the decoded f32 copy runs on the device as an F32 qmat
+    wh = gpu.randn(10, 0.02, (48, 1024)).astype(np.float16)
+    write_gguf(path, [("h", GGML["F16"], (1024, 48), wh.tobytes())])
+    g = M.Gguf(gpu, path)
+    m = g.qmat("h")
+    out = np.empty((40, 48), np.float32)
+    H.mynah_asr_qmat_mul(C.byref(m), x.ctypes.data, out.ctypes.data, 40)
+    ref = orc.gemm_f64(x, wh.astype(np.float32))
+    assert (np.abs(out - ref) <= 1e-4 * np.abs(ref) + 1e-6).all()
+    H.mynah_asr_qmat_free(C.byref(m))
     g.close()
 
 
