@@ -164,7 +164,8 @@ def run_int8act(B, M_, M):
     out = {}
     lib.set_numerics(1)
     try:
-        for name, qt, MM, shapes, seed in (("int8act_q8_0_m6000", M_.Q8_0, M, ENC_SHAPES, 0),
+        for name, qt, MM, shapes, seed in (("int8act_int8_m6000", M_.INT8, M, ENC_SHAPES, 0),
+                                           ("int8act_q8_0_m6000", M_.Q8_0, M, ENC_SHAPES, 0),
                                            ("int8act_q4_k_m12000", M_.Q4_K, 12000, KQ_SHAPES, 100),
                                            ("int8act_q5_k_m12000", M_.Q5_K, 12000, KQ_SHAPES, 100)):
             log(f"[bench] {name}")

@@ -224,13 +224,14 @@ void prep_sizes(int kind, int Mpad, int Kp, size_t b[3]) {
 // (xp, xs16, xpf), sized by prep_sizes:
 //   EXACT:           xp = f16 (hi, lo) A fragments, xs16 = the mins operand of
 //                    the affine formats, xpf = chunk fold factors
-//   INT8ACT QMAT:    xp = int8 A fragments, xs16 = row scales sx
+//   INT8ACT QMAT:    xp = int8 A fragments, xs16 = row scales sx (xpf holds
+//                    each row's factor 127 / amax while the preparation runs)
 //   INT8ACT ROW/SB:  xp = int8 values as f16 A fragments, xpf = their scales
 //                    per chunk, xs16 = the mins operand of the affine formats
 hipError_t launch_prep(int kind, const mynah_asr_hip_weight *W, const float *dx, int T, uint8_t *xp, float *xs16,
                        float *xpf, hipStream_t st) {
     const int Mpad = mh_mpad(T), Kp = W->dw.Kp, k = W->dw.k;
-    if (kind == MH_I8_QMAT) return mh_launch_prep_i8(dx, T, k, Kp, Mpad, xp, xs16, st);
+    if (kind == MH_I8_QMAT) return mh_launch_prep_i8(dx, T, k, Kp, Mpad, xp, xs16, xpf, st);   // (xpf: Mpad * Kp / 128 floats)
     if (kind) return mh_launch_prep_a1(kind, dx, T, k, Kp, Mpad, xp, xs16, xpf, wants_xsum(W->qtype), st);
     const int vec = (k % 8 == 0) && (((uintptr_t)dx & 15) == 0);
     return mh_launch_prep(dx, T, k, Kp, Mpad, xp, xs16, xpf, wants_xsum(W->qtype), vec, st);

@@ -1330,64 +1330,138 @@ __device__ __forceinline__ int act_q8(float v, float inv) {
     return q > 127 ? 127 : (q < -127 ? -127 : q);
 }
 
-// one workgroup (4 waves) per 32-row group
-// 16 waves per 32-row group: two rows each for the row maxima, then the
-// ksteps split over the waves (a 32-row group per 4 waves left the chip idle)
-constexpr int PREP_I8_NW = 16;
-template <bool VEC>
-__global__ __launch_bounds__(PREP_I8_NW * 64) void k_prep_i8(const float *__restrict__ x, int M, int K, int Kp,
-                                                             uint8_t *__restrict__ qx, float *__restrict__ sx) {
-    __shared__ float invs[32];
-    const int G = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    constexpr int RPW = 32 / PREP_I8_NW;
-    for (int rr = 0; rr < RPW; rr++) {
-        const int m = 32 * G + RPW * wave + rr;
-        float amax = 0.0f;
-        if (m < M) {
-            const float *row = x + (size_t)m * K;
-#pragma unroll 4
-            for (int j = lane; j < K; j += 64) amax = fmaxf(amax, fabsf(row[j]));
-        }
-        for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
-        if (lane == 0) {
-            invs[RPW * wave + rr] = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-            sx[m] = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 0.0f;
+// Otherwise two launches, each with work for the whole chip: the row scales (one wave
+// per row: sx = amax / 127 and its factor 127 / amax, both rounded once, as
+// quantize_act_int8 forms them), then the int8 values (one wave per 32-row
+// group and kstep, the MFMA A-fragment layout).
+// One pass for K <= 4096 with 16-byte rows: a wave per row holds the whole
+// row in registers. Lane l owns NSL of the row's 16-byte fragment slots
+// (slot q = l + 64 t: kstep q / 2, half hh = q % 2, elements 32 s + 8 hh ..
+// +7 and 32 s + 16 + 8 hh .. +7), loads them, takes the row maximum over the
+// wave, then quantizes and stores exactly those slots. A workgroup holds 8
+// consecutive rows: the 8 lanes of one 128-byte line of a fragment are its
+// rows r .. r + 7, so every line is written by one workgroup.
+template <int NSL>
+__global__ __launch_bounds__(512) void k_prep_i8_row(const float *__restrict__ x, int M, int K, int Kp, int Mpad,
+                                                     uint8_t *__restrict__ qx, float *__restrict__ sx) {
+    const int m = blockIdx.x * 8 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (m >= Mpad) return;
+    const int S = Kp / 32, G = m >> 5, r = m & 31;
+    const bool live_row = m < M;
+    const float *row = x + (size_t)(live_row ? m : 0) * K;
+    float v[NSL][16];
+    float amax = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NSL; t++) {
+        const int q = lane + 64 * t, s = q >> 1, hh = q & 1;
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++) {
+            const int k0 = 32 * s + 16 * kh + 8 * hh;
+            float4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
+            if (live_row && q < 2 * S && k0 < K) {
+                a = *(const float4 *)(row + k0);
+                b = *(const float4 *)(row + k0 + 4);
+            }
+            v[t][8 * kh + 0] = a.x; v[t][8 * kh + 1] = a.y; v[t][8 * kh + 2] = a.z; v[t][8 * kh + 3] = a.w;
+            v[t][8 * kh + 4] = b.x; v[t][8 * kh + 5] = b.y; v[t][8 * kh + 6] = b.z; v[t][8 * kh + 7] = b.w;
         }
     }
-    __syncthreads();
-    const int r = lane & 31, hh = lane >> 5, m = 32 * G + r;
-    const float inv = invs[r];
-    const bool live = m < M && inv > 0.0f;
-    const float *row = x + (size_t)(m < M ? m : 0) * K;
-    const int S = Kp / 32;
+#pragma unroll
+    for (int t = 0; t < NSL; t++)
+#pragma unroll
+        for (int j = 0; j < 16; j++) amax = fmaxf(amax, fabsf(v[t][j]));
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    const float iv = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    if (lane == 0) sx[m] = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 0.0f;
+    const bool live = live_row && iv > 0.0f;
     static const int kWord[8] = {0, 0, 1, 1, 0, 0, 1, 1};
     static const int kByte[8] = {0, 2, 0, 2, 1, 3, 1, 3};
-    for (int s = wave; s < S; s += PREP_I8_NW) {
+#pragma unroll
+    for (int t = 0; t < NSL; t++) {
+        const int q = lane + 64 * t, s = q >> 1, hh = q & 1;
+        if (q >= 2 * S) continue;
         uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int kh = 0; kh < 2; kh++) {
             const int k0 = 32 * s + 16 * kh + 8 * hh;
-            float v[8];
-            if constexpr (VEC) {   // K % 8 == 0, 16-byte rows: the lane's 8 elements in two loads
-                float4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
-                if (live && k0 < K) {
-                    a = *(const float4 *)(row + k0);
-                    b = *(const float4 *)(row + k0 + 4);
-                }
-                v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-                v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; j++) v[j] = (live && k0 + j < K) ? row[k0 + j] : 0.0f;
-            }
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const int q = (live && k0 + j < K) ? act_q8(v[j], inv) : 0;
-                w[2 * kh + kWord[j]] |= ((uint32_t)q & 0xffu) << (8 * kByte[j]);
+                const int qv = (live && k0 + j < K) ? act_q8(v[t][8 * kh + j], iv) : 0;
+                w[2 * kh + kWord[j]] |= ((uint32_t)qv & 0xffu) << (8 * kByte[j]);
             }
         }
-        *(uint4 *)(qx + (((size_t)G * S + s) * 64 + lane) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+        *(uint4 *)(qx + (((size_t)G * S + s) * 64 + r + 32 * hh) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
     }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_rowscale_i8(const float *__restrict__ x, int M, int K, int Mpad,
+                                                     float *__restrict__ sx, float *__restrict__ inv) {
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (m >= Mpad) return;
+    float amax = 0.0f;
+    if (m < M) {
+        const float *row = x + (size_t)m * K;
+        if constexpr (VEC) {   // K % 8 == 0, 16-byte rows: four 16-byte loads per lane at a time
+            for (int j0 = 4 * lane; j0 < K; j0 += 1024) {
+                float4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int j = j0 + 256 * u;
+                    v[u] = j < K ? *(const float4 *)(row + j) : float4{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    amax = fmaxf(fmaxf(fmaxf(amax, fabsf(v[u].x)), fmaxf(fabsf(v[u].y), fabsf(v[u].z))), fabsf(v[u].w));
+            }
+        } else {
+#pragma unroll 4
+            for (int j = lane; j < K; j += 64) amax = fmaxf(amax, fabsf(row[j]));
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    if (lane == 0) {
+        inv[m] = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+        sx[m] = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 0.0f;
+    }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_quant_i8(const float *__restrict__ x, int M, int K, int Kp,
+                                                  uint8_t *__restrict__ qx, const float *__restrict__ inv) {
+    const int G = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int S = Kp / 32, s = blockIdx.y * 4 + wave;
+    if (s >= S) return;
+    const int r = lane & 31, hh = lane >> 5, m = 32 * G + r;
+    const float iv = inv[m];
+    const bool live = m < M && iv > 0.0f;
+    const float *row = x + (size_t)(m < M ? m : 0) * K;
+    static const int kWord[8] = {0, 0, 1, 1, 0, 0, 1, 1};
+    static const int kByte[8] = {0, 2, 0, 2, 1, 3, 1, 3};
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int kh = 0; kh < 2; kh++) {
+        const int k0 = 32 * s + 16 * kh + 8 * hh;
+        float v[8];
+        if constexpr (VEC) {   // the lane's 8 elements in two 16-byte loads
+            float4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
+            if (live && k0 < K) {
+                a = *(const float4 *)(row + k0);
+                b = *(const float4 *)(row + k0 + 4);
+            }
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = (live && k0 + j < K) ? row[k0 + j] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int q = (live && k0 + j < K) ? act_q8(v[j], iv) : 0;
+            w[2 * kh + kWord[j]] |= ((uint32_t)q & 0xffu) << (8 * kByte[j]);
+        }
+    }
+    *(uint4 *)(qx + (((size_t)G * S + s) * 64 + lane) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 // ---------------------------------------------------------------------------
@@ -1491,6 +1565,7 @@ __global__ __launch_bounds__(64) void k_prep_a1_sb(const float *__restrict__ x, 
 
 // PA1_ROW: workgroup = one 32-row group; 16 waves find the row maxima (two
 // rows each), then take the chunks in turn
+constexpr int PREP_I8_NW = 16;
 template <bool VEC>
 __global__ __launch_bounds__(PREP_I8_NW * 64) void k_prep_a1_row(const float *__restrict__ x, int M, int K, int Kp,
                                                                  uint8_t *__restrict__ xp, float *__restrict__ xpf) {
@@ -1623,6 +1698,164 @@ __global__ __launch_bounds__(256) void k_gemm_i8(DevW W, const uint8_t *__restri
             else v = __fmul_rn(acc[i][e], sx[m]);
             y[(size_t)m * W.n + n] = act ? silu_f(v) : v;
         }
+}
+
+// The qmat INT8 product at encoder sizes: one int32 sum per output over all
+// of K (qmat.c:464-500), so the main loop is MFMAs only. Workgroup = 4 waves
+// side by side over N: tile TR row groups x 4 CW column groups of 32, wave w
+// takes every row group against column groups CW w .. CW w + CW - 1. The
+// loop runs in steps of SK ksteps:
+//   * the activations, which all four waves read, go global -> registers
+//     two steps ahead, then into one of two LDS slots at the end of the step
+//     before their use (one barrier per step);
+//   * each wave's weight fragments are its own (no reuse between waves), so
+//     they go global -> registers one step ahead and never touch LDS.
+// Only ordinary loads are used, so the compiler's own waits before each use
+// count exactly what is still in flight (with global_load_lds it cannot, and
+// waits for everything). Row groups past the prepared rows and column groups
+// past Np load a valid neighbour's bytes (no output reads them), and the
+// loads past the last step reload it, so every step issues the same loads.
+// Every fragment is the MFMA's own 1 KiB lane-order block ([group][kstep][64]
+// [16 B]): coalesced 16-byte loads, conflict-free 16-byte LDS accesses.
+// Tiles go to the XCDs in contiguous band-major runs (as k_gemm), so a row
+// band's column tiles share one L2. The sums are exact integers: the result
+// has the bits of k_gemm_i8.
+template <int TR, int CW, int SK>
+__global__ __launch_bounds__(256, 2) void k_gemm_i8t(DevW W, const uint8_t *__restrict__ qx,
+                                                     const float *__restrict__ sx, float *__restrict__ y, int M,
+                                                     int act, int tilesM, int tilesN) {
+    constexpr int TC = 4 * CW;                  // tile in column groups
+    constexpr int STB = TR * SK * 1024;         // LDS slot: [TR][SK][1 KiB] activations
+    constexpr int PPW = TR * SK / 4;            // activation fragments per wave and step
+    constexpr int LDSB = 2 * STB > 4 * 32 * 36 * 4 ? 2 * STB : 4 * 32 * 36 * 4;   // two slots; the epilogue's tiles
+    static_assert(TR * SK % 4 == 0, "step shape");
+    __shared__ __attribute__((aligned(16))) uint8_t sbuf[LDSB];
+    const int ntiles = tilesM * tilesN, bid = blockIdx.x;
+    const int q8 = ntiles / 8, rem = ntiles % 8, xcd = bid % 8, loc = bid / 8;
+    const int t = xcd < rem ? xcd * (q8 + 1) + loc : rem * (q8 + 1) + (xcd - rem) * q8 + loc;
+    const int tm = t / tilesN, tn = t - tm * tilesN;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int hh = lane >> 5, col = lane & 31;
+    const int S = W.Kp / 32, NS = S / SK;
+    const int G0 = tm * TR, GC0 = tn * TC + CW * wave;
+    const int Gend = (M + 63) / 64 * 2, GCend = W.Np / 32;   // prepared row groups (M padded to 64); column groups
+
+    const uint8_t *bsrc[CW];
+#pragma unroll
+    for (int j = 0; j < CW; j++) bsrc[j] = W.p0 + (size_t)min(GC0 + j, GCend - 1) * S * 1024 + lane * 16;
+    const uint8_t *asrc[PPW];
+    int aoff[PPW];   // LDS offset of the wave's fragment u within a slot
+#pragma unroll
+    for (int u = 0; u < PPW; u++) {
+        const int pc = wave * PPW + u, grp = pc / SK, sl = pc % SK;
+        asrc[u] = qx + ((size_t)min(G0 + grp, Gend - 1) * S + sl) * 1024 + lane * 16;
+        aoff[u] = (grp * SK + sl) * 1024 + lane * 16;
+    }
+    auto load_b = [&](int st, i4v(&b)[CW][SK]) {
+        st = min(st, NS - 1);
+#pragma unroll
+        for (int j = 0; j < CW; j++)
+#pragma unroll
+            for (int k = 0; k < SK; k++) b[j][k] = *(const i4v *)(bsrc[j] + (size_t)(SK * st + k) * 1024);
+    };
+    auto load_a = [&](int st, i4v(&r)[PPW]) {
+        st = min(st, NS - 1);
+#pragma unroll
+        for (int u = 0; u < PPW; u++) r[u] = *(const i4v *)(asrc[u] + (size_t)SK * st * 1024);
+    };
+    auto put_a = [&](const i4v(&r)[PPW], uint8_t *B) {
+#pragma unroll
+        for (int u = 0; u < PPW; u++) *(i4v *)(B + aoff[u]) = r[u];
+    };
+
+    i16v acc[TR][CW];
+#pragma unroll
+    for (int i = 0; i < TR; i++)
+#pragma unroll
+        for (int j = 0; j < CW; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0;
+    i4v bb0[CW][SK], bb1[CW][SK], ra0[PPW], ra1[PPW];
+    load_b(0, bb0);
+    load_a(0, ra0);
+    load_a(1, ra1);
+    put_a(ra0, sbuf);
+    __syncthreads();
+    // step st: b = B(st), ra = A(st + 1) (written to slot (st + 1) & 1 at
+    // the end), rn receives A(st + 2), bn receives B(st + 1)
+    auto step = [&](int st, const i4v(&b)[CW][SK], i4v(&bn)[CW][SK], const i4v(&ra)[PPW], i4v(&rn)[PPW]) {
+        load_b(st + 1, bn);
+        load_a(st + 2, rn);
+        __builtin_amdgcn_sched_barrier(0);   // (the loads go out before the step's MFMAs)
+        const uint8_t *B = sbuf + (st & 1) * STB;
+#pragma unroll
+        for (int k = 0; k < SK; k++) {
+            i4v a[TR];
+#pragma unroll
+            for (int i = 0; i < TR; i++) a[i] = *(const i4v *)(B + (i * SK + k) * 1024 + lane * 16);
+#pragma unroll
+            for (int i = 0; i < TR; i++)
+#pragma unroll
+                for (int j = 0; j < CW; j++) {
+                    acc[i][j] = mfma_i8(a[i], b[j][k], acc[i][j]);
+                }
+        }
+        // slot (st + 1) & 1 was last read at step st - 1, before the barrier
+        // that ended it
+        put_a(ra, sbuf + ((st + 1) & 1) * STB);
+        __syncthreads();
+    };
+    for (int st = 0; st < NS; st += 2) {
+        step(st, bb0, bb1, ra1, ra0);
+        if (st + 1 < NS) step(st + 1, bb1, bb0, ra0, ra1);
+    }
+    // epilogue: y = (acc * ws[n]) * sx[m] (SiLU when act). Each 32 x 32
+    // block goes through the wave's own 4 KiB of LDS (row stride 36 floats)
+    // and out as rows of 32 columns in 16-byte stores, 8 lanes per row;
+    // without 16-byte alignment (y, or N not a multiple of 4), element by
+    // element.
+    const bool vec = (W.n & 3) == 0 && ((uintptr_t)y & 15) == 0;
+    float *T = (float *)sbuf + wave * 32 * 36;   // (the last step ended with a barrier)
+#pragma unroll
+    for (int i = 0; i < TR; i++) {
+        float sxr[16];
+#pragma unroll
+        for (int e = 0; e < 16; e++) sxr[e] = sx[min(32 * (G0 + i) + drow(e, hh), M - 1)];
+#pragma unroll
+        for (int j = 0; j < CW; j++) {
+            const int n = 32 * (GC0 + j) + col;
+            const float ws = W.h2[min(n, W.n - 1)];
+            if (vec) {
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const float v = __fmul_rn(__fmul_rn((float)acc[i][j][e], ws), sxr[e]);
+                    T[drow(e, hh) * 36 + col] = act ? silu_f(v) : v;
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                const int nc = 32 * (GC0 + j) + 4 * (lane & 7);
+#pragma unroll
+                for (int r0 = 0; r0 < 32; r0 += 8) {
+                    const int r = r0 + (lane >> 3), m = 32 * (G0 + i) + r;
+                    const float4 v = *(const float4 *)(T + r * 36 + 4 * (lane & 7));
+                    if (m < M && nc < W.n) *(float4 *)(y + (size_t)m * W.n + nc) = v;
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            } else if (n < W.n) {
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int m = 32 * (G0 + i) + drow(e, hh);
+                    if (m >= M) continue;
+                    const float v = __fmul_rn(__fmul_rn((float)acc[i][j][e], ws), sxr[e]);
+                    y[(size_t)m * W.n + n] = act ? silu_f(v) : v;
+                }
+            }
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -2073,12 +2306,22 @@ hipError_t mh_launch_prep_a1(int kind, const float *x, int M, int K, int Kp, int
     return hipGetLastError();
 }
 
-hipError_t mh_launch_prep_i8(const float *x, int M, int K, int Kp, int Mpad, uint8_t *qx, float *sx,
+hipError_t mh_launch_prep_i8(const float *x, int M, int K, int Kp, int Mpad, uint8_t *qx, float *sx, float *inv,
                              hipStream_t st) {
-    if (K % 8 == 0 && ((uintptr_t)x & 15) == 0)
-        hipLaunchKernelGGL(k_prep_i8<true>, dim3(Mpad / 32), dim3(PREP_I8_NW * 64), 0, st, x, M, K, Kp, qx, sx);
-    else
-        hipLaunchKernelGGL(k_prep_i8<false>, dim3(Mpad / 32), dim3(PREP_I8_NW * 64), 0, st, x, M, K, Kp, qx, sx);
+    const dim3 gq(Mpad / 32, (Kp / 32 + 3) / 4);
+    const bool vec = K % 8 == 0 && ((uintptr_t)x & 15) == 0;
+    if (vec && Kp <= 4096) {
+        const dim3 g(Mpad / 8);
+        if (Kp <= 1024) hipLaunchKernelGGL(k_prep_i8_row<1>, g, dim3(512), 0, st, x, M, K, Kp, Mpad, qx, sx);
+        else if (Kp <= 2048) hipLaunchKernelGGL(k_prep_i8_row<2>, g, dim3(512), 0, st, x, M, K, Kp, Mpad, qx, sx);
+        else hipLaunchKernelGGL(k_prep_i8_row<4>, g, dim3(512), 0, st, x, M, K, Kp, Mpad, qx, sx);
+    } else if (vec) {
+        hipLaunchKernelGGL(k_rowscale_i8<true>, dim3(Mpad / 4), dim3(256), 0, st, x, M, K, Mpad, sx, inv);
+        hipLaunchKernelGGL(k_quant_i8<true>, gq, dim3(256), 0, st, x, M, K, Kp, qx, inv);
+    } else {
+        hipLaunchKernelGGL(k_rowscale_i8<false>, dim3(Mpad / 4), dim3(256), 0, st, x, M, K, Mpad, sx, inv);
+        hipLaunchKernelGGL(k_quant_i8<false>, gq, dim3(256), 0, st, x, M, K, Kp, qx, inv);
+    }
     return hipGetLastError();
 }
 
@@ -2092,9 +2335,32 @@ static hipError_t launch_i8(const DevW &W, const uint8_t *qx, const float *sx, f
     return hipGetLastError();
 }
 
+// the tiled INT8 product, tile TR x 4 CW groups of 32
+template <int TR, int CW>
+static hipError_t launch_i8t(const DevW &W, const uint8_t *qx, const float *sx, float *y, int M, int act,
+                             hipStream_t st) {
+    const int tilesM = (mh_mpad(M) / 32 + TR - 1) / TR, tilesN = (W.Np / 32 + 4 * CW - 1) / (4 * CW);
+    hipLaunchKernelGGL((k_gemm_i8t<TR, CW, 4>), dim3(tilesM * tilesN), dim3(256), 0, st, W, qx, sx, y, M, act,
+                       tilesM, tilesN);
+    return hipGetLastError();
+}
+
+// work on the busiest CU, in tile units of 32 x 32, for tiles of tr x tc
+// groups dealt over the 256 CUs
+static long i8t_makespan(int M, int Np, int tr, int tc) {
+    const long tiles = (long)((mh_mpad(M) / 32 + tr - 1) / tr) * ((Np / 32 + tc - 1) / tc);
+    return (tiles + 255) / 256 * tr * tc;
+}
+
 template <int QT>
 static hipError_t gemm_i8_t(const DevW &W, const uint8_t *qx, const float *sx, float *y, int M, int act,
                             hipStream_t st) {
+    if (QT == QT_INT8 && M > 64) {
+        // 96 x 256 or 64 x 256 tiles, whichever leaves less on the busiest CU
+        if (i8t_makespan(M, W.Np, 3, 8) <= i8t_makespan(M, W.Np, 2, 8))
+            return launch_i8t<3, 2>(W, qx, sx, y, M, act, st);
+        return launch_i8t<2, 2>(W, qx, sx, y, M, act, st);
+    }
     if (M <= 64 || mh_mpad(M) % 64 != 0) return launch_i8<QT, 1>(W, qx, sx, y, M, act, st);
     return launch_i8<QT, 2>(W, qx, sx, y, M, act, st);
 }

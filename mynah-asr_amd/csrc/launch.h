@@ -100,7 +100,9 @@ int mh_i8_kind(int qtype);
 // (Mpad * Kp / 4 bytes) when want_xsum (MH_I8_SB only)
 hipError_t mh_launch_prep_a1(int kind, const float *x, int M, int K, int Kp, int Mpad, uint8_t *xp, float *xs16,
                              float *xpf, int want_xsum, hipStream_t st);
-hipError_t mh_launch_prep_i8(const float *x, int M, int K, int Kp, int Mpad, uint8_t *qx, float *sx,
+// MH_I8_QMAT: qx (Mpad * Kp bytes), sx (Mpad floats); inv: Mpad floats of
+// scratch (each row's 127 / amax, between the two launches)
+hipError_t mh_launch_prep_i8(const float *x, int M, int K, int Kp, int Mpad, uint8_t *qx, float *sx, float *inv,
                              hipStream_t st);
 hipError_t mh_launch_gemm_i8(int qtype, const DevW &W, const uint8_t *qx, const float *sx, float *y, int M,
                              int act, hipStream_t st);

@@ -102,6 +102,38 @@ def test_int8act_large_products_bit_exact(int8act, orc, qt):
         dw.close()
 
 
+def test_int8act_int8_tiled_rows_match(int8act, orc):
+    """qmat INT8 weights above 64 rows run the tiled int8 GEMM (96 x 256 or
+    64 x 256 tiles), at most 64 rows the one-wave form: the same exact int32
+    sums and epilogue, so every row must carry the same bits at every M
+    (ragged N and K, M = 2100 down to 1), and sampled rows match the
+    reference's int8 path (qmat.c:464-500) restated in the oracle. The
+    preparation runs in one pass for 16-byte rows with K <= 4096 and in two
+    otherwise (K = 1001, 8192)."""
+    import torch
+    say("int8act INT8 tiled vs one-wave")
+    gpu = int8act
+    for (n, k) in ((1000, 1056), (4096, 1024), (1024, 4096), (96, 2080), (200, 1001), (64, 8192)):
+        w = M.Weight.make(gpu, M.INT8, gpu.randn(7, 0.02, (n, k)))
+        dw = M.DeviceWeight(gpu, w)
+        x = gpu.randn(8, 1.0, (2100, k))
+        x[5] = 0.0
+        xd = torch.from_numpy(x).cuda()
+        outs = {}
+        for T in (2100, 700, 129, 65, 64, 16, 1):
+            y = torch.full((T, n), float("nan"), dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+            dw.gemm(xd.data_ptr(), y.data_ptr(), T)
+            torch.cuda.synchronize()
+            outs[T] = y.cpu().numpy()
+        for T in (700, 129, 65, 64, 16, 1):
+            assert np.array_equal(outs[T].view(np.uint32), outs[2100][:T].view(np.uint32)), (n, k, T)
+        rows = np.r_[0:8, 1000:1004, 2092:2100]
+        ref = oracle_int8(orc, w, x[rows])
+        assert np.array_equal(outs[2100][rows].view(np.uint32), ref.view(np.uint32)), (n, k)
+        dw.close()
+
+
 @pytest.mark.parametrize("name", ["Q4_K", "Q5_K", "Q8_0", "Q4_0", "Q2_K", "Q3_K", "Q6_K"])
 def test_int8act_reference_budget(int8act, orc, name):
     """test_quant.c:157-205: 37 rows of 0.02 * uniform(-1, 1), 131 tokens of

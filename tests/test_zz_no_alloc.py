@@ -71,7 +71,7 @@ def test_noalloc_matches_qgemm_dev(gpu, qt, n, k, m1, m2):
 # INT8ACT's three activation forms: per-row (Q8_0), per-super-block with the
 # mins operand (Q4_K), and the qmat INT4 form on the i8 MFMA; calls of 900, 33
 # and 5 rows in a row (the last takes the M <= 16 path)
-@pytest.mark.parametrize("qt", [M.Q8_0, M.Q4_K, M.INT4], ids=lambda q: M.NAMES[q])
+@pytest.mark.parametrize("qt", [M.Q8_0, M.Q4_K, M.INT4, M.INT8], ids=lambda q: M.NAMES[q])
 def test_noalloc_int8act_matches_qgemm_dev(gpu, qt):
     import torch
     say("noalloc INT8ACT", M.NAMES[qt])
