@@ -1607,6 +1607,53 @@ __global__ __launch_bounds__(PREP_I8_NW * 64) void k_prep_a1_row(const float *__
     }
 }
 
+// PA1_ROW in one pass for K <= 4096 with 16-byte rows (as k_prep_i8_row): a
+// wave per row holds the row in registers. Lane l owns NSL of the row's
+// 16-byte fragment slots (slot q = l + 64 t: chunk q / 16, half-step
+// (q / 2) % 8, half q % 2: 8 elements), takes the row maximum over the wave,
+// then stores those slots; lanes l < Kc (and l + 64 ...) store the chunk
+// scales. A workgroup holds 8 consecutive rows, so every 128-byte line of a
+// fragment is written by one workgroup.
+template <int NSL>
+__global__ __launch_bounds__(512) void k_prep_a1_row1(const float *__restrict__ x, int M, int K, int Kp, int Mpad,
+                                                      uint8_t *__restrict__ xp, float *__restrict__ xpf) {
+    const int m = blockIdx.x * 8 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (m >= Mpad) return;
+    const int Kc = Kp / 128, NQ = Kp / 8, G = m >> 5, r = m & 31;
+    const bool live_row = m < M;
+    const float *row = x + (size_t)(live_row ? m : 0) * K;
+    float v[NSL][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NSL; t++) {
+        const int q = lane + 64 * t, k0 = 8 * q;   // slot q's elements: 128 c + 16 u + 8 hh = 8 q
+        float4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
+        if (live_row && q < NQ && k0 < K) {
+            a = *(const float4 *)(row + k0);
+            b = *(const float4 *)(row + k0 + 4);
+        }
+        v[t][0] = a.x; v[t][1] = a.y; v[t][2] = a.z; v[t][3] = a.w;
+        v[t][4] = b.x; v[t][5] = b.y; v[t][6] = b.z; v[t][7] = b.w;
+#pragma unroll
+        for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[t][j]));
+    }
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    const float inv = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    const float sx = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 0.0f;
+    const bool live = live_row && inv > 0.0f;
+#pragma unroll
+    for (int t = 0; t < NSL; t++) {
+        const int q = lane + 64 * t;
+        if (q >= NQ) continue;
+        const int c = q >> 4, u = (q >> 1) & 7, hh = q & 1, k0 = 8 * q;
+        half8 h;
+#pragma unroll
+        for (int j = 0; j < 8; j++) h[j] = (_Float16)(float)((live && k0 + j < K) ? act_q8(v[t][j], inv) : 0);
+        *(half8 *)(xp + ((((size_t)G * Kc + c) * HSTEPS + u) * 64 + r + 32 * hh) * 16) = h;
+    }
+    for (int c = lane; c < Kc; c += 64) xpf[((size_t)G * Kc + c) * 32 + r] = sx;
+}
+
 // 4 waves per workgroup, one 32-column group each, WM row groups per wave.
 template <int QT, int WM>
 __global__ __launch_bounds__(256) void k_gemm_i8(DevW W, const uint8_t *__restrict__ qx,
@@ -2289,7 +2336,13 @@ hipError_t mh_launch_prep_a1(int kind, const float *x, int M, int K, int Kp, int
                              float *xpf, int want_xsum, hipStream_t st) {
     const bool vec = K % 8 == 0 && ((uintptr_t)x & 15) == 0;
     if (kind == MH_I8_ROW) {
-        if (vec)
+        if (vec && Kp <= 4096) {
+            const dim3 g(Mpad / 8);
+            if (Kp <= 512) hipLaunchKernelGGL(k_prep_a1_row1<1>, g, dim3(512), 0, st, x, M, K, Kp, Mpad, xp, xpf);
+            else if (Kp <= 1024) hipLaunchKernelGGL(k_prep_a1_row1<2>, g, dim3(512), 0, st, x, M, K, Kp, Mpad, xp, xpf);
+            else if (Kp <= 2048) hipLaunchKernelGGL(k_prep_a1_row1<4>, g, dim3(512), 0, st, x, M, K, Kp, Mpad, xp, xpf);
+            else hipLaunchKernelGGL(k_prep_a1_row1<8>, g, dim3(512), 0, st, x, M, K, Kp, Mpad, xp, xpf);
+        } else if (vec)
             hipLaunchKernelGGL(k_prep_a1_row<true>, dim3(Mpad / 32), dim3(PREP_I8_NW * 64), 0, st, x, M, K, Kp, xp, xpf);
         else
             hipLaunchKernelGGL(k_prep_a1_row<false>, dim3(Mpad / 32), dim3(PREP_I8_NW * 64), 0, st, x, M, K, Kp, xp, xpf);

@@ -79,10 +79,11 @@ def test_int8act_bit_exact(int8act, orc, qt, T):
         f"{int((y != ref).sum())} of {y.size} differ; max abs {np.abs(y - ref).max()}"
 
 
-@pytest.mark.parametrize("qt", [M.Q4_K, M.Q5_K, M.Q6_K], ids=lambda q: M.NAMES[q])
+@pytest.mark.parametrize("qt", [M.Q4_K, M.Q5_K, M.Q6_K, M.Q8_0, M.Q4_0], ids=lambda q: M.NAMES[q])
 def test_int8act_large_products_bit_exact(int8act, orc, qt):
     """The encoder's widest shapes (split-K and unsplit launches, three
-    workgroups per CU), sampled rows against the oracle."""
+    workgroups per CU; for Q8_0 / Q4_0 the one-pass row preparation at
+    K = 1024 and 4096), sampled rows against the oracle."""
     import torch
     say("int8act large", M.NAMES[qt])
     gpu = int8act
