@@ -154,12 +154,15 @@ def run_encoder_set(B, M_, qt, M, shapes, steps, warmup, seed0):
 
 
 def run_int8act(B, M_, M):
-    """INT8ACT numerics: the Q8_0 encoder set at M = 6000 (per-row int8
+    """INT8ACT numerics: the qmat INT8 encoder set at M = 6000 (the reference's
+    own int8 GEMM, qmat.c:464-500, 598-643: int8 MFMA, one int32 sum per
+    output), the Q8_0 encoder set at M = 6000 (per-row int8
     activations, qmat.c:186-202) and the Q4_K / Q5_K layer sets at config 4's
     M = 12000 (per-super-block int8 activations, ingot's int8 path,
-    third_party/ingot/src/kernels.c:719-750, 1649-1795). The products run on
-    the f16 MFMA with the int8 values as single exact terms; the fractions
-    are given against both the int8 (5.0 POP/s) and the f16 (2.5 PF) peak."""
+    third_party/ingot/src/kernels.c:719-750, 1649-1795). The block formats'
+    products run on the f16 MFMA with the int8 values as single exact terms;
+    the fractions are given against both the int8 (5.0 POP/s) and the f16
+    (2.5 PF) peak."""
     lib = B.lib
     out = {}
     lib.set_numerics(1)
@@ -533,6 +536,8 @@ def headline_summary(details: dict, rows: list) -> dict:
               and r.get("n") == 4096]
         if c1:
             s["config1_us_per_call"] = c1[0].get("call_us")
+    if "int8act_int8_m6000" in details:
+        s["int8_qmat_set_tops"] = details["int8act_int8_m6000"]["tops"]
     return s
 
 
