@@ -1836,17 +1836,23 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8t(DevW W, const uint8_t *__re
         load_a(st + 2, rn);
         __builtin_amdgcn_sched_barrier(0);   // (the loads go out before the step's MFMAs)
         const uint8_t *B = sbuf + (st & 1) * STB;
+        // kstep k + 1's activation fragments are read before kstep k's MFMAs
+        // (with one wave per SIMD nothing else hides the LDS latency)
+        i4v a[2][TR];
+#pragma unroll
+        for (int i = 0; i < TR; i++) a[0][i] = *(const i4v *)(B + (i * SK) * 1024 + lane * 16);
 #pragma unroll
         for (int k = 0; k < SK; k++) {
-            i4v a[TR];
+            if (k + 1 < SK) {
 #pragma unroll
-            for (int i = 0; i < TR; i++) a[i] = *(const i4v *)(B + (i * SK + k) * 1024 + lane * 16);
+                for (int i = 0; i < TR; i++) a[(k + 1) & 1][i] = *(const i4v *)(B + (i * SK + k + 1) * 1024 + lane * 16);
+            }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < TR; i++)
 #pragma unroll
-                for (int j = 0; j < CW; j++) {
-                    acc[i][j] = mfma_i8(a[i], b[j][k], acc[i][j]);
-                }
+                for (int j = 0; j < CW; j++) acc[i][j] = mfma_i8(a[k & 1][i], b[j][k], acc[i][j]);
+            __builtin_amdgcn_sched_barrier(0);
         }
         // slot (st + 1) & 1 was last read at step st - 1, before the barrier
         // that ended it
