@@ -227,6 +227,45 @@ int mynah_asr_hip_relpos_attention_dev(const float *q, const float *k, const flo
                                        const float *bias_u, const float *bias_v, float *ctx, int T, int d,
                                        int H, int left, int right, int nseq, void *stream);
 
+/* One FastConformer encoder layer on the device: the device twin of
+ * mynah_asr_encoder_layer (src/encoder.c:485-521) in its batched form
+ * encoder_layer_batch (:901-946). The fields follow mynah_asr_enc_layer
+ * (src/encoder.h:12-32): linears are resident weights (relk_w, the position
+ * projection, too: the reference keeps it f32, and an F32 weight here does
+ * the same), every other tensor is a device pointer of f32, and a NULL bias
+ * is absent. The conv norm is the folded batch norm (cnorm_scale,
+ * cnorm_shift) or, when cnorm_scale is NULL, a layer norm (cnorm_w, cnorm_b). */
+typedef struct {
+    const float *ln_ff1_w, *ln_ff1_b;
+    const mynah_asr_hip_weight *ff1_w1, *ff1_w2;
+    const float *ln_att_w, *ln_att_b;
+    const mynah_asr_hip_weight *q_w, *k_w, *v_w, *o_w, *relk_w;
+    const float *bias_u, *bias_v;
+    const float *ln_conv_w, *ln_conv_b;
+    const mynah_asr_hip_weight *pw1_w, *pw2_w;
+    const float *dw_w, *cnorm_w, *cnorm_b;
+    const float *ff1_b1, *ff1_b2, *ff2_b1, *ff2_b2;
+    const float *q_b, *k_b, *v_b, *o_b;
+    const float *pw1_b, *dw_b, *pw2_b;
+    const float *cnorm_scale, *cnorm_shift;
+    const float *ln_ff2_w, *ln_ff2_b;
+    const mynah_asr_hip_weight *ff2_w1, *ff2_w2;
+    const float *ln_out_w, *ln_out_b;
+} mynah_asr_hip_enc_layer;
+
+/* The layer in place on x: nseq segments of T frames packed back to back
+ * ([nseq * T, d], the reference's padding-free batch with equal lengths).
+ * The products and layer norms run over all rows; attention and the
+ * depthwise conv per segment. pe [2T-1, d]: the segments' relative positional
+ * embedding (mynah_asr_pos_emb). d: the model width, a multiple of 256 up to
+ * 4096; H heads of 64 or 128; conv_k the depthwise kernel (causal: left pad
+ * conv_k - 1, else (conv_k - 1) / 2 per side); left / right the attention
+ * context as mynah_asr_encoder_layer's (left < 0: full). Each product runs in
+ * the current numerics mode; -1 and the reason (mynah_asr_hip_last_error) on
+ * a bad argument or a failed launch. */
+int mynah_asr_hip_encoder_layer_dev(const mynah_asr_hip_enc_layer *L, float *x, int T, int nseq, const float *pe,
+                                    int d, int H, int conv_k, int causal, int left, int right, void *stream);
+
 /* AED (Canary) decoder on the device: src/decoder_aed.h:12-36 with every
  * linear a resident weight (mynah_asr_hip_weight_create) and every other tensor
  * a device pointer. Biases may not be NULL except proj_b. */

@@ -70,7 +70,7 @@ def _run(cmd: list[str]) -> list[str]:
 
 def build_hip() -> str:
     os.makedirs(LIB, exist_ok=True)
-    srcs = [os.path.join(CSRC, f) for f in ("kernels.hip", "attention.hip", "decoder.hip", "backend.cpp", "repack.cpp")]
+    srcs = [os.path.join(CSRC, f) for f in ("kernels.hip", "attention.hip", "decoder.hip", "encoder.hip", "backend.cpp", "repack.cpp")]
     objs = []
     # the units compile side by side (each hipcc runs one device pass)
     jobs = []

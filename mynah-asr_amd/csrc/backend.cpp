@@ -100,6 +100,7 @@ struct Ctx {
     DBuf x, y, h;
     DBuf att;    // the host-pointer attention call's q, k, v, rk, biases and ctx
     DBuf aed;    // the AED decoder's caches and vectors
+    DBuf enc;    // the encoder layer's activations
     DBuf gs;     // split-K GEMV workspace
     DBuf gk;     // split-K GEMM workspace (chunk results)
     int *pin = nullptr;   // pinned host int[2][2]: the step state of two positions read back
@@ -752,6 +753,131 @@ int gemm_noalloc(const mynah_asr_hip_weight *W, const float *dx, float *dy, int 
     return e == hipSuccess ? 0 : fail("launch failed", hipGetErrorString(e));
 }
 
+// ---------------------------------------------------------------- encoder layer
+// The steps of src/encoder.c:485-521 (encoder_layer; batched, :901-946) on
+// device buffers: every product through the same entry points the callers
+// use one by one (each in the current numerics mode), the rest through the
+// encoder.hip kernels.
+int enc_check(const mynah_asr_hip_enc_layer *L, int T, int nseq, int d, int H, int conv_k) {
+    if (!L || T < 0 || nseq < 0 || d <= 0 || H <= 0 || d % H != 0 || conv_k <= 0) return fail("bad argument");
+    if (!mh_enc_d_supported(d)) return fail("encoder layer: d must be a multiple of 256 up to 4096");
+    if (!mh_attn_supported(d / H)) return fail("head size must be 64 or 128");
+    const mynah_asr_hip_weight *sq[] = {L->q_w, L->k_w, L->v_w, L->o_w, L->relk_w, L->pw2_w};
+    for (const mynah_asr_hip_weight *w : sq)
+        if (!w || w->dw.n != d || w->dw.k != d) return fail("encoder layer: q/k/v/o/relk/pw2 must be [d, d]");
+    if (!L->pw1_w || L->pw1_w->dw.n != 2 * d || L->pw1_w->dw.k != d) return fail("encoder layer: pw1 must be [2d, d]");
+    const mynah_asr_hip_weight *ff[] = {L->ff1_w1, L->ff1_w2, L->ff2_w1, L->ff2_w2};
+    for (const mynah_asr_hip_weight *w : ff)
+        if (!w) return fail("encoder layer: missing FFN weight");
+    if (L->ff1_w1->dw.k != d || L->ff1_w2->dw.n != d || L->ff1_w2->dw.k != L->ff1_w1->dw.n ||
+        L->ff2_w1->dw.k != d || L->ff2_w2->dw.n != d || L->ff2_w2->dw.k != L->ff2_w1->dw.n)
+        return fail("encoder layer: FFN weights must be [f, d] and [d, f]");
+    const float *req[] = {L->ln_ff1_w, L->ln_ff1_b, L->ln_att_w, L->ln_att_b, L->bias_u, L->bias_v,
+                          L->ln_conv_w, L->ln_conv_b, L->dw_w, L->ln_ff2_w, L->ln_ff2_b, L->ln_out_w, L->ln_out_b};
+    for (const float *p : req)
+        if (!p) return fail("encoder layer: missing tensor");
+    if (L->cnorm_scale ? !L->cnorm_shift : (!L->cnorm_w || !L->cnorm_b))
+        return fail("encoder layer: the conv norm needs cnorm_scale and cnorm_shift, or cnorm_w and cnorm_b");
+    return 0;
+}
+
+int bias_add(float *y, const float *b, size_t rows, int n, hipStream_t st) {
+    if (!b) return 0;
+    hipError_t e = mh_launch_bias_rows(y, b, rows, n, st);
+    return e == hipSuccess ? 0 : fail("bias launch failed", hipGetErrorString(e));
+}
+
+// half_ffn (encoder.c:464-483) on xn: the fused FFN when both biases are
+// absent, else product, bias, SiLU, product, bias
+int enc_half_ffn(Ctx *c, const mynah_asr_hip_weight *w1, const mynah_asr_hip_weight *w2, const float *b1,
+                 const float *b2, const float *xn, float *out, float *h, int M, hipStream_t st) {
+    if (!b1 && !b2) return ffn_dev(c, w1, w2, xn, out, M, st);
+    const int f = w1->dw.n;
+    {
+        NumScope s1(eff_num(w1->qtype, w1->dw.k, M));
+        if (gemm_dev(c, w1, xn, h, M, 0, st)) return -1;
+    }
+    if (bias_add(h, b1, M, f, st)) return -1;
+    hipError_t e = mh_launch_silu(h, (size_t)M * f, st);
+    if (e != hipSuccess) return fail("silu launch failed", hipGetErrorString(e));
+    {
+        NumScope s2(eff_num(w2->qtype, w2->dw.k, M));
+        if (gemm_dev(c, w2, h, out, M, 0, st)) return -1;
+    }
+    return bias_add(out, b2, M, w2->dw.n, st);
+}
+
+int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T, int nseq, const float *pe, int d,
+                      int H, int conv_k, int causal, int left, int right, hipStream_t st) {
+    const int M = T * nseq, P = 2 * T - 1;
+    const int f = L->ff1_w1->dw.n > L->ff2_w1->dw.n ? L->ff1_w1->dw.n : L->ff2_w1->dw.n;
+    const bool biased_ffn = L->ff1_b1 || L->ff1_b2 || L->ff2_b1 || L->ff2_b2;
+    const size_t md = (size_t)M * d;
+    // xn, tmp, q, k, v, ctx [M, d]; h [M, 2d] (pw1, GLU); rk [P, d]; the FFN
+    // intermediate [M, f] only with FFN biases
+    const size_t need = 6 * md + 2 * md + (size_t)P * d + (biased_ffn ? (size_t)M * f : 0);
+    float *base = (float *)c->enc.get(need * sizeof(float));
+    if (!base) return fail("device buffer allocation failed");
+    float *xn = base, *tmp = xn + md, *q = tmp + md, *k = q + md, *v = k + md, *ctx = v + md, *h = ctx + md,
+          *rk = h + 2 * md, *hf = rk + (size_t)P * d;
+    hipError_t e;
+#define ENC_TRY(expr)                                                                   \
+    do {                                                                                \
+        e = (expr);                                                                     \
+        if (e != hipSuccess) return fail("encoder layer launch failed", hipGetErrorString(e)); \
+    } while (0)
+    // 1/2 FFN1 (:492-494)
+    ENC_TRY(mh_launch_add_ln(x, nullptr, 0.0f, L->ln_ff1_w, L->ln_ff1_b, xn, M, d, st));
+    if (enc_half_ffn(c, L->ff1_w1, L->ff1_w2, L->ff1_b1, L->ff1_b2, xn, tmp, hf, M, st)) return -1;
+    // x += 0.5 tmp; MHSA on LN(x) (:495-502)
+    ENC_TRY(mh_launch_add_ln(x, tmp, 0.5f, L->ln_att_w, L->ln_att_b, xn, M, d, st));
+    const mynah_asr_hip_weight *W3[3] = {L->q_w, L->k_w, L->v_w};
+    float *const y3[3] = {q, k, v};
+    if (qkv_dev(c, W3, xn, y3, M, st)) return -1;
+    if (bias_add(q, L->q_b, M, d, st) || bias_add(k, L->k_b, M, d, st) || bias_add(v, L->v_b, M, d, st)) return -1;
+    {
+        // rk = pe . relk^T (:336): the segments share T, so one product serves
+        // them all; in f32 arithmetic whatever the mode (relk_w stays f32 in
+        // the reference, encoder.h:17)
+        NumScope sp(MYNAH_ASR_HIP_EXACT);
+        if (gemm_dev(c, L->relk_w, pe, rk, P, 0, st)) return -1;
+    }
+    ENC_TRY(mh_launch_relpos_attn(q, k, v, rk, L->bias_u, L->bias_v, ctx, T, d, H, left, right, nseq, st));
+    {
+        NumScope so(eff_num(L->o_w->qtype, d, M));
+        if (gemm_dev(c, L->o_w, ctx, tmp, M, 0, st)) return -1;
+    }
+    if (bias_add(tmp, L->o_b, M, d, st)) return -1;
+    // x += tmp; conv module on LN(x) (:503-507, 413-462)
+    ENC_TRY(mh_launch_add_ln(x, tmp, 1.0f, L->ln_conv_w, L->ln_conv_b, xn, M, d, st));
+    {
+        NumScope s1(eff_num(L->pw1_w->qtype, d, M));
+        if (gemm_dev(c, L->pw1_w, xn, h, M, 0, st)) return -1;
+    }
+    if (bias_add(h, L->pw1_b, M, 2 * d, st)) return -1;
+    ENC_TRY(mh_launch_glu(h, q, M, d, st));   // g (q is free now)
+    if (L->cnorm_scale) {
+        ENC_TRY(mh_launch_dwconv(q, L->dw_w, L->dw_b, L->cnorm_scale, L->cnorm_shift, k, T, nseq, d, conv_k, causal,
+                                 st));
+    } else {
+        ENC_TRY(mh_launch_dwconv(q, L->dw_w, L->dw_b, nullptr, nullptr, v, T, nseq, d, conv_k, causal, st));
+        ENC_TRY(mh_launch_add_ln(v, nullptr, 0.0f, L->cnorm_w, L->cnorm_b, k, M, d, st));
+        ENC_TRY(mh_launch_silu(k, md, st));
+    }
+    {
+        NumScope s2(eff_num(L->pw2_w->qtype, d, M));
+        if (gemm_dev(c, L->pw2_w, k, tmp, M, 0, st)) return -1;
+    }
+    if (bias_add(tmp, L->pw2_b, M, d, st)) return -1;
+    // x += tmp; 1/2 FFN2 on LN(x) (:508-511)
+    ENC_TRY(mh_launch_add_ln(x, tmp, 1.0f, L->ln_ff2_w, L->ln_ff2_b, xn, M, d, st));
+    if (enc_half_ffn(c, L->ff2_w1, L->ff2_w2, L->ff2_b1, L->ff2_b2, xn, tmp, hf, M, st)) return -1;
+    // x += 0.5 tmp; x = LN_out(x) (:511-515)
+    ENC_TRY(mh_launch_add_ln(x, tmp, 0.5f, L->ln_out_w, L->ln_out_b, x, M, d, st));
+#undef ENC_TRY
+    return 0;
+}
+
 int begin(Ctx **c) {
     t_err[0] = 0;
     if (!mynah_asr_hip_available()) return fail("no gfx950 device");
@@ -957,6 +1083,23 @@ int mynah_asr_hip_relpos_attention(const float *q, const float *k, const float *
     if (mynah_asr_hip_relpos_attention_dev(dq, dk, dv, drk, dbu, dbv, dctx, T, d, H, left, right, 1, c->st))
         return -1;
     return d2h_sync(c, ctx, dctx, td);
+}
+
+int mynah_asr_hip_encoder_layer_dev(const mynah_asr_hip_enc_layer *L, float *x, int T, int nseq, const float *pe,
+                                    int d, int H, int conv_k, int causal, int left, int right, void *stream) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    note_capture(pick_stream(stream));
+    if (enc_check(L, T, nseq, d, H, conv_k)) return -1;
+    if (!x || !pe) return fail("bad argument");
+    if (left >= 0 && right < 0) return fail("chunked attention needs right >= 0");
+    if (((uintptr_t)x | (uintptr_t)pe) % 16) return fail("encoder layer buffers must be 16-byte aligned");
+    if (T == 0 || nseq == 0) return 0;
+    const mynah_asr_hip_weight *lin[] = {L->ff1_w1, L->ff1_w2, L->q_w, L->k_w, L->v_w, L->o_w,
+                                         L->pw1_w, L->pw2_w, L->ff2_w1, L->ff2_w2};
+    for (const mynah_asr_hip_weight *w : lin)
+        if (check_numerics_supported(w->qtype, w->dw.k, T * nseq)) return -1;
+    return encoder_layer_dev(c, L, x, T, nseq, pe, d, H, conv_k, causal, left, right, pick_stream(stream));
 }
 
 // The decoder entry points cannot run under a caller's graph capture: each

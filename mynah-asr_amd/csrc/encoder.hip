@@ -1,0 +1,176 @@
+// encoder.hip — the steps of one FastConformer encoder layer around its
+// products and its attention core (src/encoder.c:485-521 and the batched form
+// :901-946): the layer norms with the residual add that precedes each of
+// them, the GLU, and the depthwise convolution with its conv norm and SiLU
+// (conv_module, :413-462).
+//
+//   k_add_ln    x += alpha * res (when res), then out = LN(x) per row
+//               (layer_norm_f, :25-37; the adds of :495, 502, 507, 511)
+//   k_glu       g = a * sigmoid(b) over the two halves of each row  :426-432
+//   k_dwconv    depthwise conv over time within each segment (causal: left
+//               pad k-1; else 'same'), + dw_b, then the folded batch norm
+//               x * scale + shift and SiLU when scale is given     :434-459
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "launch.h"
+
+namespace {
+
+// the reference's stable sigmoid (src/qmat.h:31-35): exp only of -|x|
+__device__ __forceinline__ float sigmoid_f(float x) {
+    if (x >= 0.0f) return 1.0f / (1.0f + expf(-x));
+    const float e = expf(x);
+    return e / (1.0f + e);
+}
+
+// One wave per row of d = 256 V4 floats (lane l holds elements 4l + 256u ..
+// +3). Sums in double in two passes, as layer_norm_f: mean, then the sum of
+// (x - mean)^2; inv = (float)(1 / sqrt(var + 1e-5)); out = ((x - (float)mean)
+// * inv) * w + b in f32. out may be x.
+template <int V4>
+__global__ __launch_bounds__(256) void k_add_ln(float *x, const float *__restrict__ res, float alpha,
+                                                const float *__restrict__ w, const float *__restrict__ b,
+                                                float *out, int rows) {
+    constexpr int d = 256 * V4;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    float *xr = x + (size_t)r * d;
+    float4 v[V4], wv[V4], bv[V4];
+#pragma unroll
+    for (int u = 0; u < V4; u++) {
+        const int i = 4 * lane + 256 * u;
+        v[u] = *(const float4 *)(xr + i);
+        wv[u] = *(const float4 *)(w + i);
+        bv[u] = *(const float4 *)(b + i);
+    }
+    if (res) {
+        const float *rr = res + (size_t)r * d;
+#pragma unroll
+        for (int u = 0; u < V4; u++) {
+            const float4 a = *(const float4 *)(rr + 4 * lane + 256 * u);
+            v[u].x = fmaf(alpha, a.x, v[u].x);
+            v[u].y = fmaf(alpha, a.y, v[u].y);
+            v[u].z = fmaf(alpha, a.z, v[u].z);
+            v[u].w = fmaf(alpha, a.w, v[u].w);
+            *(float4 *)(xr + 4 * lane + 256 * u) = v[u];
+        }
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int u = 0; u < V4; u++) s += ((double)v[u].x + (double)v[u].y) + ((double)v[u].z + (double)v[u].w);
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    const double mu = s / d;
+    double q = 0.0;
+#pragma unroll
+    for (int u = 0; u < V4; u++) {
+        const double c0 = (double)v[u].x - mu, c1 = (double)v[u].y - mu;
+        const double c2 = (double)v[u].z - mu, c3 = (double)v[u].w - mu;
+        q += (c0 * c0 + c1 * c1) + (c2 * c2 + c3 * c3);
+    }
+    for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+    const float inv = (float)(1.0 / sqrt(q / d + 1e-5));
+    const float muf = (float)mu;
+    float *orow = out + (size_t)r * d;
+#pragma unroll
+    for (int u = 0; u < V4; u++) {
+        float4 o;
+        o.x = ((v[u].x - muf) * inv) * wv[u].x + bv[u].x;
+        o.y = ((v[u].y - muf) * inv) * wv[u].y + bv[u].y;
+        o.z = ((v[u].z - muf) * inv) * wv[u].z + bv[u].z;
+        o.w = ((v[u].w - muf) * inv) * wv[u].w + bv[u].w;
+        *(float4 *)(orow + 4 * lane + 256 * u) = o;
+    }
+}
+
+// g[r, i] = h[r, i] * sigmoid(h[r, d + i]); thread = 4 elements
+__global__ __launch_bounds__(256) void k_glu(const float *__restrict__ h, float *__restrict__ g, size_t rows,
+                                             int d) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x, d4 = d / 4;
+    if (idx >= rows * d4) return;
+    const size_t r = idx / d4, i = 4 * (idx - r * d4);
+    const float4 a = *(const float4 *)(h + r * 2 * d + i), b = *(const float4 *)(h + r * 2 * d + d + i);
+    const float4 o = {a.x * sigmoid_f(b.x), a.y * sigmoid_f(b.y), a.z * sigmoid_f(b.z), a.w * sigmoid_f(b.w)};
+    *(float4 *)(g + r * d + i) = o;
+}
+
+// x * sigmoid(x) with the stable sigmoid (mynah_asr_silu)
+__device__ __forceinline__ float silu_e(float x) { return x * sigmoid_f(x); }
+
+// c[t, i] = dw_b[i] + sum_j w[i, j] * g[t - pc + j, i] over the taps inside
+// the segment (in tap order from j0), then, with scale: silu(c * scale +
+// shift). Thread = (row, 4 channels).
+__global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ g, const float *__restrict__ w,
+                                                const float *__restrict__ bias, const float *__restrict__ scale,
+                                                const float *__restrict__ shift, float *__restrict__ out, int T,
+                                                int nseq, int d, int k, int pc) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const int d4 = d / 4;
+    if (idx >= (size_t)nseq * T * d4) return;
+    const int row = (int)(idx / d4), i = 4 * (int)(idx - (size_t)row * d4);
+    const int s = row / T, t = row - s * T;
+    const float *gs = g + (size_t)s * T * d;
+    float4 o = bias ? *(const float4 *)(bias + i) : float4{0.f, 0.f, 0.f, 0.f};
+    const int j0 = t - pc < 0 ? pc - t : 0, j1 = t - pc + k > T ? T - t + pc : k;
+    for (int j = j0; j < j1; j++) {
+        const float4 src = *(const float4 *)(gs + (size_t)(t - pc + j) * d + i);
+        o.x = fmaf(w[(size_t)(i + 0) * k + j], src.x, o.x);
+        o.y = fmaf(w[(size_t)(i + 1) * k + j], src.y, o.y);
+        o.z = fmaf(w[(size_t)(i + 2) * k + j], src.z, o.z);
+        o.w = fmaf(w[(size_t)(i + 3) * k + j], src.w, o.w);
+    }
+    if (scale) {
+        const float4 sc = *(const float4 *)(scale + i), sh = *(const float4 *)(shift + i);
+        o.x = silu_e(fmaf(o.x, sc.x, sh.x));
+        o.y = silu_e(fmaf(o.y, sc.y, sh.y));
+        o.z = silu_e(fmaf(o.z, sc.z, sh.z));
+        o.w = silu_e(fmaf(o.w, sc.w, sh.w));
+    }
+    *(float4 *)(out + (size_t)row * d + i) = o;
+}
+
+}  // namespace
+
+bool mh_enc_d_supported(int d) { return d > 0 && d % 256 == 0 && d <= 4096; }
+
+hipError_t mh_launch_add_ln(float *x, const float *res, float alpha, const float *w, const float *b, float *out,
+                            int rows, int d, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (!mh_enc_d_supported(d)) return hipErrorInvalidValue;
+    const dim3 grid((rows + 3) / 4), blk(256);
+    switch (d / 256) {
+    case 1: hipLaunchKernelGGL(k_add_ln<1>, grid, blk, 0, st, x, res, alpha, w, b, out, rows); break;
+    case 2: hipLaunchKernelGGL(k_add_ln<2>, grid, blk, 0, st, x, res, alpha, w, b, out, rows); break;
+    case 3: hipLaunchKernelGGL(k_add_ln<3>, grid, blk, 0, st, x, res, alpha, w, b, out, rows); break;
+    case 4: hipLaunchKernelGGL(k_add_ln<4>, grid, blk, 0, st, x, res, alpha, w, b, out, rows); break;
+    case 5: hipLaunchKernelGGL(k_add_ln<5>, grid, blk, 0, st, x, res, alpha, w, b, out, rows); break;
+    case 6: hipLaunchKernelGGL(k_add_ln<6>, grid, blk, 0, st, x, res, alpha, w, b, out, rows); break;
+    case 7: hipLaunchKernelGGL(k_add_ln<7>, grid, blk, 0, st, x, res, alpha, w, b, out, rows); break;
+    case 8: hipLaunchKernelGGL(k_add_ln<8>, grid, blk, 0, st, x, res, alpha, w, b, out, rows); break;
+    case 12: hipLaunchKernelGGL(k_add_ln<12>, grid, blk, 0, st, x, res, alpha, w, b, out, rows); break;
+    case 16: hipLaunchKernelGGL(k_add_ln<16>, grid, blk, 0, st, x, res, alpha, w, b, out, rows); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t mh_launch_glu(const float *h, float *g, size_t rows, int d, hipStream_t st) {
+    if (!rows) return hipSuccess;
+    if (d % 4) return hipErrorInvalidValue;
+    const size_t n = rows * (size_t)(d / 4);
+    hipLaunchKernelGGL(k_glu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, h, g, rows, d);
+    return hipGetLastError();
+}
+
+hipError_t mh_launch_dwconv(const float *g, const float *w, const float *bias, const float *scale,
+                            const float *shift, float *out, int T, int nseq, int d, int k, int causal,
+                            hipStream_t st) {
+    if (T <= 0 || nseq <= 0) return hipSuccess;
+    if (d % 4 || k <= 0) return hipErrorInvalidValue;
+    const int pc = causal ? k - 1 : (k - 1) / 2;
+    const size_t n = (size_t)nseq * T * (d / 4);
+    hipLaunchKernelGGL(k_dwconv, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, w, bias, scale, shift, out,
+                       T, nseq, d, k, pc);
+    return hipGetLastError();
+}

@@ -113,6 +113,22 @@ hipError_t mh_launch_relpos_attn(const float *q, const float *k, const float *v,
                                  const float *bias_u, const float *bias_v, float *ctx, int T, int d, int H,
                                  int left, int right, int nseq, hipStream_t st);
 
+// Encoder layer steps around the products (encoder.hip). d: a multiple of
+// 256 up to 4096 for the layer norm (mh_enc_d_supported), of 4 for the rest.
+bool mh_enc_d_supported(int d);
+// x += alpha * res (res may be null: no add), then out = LN(x) (w, b) per row;
+// out may be x
+hipError_t mh_launch_add_ln(float *x, const float *res, float alpha, const float *w, const float *b, float *out,
+                            int rows, int d, hipStream_t st);
+// g [rows, d] = h[:, :d] * sigmoid(h[:, d:]) for h [rows, 2d]
+hipError_t mh_launch_glu(const float *h, float *g, size_t rows, int d, hipStream_t st);
+// depthwise conv over time in each of nseq segments of T rows (w [d, k];
+// causal: left pad k - 1, else (k - 1) / 2 per side), + bias (or null); with
+// scale: silu(c * scale + shift)
+hipError_t mh_launch_dwconv(const float *g, const float *w, const float *bias, const float *scale,
+                            const float *shift, float *out, int T, int nseq, int d, int k, int causal,
+                            hipStream_t st);
+
 // AED decoder step kernels (decoder.hip); st = device int[2]: position p, last argmax
 int mh_att_splits(int n);   // attention splits for n keys
 hipError_t mh_launch_embed_ln(const float *emb, const float *pos, const int *prompt, int n_prompt, const int *st,

@@ -40,6 +40,7 @@ HIP_SYMBOLS = [
     "mynah_asr_hip_relpos_attention_dev", "mynah_asr_hip_relpos_attention",
     "mynah_asr_hip_aed_decode_dev", "mynah_asr_hip_aed_forced_dev",
     "mynah_asr_hip_qgemm_noalloc_dev", "mynah_asr_hip_noalloc_bytes", "mynah_asr_hip_read_floor_dev",
+    "mynah_asr_hip_encoder_layer_dev",
 ]
 HOST_SYMBOLS = [
     "mynah_asr_set_backend", "mynah_asr_backend", "mynah_asr_gemm_wt", "mynah_asr_silu",
@@ -69,6 +70,15 @@ class AedC(C.Structure):
                 ("vocab", C.c_int), ("max_seq", C.c_int)] + \
                [(f, C.c_void_p) for f in ("proj", "proj_b", "emb", "pos", "embln_w", "embln_b", "fin_w", "fin_b",
                                           "head", "head_b")] + [("layers", C.POINTER(AedLayerC))]
+
+
+class EncLayerC(C.Structure):
+    """mynah_asr_hip_enc_layer (include/mynah_asr_hip.h; src/encoder.h:12-32)."""
+    FIELDS = ("ln_ff1_w", "ln_ff1_b", "ff1_w1", "ff1_w2", "ln_att_w", "ln_att_b", "q_w", "k_w", "v_w", "o_w",
+              "relk_w", "bias_u", "bias_v", "ln_conv_w", "ln_conv_b", "pw1_w", "pw2_w", "dw_w", "cnorm_w", "cnorm_b",
+              "ff1_b1", "ff1_b2", "ff2_b1", "ff2_b2", "q_b", "k_b", "v_b", "o_b", "pw1_b", "dw_b", "pw2_b",
+              "cnorm_scale", "cnorm_shift", "ln_ff2_w", "ln_ff2_b", "ff2_w1", "ff2_w2", "ln_out_w", "ln_out_b")
+    _fields_ = [(f, C.c_void_p) for f in FIELDS]
 
 
 class WDesc(C.Structure):
@@ -135,6 +145,9 @@ class HipLib:
         if hasattr(L, "mynah_asr_hip_relpos_attention_dev"):
             L.mynah_asr_hip_relpos_attention_dev.argtypes = [_P] * 7 + [C.c_int] * 6 + [_P]
             L.mynah_asr_hip_relpos_attention.argtypes = [_P] * 7 + [C.c_int] * 5
+        if hasattr(L, "mynah_asr_hip_encoder_layer_dev"):
+            L.mynah_asr_hip_encoder_layer_dev.argtypes = [C.POINTER(EncLayerC), _P, C.c_int, C.c_int, _P] + \
+                [C.c_int] * 6 + [_P]
         if hasattr(L, "mynah_asr_hip_aed_decode_dev"):
             L.mynah_asr_hip_aed_decode_dev.argtypes = [C.POINTER(AedC), _P, C.c_int, _P, C.c_int, C.c_int, _P,
                                                        C.c_int, _P]
@@ -438,6 +451,52 @@ class DeviceAed:
         if n < 0:
             raise RuntimeError(f"aed_decode_dev failed: {self.lib.last_error()}")
         return [int(t) for t in toks[:n]]
+
+    def close(self):
+        for k in self._keep:
+            if isinstance(k, DeviceWeight):
+                k.close()
+        self._keep = []
+
+
+class DeviceEncoderLayer:
+    """One FastConformer encoder layer on the device. `params` holds the
+    reference's tensors by their mynah_asr_enc_layer names (src/encoder.h:
+    12-32) as f32 arrays ([n, k] weights; absent biases omitted or None).
+    The linears are quantized to `qtype` by the library's quantizers and made
+    resident, relk_w as an F32 weight (the reference keeps it f32); the rest
+    are copied to device tensors. `weights` keeps the host blocks, for the
+    oracle's dequantization."""
+
+    LINEARS = ("ff1_w1", "ff1_w2", "q_w", "k_w", "v_w", "o_w", "relk_w", "pw1_w", "pw2_w", "ff2_w1", "ff2_w2")
+
+    def __init__(self, lib: "HipLib", params: dict, qtype: int):
+        import torch
+        self.lib, self.torch = lib, torch
+        self._keep, self.weights = [], {}
+        self.c = EncLayerC()
+        for f in EncLayerC.FIELDS:
+            a = params.get(f)
+            if a is None:
+                continue
+            if f in self.LINEARS:
+                hw = Weight.make(lib, F32 if f == "relk_w" else qtype, np.asarray(a, np.float32))
+                dw = DeviceWeight(lib, hw)
+                self.weights[f] = hw
+                self._keep.append(dw)
+                setattr(self.c, f, dw.h)
+            else:
+                t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+                self._keep.append(t)
+                setattr(self.c, f, t.data_ptr())
+        torch.cuda.synchronize()
+
+    def run(self, x_ptr: int, T: int, nseq: int, pe_ptr: int, d: int, H: int, conv_k: int, causal: int,
+            left: int = -1, right: int = 0, stream: int = 0) -> None:
+        """mynah_asr_hip_encoder_layer_dev on x [nseq * T, d] in place."""
+        rc = self.lib.L.mynah_asr_hip_encoder_layer_dev(C.byref(self.c), x_ptr, T, nseq, pe_ptr, d, H, conv_k, causal,
+                                                        left, right, stream or None)
+        self.lib._check(rc, "encoder_layer_dev")
 
     def close(self):
         for k in self._keep:

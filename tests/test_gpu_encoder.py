@@ -1,0 +1,144 @@
+"""The device encoder layer (mynah_asr_hip_encoder_layer_dev) against the
+float64 restatement of src/encoder.c:485-521 (oracle/encoder.py), over the
+dequantized values of the weights it runs with, and its segments' rows
+bit-identical to each segment run alone (encoder.c:876-878: the batched
+form is bit-identical to the serial loop).
+
+Bar: |y - ref| <= 2e-6 * (1 + |ref|) per element (the layer ends in a layer
+norm, so its outputs are O(1)): the measured worst over these cases is
+3.1e-7 (Q8_0 and Q4_K weights, biases or none, folded batch norm or layer
+norm, causal or 'same' conv, full or chunked attention). Each case prints
+its own."""
+import sys
+
+import numpy as np
+import pytest
+
+import encoder as E
+import mynah_hip as M
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def make_params(seed, d, f, k, biases, bn):
+    r = np.random.default_rng(seed)
+    g = lambda *s: r.standard_normal(s).astype(np.float32)
+    p = {}
+    for n in ("ff1", "ff2", "att", "conv", "out"):
+        p[f"ln_{n}_w"], p[f"ln_{n}_b"] = 1 + 0.1 * g(d), 0.1 * g(d)
+    for n in ("ff1", "ff2"):
+        p[f"{n}_w1"], p[f"{n}_w2"] = 0.02 * g(f, d), 0.02 * g(d, f)
+        if biases:
+            p[f"{n}_b1"], p[f"{n}_b2"] = 0.1 * g(f), 0.1 * g(d)
+    for n in ("q", "k", "v", "o", "relk"):
+        p[f"{n}_w"] = 0.02 * g(d, d)
+        if biases and n != "relk":
+            p[f"{n}_b"] = 0.1 * g(d)
+    p["bias_u"], p["bias_v"] = 0.1 * g(d), 0.1 * g(d)
+    p["pw1_w"], p["pw2_w"], p["dw_w"] = 0.02 * g(2 * d, d), 0.02 * g(d, d), 0.3 * g(d, k)
+    if biases:
+        p["pw1_b"], p["dw_b"], p["pw2_b"] = 0.1 * g(2 * d), 0.1 * g(d), 0.1 * g(d)
+    if bn:
+        p["cnorm_scale"], p["cnorm_shift"] = 1 + 0.1 * g(d), 0.1 * g(d)
+    else:
+        p["cnorm_w"], p["cnorm_b"] = 1 + 0.1 * g(d), 0.1 * g(d)
+    return p
+
+
+def oracle_params(orc, dev, p, qt):
+    """The float64 values the device products use: quantized linears
+    dequantized by the oracle, relk_w as given (F32)."""
+    q = {}
+    for f, a in p.items():
+        if f in M.DeviceEncoderLayer.LINEARS and f != "relk_w":
+            w = dev.weights[f]
+            oq = {M.Q8_0: O.Q8_0, M.Q4_K: O.Q4_K}[qt]
+            q[f] = orc.dequant(oq, w.data, w.n * w.k).reshape(w.n, w.k).astype(np.float64)
+        else:
+            q[f] = np.asarray(a, np.float64)
+    return q
+
+
+CASES = [
+    # d, H, f, k, T, nseq, causal, biases, bn, left, right, qt
+    (256, 4, 512, 9, 37, 3, 0, False, True, -1, 0, M.Q8_0),
+    (256, 4, 512, 9, 29, 2, 1, True, False, -1, 0, M.Q8_0),
+    (256, 2, 768, 5, 41, 2, 0, True, True, 12, 3, M.Q4_K),
+    (1024, 8, 4096, 9, 120, 2, 0, False, True, -1, 0, M.Q8_0),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"d{c[0]}-T{c[4]}x{c[5]}-{'causal' if c[6] else 'same'}"
+                                             f"-{'bias' if c[7] else 'nobias'}-{'bn' if c[8] else 'ln'}"
+                                             f"-L{c[9]}" for c in CASES])
+def test_encoder_layer_matches_oracle(gpu, orc, case):
+    import torch
+    d, H, f, k, T, nseq, causal, biases, bn, left, right, qt = case
+    say("encoder layer", case)
+    p = make_params(7, d, f, k, biases, bn)
+    dev = M.DeviceEncoderLayer(gpu, p, qt)
+    try:
+        x = np.random.default_rng(8).standard_normal((nseq * T, d)).astype(np.float32)
+        pe = E.pos_emb(T, d).astype(np.float32)
+        xd, ped = torch.from_numpy(x).cuda(), torch.from_numpy(pe).cuda()
+        dev.run(xd.data_ptr(), T, nseq, ped.data_ptr(), d, H, k, causal, left, right)
+        torch.cuda.synchronize()
+        y = xd.cpu().numpy()
+        ref = E.encoder_layer(x, oracle_params(orc, dev, p, qt), T, nseq, pe, H, k, causal, left, right)
+        err = np.abs(y - ref)
+        say(f"  max |y - ref| {err.max():.3g}, max err / (1 + |ref|) {(err / (1 + np.abs(ref))).max():.3g}")
+        assert np.isfinite(y).all()
+        assert (err <= 2e-6 * (1 + np.abs(ref))).all()
+    finally:
+        dev.close()
+
+
+def test_encoder_layer_segments_are_independent(gpu):
+    """Three segments packed: each segment's rows carry the bits of that
+    segment run alone (products are row-stable; layer norms are per row;
+    attention and the depthwise conv are per segment)."""
+    import torch
+    say("encoder layer segments")
+    d, H, f, k, T = 256, 4, 512, 9, 33
+    p = make_params(9, d, f, k, True, True)
+    dev = M.DeviceEncoderLayer(gpu, p, M.Q8_0)
+    try:
+        x = np.random.default_rng(10).standard_normal((3 * T, d)).astype(np.float32)
+        ped = torch.from_numpy(E.pos_emb(T, d).astype(np.float32)).cuda()
+        xa = torch.from_numpy(x).cuda()
+        dev.run(xa.data_ptr(), T, 3, ped.data_ptr(), d, H, k, 0)
+        for s in range(3):
+            xs = torch.from_numpy(x[s * T:(s + 1) * T].copy()).cuda()
+            dev.run(xs.data_ptr(), T, 1, ped.data_ptr(), d, H, k, 0)
+            torch.cuda.synchronize()
+            assert torch.equal(xs.view(torch.int32), xa[s * T:(s + 1) * T].view(torch.int32)), s
+    finally:
+        dev.close()
+
+
+def test_encoder_layer_refuses_bad_shapes(gpu):
+    import torch
+    say("encoder layer refusals")
+    d, H, f, k, T = 256, 4, 512, 9, 8
+    p = make_params(11, d, f, k, False, True)
+    dev = M.DeviceEncoderLayer(gpu, p, M.Q8_0)
+    try:
+        x = torch.zeros((T, d), dtype=torch.float32, device="cuda")
+        pe = torch.zeros((2 * T - 1, d), dtype=torch.float32, device="cuda")
+        with pytest.raises(RuntimeError, match="head size"):
+            dev.run(x.data_ptr(), T, 1, pe.data_ptr(), d, 1, k, 0)      # dk = 256
+        with pytest.raises(RuntimeError, match="q/k/v/o"):
+            dev.run(x.data_ptr(), T, 1, pe.data_ptr(), 512, 8, k, 0)    # weights are [256, 256]
+        c = dev.c
+        saved, c.cnorm_shift = c.cnorm_shift, None
+        with pytest.raises(RuntimeError, match="conv norm"):
+            dev.run(x.data_ptr(), T, 1, pe.data_ptr(), d, H, k, 0)
+        c.cnorm_shift = saved
+    finally:
+        dev.close()
