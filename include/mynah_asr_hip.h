@@ -266,6 +266,30 @@ typedef struct {
 int mynah_asr_hip_encoder_layer_dev(const mynah_asr_hip_enc_layer *L, float *x, int T, int nseq, const float *pe,
                                     int d, int H, int conv_k, int causal, int left, int right, void *stream);
 
+/* The dw_striding 8x subsampling on the device (the device twin of
+ * mynah_asr_subsampling_forward, src/subsampling.c:208-268; tensors of
+ * mynah_asr_subsampling, src/subsampling.h:12-21): the 3x3 stride-2 conv
+ * 1 -> C channels + ReLU, twice (depthwise 3x3 stride 2, pointwise 1x1, ReLU),
+ * the channel-major flatten and the linear to d_model. The pointwise convs and
+ * the linear are resident weights (f32 arithmetic: the reference multiplies
+ * them in f32); the rest are device pointers. */
+typedef struct {
+    const float *conv_in_w, *conv_in_b;      /* [C, 1, 3, 3], [C] */
+    const float *dw_w[2], *dw_b[2];          /* [C, 1, 3, 3], [C] */
+    const mynah_asr_hip_weight *pw_w[2];     /* [C, C] */
+    const float *pw_b[2];                    /* [C] */
+    const mynah_asr_hip_weight *lin_w;       /* [d_model, C * F'], F' the features after three stages */
+    const float *lin_b;                      /* [d_model] */
+    int channels, d_model, causal;           /* causal: pads (2, 1), else (1, 1) */
+} mynah_asr_hip_subsampling;
+
+/* feats: nseq segments of T frames of n_mels features ([nseq * T, n_mels],
+ * equal lengths) -> out [nseq * T', d_model], each row times xscale (the
+ * encoder's layer input scale, encoder.c:958-959; 1 for none). *t_out = T'.
+ * C a multiple of 4; 16-byte aligned buffers. */
+int mynah_asr_hip_subsampling_dev(const mynah_asr_hip_subsampling *ss, const float *feats, int T, int nseq,
+                                  int n_mels, float xscale, float *out, int *t_out, void *stream);
+
 /* AED (Canary) decoder on the device: src/decoder_aed.h:12-36 with every
  * linear a resident weight (mynah_asr_hip_weight_create) and every other tensor
  * a device pointer. Biases may not be NULL except proj_b. */

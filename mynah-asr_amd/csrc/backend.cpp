@@ -101,6 +101,7 @@ struct Ctx {
     DBuf att;    // the host-pointer attention call's q, k, v, rk, biases and ctx
     DBuf aed;    // the AED decoder's caches and vectors
     DBuf enc;    // the encoder layer's activations
+    DBuf ssb;    // the subsampling's activations
     DBuf gs;     // split-K GEMV workspace
     DBuf gk;     // split-K GEMM workspace (chunk results)
     int *pin = nullptr;   // pinned host int[2][2]: the step state of two positions read back
@@ -878,6 +879,42 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
     return 0;
 }
 
+// mynah_asr_subsampling_forward (src/subsampling.c:208-268) on device
+// buffers, activations channel-last; every product in f32 arithmetic.
+int subsampling_dev(Ctx *c, const mynah_asr_hip_subsampling *ss, const float *feats, int T, int nseq, int F,
+                    float xscale, float *out, int *t_out, hipStream_t st) {
+    const int C = ss->channels, cz = ss->causal;
+    const int T1 = mh_ss_out_len(T, cz), F1 = mh_ss_out_len(F, cz);
+    const int T2 = mh_ss_out_len(T1, cz), F2 = mh_ss_out_len(F1, cz);
+    const int T3 = mh_ss_out_len(T2, cz), F3 = mh_ss_out_len(F2, cz);
+    *t_out = T3;
+    if (T3 <= 0 || F3 <= 0) return fail("subsampling: input too short for three stride-2 stages");
+    if (ss->lin_w->dw.k != C * F3) return fail("subsampling: lin_w must be [d_model, channels * F']");
+    // A holds the stage-0 output, then the pointwise outputs; B the depthwise
+    // outputs, then the flattened rows
+    const size_t a = (size_t)nseq * T1 * F1 * C, b = (size_t)nseq * T2 * F2 * C;
+    float *A = (float *)c->ssb.get((a + b) * sizeof(float));
+    if (!A) return fail("device buffer allocation failed");
+    float *B = A + a;
+    hipError_t e;
+#define SS_TRY(expr)                                                                 \
+    do {                                                                             \
+        e = (expr);                                                                  \
+        if (e != hipSuccess) return fail("subsampling launch failed", hipGetErrorString(e)); \
+    } while (0)
+    NumScope sc(MYNAH_ASR_HIP_EXACT);
+    SS_TRY(mh_launch_conv_in(feats, ss->conv_in_w, ss->conv_in_b, A, nseq, T, F, C, cz, st));
+    SS_TRY(mh_launch_dw_s2(A, nullptr, ss->dw_w[0], ss->dw_b[0], B, nseq, T1, F1, C, cz, st));
+    if (gemm_dev(c, ss->pw_w[0], B, A, nseq * T2 * F2, 0, st)) return -1;
+    SS_TRY(mh_launch_dw_s2(A, ss->pw_b[0], ss->dw_w[1], ss->dw_b[1], B, nseq, T2, F2, C, cz, st));
+    if (gemm_dev(c, ss->pw_w[1], B, A, nseq * T3 * F3, 0, st)) return -1;
+    SS_TRY(mh_launch_flatten(A, ss->pw_b[1], B, (size_t)nseq * T3, F3, C, st));
+    if (gemm_dev(c, ss->lin_w, B, out, nseq * T3, 0, st)) return -1;
+    SS_TRY(mh_launch_bias_scale(out, ss->lin_b, (size_t)nseq * T3, ss->d_model, xscale, st));
+#undef SS_TRY
+    return 0;
+}
+
 int begin(Ctx **c) {
     t_err[0] = 0;
     if (!mynah_asr_hip_available()) return fail("no gfx950 device");
@@ -1100,6 +1137,28 @@ int mynah_asr_hip_encoder_layer_dev(const mynah_asr_hip_enc_layer *L, float *x, 
     for (const mynah_asr_hip_weight *w : lin)
         if (check_numerics_supported(w->qtype, w->dw.k, T * nseq)) return -1;
     return encoder_layer_dev(c, L, x, T, nseq, pe, d, H, conv_k, causal, left, right, pick_stream(stream));
+}
+
+int mynah_asr_hip_subsampling_dev(const mynah_asr_hip_subsampling *ss, const float *feats, int T, int nseq,
+                                  int n_mels, float xscale, float *out, int *t_out, void *stream) {
+    Ctx *c;
+    if (begin(&c)) return -1;
+    note_capture(pick_stream(stream));
+    if (!ss || !feats || !out || !t_out || T < 0 || nseq < 0 || n_mels <= 0) return fail("bad argument");
+    const int C = ss->channels;
+    if (C <= 0 || C % 4 || ss->d_model <= 0) return fail("subsampling: channels must be a multiple of 4");
+    if (!ss->conv_in_w || !ss->conv_in_b || !ss->lin_w || !ss->lin_b) return fail("subsampling: missing tensor");
+    for (int i = 0; i < 2; i++)
+        if (!ss->dw_w[i] || !ss->dw_b[i] || !ss->pw_w[i] || !ss->pw_b[i]) return fail("subsampling: missing tensor");
+    for (int i = 0; i < 2; i++)
+        if (ss->pw_w[i]->dw.n != C || ss->pw_w[i]->dw.k != C) return fail("subsampling: pw_w must be [C, C]");
+    if (ss->lin_w->dw.n != ss->d_model) return fail("subsampling: lin_w must be [d_model, channels * F']");
+    if (((uintptr_t)feats | (uintptr_t)out) % 16) return fail("subsampling buffers must be 16-byte aligned");
+    if (T == 0 || nseq == 0) {
+        *t_out = 0;
+        return 0;
+    }
+    return subsampling_dev(c, ss, feats, T, nseq, n_mels, xscale, out, t_out, pick_stream(stream));
 }
 
 // The decoder entry points cannot run under a caller's graph capture: each

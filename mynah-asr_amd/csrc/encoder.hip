@@ -10,6 +10,17 @@
 //   k_dwconv    depthwise conv over time within each segment (causal: left
 //               pad k-1; else 'same'), + dw_b, then the folded batch norm
 //               x * scale + shift and SiLU when scale is given     :434-459
+//
+// and of the dw_striding subsampling in front of the layers
+// (src/subsampling.c:208-268, 109-200), with activations channel-last,
+// [segment][time][freq][channel], so that its pointwise convolutions and its
+// final linear are this unit's products:
+//   k_conv_in   the full 3x3 stride-2 conv of the mel features, 1 -> C
+//               channels, + bias, ReLU                            :222-226
+//   k_dw_s2     the depthwise 3x3 stride-2 conv, + bias; its input may take
+//               the previous pointwise conv's bias and ReLU on load  :231-244
+//   k_flatten   the last pointwise conv's bias and ReLU, then the
+//               channel-major flatten [t][c * F' + f] of :249-257
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -130,6 +141,108 @@ __global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ g, con
     *(float4 *)(out + (size_t)row * d + i) = o;
 }
 
+// out[s][to][fo][c] = relu(b[c] + sum_{dt, df} w[c][3 dt + df] x[s][2 to - pl + dt][2 fo - pl + df])
+// with zeros outside [0, T) x [0, F). Thread = (row (s, to, fo), 4 channels).
+__global__ __launch_bounds__(256) void k_conv_in(const float *__restrict__ x, const float *__restrict__ w,
+                                                 const float *__restrict__ b, float *__restrict__ out, int nseq,
+                                                 int T, int F, int To, int Fo, int C, int pl) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const int C4 = C / 4;
+    if (idx >= (size_t)nseq * To * Fo * C4) return;
+    const size_t row = idx / C4;
+    const int c = 4 * (int)(idx - row * C4);
+    const int fo = (int)(row % Fo), to = (int)((row / Fo) % To), s = (int)(row / ((size_t)Fo * To));
+    const float *xs = x + (size_t)s * T * F;
+    float v[9];
+#pragma unroll
+    for (int dt = 0; dt < 3; dt++)
+#pragma unroll
+        for (int df = 0; df < 3; df++) {
+            const int t = 2 * to - pl + dt, f = 2 * fo - pl + df;
+            v[3 * dt + df] = t >= 0 && t < T && f >= 0 && f < F ? xs[(size_t)t * F + f] : 0.0f;
+        }
+    float o[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float *wc = w + (size_t)(c + q) * 9;
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 9; j++) acc = fmaf(wc[j], v[j], acc);
+        const float r = acc + b[c + q];
+        o[q] = r < 0.0f ? 0.0f : r;
+    }
+    *(float4 *)(out + row * C + c) = float4{o[0], o[1], o[2], o[3]};
+}
+
+// out[s][to][fo][c] = b[c] + sum w[c][3 dt + df] in[s][2 to - pl + dt][2 fo - pl + df][c],
+// in the reference's term order (the nine products summed left to right,
+// subsampling.c:96-98); with pb, each input value is relu(in + pb[c]) first.
+__global__ __launch_bounds__(256) void k_dw_s2(const float *__restrict__ in, const float *__restrict__ pb,
+                                               const float *__restrict__ w, const float *__restrict__ b,
+                                               float *__restrict__ out, int nseq, int T, int F, int To, int Fo,
+                                               int C, int pl) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const int C4 = C / 4;
+    if (idx >= (size_t)nseq * To * Fo * C4) return;
+    const size_t row = idx / C4;
+    const int c = 4 * (int)(idx - row * C4);
+    const int fo = (int)(row % Fo), to = (int)((row / Fo) % To), s = (int)(row / ((size_t)Fo * To));
+    const float *is = in + (size_t)s * T * F * C;
+    const float4 pbv = pb ? *(const float4 *)(pb + c) : float4{0.f, 0.f, 0.f, 0.f};
+    float4 v[9];
+#pragma unroll
+    for (int dt = 0; dt < 3; dt++)
+#pragma unroll
+        for (int df = 0; df < 3; df++) {
+            const int t = 2 * to - pl + dt, f = 2 * fo - pl + df;
+            float4 a = {0.f, 0.f, 0.f, 0.f};
+            if (t >= 0 && t < T && f >= 0 && f < F) {
+                a = *(const float4 *)(is + ((size_t)t * F + f) * C + c);
+                if (pb) {
+                    a.x = fmaxf(a.x + pbv.x, 0.0f);
+                    a.y = fmaxf(a.y + pbv.y, 0.0f);
+                    a.z = fmaxf(a.z + pbv.z, 0.0f);
+                    a.w = fmaxf(a.w + pbv.w, 0.0f);
+                }
+            }
+            v[3 * dt + df] = a;
+        }
+    float o[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float *wc = w + (size_t)(c + q) * 9;
+        float acc = wc[0] * v[0][q];
+#pragma unroll
+        for (int j = 1; j < 9; j++) acc = fmaf(wc[j], v[j][q], acc);
+        o[q] = b[c + q] + acc;
+    }
+    *(float4 *)(out + row * C + c) = float4{o[0], o[1], o[2], o[3]};
+}
+
+// flat[s * To + t][c * Fo + f] = relu(in[s][t][f][c] + pb[c]); thread = one
+// output element, consecutive threads along f then c (coalesced writes)
+__global__ __launch_bounds__(256) void k_flatten(const float *__restrict__ in, const float *__restrict__ pb,
+                                                 float *__restrict__ flat, size_t rows, int Fo, int C) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t CF = (size_t)C * Fo;
+    if (idx >= rows * CF) return;
+    const size_t r = idx / CF;
+    const int j = (int)(idx - r * CF), c = j / Fo, f = j - c * Fo;
+    const float v = in[(r * Fo + f) * C + c] + pb[c];
+    flat[idx] = v < 0.0f ? 0.0f : v;
+}
+
+// y[r][i] = (y[r][i] + b[i]) * scale (the subsampling's linear bias, then
+// the layer input scale: encoder.c:958-959)
+__global__ __launch_bounds__(256) void k_bias_scale(float *__restrict__ y, const float *__restrict__ b, size_t rows,
+                                                    int d, float scale) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= rows * d) return;
+    const int i = (int)(idx % d);
+    const float v = y[idx] + b[i];
+    y[idx] = scale != 1.0f ? v * scale : v;
+}
+
 }  // namespace
 
 bool mh_enc_d_supported(int d) { return d > 0 && d % 256 == 0 && d <= 4096; }
@@ -172,5 +285,48 @@ hipError_t mh_launch_dwconv(const float *g, const float *w, const float *bias, c
     const size_t n = (size_t)nseq * T * (d / 4);
     hipLaunchKernelGGL(k_dwconv, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, w, bias, scale, shift, out,
                        T, nseq, d, k, pc);
+    return hipGetLastError();
+}
+
+int mh_ss_out_len(int n, int causal) {
+    // (n + pl + pr - 3) / 2 + 1 with pads (2, 1) causal, (1, 1) otherwise
+    const int p = causal ? 3 : 2;
+    return (n + p - 3) / 2 + 1;
+}
+
+hipError_t mh_launch_conv_in(const float *x, const float *w, const float *b, float *out, int nseq, int T, int F,
+                             int C, int causal, hipStream_t st) {
+    if (C % 4) return hipErrorInvalidValue;
+    const int To = mh_ss_out_len(T, causal), Fo = mh_ss_out_len(F, causal);
+    const size_t n = (size_t)nseq * To * Fo * (C / 4);
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(k_conv_in, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, w, b, out, nseq, T, F, To, Fo,
+                       C, causal ? 2 : 1);
+    return hipGetLastError();
+}
+
+hipError_t mh_launch_dw_s2(const float *in, const float *pb, const float *w, const float *b, float *out, int nseq,
+                           int T, int F, int C, int causal, hipStream_t st) {
+    if (C % 4) return hipErrorInvalidValue;
+    const int To = mh_ss_out_len(T, causal), Fo = mh_ss_out_len(F, causal);
+    const size_t n = (size_t)nseq * To * Fo * (C / 4);
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(k_dw_s2, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, in, pb, w, b, out, nseq, T, F, To,
+                       Fo, C, causal ? 2 : 1);
+    return hipGetLastError();
+}
+
+hipError_t mh_launch_flatten(const float *in, const float *pb, float *flat, size_t rows, int Fo, int C,
+                             hipStream_t st) {
+    const size_t n = rows * (size_t)C * Fo;
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(k_flatten, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, in, pb, flat, rows, Fo, C);
+    return hipGetLastError();
+}
+
+hipError_t mh_launch_bias_scale(float *y, const float *b, size_t rows, int d, float scale, hipStream_t st) {
+    const size_t n = rows * (size_t)d;
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(k_bias_scale, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, b, rows, d, scale);
     return hipGetLastError();
 }

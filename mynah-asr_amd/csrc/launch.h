@@ -129,6 +129,20 @@ hipError_t mh_launch_dwconv(const float *g, const float *w, const float *bias, c
                             const float *shift, float *out, int T, int nseq, int d, int k, int causal,
                             hipStream_t st);
 
+// The dw_striding subsampling's steps (encoder.hip), channel-last activations
+// [segment][time][freq][channel] (C a multiple of 4); causal pads (2, 1),
+// else (1, 1), in time and frequency alike.
+int mh_ss_out_len(int n, int causal);   // the length after one stride-2 stage
+hipError_t mh_launch_conv_in(const float *x, const float *w, const float *b, float *out, int nseq, int T, int F,
+                             int C, int causal, hipStream_t st);
+// pb (or null): the previous pointwise conv's bias, applied with ReLU on load
+hipError_t mh_launch_dw_s2(const float *in, const float *pb, const float *w, const float *b, float *out, int nseq,
+                           int T, int F, int C, int causal, hipStream_t st);
+hipError_t mh_launch_flatten(const float *in, const float *pb, float *flat, size_t rows, int Fo, int C,
+                             hipStream_t st);
+// y = (y + b) * scale per row (scale 1: the bias alone)
+hipError_t mh_launch_bias_scale(float *y, const float *b, size_t rows, int d, float scale, hipStream_t st);
+
 // AED decoder step kernels (decoder.hip); st = device int[2]: position p, last argmax
 int mh_att_splits(int n);   // attention splits for n keys
 hipError_t mh_launch_embed_ln(const float *emb, const float *pos, const int *prompt, int n_prompt, const int *st,

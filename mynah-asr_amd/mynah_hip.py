@@ -40,7 +40,7 @@ HIP_SYMBOLS = [
     "mynah_asr_hip_relpos_attention_dev", "mynah_asr_hip_relpos_attention",
     "mynah_asr_hip_aed_decode_dev", "mynah_asr_hip_aed_forced_dev",
     "mynah_asr_hip_qgemm_noalloc_dev", "mynah_asr_hip_noalloc_bytes", "mynah_asr_hip_read_floor_dev",
-    "mynah_asr_hip_encoder_layer_dev",
+    "mynah_asr_hip_encoder_layer_dev", "mynah_asr_hip_subsampling_dev",
 ]
 HOST_SYMBOLS = [
     "mynah_asr_set_backend", "mynah_asr_backend", "mynah_asr_gemm_wt", "mynah_asr_silu",
@@ -79,6 +79,14 @@ class EncLayerC(C.Structure):
               "ff1_b1", "ff1_b2", "ff2_b1", "ff2_b2", "q_b", "k_b", "v_b", "o_b", "pw1_b", "dw_b", "pw2_b",
               "cnorm_scale", "cnorm_shift", "ln_ff2_w", "ln_ff2_b", "ff2_w1", "ff2_w2", "ln_out_w", "ln_out_b")
     _fields_ = [(f, C.c_void_p) for f in FIELDS]
+
+
+class SubsamplingC(C.Structure):
+    """mynah_asr_hip_subsampling (include/mynah_asr_hip.h; src/subsampling.h:12-21)."""
+    _fields_ = [("conv_in_w", C.c_void_p), ("conv_in_b", C.c_void_p), ("dw_w", C.c_void_p * 2),
+                ("dw_b", C.c_void_p * 2), ("pw_w", C.c_void_p * 2), ("pw_b", C.c_void_p * 2),
+                ("lin_w", C.c_void_p), ("lin_b", C.c_void_p), ("channels", C.c_int), ("d_model", C.c_int),
+                ("causal", C.c_int)]
 
 
 class WDesc(C.Structure):
@@ -148,6 +156,9 @@ class HipLib:
         if hasattr(L, "mynah_asr_hip_encoder_layer_dev"):
             L.mynah_asr_hip_encoder_layer_dev.argtypes = [C.POINTER(EncLayerC), _P, C.c_int, C.c_int, _P] + \
                 [C.c_int] * 6 + [_P]
+        if hasattr(L, "mynah_asr_hip_subsampling_dev"):
+            L.mynah_asr_hip_subsampling_dev.argtypes = [C.POINTER(SubsamplingC), _P, C.c_int, C.c_int, C.c_int,
+                                                        C.c_float, _P, C.POINTER(C.c_int), _P]
         if hasattr(L, "mynah_asr_hip_aed_decode_dev"):
             L.mynah_asr_hip_aed_decode_dev.argtypes = [C.POINTER(AedC), _P, C.c_int, _P, C.c_int, C.c_int, _P,
                                                        C.c_int, _P]
@@ -497,6 +508,54 @@ class DeviceEncoderLayer:
         rc = self.lib.L.mynah_asr_hip_encoder_layer_dev(C.byref(self.c), x_ptr, T, nseq, pe_ptr, d, H, conv_k, causal,
                                                         left, right, stream or None)
         self.lib._check(rc, "encoder_layer_dev")
+
+    def close(self):
+        for k in self._keep:
+            if isinstance(k, DeviceWeight):
+                k.close()
+        self._keep = []
+
+
+class DeviceSubsampling:
+    """The dw_striding subsampling on the device. `params`: conv_in_w [C, 1,
+    3, 3], conv_in_b, dw_w0/dw_w1 [C, 1, 3, 3], dw_b0/dw_b1, pw_w0/pw_w1
+    [C, C] (or [C, C, 1, 1]), pw_b0/pw_b1, lin_w [d_model, C * F'], lin_b, as
+    f32 arrays (src/subsampling.h:12-21). The pointwise convs and the linear
+    become resident F32 weights."""
+
+    def __init__(self, lib: "HipLib", params: dict, causal: int):
+        import torch
+        self.lib, self.torch = lib, torch
+        self._keep = []
+
+        def dev(a):
+            t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32).reshape(-1)).cuda()
+            self._keep.append(t)
+            return t.data_ptr()
+
+        def lin(a):
+            a = np.asarray(a, np.float32)
+            dw = DeviceWeight(lib, Weight.make(lib, F32, a.reshape(a.shape[0], -1)))
+            self._keep.append(dw)
+            return dw.h
+
+        c = self.c = SubsamplingC()
+        c.conv_in_w, c.conv_in_b = dev(params["conv_in_w"]), dev(params["conv_in_b"])
+        for i in range(2):
+            c.dw_w[i], c.dw_b[i] = dev(params[f"dw_w{i}"]), dev(params[f"dw_b{i}"])
+            c.pw_w[i], c.pw_b[i] = lin(params[f"pw_w{i}"]), dev(params[f"pw_b{i}"])
+        c.lin_w, c.lin_b = lin(params["lin_w"]), dev(params["lin_b"])
+        c.channels, c.d_model, c.causal = params["conv_in_w"].shape[0], params["lin_w"].shape[0], causal
+        torch.cuda.synchronize()
+
+    def run(self, feats_ptr: int, T: int, nseq: int, n_mels: int, out_ptr: int, xscale: float = 1.0,
+            stream: int = 0) -> int:
+        """mynah_asr_hip_subsampling_dev: returns T' (rows per segment of out)."""
+        t_out = C.c_int(0)
+        rc = self.lib.L.mynah_asr_hip_subsampling_dev(C.byref(self.c), feats_ptr, T, nseq, n_mels, xscale, out_ptr,
+                                                      C.byref(t_out), stream or None)
+        self.lib._check(rc, "subsampling_dev")
+        return t_out.value
 
     def close(self):
         for k in self._keep:

@@ -107,3 +107,38 @@ def pos_emb(T, d):
     pe[:, 0::2] = np.sin(f)
     pe[:, 1::2] = np.cos(f)
     return pe
+
+
+# ------------------------------------------------------------ subsampling
+def conv2d_s2(x, w, b, pl, pr, depthwise):
+    """subsampling.c:109-200: 3x3 stride-2 conv of x [C_in, T, F] with zero
+    pads (pl, pr) in time and frequency; w [C_out, C_in or 1, 3, 3]."""
+    x = np.asarray(x, np.float64)
+    Cin, T, F = x.shape
+    xp = np.zeros((Cin, T + pl + pr, F + pl + pr))
+    xp[:, pl:pl + T, pl:pl + F] = x
+    To, Fo = (T + pl + pr - 3) // 2 + 1, (F + pl + pr - 3) // 2 + 1
+    Cout = w.shape[0]
+    out = np.zeros((Cout, To, Fo)) + np.asarray(b, np.float64)[:, None, None]
+    for dt in range(3):
+        for df in range(3):
+            win = xp[:, dt:dt + 2 * To - 1:2, df:df + 2 * Fo - 1:2]          # [Cin, To, Fo]
+            if depthwise:
+                out += w[:, 0, dt, df][:, None, None] * win
+            else:
+                out += np.einsum("oi,itf->otf", w[:, :, dt, df], win)
+    return out
+
+
+def subsampling(feats, p, causal):
+    """subsampling.c:208-268 on one segment feats [T, n_mels]: conv_in + ReLU,
+    twice (depthwise, pointwise, ReLU), channel-major flatten, linear."""
+    pl, pr = (2, 1) if causal else (1, 1)
+    relu = lambda a: np.maximum(a, 0.0)
+    a = relu(conv2d_s2(np.asarray(feats, np.float64)[None], p["conv_in_w"], p["conv_in_b"], pl, pr, False))
+    for i in range(2):
+        bb = conv2d_s2(a, p[f"dw_w{i}"], p[f"dw_b{i}"], pl, pr, True)
+        a = relu(np.einsum("oc,ctf->otf", p[f"pw_w{i}"], bb) + np.asarray(p[f"pw_b{i}"], np.float64)[:, None, None])
+    C, To, Fo = a.shape
+    flat = a.transpose(1, 0, 2).reshape(To, C * Fo)                        # flat[t, c * Fo + f]
+    return linear(flat, p["lin_w"], p["lin_b"])

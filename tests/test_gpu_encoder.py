@@ -142,3 +142,50 @@ def test_encoder_layer_refuses_bad_shapes(gpu):
         c.cnorm_shift = saved
     finally:
         dev.close()
+
+
+def ss_params(seed, C, n_mels, d, causal):
+    r = np.random.default_rng(seed)
+    g = lambda *s: r.standard_normal(s).astype(np.float32)
+    F = n_mels
+    for _ in range(3):
+        F = (F + (3 if causal else 2) - 3) // 2 + 1
+    return {"conv_in_w": 0.3 * g(C, 1, 3, 3), "conv_in_b": 0.1 * g(C),
+            "dw_w0": 0.3 * g(C, 1, 3, 3), "dw_b0": 0.1 * g(C), "pw_w0": 0.1 * g(C, C), "pw_b0": 0.1 * g(C),
+            "dw_w1": 0.3 * g(C, 1, 3, 3), "dw_b1": 0.1 * g(C), "pw_w1": 0.1 * g(C, C), "pw_b1": 0.1 * g(C),
+            "lin_w": 0.05 * g(d, C * F), "lin_b": 0.1 * g(d)}
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_subsampling_matches_oracle(gpu, causal):
+    """mynah_asr_hip_subsampling_dev against the float64 restatement of
+    src/subsampling.c:208-268 (oracle/encoder.py, pinned against the
+    reference's direct loop): 3 segments of 203 frames of 80 mel features,
+    C = 64, d_model 256, xscale 2. Bar: |y - ref| <= 5e-6 * (|ref| + rms(ref))
+    (measured worst 8.2e-7: f32-weight products and 9-term f32 convolution
+    sums)."""
+    import torch
+    say("subsampling, causal", causal)
+    C, nm, d, T, nseq = 64, 80, 256, 203, 3
+    p = ss_params(12, C, nm, d, causal)
+    dev = M.DeviceSubsampling(gpu, p, causal)
+    try:
+        x = np.random.default_rng(13).standard_normal((nseq * T, nm)).astype(np.float32)
+        To = (T + (3 if causal else 2) - 3) // 2 + 1
+        for _ in range(2):
+            To = (To + (3 if causal else 2) - 3) // 2 + 1
+        out = torch.full((nseq * To, d), float("nan"), dtype=torch.float32, device="cuda")
+        xd = torch.from_numpy(x).cuda()
+        t_out = dev.run(xd.data_ptr(), T, nseq, nm, out.data_ptr(), xscale=2.0)
+        torch.cuda.synchronize()
+        assert t_out == To
+        y = out.cpu().numpy()
+        pp = {k: (v.reshape(v.shape[0], -1) if k.startswith("pw_w") else v) for k, v in p.items()}
+        ref = np.concatenate([2.0 * E.subsampling(x[s * T:(s + 1) * T], pp, causal) for s in range(nseq)])
+        err = np.abs(y - ref)
+        rms = float(np.sqrt((ref ** 2).mean()))
+        say(f"  max |y - ref| {err.max():.3g} (rms ref {rms:.3g}), worst / (|ref| + rms) "
+            f"{(err / (np.abs(ref) + rms)).max():.3g}")
+        assert (err <= 5e-6 * (np.abs(ref) + rms)).all()
+    finally:
+        dev.close()

@@ -152,3 +152,78 @@ def test_pos_emb_closed_form():
     p, j = 1, 2
     assert np.isclose(pe[p, 2 * j], np.sin((T - 1 - p) * 10000.0 ** (-2.0 * j / d)))
     assert np.isclose(pe[p, 2 * j + 1], np.cos((T - 1 - p) * 10000.0 ** (-2.0 * j / d)))
+
+
+def conv2d_direct(x, w, b, pl, pr, depthwise):
+    """The reference's direct loop (subsampling.c:169-197), element by
+    element, for tiny inputs: the vectorized oracle must equal it."""
+    Cin, T, F = x.shape
+    To, Fo = (T + pl + pr - 3) // 2 + 1, (F + pl + pr - 3) // 2 + 1
+    Cout = w.shape[0]
+    out = np.zeros((Cout, To, Fo))
+    for co in range(Cout):
+        for ci in ([co] if depthwise else range(Cin)):
+            ker = w[co, 0] if depthwise else w[co, ci]
+            for to in range(To):
+                for fo in range(Fo):
+                    acc = 0.0
+                    for dt in range(3):
+                        t = 2 * to - pl + dt
+                        if t < 0 or t >= T:
+                            continue
+                        for df in range(3):
+                            f = 2 * fo - pl + df
+                            if 0 <= f < F:
+                                acc += ker[dt, df] * x[ci, t, f]
+                    out[co, to, fo] += acc
+        out[co] += b[co]
+    return out
+
+
+@pytest.mark.parametrize("pl,pr", [(1, 1), (2, 1)])
+def test_conv2d_s2_equals_the_direct_loop(pl, pr):
+    r = rng(20)
+    x = r.standard_normal((3, 9, 7))
+    w, b = r.standard_normal((4, 3, 3, 3)), r.standard_normal(4)
+    assert np.allclose(E.conv2d_s2(x, w, b, pl, pr, False), conv2d_direct(x, w, b, pl, pr, False))
+    wd = r.standard_normal((3, 1, 3, 3))
+    assert np.allclose(E.conv2d_s2(x, wd, b[:3], pl, pr, True), conv2d_direct(x, wd, b[:3], pl, pr, True))
+    # output sizes: (n + pl + pr - 3) // 2 + 1
+    assert E.conv2d_s2(x, w, b, pl, pr, False).shape == (4, (9 + pl + pr - 3) // 2 + 1, (7 + pl + pr - 3) // 2 + 1)
+
+
+def test_conv2d_s2_centre_tap_subsamples():
+    """A kernel with only tap (pl, pl) picks x[2 to, 2 fo] (the stride)."""
+    x = rng(21).standard_normal((1, 10, 8))
+    for pl, pr in ((1, 1), (2, 1)):
+        w = np.zeros((1, 1, 3, 3))
+        w[0, 0, pl, pl] = 1.0
+        out = E.conv2d_s2(x, w, np.zeros(1), pl, pr, False)
+        To, Fo = out.shape[1:]
+        want = np.zeros((To, Fo))            # positions past the end read the right pad (zero)
+        sub = x[0, 0:2 * To:2, 0:2 * Fo:2]
+        want[:sub.shape[0], :sub.shape[1]] = sub
+        assert np.array_equal(out[0], want)
+
+
+def test_subsampling_flatten_order():
+    """subsampling.c:248-264: the linear sees flat[t, c * F' + f]. With
+    identity-like convs (centre taps one, pointwise I, zero biases) and a
+    positive input, the output picks the input at (8 t, 8 f) through the
+    linear's column c * F' + f."""
+    T, nm, C, d = 24, 16, 4, 5
+    x = np.abs(rng(22).standard_normal((T, nm))) + 0.1
+    p = {"conv_in_w": np.zeros((C, 1, 3, 3)), "conv_in_b": np.zeros(C), "lin_b": np.zeros(d)}
+    p["conv_in_w"][:, 0, 1, 1] = 1.0
+    for i in range(2):
+        p[f"dw_w{i}"] = np.zeros((C, 1, 3, 3))
+        p[f"dw_w{i}"][:, 0, 1, 1] = 1.0
+        p[f"dw_b{i}"], p[f"pw_w{i}"], p[f"pw_b{i}"] = np.zeros(C), np.eye(C), np.zeros(C)
+    Fo, To = 2, 3   # 16 -> 8 -> 4 -> 2; 24 -> 12 -> 6 -> 3
+    for c in range(C):
+        for f in range(Fo):
+            lw = np.zeros((d, C * Fo))
+            lw[0, c * Fo + f] = 1.0
+            out = E.subsampling(x, dict(p, lin_w=lw), causal=0)
+            assert out.shape == (To, d)
+            assert np.allclose(out[:, 0], x[0:8 * To:8, 8 * f])
