@@ -197,10 +197,9 @@ def run_config5(B, M_, reps=3):
     segment, 16 x 1499 rows; one product over the 1499 shared rows gives the
     same values), the relative-position attention core over the 16 segments,
     and the conv module's pointwise convolutions (1024->2048 before the GLU,
-    1024->1024 after). Not built here: layer norms, GLU, depthwise conv, batch
-    norm, residual adds, subsampling. Each call is timed with HIP events on the
-    stream (preparation included); the layer's time is their sum, the
-    forward's 24 times that; RTF over 16 x 60 s of audio."""
+    1024->1024 after). Each call is timed with HIP events on the stream
+    (preparation included), for the per-GEMM roofline fractions; the whole
+    forward is run_config5_forward's."""
     torch, lib = B.torch, B.lib
     Mr, T, nseq, d, H = 12000, 750, 16, 1024, 8
     mk = lambda seed, n, k: M_.DeviceWeight(lib, M_.Weight.make(lib, M_.Q8_0, lib.randn(seed, 0.02, (n, k))))
@@ -262,9 +261,100 @@ def run_config5(B, M_, reps=3):
     fwd_ms = 24 * seq_us / 1e3
     return {"rows": Mr, "segments": nseq, "frames": T, "layers": 24, "format": "Q8_0", "numerics": "EXACT",
             "steps": rows, "layer_us_sum_of_steps": round(total, 1), "layer_us_sequence": round(seq_us, 1),
-            "forward_ms_built_parts": round(fwd_ms, 2), "rtf_built_parts": float(f"{fwd_ms / 1e3 / 960.0:.3g}"),
-            "note": "linears + pos projection + attention core of 24 layers only (layer norms, GLU, depthwise "
-                    "conv, batch norm, residuals and subsampling are outside this build); RTF over 960 s of audio"}
+            "products_attention_24_layers_ms": round(fwd_ms, 2),
+            "note": "the products and attention core of one layer, step by step; the whole encoder forward "
+                    "(subsampling, layer norms, GLU, depthwise conv, residuals): config5_forward"}
+
+
+def run_config5_forward(B, M_, reps=3):
+    """BASELINE config 5 end to end, on the device: a random-init
+    FastConformer-0.6B encoder (24 layers, d_model 1024, 8 heads, FFN 4096
+    macaron, depthwise conv kernel 9, dw_striding 8x subsampling with 256
+    channels) over 16 segments of 60 s (6000 log-mel frames of 80 features,
+    N(0, 1)), all 16 segments as one batch of 12000 encoder rows: the
+    subsampling (mynah_asr_hip_subsampling_dev), then the 24 layers
+    (mynah_asr_hip_encoder_layer_dev; src/encoder.c:948-1010 forward_batch
+    without its final projection). Linears Q8_0 (EXACT numerics), the
+    position projection and the subsampling's pointwise convs and linear f32;
+    no linear biases (the reference's fused-FFN path), the folded batch norm,
+    'same' conv padding, full attention, xscale 1. Every layer has its own
+    weights (624 MB resident). Timed with HIP events on the bench stream;
+    RTF = forward time / 960 s of audio."""
+    torch, lib = B.torch, B.lib
+    nseq, Tm, nm, d, H, f, k, C, L = 16, 6000, 80, 1024, 8, 4096, 9, 256, 24
+    r = np.random.default_rng(600)
+    g = lambda *shape: r.standard_normal(shape).astype(np.float32)
+    t0 = time.perf_counter()
+    layers = []
+    for li in range(L):
+        sd = 1000 + 100 * li
+        p = {"relk_w": lib.randn(sd + 9, 0.02, (d, d)), "bias_u": 0.1 * g(d), "bias_v": 0.1 * g(d),
+             "dw_w": 0.3 * g(d, k), "cnorm_scale": 1 + 0.1 * g(d), "cnorm_shift": 0.1 * g(d)}
+        for n in ("ff1", "att", "conv", "ff2", "out"):
+            p[f"ln_{n}_w"], p[f"ln_{n}_b"] = 1 + 0.1 * g(d), 0.1 * g(d)
+        for j, (n, shape) in enumerate((("ff1_w1", (f, d)), ("ff1_w2", (d, f)), ("ff2_w1", (f, d)), ("ff2_w2", (d, f)),
+                                        ("q_w", (d, d)), ("k_w", (d, d)), ("v_w", (d, d)), ("o_w", (d, d)),
+                                        ("pw1_w", (2 * d, d)), ("pw2_w", (d, d)))):
+            p[n] = lib.randn(sd + j, 0.02, shape)
+        layers.append(M_.DeviceEncoderLayer(lib, p, M_.Q8_0))
+    Fo = nm
+    for _ in range(3):
+        Fo = (Fo + 2 - 3) // 2 + 1
+    ssp = {"conv_in_w": 0.3 * g(C, 1, 3, 3), "conv_in_b": 0.1 * g(C), "lin_w": lib.randn(1999, 0.02, (d, C * Fo)),
+           "lin_b": 0.1 * g(d)}
+    for i in range(2):
+        ssp[f"dw_w{i}"], ssp[f"dw_b{i}"] = 0.3 * g(C, 1, 3, 3), 0.1 * g(C)
+        ssp[f"pw_w{i}"], ssp[f"pw_b{i}"] = lib.randn(1998 - i, 0.05, (C, C)), 0.1 * g(C)
+    ss = M_.DeviceSubsampling(lib, ssp, 0)
+    setup_s = time.perf_counter() - t0
+    mel = B.dev(lib.randn(1997, 1.0, (nseq * Tm, nm)))
+    T = (Tm - 1) // 2 + 1
+    T = (T - 1) // 2 + 1
+    T = (T - 1) // 2 + 1
+    # the relative positional embedding (encoder.c:201-212), formed on the host as the reference does
+    pos = (T - 1 - np.arange(2 * T - 1, dtype=np.float64))[:, None]
+    fr = pos * np.power(10000.0, -2.0 * np.arange(d // 2, dtype=np.float64)[None, :] / d)
+    pe_h = np.empty((2 * T - 1, d), np.float32)
+    pe_h[:, 0::2], pe_h[:, 1::2] = np.sin(fr), np.cos(fr)
+    pe = B.dev(pe_h)
+    x = B.empty(nseq * T, d)
+    sp = B.sp
+
+    def forward():
+        t_out = ss.run(mel.data_ptr(), Tm, nseq, nm, x.data_ptr(), 1.0, sp)
+        assert t_out == T
+        for ly in layers:
+            ly.run(x.data_ptr(), T, nseq, pe.data_ptr(), d, H, k, 0, -1, 0, sp)
+
+    forward()
+    B.sync()
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    e0, e1, e2 = ev(), ev(), ev()
+    e0.record(B.stream)
+    for _ in range(reps):
+        forward()
+    e1.record(B.stream)
+    B.sync()
+    fwd_ms = e0.elapsed_time(e1) / reps
+    # the subsampling alone and one layer alone, for the split
+    e0.record(B.stream)
+    for _ in range(reps):
+        ss.run(mel.data_ptr(), Tm, nseq, nm, x.data_ptr(), 1.0, sp)
+    e1.record(B.stream)
+    for _ in range(reps):
+        layers[0].run(x.data_ptr(), T, nseq, pe.data_ptr(), d, H, k, 0, -1, 0, sp)
+    e2.record(B.stream)
+    B.sync()
+    ss_ms, layer_ms = e0.elapsed_time(e1) / reps, e1.elapsed_time(e2) / reps
+    finite = bool(torch.isfinite(x).all().item())
+    for ly in layers:
+        ly.close()
+    ss.close()
+    return {"segments": nseq, "mel_frames": Tm, "encoder_frames": T, "rows": nseq * T, "layers": L,
+            "format": "Q8_0", "numerics": "EXACT", "forward_ms": round(fwd_ms, 2),
+            "subsampling_ms": round(ss_ms, 3), "layer_ms": round(layer_ms, 3),
+            "rtf": float(f"{fwd_ms / 1e3 / (nseq * 60.0):.3g}"), "output_finite": finite,
+            "weights_setup_s": round(setup_s, 1)}
 
 
 def read_floor_us(B, nbytes, copies):
@@ -536,6 +626,8 @@ def headline_summary(details: dict, rows: list) -> dict:
               and r.get("n") == 4096]
         if c1:
             s["config1_us_per_call"] = c1[0].get("call_us")
+    if "config5_forward" in details:
+        s["config5_rtf"] = details["config5_forward"]["rtf"]
     if "int8act_int8_m6000" in details:
         s["int8_qmat_set_tops"] = details["int8act_int8_m6000"]["tops"]
     return s
@@ -810,7 +902,8 @@ def main():
         print(json.dumps(run_int8act(B, M_, M)), flush=True)
         return
     if args.config5:
-        print(json.dumps({"config5_layer": run_config5(B, M_)}), flush=True)
+        print(json.dumps({"config5_layer": run_config5(B, M_), "config5_forward": run_config5_forward(B, M_)}),
+              flush=True)
         return
     if args.vendor:
         print(json.dumps({"vendor_gemm": run_vendor_gemm(B)}), flush=True)
@@ -868,6 +961,8 @@ def main():
         details["gemm_small_m"] = run_small_m(B, M_)
         log("[bench] config5")
         details["config5_layer"] = run_config5(B, M_)
+        log("[bench] config5 forward")
+        details["config5_forward"] = run_config5_forward(B, M_)
         log("[bench] vendor gemm")
         details["vendor_gemm"] = run_vendor_gemm(B)
 
