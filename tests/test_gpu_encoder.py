@@ -189,3 +189,41 @@ def test_subsampling_matches_oracle(gpu, causal):
         assert (err <= 5e-6 * (np.abs(ref) + rms)).all()
     finally:
         dev.close()
+
+
+@pytest.mark.parametrize("mode", [M.INT8ACT, M.QMAT], ids=["int8act", "qmat"])
+def test_encoder_layer_in_other_numerics(gpu, mode):
+    """Each product of the layer runs in the current numerics mode (the
+    f32 position projection stays f32, as the reference keeps relk_w): in
+    INT8ACT (Q8_0: per-row int8 activations) the layer stays within the int8
+    path's budget of the EXACT layer (relative L2 < 1e-2; the output is a
+    layer norm, O(1)); QMAT numerics runs Q8_0 products EXACT (qmat.c's
+    dispatch takes the int8 path for INT8/INT4 weights only), so its output
+    has the EXACT layer's bits."""
+    import torch
+    say("encoder layer, numerics", mode)
+    d, H, f, k, T, nseq = 256, 4, 512, 9, 40, 2
+    p = make_params(14, d, f, k, True, True)
+    dev = M.DeviceEncoderLayer(gpu, p, M.Q8_0)
+    try:
+        x = np.random.default_rng(15).standard_normal((nseq * T, d)).astype(np.float32)
+        ped = torch.from_numpy(E.pos_emb(T, d).astype(np.float32)).cuda()
+        ys = {}
+        for m in (M.EXACT, mode):
+            assert gpu.set_numerics(m) == m
+            xd = torch.from_numpy(x).cuda()
+            dev.run(xd.data_ptr(), T, nseq, ped.data_ptr(), d, H, k, 0)
+            torch.cuda.synchronize()
+            ys[m] = xd.cpu().numpy()
+        gpu.set_numerics(M.EXACT)
+        y, ex = ys[mode], ys[M.EXACT]
+        assert np.isfinite(y).all()
+        if mode == M.QMAT:
+            assert np.array_equal(y.view(np.uint32), ex.view(np.uint32))
+        else:
+            rel = float(np.linalg.norm(y - ex) / np.linalg.norm(ex))
+            say(f"  relative L2 vs EXACT {rel:.3g}")
+            assert 0 < rel < 1e-2
+    finally:
+        gpu.set_numerics(M.EXACT)
+        dev.close()
