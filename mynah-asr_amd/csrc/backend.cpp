@@ -816,11 +816,12 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
     const size_t md = (size_t)M * d;
     // xn, tmp, q, k, v, ctx [M, d]; h [M, 2d] (pw1, GLU); rk [P, d]; the FFN
     // intermediate [M, f] only with FFN biases
-    const size_t need = 6 * md + 2 * md + (size_t)P * d + (biased_ffn ? (size_t)M * f : 0);
+    const size_t kd = ((size_t)conv_k * d + 3) / 4 * 4;   // the depthwise taps, tap-major
+    const size_t need = 6 * md + 2 * md + (size_t)P * d + kd + (biased_ffn ? (size_t)M * f : 0);
     float *base = (float *)c->enc.get(need * sizeof(float));
     if (!base) return fail("device buffer allocation failed");
     float *xn = base, *tmp = xn + md, *q = tmp + md, *k = q + md, *v = k + md, *ctx = v + md, *h = ctx + md,
-          *rk = h + 2 * md, *hf = rk + (size_t)P * d;
+          *rk = h + 2 * md, *dwt = rk + (size_t)P * d, *hf = dwt + kd;
     hipError_t e;
 #define ENC_TRY(expr)                                                                   \
     do {                                                                                \
@@ -857,11 +858,11 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
     }
     if (bias_add(h, L->pw1_b, M, 2 * d, st)) return -1;
     ENC_TRY(mh_launch_glu(h, q, M, d, st));   // g (q is free now)
+    ENC_TRY(mh_launch_transpose_taps(L->dw_w, dwt, d, conv_k, st));
     if (L->cnorm_scale) {
-        ENC_TRY(mh_launch_dwconv(q, L->dw_w, L->dw_b, L->cnorm_scale, L->cnorm_shift, k, T, nseq, d, conv_k, causal,
-                                 st));
+        ENC_TRY(mh_launch_dwconv(q, dwt, L->dw_b, L->cnorm_scale, L->cnorm_shift, k, T, nseq, d, conv_k, causal, st));
     } else {
-        ENC_TRY(mh_launch_dwconv(q, L->dw_w, L->dw_b, nullptr, nullptr, v, T, nseq, d, conv_k, causal, st));
+        ENC_TRY(mh_launch_dwconv(q, dwt, L->dw_b, nullptr, nullptr, v, T, nseq, d, conv_k, causal, st));
         ENC_TRY(mh_launch_add_ln(v, nullptr, 0.0f, L->cnorm_w, L->cnorm_b, k, M, d, st));
         ENC_TRY(mh_launch_silu(k, md, st));
     }
@@ -892,10 +893,10 @@ int subsampling_dev(Ctx *c, const mynah_asr_hip_subsampling *ss, const float *fe
     if (ss->lin_w->dw.k != C * F3) return fail("subsampling: lin_w must be [d_model, channels * F']");
     // A holds the stage-0 output, then the pointwise outputs; B the depthwise
     // outputs, then the flattened rows
-    const size_t a = (size_t)nseq * T1 * F1 * C, b = (size_t)nseq * T2 * F2 * C;
-    float *A = (float *)c->ssb.get((a + b) * sizeof(float));
+    const size_t a = (size_t)nseq * T1 * F1 * C, b = (size_t)nseq * T2 * F2 * C, tw = (size_t)27 * C;
+    float *A = (float *)c->ssb.get((a + b + tw) * sizeof(float));
     if (!A) return fail("device buffer allocation failed");
-    float *B = A + a;
+    float *B = A + a, *w0 = B + b, *w1 = w0 + 9 * (size_t)C, *w2 = w1 + 9 * (size_t)C;   // taps tap-major
     hipError_t e;
 #define SS_TRY(expr)                                                                 \
     do {                                                                             \
@@ -903,10 +904,13 @@ int subsampling_dev(Ctx *c, const mynah_asr_hip_subsampling *ss, const float *fe
         if (e != hipSuccess) return fail("subsampling launch failed", hipGetErrorString(e)); \
     } while (0)
     NumScope sc(MYNAH_ASR_HIP_EXACT);
-    SS_TRY(mh_launch_conv_in(feats, ss->conv_in_w, ss->conv_in_b, A, nseq, T, F, C, cz, st));
-    SS_TRY(mh_launch_dw_s2(A, nullptr, ss->dw_w[0], ss->dw_b[0], B, nseq, T1, F1, C, cz, st));
+    SS_TRY(mh_launch_transpose_taps(ss->conv_in_w, w0, C, 9, st));
+    SS_TRY(mh_launch_transpose_taps(ss->dw_w[0], w1, C, 9, st));
+    SS_TRY(mh_launch_transpose_taps(ss->dw_w[1], w2, C, 9, st));
+    SS_TRY(mh_launch_conv_in(feats, w0, ss->conv_in_b, A, nseq, T, F, C, cz, st));
+    SS_TRY(mh_launch_dw_s2(A, nullptr, w1, ss->dw_b[0], B, nseq, T1, F1, C, cz, st));
     if (gemm_dev(c, ss->pw_w[0], B, A, nseq * T2 * F2, 0, st)) return -1;
-    SS_TRY(mh_launch_dw_s2(A, ss->pw_b[0], ss->dw_w[1], ss->dw_b[1], B, nseq, T2, F2, C, cz, st));
+    SS_TRY(mh_launch_dw_s2(A, ss->pw_b[0], w2, ss->dw_b[1], B, nseq, T2, F2, C, cz, st));
     if (gemm_dev(c, ss->pw_w[1], B, A, nseq * T3 * F3, 0, st)) return -1;
     SS_TRY(mh_launch_flatten(A, ss->pw_b[1], B, (size_t)nseq * T3, F3, C, st));
     if (gemm_dev(c, ss->lin_w, B, out, nseq * T3, 0, st)) return -1;

@@ -111,8 +111,9 @@ __device__ __forceinline__ float silu_e(float x) { return x * sigmoid_f(x); }
 
 // c[t, i] = dw_b[i] + sum_j w[i, j] * g[t - pc + j, i] over the taps inside
 // the segment (in tap order from j0), then, with scale: silu(c * scale +
-// shift). Thread = (row, 4 channels).
-__global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ g, const float *__restrict__ w,
+// shift). Thread = (row, 4 channels); the weights tap-major, wt[j][i]
+// (k_transpose), so each tap is one 16-byte load.
+__global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ g, const float *__restrict__ wt,
                                                 const float *__restrict__ bias, const float *__restrict__ scale,
                                                 const float *__restrict__ shift, float *__restrict__ out, int T,
                                                 int nseq, int d, int k, int pc) {
@@ -126,10 +127,11 @@ __global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ g, con
     const int j0 = t - pc < 0 ? pc - t : 0, j1 = t - pc + k > T ? T - t + pc : k;
     for (int j = j0; j < j1; j++) {
         const float4 src = *(const float4 *)(gs + (size_t)(t - pc + j) * d + i);
-        o.x = fmaf(w[(size_t)(i + 0) * k + j], src.x, o.x);
-        o.y = fmaf(w[(size_t)(i + 1) * k + j], src.y, o.y);
-        o.z = fmaf(w[(size_t)(i + 2) * k + j], src.z, o.z);
-        o.w = fmaf(w[(size_t)(i + 3) * k + j], src.w, o.w);
+        const float4 wv = *(const float4 *)(wt + (size_t)j * d + i);
+        o.x = fmaf(wv.x, src.x, o.x);
+        o.y = fmaf(wv.y, src.y, o.y);
+        o.z = fmaf(wv.z, src.z, o.z);
+        o.w = fmaf(wv.w, src.w, o.w);
     }
     if (scale) {
         const float4 sc = *(const float4 *)(scale + i), sh = *(const float4 *)(shift + i);
@@ -142,8 +144,9 @@ __global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ g, con
 }
 
 // out[s][to][fo][c] = relu(b[c] + sum_{dt, df} w[c][3 dt + df] x[s][2 to - pl + dt][2 fo - pl + df])
-// with zeros outside [0, T) x [0, F). Thread = (row (s, to, fo), 4 channels).
-__global__ __launch_bounds__(256) void k_conv_in(const float *__restrict__ x, const float *__restrict__ w,
+// with zeros outside [0, T) x [0, F). Thread = (row (s, to, fo), 4 channels);
+// the weights tap-major, wt[j][c].
+__global__ __launch_bounds__(256) void k_conv_in(const float *__restrict__ x, const float *__restrict__ wt,
                                                  const float *__restrict__ b, float *__restrict__ out, int nseq,
                                                  int T, int F, int To, int Fo, int C, int pl) {
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -161,24 +164,26 @@ __global__ __launch_bounds__(256) void k_conv_in(const float *__restrict__ x, co
             const int t = 2 * to - pl + dt, f = 2 * fo - pl + df;
             v[3 * dt + df] = t >= 0 && t < T && f >= 0 && f < F ? xs[(size_t)t * F + f] : 0.0f;
         }
-    float o[4];
+    float4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const float *wc = w + (size_t)(c + q) * 9;
-        float acc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 9; j++) acc = fmaf(wc[j], v[j], acc);
-        const float r = acc + b[c + q];
-        o[q] = r < 0.0f ? 0.0f : r;
+    for (int j = 0; j < 9; j++) {
+        const float4 wv = *(const float4 *)(wt + (size_t)j * C + c);
+        acc.x = fmaf(wv.x, v[j], acc.x);
+        acc.y = fmaf(wv.y, v[j], acc.y);
+        acc.z = fmaf(wv.z, v[j], acc.z);
+        acc.w = fmaf(wv.w, v[j], acc.w);
     }
-    *(float4 *)(out + row * C + c) = float4{o[0], o[1], o[2], o[3]};
+    const float4 bb = *(const float4 *)(b + c);
+    *(float4 *)(out + row * C + c) = float4{fmaxf(acc.x + bb.x, 0.0f), fmaxf(acc.y + bb.y, 0.0f),
+                                            fmaxf(acc.z + bb.z, 0.0f), fmaxf(acc.w + bb.w, 0.0f)};
 }
 
 // out[s][to][fo][c] = b[c] + sum w[c][3 dt + df] in[s][2 to - pl + dt][2 fo - pl + df][c],
 // in the reference's term order (the nine products summed left to right,
 // subsampling.c:96-98); with pb, each input value is relu(in + pb[c]) first.
+// The weights tap-major, wt[j][c].
 __global__ __launch_bounds__(256) void k_dw_s2(const float *__restrict__ in, const float *__restrict__ pb,
-                                               const float *__restrict__ w, const float *__restrict__ b,
+                                               const float *__restrict__ wt, const float *__restrict__ b,
                                                float *__restrict__ out, int nseq, int T, int F, int To, int Fo,
                                                int C, int pl) {
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -207,16 +212,18 @@ __global__ __launch_bounds__(256) void k_dw_s2(const float *__restrict__ in, con
             }
             v[3 * dt + df] = a;
         }
-    float o[4];
+    float4 wv = *(const float4 *)(wt + c);
+    float4 acc = {wv.x * v[0].x, wv.y * v[0].y, wv.z * v[0].z, wv.w * v[0].w};
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const float *wc = w + (size_t)(c + q) * 9;
-        float acc = wc[0] * v[0][q];
-#pragma unroll
-        for (int j = 1; j < 9; j++) acc = fmaf(wc[j], v[j][q], acc);
-        o[q] = b[c + q] + acc;
+    for (int j = 1; j < 9; j++) {
+        wv = *(const float4 *)(wt + (size_t)j * C + c);
+        acc.x = fmaf(wv.x, v[j].x, acc.x);
+        acc.y = fmaf(wv.y, v[j].y, acc.y);
+        acc.z = fmaf(wv.z, v[j].z, acc.z);
+        acc.w = fmaf(wv.w, v[j].w, acc.w);
     }
-    *(float4 *)(out + row * C + c) = float4{o[0], o[1], o[2], o[3]};
+    const float4 bb = *(const float4 *)(b + c);
+    *(float4 *)(out + row * C + c) = float4{bb.x + acc.x, bb.y + acc.y, bb.z + acc.z, bb.w + acc.w};
 }
 
 // flat[s * To + t][c * Fo + f] = relu(in[s][t][f][c] + pb[c]); thread = one
@@ -230,6 +237,15 @@ __global__ __launch_bounds__(256) void k_flatten(const float *__restrict__ in, c
     const int j = (int)(idx - r * CF), c = j / Fo, f = j - c * Fo;
     const float v = in[(r * Fo + f) * C + c] + pb[c];
     flat[idx] = v < 0.0f ? 0.0f : v;
+}
+
+// wt[j][c] = w[c][j] for w [C][k]: the per-channel taps tap-major
+__global__ __launch_bounds__(256) void k_transpose(const float *__restrict__ w, float *__restrict__ wt, int C,
+                                                   int k) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= C * k) return;
+    const int j = idx / C, c = idx - j * C;
+    wt[idx] = w[(size_t)c * k + j];
 }
 
 // y[r][i] = (y[r][i] + b[i]) * scale (the subsampling's linear bias, then
@@ -328,5 +344,11 @@ hipError_t mh_launch_bias_scale(float *y, const float *b, size_t rows, int d, fl
     const size_t n = rows * (size_t)d;
     if (!n) return hipSuccess;
     hipLaunchKernelGGL(k_bias_scale, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, b, rows, d, scale);
+    return hipGetLastError();
+}
+
+hipError_t mh_launch_transpose_taps(const float *w, float *wt, int C, int k, hipStream_t st) {
+    if (C * k <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_transpose, dim3((C * k + 255) / 256), dim3(256), 0, st, w, wt, C, k);
     return hipGetLastError();
 }
