@@ -257,8 +257,8 @@ typedef struct {
  * ([nseq * T, d], the reference's padding-free batch with equal lengths).
  * The products and layer norms run over all rows; attention and the
  * depthwise conv per segment. pe [2T-1, d]: the segments' relative positional
- * embedding (mynah_asr_pos_emb). d: the model width, a multiple of 256 up to
- * 4096; H heads of 64 or 128; conv_k the depthwise kernel (causal: left pad
+ * embedding (mynah_asr_pos_emb). d: the model width, 256 times 1 to 8, 12 or
+ * 16 (up to 4096); H heads of 64 or 128; conv_k the depthwise kernel (causal: left pad
  * conv_k - 1, else (conv_k - 1) / 2 per side); left / right the attention
  * context as mynah_asr_encoder_layer's (left < 0: full). Each product runs in
  * the current numerics mode; -1 and the reason (mynah_asr_hip_last_error) on

@@ -761,7 +761,7 @@ int gemm_noalloc(const mynah_asr_hip_weight *W, const float *dx, float *dy, int 
 // encoder.hip kernels.
 int enc_check(const mynah_asr_hip_enc_layer *L, int T, int nseq, int d, int H, int conv_k) {
     if (!L || T < 0 || nseq < 0 || d <= 0 || H <= 0 || d % H != 0 || conv_k <= 0) return fail("bad argument");
-    if (!mh_enc_d_supported(d)) return fail("encoder layer: d must be a multiple of 256 up to 4096");
+    if (!mh_enc_d_supported(d)) return fail("encoder layer: d must be 256 times 1 to 8, 12 or 16");
     if (!mh_attn_supported(d / H)) return fail("head size must be 64 or 128");
     const mynah_asr_hip_weight *sq[] = {L->q_w, L->k_w, L->v_w, L->o_w, L->relk_w, L->pw2_w};
     for (const mynah_asr_hip_weight *w : sq)

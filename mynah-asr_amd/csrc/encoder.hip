@@ -261,7 +261,12 @@ __global__ __launch_bounds__(256) void k_bias_scale(float *__restrict__ y, const
 
 }  // namespace
 
-bool mh_enc_d_supported(int d) { return d > 0 && d % 256 == 0 && d <= 4096; }
+// the widths k_add_ln is instantiated for: 256 V4 with V4 = 1..8, 12, 16
+bool mh_enc_d_supported(int d) {
+    if (d <= 0 || d % 256) return false;
+    const int v = d / 256;
+    return v <= 8 || v == 12 || v == 16;
+}
 
 hipError_t mh_launch_add_ln(float *x, const float *res, float alpha, const float *w, const float *b, float *out,
                             int rows, int d, hipStream_t st) {

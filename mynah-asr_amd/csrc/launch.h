@@ -113,8 +113,8 @@ hipError_t mh_launch_relpos_attn(const float *q, const float *k, const float *v,
                                  const float *bias_u, const float *bias_v, float *ctx, int T, int d, int H,
                                  int left, int right, int nseq, hipStream_t st);
 
-// Encoder layer steps around the products (encoder.hip). d: a multiple of
-// 256 up to 4096 for the layer norm (mh_enc_d_supported), of 4 for the rest.
+// Encoder layer steps around the products (encoder.hip). d: 256 * {1..8, 12,
+// 16} for the layer norm (mh_enc_d_supported), a multiple of 4 for the rest.
 bool mh_enc_d_supported(int d);
 // x += alpha * res (res may be null: no add), then out = LN(x) (w, b) per row;
 // out may be x

@@ -135,6 +135,8 @@ def test_encoder_layer_refuses_bad_shapes(gpu):
             dev.run(x.data_ptr(), T, 1, pe.data_ptr(), d, 1, k, 0)      # dk = 256
         with pytest.raises(RuntimeError, match="q/k/v/o"):
             dev.run(x.data_ptr(), T, 1, pe.data_ptr(), 512, 8, k, 0)    # weights are [256, 256]
+        with pytest.raises(RuntimeError, match="256 times"):
+            dev.run(x.data_ptr(), T, 1, pe.data_ptr(), 2304, 18, k, 0)  # no layer-norm width for 9 x 256
         c = dev.c
         saved, c.cnorm_shift = c.cnorm_shift, None
         with pytest.raises(RuntimeError, match="conv norm"):
