@@ -215,8 +215,10 @@ int mynah_asr_hip_read_floor_dev(const void *p, size_t bytes, void *stream);
  * (head h at columns h*dk .. h*dk+dk-1, dk = d / H, 64 or 128). nseq > 1 runs
  * independent equal-length segments in one launch (the reference calls the
  * layer once per segment). All pointers 16-byte aligned. ctx may not alias
- * q, k or v. Outputs are f32 sums in another order than the reference's BLAS:
- * equal within |y - ref| <= 1e-4*|ref| + 1e-5*max|v|. */
+ * q, k or v. Outputs are f32 sums in another order than the reference's BLAS
+ * (full attention forms its scores from f16 hi + lo splits of each row scaled
+ * by a power of two, 22 bits of the row's maximum): equal within
+ * |y - ref| <= 1e-4*|ref| + 1e-5*max|v|. */
 /* The same on host buffers, one segment (the call encoder.c's attention() and
  * attention_banded() would make in place of their per-head loops, after rk is
  * formed): copies in, computes, copies ctx out. d must be a multiple of 4. */

@@ -1,7 +1,8 @@
 // attention.hip — the relative-position self-attention core of the FastConformer
 // encoder layer (the reference's src/encoder.c:315-410 for full attention and
-// its banded twin encoder.c:220-313 for chunked-limited attention), on fp32
-// MFMA (v_mfma_f32_16x16x4_f32) for gfx950.
+// its banded twin encoder.c:220-313 for chunked-limited attention), on the
+// MFMA of gfx950: fp32 (v_mfma_f32_16x16x4_f32), and for the scores of full
+// attention f16 (v_mfma_f32_16x16x32_f16) on split operands.
 //
 // Per head h (columns h*DK .. h*DK+DK-1 of the [T, d] buffers):
 //   s[t, j] = ((q[t] + bias_u) . k[j] + (q[t] + bias_v) . rk[T-1 + j - t]) / sqrt(DK)
@@ -29,8 +30,17 @@
 //      scores pre-scaled by log2(e)/sqrt(DK)), and
 //   5. multiplies the probabilities (re-laid out as an MFMA A operand through
 //      LDS) by the V tile into its 16 x DK context accumulator.
-// fp32 products and sums throughout: the result is the reference's f32
-// computation up to summation order and the exponential's rounding.
+// fp32 products and sums throughout (SPL = false): the result is the
+// reference's f32 computation up to summation order and the exponential's
+// rounding.
+//
+// SPL = true (full attention) forms the two score products on the f16 MFMA
+// instead. Each q, K and rk row is scaled by a power of two 2^e that puts its
+// largest magnitude in [2^14, 2^15) and split into f16 pairs hi + lo (hi =
+// f16(x 2^e), lo = f16(x 2^e - hi)), which hold x to 2^-22 of the row's
+// maximum; a score is hi.hi + hi.lo + lo.hi summed in f32 (the dropped lo.lo
+// is below 2^-22 of the same scale) and multiplied by 2^-(e_q + e_k), which
+// is exact. The probabilities and the V product stay fp32.
 //
 // MFMA 16x16x4 f32 operand layout (lane l, c = l & 15, g = l >> 4):
 //   A: row c, k-slot g;  B: column c, k-slot g;  D: rows 4g + e (e = 0..3), column c.
@@ -49,24 +59,55 @@ typedef float f2 __attribute__((ext_vector_type(2)));
 
 constexpr int KT = 32;           // keys per tile
 
-// NW waves per workgroup, 16 query rows each
-template <int DK, int NW>
+// NW waves per workgroup, 16 query rows each. SPL: K and the rk ring hold
+// f16 (hi, lo) pairs (rows of KSH halves each, hi rows then lo rows) and
+// each row's scale exponent (EK, ER), in place of f32 rows.
+template <int DK, int NW, bool SPL = false>
 struct AttnLds {
     static constexpr int NTH = 64 * NW;
     static constexpr int RB = 16 * NW;        // query rows per workgroup
     static constexpr int NB = RB + KT - 16;   // rk rows a key tile reads (all waves' position columns): the ring
     static constexpr int KS = DK + 4;   // K / rk row stride (16-byte rows, conflict-free b128 reads)
+    static constexpr int KSH = DK + 8;  // SPL: the same in halves
+    static constexpr int RS = SPL ? KSH : KS;   // floats per K / rk row (SPL: two rows of KSH halves)
     static constexpr int VT = KT + 4;   // V is stored transposed, [DK][VT]: conflict-free b128 reads
     static constexpr int BS = 53;       // band scratch row stride
     static constexpr int PS = 36;       // probability scratch row stride
     static constexpr int K0 = 0;
-    static constexpr int V0 = K0 + KT * KS;
+    static constexpr int V0 = K0 + KT * RS;
     static constexpr int R0 = V0 + DK * VT;
-    static constexpr int W0 = R0 + NB * KS;
+    static constexpr int EK0 = R0 + NB * RS;            // SPL: key rows' exponents, then rk rows'
+    static constexpr int ER0 = EK0 + (SPL ? KT : 0);
+    static constexpr int W0 = (ER0 + (SPL ? NB : 0) + 3) / 4 * 4;
     static constexpr int WB = 16 * BS;
     static constexpr int WSZ = WB;      // the probabilities reuse the band scratch
     static constexpr int TOTAL = W0 + NW * WSZ;   // floats
 };
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f4 mfma16h(h8 a, h8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// The exponent s that puts a row's largest magnitude amax in [2^14, 2^15)
+// (0 for a row of zeros or a non-finite amax: its products are then what
+// f16 makes of them, as the f32 products would be infinite or NaN)
+__device__ __forceinline__ int row_exp(float amax) {
+    if (!(amax > 0.0f) || !(amax < INFINITY)) return 0;
+    int E;
+    (void)frexpf(amax, &E);
+    return min(max(15 - E, -120), 120);
+}
+
+// x * 2^s as an f16 pair: hi = f16(y), lo = f16(y - hi); y - hi is exact in
+// f32, so hi + lo keeps 22 bits of x (the products of the score MFMAs drop
+// only lo * lo, 2^-22 of a term)
+__device__ __forceinline__ void split_h(float x, int s, _Float16 &hi, _Float16 &lo) {
+    const float y = ldexpf(x, s);
+    hi = (_Float16)y;
+    lo = (_Float16)(y - (float)hi);
+}
 
 __device__ __forceinline__ f4 mfma16(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -110,15 +151,17 @@ struct Window {
     __device__ int j1(int t) const { return lim ? min((t / chunk + 1) * chunk, T) : T; }
 };
 
-template <int DK, int NW>
+template <int DK, int NW, bool SPL>
 __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restrict__ q, const float *__restrict__ k,
                                                         const float *__restrict__ v, const float *__restrict__ rk,
                                                         const float *__restrict__ bu, const float *__restrict__ bv,
                                                         float *__restrict__ ctx, int T, int d, int left, int right,
                                                         float kscale) {
-    using L = AttnLds<DK, NW>;
+    using L = AttnLds<DK, NW, SPL>;
     constexpr int NTH = L::NTH, RB = L::RB, NB = L::NB;
-    constexpr int NS = DK / 4;    // reduction steps of a score product
+    constexpr int NS = DK / 4;    // reduction steps of a score product (f32 MFMA)
+    constexpr int NKS = DK / 32;  // SPL: reduction steps of the f16 score MFMAs
+    constexpr int TPR = DK / 4;   // staging threads per K / rk row
     constexpr int NT = DK / 16;   // context column tiles
     extern __shared__ float lds[];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -137,9 +180,60 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     win.T = T;
     const int ja = win.j0(t0), jb = win.j1(min(t0 + RB - 1, T - 1));
 
+    // SPL: (q + bias_u), (q + bias_v) of query row tw + c, features 32 i +
+    // 8 g .. +7 of step i, as f16 pairs scaled by the row's 2^e; the
+    // exponents of this lane's output rows 4 g + e
+    h8 qah[SPL ? NKS : 1], qal[SPL ? NKS : 1], qbh[SPL ? NKS : 1], qbl[SPL ? NKS : 1];
+    int eqa[4], eqb[4];
+    if constexpr (SPL) {
+        const int t = tw + c;
+        float xa[SPL ? DK / 4 : 1], xb[SPL ? DK / 4 : 1];
+        float ma = 0.0f, mb = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NKS; i++)
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                const int f = ho + 32 * i + 8 * g + 4 * hf;
+                f4 u = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
+                if (t < T) {
+                    const f4 x = *(const f4 *)(q + (size_t)t * d + f);
+                    u = x + *(const f4 *)(bu + f);
+                    b = x + *(const f4 *)(bv + f);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    xa[8 * i + 4 * hf + j] = u[j];
+                    xb[8 * i + 4 * hf + j] = b[j];
+                    ma = fmaxf(ma, fabsf(u[j]));
+                    mb = fmaxf(mb, fabsf(b[j]));
+                }
+            }
+        ma = fmaxf(ma, __shfl_xor(ma, 16));
+        ma = fmaxf(ma, __shfl_xor(ma, 32));
+        mb = fmaxf(mb, __shfl_xor(mb, 16));
+        mb = fmaxf(mb, __shfl_xor(mb, 32));
+        const int ea = row_exp(ma), eb = row_exp(mb);
+#pragma unroll
+        for (int i = 0; i < NKS; i++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                _Float16 h, l;
+                split_h(xa[8 * i + j], ea, h, l);
+                qah[i][j] = h;
+                qal[i][j] = l;
+                split_h(xb[8 * i + j], eb, h, l);
+                qbh[i][j] = h;
+                qbl[i][j] = l;
+            }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            eqa[e] = __shfl(ea, 4 * g + e);
+            eqb[e] = __shfl(eb, 4 * g + e);
+        }
+    }
     // (q + bias_u), (q + bias_v) of query row tw + c, features NS*g .. NS*g + NS-1
-    float qa[NS], qb[NS];
-    {
+    float qa[SPL ? 1 : NS], qb[SPL ? 1 : NS];
+    if constexpr (!SPL) {
         const int t = tw + c;
         const int f = ho + NS * g;
 #pragma unroll
@@ -170,6 +264,30 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     for (int n = 0; n < NT; n++) acc[n] = f4{0.f, 0.f, 0.f, 0.f};
 
     float *Ks = lds + L::K0, *Vs = lds + L::V0, *Rs = lds + L::R0;
+    // SPL: the same K and rk rows as f16 pairs and their exponents
+    _Float16 *Kh = (_Float16 *)(lds + L::K0), *Kl = Kh + KT * L::KSH;
+    _Float16 *Rh = (_Float16 *)(lds + L::R0), *Rl = Rh + NB * L::KSH;
+    int *EK = (int *)(lds + L::EK0), *ER = (int *)(lds + L::ER0);
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    // one staging thread's 4 features cc .. cc+3 of row `row` (the TPR threads
+    // of a row are consecutive lanes: the row's maximum is a lane reduction)
+    auto put_row = [&](const f4 &x, int row, int cc, _Float16 *H, _Float16 *Lo, int *E) {
+        float a = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+#pragma unroll
+        for (int o = TPR / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o));
+        const int e = row_exp(a);
+        h4 hv, lv;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            _Float16 hh, ll;
+            split_h(x[j], e, hh, ll);
+            hv[j] = hh;
+            lv[j] = ll;
+        }
+        *(h4 *)(H + row * L::KSH + cc) = hv;
+        *(h4 *)(Lo + row * L::KSH + cc) = lv;
+        if (cc == 0) E[row] = e;
+    };
     float *Bw = lds + L::W0 + w * L::WSZ, *Pw = Bw;
     const int P = 2 * T - 1;
 
@@ -207,7 +325,8 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
 #pragma unroll
         for (int u = 0; u < UKV; u++) {
             const int i = tid + NTH * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
-            *(f4 *)(Ks + r * L::KS + cc) = gk[u];
+            if constexpr (SPL) put_row(gk[u], r, cc, Kh, Kl, EK);
+            else *(f4 *)(Ks + r * L::KS + cc) = gk[u];
             const int rv = i % KT, cv = 4 * (i / KT);
 #pragma unroll
             for (int e = 0; e < 4; e++) Vs[(cv + e) * L::VT + rv] = gv[u][e];
@@ -215,7 +334,9 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
 #pragma unroll
         for (int u = 0; u < UR; u++) {
             const int i = tid + NTH * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
-            *(f4 *)(Rs + ((32 * ti + NB - 32 + r) % NB) * L::KS + cc) = gr[u];
+            const int slot = (32 * ti + NB - 32 + r) % NB;
+            if constexpr (SPL) put_row(gr[u], slot, cc, Rh, Rl, ER);
+            else *(f4 *)(Rs + slot * L::KS + cc) = gr[u];
         }
     };
     // Position columns are computed in tiles of 16 offsets delta = j - t.
@@ -227,6 +348,25 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     // ring slots of this lane's window rows prow + 16n + c at tile ti
     auto rrow = [&](int ti, int n) { return (32 * ti + prow + 16 * n + c) % NB; };
     auto bd_tiles = [&](f4 *bd, int n0) {   // tile 0
+        if constexpr (SPL) {
+#pragma unroll
+            for (int i = 0; i < NKS; i++)
+#pragma unroll
+                for (int n = n0; n < 2; n++) {
+                    const int o = rrow(0, n) * L::KSH + 32 * i + 8 * g;
+                    const h8 rh = *(const h8 *)(Rh + o), rl = *(const h8 *)(Rl + o);
+                    bd[n] = mfma16h(qbh[i], rh, bd[n]);
+                    bd[n] = mfma16h(qbh[i], rl, bd[n]);
+                    bd[n] = mfma16h(qbl[i], rh, bd[n]);
+                }
+#pragma unroll
+            for (int n = n0; n < 2; n++) {
+                const int er = ER[rrow(0, n)];
+#pragma unroll
+                for (int e = 0; e < 4; e++) bd[n][e] = ldexpf(bd[n][e], -(eqb[e] + er));
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < NS / 4; i++) {
             f4 rx[2];
@@ -245,7 +385,9 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
         for (int i = tid; i < NB * DK / 4; i += NTH) {
             const int r = i / (DK / 4), cc = 4 * (i % (DK / 4));
             const int p = min(max(pb0 + r, 0), P - 1);
-            *(f4 *)(Rs + r * L::KS + cc) = *(const f4 *)(rk + (size_t)p * d + ho + cc);
+            const f4 x = *(const f4 *)(rk + (size_t)p * d + ho + cc);
+            if constexpr (SPL) put_row(x, r, cc, Rh, Rl, ER);
+            else *(f4 *)(Rs + r * L::KS + cc) = x;
         }
         __syncthreads();
         f4 bd[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -263,8 +405,43 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
         // 1. content scores (16 rows x 32 keys), 2. position tiles D1, D2
         f4 s[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
         f4 bd[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        if constexpr (SPL) {
+            // three f16 MFMAs per product (hi.hi, hi.lo, lo.hi), then the
+            // rows' scales undone (exact: powers of two)
 #pragma unroll
-        for (int i = 0; i < NS / 4; i++) {
+            for (int i = 0; i < NKS; i++) {
+                h8 kh[2], kl[2], rh[2], rl[2];
+#pragma unroll
+                for (int n = 0; n < 2; n++) {
+                    const int ok = (16 * n + c) * L::KSH + 32 * i + 8 * g;
+                    kh[n] = *(const h8 *)(Kh + ok);
+                    kl[n] = *(const h8 *)(Kl + ok);
+                    const int orr = rrow(ti, n) * L::KSH + 32 * i + 8 * g;
+                    rh[n] = *(const h8 *)(Rh + orr);
+                    rl[n] = *(const h8 *)(Rl + orr);
+                }
+#pragma unroll
+                for (int n = 0; n < 2; n++) {
+                    s[n] = mfma16h(qah[i], kh[n], s[n]);
+                    s[n] = mfma16h(qah[i], kl[n], s[n]);
+                    s[n] = mfma16h(qal[i], kh[n], s[n]);
+                    bd[n] = mfma16h(qbh[i], rh[n], bd[n]);
+                    bd[n] = mfma16h(qbh[i], rl[n], bd[n]);
+                    bd[n] = mfma16h(qbl[i], rh[n], bd[n]);
+                }
+            }
+#pragma unroll
+            for (int n = 0; n < 2; n++) {
+                const int ek = EK[16 * n + c], er = ER[rrow(ti, n)];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    s[n][e] = ldexpf(s[n][e], -(eqa[e] + ek));
+                    bd[n][e] = ldexpf(bd[n][e], -(eqb[e] + er));
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < (SPL ? 0 : NS / 4); i++) {
             f4 kx[2], rx[2];
 #pragma unroll
             for (int n = 0; n < 2; n++) kx[n] = *(const f4 *)(Ks + (16 * n + c) * L::KS + NS * g + 4 * i);
@@ -359,20 +536,20 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     }
 }
 
-template <int DK, int NW>
+template <int DK, int NW, bool SPL>
 hipError_t launch_attn(const float *q, const float *k, const float *v, const float *rk, const float *bu,
-                       const float *bv, float *ctx, int T, int d, int H, int left, int right, int nseq,
-                       hipStream_t st) {
-    using L = AttnLds<DK, NW>;
+                         const float *bv, float *ctx, int T, int d, int H, int left, int right, int nseq,
+                         hipStream_t st) {
+    using L = AttnLds<DK, NW, SPL>;
     const size_t bytes = sizeof(float) * L::TOTAL;
     // set once per instantiation (thread-safe static initialisation)
-    static const hipError_t attr = hipFuncSetAttribute((const void *)k_relpos_attn<DK, NW>,
+    static const hipError_t attr = hipFuncSetAttribute((const void *)k_relpos_attn<DK, NW, SPL>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
     if (attr != hipSuccess) return attr;
     // exponentials are base 2: scores carry log2(e) / sqrt(DK)
     const float kscale = (1.0f / sqrtf((float)DK)) * 1.4426950408889634f;
     dim3 grid((T + L::RB - 1) / L::RB, H, nseq);
-    hipLaunchKernelGGL((k_relpos_attn<DK, NW>), grid, dim3(L::NTH), bytes, st, q, k, v, rk, bu, bv, ctx, T, d,
+    hipLaunchKernelGGL((k_relpos_attn<DK, NW, SPL>), grid, dim3(L::NTH), bytes, st, q, k, v, rk, bu, bv, ctx, T, d,
                        left, right, kscale);
     return hipGetLastError();
 }
@@ -390,9 +567,13 @@ template <int DK>
 hipError_t launch_dk(const float *q, const float *k, const float *v, const float *rk, const float *bu,
                      const float *bv, float *ctx, int T, int d, int H, int left, int right, int nseq,
                      hipStream_t st) {
-    if (use8(T, H, left, nseq)) return launch_attn<DK, 8>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, st);
-    if (left >= 0) return launch_attn<DK, 2>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, st);
-    return launch_attn<DK, 4>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, st);
+    // Full attention computes its scores on the f16 MFMA from split operands
+    // (18% faster at T = 750); chunked windows stage as many K / rk rows per
+    // score they keep, so the splitting costs more than it saves there.
+    if (use8(T, H, left, nseq))
+        return launch_attn<DK, 8, true>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, st);
+    if (left >= 0) return launch_attn<DK, 2, false>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, st);
+    return launch_attn<DK, 4, true>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, st);
 }
 
 }  // namespace

@@ -4,8 +4,10 @@ of src/encoder.c:315-410 (full) and :220-313 (chunked-limited).
 
 Bar: |ctx - ref| <= 1e-4*|ref| + 1e-5*max|v| per element. The kernel computes
 in f32 like the reference, with another summation order and base-2
-exponentials, so a context element near zero (a cancelling weighted sum of v)
-carries an absolute error of order 1e-6 * max|v| — the scale term covers that.
+exponentials (full attention forms its scores from f16 hi + lo splits of
+row-scaled operands, 22 bits of each row's maximum), so a context element near
+zero (a cancelling weighted sum of v) carries an absolute error of order
+1e-6 * max|v| — the scale term covers that.
 Inputs: q, k, v, rk N(0, 1) and bias_u, bias_v N(0, 0.1), seeded.
 """
 import sys
@@ -90,6 +92,27 @@ def test_relpos_attention_many_segments(gpu, d):
     arrs = make(21 + d, T, d, nseq)
     out = run_gpu(gpu, arrs, T, d, H, -1, 0, nseq)
     check(out, arrs, H, -1, 0)
+
+
+@pytest.mark.parametrize("left,right", [(-1, 0), (1000, 299)])
+def test_relpos_attention_wide_row_scales(gpu, left, right):
+    """Rows of q, k and rk scaled by 2^-30 .. 2^30, rows of zeros, and rows
+    with one feature 1e4 times the rest: the split scores carry each row's own
+    scale, so the bar holds as for N(0, 1) rows (full attention on the split
+    path, and the one-chunk window, the same scores on the f32 path)."""
+    T, d, H = 150, 256, 2
+    r = np.random.default_rng(77)
+    q, k, v, rk, bu, bv = make(41, T, d, 1)
+    for a, n in ((q[0], T), (k[0], T), (rk, 2 * T - 1)):
+        a *= np.exp2(r.integers(-30, 31, size=(n, 1))).astype(np.float32)
+        a[r.integers(0, n, size=5)] = 0.0
+        a[r.integers(0, n, size=5), r.integers(0, d, size=5)] *= 1e4
+    bu[:] = 0.0
+    bv[:] = 0.0
+    say("attention wide row scales", left, right)
+    arrs = (q, k, v, rk, bu, bv)
+    out = run_gpu(gpu, arrs, T, d, H, left, right, 1)
+    check(out, arrs, H, left, right)
 
 
 def test_relpos_attention_segments_independent(gpu):
