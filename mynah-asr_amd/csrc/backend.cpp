@@ -891,9 +891,9 @@ int subsampling_dev(Ctx *c, const mynah_asr_hip_subsampling *ss, const float *fe
     *t_out = T3;
     if (T3 <= 0 || F3 <= 0) return fail("subsampling: input too short for three stride-2 stages");
     if (ss->lin_w->dw.k != C * F3) return fail("subsampling: lin_w must be [d_model, channels * F']");
-    // A holds the stage-0 output, then the pointwise outputs; B the depthwise
-    // outputs, then the flattened rows
-    const size_t a = (size_t)nseq * T1 * F1 * C, b = (size_t)nseq * T2 * F2 * C, tw = (size_t)27 * C;
+    // A holds the pointwise outputs; B the depthwise outputs, then the
+    // flattened rows (the first conv's output is never stored)
+    const size_t a = (size_t)nseq * T2 * F2 * C, b = a, tw = (size_t)27 * C;
     float *A = (float *)c->ssb.get((a + b + tw) * sizeof(float));
     if (!A) return fail("device buffer allocation failed");
     float *B = A + a, *w0 = B + b, *w1 = w0 + 9 * (size_t)C, *w2 = w1 + 9 * (size_t)C;   // taps tap-major
@@ -907,8 +907,7 @@ int subsampling_dev(Ctx *c, const mynah_asr_hip_subsampling *ss, const float *fe
     SS_TRY(mh_launch_transpose_taps(ss->conv_in_w, w0, C, 9, st));
     SS_TRY(mh_launch_transpose_taps(ss->dw_w[0], w1, C, 9, st));
     SS_TRY(mh_launch_transpose_taps(ss->dw_w[1], w2, C, 9, st));
-    SS_TRY(mh_launch_conv_in(feats, w0, ss->conv_in_b, A, nseq, T, F, C, cz, st));
-    SS_TRY(mh_launch_dw_s2(A, nullptr, w1, ss->dw_b[0], B, nseq, T1, F1, C, cz, st));
+    SS_TRY(mh_launch_conv_in_dw(feats, w0, ss->conv_in_b, w1, ss->dw_b[0], B, nseq, T, F, C, cz, st));
     if (gemm_dev(c, ss->pw_w[0], B, A, nseq * T2 * F2, 0, st)) return -1;
     SS_TRY(mh_launch_dw_s2(A, ss->pw_b[0], w2, ss->dw_b[1], B, nseq, T2, F2, C, cz, st));
     if (gemm_dev(c, ss->pw_w[1], B, A, nseq * T3 * F3, 0, st)) return -1;

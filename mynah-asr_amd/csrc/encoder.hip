@@ -15,10 +15,11 @@
 // (src/subsampling.c:208-268, 109-200), with activations channel-last,
 // [segment][time][freq][channel], so that its pointwise convolutions and its
 // final linear are this unit's products:
-//   k_conv_in   the full 3x3 stride-2 conv of the mel features, 1 -> C
-//               channels, + bias, ReLU                            :222-226
-//   k_dw_s2     the depthwise 3x3 stride-2 conv, + bias; its input may take
-//               the previous pointwise conv's bias and ReLU on load  :231-244
+//   k_conv_in_dw  the full 3x3 stride-2 conv of the mel features, 1 -> C
+//               channels, + bias, ReLU (:222-226), fused into the first
+//               depthwise 3x3 stride-2 conv, + bias (:231-236)
+//   k_dw_s2     the depthwise 3x3 stride-2 conv, + bias; its input takes
+//               the previous pointwise conv's bias and ReLU on load  :237-244
 //   k_flatten   the last pointwise conv's bias and ReLU, then the
 //               channel-major flatten [t][c * F' + f] of :249-257
 #include <hip/hip_runtime.h>
@@ -143,39 +144,85 @@ __global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ g, con
     *(float4 *)(out + (size_t)row * d + i) = o;
 }
 
-// out[s][to][fo][c] = relu(b[c] + sum_{dt, df} w[c][3 dt + df] x[s][2 to - pl + dt][2 fo - pl + df])
-// with zeros outside [0, T) x [0, F). Thread = (row (s, to, fo), 4 channels);
-// the weights tap-major, wt[j][c].
-__global__ __launch_bounds__(256) void k_conv_in(const float *__restrict__ x, const float *__restrict__ wt,
-                                                 const float *__restrict__ b, float *__restrict__ out, int nseq,
-                                                 int T, int F, int To, int Fo, int C, int pl) {
-    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const int C4 = C / 4;
-    if (idx >= (size_t)nseq * To * Fo * C4) return;
-    const size_t row = idx / C4;
-    const int c = 4 * (int)(idx - row * C4);
-    const int fo = (int)(row % Fo), to = (int)((row / Fo) % To), s = (int)(row / ((size_t)Fo * To));
+// The first two stages in one pass: out[s][to][fo][c] = the depthwise 3x3
+// stride-2 conv (+ b1) of y = relu(conv_in(x) + b0), the 1 -> C 3x3 stride-2
+// conv of the mel features (subsampling.c:222-226, 231-236). y is formed
+// where a depthwise tap reads it and never stored (at config 5 it would be
+// 2 GB written and read back). Per tap the operations are those of the
+// conv alone (nine fmas from zero in tap order, + b0, ReLU) and of the
+// depthwise conv (a product, then eight fmas, + b1 last); a tap outside
+// y's [T1, F1] reads zero (the depthwise conv's pad), and a mel sample
+// outside [T, F] reads zero (the first conv's pad).
+//
+// One wave per output row (s, to), its lanes over the channels 4 at a time,
+// sliding along fo: the 3 x 3 window of y a depthwise output reads stays in
+// registers, and each step forms y's two new columns (y column 2 of one
+// step is column 0 of the next). The mel samples are wave-uniform and read
+// through the scalar cache; each lane holds its channels' 2 x 9 taps.
+// Weights tap-major, w0[j][C] and w1[j][C].
+__global__ __launch_bounds__(256) void k_conv_in_dw(const float *__restrict__ x, const float *__restrict__ w0,
+                                                    const float *__restrict__ b0, const float *__restrict__ w1,
+                                                    const float *__restrict__ b1, float *__restrict__ out, int nseq,
+                                                    int T, int F, int T1, int F1, int To, int Fo, int C, int pl) {
+    const int wrow = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
+    if (wrow >= nseq * To) return;
+    const int lane = threadIdx.x & 63;
+    const int to = wrow % To, s = wrow / To;
     const float *xs = x + (size_t)s * T * F;
-    float v[9];
+    for (int c = 4 * lane; c < C; c += 256) {
+        float4 wa[9], wb[9];
 #pragma unroll
-    for (int dt = 0; dt < 3; dt++)
-#pragma unroll
-        for (int df = 0; df < 3; df++) {
-            const int t = 2 * to - pl + dt, f = 2 * fo - pl + df;
-            v[3 * dt + df] = t >= 0 && t < T && f >= 0 && f < F ? xs[(size_t)t * F + f] : 0.0f;
+        for (int j = 0; j < 9; j++) {
+            wa[j] = *(const float4 *)(w0 + (size_t)j * C + c);
+            wb[j] = *(const float4 *)(w1 + (size_t)j * C + c);
         }
-    float4 acc = {0.f, 0.f, 0.f, 0.f};
+        const float4 bb0 = *(const float4 *)(b0 + c), bb1 = *(const float4 *)(b1 + c);
+        // y at (t1 = 2 to - pl + r, f1): relu(b0 + conv_in), zero outside [T1, F1]
+        auto yat = [&](int r, int f1) {
+            const int t1 = 2 * to - pl + r;
+            float4 y = {0.f, 0.f, 0.f, 0.f};
+            if (t1 >= 0 && t1 < T1 && f1 >= 0 && f1 < F1) {
+                float4 ci = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 9; j++) {
-        const float4 wv = *(const float4 *)(wt + (size_t)j * C + c);
-        acc.x = fmaf(wv.x, v[j], acc.x);
-        acc.y = fmaf(wv.y, v[j], acc.y);
-        acc.z = fmaf(wv.z, v[j], acc.z);
-        acc.w = fmaf(wv.w, v[j], acc.w);
+                for (int dt = 0; dt < 3; dt++)
+#pragma unroll
+                    for (int df = 0; df < 3; df++) {
+                        const int t = 2 * t1 - pl + dt, f = 2 * f1 - pl + df;
+                        const float v = t >= 0 && t < T && f >= 0 && f < F ? xs[(size_t)t * F + f] : 0.0f;
+                        const float4 wv = wa[3 * dt + df];
+                        ci.x = fmaf(wv.x, v, ci.x);
+                        ci.y = fmaf(wv.y, v, ci.y);
+                        ci.z = fmaf(wv.z, v, ci.z);
+                        ci.w = fmaf(wv.w, v, ci.w);
+                    }
+                y = float4{fmaxf(ci.x + bb0.x, 0.0f), fmaxf(ci.y + bb0.y, 0.0f), fmaxf(ci.z + bb0.z, 0.0f),
+                           fmaxf(ci.w + bb0.w, 0.0f)};
+            }
+            return y;
+        };
+        float4 yw[3][3];
+#pragma unroll
+        for (int r = 0; r < 3; r++) yw[r][2] = yat(r, -pl);
+        for (int fo = 0; fo < Fo; fo++) {
+#pragma unroll
+            for (int r = 0; r < 3; r++) {
+                yw[r][0] = yw[r][2];
+                yw[r][1] = yat(r, 2 * fo - pl + 1);
+                yw[r][2] = yat(r, 2 * fo - pl + 2);
+            }
+            float4 acc = {wb[0].x * yw[0][0].x, wb[0].y * yw[0][0].y, wb[0].z * yw[0][0].z, wb[0].w * yw[0][0].w};
+#pragma unroll
+            for (int j = 1; j < 9; j++) {
+                const float4 wv = wb[j], y = yw[j / 3][j % 3];
+                acc.x = fmaf(wv.x, y.x, acc.x);
+                acc.y = fmaf(wv.y, y.y, acc.y);
+                acc.z = fmaf(wv.z, y.z, acc.z);
+                acc.w = fmaf(wv.w, y.w, acc.w);
+            }
+            *(float4 *)(out + ((size_t)wrow * Fo + fo) * C + c) =
+                float4{bb1.x + acc.x, bb1.y + acc.y, bb1.z + acc.z, bb1.w + acc.w};
+        }
     }
-    const float4 bb = *(const float4 *)(b + c);
-    *(float4 *)(out + row * C + c) = float4{fmaxf(acc.x + bb.x, 0.0f), fmaxf(acc.y + bb.y, 0.0f),
-                                            fmaxf(acc.z + bb.z, 0.0f), fmaxf(acc.w + bb.w, 0.0f)};
 }
 
 // out[s][to][fo][c] = b[c] + sum w[c][3 dt + df] in[s][2 to - pl + dt][2 fo - pl + df][c],
@@ -315,14 +362,17 @@ int mh_ss_out_len(int n, int causal) {
     return (n + p - 3) / 2 + 1;
 }
 
-hipError_t mh_launch_conv_in(const float *x, const float *w, const float *b, float *out, int nseq, int T, int F,
-                             int C, int causal, hipStream_t st) {
+hipError_t mh_launch_conv_in_dw(const float *x, const float *w0, const float *b0, const float *w1, const float *b1,
+                                float *out, int nseq, int T, int F, int C, int causal, hipStream_t st) {
     if (C % 4) return hipErrorInvalidValue;
-    const int To = mh_ss_out_len(T, causal), Fo = mh_ss_out_len(F, causal);
-    const size_t n = (size_t)nseq * To * Fo * (C / 4);
-    if (!n) return hipSuccess;
-    hipLaunchKernelGGL(k_conv_in, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, w, b, out, nseq, T, F, To, Fo,
-                       C, causal ? 2 : 1);
+    const int T1 = mh_ss_out_len(T, causal), F1 = mh_ss_out_len(F, causal);
+    const int To = mh_ss_out_len(T1, causal), Fo = mh_ss_out_len(F1, causal);
+    if (T1 <= 0 || F1 <= 0 || To <= 0 || Fo <= 0) return hipSuccess;
+    const size_t rows = (size_t)nseq * To;   // one wave per output row (s, to)
+    if (!rows) return hipSuccess;
+    if (rows > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_conv_in_dw, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, x, w0, b0, w1, b1, out, nseq,
+                       T, F, T1, F1, To, Fo, C, causal ? 2 : 1);
     return hipGetLastError();
 }
 

@@ -134,14 +134,16 @@ hipError_t mh_launch_dwconv(const float *g, const float *w, const float *bias, c
 // [segment][time][freq][channel] (C a multiple of 4); causal pads (2, 1),
 // else (1, 1), in time and frequency alike.
 int mh_ss_out_len(int n, int causal);   // the length after one stride-2 stage
-hipError_t mh_launch_conv_in(const float *x, const float *w, const float *b, float *out, int nseq, int T, int F,
-                             int C, int causal, hipStream_t st);
+// the first conv (1 -> C, + b0, ReLU) and the first depthwise conv (+ b1) in
+// one pass: x [nseq][T][F] -> out [nseq][T2][F2][C]
+hipError_t mh_launch_conv_in_dw(const float *x, const float *w0, const float *b0, const float *w1, const float *b1,
+                                float *out, int nseq, int T, int F, int C, int causal, hipStream_t st);
 // pb (or null): the previous pointwise conv's bias, applied with ReLU on load
 hipError_t mh_launch_dw_s2(const float *in, const float *pb, const float *w, const float *b, float *out, int nseq,
                            int T, int F, int C, int causal, hipStream_t st);
 hipError_t mh_launch_flatten(const float *in, const float *pb, float *flat, size_t rows, int Fo, int C,
                              hipStream_t st);
-// wt [k][C] = the taps of w [C][k] tap-major (the layout k_dwconv, k_conv_in
+// wt [k][C] = the taps of w [C][k] tap-major (the layout k_dwconv, k_conv_in_dw
 // and k_dw_s2 read: w, the argument of their launchers, is this copy)
 hipError_t mh_launch_transpose_taps(const float *w, float *wt, int C, int k, hipStream_t st);
 // y = (y + b) * scale per row (scale 1: the bias alone)
