@@ -92,6 +92,10 @@ struct DBuf {
 struct PrepBuf {
     DBuf xp, xs16, xpf;
     int T = -1, Kp = 0, xsum = 0, i8 = 0;
+    // non-null: the activations whose EXACT preparation (no row sums) these
+    // buffers hold, written by the layer norm that produced them in place
+    // of f32 rows; a preparation of those activations is then skipped
+    const void *src = nullptr;
 };
 
 struct Ctx {
@@ -244,6 +248,9 @@ hipError_t launch_prep(int kind, const mynah_asr_hip_weight *W, const float *dx,
 int prep_into(PrepBuf &P, const mynah_asr_hip_weight *W, const float *dx, int T, hipStream_t st) {
     const int Mpad = mh_mpad(T), Kp = W->dw.Kp;
     const int kind = prep_kind(W->qtype);
+    if (P.src && P.src == dx && kind == 0 && !wants_xsum(W->qtype) && P.T == T && P.Kp == Kp && P.i8 == 0)
+        return 0;
+    P.src = nullptr;
     size_t b[3];
     prep_sizes(kind, Mpad, Kp, b);
     uint8_t *xp = (uint8_t *)P.xp.get(b[0]);
@@ -808,9 +815,57 @@ int enc_half_ffn(Ctx *c, const mynah_asr_hip_weight *w1, const mynah_asr_hip_wei
     return bias_add(out, b2, M, w2->dw.n, st);
 }
 
+// Whether the products W[0..n) of one layer-norm output xn all read it as
+// the EXACT GEMM path's prepared input (no GEMV, no row sums, K = Kp = d):
+// then the layer norm writes that input directly.
+// MYNAH_ASR_HIP_LN_PREP=0 turns this off (f32 rows, then the products'
+// own preparation: the same bits, one more pass).
+bool ln_preps(const mynah_asr_hip_weight *const *W, int n, int M, int d) {
+    const char *env = getenv("MYNAH_ASR_HIP_LN_PREP");
+    if ((env && env[0] == '0') || !mh_add_ln_prep_supported(d)) return false;
+    for (int i = 0; i < n; i++)
+        if (eff_num(W[i]->qtype, W[i]->dw.k, M) != MYNAH_ASR_HIP_EXACT || mh_use_gemv(W[i]->dw, M) ||
+            wants_xsum(W[i]->qtype) || W[i]->dw.k != d || W[i]->dw.Kp != d)
+            return false;
+    return true;
+}
+
+// xn = LN(x += alpha res) for the products W[0..n): as their prepared input
+// (c->pa, tagged xn; xn itself is then not written) when ln_preps allows,
+// else as f32 rows
+int enc_add_ln(Ctx *c, float *x, const float *res, float alpha, const float *w, const float *b, float *xn, int M,
+               int d, const mynah_asr_hip_weight *const *W, int n, hipStream_t st) {
+    hipError_t e;
+    c->pa.src = nullptr;
+    if (ln_preps(W, n, M, d)) {
+        const int Mpad = mh_mpad(M);
+        size_t bs[3];
+        prep_sizes(0, Mpad, d, bs);
+        uint8_t *xp = (uint8_t *)c->pa.xp.get(bs[0]);
+        float *xs16 = (float *)c->pa.xs16.get(bs[1]);
+        float *xpf = (float *)c->pa.xpf.get(bs[2]);
+        if (!xp || !xs16 || !xpf) return fail("workspace allocation failed");
+        e = mh_launch_add_ln_prep(x, res, alpha, w, b, M, d, xp, xpf, st);
+        if (e != hipSuccess) return fail("encoder layer launch failed", hipGetErrorString(e));
+        c->pa.T = M;
+        c->pa.Kp = d;
+        c->pa.xsum = 0;
+        c->pa.i8 = 0;
+        c->pa.src = xn;
+        return 0;
+    }
+    e = mh_launch_add_ln(x, res, alpha, w, b, xn, M, d, st);
+    return e == hipSuccess ? 0 : fail("encoder layer launch failed", hipGetErrorString(e));
+}
+
 int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T, int nseq, const float *pe, int d,
                       int H, int conv_k, int causal, int left, int right, hipStream_t st) {
     const int M = T * nseq, P = 2 * T - 1;
+    // the prepared-input tag never outlives this call (an error return included)
+    struct TagClear {
+        PrepBuf &pa;
+        ~TagClear() { pa.src = nullptr; }
+    } tag_clear{c->pa};
     const int f = L->ff1_w1->dw.n > L->ff2_w1->dw.n ? L->ff1_w1->dw.n : L->ff2_w1->dw.n;
     const bool biased_ffn = L->ff1_b1 || L->ff1_b2 || L->ff2_b1 || L->ff2_b2;
     const size_t md = (size_t)M * d;
@@ -829,13 +884,17 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
         if (e != hipSuccess) return fail("encoder layer launch failed", hipGetErrorString(e)); \
     } while (0)
     // 1/2 FFN1 (:492-494)
-    ENC_TRY(mh_launch_add_ln(x, nullptr, 0.0f, L->ln_ff1_w, L->ln_ff1_b, xn, M, d, st));
+    // (each layer norm whose output only feeds products tags the prepared
+    // input with xn; the tag is cleared once those products have run)
+    if (enc_add_ln(c, x, nullptr, 0.0f, L->ln_ff1_w, L->ln_ff1_b, xn, M, d, &L->ff1_w1, 1, st)) return -1;
     if (enc_half_ffn(c, L->ff1_w1, L->ff1_w2, L->ff1_b1, L->ff1_b2, xn, tmp, hf, M, st)) return -1;
+    c->pa.src = nullptr;
     // x += 0.5 tmp; MHSA on LN(x) (:495-502)
-    ENC_TRY(mh_launch_add_ln(x, tmp, 0.5f, L->ln_att_w, L->ln_att_b, xn, M, d, st));
     const mynah_asr_hip_weight *W3[3] = {L->q_w, L->k_w, L->v_w};
+    if (enc_add_ln(c, x, tmp, 0.5f, L->ln_att_w, L->ln_att_b, xn, M, d, W3, 3, st)) return -1;
     float *const y3[3] = {q, k, v};
     if (qkv_dev(c, W3, xn, y3, M, st)) return -1;
+    c->pa.src = nullptr;
     if (bias_add(q, L->q_b, M, d, st) || bias_add(k, L->k_b, M, d, st) || bias_add(v, L->v_b, M, d, st)) return -1;
     {
         // rk = pe . relk^T (:336): the segments share T, so one product serves
@@ -851,11 +910,12 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
     }
     if (bias_add(tmp, L->o_b, M, d, st)) return -1;
     // x += tmp; conv module on LN(x) (:503-507, 413-462)
-    ENC_TRY(mh_launch_add_ln(x, tmp, 1.0f, L->ln_conv_w, L->ln_conv_b, xn, M, d, st));
+    if (enc_add_ln(c, x, tmp, 1.0f, L->ln_conv_w, L->ln_conv_b, xn, M, d, &L->pw1_w, 1, st)) return -1;
     {
         NumScope s1(eff_num(L->pw1_w->qtype, d, M));
         if (gemm_dev(c, L->pw1_w, xn, h, M, 0, st)) return -1;
     }
+    c->pa.src = nullptr;
     if (bias_add(h, L->pw1_b, M, 2 * d, st)) return -1;
     ENC_TRY(mh_launch_glu(h, q, M, d, st));   // g (q is free now)
     ENC_TRY(mh_launch_transpose_taps(L->dw_w, dwt, d, conv_k, st));
@@ -872,8 +932,9 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
     }
     if (bias_add(tmp, L->pw2_b, M, d, st)) return -1;
     // x += tmp; 1/2 FFN2 on LN(x) (:508-511)
-    ENC_TRY(mh_launch_add_ln(x, tmp, 1.0f, L->ln_ff2_w, L->ln_ff2_b, xn, M, d, st));
+    if (enc_add_ln(c, x, tmp, 1.0f, L->ln_ff2_w, L->ln_ff2_b, xn, M, d, &L->ff2_w1, 1, st)) return -1;
     if (enc_half_ffn(c, L->ff2_w1, L->ff2_w2, L->ff2_b1, L->ff2_b2, xn, tmp, hf, M, st)) return -1;
+    c->pa.src = nullptr;
     // x += 0.5 tmp; x = LN_out(x) (:511-515)
     ENC_TRY(mh_launch_add_ln(x, tmp, 0.5f, L->ln_out_w, L->ln_out_b, x, M, d, st));
 #undef ENC_TRY

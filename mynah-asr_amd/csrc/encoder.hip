@@ -26,6 +26,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include "fmt.h"
 #include "launch.h"
 
 namespace {
@@ -38,18 +39,16 @@ __device__ __forceinline__ float sigmoid_f(float x) {
 }
 
 // One wave per row of d = 256 V4 floats (lane l holds elements 4l + 256u ..
-// +3). Sums in double in two passes, as layer_norm_f: mean, then the sum of
-// (x - mean)^2; inv = (float)(1 / sqrt(var + 1e-5)); out = ((x - (float)mean)
-// * inv) * w + b in f32. out may be x.
+// +3): x += alpha res (stored; res may be null), then the layer norm into
+// v. Sums in double in two passes, as layer_norm_f: mean, then the sum of
+// (x - mean)^2; inv = (float)(1 / sqrt(var + 1e-5)); v = ((x - (float)mean)
+// * inv) * w + b in f32.
 template <int V4>
-__global__ __launch_bounds__(256) void k_add_ln(float *x, const float *__restrict__ res, float alpha,
-                                                const float *__restrict__ w, const float *__restrict__ b,
-                                                float *out, int rows) {
+__device__ __forceinline__ void add_ln_row(float *xr, const float *__restrict__ rr, float alpha,
+                                           const float *__restrict__ w, const float *__restrict__ b, int lane,
+                                           float4 (&v)[V4]) {
     constexpr int d = 256 * V4;
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (r >= rows) return;
-    float *xr = x + (size_t)r * d;
-    float4 v[V4], wv[V4], bv[V4];
+    float4 wv[V4], bv[V4];
 #pragma unroll
     for (int u = 0; u < V4; u++) {
         const int i = 4 * lane + 256 * u;
@@ -57,8 +56,7 @@ __global__ __launch_bounds__(256) void k_add_ln(float *x, const float *__restric
         wv[u] = *(const float4 *)(w + i);
         bv[u] = *(const float4 *)(b + i);
     }
-    if (res) {
-        const float *rr = res + (size_t)r * d;
+    if (rr) {
 #pragma unroll
         for (int u = 0; u < V4; u++) {
             const float4 a = *(const float4 *)(rr + 4 * lane + 256 * u);
@@ -84,15 +82,93 @@ __global__ __launch_bounds__(256) void k_add_ln(float *x, const float *__restric
     for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
     const float inv = (float)(1.0 / sqrt(q / d + 1e-5));
     const float muf = (float)mu;
-    float *orow = out + (size_t)r * d;
 #pragma unroll
     for (int u = 0; u < V4; u++) {
-        float4 o;
-        o.x = ((v[u].x - muf) * inv) * wv[u].x + bv[u].x;
-        o.y = ((v[u].y - muf) * inv) * wv[u].y + bv[u].y;
-        o.z = ((v[u].z - muf) * inv) * wv[u].z + bv[u].z;
-        o.w = ((v[u].w - muf) * inv) * wv[u].w + bv[u].w;
-        *(float4 *)(orow + 4 * lane + 256 * u) = o;
+        v[u].x = ((v[u].x - muf) * inv) * wv[u].x + bv[u].x;
+        v[u].y = ((v[u].y - muf) * inv) * wv[u].y + bv[u].y;
+        v[u].z = ((v[u].z - muf) * inv) * wv[u].z + bv[u].z;
+        v[u].w = ((v[u].w - muf) * inv) * wv[u].w + bv[u].w;
+    }
+}
+
+// out = LN(x += alpha res), one wave per row. out may be x.
+template <int V4>
+__global__ __launch_bounds__(256) void k_add_ln(float *x, const float *__restrict__ res, float alpha,
+                                                const float *__restrict__ w, const float *__restrict__ b,
+                                                float *out, int rows) {
+    constexpr int d = 256 * V4;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    float4 v[V4];
+    add_ln_row<V4>(x + (size_t)r * d, res ? res + (size_t)r * d : nullptr, alpha, w, b, lane, v);
+    float *orow = out + (size_t)r * d;
+#pragma unroll
+    for (int u = 0; u < V4; u++) *(float4 *)(orow + 4 * lane + 256 * u) = v[u];
+}
+
+// LN(x += alpha res) as the products' prepared input in EXACT numerics, in
+// place of the f32 rows: the split of each row's 128-element chunks that the
+// products' preparation forms (the same values: shift sh from the chunk's
+// largest magnitude, hi = f16(v 2^sh), lo = f16(v 2^sh - hi), fold factor
+// 2^-sh), in its layout
+//   xp   [row group G][chunk][half-step u][hi, lo][64 slots][16 B], slot r + 32 hh
+//        holding chunk elements 16u + 8hh .. +7 of row 32G + r
+//   xpf  [G][chunk][32]
+// Lane l's float4 u is chunk 2u + l / 32, elements 4 (l % 32) .. +3: half-step
+// (l % 32) / 4, half hh = (l / 2) % 2, the 8-byte half l % 2 of the slot. A
+// workgroup holds 8 consecutive rows (8 waves): for each (chunk, half-step,
+// term, hh) their slots are one 128-byte line of xp. The pieces go to LDS
+// first, in that line order, so that the stores to xp are whole lines (a
+// wave's store covers 8 of them). Rows rows .. Mpad-1 are the zero rows the
+// preparation pads with (fold factor 1).
+template <int V4>
+__global__ __launch_bounds__(512) void k_add_ln_prep(float *x, const float *__restrict__ res, float alpha,
+                                                     const float *__restrict__ w, const float *__restrict__ b,
+                                                     int rows, uint8_t *__restrict__ xp, float *__restrict__ xpf) {
+    constexpr int d = 256 * V4, Kc = d / 128, NL = Kc * 32;   // lines of the workgroup
+    __shared__ uint4 stage[NL * 8];
+    const int wave = threadIdx.x >> 6, m = blockIdx.x * 8 + wave, lane = threadIdx.x & 63;
+    const int G = m >> 5, r = m & 31, l32 = lane & 31;
+    float4 v[V4];
+    if (m < rows) {
+        add_ln_row<V4>(x + (size_t)m * d, res ? res + (size_t)m * d : nullptr, alpha, w, b, lane, v);
+    } else {
+#pragma unroll
+        for (int u = 0; u < V4; u++) v[u] = float4{0.f, 0.f, 0.f, 0.f};
+    }
+    const int hu = l32 >> 2, hh = (l32 >> 1) & 1;
+#pragma unroll
+    for (int u = 0; u < V4; u++) {
+        const int c = 2 * u + (lane >> 5);
+        float a = fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w)));
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+        const int sh = chunk_shift(a);
+        const float xs[4] = {ldexpf(v[u].x, sh), ldexpf(v[u].y, sh), ldexpf(v[u].z, sh), ldexpf(v[u].w, sh)};
+        _Float16 hv[4], lv[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            hv[j] = (_Float16)xs[j];
+            lv[j] = (_Float16)(xs[j] - (float)hv[j]);
+        }
+        uint2 hw, lw;
+        __builtin_memcpy(&hw, hv, 8);
+        __builtin_memcpy(&lw, lv, 8);
+        // line ((c * 8 + hu) * 2 + term) * 2 + hh, slot wave (the row within the 8)
+        uint8_t *o = (uint8_t *)stage + (((((c * 8 + hu) * 2) * 2 + hh) * 8 + wave) * 16 + 8 * (lane & 1));
+        *(uint2 *)o = hw;
+        *(uint2 *)(o + 2 * 8 * 16) = lw;
+        if (l32 == 0) xpf[((size_t)G * Kc + c) * 32 + r] = ldexpf(1.0f, -sh);
+    }
+    __syncthreads();
+    // line L = (q * 2 + hh), q = (c * 8 + hu) * 2 + term, lies at xp offset
+    // (G * Kc * 16 + q) * 1024 + hh * 512 + (8-row block) * 128
+    const int rb = (blockIdx.x & 3) * 128;
+    uint8_t *gx = xp + (size_t)(blockIdx.x >> 2) * Kc * 16 * 1024 + rb;
+#pragma unroll
+    for (int i = threadIdx.x; i < NL * 8; i += 512) {
+        const int L = i >> 3, sl = i & 7;
+        *(uint4 *)(gx + (size_t)(L >> 1) * 1024 + (L & 1) * 512 + sl * 16) = stage[i];
     }
 }
 
@@ -331,6 +407,24 @@ hipError_t mh_launch_add_ln(float *x, const float *res, float alpha, const float
     case 8: hipLaunchKernelGGL(k_add_ln<8>, grid, blk, 0, st, x, res, alpha, w, b, out, rows); break;
     case 12: hipLaunchKernelGGL(k_add_ln<12>, grid, blk, 0, st, x, res, alpha, w, b, out, rows); break;
     case 16: hipLaunchKernelGGL(k_add_ln<16>, grid, blk, 0, st, x, res, alpha, w, b, out, rows); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// d = 256 .. 2048 (wider rows would spill at two waves per SIMD)
+bool mh_add_ln_prep_supported(int d) { return d > 0 && d % 256 == 0 && d / 256 <= 8; }
+
+hipError_t mh_launch_add_ln_prep(float *x, const float *res, float alpha, const float *w, const float *b, int rows,
+                                 int d, uint8_t *xp, float *xpf, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (!mh_add_ln_prep_supported(d)) return hipErrorInvalidValue;
+    const dim3 grid(mh_mpad(rows) / 8), blk(512);
+    switch (d / 256) {
+#define LNP(V) \
+    case V: hipLaunchKernelGGL(k_add_ln_prep<V>, grid, blk, 0, st, x, res, alpha, w, b, rows, xp, xpf); break;
+    LNP(1) LNP(2) LNP(3) LNP(4) LNP(5) LNP(6) LNP(7) LNP(8)
+#undef LNP
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

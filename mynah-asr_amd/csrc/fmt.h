@@ -59,6 +59,15 @@ struct DevW {
     int Np, Kp;          // padded: Np multiple of 128, Kp multiple of 256
 };
 
+// The activation split's chunk shift (the products' preparation, and the
+// layer norm that prepares its output for them): sh puts the chunk's largest
+// magnitude in [2^14, 2^15); 0 for a chunk of zeros.
+__device__ __forceinline__ int chunk_shift(float amax) {
+    int e = 0;
+    if (amax > 0.0f) (void)frexpf(amax, &e);
+    return amax > 0.0f ? 15 - e : 0;
+}
+
 __device__ __forceinline__ half8 pairs_to_half8(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
                                                 _Float16 bias) {
     // each dword holds two f16 values 1024+code (exact integers); subtract the

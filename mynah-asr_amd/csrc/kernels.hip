@@ -59,13 +59,6 @@ struct XChunk {
     float p;           // 2^-sh: the chunk's fold factor for this row
 };
 
-// the chunk shift: sh puts the chunk's largest magnitude in [2^14, 2^15)
-__device__ __forceinline__ int chunk_shift(float amax) {
-    int e = 0;
-    if (amax > 0.0f) (void)frexpf(amax, &e);
-    return amax > 0.0f ? 15 - e : 0;
-}
-
 // f16(x0 - h.lo), f16(x1 - h.hi) as one packed pair: x - h is exact in f32
 // (h is x rounded to f16), and v_fma_mixlo / v_fma_mixhi form it with h read as f16 in place
 // and rounds it to f16 once: the value of (_Float16)(x - (float)h), in two

@@ -120,6 +120,12 @@ bool mh_enc_d_supported(int d);
 // out may be x
 hipError_t mh_launch_add_ln(float *x, const float *res, float alpha, const float *w, const float *b, float *out,
                             int rows, int d, hipStream_t st);
+// the same, its output as the EXACT products' prepared input (xp: mh_mpad(rows)
+// * d * 4 bytes, xpf: mh_mpad(rows) * d / 128 floats) in place of f32 rows;
+// for d a multiple of 256 up to 2048
+bool mh_add_ln_prep_supported(int d);
+hipError_t mh_launch_add_ln_prep(float *x, const float *res, float alpha, const float *w, const float *b, int rows,
+                                 int d, uint8_t *xp, float *xpf, hipStream_t st);
 // g [rows, d] = h[:, :d] * sigmoid(h[:, d:]) for h [rows, 2d]
 hipError_t mh_launch_glu(const float *h, float *g, size_t rows, int d, hipStream_t st);
 // depthwise conv over time in each of nseq segments of T rows (w: the taps

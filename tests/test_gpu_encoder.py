@@ -122,6 +122,35 @@ def test_encoder_layer_segments_are_independent(gpu):
         dev.close()
 
 
+@pytest.mark.parametrize("d,f,biases,qt", [(1024, 4096, False, M.Q8_0), (256, 512, True, M.Q8_0),
+                                           (512, 1024, False, M.Q4_K)])
+def test_encoder_layer_ln_prep_bit_identical(gpu, monkeypatch, d, f, biases, qt):
+    """Layer norms that write the products' prepared input directly (the
+    default whenever every product of a norm's output takes the EXACT GEMM
+    path) give the bits of the layer with f32 norm outputs and the products'
+    own preparation (MYNAH_ASR_HIP_LN_PREP=0): the same split of the same
+    values. Q4_K products read row sums, so that layer keeps f32 rows."""
+    import torch
+    say("encoder layer ln prep", d, f, biases, qt)
+    H, k, T, nseq = d // 128, 9, 150, 2
+    p = make_params(11, d, f, k, biases, True)
+    dev = M.DeviceEncoderLayer(gpu, p, qt)
+    try:
+        x = np.random.default_rng(12).standard_normal((nseq * T, d)).astype(np.float32)
+        ped = torch.from_numpy(E.pos_emb(T, d).astype(np.float32)).cuda()
+        outs = []
+        for flag in ("1", "0"):
+            monkeypatch.setenv("MYNAH_ASR_HIP_LN_PREP", flag)
+            xd = torch.from_numpy(x).cuda()
+            dev.run(xd.data_ptr(), T, nseq, ped.data_ptr(), d, H, k, 0)
+            torch.cuda.synchronize()
+            outs.append(xd)
+        assert torch.isfinite(outs[0]).all()
+        assert torch.equal(outs[0].view(torch.int32), outs[1].view(torch.int32))
+    finally:
+        dev.close()
+
+
 def test_encoder_layer_refuses_bad_shapes(gpu):
     import torch
     say("encoder layer refusals")
