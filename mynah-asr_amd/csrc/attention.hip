@@ -76,7 +76,7 @@ struct AttnLds {
     static constexpr int K0 = 0;
     static constexpr int V0 = K0 + KT * RS;
     static constexpr int R0 = V0 + DK * VT;
-    static constexpr int EK0 = R0 + NB * RS;            // SPL: key rows' exponents, then rk rows'
+    static constexpr int EK0 = R0 + NB * RS;            // SPL: key rows' exponents, then rk rows' (negated)
     static constexpr int ER0 = EK0 + (SPL ? KT : 0);
     static constexpr int W0 = (ER0 + (SPL ? NB : 0) + 3) / 4 * 4;
     static constexpr int WB = 16 * BS;
@@ -108,6 +108,14 @@ __device__ __forceinline__ void split_h(float x, int s, _Float16 &hi, _Float16 &
     hi = (_Float16)y;
     lo = (_Float16)(y - (float)hi);
 }
+
+// SPL: K and rk as f16 (hi, lo) planes ([rows][d] each, the f32 tensors'
+// indexing) and each (row, head)'s exponent ([rows][H]), formed once per
+// call by k_attn_split instead of by every workgroup that stages a row
+struct SplitIn {
+    const _Float16 *kh, *kl, *rh, *rl;
+    const int *ke, *re;
+};
 
 __device__ __forceinline__ f4 mfma16(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -156,12 +164,11 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
                                                         const float *__restrict__ v, const float *__restrict__ rk,
                                                         const float *__restrict__ bu, const float *__restrict__ bv,
                                                         float *__restrict__ ctx, int T, int d, int left, int right,
-                                                        float kscale) {
+                                                        float kscale, SplitIn sp) {
     using L = AttnLds<DK, NW, SPL>;
     constexpr int NTH = L::NTH, RB = L::RB, NB = L::NB;
     constexpr int NS = DK / 4;    // reduction steps of a score product (f32 MFMA)
     constexpr int NKS = DK / 32;  // SPL: reduction steps of the f16 score MFMAs
-    constexpr int TPR = DK / 4;   // staging threads per K / rk row
     constexpr int NT = DK / 16;   // context column tiles
     extern __shared__ float lds[];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -172,6 +179,12 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     k += so;
     v += so;
     ctx += so;
+    const int H = d / DK;
+    if constexpr (SPL) {
+        sp.kh += so;
+        sp.kl += so;
+        sp.ke += (size_t)blockIdx.z * T * H;
+    }
     const int t0 = blockIdx.x * RB, tw = t0 + 16 * w;
     Window win;
     win.lim = left >= 0;
@@ -182,7 +195,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
 
     // SPL: (q + bias_u), (q + bias_v) of query row tw + c, features 32 i +
     // 8 g .. +7 of step i, as f16 pairs scaled by the row's 2^e; the
-    // exponents of this lane's output rows 4 g + e
+    // exponents of this lane's output rows 4 g + e, negated
     h8 qah[SPL ? NKS : 1], qal[SPL ? NKS : 1], qbh[SPL ? NKS : 1], qbl[SPL ? NKS : 1];
     int eqa[4], eqb[4];
     if constexpr (SPL) {
@@ -227,8 +240,8 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
             }
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            eqa[e] = __shfl(ea, 4 * g + e);
-            eqb[e] = __shfl(eb, 4 * g + e);
+            eqa[e] = -__shfl(ea, 4 * g + e);   // negated: the unscale adds them
+            eqb[e] = -__shfl(eb, 4 * g + e);
         }
     }
     // (q + bias_u), (q + bias_v) of query row tw + c, features NS*g .. NS*g + NS-1
@@ -268,26 +281,6 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     _Float16 *Kh = (_Float16 *)(lds + L::K0), *Kl = Kh + KT * L::KSH;
     _Float16 *Rh = (_Float16 *)(lds + L::R0), *Rl = Rh + NB * L::KSH;
     int *EK = (int *)(lds + L::EK0), *ER = (int *)(lds + L::ER0);
-    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-    // one staging thread's 4 features cc .. cc+3 of row `row` (the TPR threads
-    // of a row are consecutive lanes: the row's maximum is a lane reduction)
-    auto put_row = [&](const f4 &x, int row, int cc, _Float16 *H, _Float16 *Lo, int *E) {
-        float a = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
-#pragma unroll
-        for (int o = TPR / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o));
-        const int e = row_exp(a);
-        h4 hv, lv;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            _Float16 hh, ll;
-            split_h(x[j], e, hh, ll);
-            hv[j] = hh;
-            lv[j] = ll;
-        }
-        *(h4 *)(H + row * L::KSH + cc) = hv;
-        *(h4 *)(Lo + row * L::KSH + cc) = lv;
-        if (cc == 0) E[row] = e;
-    };
     float *Bw = lds + L::W0 + w * L::WSZ, *Pw = Bw;
     const int P = 2 * T - 1;
 
@@ -303,29 +296,46 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     // retires the 32 lowest and stages 32 new ones into their slots.
     constexpr int UKV = KT * DK / 4 / NTH, UR = KT * DK / 4 / NTH;
     static_assert(UKV * NTH == KT * DK / 4, "staging split");
-    f4 gk[UKV], gv[UKV], gr[UR];
+    f4 gk[SPL ? 1 : UKV], gv[UKV], gr[SPL ? 1 : UR];
+    uint4 sk[SPL ? UKV : 1], sr[SPL ? UR : 1];   // SPL: (hi, lo) halves of the same 4 features
+    int ek[SPL ? UKV : 1], er[SPL ? UR : 1];
     const int pb0 = T + (ja - KT) - t0 - (RB - 16);
+    // SPL: the (hi, lo) halves and the (row, head) exponent of row `row` of a split tensor
+    auto sload = [&](const _Float16 *hp, const _Float16 *lp, const int *ep, int row, int cc, uint4 &o, int &e) {
+        const unsigned off = (unsigned)(row * d + ho + cc);   // < 2^31: checked at launch
+        const uint2 a = *(const uint2 *)(hp + off), b = *(const uint2 *)(lp + off);
+        o = make_uint4(a.x, a.y, b.x, b.y);
+        e = ep[(unsigned)(row * H) + blockIdx.y];
+    };
+    auto sstore = [&](const uint4 &o, int e, int row, int cc, _Float16 *Hd, _Float16 *Ld, int *E) {
+        *(uint2 *)(Hd + row * L::KSH + cc) = make_uint2(o.x, o.y);
+        *(uint2 *)(Ld + row * L::KSH + cc) = make_uint2(o.z, o.w);
+        if (cc == 0) E[row] = -e;   // negated: the unscale adds them
+    };
     auto gload = [&](int jt, int ti) {
 #pragma unroll
         for (int u = 0; u < UKV; u++) {
             const int i = tid + NTH * u;
             const int r = i / (DK / 4), cc = 4 * (i % (DK / 4));
-            gk[u] = *(const f4 *)(k + (size_t)min(max(jt + r, 0), T - 1) * d + ho + cc);
+            const int kr = min(max(jt + r, 0), T - 1);
+            if constexpr (SPL) sload(sp.kh, sp.kl, sp.ke, kr, cc, sk[u], ek[u]);
+            else gk[u] = *(const f4 *)(k + (unsigned)(kr * d + ho + cc));
             const int rv = i % KT, cv = 4 * (i / KT);   // V: lanes along keys (transposed store)
-            gv[u] = *(const f4 *)(v + (size_t)min(max(jt + rv, 0), T - 1) * d + ho + cv);
+            gv[u] = *(const f4 *)(v + (unsigned)(min(max(jt + rv, 0), T - 1) * d + ho + cv));
         }
 #pragma unroll
         for (int u = 0; u < UR; u++) {
             const int i = tid + NTH * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
             const int p = min(max(pb0 + 32 * ti + NB - 32 + r, 0), P - 1);
-            gr[u] = *(const f4 *)(rk + (size_t)p * d + ho + cc);
+            if constexpr (SPL) sload(sp.rh, sp.rl, sp.re, p, cc, sr[u], er[u]);
+            else gr[u] = *(const f4 *)(rk + (unsigned)(p * d + ho + cc));
         }
     };
     auto lstore = [&](int ti) {
 #pragma unroll
         for (int u = 0; u < UKV; u++) {
             const int i = tid + NTH * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
-            if constexpr (SPL) put_row(gk[u], r, cc, Kh, Kl, EK);
+            if constexpr (SPL) sstore(sk[u], ek[u], r, cc, Kh, Kl, EK);
             else *(f4 *)(Ks + r * L::KS + cc) = gk[u];
             const int rv = i % KT, cv = 4 * (i / KT);
 #pragma unroll
@@ -335,7 +345,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
         for (int u = 0; u < UR; u++) {
             const int i = tid + NTH * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
             const int slot = (32 * ti + NB - 32 + r) % NB;
-            if constexpr (SPL) put_row(gr[u], slot, cc, Rh, Rl, ER);
+            if constexpr (SPL) sstore(sr[u], er[u], slot, cc, Rh, Rl, ER);
             else *(f4 *)(Rs + slot * L::KS + cc) = gr[u];
         }
     };
@@ -363,7 +373,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
             for (int n = n0; n < 2; n++) {
                 const int er = ER[rrow(0, n)];
 #pragma unroll
-                for (int e = 0; e < 4; e++) bd[n][e] = ldexpf(bd[n][e], -(eqb[e] + er));
+                for (int e = 0; e < 4; e++) bd[n][e] = ldexpf(bd[n][e], eqb[e] + er);
             }
             return;
         }
@@ -385,9 +395,14 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
         for (int i = tid; i < NB * DK / 4; i += NTH) {
             const int r = i / (DK / 4), cc = 4 * (i % (DK / 4));
             const int p = min(max(pb0 + r, 0), P - 1);
-            const f4 x = *(const f4 *)(rk + (size_t)p * d + ho + cc);
-            if constexpr (SPL) put_row(x, r, cc, Rh, Rl, ER);
-            else *(f4 *)(Rs + r * L::KS + cc) = x;
+            if constexpr (SPL) {
+                uint4 o;
+                int e;
+                sload(sp.rh, sp.rl, sp.re, p, cc, o, e);
+                sstore(o, e, r, cc, Rh, Rl, ER);
+            } else {
+                *(f4 *)(Rs + r * L::KS + cc) = *(const f4 *)(rk + (size_t)p * d + ho + cc);
+            }
         }
         __syncthreads();
         f4 bd[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -396,7 +411,12 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
         gload(ja, 1);
     }
 
+    // ring slots of this lane's window rows at tile ti, carried from tile to
+    // tile (each tile moves them 32 rows on)
+    int rb0 = (32 + prow + c) % NB;
     for (int jt = ja, ti = 1; jt < jb; jt += KT, ti++) {
+        const int rr[2] = {rb0, rb0 + 16 >= NB ? rb0 + 16 - NB : rb0 + 16};
+        rb0 = rb0 + 32 >= NB ? rb0 + 32 - NB : rb0 + 32;
         __syncthreads();   // every wave is done with the previous tile
         lstore(ti);
         __syncthreads();
@@ -416,7 +436,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
                     const int ok = (16 * n + c) * L::KSH + 32 * i + 8 * g;
                     kh[n] = *(const h8 *)(Kh + ok);
                     kl[n] = *(const h8 *)(Kl + ok);
-                    const int orr = rrow(ti, n) * L::KSH + 32 * i + 8 * g;
+                    const int orr = rr[n] * L::KSH + 32 * i + 8 * g;
                     rh[n] = *(const h8 *)(Rh + orr);
                     rl[n] = *(const h8 *)(Rl + orr);
                 }
@@ -432,11 +452,11 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
             }
 #pragma unroll
             for (int n = 0; n < 2; n++) {
-                const int ek = EK[16 * n + c], er = ER[rrow(ti, n)];
+                const int ek = EK[16 * n + c], er = ER[rr[n]];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    s[n][e] = ldexpf(s[n][e], -(eqa[e] + ek));
-                    bd[n][e] = ldexpf(bd[n][e], -(eqb[e] + er));
+                    s[n][e] = ldexpf(s[n][e], eqa[e] + ek);
+                    bd[n][e] = ldexpf(bd[n][e], eqb[e] + er);
                 }
             }
         }
@@ -446,7 +466,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
 #pragma unroll
             for (int n = 0; n < 2; n++) kx[n] = *(const f4 *)(Ks + (16 * n + c) * L::KS + NS * g + 4 * i);
 #pragma unroll
-            for (int n = 0; n < 2; n++) rx[n] = *(const f4 *)(Rs + rrow(ti, n) * L::KS + NS * g + 4 * i);
+            for (int n = 0; n < 2; n++) rx[n] = *(const f4 *)(Rs + rr[n] * L::KS + NS * g + 4 * i);
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 s[0] = mfma16(qa[4 * i + u], kx[0][u], s[0]);
@@ -473,14 +493,30 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
                 const int i = 4 * g + e;
                 sv[n][e] = Bw[i * L::BS + 16 * n + c - i + 15];
             }
+        if constexpr (SPL) {
+            // full attention: every key below T is visible, and only the
+            // last tile reaches past T
 #pragma unroll
-        for (int n = 0; n < 2; n++)
+            for (int n = 0; n < 2; n++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int j = jt + 16 * n + c;
-                const float x = (s[n][e] + sv[n][e]) * kscale;
-                sv[n][e] = (unsigned)(j - rj0[e]) < (unsigned)(rj1[e] - rj0[e]) ? x : -INFINITY;
+                for (int e = 0; e < 4; e++) sv[n][e] = (s[n][e] + sv[n][e]) * kscale;
+            if (jt + KT > T) {
+#pragma unroll
+                for (int n = 0; n < 2; n++)
+                    if (jt + 16 * n + c >= T)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) sv[n][e] = -INFINITY;
             }
+        } else {
+#pragma unroll
+            for (int n = 0; n < 2; n++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int j = jt + 16 * n + c;
+                    const float x = (s[n][e] + sv[n][e]) * kscale;
+                    sv[n][e] = (unsigned)(j - rj0[e]) < (unsigned)(rj1[e] - rj0[e]) ? x : -INFINITY;
+                }
+        }
         // 4. online softmax over the tile
         float alpha[4];
 #pragma unroll
@@ -536,10 +572,80 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     }
 }
 
+// The split of rows of DK features (x [rows][d], heads of DK columns): per
+// (row, head) the exponent e that puts the largest magnitude in [2^14, 2^15)
+// and the planes hi = f16(x 2^e), lo = f16(x 2^e - hi), as the attention
+// kernel's q split forms them. Thread = 4 features; the DK / 4 threads of a
+// (row, head) are consecutive lanes.
+template <int DK>
+__global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ x, size_t n4, int d,
+                                                    _Float16 *__restrict__ hi, _Float16 *__restrict__ lo,
+                                                    int *__restrict__ ex) {
+    constexpr int TPR = DK / 4;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= n4) return;   // whole (row, head) groups only: n4 is a multiple of TPR
+    const f4 v = *(const f4 *)(x + 4 * idx);
+    float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+    for (int o = TPR / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o));
+    const int e = row_exp(a);
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 hv, lv;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        _Float16 hh, ll;
+        split_h(v[j], e, hh, ll);
+        hv[j] = hh;
+        lv[j] = ll;
+    }
+    *(h4 *)(hi + 4 * idx) = hv;
+    *(h4 *)(lo + 4 * idx) = lv;
+    if (idx % TPR == 0) ex[idx / TPR] = e;   // [row][head]: (4 idx / d) * (d / DK) + head
+}
+
+size_t al256(size_t b) { return (b + 255) / 256 * 256; }
+
+// the workspace of the split path: K planes and exponents, then rk's
+struct SplitWs {
+    size_t kp, ke, rp, re, total;
+    SplitWs(int T, int d, int H, int nseq) {
+        const size_t kr = (size_t)nseq * T, pr = (size_t)(2 * T - 1);
+        kp = al256(kr * d * sizeof(_Float16));
+        ke = al256(kr * H * sizeof(int));
+        rp = al256(pr * d * sizeof(_Float16));
+        re = al256(pr * H * sizeof(int));
+        total = 2 * kp + ke + 2 * rp + re;
+    }
+};
+
+template <int DK>
+hipError_t launch_split(const float *x, size_t rows, int d, _Float16 *hi, _Float16 *lo, int *ex, hipStream_t st) {
+    const size_t n4 = rows * (size_t)(d / 4);
+    if (!n4) return hipSuccess;
+    hipLaunchKernelGGL(k_attn_split<DK>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, x, n4, d, hi, lo, ex);
+    return hipGetLastError();
+}
+
 template <int DK, int NW, bool SPL>
 hipError_t launch_attn(const float *q, const float *k, const float *v, const float *rk, const float *bu,
                          const float *bv, float *ctx, int T, int d, int H, int left, int right, int nseq,
-                         hipStream_t st) {
+                         void *ws, hipStream_t st) {
+    if ((size_t)(2 * (size_t)T) * d >= 0x7fffffffu) return hipErrorInvalidValue;   // 32-bit row offsets
+    if (SPL && left >= 0) return hipErrorInvalidValue;   // the split path assumes the full window
+    SplitIn sp{};
+    if constexpr (SPL) {
+        if (!ws) return hipErrorInvalidValue;
+        const SplitWs W(T, d, H, nseq);
+        uint8_t *b = (uint8_t *)ws;
+        _Float16 *kh = (_Float16 *)b, *kl = (_Float16 *)(b + W.kp);
+        int *ke = (int *)(b + 2 * W.kp);
+        _Float16 *rh = (_Float16 *)(b + 2 * W.kp + W.ke), *rl = (_Float16 *)(b + 2 * W.kp + W.ke + W.rp);
+        int *re = (int *)(b + 2 * W.kp + W.ke + 2 * W.rp);
+        hipError_t e = launch_split<DK>(k, (size_t)nseq * T, d, kh, kl, ke, st);
+        if (e == hipSuccess) e = launch_split<DK>(rk, (size_t)(2 * T - 1), d, rh, rl, re, st);
+        if (e != hipSuccess) return e;
+        sp = SplitIn{kh, kl, rh, rl, ke, re};
+    }
     using L = AttnLds<DK, NW, SPL>;
     const size_t bytes = sizeof(float) * L::TOTAL;
     // set once per instantiation (thread-safe static initialisation)
@@ -550,7 +656,7 @@ hipError_t launch_attn(const float *q, const float *k, const float *v, const flo
     const float kscale = (1.0f / sqrtf((float)DK)) * 1.4426950408889634f;
     dim3 grid((T + L::RB - 1) / L::RB, H, nseq);
     hipLaunchKernelGGL((k_relpos_attn<DK, NW, SPL>), grid, dim3(L::NTH), bytes, st, q, k, v, rk, bu, bv, ctx, T, d,
-                       left, right, kscale);
+                       left, right, kscale, sp);
     return hipGetLastError();
 }
 
@@ -565,26 +671,31 @@ bool use8(int T, int H, int left, int nseq) {
 
 template <int DK>
 hipError_t launch_dk(const float *q, const float *k, const float *v, const float *rk, const float *bu,
-                     const float *bv, float *ctx, int T, int d, int H, int left, int right, int nseq,
+                     const float *bv, float *ctx, int T, int d, int H, int left, int right, int nseq, void *ws,
                      hipStream_t st) {
     // Full attention computes its scores on the f16 MFMA from split operands
     // (18% faster at T = 750); chunked windows stage as many K / rk rows per
     // score they keep, so the splitting costs more than it saves there.
     if (use8(T, H, left, nseq))
-        return launch_attn<DK, 8, true>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, st);
-    if (left >= 0) return launch_attn<DK, 2, false>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, st);
-    return launch_attn<DK, 4, true>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, st);
+        return launch_attn<DK, 8, true>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, ws, st);
+    if (left >= 0) return launch_attn<DK, 2, false>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, ws, st);
+    return launch_attn<DK, 4, true>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, ws, st);
 }
 
 }  // namespace
 
 bool mh_attn_supported(int dk) { return dk == 64 || dk == 128; }
 
+size_t mh_attn_ws_bytes(int T, int d, int H, int nseq, int left) {
+    if (left >= 0 || T <= 0 || nseq <= 0 || H <= 0) return 0;   // chunked windows: f32 scores, no split
+    return SplitWs(T, d, H, nseq).total;
+}
+
 hipError_t mh_launch_relpos_attn(const float *q, const float *k, const float *v, const float *rk,
                                  const float *bias_u, const float *bias_v, float *ctx, int T, int d, int H,
-                                 int left, int right, int nseq, hipStream_t st) {
+                                 int left, int right, int nseq, void *ws, hipStream_t st) {
     const int dk = d / H;
-    if (dk == 128) return launch_dk<128>(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, st);
-    if (dk == 64) return launch_dk<64>(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, st);
+    if (dk == 128) return launch_dk<128>(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, ws, st);
+    if (dk == 64) return launch_dk<64>(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, ws, st);
     return hipErrorInvalidValue;
 }

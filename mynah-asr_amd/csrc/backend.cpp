@@ -103,6 +103,7 @@ struct Ctx {
     hipStream_t st = nullptr;
     DBuf x, y, h;
     DBuf att;    // the host-pointer attention call's q, k, v, rk, biases and ctx
+    DBuf attw;   // the attention core's workspace (K and rk split into f16 planes)
     DBuf aed;    // the AED decoder's caches and vectors
     DBuf enc;    // the encoder layer's activations
     DBuf ssb;    // the subsampling's activations
@@ -903,7 +904,12 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
         NumScope sp(MYNAH_ASR_HIP_EXACT);
         if (gemm_dev(c, L->relk_w, pe, rk, P, 0, st)) return -1;
     }
-    ENC_TRY(mh_launch_relpos_attn(q, k, v, rk, L->bias_u, L->bias_v, ctx, T, d, H, left, right, nseq, st));
+    {
+        const size_t wb = mh_attn_ws_bytes(T, d, H, nseq, left);
+        void *ws = wb ? c->attw.get(wb) : nullptr;
+        if (wb && !ws) return fail("device buffer allocation failed");
+        ENC_TRY(mh_launch_relpos_attn(q, k, v, rk, L->bias_u, L->bias_v, ctx, T, d, H, left, right, nseq, ws, st));
+    }
     {
         NumScope so(eff_num(L->o_w->qtype, d, M));
         if (gemm_dev(c, L->o_w, ctx, tmp, M, 0, st)) return -1;
@@ -1155,7 +1161,10 @@ int mynah_asr_hip_relpos_attention_dev(const float *q, const float *k, const flo
         if ((uintptr_t)p % 16) return fail("attention buffers must be 16-byte aligned");
     if (ctx == q || ctx == k || ctx == v) return fail("ctx may not alias q, k or v");
     if (T == 0 || nseq == 0) return 0;
-    hipError_t e = mh_launch_relpos_attn(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq,
+    const size_t wb = mh_attn_ws_bytes(T, d, H, nseq, left);
+    void *ws = wb ? c->attw.get(wb) : nullptr;
+    if (wb && !ws) return fail("device buffer allocation failed");
+    hipError_t e = mh_launch_relpos_attn(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, ws,
                                          pick_stream(stream));
     if (e != hipSuccess) return fail("attention launch failed", hipGetErrorString(e));
     return 0;

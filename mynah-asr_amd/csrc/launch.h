@@ -109,9 +109,12 @@ hipError_t mh_launch_gemm_i8(int qtype, const DevW &W, const uint8_t *qx, const 
 
 // Relative-position self-attention core (attention.hip): head size d / H of 64 or 128
 bool mh_attn_supported(int dk);
+// ws: mh_attn_ws_bytes of device workspace (full attention splits K and rk
+// into f16 planes there first; may be null when that is 0)
+size_t mh_attn_ws_bytes(int T, int d, int H, int nseq, int left);
 hipError_t mh_launch_relpos_attn(const float *q, const float *k, const float *v, const float *rk,
                                  const float *bias_u, const float *bias_v, float *ctx, int T, int d, int H,
-                                 int left, int right, int nseq, hipStream_t st);
+                                 int left, int right, int nseq, void *ws, hipStream_t st);
 
 // Encoder layer steps around the products (encoder.hip). d: 256 * {1..8, 12,
 // 16} for the layer norm (mh_enc_d_supported), a multiple of 4 for the rest.
