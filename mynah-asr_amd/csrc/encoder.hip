@@ -220,6 +220,58 @@ __global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ g, con
     *(float4 *)(out + (size_t)row * d + i) = o;
 }
 
+// The same in tiles: a workgroup = DW_R rows of one segment x 256 channels.
+// The rows t0 - pc .. t0 + DW_R - 1 - pc + k - 1 of g (zero outside the
+// segment) and the k taps are staged in LDS once, so each input row is read
+// from memory once per tile instead of once per tap; thread = (4 channels,
+// every 4th row of the tile). Per output the operations and their order are
+// those of k_dwconv (taps outside the segment skipped, not added as zeros).
+constexpr int DW_R = 32;
+__global__ __launch_bounds__(256) void k_dwconv_tile(const float *__restrict__ g, const float *__restrict__ wt,
+                                                     const float *__restrict__ bias, const float *__restrict__ scale,
+                                                     const float *__restrict__ shift, float *__restrict__ out,
+                                                     int T, int d, int k, int pc) {
+    extern __shared__ float4 dws[];   // [DW_R + k - 1][64] rows of g, then [k][64] taps
+    const int tid = threadIdx.x, q = tid & 63, t0 = blockIdx.x * DW_R, c0 = blockIdx.y * 256;
+    const int nrow = DW_R + k - 1;
+    const float *gs = g + (size_t)blockIdx.z * T * d + c0;
+    float4 *taps = dws + nrow * 64;
+    for (int i = tid; i < nrow * 64; i += 256) {
+        const int t = t0 - pc + (i >> 6);
+        dws[i] = t >= 0 && t < T ? *(const float4 *)(gs + (size_t)t * d + 4 * (i & 63)) : float4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int i = tid; i < k * 64; i += 256) taps[i] = *(const float4 *)(wt + (size_t)(i >> 6) * d + c0 + 4 * (i & 63));
+    __syncthreads();
+    const int i = c0 + 4 * q;
+    const float4 b0 = bias ? *(const float4 *)(bias + i) : float4{0.f, 0.f, 0.f, 0.f};
+    float4 sc = {0.f, 0.f, 0.f, 0.f}, sh = sc;
+    if (scale) {
+        sc = *(const float4 *)(scale + i);
+        sh = *(const float4 *)(shift + i);
+    }
+    float *os = out + (size_t)blockIdx.z * T * d + i;
+    for (int rr = tid >> 6; rr < DW_R; rr += 4) {
+        const int t = t0 + rr;
+        if (t >= T) break;
+        const int j0 = t - pc < 0 ? pc - t : 0, j1 = t - pc + k > T ? T - t + pc : k;
+        float4 o = b0;
+        for (int j = j0; j < j1; j++) {
+            const float4 src = dws[(rr + j) * 64 + q], wv = taps[j * 64 + q];
+            o.x = fmaf(wv.x, src.x, o.x);
+            o.y = fmaf(wv.y, src.y, o.y);
+            o.z = fmaf(wv.z, src.z, o.z);
+            o.w = fmaf(wv.w, src.w, o.w);
+        }
+        if (scale) {
+            o.x = silu_e(fmaf(o.x, sc.x, sh.x));
+            o.y = silu_e(fmaf(o.y, sc.y, sh.y));
+            o.z = silu_e(fmaf(o.z, sc.z, sh.z));
+            o.w = silu_e(fmaf(o.w, sc.w, sh.w));
+        }
+        *(float4 *)(os + (size_t)t * d) = o;
+    }
+}
+
 // The first two stages in one pass: out[s][to][fo][c] = the depthwise 3x3
 // stride-2 conv (+ b1) of y = relu(conv_in(x) + b0), the 1 -> C 3x3 stride-2
 // conv of the mel features (subsampling.c:222-226, 231-236). y is formed
@@ -444,6 +496,12 @@ hipError_t mh_launch_dwconv(const float *g, const float *w, const float *bias, c
     if (T <= 0 || nseq <= 0) return hipSuccess;
     if (d % 4 || k <= 0) return hipErrorInvalidValue;
     const int pc = causal ? k - 1 : (k - 1) / 2;
+    const size_t lds = sizeof(float4) * 64 * (size_t)(DW_R + 2 * k - 1);
+    if (d % 256 == 0 && lds <= 64 * 1024) {
+        hipLaunchKernelGGL(k_dwconv_tile, dim3((unsigned)((T + DW_R - 1) / DW_R), d / 256, nseq), dim3(256), lds, st, g,
+                           w, bias, scale, shift, out, T, d, k, pc);
+        return hipGetLastError();
+    }
     const size_t n = (size_t)nseq * T * (d / 4);
     hipLaunchKernelGGL(k_dwconv, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, w, bias, scale, shift, out,
                        T, nseq, d, k, pc);
