@@ -923,12 +923,18 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
     }
     c->pa.src = nullptr;
     if (bias_add(h, L->pw1_b, M, 2 * d, st)) return -1;
-    ENC_TRY(mh_launch_glu(h, q, M, d, st));   // g (q is free now)
     ENC_TRY(mh_launch_transpose_taps(L->dw_w, dwt, d, conv_k, st));
+    // the GLU (g = q, free now) folded into the depthwise conv where it can be
+    const bool glu_dw = mh_glu_dwconv_supported(d, conv_k);
+    if (!glu_dw) ENC_TRY(mh_launch_glu(h, q, M, d, st));
+    auto dwconv = [&](const float *sc, const float *sh, float *o) {
+        return glu_dw ? mh_launch_glu_dwconv(h, dwt, L->dw_b, sc, sh, o, T, nseq, d, conv_k, causal, st)
+                      : mh_launch_dwconv(q, dwt, L->dw_b, sc, sh, o, T, nseq, d, conv_k, causal, st);
+    };
     if (L->cnorm_scale) {
-        ENC_TRY(mh_launch_dwconv(q, dwt, L->dw_b, L->cnorm_scale, L->cnorm_shift, k, T, nseq, d, conv_k, causal, st));
+        ENC_TRY(dwconv(L->cnorm_scale, L->cnorm_shift, k));
     } else {
-        ENC_TRY(mh_launch_dwconv(q, dwt, L->dw_b, nullptr, nullptr, v, T, nseq, d, conv_k, causal, st));
+        ENC_TRY(dwconv(nullptr, nullptr, v));
         ENC_TRY(mh_launch_add_ln(v, nullptr, 0.0f, L->cnorm_w, L->cnorm_b, k, M, d, st));
         ENC_TRY(mh_launch_silu(k, md, st));
     }

@@ -6,10 +6,14 @@
 //
 //   k_add_ln    x += alpha * res (when res), then out = LN(x) per row
 //               (layer_norm_f, :25-37; the adds of :495, 502, 507, 511)
+//   k_add_ln_prep  the same, its output written as the products' prepared
+//               input (EXACT numerics) instead of f32 rows
 //   k_glu       g = a * sigmoid(b) over the two halves of each row  :426-432
 //   k_dwconv    depthwise conv over time within each segment (causal: left
 //               pad k-1; else 'same'), + dw_b, then the folded batch norm
 //               x * scale + shift and SiLU when scale is given     :434-459
+//   k_dwconv_tile  the same on LDS tiles of 32 rows, optionally forming the
+//               GLU as it stages its input
 //
 // and of the dw_striding subsampling in front of the layers
 // (src/subsampling.c:208-268, 109-200), with activations channel-last,
@@ -226,7 +230,10 @@ __global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ g, con
 // from memory once per tile instead of once per tap; thread = (4 channels,
 // every 4th row of the tile). Per output the operations and their order are
 // those of k_dwconv (taps outside the segment skipped, not added as zeros).
+// GLU: g is formed from pw1's output h [rows][2d] as it is staged (k_glu's
+// operations; the halo rows' values are formed again by the next tile).
 constexpr int DW_R = 32;
+template <bool GLU>
 __global__ __launch_bounds__(256) void k_dwconv_tile(const float *__restrict__ g, const float *__restrict__ wt,
                                                      const float *__restrict__ bias, const float *__restrict__ scale,
                                                      const float *__restrict__ shift, float *__restrict__ out,
@@ -234,11 +241,21 @@ __global__ __launch_bounds__(256) void k_dwconv_tile(const float *__restrict__ g
     extern __shared__ float4 dws[];   // [DW_R + k - 1][64] rows of g, then [k][64] taps
     const int tid = threadIdx.x, q = tid & 63, t0 = blockIdx.x * DW_R, c0 = blockIdx.y * 256;
     const int nrow = DW_R + k - 1;
-    const float *gs = g + (size_t)blockIdx.z * T * d + c0;
+    const int gw = GLU ? 2 * d : d;   // the input's row width
+    const float *gs = g + (size_t)blockIdx.z * T * gw + c0;
     float4 *taps = dws + nrow * 64;
     for (int i = tid; i < nrow * 64; i += 256) {
         const int t = t0 - pc + (i >> 6);
-        dws[i] = t >= 0 && t < T ? *(const float4 *)(gs + (size_t)t * d + 4 * (i & 63)) : float4{0.f, 0.f, 0.f, 0.f};
+        float4 o = {0.f, 0.f, 0.f, 0.f};
+        if (t >= 0 && t < T) {
+            const float *p = gs + (size_t)t * gw + 4 * (i & 63);
+            o = *(const float4 *)p;
+            if constexpr (GLU) {
+                const float4 b = *(const float4 *)(p + d);
+                o = float4{o.x * sigmoid_f(b.x), o.y * sigmoid_f(b.y), o.z * sigmoid_f(b.z), o.w * sigmoid_f(b.w)};
+            }
+        }
+        dws[i] = o;
     }
     for (int i = tid; i < k * 64; i += 256) taps[i] = *(const float4 *)(wt + (size_t)(i >> 6) * d + c0 + 4 * (i & 63));
     __syncthreads();
@@ -490,16 +507,32 @@ hipError_t mh_launch_glu(const float *h, float *g, size_t rows, int d, hipStream
     return hipGetLastError();
 }
 
+bool mh_glu_dwconv_supported(int d, int k) {
+    return d > 0 && d % 256 == 0 && k > 0 && sizeof(float4) * 64 * (size_t)(DW_R + 2 * k - 1) <= 64 * 1024;
+}
+
+hipError_t mh_launch_glu_dwconv(const float *h, const float *w, const float *bias, const float *scale,
+                                const float *shift, float *out, int T, int nseq, int d, int k, int causal,
+                                hipStream_t st) {
+    if (T <= 0 || nseq <= 0) return hipSuccess;
+    if (!mh_glu_dwconv_supported(d, k)) return hipErrorInvalidValue;
+    const int pc = causal ? k - 1 : (k - 1) / 2;
+    const size_t lds = sizeof(float4) * 64 * (size_t)(DW_R + 2 * k - 1);
+    hipLaunchKernelGGL(k_dwconv_tile<true>, dim3((unsigned)((T + DW_R - 1) / DW_R), d / 256, nseq), dim3(256), lds, st,
+                       h, w, bias, scale, shift, out, T, d, k, pc);
+    return hipGetLastError();
+}
+
 hipError_t mh_launch_dwconv(const float *g, const float *w, const float *bias, const float *scale,
                             const float *shift, float *out, int T, int nseq, int d, int k, int causal,
                             hipStream_t st) {
     if (T <= 0 || nseq <= 0) return hipSuccess;
     if (d % 4 || k <= 0) return hipErrorInvalidValue;
     const int pc = causal ? k - 1 : (k - 1) / 2;
-    const size_t lds = sizeof(float4) * 64 * (size_t)(DW_R + 2 * k - 1);
-    if (d % 256 == 0 && lds <= 64 * 1024) {
-        hipLaunchKernelGGL(k_dwconv_tile, dim3((unsigned)((T + DW_R - 1) / DW_R), d / 256, nseq), dim3(256), lds, st, g,
-                           w, bias, scale, shift, out, T, d, k, pc);
+    if (mh_glu_dwconv_supported(d, k)) {
+        const size_t lds = sizeof(float4) * 64 * (size_t)(DW_R + 2 * k - 1);
+        hipLaunchKernelGGL(k_dwconv_tile<false>, dim3((unsigned)((T + DW_R - 1) / DW_R), d / 256, nseq), dim3(256),
+                           lds, st, g, w, bias, scale, shift, out, T, d, k, pc);
         return hipGetLastError();
     }
     const size_t n = (size_t)nseq * T * (d / 4);

@@ -138,6 +138,13 @@ hipError_t mh_launch_glu(const float *h, float *g, size_t rows, int d, hipStream
 hipError_t mh_launch_dwconv(const float *g, const float *w, const float *bias, const float *scale,
                             const float *shift, float *out, int T, int nseq, int d, int k, int causal,
                             hipStream_t st);
+// GLU and the depthwise conv in one pass: h = pw1's output [rows][2d],
+// g = h[:, :d] * sigmoid(h[:, d:]) formed as it is read (bit-identical to
+// mh_launch_glu, then mh_launch_dwconv); for d a multiple of 256, k <= 16
+bool mh_glu_dwconv_supported(int d, int k);
+hipError_t mh_launch_glu_dwconv(const float *h, const float *w, const float *bias, const float *scale,
+                                const float *shift, float *out, int T, int nseq, int d, int k, int causal,
+                                hipStream_t st);
 
 // The dw_striding subsampling's steps (encoder.hip), channel-last activations
 // [segment][time][freq][channel] (C a multiple of 4); causal pads (2, 1),
