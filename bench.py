@@ -24,7 +24,7 @@ from the host), products of 16 to 750 rows on one stream (qgemm_dev calls: few t
 K split over workgroups), the f32-weight GEMM, the relative-position attention core at T = 750
 (16 segments as in benchmark config 5, d 1024, 8 heads; full and chunked-limited [70, 13] windows;
 useful flops = 6 * dk per visible (row, key) pair, against the 157.3 TFLOP/s
-fp32 MFMA peak; full attention forms its scores on the f16 MFMA from split
+fp32 MFMA peak; full attention forms its products on the f16 MFMA from split
 hi + lo operands, three f16 products per f32 one), and the reference CPU path timed on this host (ingot dequant, compiled from
 the reference's sources, + OpenBLAS sgemm, as src/weights.c:103-114 +
 src/backend.c:79 do).
@@ -734,7 +734,7 @@ def run_attention(B, M_, T=750, d=1024, H=8, nseq=16, reps=10):
         out.append({"T": T, "d": d, "heads": H, "segments": nseq, "left": left, "right": right,
                     "kernel_us": round(ms * 1e3, 2), "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
                     "fp32_mfma_frac": round(fl / (ms * 1e-3) / 1e12 / PEAK_FP32, 4),
-                    "scores_on": "f32 MFMA" if left >= 0 else "f16 MFMA, split operands"})
+                    "products_on": "f32 MFMA" if left >= 0 else "f16 MFMA, split operands"})
     return out
 
 

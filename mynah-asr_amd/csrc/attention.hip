@@ -1,8 +1,8 @@
 // attention.hip — the relative-position self-attention core of the FastConformer
 // encoder layer (the reference's src/encoder.c:315-410 for full attention and
 // its banded twin encoder.c:220-313 for chunked-limited attention), on the
-// MFMA of gfx950: fp32 (v_mfma_f32_16x16x4_f32), and for the scores of full
-// attention f16 (v_mfma_f32_16x16x32_f16) on split operands.
+// MFMA of gfx950: fp32 (v_mfma_f32_16x16x4_f32) for chunked windows, f16
+// (v_mfma_f32_16x16x32_f16) on split operands for full attention.
 //
 // Per head h (columns h*DK .. h*DK+DK-1 of the [T, d] buffers):
 //   s[t, j] = ((q[t] + bias_u) . k[j] + (q[t] + bias_v) . rk[T-1 + j - t]) / sqrt(DK)
@@ -34,13 +34,17 @@
 // reference's f32 computation up to summation order and the exponential's
 // rounding.
 //
-// SPL = true (full attention) forms the two score products on the f16 MFMA
-// instead. Each q, K and rk row is scaled by a power of two 2^e that puts its
-// largest magnitude in [2^14, 2^15) and split into f16 pairs hi + lo (hi =
-// f16(x 2^e), lo = f16(x 2^e - hi)), which hold x to 2^-22 of the row's
-// maximum; a score is hi.hi + hi.lo + lo.hi summed in f32 (the dropped lo.lo
-// is below 2^-22 of the same scale) and multiplied by 2^-(e_q + e_k), which
-// is exact. The probabilities and the V product stay fp32.
+// SPL = true (full attention) forms the products on the f16 MFMA instead.
+// Each q, K and rk row is scaled by a power of two 2^e that puts its largest
+// magnitude in [2^14, 2^15) and split into f16 pairs hi + lo (hi = f16(x 2^e),
+// lo = f16(x 2^e - hi)), which hold x to 2^-22 of the row's maximum; a score
+// is hi.hi + hi.lo + lo.hi summed in f32 (the dropped lo.lo is below 2^-22 of
+// the same scale) and multiplied by 2^-(e_q + e_k), which is exact. The
+// context update splits the probabilities (<= 1) at the fixed scale 2^14 and
+// V per (tile of 32 keys, feature), and undoes both per tile with one exact
+// power of two. K, rk and V are split once per call by pre-passes
+// (k_attn_split, k_attn_split_v); the q rows once per wave. The softmax
+// stays fp32.
 //
 // MFMA 16x16x4 f32 operand layout (lane l, c = l & 15, g = l >> 4):
 //   A: row c, k-slot g;  B: column c, k-slot g;  D: rows 4g + e (e = 0..3), column c.
@@ -71,14 +75,17 @@ struct AttnLds {
     static constexpr int KSH = DK + 8;  // SPL: the same in halves
     static constexpr int RS = SPL ? KSH : KS;   // floats per K / rk row (SPL: two rows of KSH halves)
     static constexpr int VT = KT + 4;   // V is stored transposed, [DK][VT]: conflict-free b128 reads
+    static constexpr int VTH = KT + 8;  // SPL: the same in halves, hi plane then lo plane
+    static constexpr int VSZ = SPL ? DK * VTH : DK * VT;   // floats
     static constexpr int BS = 53;       // band scratch row stride
     static constexpr int PS = 36;       // probability scratch row stride
     static constexpr int K0 = 0;
     static constexpr int V0 = K0 + KT * RS;
-    static constexpr int R0 = V0 + DK * VT;
+    static constexpr int R0 = V0 + VSZ;
     static constexpr int EK0 = R0 + NB * RS;            // SPL: key rows' exponents, then rk rows' (negated)
     static constexpr int ER0 = EK0 + (SPL ? KT : 0);
-    static constexpr int W0 = (ER0 + (SPL ? NB : 0) + 3) / 4 * 4;
+    static constexpr int EV0 = ER0 + (SPL ? NB : 0);     // SPL: the V tile's scale per feature
+    static constexpr int W0 = (EV0 + (SPL ? DK : 0) + 3) / 4 * 4;
     static constexpr int WB = 16 * BS;
     static constexpr int WSZ = WB;      // the probabilities reuse the band scratch
     static constexpr int TOTAL = W0 + NW * WSZ;   // floats
@@ -112,9 +119,15 @@ __device__ __forceinline__ void split_h(float x, int s, _Float16 &hi, _Float16 &
 // SPL: K and rk as f16 (hi, lo) planes ([rows][d] each, the f32 tensors'
 // indexing) and each (row, head)'s exponent ([rows][H]), formed once per
 // call by k_attn_split instead of by every workgroup that stages a row
+// V likewise, per tile of 32 keys (from key 0) and transposed: planes
+// [segment][tile][d][32], and per (segment, tile, feature) the scale
+// 2^-(14 + e) that undoes both the feature's exponent e and the
+// probabilities' fixed 2^14
 struct SplitIn {
     const _Float16 *kh, *kl, *rh, *rl;
     const int *ke, *re;
+    const _Float16 *vh, *vl;
+    const float *vs;
 };
 
 __device__ __forceinline__ f4 mfma16(float a, float b, f4 c) {
@@ -180,10 +193,14 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     v += so;
     ctx += so;
     const int H = d / DK;
+    const int ntile = (T + KT - 1) / KT;
     if constexpr (SPL) {
         sp.kh += so;
         sp.kl += so;
         sp.ke += (size_t)blockIdx.z * T * H;
+        sp.vh += (size_t)blockIdx.z * ntile * d * KT;
+        sp.vl += (size_t)blockIdx.z * ntile * d * KT;
+        sp.vs += (size_t)blockIdx.z * ntile * d;
     }
     const int t0 = blockIdx.x * RB, tw = t0 + 16 * w;
     Window win;
@@ -280,6 +297,8 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     // SPL: the same K and rk rows as f16 pairs and their exponents
     _Float16 *Kh = (_Float16 *)(lds + L::K0), *Kl = Kh + KT * L::KSH;
     _Float16 *Rh = (_Float16 *)(lds + L::R0), *Rl = Rh + NB * L::KSH;
+    _Float16 *Vh = (_Float16 *)(lds + L::V0), *Vl = Vh + DK * L::VTH;
+    float *EVs = lds + L::EV0;
     int *EK = (int *)(lds + L::EK0), *ER = (int *)(lds + L::ER0);
     float *Bw = lds + L::W0 + w * L::WSZ, *Pw = Bw;
     const int P = 2 * T - 1;
@@ -296,7 +315,11 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     // retires the 32 lowest and stages 32 new ones into their slots.
     constexpr int UKV = KT * DK / 4 / NTH, UR = KT * DK / 4 / NTH;
     static_assert(UKV * NTH == KT * DK / 4, "staging split");
-    f4 gk[SPL ? 1 : UKV], gv[UKV], gr[SPL ? 1 : UR];
+    // SPL: V tile pieces of 16 bytes (8 keys of one feature, hi or lo plane)
+    constexpr int NVP = 2 * DK * 4, UVP = (NVP + NTH - 1) / NTH;
+    f4 gk[SPL ? 1 : UKV], gv[SPL ? 1 : UKV], gr[SPL ? 1 : UR];
+    uint4 svp[SPL ? UVP : 1];
+    float svs = 0.0f;
     uint4 sk[SPL ? UKV : 1], sr[SPL ? UR : 1];   // SPL: (hi, lo) halves of the same 4 features
     int ek[SPL ? UKV : 1], er[SPL ? UR : 1];
     const int pb0 = T + (ja - KT) - t0 - (RB - 16);
@@ -320,8 +343,23 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
             const int kr = min(max(jt + r, 0), T - 1);
             if constexpr (SPL) sload(sp.kh, sp.kl, sp.ke, kr, cc, sk[u], ek[u]);
             else gk[u] = *(const f4 *)(k + (unsigned)(kr * d + ho + cc));
-            const int rv = i % KT, cv = 4 * (i / KT);   // V: lanes along keys (transposed store)
-            gv[u] = *(const f4 *)(v + (unsigned)(min(max(jt + rv, 0), T - 1) * d + ho + cv));
+            if constexpr (!SPL) {
+                const int rv = i % KT, cv = 4 * (i / KT);   // V: lanes along keys (transposed store)
+                gv[u] = *(const f4 *)(v + (unsigned)(min(max(jt + rv, 0), T - 1) * d + ho + cv));
+            }
+        }
+        if constexpr (SPL) {
+            const int vt = jt / KT;   // full attention: tiles start at key 0
+#pragma unroll
+            for (int u = 0; u < UVP; u++) {
+                const int pc = tid + NTH * u;
+                if (NVP % NTH == 0 || pc < NVP) {
+                    const int f = (pc >> 2) % DK, part = pc & 3;
+                    const _Float16 *pl = pc < DK * 4 ? sp.vh : sp.vl;
+                    svp[u] = *(const uint4 *)(pl + ((unsigned)(vt * d + ho + f) * KT + 8 * part));
+                }
+            }
+            if (tid < DK) svs = sp.vs[(unsigned)(vt * d + ho + tid)];
         }
 #pragma unroll
         for (int u = 0; u < UR; u++) {
@@ -337,9 +375,23 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
             const int i = tid + NTH * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
             if constexpr (SPL) sstore(sk[u], ek[u], r, cc, Kh, Kl, EK);
             else *(f4 *)(Ks + r * L::KS + cc) = gk[u];
-            const int rv = i % KT, cv = 4 * (i / KT);
+            if constexpr (!SPL) {
+                const int rv = i % KT, cv = 4 * (i / KT);
 #pragma unroll
-            for (int e = 0; e < 4; e++) Vs[(cv + e) * L::VT + rv] = gv[u][e];
+                for (int e = 0; e < 4; e++) Vs[(cv + e) * L::VT + rv] = gv[u][e];
+            }
+        }
+        if constexpr (SPL) {
+#pragma unroll
+            for (int u = 0; u < UVP; u++) {
+                const int pc = tid + NTH * u;
+                if (NVP % NTH == 0 || pc < NVP) {
+                    const int f = (pc >> 2) % DK, part = pc & 3;
+                    _Float16 *pl = pc < DK * 4 ? Vh : Vl;
+                    *(uint4 *)(pl + f * L::VTH + 8 * part) = svp[u];
+                }
+            }
+            if (tid < DK) EVs[tid] = svs;
         }
 #pragma unroll
         for (int u = 0; u < UR; u++) {
@@ -542,6 +594,31 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
         wave_lds_order();
         const f4 pa0 = *(const f4 *)(Pw + c * L::PS + 8 * g);
         const f4 pa1 = *(const f4 *)(Pw + c * L::PS + 8 * g + 4);
+        if constexpr (SPL) {
+            // probabilities (<= 1) split at the fixed scale 2^14, V split by
+            // the pre-pass; the tile's scales undone by an exact power of two
+            h8 ph, pl;
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                _Float16 hh, ll;
+                split_h(u < 4 ? pa0[u] : pa1[u - 4], 14, hh, ll);
+                ph[u] = hh;
+                pl[u] = ll;
+            }
+#pragma unroll
+            for (int n = 0; n < NT; n++) {
+                const int o = (16 * n + c) * L::VTH + 8 * g;
+                const h8 vh = *(const h8 *)(Vh + o), vl = *(const h8 *)(Vl + o);
+                f4 t = {0.f, 0.f, 0.f, 0.f};
+                t = mfma16h(ph, vh, t);
+                t = mfma16h(ph, vl, t);
+                t = mfma16h(pl, vh, t);
+                const float sc = EVs[16 * n + c];
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[n][e] = fmaf(t[e], sc, acc[n][e]);
+            }
+            continue;
+        }
         const float pa[8] = {pa0.x, pa0.y, pa0.z, pa0.w, pa1.x, pa1.y, pa1.z, pa1.w};
         // B operand: column 16n + c, keys 8g .. 8g+7 of the transposed V tile
         f4 vb[2][2];
@@ -603,18 +680,62 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ x,
     if (idx % TPR == 0) ex[idx / TPR] = e;   // [row][head]: (4 idx / d) * (d / DK) + head
 }
 
+// V per tile of 32 keys (from key 0), transposed. Per feature the exponent
+// e that puts the tile's largest magnitude in [2^14, 2^15) (clamped to
+// [-100, 100], so that the scale below stays a normal float), the planes
+// hi = f16(v 2^e), lo = f16(v 2^e - hi) as [segment][tile][d][32] (keys past
+// T zero), and the scale 2^-(14 + e). Thread = (segment, tile, feature, 8
+// keys): the 4 threads of a feature are consecutive lanes (the maximum is a
+// quad reduction), and a wave's stores cover 16 features' 64-byte rows.
+__global__ __launch_bounds__(256) void k_attn_split_v(const float *__restrict__ v, int T, int d, int nseq,
+                                                      _Float16 *__restrict__ hi, _Float16 *__restrict__ lo,
+                                                      float *__restrict__ vs) {
+    const int ntile = (T + KT - 1) / KT;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)nseq * ntile * d * 4) return;   // whole quads only
+    const int part = (int)(idx & 3);
+    const size_t fi = idx >> 2;   // (segment, tile, feature)
+    const int f = (int)(fi % d), tile = (int)((fi / d) % ntile), s = (int)(fi / ((size_t)d * ntile));
+    const int k0 = tile * KT + 8 * part;
+    const float *vr = v + ((size_t)s * T + k0) * d + f;
+    float x[8];
+    float a = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+        x[jj] = k0 + jj < T ? vr[(size_t)jj * d] : 0.0f;
+        a = fmaxf(a, fabsf(x[jj]));
+    }
+    a = fmaxf(a, __shfl_xor(a, 1));
+    a = fmaxf(a, __shfl_xor(a, 2));
+    const int ex = min(max(row_exp(a), -100), 100);
+    h8 hv, lv;
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+        _Float16 hh, ll;
+        split_h(x[jj], ex, hh, ll);
+        hv[jj] = hh;
+        lv[jj] = ll;
+    }
+    *(h8 *)(hi + fi * KT + 8 * part) = hv;
+    *(h8 *)(lo + fi * KT + 8 * part) = lv;
+    if (part == 0) vs[fi] = __int_as_float((127 - 14 - ex) << 23);
+}
+
 size_t al256(size_t b) { return (b + 255) / 256 * 256; }
 
 // the workspace of the split path: K planes and exponents, then rk's
 struct SplitWs {
-    size_t kp, ke, rp, re, total;
+    size_t kp, ke, rp, re, vp, vs, total;
     SplitWs(int T, int d, int H, int nseq) {
         const size_t kr = (size_t)nseq * T, pr = (size_t)(2 * T - 1);
+        const size_t vt = (size_t)nseq * ((T + KT - 1) / KT);
         kp = al256(kr * d * sizeof(_Float16));
         ke = al256(kr * H * sizeof(int));
         rp = al256(pr * d * sizeof(_Float16));
         re = al256(pr * H * sizeof(int));
-        total = 2 * kp + ke + 2 * rp + re;
+        vp = al256(vt * d * KT * sizeof(_Float16));
+        vs = al256(vt * d * sizeof(float));
+        total = 2 * kp + ke + 2 * rp + re + 2 * vp + vs;
     }
 };
 
@@ -641,10 +762,19 @@ hipError_t launch_attn(const float *q, const float *k, const float *v, const flo
         int *ke = (int *)(b + 2 * W.kp);
         _Float16 *rh = (_Float16 *)(b + 2 * W.kp + W.ke), *rl = (_Float16 *)(b + 2 * W.kp + W.ke + W.rp);
         int *re = (int *)(b + 2 * W.kp + W.ke + 2 * W.rp);
+        uint8_t *vb = b + 2 * W.kp + W.ke + 2 * W.rp + W.re;
+        _Float16 *vh = (_Float16 *)vb, *vl = (_Float16 *)(vb + W.vp);
+        float *vsc = (float *)(vb + 2 * W.vp);
         hipError_t e = launch_split<DK>(k, (size_t)nseq * T, d, kh, kl, ke, st);
         if (e == hipSuccess) e = launch_split<DK>(rk, (size_t)(2 * T - 1), d, rh, rl, re, st);
+        if (e == hipSuccess) {
+            const size_t n = (size_t)nseq * ((T + KT - 1) / KT) * d * 4;
+            hipLaunchKernelGGL(k_attn_split_v, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, v, T, d, nseq, vh,
+                               vl, vsc);
+            e = hipGetLastError();
+        }
         if (e != hipSuccess) return e;
-        sp = SplitIn{kh, kl, rh, rl, ke, re};
+        sp = SplitIn{kh, kl, rh, rl, ke, re, vh, vl, vsc};
     }
     using L = AttnLds<DK, NW, SPL>;
     const size_t bytes = sizeof(float) * L::TOTAL;
