@@ -97,9 +97,11 @@ def test_relpos_attention_many_segments(gpu, d):
 @pytest.mark.parametrize("left,right", [(-1, 0), (1000, 299)])
 def test_relpos_attention_wide_row_scales(gpu, left, right):
     """Rows of q, k and rk scaled by 2^-30 .. 2^30, rows of zeros, and rows
-    with one feature 1e4 times the rest: the split scores carry each row's own
-    scale, so the bar holds as for N(0, 1) rows (full attention on the split
-    path, and the one-chunk window, the same scores on the f32 path)."""
+    with one feature 1e4 times the rest; V's features scaled by 2^-20 .. 2^20
+    with a zero key tile: the split operands carry each row's (V: each key
+    tile and feature's) own scale, so the bar holds as for N(0, 1) inputs
+    (full attention on the split path, and the one-chunk window, the same
+    products on the f32 path)."""
     T, d, H = 150, 256, 2
     r = np.random.default_rng(77)
     q, k, v, rk, bu, bv = make(41, T, d, 1)
@@ -107,12 +109,22 @@ def test_relpos_attention_wide_row_scales(gpu, left, right):
         a *= np.exp2(r.integers(-30, 31, size=(n, 1))).astype(np.float32)
         a[r.integers(0, n, size=5)] = 0.0
         a[r.integers(0, n, size=5), r.integers(0, d, size=5)] *= 1e4
+    # V: features scaled by 2^-20 .. 2^20 (its split carries one exponent per
+    # key tile and feature), a zero tile of keys, zero rows
+    v[0] *= np.exp2(r.integers(-20, 21, size=(1, d))).astype(np.float32)
+    v[0, 32:64] = 0.0
+    v[0, r.integers(0, T, size=5)] = 0.0
     bu[:] = 0.0
     bv[:] = 0.0
     say("attention wide row scales", left, right)
     arrs = (q, k, v, rk, bu, bv)
     out = run_gpu(gpu, arrs, T, d, H, left, right, 1)
-    check(out, arrs, H, left, right)
+    # the bar per feature: a context column's error scales with that column of V
+    ref = relpos_attention(q[0], k[0], v[0], rk, bu, bv, H, left, right)
+    err = np.abs(out[0] - ref)
+    lim = RTOL * np.abs(ref) + VTOL * np.abs(v[0]).max(axis=0, keepdims=True)
+    assert np.isfinite(out[0]).all()
+    assert (err <= lim).all(), f"{int((err > lim).sum())} outside, worst ratio {(err / lim).max():.3g}"
 
 
 def test_relpos_attention_segments_independent(gpu):
