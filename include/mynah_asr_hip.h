@@ -216,9 +216,12 @@ int mynah_asr_hip_read_floor_dev(const void *p, size_t bytes, void *stream);
  * independent equal-length segments in one launch (the reference calls the
  * layer once per segment). All pointers 16-byte aligned. ctx may not alias
  * q, k or v. Outputs are f32 sums in another order than the reference's BLAS
- * (full attention forms its scores from f16 hi + lo splits of each row scaled
- * by a power of two, 22 bits of the row's maximum): equal within
- * |y - ref| <= 1e-4*|ref| + 1e-5*max|v|. */
+ * (full attention forms its products from f16 hi + lo splits scaled by
+ * powers of two, 22 bits of each row's, or V tile column's, maximum): equal
+ * within |y - ref| <= 1e-4*|ref| + 1e-5*max|v|. Full attention first splits
+ * K, rk and V into the calling thread's workspace (the size of K + V + rk,
+ * grown as needed, as the other _dev calls' buffers are); 2T * d must stay
+ * below 2^31. */
 /* The same on host buffers, one segment (the call encoder.c's attention() and
  * attention_banded() would make in place of their per-head loops, after rk is
  * formed): copies in, computes, copies ctx out. d must be a multiple of 4. */

@@ -1157,6 +1157,7 @@ int mynah_asr_hip_relpos_attention_dev(const float *q, const float *k, const flo
                                        int H, int left, int right, int nseq, void *stream) {
     Ctx *c;
     if (begin(&c)) return -1;
+    note_capture(pick_stream(stream));   // the split workspace may grow
     if (!q || !k || !v || !rk || !bias_u || !bias_v || !ctx || T < 0 || nseq < 0 || H <= 0 || d <= 0 ||
         d % H != 0)
         return fail("bad argument");
