@@ -771,6 +771,7 @@ int enc_check(const mynah_asr_hip_enc_layer *L, int T, int nseq, int d, int H, i
     if (!L || T < 0 || nseq < 0 || d <= 0 || H <= 0 || d % H != 0 || conv_k <= 0) return fail("bad argument");
     if (!mh_enc_d_supported(d)) return fail("encoder layer: d must be 256 times 1 to 8, 12 or 16");
     if (!mh_attn_supported(d / H)) return fail("head size must be 64 or 128");
+    if ((size_t)2 * T * d >= 0x7fffffffu) return fail("attention: 2 T d must stay below 2^31");
     const mynah_asr_hip_weight *sq[] = {L->q_w, L->k_w, L->v_w, L->o_w, L->relk_w, L->pw2_w};
     for (const mynah_asr_hip_weight *w : sq)
         if (!w || w->dw.n != d || w->dw.k != d) return fail("encoder layer: q/k/v/o/relk/pw2 must be [d, d]");
@@ -1167,6 +1168,7 @@ int mynah_asr_hip_relpos_attention_dev(const float *q, const float *k, const flo
     for (const void *p : ptrs)
         if ((uintptr_t)p % 16) return fail("attention buffers must be 16-byte aligned");
     if (ctx == q || ctx == k || ctx == v) return fail("ctx may not alias q, k or v");
+    if ((size_t)2 * T * d >= 0x7fffffffu) return fail("attention: 2 T d must stay below 2^31");
     if (T == 0 || nseq == 0) return 0;
     const size_t wb = mh_attn_ws_bytes(T, d, H, nseq, left);
     void *ws = wb ? c->attw.get(wb) : nullptr;
