@@ -40,9 +40,9 @@
 // lo = f16(x 2^e - hi)), which hold x to 2^-22 of the row's maximum; a score
 // is hi.hi + hi.lo + lo.hi summed in f32 (the dropped lo.lo is below 2^-22 of
 // the same scale) and multiplied by 2^-(e_q + e_k), which is exact. The
-// context update splits the probabilities (<= 1) at the fixed scale 2^14 and
-// V per (tile of 32 keys, feature), and undoes both per tile with one exact
-// power of two. K, rk and V are split once per call by pre-passes
+// context update splits the probabilities (<= 256: the running maximum
+// moves only by steps above 2^8) at the fixed scale 2^6 and V per (tile of
+// 32 keys, feature), and undoes both per tile with one exact power of two. K, rk and V are split once per call by pre-passes
 // (k_attn_split, k_attn_split_v); the q rows once per wave. The softmax
 // stays fp32.
 //
@@ -121,8 +121,8 @@ __device__ __forceinline__ void split_h(float x, int s, _Float16 &hi, _Float16 &
 // call by k_attn_split instead of by every workgroup that stages a row
 // V likewise, per tile of 32 keys (from key 0) and transposed: planes
 // [segment][tile][d][32], and per (segment, tile, feature) the scale
-// 2^-(14 + e) that undoes both the feature's exponent e and the
-// probabilities' fixed 2^14
+// 2^-(6 + e) that undoes both the feature's exponent e and the
+// probabilities' fixed 2^6
 struct SplitIn {
     const _Float16 *kh, *kl, *rh, *rl;
     const int *ke, *re;
@@ -570,21 +570,55 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
                 }
         }
         // 4. online softmax over the tile
-        float alpha[4];
+        if constexpr (SPL) {
+            // The running maxima move only when some row of the wave would
+            // exceed its maximum by more than 2^8 (base 2): the probabilities
+            // stay <= 256, the context and the sum carry the same maximum,
+            // and most tiles skip the rescale.
+            float mx[4];
+            bool grow = false;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float mx = max16(fmaxf(sv[0][e], sv[1][e]));
-            const float mn = fmaxf(m[e], mx);
-            alpha[e] = exp2f(m[e] - mn);
-            m[e] = mn;
-            sv[0][e] = exp2f(sv[0][e] - mn);
-            sv[1][e] = exp2f(sv[1][e] - mn);
-            l[e] = l[e] * alpha[e] + sum16(sv[0][e] + sv[1][e]);
+            for (int e = 0; e < 4; e++) {
+                mx[e] = max16(fmaxf(sv[0][e], sv[1][e]));
+                grow |= mx[e] > m[e] + 8.0f;
+            }
+            if (__any(grow)) {
+                float alpha[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float mn = fmaxf(m[e], mx[e]);
+                    alpha[e] = exp2f(m[e] - mn);
+                    m[e] = mn;
+                    l[e] *= alpha[e];
+                }
+#pragma unroll
+                for (int n = 0; n < NT; n++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[n][e] *= alpha[e];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                sv[0][e] = exp2f(sv[0][e] - m[e]);
+                sv[1][e] = exp2f(sv[1][e] - m[e]);
+                l[e] += sum16(sv[0][e] + sv[1][e]);
+            }
+        } else {
+            float alpha[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float mx = max16(fmaxf(sv[0][e], sv[1][e]));
+                const float mn = fmaxf(m[e], mx);
+                alpha[e] = exp2f(m[e] - mn);
+                m[e] = mn;
+                sv[0][e] = exp2f(sv[0][e] - mn);
+                sv[1][e] = exp2f(sv[1][e] - mn);
+                l[e] = l[e] * alpha[e] + sum16(sv[0][e] + sv[1][e]);
+            }
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[n][e] *= alpha[e];
         }
-#pragma unroll
-        for (int n = 0; n < NT; n++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) acc[n][e] *= alpha[e];
         // 5. probabilities to the A layout (row c, keys 8g .. 8g+7), then P . V
         wave_lds_order();   // the band reads above precede these writes
 #pragma unroll
@@ -595,13 +629,13 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
         const f4 pa0 = *(const f4 *)(Pw + c * L::PS + 8 * g);
         const f4 pa1 = *(const f4 *)(Pw + c * L::PS + 8 * g + 4);
         if constexpr (SPL) {
-            // probabilities (<= 1) split at the fixed scale 2^14, V split by
+            // probabilities (<= 256) split at the fixed scale 2^6, V split by
             // the pre-pass; the tile's scales undone by an exact power of two
             h8 ph, pl;
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 _Float16 hh, ll;
-                split_h(u < 4 ? pa0[u] : pa1[u - 4], 14, hh, ll);
+                split_h(u < 4 ? pa0[u] : pa1[u - 4], 6, hh, ll);
                 ph[u] = hh;
                 pl[u] = ll;
             }
@@ -684,7 +718,7 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ x,
 // e that puts the tile's largest magnitude in [2^14, 2^15) (clamped to
 // [-100, 100], so that the scale below stays a normal float), the planes
 // hi = f16(v 2^e), lo = f16(v 2^e - hi) as [segment][tile][d][32] (keys past
-// T zero), and the scale 2^-(14 + e). Thread = (segment, tile, feature, 8
+// T zero), and the scale 2^-(6 + e). Thread = (segment, tile, feature, 8
 // keys): the 4 threads of a feature are consecutive lanes (the maximum is a
 // quad reduction), and a wave's stores cover 16 features' 64-byte rows.
 __global__ __launch_bounds__(256) void k_attn_split_v(const float *__restrict__ v, int T, int d, int nseq,
@@ -718,7 +752,7 @@ __global__ __launch_bounds__(256) void k_attn_split_v(const float *__restrict__ 
     }
     *(h8 *)(hi + fi * KT + 8 * part) = hv;
     *(h8 *)(lo + fi * KT + 8 * part) = lv;
-    if (part == 0) vs[fi] = __int_as_float((127 - 14 - ex) << 23);
+    if (part == 0) vs[fi] = __int_as_float((127 - 6 - ex) << 23);
 }
 
 size_t al256(size_t b) { return (b + 255) / 256 * 256; }
