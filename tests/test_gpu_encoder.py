@@ -71,6 +71,7 @@ CASES = [
     (256, 4, 512, 9, 29, 2, 1, True, False, -1, 0, M.Q8_0),
     (256, 2, 768, 5, 41, 2, 0, True, True, 12, 3, M.Q4_K),
     (1024, 8, 4096, 9, 120, 2, 0, False, True, -1, 0, M.Q8_0),
+    (256, 2, 512, 31, 45, 2, 1, True, True, -1, 0, M.Q8_0),   # k 31: the untiled depthwise conv
 ]
 
 
@@ -187,17 +188,18 @@ def ss_params(seed, C, n_mels, d, causal):
             "lin_w": 0.05 * g(d, C * F), "lin_b": 0.1 * g(d)}
 
 
-@pytest.mark.parametrize("causal", [0, 1])
-def test_subsampling_matches_oracle(gpu, causal):
+@pytest.mark.parametrize("causal,C", [(0, 64), (1, 64), (0, 320)])
+def test_subsampling_matches_oracle(gpu, causal, C):
     """mynah_asr_hip_subsampling_dev against the float64 restatement of
     src/subsampling.c:208-268 (oracle/encoder.py, pinned against the
     reference's direct loop): 3 segments of 203 frames of 80 mel features,
-    C = 64, d_model 256, xscale 2. Bar: |y - ref| <= 5e-6 * (|ref| + rms(ref))
+    C = 64 (and 320: the fused first stage's lanes take channels 4 at a
+    time, 256 per pass), d_model 256, xscale 2. Bar: |y - ref| <= 5e-6 * (|ref| + rms(ref))
     (measured worst 8.2e-7: f32-weight products and 9-term f32 convolution
     sums)."""
     import torch
-    say("subsampling, causal", causal)
-    C, nm, d, T, nseq = 64, 80, 256, 203, 3
+    say("subsampling, causal", causal, "channels", C)
+    nm, d, T, nseq = 80, 256, 203, 3
     p = ss_params(12, C, nm, d, causal)
     dev = M.DeviceSubsampling(gpu, p, causal)
     try:
