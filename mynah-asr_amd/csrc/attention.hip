@@ -54,6 +54,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include "fmt.h"
 #include "launch.h"
 
 namespace {
@@ -123,11 +124,18 @@ __device__ __forceinline__ void split_h(float x, int s, _Float16 &hi, _Float16 &
 // [segment][tile][d][32], and per (segment, tile, feature) the scale
 // 2^-(6 + e) that undoes both the feature's exponent e and the
 // probabilities' fixed 2^6
+//
+// xp (DK = 128, may be null): the context is written as the EXACT products'
+// prepared input (the f16 split of each row's 128-element chunks, a chunk
+// being one head, with the fold factors xpf, for M = nseq T rows padded to
+// mh_mpad(M)) in place of ctx, for the output projection.
 struct SplitIn {
     const _Float16 *kh, *kl, *rh, *rl;
     const int *ke, *re;
     const _Float16 *vh, *vl;
     const float *vs;
+    uint8_t *xp;
+    float *xpf;
 };
 
 __device__ __forceinline__ f4 mfma16(float a, float b, f4 c) {
@@ -671,6 +679,77 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
         }
     }
 
+    if constexpr (SPL && DK == 128) {
+        if (sp.xp) {
+            // The context rows as the output projection's prepared input: the
+            // values ctx would hold, split per (row, head) exactly as the
+            // products' preparation splits a 128-element chunk, re-laid out
+            // through LDS (free once every wave is past its last tile) into
+            // 16-byte fragment slots.
+            const int Kc = d / 128, chunk = blockIdx.y;
+            __syncthreads();
+            _Float16 *ph = (_Float16 *)lds + w * 4096, *pl = ph + 2048;   // [16 rows][128], hi then lo
+            float fold[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int t = tw + 4 * g + e;
+                const float inv = t < T ? 1.0f / l[e] : 0.0f;
+                float vv[NT], a = 0.0f;
+#pragma unroll
+                for (int n = 0; n < NT; n++) {
+                    vv[n] = acc[n][e] * inv;
+                    a = fmaxf(a, fabsf(vv[n]));
+                }
+                a = max16(a);
+                const int sh = chunk_shift(a);
+                fold[e] = ldexpf(1.0f, -sh);
+#pragma unroll
+                for (int n = 0; n < NT; n++) {
+                    const float xs = ldexpf(vv[n], sh);
+                    const _Float16 hh = (_Float16)xs;
+                    ph[(4 * g + e) * 128 + 16 * n + c] = hh;
+                    pl[(4 * g + e) * 128 + 16 * n + c] = (_Float16)(xs - (float)hh);
+                }
+            }
+            wave_lds_order();
+            const size_t mb = (size_t)blockIdx.z * T;
+            // 512 slots per wave: lanes run along the 16 rows, so a store covers
+            // consecutive slots of one (half-step, term, half)
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int pc = lane + 64 * i, r16 = pc & 15, q = pc >> 4;
+                const int plane = q >> 4, hu = (q >> 1) & 7, hh = q & 1;
+                const int t = tw + r16;
+                if (t < T) {
+                    const size_t m = mb + t;
+                    const uint4 val = *(const uint4 *)((plane ? pl : ph) + r16 * 128 + 16 * hu + 8 * hh);
+                    *(uint4 *)(sp.xp + ((((m >> 5) * Kc + chunk) * 8 + hu) * 2 * 64 + plane * 64 + (m & 31) +
+                                        32 * hh) * 16) = val;
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int t = tw + 4 * g + e;
+                if (t < T && c == 0) {
+                    const size_t m = mb + t;
+                    sp.xpf[((m >> 5) * Kc + chunk) * 32 + (m & 31)] = fold[e];
+                }
+            }
+            // the rows past M up to the 64-row padding: zeros (fold factor 1),
+            // as the preparation pads; by the last block of the last segment
+            if (blockIdx.z == gridDim.z - 1 && blockIdx.x == gridDim.x - 1 && w == 0) {
+                const size_t M = (size_t)gridDim.z * T, Mp = (M + 63) / 64 * 64;
+                for (size_t i = lane; i < (Mp - M) * 32; i += 64) {
+                    const size_t m = M + (i >> 5);
+                    const int q = (int)(i & 31), plane = q >> 4, hu = (q >> 1) & 7, hh = q & 1;
+                    *(uint4 *)(sp.xp + ((((m >> 5) * Kc + chunk) * 8 + hu) * 2 * 64 + plane * 64 + (m & 31) +
+                                        32 * hh) * 16) = make_uint4(0, 0, 0, 0);
+                    if (q == 0) sp.xpf[((m >> 5) * Kc + chunk) * 32 + (m & 31)] = 1.0f;
+                }
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         const int t = tw + 4 * g + e;
@@ -784,9 +863,10 @@ hipError_t launch_split(const float *x, size_t rows, int d, _Float16 *hi, _Float
 template <int DK, int NW, bool SPL>
 hipError_t launch_attn(const float *q, const float *k, const float *v, const float *rk, const float *bu,
                          const float *bv, float *ctx, int T, int d, int H, int left, int right, int nseq,
-                         void *ws, hipStream_t st) {
+                         void *ws, uint8_t *xp, float *xpf, hipStream_t st) {
     if ((size_t)(2 * (size_t)T) * d >= 0x7fffffffu) return hipErrorInvalidValue;   // 32-bit row offsets
     if (SPL && left >= 0) return hipErrorInvalidValue;   // the split path assumes the full window
+    if (xp && !(SPL && DK == 128)) return hipErrorInvalidValue;   // the prepared output: split path, dk 128
     SplitIn sp{};
     if constexpr (SPL) {
         if (!ws) return hipErrorInvalidValue;
@@ -808,7 +888,7 @@ hipError_t launch_attn(const float *q, const float *k, const float *v, const flo
             e = hipGetLastError();
         }
         if (e != hipSuccess) return e;
-        sp = SplitIn{kh, kl, rh, rl, ke, re, vh, vl, vsc};
+        sp = SplitIn{kh, kl, rh, rl, ke, re, vh, vl, vsc, DK == 128 ? xp : nullptr, xpf};
     }
     using L = AttnLds<DK, NW, SPL>;
     const size_t bytes = sizeof(float) * L::TOTAL;
@@ -836,14 +916,14 @@ bool use8(int T, int H, int left, int nseq) {
 template <int DK>
 hipError_t launch_dk(const float *q, const float *k, const float *v, const float *rk, const float *bu,
                      const float *bv, float *ctx, int T, int d, int H, int left, int right, int nseq, void *ws,
-                     hipStream_t st) {
+                     uint8_t *xp, float *xpf, hipStream_t st) {
     // Full attention computes its scores on the f16 MFMA from split operands
     // (18% faster at T = 750); chunked windows stage as many K / rk rows per
     // score they keep, so the splitting costs more than it saves there.
     if (use8(T, H, left, nseq))
-        return launch_attn<DK, 8, true>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, ws, st);
-    if (left >= 0) return launch_attn<DK, 2, false>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, ws, st);
-    return launch_attn<DK, 4, true>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, ws, st);
+        return launch_attn<DK, 8, true>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, ws, xp, xpf, st);
+    if (left >= 0) return launch_attn<DK, 2, false>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, ws, xp, xpf, st);
+    return launch_attn<DK, 4, true>(q, k, v, rk, bu, bv, ctx, T, d, H, left, right, nseq, ws, xp, xpf, st);
 }
 
 }  // namespace
@@ -857,9 +937,14 @@ size_t mh_attn_ws_bytes(int T, int d, int H, int nseq, int left) {
 
 hipError_t mh_launch_relpos_attn(const float *q, const float *k, const float *v, const float *rk,
                                  const float *bias_u, const float *bias_v, float *ctx, int T, int d, int H,
-                                 int left, int right, int nseq, void *ws, hipStream_t st) {
+                                 int left, int right, int nseq, void *ws, uint8_t *xp, float *xpf,
+                                 hipStream_t st) {
     const int dk = d / H;
-    if (dk == 128) return launch_dk<128>(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, ws, st);
-    if (dk == 64) return launch_dk<64>(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, ws, st);
+    if (dk == 128)
+        return launch_dk<128>(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, ws, xp, xpf, st);
+    if (dk == 64 && !xp)
+        return launch_dk<64>(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, ws, nullptr, nullptr, st);
     return hipErrorInvalidValue;
 }
+
+bool mh_attn_preps_out(int d, int H, int left) { return left < 0 && H > 0 && d / H == 128; }

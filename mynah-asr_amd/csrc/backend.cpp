@@ -820,8 +820,9 @@ int enc_half_ffn(Ctx *c, const mynah_asr_hip_weight *w1, const mynah_asr_hip_wei
 // Whether the products W[0..n) of one layer-norm output xn all read it as
 // the EXACT GEMM path's prepared input (no GEMV, no row sums, K = Kp = d):
 // then the layer norm writes that input directly.
-// MYNAH_ASR_HIP_LN_PREP=0 turns this off (f32 rows, then the products'
-// own preparation: the same bits, one more pass).
+// MYNAH_ASR_HIP_LN_PREP=0 turns this off, here and for the attention core's
+// output (f32 rows, then the products' own preparation: the same bits, one
+// more pass).
 bool ln_preps(const mynah_asr_hip_weight *const *W, int n, int M, int d) {
     const char *env = getenv("MYNAH_ASR_HIP_LN_PREP");
     if ((env && env[0] == '0') || !mh_add_ln_prep_supported(d)) return false;
@@ -909,12 +910,34 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
         const size_t wb = mh_attn_ws_bytes(T, d, H, nseq, left);
         void *ws = wb ? c->attw.get(wb) : nullptr;
         if (wb && !ws) return fail("device buffer allocation failed");
-        ENC_TRY(mh_launch_relpos_attn(q, k, v, rk, L->bias_u, L->bias_v, ctx, T, d, H, left, right, nseq, ws, st));
+        // the context as the output projection's prepared input (tagged ctx),
+        // when that product takes the EXACT GEMM path
+        uint8_t *xp = nullptr;
+        float *xpf = nullptr;
+        c->pa.src = nullptr;
+        if (mh_attn_preps_out(d, H, left) && ln_preps(&L->o_w, 1, M, d)) {
+            size_t bs[3];
+            prep_sizes(0, mh_mpad(M), d, bs);
+            xp = (uint8_t *)c->pa.xp.get(bs[0]);
+            float *xs16 = (float *)c->pa.xs16.get(bs[1]);
+            xpf = (float *)c->pa.xpf.get(bs[2]);
+            if (!xp || !xs16 || !xpf) return fail("workspace allocation failed");
+        }
+        ENC_TRY(mh_launch_relpos_attn(q, k, v, rk, L->bias_u, L->bias_v, ctx, T, d, H, left, right, nseq, ws, xp,
+                                      xpf, st));
+        if (xp) {
+            c->pa.T = M;
+            c->pa.Kp = d;
+            c->pa.xsum = 0;
+            c->pa.i8 = 0;
+            c->pa.src = ctx;
+        }
     }
     {
         NumScope so(eff_num(L->o_w->qtype, d, M));
         if (gemm_dev(c, L->o_w, ctx, tmp, M, 0, st)) return -1;
     }
+    c->pa.src = nullptr;
     if (bias_add(tmp, L->o_b, M, d, st)) return -1;
     // x += tmp; conv module on LN(x) (:503-507, 413-462)
     if (enc_add_ln(c, x, tmp, 1.0f, L->ln_conv_w, L->ln_conv_b, xn, M, d, &L->pw1_w, 1, st)) return -1;
@@ -1174,7 +1197,7 @@ int mynah_asr_hip_relpos_attention_dev(const float *q, const float *k, const flo
     void *ws = wb ? c->attw.get(wb) : nullptr;
     if (wb && !ws) return fail("device buffer allocation failed");
     hipError_t e = mh_launch_relpos_attn(q, k, v, rk, bias_u, bias_v, ctx, T, d, H, left, right, nseq, ws,
-                                         pick_stream(stream));
+                                         nullptr, nullptr, pick_stream(stream));
     if (e != hipSuccess) return fail("attention launch failed", hipGetErrorString(e));
     return 0;
 }

@@ -109,12 +109,17 @@ hipError_t mh_launch_gemm_i8(int qtype, const DevW &W, const uint8_t *qx, const 
 
 // Relative-position self-attention core (attention.hip): head size d / H of 64 or 128
 bool mh_attn_supported(int dk);
-// ws: mh_attn_ws_bytes of device workspace (full attention splits K and rk
-// into f16 planes there first; may be null when that is 0)
+// ws: mh_attn_ws_bytes of device workspace (full attention splits K, rk and
+// V into f16 planes there first; may be null when that is 0). xp, xpf (null,
+// or when mh_attn_preps_out): the context written as the EXACT products'
+// prepared input of the M = nseq T rows (xp: mh_mpad(M) * d * 4 bytes, xpf:
+// mh_mpad(M) * d / 128 floats) instead of into ctx.
 size_t mh_attn_ws_bytes(int T, int d, int H, int nseq, int left);
+bool mh_attn_preps_out(int d, int H, int left);
 hipError_t mh_launch_relpos_attn(const float *q, const float *k, const float *v, const float *rk,
                                  const float *bias_u, const float *bias_v, float *ctx, int T, int d, int H,
-                                 int left, int right, int nseq, void *ws, hipStream_t st);
+                                 int left, int right, int nseq, void *ws, uint8_t *xp, float *xpf,
+                                 hipStream_t st);
 
 // Encoder layer steps around the products (encoder.hip). d: 256 * {1..8, 12,
 // 16} for the layer norm (mh_enc_d_supported), a multiple of 4 for the rest.
