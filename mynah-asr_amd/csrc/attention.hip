@@ -44,7 +44,8 @@
 // moves only by steps above 2^8) at the fixed scale 2^6 and V per (tile of
 // 32 keys, feature), and undoes both per tile with one exact power of two. K, rk and V are split once per call by pre-passes
 // (k_attn_split, k_attn_split_v); the q rows once per wave. The softmax
-// stays fp32.
+// stays fp32. With dk = 128 the context can be written directly as the output
+// projection's prepared input (SplitIn::xp) instead of as f32 rows.
 //
 // MFMA 16x16x4 f32 operand layout (lane l, c = l & 15, g = l >> 4):
 //   A: row c, k-slot g;  B: column c, k-slot g;  D: rows 4g + e (e = 0..3), column c.

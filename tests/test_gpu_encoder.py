@@ -126,11 +126,12 @@ def test_encoder_layer_segments_are_independent(gpu):
 @pytest.mark.parametrize("d,f,biases,qt", [(1024, 4096, False, M.Q8_0), (256, 512, True, M.Q8_0),
                                            (512, 1024, False, M.Q4_K)])
 def test_encoder_layer_ln_prep_bit_identical(gpu, monkeypatch, d, f, biases, qt):
-    """Layer norms that write the products' prepared input directly (the
-    default whenever every product of a norm's output takes the EXACT GEMM
-    path) give the bits of the layer with f32 norm outputs and the products'
-    own preparation (MYNAH_ASR_HIP_LN_PREP=0): the same split of the same
-    values. Q4_K products read row sums, so that layer keeps f32 rows."""
+    """Layer norms, and the attention core for the output projection, that
+    write the products' prepared input directly (the default whenever every
+    product of that output takes the EXACT GEMM path) give the bits of the
+    layer with f32 outputs and the products' own preparation
+    (MYNAH_ASR_HIP_LN_PREP=0): the same split of the same values. Q4_K
+    products read row sums, so that layer keeps f32 rows."""
     import torch
     say("encoder layer ln prep", d, f, biases, qt)
     H, k, T, nseq = d // 128, 9, 150, 2
