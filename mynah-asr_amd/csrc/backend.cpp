@@ -951,14 +951,34 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
     // the GLU (g = q, free now) folded into the depthwise conv where it can be
     const bool glu_dw = mh_glu_dwconv_supported(d, conv_k);
     if (!glu_dw) ENC_TRY(mh_launch_glu(h, q, M, d, st));
-    auto dwconv = [&](const float *sc, const float *sh, float *o) {
-        return glu_dw ? mh_launch_glu_dwconv(h, dwt, L->dw_b, sc, sh, o, T, nseq, d, conv_k, causal, st)
+    auto dwconv = [&](const float *sc, const float *sh, float *o, uint8_t *xp, float *xpf) {
+        return glu_dw ? mh_launch_glu_dwconv(h, dwt, L->dw_b, sc, sh, o, T, nseq, d, conv_k, causal, xp, xpf, st)
                       : mh_launch_dwconv(q, dwt, L->dw_b, sc, sh, o, T, nseq, d, conv_k, causal, st);
     };
     if (L->cnorm_scale) {
-        ENC_TRY(dwconv(L->cnorm_scale, L->cnorm_shift, k));
+        // with the folded batch norm the conv's output feeds only pw2: written
+        // as its prepared input (tagged k) when pw2 takes the EXACT GEMM path
+        uint8_t *xp = nullptr;
+        float *xpf = nullptr;
+        c->pa.src = nullptr;
+        if (glu_dw && ln_preps(&L->pw2_w, 1, M, d)) {
+            size_t bs[3];
+            prep_sizes(0, mh_mpad(M), d, bs);
+            xp = (uint8_t *)c->pa.xp.get(bs[0]);
+            float *xs16 = (float *)c->pa.xs16.get(bs[1]);
+            xpf = (float *)c->pa.xpf.get(bs[2]);
+            if (!xp || !xs16 || !xpf) return fail("workspace allocation failed");
+        }
+        ENC_TRY(dwconv(L->cnorm_scale, L->cnorm_shift, k, xp, xpf));
+        if (xp) {
+            c->pa.T = M;
+            c->pa.Kp = d;
+            c->pa.xsum = 0;
+            c->pa.i8 = 0;
+            c->pa.src = k;
+        }
     } else {
-        ENC_TRY(dwconv(nullptr, nullptr, v));
+        ENC_TRY(dwconv(nullptr, nullptr, v, nullptr, nullptr));
         ENC_TRY(mh_launch_add_ln(v, nullptr, 0.0f, L->cnorm_w, L->cnorm_b, k, M, d, st));
         ENC_TRY(mh_launch_silu(k, md, st));
     }
@@ -966,6 +986,7 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
         NumScope s2(eff_num(L->pw2_w->qtype, d, M));
         if (gemm_dev(c, L->pw2_w, k, tmp, M, 0, st)) return -1;
     }
+    c->pa.src = nullptr;
     if (bias_add(tmp, L->pw2_b, M, d, st)) return -1;
     // x += tmp; 1/2 FFN2 on LN(x) (:508-511)
     if (enc_add_ln(c, x, tmp, 1.0f, L->ln_ff2_w, L->ln_ff2_b, xn, M, d, &L->ff2_w1, 1, st)) return -1;

@@ -233,12 +233,23 @@ __global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ g, con
 // GLU: g is formed from pw1's output h [rows][2d] as it is staged (k_glu's
 // operations; the halo rows' values are formed again by the next tile).
 constexpr int DW_R = 32;
-template <bool GLU>
+// PREP: the output rows are written as the EXACT products' prepared input
+// (xp, xpf, for M = nseq T rows padded to 64, as k_add_ln_prep writes it)
+// instead of into out: per (row, 128-channel chunk: 32 lanes) the split the
+// preparation forms, held in registers until the tile is done, then staged
+// in the input rows' LDS so the stores run along rows.
+template <bool GLU, bool PREP>
 __global__ __launch_bounds__(256) void k_dwconv_tile(const float *__restrict__ g, const float *__restrict__ wt,
                                                      const float *__restrict__ bias, const float *__restrict__ scale,
                                                      const float *__restrict__ shift, float *__restrict__ out,
-                                                     int T, int d, int k, int pc) {
-    extern __shared__ float4 dws[];   // [DW_R + k - 1][64] rows of g, then [k][64] taps
+                                                     int T, int d, int k, int pc, uint8_t *__restrict__ xp,
+                                                     float *__restrict__ xpf) {
+    // [DW_R + k - 1][64] rows of g, then [k][64] taps; PREP, once the tile is
+    // done: the staged slots [DW_R rows][2 chunks][8 half-steps][2 terms][2
+    // halves] over the rows, the fold factors [DW_R][2] over the taps
+    extern __shared__ float4 dws[];
+    uint2 ph[PREP ? DW_R / 4 : 1], pl[PREP ? DW_R / 4 : 1];
+    float pf[PREP ? DW_R / 4 : 1];
     const int tid = threadIdx.x, q = tid & 63, t0 = blockIdx.x * DW_R, c0 = blockIdx.y * 256;
     const int nrow = DW_R + k - 1;
     const int gw = GLU ? 2 * d : d;   // the input's row width
@@ -267,8 +278,9 @@ __global__ __launch_bounds__(256) void k_dwconv_tile(const float *__restrict__ g
         sh = *(const float4 *)(shift + i);
     }
     float *os = out + (size_t)blockIdx.z * T * d + i;
-    for (int rr = tid >> 6; rr < DW_R; rr += 4) {
-        const int t = t0 + rr;
+#pragma unroll
+    for (int u = 0; u < DW_R / 4; u++) {
+        const int rr = (tid >> 6) + 4 * u, t = t0 + rr;
         if (t >= T) break;
         const int j0 = t - pc < 0 ? pc - t : 0, j1 = t - pc + k > T ? T - t + pc : k;
         float4 o = b0;
@@ -285,7 +297,78 @@ __global__ __launch_bounds__(256) void k_dwconv_tile(const float *__restrict__ g
             o.z = silu_e(fmaf(o.z, sc.z, sh.z));
             o.w = silu_e(fmaf(o.w, sc.w, sh.w));
         }
-        *(float4 *)(os + (size_t)t * d) = o;
+        if constexpr (PREP) {
+            // lanes 32 cl .. 32 cl + 31 hold chunk cl's 128 channels of row t
+            float a = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
+#pragma unroll
+            for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+            const int shf = chunk_shift(a);
+            const float xs[4] = {ldexpf(o.x, shf), ldexpf(o.y, shf), ldexpf(o.z, shf), ldexpf(o.w, shf)};
+            _Float16 hv[4], lv[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                hv[j] = (_Float16)xs[j];
+                lv[j] = (_Float16)(xs[j] - (float)hv[j]);
+            }
+            __builtin_memcpy(&ph[u], hv, 8);
+            __builtin_memcpy(&pl[u], lv, 8);
+            pf[u] = ldexpf(1.0f, -shf);
+        } else {
+            *(float4 *)(os + (size_t)t * d) = o;
+        }
+    }
+    if constexpr (PREP) {
+        __syncthreads();   // every wave is done with the input rows and the taps
+        float4 *stage = dws;
+        float *fold = (float *)taps;
+        {
+            const int l32 = q & 31, cl = q >> 5, hu = l32 >> 2, hh = (l32 >> 1) & 1;
+#pragma unroll
+            for (int u = 0; u < DW_R / 4; u++) {
+                const int rr = (tid >> 6) + 4 * u;
+                if (t0 + rr >= T) break;
+                uint8_t *o8 = (uint8_t *)(stage + (((rr * 2 + cl) * 8 + hu) * 2) * 2 + hh) + 8 * (l32 & 1);
+                *(uint2 *)o8 = ph[u];
+                *(uint2 *)(o8 + 2 * 16) = pl[u];   // term 1: two slots on
+                if (l32 == 0) fold[rr * 2 + cl] = pf[u];
+            }
+        }
+        __syncthreads();
+        const int Kc = d / 128;
+        const size_t mb = (size_t)blockIdx.z * T;
+        // 2048 slots; consecutive threads run along the 32 rows
+        for (int p = tid; p < DW_R * 64; p += 256) {
+            const int rr = p & 31, rest = p >> 5;
+            const int cl = rest >> 5, hu = (rest >> 2) & 7, term = (rest >> 1) & 1, hh = rest & 1;
+            const int t = t0 + rr;
+            if (t < T) {
+                const size_t m = mb + t;
+                const int chunk = 2 * blockIdx.y + cl;
+                *(float4 *)(xp + ((((m >> 5) * Kc + chunk) * 8 + hu) * 2 * 64 + term * 64 + (m & 31) + 32 * hh) * 16) =
+                    stage[(((rr * 2 + cl) * 8 + hu) * 2 + term) * 2 + hh];
+            }
+        }
+        if (tid < 64) {
+            const int rr = tid & 31, cl = tid >> 5, t = t0 + rr;
+            if (t < T) {
+                const size_t m = mb + t;
+                xpf[((m >> 5) * Kc + 2 * blockIdx.y + cl) * 32 + (m & 31)] = fold[rr * 2 + cl];
+            }
+        }
+        // the rows past M up to the 64-row padding: zeros (fold factor 1), as
+        // the preparation pads; by the last tile of the last segment
+        if (blockIdx.z == gridDim.z - 1 && blockIdx.x == gridDim.x - 1) {
+            const size_t M = (size_t)gridDim.z * T, Mp = (M + 63) / 64 * 64;
+            for (size_t i = tid; i < (Mp - M) * 64; i += 256) {
+                const size_t m = M + (i >> 6);
+                const int rest = (int)(i & 63), cl = rest >> 5, hu = (rest >> 2) & 7, term = (rest >> 1) & 1,
+                          hh = rest & 1;
+                const int chunk = 2 * blockIdx.y + cl;
+                *(float4 *)(xp + ((((m >> 5) * Kc + chunk) * 8 + hu) * 2 * 64 + term * 64 + (m & 31) + 32 * hh) * 16) =
+                    float4{0.f, 0.f, 0.f, 0.f};
+                if (rest == 0 || rest == 32) xpf[((m >> 5) * Kc + chunk) * 32 + (m & 31)] = 1.0f;
+            }
+        }
     }
 }
 
@@ -513,13 +596,19 @@ bool mh_glu_dwconv_supported(int d, int k) {
 
 hipError_t mh_launch_glu_dwconv(const float *h, const float *w, const float *bias, const float *scale,
                                 const float *shift, float *out, int T, int nseq, int d, int k, int causal,
-                                hipStream_t st) {
+                                uint8_t *xp, float *xpf, hipStream_t st) {
     if (T <= 0 || nseq <= 0) return hipSuccess;
     if (!mh_glu_dwconv_supported(d, k)) return hipErrorInvalidValue;
     const int pc = causal ? k - 1 : (k - 1) / 2;
-    const size_t lds = sizeof(float4) * 64 * (size_t)(DW_R + 2 * k - 1);
-    hipLaunchKernelGGL(k_dwconv_tile<true>, dim3((unsigned)((T + DW_R - 1) / DW_R), d / 256, nseq), dim3(256), lds, st,
-                       h, w, bias, scale, shift, out, T, d, k, pc);
+    const size_t lds = sizeof(float4) * 64 * (size_t)(DW_R + 2 * k - 1);   // >= the staged slots and folds
+    const dim3 grid((unsigned)((T + DW_R - 1) / DW_R), d / 256, nseq);
+    if (xp) {
+        hipLaunchKernelGGL((k_dwconv_tile<true, true>), grid, dim3(256), lds, st, h, w, bias, scale, shift, out, T, d,
+                           k, pc, xp, xpf);
+    } else {
+        hipLaunchKernelGGL((k_dwconv_tile<true, false>), grid, dim3(256), lds, st, h, w, bias, scale, shift, out, T, d,
+                           k, pc, nullptr, nullptr);
+    }
     return hipGetLastError();
 }
 
@@ -531,8 +620,8 @@ hipError_t mh_launch_dwconv(const float *g, const float *w, const float *bias, c
     const int pc = causal ? k - 1 : (k - 1) / 2;
     if (mh_glu_dwconv_supported(d, k)) {
         const size_t lds = sizeof(float4) * 64 * (size_t)(DW_R + 2 * k - 1);
-        hipLaunchKernelGGL(k_dwconv_tile<false>, dim3((unsigned)((T + DW_R - 1) / DW_R), d / 256, nseq), dim3(256),
-                           lds, st, g, w, bias, scale, shift, out, T, d, k, pc);
+        hipLaunchKernelGGL((k_dwconv_tile<false, false>), dim3((unsigned)((T + DW_R - 1) / DW_R), d / 256, nseq),
+                           dim3(256), lds, st, g, w, bias, scale, shift, out, T, d, k, pc, nullptr, nullptr);
         return hipGetLastError();
     }
     const size_t n = (size_t)nseq * T * (d / 4);

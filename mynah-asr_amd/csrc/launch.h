@@ -145,11 +145,14 @@ hipError_t mh_launch_dwconv(const float *g, const float *w, const float *bias, c
                             hipStream_t st);
 // GLU and the depthwise conv in one pass: h = pw1's output [rows][2d],
 // g = h[:, :d] * sigmoid(h[:, d:]) formed as it is read (bit-identical to
-// mh_launch_glu, then mh_launch_dwconv); for d a multiple of 256, k <= 16
+// mh_launch_glu, then mh_launch_dwconv); for d a multiple of 256, k <= 16.
+// xp, xpf (or null): the output as the EXACT products' prepared input
+// (mh_mpad(M) * d * 4 bytes, mh_mpad(M) * d / 128 floats, M = nseq T) in
+// place of out.
 bool mh_glu_dwconv_supported(int d, int k);
 hipError_t mh_launch_glu_dwconv(const float *h, const float *w, const float *bias, const float *scale,
                                 const float *shift, float *out, int T, int nseq, int d, int k, int causal,
-                                hipStream_t st);
+                                uint8_t *xp, float *xpf, hipStream_t st);
 
 // The dw_striding subsampling's steps (encoder.hip), channel-last activations
 // [segment][time][freq][channel] (C a multiple of 4); causal pads (2, 1),
