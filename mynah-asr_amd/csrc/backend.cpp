@@ -821,8 +821,8 @@ int enc_half_ffn(Ctx *c, const mynah_asr_hip_weight *w1, const mynah_asr_hip_wei
 // the EXACT GEMM path's prepared input (no GEMV, no row sums, K = Kp = d):
 // then the layer norm writes that input directly.
 // MYNAH_ASR_HIP_LN_PREP=0 turns this off, here and for the attention core's
-// output (f32 rows, then the products' own preparation: the same bits, one
-// more pass).
+// and the depthwise conv's outputs (f32 rows, then the products' own
+// preparation: the same bits, one more pass).
 bool ln_preps(const mynah_asr_hip_weight *const *W, int n, int M, int d) {
     const char *env = getenv("MYNAH_ASR_HIP_LN_PREP");
     if ((env && env[0] == '0') || !mh_add_ln_prep_supported(d)) return false;
