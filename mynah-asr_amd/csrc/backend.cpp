@@ -278,8 +278,11 @@ bool fits(const PrepBuf &P, const mynah_asr_hip_weight *W, int T) {
 bool prep_fits(const Ctx *c, const mynah_asr_hip_weight *W, int T) { return fits(c->pa, W, T); }
 
 // the product on a prepared input
+// act: 0 none, 1 SiLU; 2 and 3 (internal, the EXACT GEMM path only) add the
+// product, or half of it, into dy (the encoder layer's residual adds)
 int run_from(Ctx *c, const PrepBuf &P, const mynah_asr_hip_weight *W, float *dy, int T, int act, hipStream_t st) {
     hipError_t e;
+    if (act >= 2 && P.i8 != 0) return fail("internal: a residual epilogue outside the EXACT GEMM path");
     if (P.i8 == MH_I8_QMAT) {
         e = mh_launch_gemm_i8(W->qtype, W->dw, (const uint8_t *)P.xp.p, (const float *)P.xs16.p, dy, T, act, st);
     } else {
@@ -305,6 +308,7 @@ float *gemv_ws(Ctx *c, const mynah_asr_hip_weight *W) {
 int gemm_dev(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, float *dy, int T, int act,
              hipStream_t st) {
     if (num_now() == MYNAH_ASR_HIP_EXACT && mh_use_gemv(W->dw, T)) {
+        if (act >= 2) return fail("internal: a residual epilogue outside the EXACT GEMM path");
         const int vec = (W->dw.k % 8 == 0) && (((uintptr_t)dx & 15) == 0);
         hipError_t e = mh_launch_gemv(W->qtype, W->dw, dx, T, vec, dy, act, gemv_ws(c, W), st);
         if (e != hipSuccess) return fail("gemv launch failed", hipGetErrorString(e));
@@ -319,7 +323,7 @@ int gemm_dev(Ctx *c, const mynah_asr_hip_weight *W, const float *dx, float *dy, 
 // first product prepares the intermediate for the second in its epilogue
 // (no f32 intermediate, no preparation pass); otherwise two products.
 int ffn_dev(Ctx *c, const mynah_asr_hip_weight *W1, const mynah_asr_hip_weight *W2, const float *dx, float *dy,
-            int T, hipStream_t st) {
+            int T, hipStream_t st, int act2 = 0) {
     const int n1 = eff_num(W1->qtype, W1->dw.k, T), n2 = eff_num(W2->qtype, W2->dw.k, T);
     if (n1 != n2) {
         // (QMAT numerics: each product in its own mode, as qmat_ffn's two qmat_mul calls)
@@ -330,7 +334,7 @@ int ffn_dev(Ctx *c, const mynah_asr_hip_weight *W1, const mynah_asr_hip_weight *
             if (gemm_dev(c, W1, dx, dh, T, 1, st)) return -1;
         }
         NumScope s2(n2);
-        return gemm_dev(c, W2, dh, dy, T, 0, st);
+        return gemm_dev(c, W2, dh, dy, T, act2, st);
     }
     NumScope sc(n1);
     const bool fuse = num_now() == MYNAH_ASR_HIP_EXACT && !mh_use_gemv(W1->dw, T) &&
@@ -352,12 +356,12 @@ int ffn_dev(Ctx *c, const mynah_asr_hip_weight *W1, const mynah_asr_hip_weight *
         P.Kp = Kp;
         P.xsum = xsum;
         P.i8 = 0;
-        return run_from(c, P, W2, dy, T, 0, st);
+        return run_from(c, P, W2, dy, T, act2, st);
     }
     float *dh = (float *)c->h.get((size_t)T * W1->dw.n * sizeof(float));
     if (!dh) return fail("device buffer allocation failed");
     if (gemm_dev(c, W1, dx, dh, T, 1, st)) return -1;
-    return gemm_dev(c, W2, dh, dy, T, 0, st);
+    return gemm_dev(c, W2, dh, dy, T, act2, st);
 }
 
 // three products of one input: prepared once whenever it fits them all
@@ -800,8 +804,8 @@ int bias_add(float *y, const float *b, size_t rows, int n, hipStream_t st) {
 // half_ffn (encoder.c:464-483) on xn: the fused FFN when both biases are
 // absent, else product, bias, SiLU, product, bias
 int enc_half_ffn(Ctx *c, const mynah_asr_hip_weight *w1, const mynah_asr_hip_weight *w2, const float *b1,
-                 const float *b2, const float *xn, float *out, float *h, int M, hipStream_t st) {
-    if (!b1 && !b2) return ffn_dev(c, w1, w2, xn, out, M, st);
+                 const float *b2, const float *xn, float *out, float *h, int M, hipStream_t st, int act2 = 0) {
+    if (!b1 && !b2) return ffn_dev(c, w1, w2, xn, out, M, st, act2);
     const int f = w1->dw.n;
     {
         NumScope s1(eff_num(w1->qtype, w1->dw.k, M));
@@ -820,12 +824,16 @@ int enc_half_ffn(Ctx *c, const mynah_asr_hip_weight *w1, const mynah_asr_hip_wei
 // Whether the products W[0..n) of one layer-norm output xn all read it as
 // the EXACT GEMM path's prepared input (no GEMV, no row sums, K = Kp = d):
 // then the layer norm writes that input directly.
-// MYNAH_ASR_HIP_LN_PREP=0 turns this off, here and for the attention core's
-// and the depthwise conv's outputs (f32 rows, then the products' own
-// preparation: the same bits, one more pass).
-bool ln_preps(const mynah_asr_hip_weight *const *W, int n, int M, int d) {
+// The encoder layer's fused hand-offs (prepared inputs written by their
+// producers, residual adds in the products' epilogues) are on unless
+// MYNAH_ASR_HIP_LN_PREP=0 (f32 rows and separate passes: the same bits).
+bool enc_fused() {
     const char *env = getenv("MYNAH_ASR_HIP_LN_PREP");
-    if ((env && env[0] == '0') || !mh_add_ln_prep_supported(d)) return false;
+    return !(env && env[0] == '0');
+}
+
+bool ln_preps(const mynah_asr_hip_weight *const *W, int n, int M, int d) {
+    if (!enc_fused() || !mh_add_ln_prep_supported(d)) return false;
     for (int i = 0; i < n; i++)
         if (eff_num(W[i]->qtype, W[i]->dw.k, M) != MYNAH_ASR_HIP_EXACT || mh_use_gemv(W[i]->dw, M) ||
             wants_xsum(W[i]->qtype) || W[i]->dw.k != d || W[i]->dw.Kp != d)
@@ -889,12 +897,23 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
     // 1/2 FFN1 (:492-494)
     // (each layer norm whose output only feeds products tags the prepared
     // input with xn; the tag is cleared once those products have run)
+    //
+    // A product with no bias on the EXACT GEMM path adds its output into x
+    // itself (x += tmp or x += tmp / 2, the same operations as the layer
+    // norm's residual add), and the next layer norm reads x alone.
+    auto res_ok = [&](const mynah_asr_hip_weight *W, bool biased) {
+        return !biased && enc_fused() && eff_num(W->qtype, W->dw.k, M) == MYNAH_ASR_HIP_EXACT &&
+               !mh_use_gemv(W->dw, M);
+    };
     if (enc_add_ln(c, x, nullptr, 0.0f, L->ln_ff1_w, L->ln_ff1_b, xn, M, d, &L->ff1_w1, 1, st)) return -1;
-    if (enc_half_ffn(c, L->ff1_w1, L->ff1_w2, L->ff1_b1, L->ff1_b2, xn, tmp, hf, M, st)) return -1;
+    const bool r1 = res_ok(L->ff1_w2, L->ff1_b1 || L->ff1_b2);
+    if (enc_half_ffn(c, L->ff1_w1, L->ff1_w2, L->ff1_b1, L->ff1_b2, xn, r1 ? x : tmp, hf, M, st, r1 ? 3 : 0))
+        return -1;
     c->pa.src = nullptr;
     // x += 0.5 tmp; MHSA on LN(x) (:495-502)
     const mynah_asr_hip_weight *W3[3] = {L->q_w, L->k_w, L->v_w};
-    if (enc_add_ln(c, x, tmp, 0.5f, L->ln_att_w, L->ln_att_b, xn, M, d, W3, 3, st)) return -1;
+    if (enc_add_ln(c, x, r1 ? nullptr : tmp, r1 ? 0.0f : 0.5f, L->ln_att_w, L->ln_att_b, xn, M, d, W3, 3, st))
+        return -1;
     float *const y3[3] = {q, k, v};
     if (qkv_dev(c, W3, xn, y3, M, st)) return -1;
     c->pa.src = nullptr;
@@ -933,14 +952,17 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
             c->pa.src = ctx;
         }
     }
+    const bool r2 = res_ok(L->o_w, L->o_b != nullptr);
     {
         NumScope so(eff_num(L->o_w->qtype, d, M));
-        if (gemm_dev(c, L->o_w, ctx, tmp, M, 0, st)) return -1;
+        if (gemm_dev(c, L->o_w, ctx, r2 ? x : tmp, M, r2 ? 2 : 0, st)) return -1;
     }
     c->pa.src = nullptr;
     if (bias_add(tmp, L->o_b, M, d, st)) return -1;
     // x += tmp; conv module on LN(x) (:503-507, 413-462)
-    if (enc_add_ln(c, x, tmp, 1.0f, L->ln_conv_w, L->ln_conv_b, xn, M, d, &L->pw1_w, 1, st)) return -1;
+    if (enc_add_ln(c, x, r2 ? nullptr : tmp, r2 ? 0.0f : 1.0f, L->ln_conv_w, L->ln_conv_b, xn, M, d, &L->pw1_w, 1,
+                   st))
+        return -1;
     {
         NumScope s1(eff_num(L->pw1_w->qtype, d, M));
         if (gemm_dev(c, L->pw1_w, xn, h, M, 0, st)) return -1;
@@ -982,18 +1004,23 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
         ENC_TRY(mh_launch_add_ln(v, nullptr, 0.0f, L->cnorm_w, L->cnorm_b, k, M, d, st));
         ENC_TRY(mh_launch_silu(k, md, st));
     }
+    const bool r3 = res_ok(L->pw2_w, L->pw2_b != nullptr);
     {
         NumScope s2(eff_num(L->pw2_w->qtype, d, M));
-        if (gemm_dev(c, L->pw2_w, k, tmp, M, 0, st)) return -1;
+        if (gemm_dev(c, L->pw2_w, k, r3 ? x : tmp, M, r3 ? 2 : 0, st)) return -1;
     }
     c->pa.src = nullptr;
     if (bias_add(tmp, L->pw2_b, M, d, st)) return -1;
     // x += tmp; 1/2 FFN2 on LN(x) (:508-511)
-    if (enc_add_ln(c, x, tmp, 1.0f, L->ln_ff2_w, L->ln_ff2_b, xn, M, d, &L->ff2_w1, 1, st)) return -1;
-    if (enc_half_ffn(c, L->ff2_w1, L->ff2_w2, L->ff2_b1, L->ff2_b2, xn, tmp, hf, M, st)) return -1;
+    if (enc_add_ln(c, x, r3 ? nullptr : tmp, r3 ? 0.0f : 1.0f, L->ln_ff2_w, L->ln_ff2_b, xn, M, d, &L->ff2_w1, 1,
+                   st))
+        return -1;
+    const bool r4 = res_ok(L->ff2_w2, L->ff2_b1 || L->ff2_b2);
+    if (enc_half_ffn(c, L->ff2_w1, L->ff2_w2, L->ff2_b1, L->ff2_b2, xn, r4 ? x : tmp, hf, M, st, r4 ? 3 : 0))
+        return -1;
     c->pa.src = nullptr;
     // x += 0.5 tmp; x = LN_out(x) (:511-515)
-    ENC_TRY(mh_launch_add_ln(x, tmp, 0.5f, L->ln_out_w, L->ln_out_b, x, M, d, st));
+    ENC_TRY(mh_launch_add_ln(x, r4 ? nullptr : tmp, r4 ? 0.0f : 0.5f, L->ln_out_w, L->ln_out_b, x, M, d, st));
 #undef ENC_TRY
     return 0;
 }
@@ -1099,6 +1126,7 @@ size_t mynah_asr_hip_weight_bytes(const mynah_asr_hip_weight *w) { return w ? w-
 
 int mynah_asr_hip_qgemm_dev(const mynah_asr_hip_weight *w, const float *dx, float *dy, int T, int act,
                             void *stream) {
+    act = act != 0;   // 0 none, anything else SiLU (the residual modes are internal)
     Ctx *c;
     if (begin(&c)) return -1;
     note_capture(pick_stream(stream));
@@ -1111,6 +1139,7 @@ int mynah_asr_hip_qgemm_dev(const mynah_asr_hip_weight *w, const float *dx, floa
 
 int mynah_asr_hip_qgemm_noalloc_dev(const mynah_asr_hip_weight *w, const float *dx, float *dy, int T, int act,
                                     void *stream) {
+    act = act != 0;   // 0 none, anything else SiLU (the residual modes are internal)
     // no begin(): that creates the thread's stream; this call uses `stream`
     // as given (NULL = the null stream) and allocates nothing
     t_err[0] = 0;
@@ -1141,6 +1170,7 @@ int mynah_asr_hip_prep_dev(const mynah_asr_hip_weight *w, const float *dx, int T
 
 int mynah_asr_hip_qgemm_prepped_dev(const mynah_asr_hip_weight *w, float *dy, int T, int act,
                                     void *stream) {
+    act = act != 0;   // 0 none, anything else SiLU (the residual modes are internal)
     Ctx *c;
     if (begin(&c)) return -1;
     note_capture(pick_stream(stream));

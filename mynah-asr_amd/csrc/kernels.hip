@@ -437,6 +437,16 @@ struct PrepOut {
 #ifndef GQ_OCC
 #define GQ_OCC 3
 #endif
+// The products' output epilogue (k_gemm_fold's; k_gemm's spells it out): act
+// 1 SiLU; act 2 and 3 accumulate into y, y = fmaf(1 or 1/2, v, y) (the
+// residual adds x += tmp and x += tmp / 2 of the encoder layer, with their
+// operations); otherwise v.
+__device__ __forceinline__ float epi_out(int act, float v, const float *yp) {
+    if (act == 1) return silu_f(v);
+    if (act >= 2) return fmaf(act == 3 ? 0.5f : 1.0f, v, *yp);
+    return v;
+}
+
 template <int QT, int EPI, bool A1 = false, int WN = 1, int WM = 2> constexpr int gemm_occ() {
     if (QT == QT_Q8_0 && !A1 && WN == 1 && WM == 2 && EPI != EPI_PART) return GQ_OCC;
     if (WN > 1) return 2;
@@ -770,6 +780,30 @@ __global__ __launch_bounds__(256, (gemm_occ<QT, EPI, A1, WN, WM>())) void k_gemm
         const int n = 32 * (GC0 + WN * wave + j) + col;
         if (n >= W.n) continue;
         const int shw = wshift<QT>(W, n);
+        if (act >= 2) {
+            // the residual adds: every value of y this lane adds to is loaded
+            // first, so the loads are in flight together
+            float r[WM][16];
+#pragma unroll
+            for (int i = 0; i < WM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int m = min(32 * (G0 + i) + drow(e, hh), M - 1);
+                    r[i][e] = y[(size_t)m * W.n + n];
+                }
+            const float a = act == 3 ? 0.5f : 1.0f;
+#pragma unroll
+            for (int i = 0; i < WM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int m = 32 * (G0 + i) + drow(e, hh);
+                    if (m >= M) continue;
+                    float v = total[i][j][e];
+                    if constexpr (QT == QT_F32) v = ldexpf(v, -shw);
+                    y[(size_t)m * W.n + n] = fmaf(a, v, r[i][e]);
+                }
+            continue;
+        }
 #pragma unroll
         for (int i = 0; i < WM; i++)
 #pragma unroll
@@ -824,7 +858,8 @@ __global__ __launch_bounds__(256) void k_gemm_fold(GemmJobs J, const float *__re
         if (n + j >= W.n) return;
         float v = total[j];
         if constexpr (QT == QT_F32) v = ldexpf(v, -wshift<QT>(W, n + j));
-        y[(size_t)m * W.n + n + j] = act ? silu_f(v) : v;
+        float *yp = y + (size_t)m * W.n + n + j;
+        *yp = epi_out(act, v, yp);
     }
 }
 
