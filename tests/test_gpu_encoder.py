@@ -126,12 +126,13 @@ def test_encoder_layer_segments_are_independent(gpu):
 @pytest.mark.parametrize("d,f,biases,qt", [(1024, 4096, False, M.Q8_0), (256, 512, True, M.Q8_0),
                                            (512, 1024, False, M.Q4_K)])
 def test_encoder_layer_ln_prep_bit_identical(gpu, monkeypatch, d, f, biases, qt):
-    """Layer norms, and the attention core for the output projection, that
-    write the products' prepared input directly (the default whenever every
-    product of that output takes the EXACT GEMM path) give the bits of the
-    layer with f32 outputs and the products' own preparation
-    (MYNAH_ASR_HIP_LN_PREP=0): the same split of the same values. Q4_K
-    products read row sums, so that layer keeps f32 rows."""
+    """The layer's fused hand-offs give the bits of the layer without them
+    (MYNAH_ASR_HIP_LN_PREP=0): layer norms, the attention core and the
+    depthwise conv writing their products' prepared input directly (the same
+    split of the same values), and products without bias adding their output
+    into x in their epilogue (the layer norm's own residual fma). Q4_K
+    products read row sums, so that layer keeps f32 rows but still takes the
+    residual epilogues."""
     import torch
     say("encoder layer ln prep", d, f, biases, qt)
     H, k, T, nseq = d // 128, 9, 150, 2
