@@ -65,10 +65,12 @@ typedef float f2 __attribute__((ext_vector_type(2)));
 
 constexpr int KT = 32;           // keys per tile
 
-// NW waves per workgroup, 16 query rows each. SPL: K and the rk ring hold
-// f16 (hi, lo) pairs (rows of KSH halves each, hi rows then lo rows) and
-// each row's scale exponent (EK, ER), in place of f32 rows.
-template <int DK, int NW, bool SPL = false>
+// NW waves per workgroup, 16 query rows each. SPL: the scores on split
+// operands, K and the rk ring holding f16 (hi, lo) pairs (rows of KSH halves
+// each, hi rows then lo rows) and each row's exponent (EK, ER) in place of
+// f32 rows. FULL (implies SPL): the full window, with V split too (planes
+// of VTH halves per feature, a scale per feature in EV).
+template <int DK, int NW, bool SPL = false, bool FULL = SPL>
 struct AttnLds {
     static constexpr int NTH = 64 * NW;
     static constexpr int RB = 16 * NW;        // query rows per workgroup
@@ -78,7 +80,7 @@ struct AttnLds {
     static constexpr int RS = SPL ? KSH : KS;   // floats per K / rk row (SPL: two rows of KSH halves)
     static constexpr int VT = KT + 4;   // V is stored transposed, [DK][VT]: conflict-free b128 reads
     static constexpr int VTH = KT + 8;  // SPL: the same in halves, hi plane then lo plane
-    static constexpr int VSZ = SPL ? DK * VTH : DK * VT;   // floats
+    static constexpr int VSZ = FULL ? DK * VTH : DK * VT;   // floats
     static constexpr int BS = 53;       // band scratch row stride
     static constexpr int PS = 36;       // probability scratch row stride
     static constexpr int K0 = 0;
@@ -86,8 +88,8 @@ struct AttnLds {
     static constexpr int R0 = V0 + VSZ;
     static constexpr int EK0 = R0 + NB * RS;            // SPL: key rows' exponents, then rk rows' (negated)
     static constexpr int ER0 = EK0 + (SPL ? KT : 0);
-    static constexpr int EV0 = ER0 + (SPL ? NB : 0);     // SPL: the V tile's scale per feature
-    static constexpr int W0 = (EV0 + (SPL ? DK : 0) + 3) / 4 * 4;
+    static constexpr int EV0 = ER0 + (SPL ? NB : 0);     // FULL: the V tile's scale per feature
+    static constexpr int W0 = (EV0 + (FULL ? DK : 0) + 3) / 4 * 4;
     static constexpr int WB = 16 * BS;
     static constexpr int WSZ = WB;      // the probabilities reuse the band scratch
     static constexpr int TOTAL = W0 + NW * WSZ;   // floats
@@ -181,13 +183,14 @@ struct Window {
     __device__ int j1(int t) const { return lim ? min((t / chunk + 1) * chunk, T) : T; }
 };
 
-template <int DK, int NW, bool SPL>
+template <int DK, int NW, bool SPL, bool FULL>
 __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restrict__ q, const float *__restrict__ k,
                                                         const float *__restrict__ v, const float *__restrict__ rk,
                                                         const float *__restrict__ bu, const float *__restrict__ bv,
                                                         float *__restrict__ ctx, int T, int d, int left, int right,
                                                         float kscale, SplitIn sp) {
-    using L = AttnLds<DK, NW, SPL>;
+    using L = AttnLds<DK, NW, SPL, FULL>;
+    static_assert(SPL || !FULL, "the full-window path splits every product");
     constexpr int NTH = L::NTH, RB = L::RB, NB = L::NB;
     constexpr int NS = DK / 4;    // reduction steps of a score product (f32 MFMA)
     constexpr int NKS = DK / 32;  // SPL: reduction steps of the f16 score MFMAs
@@ -207,6 +210,8 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
         sp.kh += so;
         sp.kl += so;
         sp.ke += (size_t)blockIdx.z * T * H;
+    }
+    if constexpr (FULL) {
         sp.vh += (size_t)blockIdx.z * ntile * d * KT;
         sp.vl += (size_t)blockIdx.z * ntile * d * KT;
         sp.vs += (size_t)blockIdx.z * ntile * d;
@@ -326,8 +331,8 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     static_assert(UKV * NTH == KT * DK / 4, "staging split");
     // SPL: V tile pieces of 16 bytes (8 keys of one feature, hi or lo plane)
     constexpr int NVP = 2 * DK * 4, UVP = (NVP + NTH - 1) / NTH;
-    f4 gk[SPL ? 1 : UKV], gv[SPL ? 1 : UKV], gr[SPL ? 1 : UR];
-    uint4 svp[SPL ? UVP : 1];
+    f4 gk[SPL ? 1 : UKV], gv[FULL ? 1 : UKV], gr[SPL ? 1 : UR];
+    uint4 svp[FULL ? UVP : 1];
     float svs = 0.0f;
     uint4 sk[SPL ? UKV : 1], sr[SPL ? UR : 1];   // SPL: (hi, lo) halves of the same 4 features
     int ek[SPL ? UKV : 1], er[SPL ? UR : 1];
@@ -352,12 +357,12 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
             const int kr = min(max(jt + r, 0), T - 1);
             if constexpr (SPL) sload(sp.kh, sp.kl, sp.ke, kr, cc, sk[u], ek[u]);
             else gk[u] = *(const f4 *)(k + (unsigned)(kr * d + ho + cc));
-            if constexpr (!SPL) {
+            if constexpr (!FULL) {
                 const int rv = i % KT, cv = 4 * (i / KT);   // V: lanes along keys (transposed store)
                 gv[u] = *(const f4 *)(v + (unsigned)(min(max(jt + rv, 0), T - 1) * d + ho + cv));
             }
         }
-        if constexpr (SPL) {
+        if constexpr (FULL) {
             const int vt = jt / KT;   // full attention: tiles start at key 0
 #pragma unroll
             for (int u = 0; u < UVP; u++) {
@@ -384,13 +389,13 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
             const int i = tid + NTH * u, r = i / (DK / 4), cc = 4 * (i % (DK / 4));
             if constexpr (SPL) sstore(sk[u], ek[u], r, cc, Kh, Kl, EK);
             else *(f4 *)(Ks + r * L::KS + cc) = gk[u];
-            if constexpr (!SPL) {
+            if constexpr (!FULL) {
                 const int rv = i % KT, cv = 4 * (i / KT);
 #pragma unroll
                 for (int e = 0; e < 4; e++) Vs[(cv + e) * L::VT + rv] = gv[u][e];
             }
         }
-        if constexpr (SPL) {
+        if constexpr (FULL) {
 #pragma unroll
             for (int u = 0; u < UVP; u++) {
                 const int pc = tid + NTH * u;
@@ -554,7 +559,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
                 const int i = 4 * g + e;
                 sv[n][e] = Bw[i * L::BS + 16 * n + c - i + 15];
             }
-        if constexpr (SPL) {
+        if constexpr (FULL) {
             // full attention: every key below T is visible, and only the
             // last tile reaches past T
 #pragma unroll
@@ -579,7 +584,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
                 }
         }
         // 4. online softmax over the tile
-        if constexpr (SPL) {
+        if constexpr (FULL) {
             // The running maxima move only when some row of the wave would
             // exceed its maximum by more than 2^8 (base 2): the probabilities
             // stay <= 256, the context and the sum carry the same maximum,
@@ -637,7 +642,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
         wave_lds_order();
         const f4 pa0 = *(const f4 *)(Pw + c * L::PS + 8 * g);
         const f4 pa1 = *(const f4 *)(Pw + c * L::PS + 8 * g + 4);
-        if constexpr (SPL) {
+        if constexpr (FULL) {
             // probabilities (<= 256) split at the fixed scale 2^6, V split by
             // the pre-pass; the tile's scales undone by an exact power of two
             h8 ph, pl;
@@ -680,7 +685,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
         }
     }
 
-    if constexpr (SPL && DK == 128) {
+    if constexpr (FULL && DK == 128) {
         if (sp.xp) {
             // The context rows as the output projection's prepared input: the
             // values ctx would hold, split per (row, head) exactly as the
@@ -861,13 +866,13 @@ hipError_t launch_split(const float *x, size_t rows, int d, _Float16 *hi, _Float
     return hipGetLastError();
 }
 
-template <int DK, int NW, bool SPL>
+template <int DK, int NW, bool SPL, bool FULL = SPL>
 hipError_t launch_attn(const float *q, const float *k, const float *v, const float *rk, const float *bu,
                          const float *bv, float *ctx, int T, int d, int H, int left, int right, int nseq,
                          void *ws, uint8_t *xp, float *xpf, hipStream_t st) {
     if ((size_t)(2 * (size_t)T) * d >= 0x7fffffffu) return hipErrorInvalidValue;   // 32-bit row offsets
-    if (SPL && left >= 0) return hipErrorInvalidValue;   // the split path assumes the full window
-    if (xp && !(SPL && DK == 128)) return hipErrorInvalidValue;   // the prepared output: split path, dk 128
+    if (FULL && left >= 0) return hipErrorInvalidValue;   // the full-window path
+    if (xp && !(FULL && DK == 128)) return hipErrorInvalidValue;   // the prepared output: full window, dk 128
     SplitIn sp{};
     if constexpr (SPL) {
         if (!ws) return hipErrorInvalidValue;
@@ -882,7 +887,7 @@ hipError_t launch_attn(const float *q, const float *k, const float *v, const flo
         float *vsc = (float *)(vb + 2 * W.vp);
         hipError_t e = launch_split<DK>(k, (size_t)nseq * T, d, kh, kl, ke, st);
         if (e == hipSuccess) e = launch_split<DK>(rk, (size_t)(2 * T - 1), d, rh, rl, re, st);
-        if (e == hipSuccess) {
+        if (e == hipSuccess && FULL) {
             const size_t n = (size_t)nseq * ((T + KT - 1) / KT) * d * 4;
             hipLaunchKernelGGL(k_attn_split_v, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, v, T, d, nseq, vh,
                                vl, vsc);
@@ -891,16 +896,16 @@ hipError_t launch_attn(const float *q, const float *k, const float *v, const flo
         if (e != hipSuccess) return e;
         sp = SplitIn{kh, kl, rh, rl, ke, re, vh, vl, vsc, DK == 128 ? xp : nullptr, xpf};
     }
-    using L = AttnLds<DK, NW, SPL>;
+    using L = AttnLds<DK, NW, SPL, FULL>;
     const size_t bytes = sizeof(float) * L::TOTAL;
     // set once per instantiation (thread-safe static initialisation)
-    static const hipError_t attr = hipFuncSetAttribute((const void *)k_relpos_attn<DK, NW, SPL>,
+    static const hipError_t attr = hipFuncSetAttribute((const void *)k_relpos_attn<DK, NW, SPL, FULL>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
     if (attr != hipSuccess) return attr;
     // exponentials are base 2: scores carry log2(e) / sqrt(DK)
     const float kscale = (1.0f / sqrtf((float)DK)) * 1.4426950408889634f;
     dim3 grid((T + L::RB - 1) / L::RB, H, nseq);
-    hipLaunchKernelGGL((k_relpos_attn<DK, NW, SPL>), grid, dim3(L::NTH), bytes, st, q, k, v, rk, bu, bv, ctx, T, d,
+    hipLaunchKernelGGL((k_relpos_attn<DK, NW, SPL, FULL>), grid, dim3(L::NTH), bytes, st, q, k, v, rk, bu, bv, ctx, T, d,
                        left, right, kscale, sp);
     return hipGetLastError();
 }
@@ -932,7 +937,7 @@ hipError_t launch_dk(const float *q, const float *k, const float *v, const float
 bool mh_attn_supported(int dk) { return dk == 64 || dk == 128; }
 
 size_t mh_attn_ws_bytes(int T, int d, int H, int nseq, int left) {
-    if (left >= 0 || T <= 0 || nseq <= 0 || H <= 0) return 0;   // chunked windows: f32 scores, no split
+    if (left >= 0 || T <= 0 || nseq <= 0 || H <= 0) return 0;   // chunked windows: all f32, no split
     return SplitWs(T, d, H, nseq).total;
 }
 
