@@ -43,7 +43,7 @@
 // context update splits the probabilities (<= 256: the running maximum
 // moves only by steps above 2^8) at the fixed scale 2^6 and V per (tile of
 // 32 keys, feature), and undoes both per tile with one exact power of two. K, rk and V are split once per call by pre-passes
-// (k_attn_split, k_attn_split_v); the q rows once per wave. The softmax
+// (k_attn_split, one launch); the q rows once per wave. The softmax
 // stays fp32. With dk = 128 the context can be written directly as the output
 // projection's prepared input (SplitIn::xp) instead of as f32 rows.
 //
@@ -774,11 +774,9 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
 // kernel's q split forms them. Thread = 4 features; the DK / 4 threads of a
 // (row, head) are consecutive lanes.
 template <int DK>
-__global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ x, size_t n4, int d,
-                                                    _Float16 *__restrict__ hi, _Float16 *__restrict__ lo,
-                                                    int *__restrict__ ex) {
+__device__ __forceinline__ void split_rows(const float *__restrict__ x, size_t n4, _Float16 *__restrict__ hi,
+                                           _Float16 *__restrict__ lo, int *__restrict__ ex, size_t idx) {
     constexpr int TPR = DK / 4;
-    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= n4) return;   // whole (row, head) groups only: n4 is a multiple of TPR
     const f4 v = *(const f4 *)(x + 4 * idx);
     float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
@@ -806,11 +804,10 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ x,
 // T zero), and the scale 2^-(6 + e). Thread = (segment, tile, feature, 8
 // keys): the 4 threads of a feature are consecutive lanes (the maximum is a
 // quad reduction), and a wave's stores cover 16 features' 64-byte rows.
-__global__ __launch_bounds__(256) void k_attn_split_v(const float *__restrict__ v, int T, int d, int nseq,
-                                                      _Float16 *__restrict__ hi, _Float16 *__restrict__ lo,
-                                                      float *__restrict__ vs) {
+__device__ __forceinline__ void split_v(const float *__restrict__ v, int T, int d, int nseq,
+                                        _Float16 *__restrict__ hi, _Float16 *__restrict__ lo,
+                                        float *__restrict__ vs, size_t idx) {
     const int ntile = (T + KT - 1) / KT;
-    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= (size_t)nseq * ntile * d * 4) return;   // whole quads only
     const int part = (int)(idx & 3);
     const size_t fi = idx >> 2;   // (segment, tile, feature)
@@ -840,6 +837,30 @@ __global__ __launch_bounds__(256) void k_attn_split_v(const float *__restrict__ 
     if (part == 0) vs[fi] = __int_as_float((127 - 6 - ex) << 23);
 }
 
+// The three splits in one launch: workgroups [0, bk) split K, the next br
+// rk, the rest V (a workgroup's waves all take the same task).
+struct SplitJobs {
+    const float *k, *rk, *v;
+    size_t nk4, nr4;
+    unsigned bk, br;
+    int T, d, nseq;
+    _Float16 *kh, *kl, *rh, *rl, *vh, *vl;
+    int *ke, *re;
+    float *vs;
+};
+
+template <int DK>
+__global__ __launch_bounds__(256) void k_attn_split(SplitJobs J) {
+    const unsigned b = blockIdx.x;
+    if (b < J.bk) {
+        split_rows<DK>(J.k, J.nk4, J.kh, J.kl, J.ke, (size_t)b * 256 + threadIdx.x);
+    } else if (b < J.bk + J.br) {
+        split_rows<DK>(J.rk, J.nr4, J.rh, J.rl, J.re, (size_t)(b - J.bk) * 256 + threadIdx.x);
+    } else {
+        split_v(J.v, J.T, J.d, J.nseq, J.vh, J.vl, J.vs, (size_t)(b - J.bk - J.br) * 256 + threadIdx.x);
+    }
+}
+
 size_t al256(size_t b) { return (b + 255) / 256 * 256; }
 
 // the workspace of the split path: K planes and exponents, then rk's
@@ -858,13 +879,6 @@ struct SplitWs {
     }
 };
 
-template <int DK>
-hipError_t launch_split(const float *x, size_t rows, int d, _Float16 *hi, _Float16 *lo, int *ex, hipStream_t st) {
-    const size_t n4 = rows * (size_t)(d / 4);
-    if (!n4) return hipSuccess;
-    hipLaunchKernelGGL(k_attn_split<DK>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, x, n4, d, hi, lo, ex);
-    return hipGetLastError();
-}
 
 template <int DK, int NW, bool SPL, bool FULL = SPL>
 hipError_t launch_attn(const float *q, const float *k, const float *v, const float *rk, const float *bu,
@@ -885,14 +899,22 @@ hipError_t launch_attn(const float *q, const float *k, const float *v, const flo
         uint8_t *vb = b + 2 * W.kp + W.ke + 2 * W.rp + W.re;
         _Float16 *vh = (_Float16 *)vb, *vl = (_Float16 *)(vb + W.vp);
         float *vsc = (float *)(vb + 2 * W.vp);
-        hipError_t e = launch_split<DK>(k, (size_t)nseq * T, d, kh, kl, ke, st);
-        if (e == hipSuccess) e = launch_split<DK>(rk, (size_t)(2 * T - 1), d, rh, rl, re, st);
-        if (e == hipSuccess && FULL) {
-            const size_t n = (size_t)nseq * ((T + KT - 1) / KT) * d * 4;
-            hipLaunchKernelGGL(k_attn_split_v, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, v, T, d, nseq, vh,
-                               vl, vsc);
-            e = hipGetLastError();
-        }
+        SplitJobs J{};
+        J.k = k;
+        J.rk = rk;
+        J.v = v;
+        J.nk4 = (size_t)nseq * T * (d / 4);
+        J.nr4 = (size_t)(2 * T - 1) * (d / 4);
+        J.bk = (unsigned)((J.nk4 + 255) / 256);
+        J.br = (unsigned)((J.nr4 + 255) / 256);
+        J.T = T;
+        J.d = d;
+        J.nseq = nseq;
+        J.kh = kh, J.kl = kl, J.ke = ke, J.rh = rh, J.rl = rl, J.re = re, J.vh = vh, J.vl = vl, J.vs = vsc;
+        const size_t nv = FULL ? (size_t)nseq * ((T + KT - 1) / KT) * d * 4 : 0;
+        const unsigned bv = (unsigned)((nv + 255) / 256);
+        hipLaunchKernelGGL(k_attn_split<DK>, dim3(J.bk + J.br + bv), dim3(256), 0, st, J);
+        const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         sp = SplitIn{kh, kl, rh, rl, ke, re, vh, vl, vsc, DK == 128 ? xp : nullptr, xpf};
     }
