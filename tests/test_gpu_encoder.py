@@ -123,9 +123,10 @@ def test_encoder_layer_segments_are_independent(gpu):
         dev.close()
 
 
-@pytest.mark.parametrize("d,f,biases,qt", [(1024, 4096, False, M.Q8_0), (256, 512, True, M.Q8_0),
-                                           (512, 1024, False, M.Q4_K)])
-def test_encoder_layer_ln_prep_bit_identical(gpu, monkeypatch, d, f, biases, qt):
+@pytest.mark.parametrize("d,f,biases,qt,T,nseq", [(1024, 4096, False, M.Q8_0, 150, 2), (256, 512, True, M.Q8_0, 150, 2),
+                                                  (512, 1024, False, M.Q4_K, 150, 2),
+                                                  (256, 512, False, M.Q8_0, 128, 256)])   # 8-wave attention
+def test_encoder_layer_ln_prep_bit_identical(gpu, monkeypatch, d, f, biases, qt, T, nseq):
     """The layer's fused hand-offs give the bits of the layer without them
     (MYNAH_ASR_HIP_LN_PREP=0): layer norms, the attention core and the
     depthwise conv writing their products' prepared input directly (the same
@@ -134,8 +135,8 @@ def test_encoder_layer_ln_prep_bit_identical(gpu, monkeypatch, d, f, biases, qt)
     products read row sums, so that layer keeps f32 rows but still takes the
     residual epilogues."""
     import torch
-    say("encoder layer ln prep", d, f, biases, qt)
-    H, k, T, nseq = d // 128, 9, 150, 2
+    say("encoder layer ln prep", d, f, biases, qt, T, nseq)
+    H, k = d // 128, 9
     p = make_params(11, d, f, k, biases, True)
     dev = M.DeviceEncoderLayer(gpu, p, qt)
     try:
