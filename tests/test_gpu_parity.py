@@ -593,3 +593,27 @@ def test_empty_inputs(gpu):
     finally:
         dw.close()
     M.evict(gpu, w)
+
+
+@pytest.mark.parametrize("T", [700, 5])   # the GEMM and the GEMV paths
+def test_public_act_values_other_than_one_mean_silu(gpu, T):
+    """The C ABI's act is 0 (none) or anything else (SiLU): act values that the
+    library uses internally for its residual epilogues (2, 3) give SiLU at
+    the public entry points, bit-identical to act = 1, and never touch y's
+    previous contents."""
+    import torch
+    say("public act", T)
+    w = M.DeviceWeight(gpu, M.Weight.make(gpu, M.Q8_0, gpu.randn(6, 0.02, (256, 1024))))
+    x = torch.from_numpy(gpu.randn(7, 1.0, (T, 1024))).cuda()
+    try:
+        outs = []
+        for act in (1, 2, 3, -1):
+            y = torch.full((T, 256), 123.0, dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+            w.gemm(x.data_ptr(), y.data_ptr(), T, act=act)
+            torch.cuda.synchronize()
+            outs.append(y)
+        for y in outs[1:]:
+            assert torch.equal(y.view(torch.int32), outs[0].view(torch.int32))
+    finally:
+        w.close()
