@@ -72,6 +72,7 @@ CASES = [
     (256, 2, 768, 5, 41, 2, 0, True, True, 12, 3, M.Q4_K),
     (1024, 8, 4096, 9, 120, 2, 0, False, True, -1, 0, M.Q8_0),
     (256, 2, 512, 31, 45, 2, 1, True, True, -1, 0, M.Q8_0),   # k 31: the untiled depthwise conv
+    (256, 2, 512, 9, 7, 2, 0, False, True, -1, 0, M.Q8_0),    # M = 14: every product on the GEMV
 ]
 
 
