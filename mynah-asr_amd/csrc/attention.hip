@@ -229,6 +229,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     // exponents of this lane's output rows 4 g + e, negated
     h8 qah[SPL ? NKS : 1], qal[SPL ? NKS : 1], qbh[SPL ? NKS : 1], qbl[SPL ? NKS : 1];
     int eqa[4], eqb[4];
+    int eqo = 0;   // FULL: the negated exponent of this lane's own query row tw + c
     if constexpr (SPL) {
         const int t = tw + c;
         float xa[SPL ? DK / 4 : 1], xb[SPL ? DK / 4 : 1];
@@ -274,6 +275,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
             eqa[e] = -__shfl(ea, 4 * g + e);   // negated: the unscale adds them
             eqb[e] = -__shfl(eb, 4 * g + e);
         }
+        eqo = -ea;
     }
     // (q + bias_u), (q + bias_v) of query row tw + c, features NS*g .. NS*g + NS-1
     float qa[SPL ? 1 : NS], qb[SPL ? 1 : NS];
@@ -508,9 +510,16 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
                 }
 #pragma unroll
                 for (int n = 0; n < 2; n++) {
-                    s[n] = mfma16h(qah[i], kh[n], s[n]);
-                    s[n] = mfma16h(qah[i], kl[n], s[n]);
-                    s[n] = mfma16h(qal[i], kh[n], s[n]);
+                    if constexpr (FULL) {
+                        // transposed: rows = keys 16n + 4g + e, column = query c
+                        s[n] = mfma16h(kh[n], qah[i], s[n]);
+                        s[n] = mfma16h(kl[n], qah[i], s[n]);
+                        s[n] = mfma16h(kh[n], qal[i], s[n]);
+                    } else {
+                        s[n] = mfma16h(qah[i], kh[n], s[n]);
+                        s[n] = mfma16h(qah[i], kl[n], s[n]);
+                        s[n] = mfma16h(qal[i], kh[n], s[n]);
+                    }
                     bd[n] = mfma16h(qbh[i], rh[n], bd[n]);
                     bd[n] = mfma16h(qbh[i], rl[n], bd[n]);
                     bd[n] = mfma16h(qbl[i], rh[n], bd[n]);
@@ -519,9 +528,12 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
 #pragma unroll
             for (int n = 0; n < 2; n++) {
                 const int ek = EK[16 * n + c], er = ER[rr[n]];
+                int4 ek4 = {0, 0, 0, 0};
+                if constexpr (FULL) ek4 = *(const int4 *)(EK + 16 * n + 4 * g);
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    s[n][e] = ldexpf(s[n][e], eqa[e] + ek);
+                    if constexpr (FULL) s[n][e] = ldexpf(s[n][e], eqo + ek4[e]);
+                    else s[n][e] = ldexpf(s[n][e], eqa[e] + ek);
                     bd[n][e] = ldexpf(bd[n][e], eqb[e] + er);
                 }
             }
@@ -556,8 +568,12 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
         for (int n = 0; n < 2; n++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const int i = 4 * g + e;
-                sv[n][e] = Bw[i * L::BS + 16 * n + c - i + 15];
+                if constexpr (FULL) {   // key 16n + 4g + e of query c
+                    sv[n][e] = Bw[c * L::BS + 16 * n + 4 * g + e - c + 15];
+                } else {
+                    const int i = 4 * g + e;
+                    sv[n][e] = Bw[i * L::BS + 16 * n + c - i + 15];
+                }
             }
         if constexpr (FULL) {
             // full attention: every key below T is visible, and only the
@@ -569,9 +585,9 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
             if (jt + KT > T) {
 #pragma unroll
                 for (int n = 0; n < 2; n++)
-                    if (jt + 16 * n + c >= T)
 #pragma unroll
-                        for (int e = 0; e < 4; e++) sv[n][e] = -INFINITY;
+                    for (int e = 0; e < 4; e++)
+                        if (jt + 16 * n + 4 * g + e >= T) sv[n][e] = -INFINITY;
             }
         } else {
 #pragma unroll
@@ -585,37 +601,42 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
         }
         // 4. online softmax over the tile
         if constexpr (FULL) {
-            // The running maxima move only when some row of the wave would
-            // exceed its maximum by more than 2^8 (base 2): the probabilities
-            // stay <= 256, the context and the sum carry the same maximum,
-            // and most tiles skip the rescale.
-            float mx[4];
-            bool grow = false;
+            // One query per lane (column c; the 4 lanes of a column hold its
+            // 32 keys): its running maximum and sum in m[0], l[0]. The maxima
+            // move only when some query of the wave would exceed its maximum
+            // by more than 2^8 (base 2): the probabilities stay <= 256, the
+            // context and the sum carry the same maximum, and most tiles skip
+            // the rescale (whose factors go to the context's rows 4g + e).
+            float mx = -INFINITY;
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                mx[e] = max16(fmaxf(sv[0][e], sv[1][e]));
-                grow |= mx[e] > m[e] + 8.0f;
-            }
-            if (__any(grow)) {
-                float alpha[4];
+            for (int n = 0; n < 2; n++)
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float mn = fmaxf(m[e], mx[e]);
-                    alpha[e] = exp2f(m[e] - mn);
-                    m[e] = mn;
-                    l[e] *= alpha[e];
-                }
+                for (int e = 0; e < 4; e++) mx = fmaxf(mx, sv[n][e]);
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            if (__any(mx > m[0] + 8.0f)) {
+                const float mn = fmaxf(m[0], mx), alpha = exp2f(m[0] - mn);
+                m[0] = mn;
+                l[0] *= alpha;
+                float ae[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) ae[e] = __shfl(alpha, 4 * g + e);
 #pragma unroll
                 for (int n = 0; n < NT; n++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) acc[n][e] *= alpha[e];
+                    for (int e = 0; e < 4; e++) acc[n][e] *= ae[e];
             }
+            float ls = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                sv[0][e] = exp2f(sv[0][e] - m[e]);
-                sv[1][e] = exp2f(sv[1][e] - m[e]);
-                l[e] += sum16(sv[0][e] + sv[1][e]);
-            }
+            for (int n = 0; n < 2; n++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    sv[n][e] = exp2f(sv[n][e] - m[0]);
+                    ls += sv[n][e];
+                }
+            ls += __shfl_xor(ls, 16);
+            ls += __shfl_xor(ls, 32);
+            l[0] += ls;
         } else {
             float alpha[4];
 #pragma unroll
@@ -633,23 +654,17 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
 #pragma unroll
                 for (int e = 0; e < 4; e++) acc[n][e] *= alpha[e];
         }
-        // 5. probabilities to the A layout (row c, keys 8g .. 8g+7), then P . V
-        wave_lds_order();   // the band reads above precede these writes
-#pragma unroll
-        for (int n = 0; n < 2; n++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) Pw[(4 * g + e) * L::PS + 16 * n + c] = sv[n][e];
-        wave_lds_order();
-        const f4 pa0 = *(const f4 *)(Pw + c * L::PS + 8 * g);
-        const f4 pa1 = *(const f4 *)(Pw + c * L::PS + 8 * g + 4);
         if constexpr (FULL) {
             // probabilities (<= 256) split at the fixed scale 2^6, V split by
             // the pre-pass; the tile's scales undone by an exact power of two
+            // The A operand straight from the scores' layout: this lane's
+            // query c and its keys 4g .. 4g+3, 16+4g .. 16+4g+3 (the V planes
+            // hold a tile's keys in that order)
             h8 ph, pl;
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 _Float16 hh, ll;
-                split_h(u < 4 ? pa0[u] : pa1[u - 4], 6, hh, ll);
+                split_h(sv[u >> 2][u & 3], 6, hh, ll);
                 ph[u] = hh;
                 pl[u] = ll;
             }
@@ -667,6 +682,15 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
             }
             continue;
         }
+        // 5. (f32 path) probabilities to the A layout (row c, keys 8g .. 8g+7), then P . V
+        wave_lds_order();   // the band reads above precede these writes
+#pragma unroll
+        for (int n = 0; n < 2; n++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) Pw[(4 * g + e) * L::PS + 16 * n + c] = sv[n][e];
+        wave_lds_order();
+        const f4 pa0 = *(const f4 *)(Pw + c * L::PS + 8 * g);
+        const f4 pa1 = *(const f4 *)(Pw + c * L::PS + 8 * g + 4);
         const float pa[8] = {pa0.x, pa0.y, pa0.z, pa0.w, pa1.x, pa1.y, pa1.z, pa1.w};
         // B operand: column 16n + c, keys 8g .. 8g+7 of the transposed V tile
         f4 vb[2][2];
@@ -685,6 +709,12 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
         }
     }
 
+    if constexpr (FULL) {
+        // the per-query sums (lane column c) to the context's rows 4g + e
+        const float lc = l[0];
+#pragma unroll
+        for (int e = 0; e < 4; e++) l[e] = __shfl(lc, 4 * g + e);
+    }
     if constexpr (FULL && DK == 128) {
         if (sp.xp) {
             // The context rows as the output projection's prepared input: the
@@ -801,9 +831,11 @@ __device__ __forceinline__ void split_rows(const float *__restrict__ x, size_t n
 // e that puts the tile's largest magnitude in [2^14, 2^15) (clamped to
 // [-100, 100], so that the scale below stays a normal float), the planes
 // hi = f16(v 2^e), lo = f16(v 2^e - hi) as [segment][tile][d][32] (keys past
-// T zero), and the scale 2^-(6 + e). Thread = (segment, tile, feature, 8
-// keys): the 4 threads of a feature are consecutive lanes (the maximum is a
-// quad reduction), and a wave's stores cover 16 features' 64-byte rows.
+// T zero; within a tile in the order the kernel's P operand takes them: keys
+// 4q .. 4q+3, 16+4q .. 16+4q+3 at positions 8q .. 8q+7), and the scale
+// 2^-(6 + e). Thread = (segment, tile, feature, 8 positions): the 4 threads of
+// a feature are consecutive lanes (the maximum is a quad reduction), and a
+// wave's stores cover 16 features' 64-byte rows.
 __device__ __forceinline__ void split_v(const float *__restrict__ v, int T, int d, int nseq,
                                         _Float16 *__restrict__ hi, _Float16 *__restrict__ lo,
                                         float *__restrict__ vs, size_t idx) {
@@ -812,13 +844,16 @@ __device__ __forceinline__ void split_v(const float *__restrict__ v, int T, int 
     const int part = (int)(idx & 3);
     const size_t fi = idx >> 2;   // (segment, tile, feature)
     const int f = (int)(fi % d), tile = (int)((fi / d) % ntile), s = (int)(fi / ((size_t)d * ntile));
-    const int k0 = tile * KT + 8 * part;
-    const float *vr = v + ((size_t)s * T + k0) * d + f;
+    // stored position 8 part + jj holds key 4 part + jj (jj < 4), else
+    // 16 + 4 part + jj - 4: the keys one lane of the attention kernel's
+    // score layout holds for its query
+    const float *vs0 = v + ((size_t)s * T + (size_t)tile * KT) * d + f;
     float x[8];
     float a = 0.0f;
 #pragma unroll
     for (int jj = 0; jj < 8; jj++) {
-        x[jj] = k0 + jj < T ? vr[(size_t)jj * d] : 0.0f;
+        const int key = (jj < 4 ? 4 * part + jj : 16 + 4 * part + jj - 4);
+        x[jj] = tile * KT + key < T ? vs0[(size_t)key * d] : 0.0f;
         a = fmaxf(a, fabsf(x[jj]));
     }
     a = fmaxf(a, __shfl_xor(a, 1));
