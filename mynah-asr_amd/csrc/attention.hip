@@ -34,18 +34,21 @@
 // reference's f32 computation up to summation order and the exponential's
 // rounding.
 //
-// SPL = true (full attention) forms the products on the f16 MFMA instead.
-// Each q, K and rk row is scaled by a power of two 2^e that puts its largest
-// magnitude in [2^14, 2^15) and split into f16 pairs hi + lo (hi = f16(x 2^e),
-// lo = f16(x 2^e - hi)), which hold x to 2^-22 of the row's maximum; a score
-// is hi.hi + hi.lo + lo.hi summed in f32 (the dropped lo.lo is below 2^-22 of
-// the same scale) and multiplied by 2^-(e_q + e_k), which is exact. The
-// context update splits the probabilities (<= 256: the running maximum
-// moves only by steps above 2^8) at the fixed scale 2^6 and V per (tile of
-// 32 keys, feature), and undoes both per tile with one exact power of two. K, rk and V are split once per call by pre-passes
-// (k_attn_split, one launch); the q rows once per wave. The softmax
-// stays fp32. With dk = 128 the context can be written directly as the output
-// projection's prepared input (SplitIn::xp) instead of as f32 rows.
+// SPL = FULL = true (full attention) forms the products on the f16 MFMA
+// instead. Each q, K and rk row is scaled by a power of two 2^e that puts its
+// largest magnitude in [2^14, 2^15) and split into f16 pairs hi + lo (hi =
+// f16(x 2^e), lo = f16(x 2^e - hi)), which hold x to 2^-22 of the row's
+// maximum; a score is hi.hi + hi.lo + lo.hi summed in f32 (the dropped lo.lo
+// is below 2^-22 of the same scale) and multiplied by 2^-(e_q + e_k), which is
+// exact. The content scores are formed transposed (K . q^T: a lane holds 8
+// keys of one query), so the probabilities are already the context update's
+// A operand; that update splits them (<= 256: the running maximum moves only
+// by steps above 2^8) at the fixed scale 2^6 and V per (tile of 32 keys,
+// feature, keys stored in the A operand's order), and undoes both per tile
+// with one exact power of two. K, rk and V are split once per call by a
+// pre-pass (k_attn_split, one launch); the q rows once per wave. The softmax
+// stays fp32. With dk = 128 the context can be written directly as the
+// output projection's prepared input (SplitIn::xp) instead of as f32 rows.
 //
 // MFMA 16x16x4 f32 operand layout (lane l, c = l & 15, g = l >> 4):
 //   A: row c, k-slot g;  B: column c, k-slot g;  D: rows 4g + e (e = 0..3), column c.
