@@ -253,6 +253,39 @@ def test_split_k_gemv_rows_match_gemm(gpu, orc, qt):
     dw.close()
 
 
+@pytest.mark.parametrize("qt", [M.Q8_0, M.Q4_K, M.Q6_K], ids=lambda q: M.NAMES[q])
+def test_split_k_gemv_in_place_and_repeated(gpu, orc, qt):
+    """K = N = 2048 (64 column groups, the most the split-K GEMV takes): eight
+    calls in a row on changing inputs sharing one workspace, then one in place
+    (x aliasing y, as qgemm allows: every chunk result is formed before the
+    fold writes y). Each must be the same bits as the rows of a GEMM (M = 40)."""
+    import torch
+    say("split-K GEMV in place / repeated", M.NAMES[qt])
+    n = k = 2048
+    dw = M.DeviceWeight(gpu, M.Weight.make(gpu, qt, gpu.randn(5, 0.02, (n, k))))
+    x = torch.from_numpy(gpu.randn(6, 1.0, (40, k))).cuda()
+    ref = torch.empty((40, n), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    dw.gemm(x.data_ptr(), ref.data_ptr(), 40)
+    torch.cuda.synchronize()
+    for T in (1, 5, 16):
+        ys = [torch.full((T, n), float("nan"), dtype=torch.float32, device="cuda") for _ in range(8)]
+        xs = [x[i:i + T].contiguous() for i in range(8)]
+        torch.cuda.synchronize()
+        for xi, yi in zip(xs, ys):
+            dw.gemm(xi.data_ptr(), yi.data_ptr(), T)
+        z = x[:T].clone()
+        torch.cuda.synchronize()
+        dw.gemm(z.data_ptr(), z.data_ptr(), T)
+        torch.cuda.synchronize()
+        rb = ref.cpu().numpy().view(np.uint32)
+        for i, yi in enumerate(ys):
+            assert np.array_equal(yi.cpu().numpy().view(np.uint32), rb[i:i + T]), (T, i)
+        assert np.array_equal(z.cpu().numpy().view(np.uint32), rb[:T]), (T, "in place")
+    check_close(ref.cpu().numpy(), orc.gemm_f64(x.cpu().numpy(), oracle_dequant(orc, dw.w)), f"{M.NAMES[qt]} 2048x2048")
+    dw.close()
+
+
 @pytest.mark.parametrize("qt", ALL, ids=lambda q: M.NAMES[q])
 def test_split_k_gemm_rows_match_gemm(gpu, orc, qt):
     """A product with few tiles splits K over workgroups (chunk results to a
