@@ -882,12 +882,11 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
     const size_t md = (size_t)M * d;
     // xn, tmp, q, k, v, ctx [M, d]; h [M, 2d] (pw1, GLU); rk [P, d]; the FFN
     // intermediate [M, f] only with FFN biases
-    const size_t kd = ((size_t)conv_k * d + 3) / 4 * 4;   // the depthwise taps, tap-major
-    const size_t need = 6 * md + 2 * md + (size_t)P * d + kd + (biased_ffn ? (size_t)M * f : 0);
+    const size_t need = 6 * md + 2 * md + (size_t)P * d + (biased_ffn ? (size_t)M * f : 0);
     float *base = (float *)c->enc.get(need * sizeof(float));
     if (!base) return fail("device buffer allocation failed");
     float *xn = base, *tmp = xn + md, *q = tmp + md, *k = q + md, *v = k + md, *ctx = v + md, *h = ctx + md,
-          *rk = h + 2 * md, *dwt = rk + (size_t)P * d, *hf = dwt + kd;
+          *rk = h + 2 * md, *hf = rk + (size_t)P * d;
     hipError_t e;
 #define ENC_TRY(expr)                                                                   \
     do {                                                                                \
@@ -969,13 +968,12 @@ int encoder_layer_dev(Ctx *c, const mynah_asr_hip_enc_layer *L, float *x, int T,
     }
     c->pa.src = nullptr;
     if (bias_add(h, L->pw1_b, M, 2 * d, st)) return -1;
-    ENC_TRY(mh_launch_transpose_taps(L->dw_w, dwt, d, conv_k, st));
     // the GLU (g = q, free now) folded into the depthwise conv where it can be
     const bool glu_dw = mh_glu_dwconv_supported(d, conv_k);
     if (!glu_dw) ENC_TRY(mh_launch_glu(h, q, M, d, st));
     auto dwconv = [&](const float *sc, const float *sh, float *o, uint8_t *xp, float *xpf) {
-        return glu_dw ? mh_launch_glu_dwconv(h, dwt, L->dw_b, sc, sh, o, T, nseq, d, conv_k, causal, xp, xpf, st)
-                      : mh_launch_dwconv(q, dwt, L->dw_b, sc, sh, o, T, nseq, d, conv_k, causal, st);
+        return glu_dw ? mh_launch_glu_dwconv(h, L->dw_w, L->dw_b, sc, sh, o, T, nseq, d, conv_k, causal, xp, xpf, st)
+                      : mh_launch_dwconv(q, L->dw_w, L->dw_b, sc, sh, o, T, nseq, d, conv_k, causal, st);
     };
     if (L->cnorm_scale) {
         // with the folded batch norm the conv's output feeds only pw2: written

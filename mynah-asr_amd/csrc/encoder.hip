@@ -192,9 +192,9 @@ __device__ __forceinline__ float silu_e(float x) { return x * sigmoid_f(x); }
 
 // c[t, i] = dw_b[i] + sum_j w[i, j] * g[t - pc + j, i] over the taps inside
 // the segment (in tap order from j0), then, with scale: silu(c * scale +
-// shift). Thread = (row, 4 channels); the weights tap-major, wt[j][i]
-// (k_transpose), so each tap is one 16-byte load.
-__global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ g, const float *__restrict__ wt,
+// shift). Thread = (row, 4 channels); the weights in the reference's order
+// w[i][j] (the fallback for shapes the tiled form does not take).
+__global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ g, const float *__restrict__ w,
                                                 const float *__restrict__ bias, const float *__restrict__ scale,
                                                 const float *__restrict__ shift, float *__restrict__ out, int T,
                                                 int nseq, int d, int k, int pc) {
@@ -208,7 +208,8 @@ __global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ g, con
     const int j0 = t - pc < 0 ? pc - t : 0, j1 = t - pc + k > T ? T - t + pc : k;
     for (int j = j0; j < j1; j++) {
         const float4 src = *(const float4 *)(gs + (size_t)(t - pc + j) * d + i);
-        const float4 wv = *(const float4 *)(wt + (size_t)j * d + i);
+        const float *wj = w + (size_t)i * k + j;
+        const float4 wv = {wj[0], wj[k], wj[2 * k], wj[3 * k]};
         o.x = fmaf(wv.x, src.x, o.x);
         o.y = fmaf(wv.y, src.y, o.y);
         o.z = fmaf(wv.z, src.z, o.z);
@@ -239,7 +240,7 @@ constexpr int DW_R = 32;
 // preparation forms, held in registers until the tile is done, then staged
 // in the input rows' LDS so the stores run along rows.
 template <bool GLU, bool PREP>
-__global__ __launch_bounds__(256) void k_dwconv_tile(const float *__restrict__ g, const float *__restrict__ wt,
+__global__ __launch_bounds__(256) void k_dwconv_tile(const float *__restrict__ g, const float *__restrict__ w,
                                                      const float *__restrict__ bias, const float *__restrict__ scale,
                                                      const float *__restrict__ shift, float *__restrict__ out,
                                                      int T, int d, int k, int pc, uint8_t *__restrict__ xp,
@@ -268,7 +269,13 @@ __global__ __launch_bounds__(256) void k_dwconv_tile(const float *__restrict__ g
         }
         dws[i] = o;
     }
-    for (int i = tid; i < k * 64; i += 256) taps[i] = *(const float4 *)(wt + (size_t)(i >> 6) * d + c0 + 4 * (i & 63));
+    // the taps of w [d][k] written tap-major (each tap of 4 channels one
+    // float4): thread = channel c0 + tid, its k taps
+    {
+        float *tf = (float *)taps;
+        const float *wc = w + (size_t)(c0 + tid) * k;
+        for (int j = 0; j < k; j++) tf[j * 256 + tid] = wc[j];
+    }
     __syncthreads();
     const int i = c0 + 4 * q;
     const float4 b0 = bias ? *(const float4 *)(bias + i) : float4{0.f, 0.f, 0.f, 0.f};

@@ -137,7 +137,7 @@ hipError_t mh_launch_add_ln_prep(float *x, const float *res, float alpha, const 
 // g [rows, d] = h[:, :d] * sigmoid(h[:, d:]) for h [rows, 2d]
 hipError_t mh_launch_glu(const float *h, float *g, size_t rows, int d, hipStream_t st);
 // depthwise conv over time in each of nseq segments of T rows (w: the taps
-// tap-major, [k, d] (mh_launch_transpose_taps);
+// in the reference's order, [d, k]);
 // causal: left pad k - 1, else (k - 1) / 2 per side), + bias (or null); with
 // scale: silu(c * scale + shift)
 hipError_t mh_launch_dwconv(const float *g, const float *w, const float *bias, const float *scale,
@@ -167,8 +167,8 @@ hipError_t mh_launch_dw_s2(const float *in, const float *pb, const float *w, con
                            int T, int F, int C, int causal, hipStream_t st);
 hipError_t mh_launch_flatten(const float *in, const float *pb, float *flat, size_t rows, int Fo, int C,
                              hipStream_t st);
-// wt [k][C] = the taps of w [C][k] tap-major (the layout k_dwconv, k_conv_in_dw
-// and k_dw_s2 read: w, the argument of their launchers, is this copy)
+// wt [k][C] = the taps of w [C][k] tap-major (the layout k_conv_in_dw and
+// k_dw_s2 read: w, the argument of their launchers, is this copy)
 hipError_t mh_launch_transpose_taps(const float *w, float *wt, int C, int k, hipStream_t st);
 // y = (y + b) * scale per row (scale 1: the bias alone)
 hipError_t mh_launch_bias_scale(float *y, const float *b, size_t rows, int d, float scale, hipStream_t st);
