@@ -73,6 +73,8 @@ CASES = [
     (1024, 8, 4096, 9, 120, 2, 0, False, True, -1, 0, M.Q8_0),
     (256, 2, 512, 31, 45, 2, 1, True, True, -1, 0, M.Q8_0),   # k 31: the untiled depthwise conv
     (256, 2, 512, 9, 7, 2, 0, False, True, -1, 0, M.Q8_0),    # M = 14: every product on the GEMV
+    (512, 4, 1024, 9, 50, 2, 0, False, True, -1, 0, M.Q8_0),
+    (2048, 16, 2048, 9, 40, 2, 0, False, True, -1, 0, M.Q8_0),  # the widest fused layer norm
 ]
 
 
@@ -126,7 +128,8 @@ def test_encoder_layer_segments_are_independent(gpu):
 
 @pytest.mark.parametrize("d,f,biases,qt,T,nseq", [(1024, 4096, False, M.Q8_0, 150, 2), (256, 512, True, M.Q8_0, 150, 2),
                                                   (512, 1024, False, M.Q4_K, 150, 2),
-                                                  (256, 512, False, M.Q8_0, 128, 256)])   # 8-wave attention
+                                                  (256, 512, False, M.Q8_0, 128, 256),   # 8-wave attention
+                                                  (2048, 2048, True, M.Q8_0, 70, 2), (2048, 4096, False, M.Q8_0, 64, 3)])
 def test_encoder_layer_ln_prep_bit_identical(gpu, monkeypatch, d, f, biases, qt, T, nseq):
     """The layer's fused hand-offs give the bits of the layer without them
     (MYNAH_ASR_HIP_LN_PREP=0): layer norms, the attention core and the
