@@ -201,8 +201,23 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     extern __shared__ float lds[];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int c = lane & 15, g = lane >> 4;
-    const int ho = blockIdx.y * DK;
-    const size_t so = (size_t)blockIdx.z * (size_t)T * (size_t)d;
+    // XCD-aware order: the hardware deals workgroups to the 8 XCDs round-robin
+    // by flat id. Each XCD gets a contiguous run of the (query block, segment,
+    // head) triples, query blocks fastest, then segments: the query blocks of
+    // one (segment, head) read the same K and V planes, and the segments of
+    // one head the same rk rows, so they share the XCD's L2.
+    int bx, by, bz;
+    {
+        const int gx = gridDim.x, gz = gridDim.z;
+        const int ntot = gx * gridDim.y * gz, flat = blockIdx.x + gx * (blockIdx.y + gridDim.y * blockIdx.z);
+        const int qx = ntot / 8, rx = ntot % 8, xcd = flat % 8, loc = flat / 8;
+        const int lg = xcd < rx ? xcd * (qx + 1) + loc : rx * (qx + 1) + (xcd - rx) * qx + loc;
+        bx = lg % gx;
+        bz = (lg / gx) % gz;
+        by = lg / (gx * gz);
+    }
+    const int ho = by * DK;
+    const size_t so = (size_t)bz * (size_t)T * (size_t)d;
     q += so;
     k += so;
     v += so;
@@ -212,14 +227,14 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     if constexpr (SPL) {
         sp.kh += so;
         sp.kl += so;
-        sp.ke += (size_t)blockIdx.z * T * H;
+        sp.ke += (size_t)bz * T * H;
     }
     if constexpr (FULL) {
-        sp.vh += (size_t)blockIdx.z * ntile * d * KT;
-        sp.vl += (size_t)blockIdx.z * ntile * d * KT;
-        sp.vs += (size_t)blockIdx.z * ntile * d;
+        sp.vh += (size_t)bz * ntile * d * KT;
+        sp.vl += (size_t)bz * ntile * d * KT;
+        sp.vs += (size_t)bz * ntile * d;
     }
-    const int t0 = blockIdx.x * RB, tw = t0 + 16 * w;
+    const int t0 = bx * RB, tw = t0 + 16 * w;
     Window win;
     win.lim = left >= 0;
     win.chunk = win.lim ? right + 1 : 1;
@@ -347,7 +362,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
         const unsigned off = (unsigned)(row * d + ho + cc);   // < 2^31: checked at launch
         const uint2 a = *(const uint2 *)(hp + off), b = *(const uint2 *)(lp + off);
         o = make_uint4(a.x, a.y, b.x, b.y);
-        e = ep[(unsigned)(row * H) + blockIdx.y];
+        e = ep[(unsigned)(row * H) + by];
     };
     auto sstore = [&](const uint4 &o, int e, int row, int cc, _Float16 *Hd, _Float16 *Ld, int *E) {
         *(uint2 *)(Hd + row * L::KSH + cc) = make_uint2(o.x, o.y);
@@ -725,7 +740,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
             // products' preparation splits a 128-element chunk, re-laid out
             // through LDS (free once every wave is past its last tile) into
             // 16-byte fragment slots.
-            const int Kc = d / 128, chunk = blockIdx.y;
+            const int Kc = d / 128, chunk = by;
             __syncthreads();
             _Float16 *ph = (_Float16 *)lds + w * 4096, *pl = ph + 2048;   // [16 rows][128], hi then lo
             float fold[4];
@@ -751,7 +766,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
                 }
             }
             wave_lds_order();
-            const size_t mb = (size_t)blockIdx.z * T;
+            const size_t mb = (size_t)bz * T;
             // 512 slots per wave: lanes run along the 16 rows, so a store covers
             // consecutive slots of one (half-step, term, half)
 #pragma unroll
@@ -776,7 +791,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
             }
             // the rows past M up to the 64-row padding: zeros (fold factor 1),
             // as the preparation pads; by the last block of the last segment
-            if (blockIdx.z == gridDim.z - 1 && blockIdx.x == gridDim.x - 1 && w == 0) {
+            if (bz == gridDim.z - 1 && bx == gridDim.x - 1 && w == 0) {
                 const size_t M = (size_t)gridDim.z * T, Mp = (M + 63) / 64 * 64;
                 for (size_t i = lane; i < (Mp - M) * 32; i += 64) {
                     const size_t m = M + (i >> 5);
