@@ -201,21 +201,11 @@ __global__ __launch_bounds__(64 * NW, 1) void k_relpos_attn(const float *__restr
     extern __shared__ float lds[];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int c = lane & 15, g = lane >> 4;
-    // XCD-aware order: the hardware deals workgroups to the 8 XCDs round-robin
-    // by flat id. Each XCD gets a contiguous run of the (query block, segment,
-    // head) triples, query blocks fastest, then segments: the query blocks of
-    // one (segment, head) read the same K and V planes, and the segments of
-    // one head the same rk rows, so they share the XCD's L2.
+    // XCD-aware order (query block bx, head by, segment bz): the query blocks
+    // of one (segment, head) read the same K and V planes, and the segments of
+    // one head the same rk rows, so they run on one XCD and share its L2
     int bx, by, bz;
-    {
-        const int gx = gridDim.x, gz = gridDim.z;
-        const int ntot = gx * gridDim.y * gz, flat = blockIdx.x + gx * (blockIdx.y + gridDim.y * blockIdx.z);
-        const int qx = ntot / 8, rx = ntot % 8, xcd = flat % 8, loc = flat / 8;
-        const int lg = xcd < rx ? xcd * (qx + 1) + loc : rx * (qx + 1) + (xcd - rx) * qx + loc;
-        bx = lg % gx;
-        bz = (lg / gx) % gz;
-        by = lg / (gx * gz);
-    }
+    xcd_order(bx, by, bz);
     const int ho = by * DK;
     const size_t so = (size_t)bz * (size_t)T * (size_t)d;
     q += so;

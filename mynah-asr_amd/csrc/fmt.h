@@ -68,6 +68,22 @@ __device__ __forceinline__ int chunk_shift(float amax) {
     return amax > 0.0f ? 15 - e : 0;
 }
 
+// XCD-aware order of a 3-D grid. The hardware deals workgroups to the 8 XCDs
+// round-robin by flat id (x fastest, then y, then z), and each XCD has its own
+// L2. This gives each XCD a contiguous run of logical (x, z, y) triples, x
+// fastest, then z, then y, so that workgroups neighbouring in x (then in z)
+// run on one XCD and share what they read through its L2. A bijection of the
+// grid onto itself.
+__device__ __forceinline__ void xcd_order(int &bx, int &by, int &bz) {
+    const int gx = gridDim.x, gy = gridDim.y, gz = gridDim.z;
+    const int ntot = gx * gy * gz, flat = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+    const int qx = ntot / 8, rx = ntot % 8, xcd = flat % 8, loc = flat / 8;
+    const int lg = xcd < rx ? xcd * (qx + 1) + loc : rx * (qx + 1) + (xcd - rx) * qx + loc;
+    bx = lg % gx;
+    bz = (lg / gx) % gz;
+    by = lg / (gx * gz);
+}
+
 __device__ __forceinline__ half8 pairs_to_half8(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
                                                 _Float16 bias) {
     // each dword holds two f16 values 1024+code (exact integers); subtract the
