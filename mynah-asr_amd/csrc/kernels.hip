@@ -2165,7 +2165,18 @@ static bool gemm_wide(const DevW &W, int tilesM, int jobs) {
     // 64 x 128 tiles, three workgroups per CU, hide it better (f32 weights,
     // 256 -> 256 at 480 000 rows: 301 -> 294 us; at 120 000 rows 78 -> 75.5 us)
     if (!wide_fmt<QT, A1>() || W.Np % 256 != 0 || W.Kp < 512) return false;
-    return tilesM * (W.Np / 256) * jobs >= 512;
+    const int tw = tilesM * (W.Np / 256) * jobs;
+    if (tw < 512) return false;
+    // f32 weights: only when the wide tiles (two workgroups per CU) fill their
+    // rounds as well as the 64 x 128 ones (three per CU): 2560 -> 1024 at 12 000
+    // rows is 752 wide tiles, 1.47 rounds, 228 us, against 198 us in 1504
+    // narrow tiles, 1.96 rounds. (Q2_K 4096 -> 1024 at 12 000 rows, the same 752
+    // tiles, measured faster wide: 280 -> 264 us.)
+    if (QT == QT_F32) {
+        auto fill = [](int t, int slots) { return (double)t / (double)((t + slots - 1) / slots * slots); };
+        if (fill(tw, 512) < fill(2 * tw, 768)) return false;
+    }
+    return true;
 }
 
 template <int QT, bool A1>
