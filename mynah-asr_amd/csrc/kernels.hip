@@ -2171,7 +2171,8 @@ static bool gemm_wide(const DevW &W, int tilesM, int jobs) {
     // rounds as well as the 64 x 128 ones (three per CU): 2560 -> 1024 at 12 000
     // rows is 752 wide tiles, 1.47 rounds, 228 us, against 198 us in 1504
     // narrow tiles, 1.96 rounds. (Q2_K 4096 -> 1024 at 12 000 rows, the same 752
-    // tiles, measured faster wide: 280 -> 264 us.)
+    // tiles, measured faster wide: 280 -> 264 us; the rule on the Q2_K, Q4_K and
+    // Q5_K layer sets: 290-317 against 302-332 TOPS.)
     if (QT == QT_F32) {
         auto fill = [](int t, int slots) { return (double)t / (double)((t + slots - 1) / slots * slots); };
         if (fill(tw, 512) < fill(2 * tw, 768)) return false;
